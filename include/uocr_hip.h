@@ -1,0 +1,173 @@
+/*
+ * uocr_hip.h - MI355X extensions of libunlimitedocr.so.
+ *
+ * Three groups of extern "C" entry points, all plain pointers and sizes:
+ *
+ *  1. Engine extensions.  The reference feeds precomputed visual rows into
+ *     the decoder through an internal image_features_f16 span
+ *     (src/backend/metal/uocr_metal.m:14988-15017); uocr_generate_embeddings
+ *     exposes that path so a prompt of image-embedding rows plus text ids
+ *     can be generated without the vision encoder.
+ *     uocr_engine_open_memory opens a .uocr image already in host memory.
+ *
+ *  2. Hot-path operators.  Each runs one kernel (or fusion) of the decode
+ *     step on device buffers and replaces one reference Metal kernel, cited
+ *     per function.  Operands use the .uocr storage layout: row-major payload
+ *     plus a separate [rows][K/64] fp16 scale array (NULL for f16); all
+ *     activations are fp16 bit patterns (uint16), dots accumulate in fp32.
+ *     Operators are enqueued on one library stream on device 0 and return
+ *     before completion; uocr_hip_sync() waits.  They return 0 on success
+ *     and a negative uocr_status on error (text in uocr_hip_op_error()).
+ *
+ *  3. Device-memory plumbing (alloc/copy/sync/timers) so callers with no HIP
+ *     binding (ctypes, tests, benchmarks) can drive the operators.
+ *
+ * The synthetic .uocr builder used by the tests and benchmarks is declared
+ * in uocr_synth.h.
+ */
+#ifndef UOCR_HIP_H
+#define UOCR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "unlimitedocr.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- 1. engine extensions ------------------------------------------------ */
+
+/* Like uocr_engine_open but validates and maps a .uocr image in memory.  The
+ * caller keeps `data` alive until uocr_engine_close. */
+UOCR_API uocr_engine *uocr_engine_open_memory(const uocr_engine_opts *opts, const void *data, size_t size);
+
+#define UOCR_GEN_FLAG_IGNORE_EOS 1u  /* decode past EOS (benchmarks) */
+#define UOCR_GEN_FLAG_NO_GRAPH 2u    /* enqueue kernels directly, no hipGraph replay */
+
+/* Greedy generation from a prompt whose image positions (image_mask[i] == 1)
+ * take the next row of image_rows_f16 ([n_image_rows][1280] fp16) instead of
+ * the token embedding.  Replaces the Metal image_features_f16 span path
+ * (uocr_metal.m:14988-15017) followed by uocr_metal.m:14909-15382.
+ * Writes up to max_new_tokens ids (EOS included when it stops generation)
+ * and optionally the argmax score of each; reports prefill and decode wall
+ * time in ms.  Returns a uocr_status. */
+UOCR_API int uocr_generate_embeddings(uocr_engine *engine, const int32_t *input_ids, const uint8_t *image_mask,
+                                      const uint16_t *image_rows_f16, uint32_t n_image_rows, uint32_t n_tokens,
+                                      uint32_t max_new_tokens, uint32_t flags, int32_t *out_ids, float *out_scores,
+                                      uint32_t *out_count, double *out_prefill_ms, double *out_decode_ms);
+
+/* ---- 2. hot-path operators ----------------------------------------------- */
+
+/* Bytes of the device workspace every operator below takes (partials,
+ * counters, routing ids, intermediates, step state). */
+UOCR_API size_t uocr_op_workspace_bytes(void);
+
+/* y[r] = fp16(sum_k W[r][k] * x[k] (+ residual[r])), r < rows, K % 64 == 0,
+ * K <= 6848.  Replaces uocr_decode_linear_residual_gemv_q8_0_to_f16
+ * (kernels/decode_gemv_q8.metal:97-126) and its Q4 twin
+ * (kernels/decode_gemv_q4.metal:69-98); BASELINE config 1. */
+UOCR_API int uocr_op_gemv(uint32_t qtype, const void *w, const void *s, uint32_t rows, uint32_t k, const void *x,
+                          const void *residual, void *y);
+
+/* mid[r] = fp16(silu(G[r].xin) * (U[r].xin)), xin = x or rmsnorm(x, norm_w).
+ * Replaces uocr_decode_swiglu_gate_up_gemv_q4_0_to_f16
+ * (kernels/decode_gemv_q4.metal:101-135). */
+UOCR_API int uocr_op_swiglu(uint32_t qtype, const void *gw, const void *gs, const void *uw, const void *us,
+                            uint32_t rows, uint32_t k, const void *x, const void *norm_w, void *mid);
+
+/* y = fp16(x * 1/sqrt(mean(x^2) + 1e-6) * w).  Replaces uocr_rmsnorm_f16_to_f16
+ * (kernels/norm.metal:12-40). */
+UOCR_API int uocr_op_rmsnorm(const void *x, const void *w, uint32_t n, void *y);
+
+/* Fused [optional final RMSNorm] + LM-head GEMV + argmax over vocab rows of
+ * K = 1280 (NaN rows skipped, ties to the lowest id, none valid -> id 0).
+ * Writes the token id and its score to device memory.  Replaces
+ * uocr_lm_head_argmax_q4_0_to_f16 + uocr_argmax_pairs_f32
+ * (kernels/lm_head_q4.metal:25-98, kernels/sampling.metal:173-200);
+ * BASELINE config 2. */
+UOCR_API int uocr_op_lm_head_argmax(uint32_t qtype, const void *w, const void *s, uint32_t vocab, const void *x,
+                                    const void *norm_w, void *workspace, int32_t *token, float *score);
+
+/* MoE router over 64 fp16 rows of K = 1280: softmax, greedy top-6 with ties
+ * to the lower id, raw probabilities (renormalised when norm_topk != 0).
+ * Replaces uocr_moe_router_decode_fused_f16 (kernels/moe.metal:53-189). */
+UOCR_API int uocr_op_router(const void *router_w, const void *x, const void *norm_w, int norm_topk, uint32_t *ids,
+                            float *weights);
+
+/* Weights of one MoE FFN.  Expert projections are slabs of 64 experts:
+ * projection p of expert e at p_w + e * *_w_stride bytes and p_s + e *
+ * *_s_stride fp16 values.  Shared experts (merged, intermediate 1792) use
+ * shared_qtype; routed experts use expert_qtype. */
+typedef struct uocr_op_moe_weights {
+    const void *router;                   /* fp16 [64][1280] */
+    uint32_t expert_qtype;
+    const void *gate_w, *gate_s, *up_w, *up_s; /* [64] x [896][1280] */
+    uint64_t gu_w_stride, gu_s_stride;
+    const void *down_w, *down_s;          /* [64] x [1280][896] */
+    uint64_t dn_w_stride, dn_s_stride;
+    uint32_t shared_qtype;
+    const void *sgate_w, *sgate_s, *sup_w, *sup_s; /* [1792][1280] */
+    const void *sdown_w, *sdown_s;        /* [1280][1792] */
+} uocr_op_moe_weights;
+
+/* out = fp16(sum_r w_r D_e(mid_r) + fp16(SD(smid)) + residual) with
+ * mid_r = fp16(silu(G_e xin) * U_e xin), smid likewise for the shared
+ * experts, xin = x or rmsnorm(x, norm_w); the chosen ids and weights are
+ * also written (device).  Replaces the decode MoE sequence of
+ * uocr_metal.m:14433-14497 (router, shared SwiGLU, routed gate/up
+ * decode_gemv_q4.metal:138-180, down-combine :185-224); BASELINE config 3. */
+UOCR_API int uocr_op_moe_ffn(const uocr_op_moe_weights *m, const void *x, const void *norm_w, const void *residual,
+                             int norm_topk, void *workspace, void *out, uint32_t *ids, float *weights);
+
+/* Decode attention of one query (fp16 [10][128]) over a KV cache laid out
+ * [10 heads][cache_capacity][128] fp16, for prompt_length prompt slots plus
+ * generated_count generated tokens in the 128-token ring (generated_count
+ * counts the token just written; 0 means prompt-only).  fp32 softmax scaled
+ * by 1/sqrt(128); output fp16 [10][128].  Replaces
+ * uocr_decode_attention_flash_f16_to_f16 (kernels/attention_decode.metal:
+ * 25-131); BASELINE config 4. */
+UOCR_API int uocr_op_attention_decode(const void *q, const void *k_cache, const void *v_cache,
+                                      uint32_t cache_capacity, uint32_t prompt_length, uint32_t generated_count,
+                                      void *workspace, void *out);
+
+/* Full attention half of a decoder layer at one decode position:
+ * rmsnorm(hidden, norm_w) -> q/k/v GEMVs (qtype, K = 1280) -> split-half RoPE
+ * (theta 10000) at position prompt_length + generated_count - 1 -> K/V write
+ * into the ring slot -> decode attention -> out = fp16(O ctx + hidden).
+ * Replaces uocr_metal.m:14338-14393 (norm, QKV :11614, rope.metal:39-70,
+ * kv_cache.metal:20-62, attention, decode_gemv_q8.metal:97-126); BASELINE
+ * config 4 with projections. */
+UOCR_API int uocr_op_attention_block(uint32_t qtype, const void *wq, const void *sq, const void *wk, const void *sk,
+                                     const void *wv, const void *sv, const void *wo, const void *so,
+                                     const void *hidden, const void *norm_w, void *k_cache, void *v_cache,
+                                     uint32_t cache_capacity, uint32_t prompt_length, uint32_t generated_count,
+                                     void *workspace, void *out);
+
+/* Embedding row of `token` (device int32) dequantised to fp16 [1280];
+ * out-of-range ids give zeros.  Replaces uocr_get_rows_q4_0_to_f16_h1280_g64
+ * (kernels/embedding_q4.metal:21-56) and its Q8/f16 twins. */
+UOCR_API int uocr_op_embed(uint32_t qtype, const void *w, const void *s, uint32_t vocab, const int32_t *token,
+                           void *out);
+
+/* ---- 3. device plumbing ---------------------------------------------------- */
+UOCR_API int uocr_hip_device_count(void);
+UOCR_API void *uocr_hip_alloc(size_t bytes);
+UOCR_API int uocr_hip_free(void *p);
+UOCR_API int uocr_hip_upload(void *dst, const void *src, size_t bytes);
+UOCR_API int uocr_hip_download(void *dst, const void *src, size_t bytes);
+UOCR_API int uocr_hip_memset(void *dst, int value, size_t bytes);
+UOCR_API int uocr_hip_sync(void);
+UOCR_API const char *uocr_hip_op_error(void);
+/* hipEvent timer on the operator stream: begin records the start event, end
+ * records the stop event, waits for it and returns the elapsed ms (< 0 on
+ * error). */
+UOCR_API int uocr_hip_timer_begin(void);
+UOCR_API float uocr_hip_timer_end_ms(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UOCR_HIP_H */

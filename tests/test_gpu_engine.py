@@ -1,0 +1,129 @@
+"""End-to-end parity of the HIP decode loop with the CPU oracle.
+
+The engine runs on a synthetic .uocr image at the real decoder shape
+(12 layers, 64 experts, vocab 129280); the oracle runs the same prompt on the
+same bytes.  Greedy ids must agree while the oracle's top-2 margin exceeds
+1e-2 (after the first step whose margin is below that, the two sequences may
+legitimately diverge and the comparison stops).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+_MODELS: dict[int, object] = {}
+
+
+def model(uocr, qprofile):
+    if qprofile not in _MODELS:
+        _MODELS.clear()  # keep at most one multi-GB image alive
+        _MODELS[qprofile] = uocr.synth_model(qprofile, 7)
+    return _MODELS[qprofile]
+
+
+def compare_ids(got, ref, margins):
+    n = 0
+    for g, r, m in zip(got, ref, margins):
+        if m <= 1e-2:
+            break
+        assert g == r, f"step {n}: got {g}, oracle {r} (margin {m:.4f})"
+        n += 1
+    return n
+
+
+def prompt(rng, n_text, n_image=0):
+    ids = np.concatenate([[0], rng.integers(2, 128000, n_text - 1)]).astype(np.int32)
+    mask = np.zeros(n_text + n_image, np.uint8)
+    if n_image:
+        ids = np.concatenate([ids[:1], np.full(n_image, 128815, np.int32), ids[1:]]).astype(np.int32)
+        mask[1:1 + n_image] = 1
+    rows = (rng.standard_normal((n_image, 1280))).astype(np.float16) if n_image else None
+    return ids, mask, rows
+
+
+@pytest.mark.parametrize("qprofile", [3, 2, 1])
+def test_generate_matches_oracle(gpu, oracle, qprofile):
+    uocr = gpu
+    m = model(uocr, qprofile)
+    rng = np.random.default_rng(100 + qprofile)
+    ids, mask, rows = prompt(rng, 10, 6)
+    eng = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=256, max_gen_tokens=64)
+    got, scores, pre_ms, dec_ms = eng.generate_embeddings(ids, mask, rows, max_new_tokens=10, flags=uocr.GEN_IGNORE_EOS)
+    orc = oracle.Model(m.ptr, m.size, m, prompt_capacity=64)
+    ref, margins = orc.generate(ids, mask, rows.view(np.uint16), max_new=10, ignore_eos=True)
+    orc.close()
+    assert got.shape == (10,)
+    assert compare_ids(got.tolist(), ref.tolist(), margins.tolist()) >= 3
+    eng.close()
+
+
+def test_graph_and_eager_paths_agree(gpu):
+    uocr = gpu
+    m = model(uocr, 3)
+    rng = np.random.default_rng(5)
+    ids, mask, rows = prompt(rng, 12, 4)
+    eng = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=128, max_gen_tokens=40)
+    a = eng.generate_embeddings(ids, mask, rows, 20, flags=uocr.GEN_IGNORE_EOS)
+    b = eng.generate_embeddings(ids, mask, rows, 20, flags=uocr.GEN_IGNORE_EOS | uocr.GEN_NO_GRAPH)
+    c = eng.generate_embeddings(ids, mask, rows, 20, flags=uocr.GEN_IGNORE_EOS)
+    assert a[0].tolist() == b[0].tolist() == c[0].tolist()
+    assert np.array_equal(a[1], b[1])
+    eng.close()
+
+
+def test_ring_window_wrap_matches_oracle(gpu, oracle):
+    """More than 128 generated tokens: the KV ring overwrites its oldest slots."""
+    uocr = gpu
+    m = model(uocr, 3)
+    rng = np.random.default_rng(9)
+    ids, mask, rows = prompt(rng, 6, 2)
+    eng = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=64, max_gen_tokens=160)
+    got = eng.generate_embeddings(ids, mask, rows, 140, flags=uocr.GEN_IGNORE_EOS)[0]
+    orc = oracle.Model(m.ptr, m.size, m, prompt_capacity=64)
+    ref, margins = orc.generate(ids, mask, rows.view(np.uint16), max_new=140, ignore_eos=True)
+    orc.close()
+    n = compare_ids(got.tolist(), ref.tolist(), margins.tolist())
+    print(f"ring test: {n} ids compared")
+    assert n >= 3
+    eng.close()
+
+
+def test_text_request_through_public_abi(gpu, oracle):
+    """uocr_generate_prepared (the reference's entry point) on a text prompt."""
+    uocr = gpu
+    m = model(uocr, 3)
+    rng = np.random.default_rng(13)
+    ids, _, _ = prompt(rng, 9)
+    eng = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=64, max_gen_tokens=16, profile=True)
+    assert eng.backend == "hip"
+    got = eng.generate_prepared(ids, max_new_tokens=6)
+    orc = oracle.Model(m.ptr, m.size, m, prompt_capacity=64)
+    ref, margins = orc.generate(ids, max_new=6)
+    orc.close()
+    assert len(got) == len(ref)
+    compare_ids(got.tolist(), ref.tolist(), margins.tolist())
+    events = eng.profile_events()
+    assert "hip.decode_loop" in events and "hip.prefill" in events
+    rep = eng.memory_report()
+    assert rep.category_live_bytes[1] > 0  # kv-cache
+    with pytest.raises(RuntimeError) as ex:
+        eng.generate_prepared(np.array([0, 128815], np.int32), np.array([0, 1], np.uint8), max_new_tokens=2)
+    assert getattr(ex.value, "status", None) == uocr.UOCR_ERROR_INVALID_ARGUMENT  # image ids need views
+    eng.close()
+
+
+def test_engine_from_model_file(gpu, tmp_path):
+    uocr = gpu
+    path = tmp_path / "q4.uocr"
+    assert uocr.load_library().uocr_synth_model_write(str(path).encode(), 3, 7) == 0
+    eng = uocr.Engine(str(path), backend="hip", max_prompt_tokens=32, max_gen_tokens=8)
+    a = eng.generate_prepared(np.array([0, 5, 6, 7], np.int32), max_new_tokens=4)
+    eng.close()
+    path.unlink()
+    m = model(uocr, 3)
+    eng2 = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=32, max_gen_tokens=8)
+    b = eng2.generate_prepared(np.array([0, 5, 6, 7], np.int32), max_new_tokens=4)
+    eng2.close()
+    assert a.tolist() == b.tolist()

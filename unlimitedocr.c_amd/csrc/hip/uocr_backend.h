@@ -1,0 +1,69 @@
+/*
+ * uocr_backend.h - HIP backend behind the engine core.
+ *
+ * Replaces the reference's Metal backend interface
+ * (src/backend/metal/uocr_metal.h:170-299: context create/destroy, profile
+ * and memory-tracker hooks, map_model, runtime arenas, generate_f16 with the
+ * decoder request/result of :107-128).  One context owns one HIP stream on
+ * one device, the weights copied into HBM, the KV cache and all scratch.
+ * Every entry returns 1 on success, 0 with a message in err on failure.
+ */
+#ifndef UOCR_BACKEND_H
+#define UOCR_BACKEND_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../core/uocr_model.h"
+#include "../core/uocr_runtime.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct uocr_hip_ctx uocr_hip_ctx;
+
+/* flags of uocr_hip_decoder_request */
+#define UOCR_GEN_IGNORE_EOS 1u   /* keep decoding past token 1 (benchmarks) */
+#define UOCR_GEN_NO_GRAPH 2u     /* enqueue kernels directly instead of replaying captured graphs */
+
+typedef struct uocr_hip_decoder_request {
+    const int32_t *input_ids;
+    const uint8_t *image_mask;      /* may be NULL: no image rows */
+    const uint16_t *image_rows;     /* fp16 [n_image_rows][1280], in mask order */
+    uint32_t n_image_rows;
+    uint32_t n_tokens;
+    uint32_t max_new_tokens;
+    uint32_t flags;
+} uocr_hip_decoder_request;
+
+typedef struct uocr_hip_decoder_result {
+    int32_t *generated_ids;
+    float *generated_scores;        /* may be NULL */
+    uint32_t generated_capacity;
+    uint32_t generated_count;
+    uint32_t stopped_on_eos;
+    double prefill_ms;
+    double decode_ms;
+} uocr_hip_decoder_result;
+
+int uocr_hip_is_available(char *why, size_t why_size);
+uocr_hip_ctx *uocr_hip_context_create(char *err, size_t err_size);
+void uocr_hip_context_destroy(uocr_hip_ctx *ctx);
+void uocr_hip_context_set_profile(uocr_hip_ctx *ctx, uocr_profile_state *profile);
+void uocr_hip_context_set_memory_tracker(uocr_hip_ctx *ctx, uocr_memory_tracker *tracker);
+/* Copies the bound decoder tensors into HBM (weights + expert slabs). */
+int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_bindings *b, char *err, size_t err_size);
+/* Allocates KV cache and scratch for prompts up to prompt_capacity tokens and
+ * up to max_gen generated tokens. */
+int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t prompt_capacity, uint32_t max_gen, char *err,
+                                      size_t err_size);
+int uocr_hip_context_generate(uocr_hip_ctx *ctx, const uocr_hip_decoder_request *req, uocr_hip_decoder_result *res,
+                              char *err, size_t err_size);
+uint64_t uocr_hip_context_weight_bytes(const uocr_hip_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UOCR_BACKEND_H */

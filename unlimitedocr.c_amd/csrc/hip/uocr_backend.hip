@@ -1,0 +1,582 @@
+/*
+ * uocr_backend.hip - HIP backend: weight residency in HBM, KV cache and
+ * scratch arenas, prompt assembly, prefill and the greedy decode token loop.
+ *
+ * Per token the decode step is one captured hipGraph:
+ *   [final RMSNorm + LM-head argmax (+ step-state advance)] -> [embedding
+ *   gather of the selected token] -> 12 x decoder layer
+ * and is replayed once per generated token.  All position-dependent values
+ * (position, KV slot, ring attention plan, selected token) live in device
+ * memory (uocr_step_state), written by the LM-head finalize block, so the
+ * graph is captured once per context.  The host reads token ids back per
+ * chunk of 8 steps, one chunk behind the GPU, and stops on EOS
+ * (uocr_metal.m:15248-15358 semantics, without stalling the device).
+ *
+ * Prompt processing runs each prompt row through the same decoder-layer
+ * kernels with a causal-prefix attention plan (a replayable prefill graph).
+ */
+#include "uocr_backend.h"
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "uocr_kernels.h"
+
+#define H_SIZE 1280u
+#define DECODE_CHUNK 8u
+
+namespace {
+
+struct dev_layer {
+    uocr_qmat q, k, v, o, gate, up, down, sgate, sup, sdown;
+    const uint16_t *in_norm, *post_norm, *router;
+    uocr_expert_slab slab;
+};
+
+int bfail(char *err, size_t n, const char *fmt, ...) {
+    if (err != nullptr && n > 0u) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(err, n, fmt, ap);
+        va_end(ap);
+    }
+    return 0;
+}
+
+uint64_t align256(uint64_t v) {
+    return (v + 255u) & ~(uint64_t)255u;
+}
+
+}  // namespace
+
+struct uocr_hip_ctx {
+    int device;
+    hipStream_t stream;
+    uocr_profile_state *profile;
+    uocr_memory_tracker *mem;
+
+    uint8_t *warena;
+    uint64_t warena_bytes;
+    int mapped;
+    uocr_qmat embed, lm_head;
+    const uint16_t *final_norm;
+    dev_layer L[UOCR_DECODER_LAYERS];
+
+    int runtime_ready;
+    uint32_t prompt_cap, cache_cap, max_gen;
+    uint8_t *rarena;
+    uint64_t rarena_bytes;
+    uint64_t kv_bytes, scratch_bytes, moe_bytes, logits_bytes, prompt_bytes;
+    uint16_t *kc, *vc, *h, *a, *q, *ctxv, *mid, *smid, *prompt;
+    uint32_t *ids;
+    float *wts;
+    float *attn_part;
+    uint32_t *attn_cnt, *lm_part, *lm_cnt;
+    uocr_step_state *state;
+    int32_t *tokens;
+    float *scores;
+    int32_t *d_ids;
+    uint8_t *d_mask;
+    int32_t *h_tokens;
+    float *h_scores;
+    uint16_t *h_prompt;
+
+    float invf[UOCR_K_HEAD_DIM / 2];
+    hipGraphExec_t g_decode, g_prefill;
+    int graphs_ready;
+};
+
+#define HIPCHK(expr, what)                                                                        \
+    do {                                                                                          \
+        const hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess) return bfail(err, err_size, "%s: %s", (what), hipGetErrorString(e_)); \
+    } while (0)
+
+extern "C" int uocr_hip_is_available(char *why, size_t why_size) {
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        if (why != nullptr && why_size > 0u) {
+            snprintf(why, why_size, "no HIP device is available (%s)", e != hipSuccess ? hipGetErrorString(e) : "0 devices");
+        }
+        return 0;
+    }
+    return 1;
+}
+
+extern "C" uocr_hip_ctx *uocr_hip_context_create(char *err, size_t err_size) {
+    if (!uocr_hip_is_available(err, err_size)) return nullptr;
+    uocr_hip_ctx *ctx = (uocr_hip_ctx *)calloc(1, sizeof(uocr_hip_ctx));
+    if (ctx == nullptr) {
+        bfail(err, err_size, "failed to allocate HIP context");
+        return nullptr;
+    }
+    const char *dev = getenv("UOCR_HIP_DEVICE");
+    ctx->device = dev != nullptr ? atoi(dev) : 0;
+    if (hipSetDevice(ctx->device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        bfail(err, err_size, "failed to initialise HIP device %d", ctx->device);
+        free(ctx);
+        return nullptr;
+    }
+    /* inv_freq[d] = 2^(d * (-2 log2(theta) / head_dim)), golden.py:410-414 */
+    const float freq_scale = -2.0f * log2f((float)UOCR_ROPE_THETA) / (float)UOCR_HEAD_DIM;
+    for (int d = 0; d < UOCR_K_HEAD_DIM / 2; ++d) ctx->invf[d] = exp2f((float)d * freq_scale);
+    return ctx;
+}
+
+static void release_graphs(uocr_hip_ctx *ctx) {
+    if (ctx->graphs_ready) {
+        (void)hipGraphExecDestroy(ctx->g_decode);
+        (void)hipGraphExecDestroy(ctx->g_prefill);
+        ctx->graphs_ready = 0;
+    }
+}
+
+static void release_runtime(uocr_hip_ctx *ctx) {
+    release_graphs(ctx);
+    if (ctx->rarena != nullptr) {
+        (void)hipFree(ctx->rarena);
+        if (ctx->mem != nullptr) {
+            uocr_memory_release(ctx->mem, UOCR_MEMORY_KV_CACHE, ctx->kv_bytes);
+            uocr_memory_release(ctx->mem, UOCR_MEMORY_DECODER_SCRATCH, ctx->scratch_bytes);
+            uocr_memory_release(ctx->mem, UOCR_MEMORY_MOE_SCRATCH, ctx->moe_bytes);
+            uocr_memory_release(ctx->mem, UOCR_MEMORY_LOGITS_READBACK, ctx->logits_bytes);
+            uocr_memory_release(ctx->mem, UOCR_MEMORY_PROMPT_EMBEDDINGS, ctx->prompt_bytes);
+        }
+    }
+    if (ctx->h_tokens != nullptr) (void)hipHostFree(ctx->h_tokens);
+    if (ctx->h_scores != nullptr) (void)hipHostFree(ctx->h_scores);
+    if (ctx->h_prompt != nullptr) (void)hipHostFree(ctx->h_prompt);
+    ctx->rarena = nullptr;
+    ctx->h_tokens = nullptr;
+    ctx->h_scores = nullptr;
+    ctx->h_prompt = nullptr;
+    ctx->runtime_ready = 0;
+}
+
+extern "C" void uocr_hip_context_destroy(uocr_hip_ctx *ctx) {
+    if (ctx == nullptr) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    release_runtime(ctx);
+    if (ctx->warena != nullptr) (void)hipFree(ctx->warena);
+    (void)hipStreamDestroy(ctx->stream);
+    free(ctx);
+}
+
+extern "C" void uocr_hip_context_set_profile(uocr_hip_ctx *ctx, uocr_profile_state *profile) {
+    if (ctx != nullptr) ctx->profile = profile;
+}
+
+extern "C" void uocr_hip_context_set_memory_tracker(uocr_hip_ctx *ctx, uocr_memory_tracker *tracker) {
+    if (ctx != nullptr) ctx->mem = tracker;
+}
+
+extern "C" uint64_t uocr_hip_context_weight_bytes(const uocr_hip_ctx *ctx) {
+    return ctx != nullptr ? ctx->warena_bytes : 0u;
+}
+
+/* ---- weight residency ---------------------------------------------------- */
+
+namespace {
+
+struct placer {
+    uint64_t off = 0;
+    uint64_t take(uint64_t bytes) {
+        const uint64_t at = off;
+        off = align256(off + bytes);
+        return at;
+    }
+};
+
+uint64_t tensor_bytes(const uocr_bound_tensor &t) {
+    return align256(t.w_bytes) + align256(t.s_bytes);
+}
+
+}  // namespace
+
+static int upload(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor &t, uocr_qmat *out, char *err, size_t err_size) {
+    const uint64_t wo = p.take(t.w_bytes);
+    HIPCHK(hipMemcpy(ctx->warena + wo, t.w, t.w_bytes, hipMemcpyHostToDevice), "weight upload");
+    out->w = ctx->warena + wo;
+    out->qtype = t.qtype;
+    out->s = nullptr;
+    if (t.s != nullptr) {
+        const uint64_t so = p.take(t.s_bytes);
+        HIPCHK(hipMemcpy(ctx->warena + so, t.s, t.s_bytes, hipMemcpyHostToDevice), "scale upload");
+        out->s = (const uint16_t *)(ctx->warena + so);
+    }
+    return 1;
+}
+
+/* Uploads one projection of all 64 experts into an evenly strided slab. */
+static int upload_slab(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor *ex, uocr_qmat *out, uint64_t *w_stride,
+                       uint64_t *s_stride, char *err, size_t err_size) {
+    const uint64_t ws = align256(ex[0].w_bytes);
+    const uint64_t ss = align256(ex[0].s_bytes);
+    const uint64_t wo = p.take(ws * UOCR_ROUTED_EXPERTS);
+    const uint64_t so = ex[0].s != nullptr ? p.take(ss * UOCR_ROUTED_EXPERTS) : 0u;
+    for (uint32_t e = 0; e < UOCR_ROUTED_EXPERTS; ++e) {
+        HIPCHK(hipMemcpy(ctx->warena + wo + e * ws, ex[e].w, ex[e].w_bytes, hipMemcpyHostToDevice), "expert upload");
+        if (ex[e].s != nullptr) {
+            HIPCHK(hipMemcpy(ctx->warena + so + e * ss, ex[e].s, ex[e].s_bytes, hipMemcpyHostToDevice), "expert scale upload");
+        }
+    }
+    out->w = ctx->warena + wo;
+    out->s = ex[0].s != nullptr ? (const uint16_t *)(ctx->warena + so) : nullptr;
+    out->qtype = ex[0].qtype;
+    *w_stride = ws;
+    *s_stride = ss / 2u;
+    return 1;
+}
+
+extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_bindings *b, char *err, size_t err_size) {
+    if (ctx == nullptr || b == nullptr) return bfail(err, err_size, "invalid map_model request");
+    HIPCHK(hipSetDevice(ctx->device), "hipSetDevice");
+    if (ctx->warena != nullptr) {
+        (void)hipFree(ctx->warena);
+        ctx->warena = nullptr;
+        ctx->mapped = 0;
+        release_graphs(ctx);
+    }
+    /* size pass */
+    uint64_t total = tensor_bytes(b->embed) + tensor_bytes(b->lm_head) + tensor_bytes(b->final_norm);
+    for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
+        const uocr_bound_layer &L = b->layers[l];
+        total += tensor_bytes(L.in_norm) + tensor_bytes(L.post_norm) + tensor_bytes(L.q) + tensor_bytes(L.k) +
+                 tensor_bytes(L.v) + tensor_bytes(L.o);
+        if (l == 0u) {
+            total += tensor_bytes(L.gate) + tensor_bytes(L.up) + tensor_bytes(L.down);
+        } else {
+            total += tensor_bytes(L.router) + tensor_bytes(L.sgate) + tensor_bytes(L.sup) + tensor_bytes(L.sdown);
+            total += UOCR_ROUTED_EXPERTS * (tensor_bytes(L.egate[0]) + tensor_bytes(L.eup[0]) + tensor_bytes(L.edown[0]));
+        }
+    }
+    HIPCHK(hipMalloc((void **)&ctx->warena, total), "weight arena allocation");
+    ctx->warena_bytes = total;
+    placer p;
+    uocr_qmat fn;
+    if (!upload(ctx, p, b->embed, &ctx->embed, err, err_size) || !upload(ctx, p, b->lm_head, &ctx->lm_head, err, err_size) ||
+        !upload(ctx, p, b->final_norm, &fn, err, err_size)) {
+        return 0;
+    }
+    ctx->final_norm = (const uint16_t *)fn.w;
+    for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
+        const uocr_bound_layer &S = b->layers[l];
+        dev_layer &D = ctx->L[l];
+        memset(&D, 0, sizeof(D));
+        uocr_qmat n1, n2;
+        if (!upload(ctx, p, S.in_norm, &n1, err, err_size) || !upload(ctx, p, S.post_norm, &n2, err, err_size) ||
+            !upload(ctx, p, S.q, &D.q, err, err_size) || !upload(ctx, p, S.k, &D.k, err, err_size) ||
+            !upload(ctx, p, S.v, &D.v, err, err_size) || !upload(ctx, p, S.o, &D.o, err, err_size)) {
+            return 0;
+        }
+        D.in_norm = (const uint16_t *)n1.w;
+        D.post_norm = (const uint16_t *)n2.w;
+        if (l == 0u) {
+            if (!upload(ctx, p, S.gate, &D.gate, err, err_size) || !upload(ctx, p, S.up, &D.up, err, err_size) ||
+                !upload(ctx, p, S.down, &D.down, err, err_size)) {
+                return 0;
+            }
+            continue;
+        }
+        uocr_qmat r;
+        if (!upload(ctx, p, S.router, &r, err, err_size) || !upload(ctx, p, S.sgate, &D.sgate, err, err_size) ||
+            !upload(ctx, p, S.sup, &D.sup, err, err_size) || !upload(ctx, p, S.sdown, &D.sdown, err, err_size)) {
+            return 0;
+        }
+        D.router = (const uint16_t *)r.w;
+        uocr_expert_slab &sl = D.slab;
+        uint64_t ws2, ss2;
+        if (!upload_slab(ctx, p, S.egate, &sl.gate, &sl.gu_w_stride, &sl.gu_s_stride, err, err_size) ||
+            !upload_slab(ctx, p, S.eup, &sl.up, &ws2, &ss2, err, err_size) ||
+            !upload_slab(ctx, p, S.edown, &sl.down, &sl.dn_w_stride, &sl.dn_s_stride, err, err_size)) {
+            return 0;
+        }
+        if (ws2 != sl.gu_w_stride || ss2 != sl.gu_s_stride) return bfail(err, err_size, "expert gate/up slabs differ in stride");
+    }
+    if (p.off > total) return bfail(err, err_size, "weight arena overflow");
+    ctx->mapped = 1;
+    return 1;
+}
+
+/* ---- runtime arenas ------------------------------------------------------- */
+
+extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t prompt_capacity, uint32_t max_gen,
+                                                 char *err, size_t err_size) {
+    if (ctx == nullptr || prompt_capacity == 0u || max_gen == 0u) return bfail(err, err_size, "invalid runtime arena request");
+    if (ctx->runtime_ready && prompt_capacity <= ctx->prompt_cap && max_gen <= ctx->max_gen) return 1;
+    HIPCHK(hipSetDevice(ctx->device), "hipSetDevice");
+    HIPCHK(hipStreamSynchronize(ctx->stream), "stream sync");
+    release_runtime(ctx);
+    const uint32_t cap = prompt_capacity + UOCR_GENERATED_RING_WINDOW;
+    const uint64_t kv_one = (uint64_t)UOCR_DECODER_LAYERS * UOCR_ATTENTION_HEADS * cap * UOCR_HEAD_DIM * 2u;
+    placer p;
+    const uint64_t o_kc = p.take(kv_one), o_vc = p.take(kv_one);
+    const uint64_t o_h = p.take(H_SIZE * 2u), o_a = p.take(H_SIZE * 2u), o_q = p.take(H_SIZE * 2u), o_c = p.take(H_SIZE * 2u);
+    const uint64_t o_state = p.take(sizeof(uocr_step_state));
+    const uint64_t o_apart = p.take(UOCR_ATTN_PARTIAL_FLOATS * 4u), o_acnt = p.take(UOCR_ATTN_COUNTER_INTS * 4u);
+    const uint64_t scratch_end = p.off;
+    const uint64_t o_mid = p.take(UOCR_DENSE_LAYER0_INTERMEDIATE * 2u), o_smid = p.take(UOCR_MOE_SHARED_INTERMEDIATE * 2u);
+    const uint64_t o_ids = p.take(64u), o_wts = p.take(64u);
+    const uint64_t moe_end = p.off;
+    const uint64_t o_lpart = p.take(2u * UOCR_K_LM_BLOCKS * 4u), o_lcnt = p.take(4u);
+    const uint64_t o_tok = p.take((uint64_t)max_gen * 4u), o_sc = p.take((uint64_t)max_gen * 4u);
+    const uint64_t logits_end = p.off;
+    const uint64_t o_prompt = p.take((uint64_t)prompt_capacity * H_SIZE * 2u);
+    const uint64_t o_dids = p.take((uint64_t)prompt_capacity * 4u), o_dmask = p.take(prompt_capacity);
+    const uint64_t total = p.off;
+    HIPCHK(hipMalloc((void **)&ctx->rarena, total), "runtime arena allocation");
+    HIPCHK(hipMemset(ctx->rarena, 0, total), "runtime arena clear");
+    uint8_t *b = ctx->rarena;
+    ctx->kc = (uint16_t *)(b + o_kc);
+    ctx->vc = (uint16_t *)(b + o_vc);
+    ctx->h = (uint16_t *)(b + o_h);
+    ctx->a = (uint16_t *)(b + o_a);
+    ctx->q = (uint16_t *)(b + o_q);
+    ctx->ctxv = (uint16_t *)(b + o_c);
+    ctx->state = (uocr_step_state *)(b + o_state);
+    ctx->attn_part = (float *)(b + o_apart);
+    ctx->attn_cnt = (uint32_t *)(b + o_acnt);
+    ctx->mid = (uint16_t *)(b + o_mid);
+    ctx->smid = (uint16_t *)(b + o_smid);
+    ctx->ids = (uint32_t *)(b + o_ids);
+    ctx->wts = (float *)(b + o_wts);
+    ctx->lm_part = (uint32_t *)(b + o_lpart);
+    ctx->lm_cnt = (uint32_t *)(b + o_lcnt);
+    ctx->tokens = (int32_t *)(b + o_tok);
+    ctx->scores = (float *)(b + o_sc);
+    ctx->prompt = (uint16_t *)(b + o_prompt);
+    ctx->d_ids = (int32_t *)(b + o_dids);
+    ctx->d_mask = (uint8_t *)(b + o_dmask);
+    ctx->rarena_bytes = total;
+    ctx->kv_bytes = 2u * kv_one;
+    ctx->scratch_bytes = scratch_end - o_h;
+    ctx->moe_bytes = moe_end - scratch_end;
+    ctx->logits_bytes = logits_end - moe_end;
+    ctx->prompt_bytes = total - logits_end;
+    HIPCHK(hipHostMalloc((void **)&ctx->h_tokens, (size_t)max_gen * 4u, hipHostMallocDefault), "pinned token buffer");
+    HIPCHK(hipHostMalloc((void **)&ctx->h_scores, (size_t)max_gen * 4u, hipHostMallocDefault), "pinned score buffer");
+    HIPCHK(hipHostMalloc((void **)&ctx->h_prompt, (size_t)prompt_capacity * H_SIZE * 2u, hipHostMallocDefault),
+           "pinned prompt staging");
+    if (ctx->mem != nullptr) {
+        uocr_memory_reserve(ctx->mem, UOCR_MEMORY_KV_CACHE, ctx->kv_bytes);
+        uocr_memory_reserve(ctx->mem, UOCR_MEMORY_DECODER_SCRATCH, ctx->scratch_bytes);
+        uocr_memory_reserve(ctx->mem, UOCR_MEMORY_MOE_SCRATCH, ctx->moe_bytes);
+        uocr_memory_reserve(ctx->mem, UOCR_MEMORY_LOGITS_READBACK, ctx->logits_bytes);
+        uocr_memory_reserve(ctx->mem, UOCR_MEMORY_PROMPT_EMBEDDINGS, ctx->prompt_bytes);
+    }
+    ctx->prompt_cap = prompt_capacity;
+    ctx->cache_cap = cap;
+    ctx->max_gen = max_gen;
+    ctx->runtime_ready = 1;
+    return 1;
+}
+
+/* ---- step enqueue ----------------------------------------------------------- */
+
+static hipError_t enqueue_layers(uocr_hip_ctx *c) {
+    hipStream_t s = c->stream;
+    const uint64_t kv_layer = (uint64_t)UOCR_ATTENTION_HEADS * c->cache_cap * UOCR_HEAD_DIM;
+    hipError_t e = hipSuccess;
+#define ENQ(x)                        \
+    do {                              \
+        e = (x);                      \
+        if (e != hipSuccess) return e; \
+    } while (0)
+    for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
+        const dev_layer &L = c->L[l];
+        uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
+        ENQ(uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->invf, c->state, c->q, kc, vc, c->cache_cap));
+        ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part, c->attn_cnt, c->ctxv));
+        ENQ(uocr_launch_gemv(s, L.o, H_SIZE, H_SIZE, c->ctxv, nullptr, c->h, c->a));
+        if (l == 0u) {
+            ENQ(uocr_launch_swiglu(s, L.gate, L.up, UOCR_DENSE_LAYER0_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->mid));
+            ENQ(uocr_launch_gemv(s, L.down, H_SIZE, UOCR_DENSE_LAYER0_INTERMEDIATE, c->mid, nullptr, c->a, c->h));
+        } else {
+            ENQ(uocr_launch_router(s, L.router, c->a, L.post_norm, 0, c->ids, c->wts));
+            ENQ(uocr_launch_swiglu(s, L.sgate, L.sup, UOCR_MOE_SHARED_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->smid));
+            ENQ(uocr_launch_moe_gate_up(s, &L.slab, c->ids, c->a, L.post_norm, c->mid));
+            ENQ(uocr_launch_moe_down(s, &L.slab, c->ids, c->wts, c->mid, L.sdown, c->smid, c->a, c->h));
+        }
+    }
+    return e;
+#undef ENQ
+}
+
+static hipError_t enqueue_select(uocr_hip_ctx *c) {
+    return uocr_launch_lm_head(c->stream, c->lm_head, UOCR_VOCAB_SIZE, c->h, c->final_norm, c->lm_part, c->lm_cnt,
+                               c->state, 1, c->tokens, c->scores);
+}
+
+static hipError_t enqueue_decode_step(uocr_hip_ctx *c) {
+    hipError_t e = enqueue_select(c);
+    if (e == hipSuccess) e = uocr_launch_embed(c->stream, c->embed, UOCR_VOCAB_SIZE, nullptr, c->state, c->h);
+    if (e == hipSuccess) e = enqueue_layers(c);
+    return e;
+}
+
+static hipError_t enqueue_prefill_step(uocr_hip_ctx *c) {
+    hipError_t e = uocr_launch_prefill_next(c->stream, c->state, c->prompt, c->h);
+    if (e == hipSuccess) e = enqueue_layers(c);
+    return e;
+}
+
+static int capture(uocr_hip_ctx *c, hipError_t (*fn)(uocr_hip_ctx *), hipGraphExec_t *out, char *err, size_t err_size) {
+    hipGraph_t g = nullptr;
+    HIPCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
+    const hipError_t e = fn(c);
+    const hipError_t e2 = hipStreamEndCapture(c->stream, &g);
+    if (e != hipSuccess || e2 != hipSuccess) {
+        if (g != nullptr) (void)hipGraphDestroy(g);
+        return bfail(err, err_size, "graph capture failed: %s", hipGetErrorString(e != hipSuccess ? e : e2));
+    }
+    const hipError_t e3 = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    HIPCHK(e3, "graph instantiate");
+    return 1;
+}
+
+/* ---- generation -------------------------------------------------------------- */
+
+static int scan_chunk(uocr_hip_ctx *c, uint32_t from, uint32_t to, int ignore_eos, uint32_t *count, int *eos) {
+    for (uint32_t i = from; i < to; ++i) {
+        const int32_t id = c->h_tokens[i];
+        if (id < 0 || (uint32_t)id >= UOCR_VOCAB_SIZE) return 0;
+        *count = i + 1u;
+        if (!ignore_eos && id == UOCR_TOKEN_EOS) {
+            *eos = 1;
+            return 1;
+        }
+    }
+    return 1;
+}
+
+extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder_request *req,
+                                         uocr_hip_decoder_result *res, char *err, size_t err_size) {
+    if (c == nullptr || req == nullptr || res == nullptr || req->input_ids == nullptr) {
+        return bfail(err, err_size, "invalid HIP generation request");
+    }
+    if (!c->mapped) return bfail(err, err_size, "HIP context has no mapped model");
+    const uint32_t P = req->n_tokens, N = req->max_new_tokens;
+    if (P == 0u || N == 0u) return bfail(err, err_size, "generation needs a prompt and max_new_tokens > 0");
+    if (res->generated_ids == nullptr || res->generated_capacity < N) return bfail(err, err_size, "result capacity too small");
+    if (!uocr_hip_context_allocate_runtime(c, P > c->prompt_cap ? P : (c->prompt_cap ? c->prompt_cap : P),
+                                           N > c->max_gen ? N : (c->max_gen ? c->max_gen : N), err, err_size)) {
+        return 0;
+    }
+    HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+    const int use_graph = (req->flags & UOCR_GEN_NO_GRAPH) == 0u;
+    if (use_graph && !c->graphs_ready) {
+        if (!capture(c, enqueue_decode_step, &c->g_decode, err, err_size)) return 0;
+        if (!capture(c, enqueue_prefill_step, &c->g_prefill, err, err_size)) {
+            (void)hipGraphExecDestroy(c->g_decode);
+            return 0;
+        }
+        c->graphs_ready = 1;
+    }
+    hipStream_t s = c->stream;
+    const uint64_t t0 = uocr_now_ns();
+
+    /* prompt assembly: image rows from the caller, text rows gathered on device */
+    uint32_t n_img = 0;
+    for (uint32_t i = 0; i < P; ++i) {
+        if (req->image_mask != nullptr && req->image_mask[i] != 0u) {
+            if (req->image_rows == nullptr || n_img >= req->n_image_rows) {
+                return bfail(err, err_size, "prompt has more image positions than image rows");
+            }
+            memcpy(c->h_prompt + (size_t)i * H_SIZE, req->image_rows + (size_t)n_img * H_SIZE, H_SIZE * 2u);
+            ++n_img;
+        }
+    }
+    if (n_img != 0u) {
+        HIPCHK(hipMemcpyAsync(c->prompt, c->h_prompt, (size_t)P * H_SIZE * 2u, hipMemcpyHostToDevice, s), "prompt upload");
+    }
+    HIPCHK(hipMemcpyAsync(c->d_ids, req->input_ids, (size_t)P * 4u, hipMemcpyHostToDevice, s), "ids upload");
+    const uint8_t *dmask = nullptr;
+    if (req->image_mask != nullptr) {
+        HIPCHK(hipMemcpyAsync(c->d_mask, req->image_mask, P, hipMemcpyHostToDevice, s), "mask upload");
+        dmask = c->d_mask;
+    }
+    HIPCHK(uocr_launch_embed_rows(s, c->embed, UOCR_VOCAB_SIZE, c->d_ids, dmask, P, c->prompt), "prompt embedding");
+
+    /* prefill */
+    HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0), "state init");
+    for (uint32_t i = 0; i < P; ++i) {
+        if (use_graph) {
+            HIPCHK(hipGraphLaunch(c->g_prefill, s), "prefill graph launch");
+        } else {
+            HIPCHK(enqueue_prefill_step(c), "prefill step");
+        }
+    }
+    HIPCHK(hipStreamSynchronize(s), "prefill sync");
+    const uint64_t t1 = uocr_now_ns();
+
+    /* decode: chunks of DECODE_CHUNK steps; the host scans chunk k-1 while
+     * chunk k runs */
+    HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0), "decode state init");
+    const int ignore_eos = (req->flags & UOCR_GEN_IGNORE_EOS) != 0u;
+    uint32_t count = 0, scanned = 0;
+    int eos = 0;
+    hipEvent_t ev[2];
+    HIPCHK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming), "event create");
+    HIPCHK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming), "event create");
+    uint32_t issued = 0, chunk = 0;
+    int ok = 1;
+    while (issued < N && !eos && ok) {
+        const uint32_t end = issued + DECODE_CHUNK < N ? issued + DECODE_CHUNK : N;
+        for (uint32_t t = issued; t < end && ok; ++t) {
+            hipError_t e;
+            if (t + 1u < N) {
+                e = use_graph ? hipGraphLaunch(c->g_decode, s) : enqueue_decode_step(c);
+            } else {
+                e = enqueue_select(c);
+            }
+            if (e != hipSuccess) ok = bfail(err, err_size, "decode step %u: %s", t, hipGetErrorString(e));
+        }
+        if (!ok) break;
+        if (hipMemcpyAsync(c->h_tokens + issued, c->tokens + issued, (size_t)(end - issued) * 4u, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipEventRecord(ev[chunk & 1u], s) != hipSuccess) {
+            ok = bfail(err, err_size, "token readback failed");
+            break;
+        }
+        if (chunk > 0u) {
+            if (hipEventSynchronize(ev[(chunk - 1u) & 1u]) != hipSuccess) {
+                ok = bfail(err, err_size, "decode chunk wait failed");
+                break;
+            }
+            if (!scan_chunk(c, scanned, issued, ignore_eos, &count, &eos)) ok = bfail(err, err_size, "decode selected an invalid token id");
+            scanned = issued;
+        }
+        issued = end;
+        ++chunk;
+    }
+    const hipError_t se = hipStreamSynchronize(s);
+    (void)hipEventDestroy(ev[0]);
+    (void)hipEventDestroy(ev[1]);
+    if (se != hipSuccess) return bfail(err, err_size, "decode sync: %s", hipGetErrorString(se));
+    if (!ok) return 0;
+    if (!eos && !scan_chunk(c, scanned, issued, ignore_eos, &count, &eos)) {
+        return bfail(err, err_size, "decode selected an invalid token id");
+    }
+    const uint64_t t2 = uocr_now_ns();
+    memcpy(res->generated_ids, c->h_tokens, (size_t)count * 4u);
+    if (res->generated_scores != nullptr) {
+        HIPCHK(hipMemcpy(res->generated_scores, c->scores, (size_t)count * 4u, hipMemcpyDeviceToHost), "score readback");
+    }
+    res->generated_count = count;
+    res->stopped_on_eos = (uint32_t)eos;
+    res->prefill_ms = (double)(t1 - t0) / 1.0e6;
+    res->decode_ms = (double)(t2 - t1) / 1.0e6;
+    if (c->profile != nullptr) {
+        uocr_profile_add_ms(c->profile, "hip.prefill", res->prefill_ms);
+        uocr_profile_add_ms(c->profile, "hip.decode_loop", res->decode_ms);
+        c->profile->report.metal_command_buffer_count += use_graph ? (uint64_t)P + issued : 0u;
+        c->profile->report.metal_command_buffer_wait_count += chunk + 1u;
+    }
+    return 1;
+}

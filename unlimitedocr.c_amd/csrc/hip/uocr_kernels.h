@@ -1,0 +1,128 @@
+/*
+ * uocr_kernels.h - launch interface of the gfx950 decode kernels.
+ *
+ * Internal to libunlimitedocr.so.  Every launcher validates the shapes its
+ * kernel and grid assume before launching and returns hipErrorInvalidValue
+ * instead of launching on a mismatch.
+ *
+ * Tensor storage is the .uocr layout: row-major payload (f16, int8, or Q4_0
+ * group-half-split nibbles) plus a separate [rows][K/64] fp16 scale array.
+ * Activations are fp16; all dots accumulate in fp32.
+ */
+#ifndef UOCR_KERNELS_H
+#define UOCR_KERNELS_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+/* qtype values follow the .uocr tensor qtype enum */
+#define UOCR_QT_F16 1u
+#define UOCR_QT_Q8 3u
+#define UOCR_QT_Q4 4u
+
+#define UOCR_K_HIDDEN 1280
+#define UOCR_K_HEADS 10
+#define UOCR_K_HEAD_DIM 128
+#define UOCR_K_EXPERTS 64
+#define UOCR_K_TOPK 6
+#define UOCR_K_RING 128
+#define UOCR_K_MAX_K 6848          /* largest GEMV reduction length */
+#define UOCR_K_ATTN_SPLITS 32      /* split-K blocks per head in decode attention */
+#define UOCR_K_LM_BLOCKS 1024      /* LM-head argmax partial blocks */
+
+/* Per-step decode state kept in device memory so one captured graph can be
+ * replayed for every token.  Positions follow uocr_metal.m:14239 and the ring
+ * plan of attention_decode.metal:25-33. */
+typedef struct uocr_step_state {
+    int32_t t;            /* generated tokens selected so far */
+    int32_t prompt_len;   /* P */
+    int32_t pos;          /* position of the token being decoded */
+    int32_t cache_token;  /* KV slot written for pos */
+    int32_t attn_prompt;  /* attention indices below this map 1:1 to slots */
+    int32_t attn_len;     /* attention length */
+    int32_t first_gen;    /* logical index of the first live ring token */
+    int32_t cur_token;    /* token id embedded this step */
+} uocr_step_state;
+
+typedef struct uocr_qmat {
+    const void *w;        /* payload */
+    const uint16_t *s;    /* scales (NULL for f16) */
+    uint32_t qtype;
+} uocr_qmat;
+
+/* Expert slab of one layer: projection p of expert e at w + e * w_stride
+ * (bytes) and s + e * s_stride (fp16 values). */
+typedef struct uocr_expert_slab {
+    uocr_qmat gate, up, down;
+    uint64_t gu_w_stride, gu_s_stride;   /* gate/up: [896][1280] per expert */
+    uint64_t dn_w_stride, dn_s_stride;   /* down:    [1280][896] per expert */
+} uocr_expert_slab;
+
+/* Scratch sizes (bytes) the launchers expect. */
+#define UOCR_ATTN_PARTIAL_FLOATS (UOCR_K_HEADS * UOCR_K_ATTN_SPLITS * (UOCR_K_HEAD_DIM + 2))
+#define UOCR_ATTN_COUNTER_INTS UOCR_K_HEADS
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* y[r] = f16(dot(W_r, xin) [+ res[r]]); xin = x, or rmsnorm(x, nw) when nw. */
+hipError_t uocr_launch_gemv(hipStream_t st, uocr_qmat W, uint32_t rows, uint32_t K, const uint16_t *x,
+                            const uint16_t *nw, const uint16_t *res, uint16_t *y);
+/* mid[r] = f16(silu(G_r.xin) * (U_r.xin)); xin as above. */
+hipError_t uocr_launch_swiglu(hipStream_t st, uocr_qmat G, uocr_qmat U, uint32_t rows, uint32_t K,
+                              const uint16_t *x, const uint16_t *nw, uint16_t *mid);
+/* RMSNorm of x (fp16 [n]) with weight nw -> y (fp16). */
+hipError_t uocr_launch_rmsnorm(hipStream_t st, const uint16_t *x, const uint16_t *nw, uint32_t n, uint16_t *y);
+/* Fused attention input: rmsnorm(h) -> q,k,v GEMVs -> f16 -> split-half RoPE
+ * at st->pos -> q to qout, k/v into the caches at st->cache_token.
+ * Caches are [heads][cache_capacity][128] fp16 for one layer. */
+hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
+                                const uint16_t *nw, const float *inv_freq, const uocr_step_state *state,
+                                uint16_t *qout, uint16_t *kcache, uint16_t *vcache, uint32_t cache_capacity);
+/* Split-K decode attention over the plan in *state with a last-block merge.
+ * partials: UOCR_ATTN_PARTIAL_FLOATS floats; counters: 10 ints, zero before
+ * the first call (every call leaves them zero). */
+hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
+                                 uint32_t cache_capacity, const uocr_step_state *state, float *partials,
+                                 uint32_t *counters, uint16_t *ctx);
+/* Router: rmsnorm(x) (when nw) -> logits over 64 fp16 rows -> softmax ->
+ * greedy top-6 (ties to lower id) -> ids, raw probs (renormalised if
+ * norm_topk). */
+hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, const uint16_t *x, const uint16_t *nw,
+                              int norm_topk, uint32_t *ids, float *weights);
+/* Routed gate/up: mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = ids[r]. */
+hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
+                                   const uint16_t *x, const uint16_t *nw, uint16_t *mid);
+/* Routed down + weighted combine + shared down + residual:
+ * out[c] = f16(sum_r w_r * D_e[c].mid_r + f16(SD[c].smid) + res[c]). */
+hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
+                                const float *weights, const uint16_t *mid, uocr_qmat SD, const uint16_t *smid,
+                                const uint16_t *res, uint16_t *out);
+/* Fused final norm + LM-head argmax (two-pass, last-block finalize).
+ * token/score receive the winner at index state->t (or index 0 when
+ * state is NULL); with advance set, the finalize block also writes the next
+ * decode position into *state.  partials: 2*UOCR_K_LM_BLOCKS words; counter:
+ * one int, zero before the first call. */
+hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x, const uint16_t *nw,
+                               uint32_t *partials, uint32_t *counter, uocr_step_state *state, int advance,
+                               int32_t *tokens, float *scores);
+/* Embedding gather of tokens[0] (token == NULL: state->cur_token) -> fp16 row. */
+hipError_t uocr_launch_embed(hipStream_t st, uocr_qmat E, uint32_t vocab, const int32_t *token,
+                             const uocr_step_state *state, uint16_t *out);
+/* Prompt rows: out[b] = embedding of ids[b] for every b with !mask[b]. */
+hipError_t uocr_launch_embed_rows(hipStream_t st, uocr_qmat E, uint32_t vocab, const int32_t *ids,
+                                  const uint8_t *mask, uint32_t n, uint16_t *out);
+/* Replayable prefill step: copies prompt row state->t into h, sets the
+ * causal-prefix plan for that position and increments state->t. */
+hipError_t uocr_launch_prefill_next(hipStream_t st, uocr_step_state *state, const uint16_t *prompt, uint16_t *h);
+/* Sets *state for prompt position i (prefill through the decode kernels). */
+hipError_t uocr_launch_prefill_state(hipStream_t st, uocr_step_state *state, int32_t i);
+/* Sets *state for decode with explicit (prompt_len, gen_after_write). */
+hipError_t uocr_launch_decode_state(hipStream_t st, uocr_step_state *state, int32_t prompt_len, int32_t t);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UOCR_KERNELS_H */
