@@ -553,15 +553,17 @@ int orc_router_topk(const uint16_t *x, const uint16_t *R, uint32_t n_experts, ui
     for (uint32_t e = 0; e < n_experts; ++e) probs[e] /= den;
     if (!greedy_topk(probs, n_experts, top_k, ids, weights)) return 0;
     if (margin_out) {
+        /* selection margin in logit space: the smallest gap between
+         * consecutive ranks, including rank k against the best unselected */
         float next = -INFINITY;
         for (uint32_t e = 0; e < n_experts; ++e) {
             int taken = 0;
             for (uint32_t j = 0; j < top_k; ++j) taken |= (ids[j] == e);
-            if (!taken && probs[e] > next) next = probs[e];
+            if (!taken && logits[e] > next) next = logits[e];
         }
-        float m = weights[top_k - 1] - (n_experts > top_k ? next : 0.0f);
+        float m = n_experts > top_k ? logits[ids[top_k - 1]] - next : INFINITY;
         for (uint32_t j = 1; j < top_k; ++j) {
-            const float d = weights[j - 1] - weights[j];
+            const float d = logits[ids[j - 1]] - logits[ids[j]];
             if (d < m) m = d;
         }
         *margin_out = m;

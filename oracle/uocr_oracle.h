@@ -109,7 +109,8 @@ int orc_lm_head_argmax(uint32_t qtype, const void *W, const uint16_t *S, uint32_
  * top-k with ties to the lower id; weights are the raw probabilities unless
  * norm_topk is set (then divided by their sum).  uocr_cpu_ref.c:388-466,
  * moe.metal:53-189, golden.py:544-562.  margin_out (may be NULL) receives
- * p[k-th] - p[(k+1)-th], the selection margin. */
+ * the selection margin: the smallest logit gap between consecutive ranks,
+ * including the k-th selected expert against the best unselected one. */
 int orc_router_topk(const uint16_t *x, const uint16_t *R, uint32_t n_experts, uint32_t K, uint32_t top_k,
                     int norm_topk, uint32_t *ids, float *weights, float *probs_out, float *margin_out);
 

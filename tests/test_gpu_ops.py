@@ -220,7 +220,7 @@ def test_moe_ffn_matches_oracle(gpu, oracle, qtype, shared_qtype, norm_topk):
     nw = rng.uniform(0.8, 1.2, 1280).astype(np.float16)
     dnw = dev(uocr, nw)
     checked = 0
-    for t in range(6):
+    for t in range(10):
         x = rand_f16(rng, 1280)
         res = rand_f16(rng, 1280)
         xn = oracle.rmsnorm_f16(x.view(np.uint16), nw.view(np.uint16))
