@@ -1,0 +1,234 @@
+"""Benchmark: batch-1 greedy decode of the UnlimitedOCR 12-layer decoder on one MI355X.
+
+Workload: random-init weights of the real decoder
+shape (synthetic .uocr image), a prompt of 900 fp16 image-embedding rows
+~ N(0,1) plus 32 random text ids (BOS first), then 512 greedy decode steps at
+batch 1.  One "step" is one full generate call (prompt processing + 512 decode
+steps); `value` is decode tok/s of the mixed-Q4 profile = generated tokens /
+decode-loop seconds (src/unlimitedocr_c/perf.py:97-102), weights resident in
+HBM before timing starts.  The Q8 and fp16 profiles run the same workload and
+are reported beside it.
+
+`roofline` is the dominant kernel by bytes (the fused Q4 LM-head GEMV +
+argmax: 87,912,964 algorithmic bytes per launch) timed
+with HIP events on the stream it runs on, rotating 6 weight copies (528 MB)
+so launches stream from HBM rather than the 256 MB Infinity Cache.
+`cpu_baseline` is the C oracle's decode step (the restated reference CPU
+path) on this host's cores at the same context length, for a bounded number
+of tokens.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "unlimitedocr.c_amd"))
+
+import uocr  # noqa: E402
+
+METRIC = "decode tok/s at batch 1 (Q4, Q8, fp16); achieved HBM GB/s vs 8 TB/s peak"
+PEAK_HBM = 8.0e12
+N_IMAGE, N_TEXT, N_NEW = 900, 32, 512
+ENTRY = np.dtype([("id", "<u4"), ("family", "<u4"), ("layer", "<i4"), ("expert", "<i4"), ("projection", "<u4"),
+                  ("usage", "<u4"), ("qtype", "<u4"), ("flags", "<u4"), ("rank", "<u4"), ("lshape", "<u4", 4),
+                  ("pshape", "<u4", 4), ("payload_offset", "<u8"), ("payload_size", "<u8"), ("block_size", "<u4"),
+                  ("row_size", "<u4"), ("scale_offset", "<u8"), ("scale_size", "<u8"), ("min_offset", "<u8"),
+                  ("min_size", "<u8"), ("reasons", "<u4", 2), ("source_name", "<u4", 2)])
+assert ENTRY.itemsize == 140
+
+
+def tensor_table(model: uocr.SynthModel) -> np.ndarray:
+    """Tensor directory of a .uocr image (uocr_format.h:268-299 layout)."""
+    v = model.view()
+    hdr = v[:112]
+    n_sec = int(hdr[24:28].view("<u4")[0])
+    sec_off = int(hdr[40:48].view("<u8")[0])
+    secs = v[sec_off:sec_off + 32 * n_sec].view(np.dtype([("type", "<u4"), ("flags", "<u4"), ("offset", "<u8"),
+                                                            ("size", "<u8"), ("alignment", "<u8")]))
+    d = secs[secs["type"] == 2][0]
+    count = int(v[d["offset"] + 12:d["offset"] + 16].view("<u4")[0])
+    start = int(d["offset"]) + 16
+    return v[start:start + 140 * count].view(ENTRY)
+
+
+def decode_bytes_per_token(model: uocr.SynthModel, prompt_len: int, n_new: int) -> float:
+    """Algorithmic HBM bytes per generated token: every weight byte a decode
+    step reads (all non-expert tensors, 6 of 64 routed experts per MoE layer,
+    one embedding row) plus the KV cache read over the ring attention length
+    and the K/V write (61,440 B per token of context)."""
+    t = tensor_table(model)
+    size = t["payload_size"] + t["scale_size"]
+    is_expert = t["family"] == 8
+    is_embed = t["family"] == 1
+    dense = float(size[~is_expert & ~is_embed].sum())
+    experts = float(size[is_expert].sum()) * 6.0 / 64.0
+    embed_row = float(size[is_embed].sum()) / 129280.0
+    lens = [prompt_len + min(g, 128) for g in range(1, n_new)]
+    mean_len = float(np.mean(lens)) if lens else float(prompt_len)
+    kv = 61440.0 * (mean_len + 1.0)
+    return dense + experts + embed_row + kv
+
+
+def make_prompt(seed: int = 0):
+    rng = np.random.default_rng(seed)
+    ids = np.concatenate([[0], np.full(N_IMAGE, 128815), rng.integers(2, 128000, N_TEXT - 1)]).astype(np.int32)
+    mask = (ids == 128815).astype(np.uint8)
+    rows = rng.standard_normal((N_IMAGE, 1280)).astype(np.float16)
+    return ids, mask, rows
+
+
+def run_profile(qprofile: int, steps: int, warmup: int, log, flags: int = 0) -> dict:
+    t0 = time.time()
+    model = uocr.synth_model(qprofile, 7)
+    ids, mask, rows = make_prompt()
+    eng = uocr.Engine.from_memory(model, backend="hip", max_prompt_tokens=1024, max_gen_tokens=N_NEW)
+    log(f"profile {qprofile}: model {model.size / 1e9:.2f} GB ready in {time.time() - t0:.1f}s")
+    for _ in range(warmup):
+        eng.generate_embeddings(ids, mask, rows, N_NEW, flags=uocr.GEN_IGNORE_EOS | flags)
+    uocr.sync()
+    wall, pre, dec, gen = [], [], [], 0
+    for s in range(steps):
+        t = time.perf_counter()
+        out, _, p_ms, d_ms = eng.generate_embeddings(ids, mask, rows, N_NEW, flags=uocr.GEN_IGNORE_EOS | flags)
+        wall.append((time.perf_counter() - t) * 1e3)
+        pre.append(p_ms)
+        dec.append(d_ms)
+        gen += int(out.size)
+        log(f"  step {s}: prefill {p_ms:.1f} ms, decode {d_ms:.1f} ms ({out.size / d_ms * 1e3:.1f} tok/s)")
+    uocr.sync()
+    bpt = decode_bytes_per_token(model, ids.size, N_NEW)
+    tok_s = gen / (sum(dec) / 1e3)
+    eng.close()
+    model.close()
+    return {"tok_s": tok_s, "ms_per_step": float(np.mean(wall)), "prefill_ms": float(np.mean(pre)),
+            "decode_ms": float(np.mean(dec)), "bytes_per_token": bpt, "hbm_gbs": bpt * tok_s / 1e9,
+            "roofline_tok_s": PEAK_HBM / bpt, "frac": bpt * tok_s / PEAK_HBM, "generated": gen}
+
+
+def lm_head_roofline(log, iters: int = 60) -> dict:
+    """Q4 LM head 129280x1280 + argmax (config 2), 6 rotating weight copies."""
+    rng = np.random.default_rng(1)
+    vocab, k = 129280, 1280
+    w = rng.integers(0, 256, size=(vocab, k // 2), dtype=np.uint8)
+    s = (np.abs(rng.standard_normal((vocab, k // 64))) * 0.02 / 7).astype(np.float16)
+    x = rng.standard_normal(k).astype(np.float16)
+    copies = [(uocr.DeviceBuffer.of(w), uocr.DeviceBuffer.of(s)) for _ in range(6)]
+    dx, ws = uocr.DeviceBuffer.of(x), uocr.workspace()
+    tok, sc = uocr.DeviceBuffer(4), uocr.DeviceBuffer(4)
+    for i in range(6):
+        uocr.op_lm_head_argmax(4, copies[i][0], copies[i][1], vocab, dx, None, ws, tok, sc)
+    uocr.sync()
+    with uocr.Timer() as tm:
+        for i in range(iters):
+            cw, cs = copies[i % 6]
+            uocr.op_lm_head_argmax(4, cw, cs, vocab, dx, None, ws, tok, sc)
+    cold_ms = tm.ms / iters
+    with uocr.Timer() as tm:
+        for i in range(iters):
+            uocr.op_lm_head_argmax(4, copies[0][0], copies[0][1], vocab, dx, None, ws, tok, sc)
+    hot_ms = tm.ms / iters
+    algo = vocab * k // 2 + vocab * (k // 64) * 2 + k * 2 + 4
+    achieved = algo / (cold_ms / 1e3) / 1e9
+    log(f"lm head q4: {cold_ms * 1e3:.1f} us rotated ({achieved:.0f} GB/s), {hot_ms * 1e3:.1f} us hot "
+        f"({algo / (hot_ms / 1e3) / 1e9:.0f} GB/s)")
+    return {"kernel": "k_lm_head<4> (Q4 129280x1280 + argmax, config 2)", "bound": "hbm",
+            "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
+            "traffic": None, "avg_launch_us": round(cold_ms * 1e3, 2), "hot_cache_achieved": round(
+                algo / (hot_ms / 1e3) / 1e9, 1), "algorithmic_bytes": algo, "launches": iters,
+            "note": "per-launch time includes the op's 4-byte counter reset (hipMemsetAsync)"}
+
+
+def cpu_baseline(log, budget_s: float = 12.0) -> dict:
+    """C oracle decode steps (Q4 profile) at the config-5 context length."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import ctypes as ct
+
+    import oracle
+
+    model = uocr.synth_model(uocr.QPROFILE_Q4, 7)
+    orc = oracle.Model(model.ptr, model.size, model, prompt_capacity=1024)
+    L = oracle.lib()
+    prompt_len = N_IMAGE + N_TEXT
+    assert L.orc_session_fill_kv(ct.c_void_p(orc.s), prompt_len + 128, 5) == 1
+    assert L.orc_session_reset(ct.c_void_p(orc.s), prompt_len) == 1
+    h = (np.random.default_rng(3).standard_normal(1280)).astype(np.float16).view(np.uint16).copy()
+    tok, s1, s2 = ct.c_int32(), ct.c_float(), ct.c_float()
+    n, t0 = 0, time.perf_counter()
+    while n < 3 or time.perf_counter() - t0 < budget_s:
+        L.orc_select(ct.c_void_p(orc.s), h.ctypes.data, ct.byref(tok), ct.byref(s1), ct.byref(s2))
+        L.orc_forward_token(ct.c_void_p(orc.s), h.ctypes.data, prompt_len + n, None)
+        n += 1
+    dt = time.perf_counter() - t0
+    cores = int(L.orc_get_threads())
+    orc.close()
+    model.close()
+    log(f"cpu baseline: {n} tokens in {dt:.1f}s on {cores} threads")
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{n} decode steps (LM-head selection + 12 layers) of the mixed-Q4 model at context "
+                      f"{prompt_len}-{prompt_len + n}, C oracle with OpenMP over output rows, {dt:.1f} s"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--profiles", default="q4,q8,fp16", help="comma list of q4,q8,fp16 (q4 is always run)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="enqueue decode kernels directly instead of replaying hipGraphs (for kernel tracing)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the decode loop runs on a single MI355X (no multi-GPU path)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    def log(msg: str) -> None:
+        print(msg, file=sys.stderr, flush=True)
+
+    if uocr.load_library().uocr_hip_device_count() <= 0:
+        log("no HIP device visible")
+        sys.exit(1)
+    names = {"q4": uocr.QPROFILE_Q4, "q8": uocr.QPROFILE_Q8, "fp16": uocr.QPROFILE_FP16}
+    wanted = ["q4"] + [p for p in args.profiles.split(",") if p in names and p != "q4"]
+    flags = uocr.GEN_NO_GRAPH if args.no_graph else 0
+    results = {p: run_profile(names[p], args.steps, args.warmup, log, flags) for p in wanted}
+    roof = lm_head_roofline(log)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(log)
+    q4 = results["q4"]
+    line = {
+        "metric": METRIC,
+        "value": round(q4["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(q4["ms_per_step"], 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0/q8_0 weights x fp16 activations -> fp32 accumulate",
+        "data": "synthetic: random-init weights (seeded .uocr image), 900 N(0,1) fp16 image rows + 32 random text ids",
+        "config": {"workload": "config 5: 12-layer decoder token loop, prompt 900 image rows + 32 text ids, "
+                               "512 greedy decode steps, batch 1, mixed-Q4 profile (attention Q8_0)",
+                   "prompt_tokens": N_IMAGE + N_TEXT, "decode_steps": N_NEW},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "decode_hbm": {p: {"tok_s": round(r["tok_s"], 2), "hbm_gbs": round(r["hbm_gbs"], 1),
+                           "frac_of_8tbs": round(r["frac"], 4), "roofline_tok_s": round(r["roofline_tok_s"], 1),
+                           "bytes_per_token": int(r["bytes_per_token"]), "prefill_ms": round(r["prefill_ms"], 1),
+                           "decode_ms": round(r["decode_ms"], 1), "ms_per_step": round(r["ms_per_step"], 1)}
+                       for p, r in results.items()},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

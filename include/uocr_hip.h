@@ -93,8 +93,8 @@ UOCR_API int uocr_op_lm_head_argmax(uint32_t qtype, const void *w, const void *s
 /* MoE router over 64 fp16 rows of K = 1280: softmax, greedy top-6 with ties
  * to the lower id, raw probabilities (renormalised when norm_topk != 0).
  * Replaces uocr_moe_router_decode_fused_f16 (kernels/moe.metal:53-189). */
-UOCR_API int uocr_op_router(const void *router_w, const void *x, const void *norm_w, int norm_topk, uint32_t *ids,
-                            float *weights);
+UOCR_API int uocr_op_router(const void *router_w, const void *x, const void *norm_w, int norm_topk, void *workspace,
+                            uint32_t *ids, float *weights);
 
 /* Weights of one MoE FFN.  Expert projections are slabs of 64 experts:
  * projection p of expert e at p_w + e * *_w_stride bytes and p_s + e *

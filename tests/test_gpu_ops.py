@@ -242,7 +242,7 @@ def test_router_ties_lowest_id(gpu):
     x = np.zeros(1280, np.float16)
     r = np.zeros((64, 1280), np.float16)
     dids, dw = uocr.DeviceBuffer(24), uocr.DeviceBuffer(24)
-    uocr.op_router(dev(uocr, r), dev(uocr, x), None, 0, dids, dw)
+    uocr.op_router(dev(uocr, r), dev(uocr, x), None, 0, uocr.workspace(), dids, dw)
     uocr.sync()
     assert dids.download(np.uint32).tolist() == [0, 1, 2, 3, 4, 5]
     assert np.allclose(dw.download(np.float32), 1 / 64)

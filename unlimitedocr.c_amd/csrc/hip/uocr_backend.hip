@@ -3,8 +3,8 @@
  * scratch arenas, prompt assembly, prefill and the greedy decode token loop.
  *
  * Per token the decode step is one captured hipGraph:
- *   [final RMSNorm + LM-head argmax (+ step-state advance)] -> [embedding
- *   gather of the selected token] -> 12 x decoder layer
+ *   [final RMSNorm + LM-head argmax partials] -> [argmax finalize + step-state
+ *   advance + embedding gather of the selected token] -> 12 x decoder layer
  * and is replayed once per generated token.  All position-dependent values
  * (position, KV slot, ring attention plan, selected token) live in device
  * memory (uocr_step_state), written by the LM-head finalize block, so the
@@ -72,10 +72,8 @@ struct uocr_hip_ctx {
     uint64_t rarena_bytes;
     uint64_t kv_bytes, scratch_bytes, moe_bytes, logits_bytes, prompt_bytes;
     uint16_t *kc, *vc, *h, *a, *q, *ctxv, *mid, *smid, *prompt;
-    uint32_t *ids;
-    float *wts;
-    float *attn_part;
-    uint32_t *attn_cnt, *lm_part, *lm_cnt;
+    float *attn_part, *logits;
+    uint32_t *lm_part;
     uocr_step_state *state;
     int32_t *tokens;
     float *scores;
@@ -319,12 +317,11 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_kc = p.take(kv_one), o_vc = p.take(kv_one);
     const uint64_t o_h = p.take(H_SIZE * 2u), o_a = p.take(H_SIZE * 2u), o_q = p.take(H_SIZE * 2u), o_c = p.take(H_SIZE * 2u);
     const uint64_t o_state = p.take(sizeof(uocr_step_state));
-    const uint64_t o_apart = p.take(UOCR_ATTN_PARTIAL_FLOATS * 4u), o_acnt = p.take(UOCR_ATTN_COUNTER_INTS * 4u);
+    const uint64_t o_apart = p.take(UOCR_ATTN_PARTIAL_FLOATS * 4u), o_logits = p.take(64u * 4u);
     const uint64_t scratch_end = p.off;
     const uint64_t o_mid = p.take(UOCR_DENSE_LAYER0_INTERMEDIATE * 2u), o_smid = p.take(UOCR_MOE_SHARED_INTERMEDIATE * 2u);
-    const uint64_t o_ids = p.take(64u), o_wts = p.take(64u);
     const uint64_t moe_end = p.off;
-    const uint64_t o_lpart = p.take(2u * UOCR_K_LM_BLOCKS * 4u), o_lcnt = p.take(4u);
+    const uint64_t o_lpart = p.take(UOCR_LM_PARTIAL_WORDS * 4u);
     const uint64_t o_tok = p.take((uint64_t)max_gen * 4u), o_sc = p.take((uint64_t)max_gen * 4u);
     const uint64_t logits_end = p.off;
     const uint64_t o_prompt = p.take((uint64_t)prompt_capacity * H_SIZE * 2u);
@@ -341,13 +338,10 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->ctxv = (uint16_t *)(b + o_c);
     ctx->state = (uocr_step_state *)(b + o_state);
     ctx->attn_part = (float *)(b + o_apart);
-    ctx->attn_cnt = (uint32_t *)(b + o_acnt);
+    ctx->logits = (float *)(b + o_logits);
     ctx->mid = (uint16_t *)(b + o_mid);
     ctx->smid = (uint16_t *)(b + o_smid);
-    ctx->ids = (uint32_t *)(b + o_ids);
-    ctx->wts = (float *)(b + o_wts);
     ctx->lm_part = (uint32_t *)(b + o_lpart);
-    ctx->lm_cnt = (uint32_t *)(b + o_lcnt);
     ctx->tokens = (int32_t *)(b + o_tok);
     ctx->scores = (float *)(b + o_sc);
     ctx->prompt = (uint16_t *)(b + o_prompt);
@@ -392,30 +386,31 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c) {
         const dev_layer &L = c->L[l];
         uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
         ENQ(uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->invf, c->state, c->q, kc, vc, c->cache_cap));
-        ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part, c->attn_cnt, c->ctxv));
+        ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part, c->ctxv));
         ENQ(uocr_launch_gemv(s, L.o, H_SIZE, H_SIZE, c->ctxv, nullptr, c->h, c->a));
         if (l == 0u) {
             ENQ(uocr_launch_swiglu(s, L.gate, L.up, UOCR_DENSE_LAYER0_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->mid));
             ENQ(uocr_launch_gemv(s, L.down, H_SIZE, UOCR_DENSE_LAYER0_INTERMEDIATE, c->mid, nullptr, c->a, c->h));
         } else {
-            ENQ(uocr_launch_router(s, L.router, c->a, L.post_norm, 0, c->ids, c->wts));
-            ENQ(uocr_launch_swiglu(s, L.sgate, L.sup, UOCR_MOE_SHARED_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->smid));
-            ENQ(uocr_launch_moe_gate_up(s, &L.slab, c->ids, c->a, L.post_norm, c->mid));
-            ENQ(uocr_launch_moe_down(s, &L.slab, c->ids, c->wts, c->mid, L.sdown, c->smid, c->a, c->h));
+            ENQ(uocr_launch_moe_shared_router(s, L.sgate, L.sup, L.router, c->a, L.post_norm, c->smid, c->logits));
+            ENQ(uocr_launch_moe_gate_up(s, &L.slab, c->logits, 0, c->a, L.post_norm, c->mid, nullptr, nullptr));
+            ENQ(uocr_launch_moe_down(s, &L.slab, c->logits, 0, c->mid, L.sdown, c->smid, c->a, c->h));
         }
     }
     return e;
 #undef ENQ
 }
 
-static hipError_t enqueue_select(uocr_hip_ctx *c) {
-    return uocr_launch_lm_head(c->stream, c->lm_head, UOCR_VOCAB_SIZE, c->h, c->final_norm, c->lm_part, c->lm_cnt,
-                               c->state, 1, c->tokens, c->scores);
+/* Selection of the next token; with embed, the finalize block also writes
+ * that token's embedding row into h for the following decode step. */
+static hipError_t enqueue_select(uocr_hip_ctx *c, bool embed) {
+    uocr_qmat none = {nullptr, nullptr, UOCR_QT_Q4};
+    return uocr_launch_lm_head(c->stream, c->lm_head, UOCR_VOCAB_SIZE, c->h, c->final_norm, c->lm_part, c->state, 1,
+                               c->tokens, c->scores, embed ? c->embed : none, c->h);
 }
 
 static hipError_t enqueue_decode_step(uocr_hip_ctx *c) {
-    hipError_t e = enqueue_select(c);
-    if (e == hipSuccess) e = uocr_launch_embed(c->stream, c->embed, UOCR_VOCAB_SIZE, nullptr, c->state, c->h);
+    hipError_t e = enqueue_select(c, true);
     if (e == hipSuccess) e = enqueue_layers(c);
     return e;
 }
@@ -534,7 +529,7 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
             if (t + 1u < N) {
                 e = use_graph ? hipGraphLaunch(c->g_decode, s) : enqueue_decode_step(c);
             } else {
-                e = enqueue_select(c);
+                e = enqueue_select(c, false);
             }
             if (e != hipSuccess) ok = bfail(err, err_size, "decode step %u: %s", t, hipGetErrorString(e));
         }

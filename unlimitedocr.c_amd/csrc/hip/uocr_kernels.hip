@@ -3,32 +3,35 @@
  * batch-1 decode token loop of the UnlimitedOCR language model.
  *
  * Design (MI355X-first, not a translation of the Metal kernels):
- *  - Batch-1 decode is HBM-bound.  Weights stream once per token with 128-bit
- *    global loads; each lane owns one 16-byte chunk of a row per iteration and
- *    dequantises it in registers (Q4_0 group-half-split nibbles, Q8_0, f16).
- *  - The activation vector is staged once per workgroup in LDS as fp16; when
- *    the consumer of an RMSNorm output is a GEMV, the norm is recomputed in
- *    the GEMV prologue instead of a separate launch (same fp16 values).
- *  - Row dots reduce across the 64-lane wavefront with DPP row permutes
- *    (quad_perm / row_half_mirror / row_mirror) plus 4 readlanes, no LDS.
- *  - RoPE and the KV-cache write are fused into the QKV GEMV epilogue (a
- *    wave owns rows d and d+64 of one head, the split-half rotation pair).
+ *  - Batch-1 decode is HBM/latency-bound.  Every GEMV assigns a group of LPR
+ *    lanes to a row; each lane owns 16-byte chunks sub, sub+LPR, ... of the
+ *    row and issues all of its (up to 8) 128-bit loads and scale loads
+ *    before any arithmetic, so a wavefront keeps 64 x 8 x 16 B of weights in
+ *    flight.  LPR is chosen per (qtype, K) so a row takes at most 8 loads per
+ *    lane (e.g. Q4 K=1280: 8 lanes x 5 loads, 8 rows per wavefront).
+ *  - Dequantisation happens in registers (Q4_0 group-half-split nibbles,
+ *    Q8_0, f16); the activation vector is staged once per workgroup in LDS as
+ *    fp16, with the producing RMSNorm recomputed in the prologue instead of a
+ *    separate launch.  Group sums use DPP row permutes (quad_perm,
+ *    row_half_mirror, row_mirror) and lane swizzles beyond 16 lanes.
+ *  - RoPE and the KV-cache write are fused into the QKV GEMV epilogue (one
+ *    lane group owns rows d and d+64 of one head, the rotation pair).
  *  - Decode attention is split-K over the context (32 blocks per head, 16
- *    lanes x 8 dims per cached token) with an online-softmax partial per
- *    block and a last-block log-sum-exp merge, so no second launch is needed.
- *  - The MoE router is one 1024-thread workgroup; the softmax and greedy
- *    top-6 run in a single wavefront (one expert per lane, 64-bit keys of
- *    (probability bits, inverted id) so ties go to the lower id).
- *  - Routed experts are gathered by id from a per-layer expert slab; the down
- *    projection fuses the weighted combine, the shared-expert down GEMV and
- *    the residual add (single fp16 rounding).
- *  - The LM head fuses the final RMSNorm and a two-pass argmax whose second
- *    pass runs in the last block to finish (NaN rows skipped, ties to the
- *    lowest id); it also advances the device-side step state so a captured
- *    decode graph can be replayed per token.
- * Cross-block hand-offs use __threadfence() + a device-scope counter that
- * the last block resets, so every launch leaves its counters at zero and no
- * block ever waits on another.
+ *    lanes x 8 dims per cached token) with an online softmax; a 10-block
+ *    merge kernel combines the log-sum-exp partials.
+ *  - The MoE router logits are computed by spare blocks of the shared-expert
+ *    gate/up launch; the routed gate/up and down-combine kernels recompute
+ *    the greedy top-6 from the 64 logits in one wavefront (64-bit keys of
+ *    probability bits and inverted id, so ties go to the lower id).
+ *  - The down-combine kernel fuses the 6 routed down projections, their
+ *    weighted sum, the shared-expert down GEMV and the residual add.
+ *  - The LM head is a fused final-RMSNorm GEMV writing per-block argmax
+ *    partials; a one-block finalize picks the token (NaN rows skipped, ties to
+ *    the lowest id), advances the device-side step state and gathers the next
+ *    token's embedding row, so a captured decode graph can be replayed.
+ * No kernel waits on another block and none uses a device-scope fence
+ * (on gfx950 one costs an L2 writeback and invalidate per wavefront); every
+ * cross-block hand-off is a kernel boundary.
  */
 #include "uocr_kernels.h"
 
@@ -200,78 +203,135 @@ __device__ __forceinline__ float chunk_dot<1>(const uint4 w, const h16 *xs, uint
     return s;
 }
 
-/* NR independent row dots by one wavefront; loads of all NR rows are issued
- * before any arithmetic.  Returns wave-uniform results. */
-template <int QT, int NR>
-__device__ __forceinline__ void rows_dot(const uint8_t *const *W, const h16 *const *S, const h16 *const *X,
-                                         uint32_t C, uint32_t lane, float *out) {
-    float acc[NR];
+/* Sum over aligned groups of LPR lanes; every lane receives its group's sum.
+ * DPP quad/half-row/row permutes inside 16-lane rows, then lane swizzles. */
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+    if (LPR >= 2) v += dpp_f<0xB1>(v);
+    if (LPR >= 4) v += dpp_f<0x4E>(v);
+    if (LPR >= 8) v += dpp_f<0x141>(v);
+    if (LPR >= 16) v += dpp_f<0x140>(v);
+    if (LPR >= 32) v += __shfl_xor(v, 16);
+    if (LPR >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+/* Row dots by a group of LPR lanes: lane `sub` of the group owns the 16-byte
+ * chunks sub, sub+LPR, ... of its row.  The first J chunks of every one of the
+ * NM rows are loaded (with their scales) before any arithmetic, so a wave
+ * keeps 64*J*NM loads in flight; chunks past J*LPR fall to a tail loop.  W, S,
+ * X are per-lane pointers (row payload, row scales, activation in LDS).
+ * Every lane receives the NM dot products of its group. */
+template <int QT, int LPR, int J, int NM>
+__device__ __forceinline__ void group_dot(const uint8_t *const *W, const h16 *const *S, const h16 *const *X,
+                                          uint32_t C, uint32_t sub, float *out) {
+    uint4 w[NM][J];
+    float sc[NM][J];
 #pragma unroll
-    for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
-    for (uint32_t c = lane; c < C; c += 64u) {
-        uint4 w[NR];
-        float sc[NR];
+    for (int j = 0; j < J; ++j) {
+        const uint32_t c = sub + LPR * j;
 #pragma unroll
-        for (int r = 0; r < NR; ++r) w[r] = *(const uint4 *)(W[r] + 16u * c);
-        if (QT != 1) {
-#pragma unroll
-            for (int r = 0; r < NR; ++r) sc[r] = (float)S[r][chunk_group<QT>(c)];
+        for (int m = 0; m < NM; ++m) {
+            w[m][j] = c < C ? *(const uint4 *)(W[m] + 16u * c) : make_uint4(0u, 0u, 0u, 0u);
+            if (QT != 1) sc[m][j] = c < C ? (float)S[m][chunk_group<QT>(c)] : 0.0f;
         }
+    }
+    float acc[NM];
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const float d = chunk_dot<QT>(w[r], X[r], c);
-            acc[r] = QT == 1 ? acc[r] + d : fmaf(d, sc[r], acc[r]);
+    for (int m = 0; m < NM; ++m) acc[m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t c = sub + LPR * j;
+        if (c < C) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const float d = chunk_dot<QT>(w[m][j], X[m], c);
+                acc[m] = QT == 1 ? acc[m] + d : fmaf(d, sc[m][j], acc[m]);
+            }
+        }
+    }
+    for (uint32_t c = sub + LPR * J; c < C; c += LPR) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const float d = chunk_dot<QT>(*(const uint4 *)(W[m] + 16u * c), X[m], c);
+            acc[m] = QT == 1 ? acc[m] + d : fmaf(d, (float)S[m][chunk_group<QT>(c)], acc[m]);
         }
     }
 #pragma unroll
-    for (int r = 0; r < NR; ++r) out[r] = wave_sum(acc[r]);
+    for (int m = 0; m < NM; ++m) out[m] = group_sum<LPR>(acc[m]);
+}
+
+/* Greedy top-6 over 64 router logits by one wavefront (one expert per lane):
+ * max-subtracted softmax, then 6 rounds of a 64-bit max over
+ * (probability bits, inverted id) so ties go to the lower id
+ * (uocr_cpu_ref.c:443-463, moe.metal:12-18).  Raw probabilities unless
+ * norm_topk.  Results land in ids/w (LDS). */
+__device__ __forceinline__ void topk6_wave(const float *logits, int norm_topk, uint32_t *ids, float *w) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const float lg = logits[lane];
+    const float mx = wave_max(lg);
+    const float pe = expf(lg - mx);
+    const float prob = pe / wave_sum(pe);
+    unsigned long long key = ((unsigned long long)__float_as_uint(prob) << 32) | (0xffffffffu - lane);
+    float sel[UOCR_K_TOPK];
+    uint32_t sid[UOCR_K_TOPK];
+    float tot = 0.0f;
+#pragma unroll
+    for (int r = 0; r < UOCR_K_TOPK; ++r) {
+        const unsigned long long best = wave_max_u64(key);
+        sid[r] = 0xffffffffu - (uint32_t)(best & 0xffffffffull);
+        sel[r] = __uint_as_float((uint32_t)(best >> 32));
+        tot += sel[r];
+        if (lane == sid[r]) key = 0ull;
+    }
+    if (lane == 0u) {
+#pragma unroll
+        for (int r = 0; r < UOCR_K_TOPK; ++r) {
+            ids[r] = sid[r];
+            w[r] = norm_topk ? sel[r] / tot : sel[r];
+        }
+    }
 }
 
 /* ------------------------------------------------------------------------ */
 /* GEMV family                                                               */
 /* ------------------------------------------------------------------------ */
 
+#define GBLOCK 128 /* GEMV-family workgroup: 2 wavefronts */
+
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 
-template <int QT, int EPI>
-__global__ __launch_bounds__(BLOCK) void k_gemv(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
-                                                const uint8_t *__restrict__ W2, const h16 *__restrict__ S2,
-                                                uint32_t rows, uint32_t K, const h16 *__restrict__ x,
-                                                const h16 *__restrict__ nw, const h16 *__restrict__ res,
-                                                h16 *__restrict__ y, uint32_t rpb) {
+template <int QT, int LPR, int EPI>
+__global__ __launch_bounds__(GBLOCK) void k_gemv(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
+                                                 const uint8_t *__restrict__ W2, const h16 *__restrict__ S2,
+                                                 uint32_t rows, uint32_t K, const h16 *__restrict__ x,
+                                                 const h16 *__restrict__ nw, const h16 *__restrict__ res,
+                                                 h16 *__restrict__ y, uint32_t rpb) {
+    constexpr uint32_t R = 64u / LPR;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_MAX_K];
     __shared__ float red[16];
     stage_x(xs, x, nw, (int)K, red);
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    const uint32_t sub = lane % LPR, grp = lane / LPR;
     const uint32_t rb = row_bytes<QT>(K), C = rb / 16u, G = K / 64u;
-    const uint32_t r0 = blockIdx.x * rpb;
-    const uint32_t r1 = min(rows, r0 + rpb);
-    if (EPI == EPI_SWIGLU) {
-        for (uint32_t r = r0 + wave; r < r1; r += 4u) {
-            const uint8_t *Wp[2] = {W + (size_t)r * rb, W2 + (size_t)r * rb};
-            const h16 *Sp[2] = {S + (size_t)r * G, S2 + (size_t)r * G};
+    const uint32_t r0 = blockIdx.x * rpb, r1 = min(rows, r0 + rpb);
+    for (uint32_t base = r0 + wave * R; base < r1; base += nwave * R) {
+        const uint32_t r = base + grp;
+        const uint32_t rr = r < r1 ? r : r1 - 1u;
+        if (EPI == EPI_SWIGLU) {
+            const uint8_t *Wp[2] = {W + (size_t)rr * rb, W2 + (size_t)rr * rb};
+            const h16 *Sp[2] = {S + (size_t)rr * G, S2 + (size_t)rr * G};
             const h16 *Xp[2] = {xs, xs};
             float d[2];
-            rows_dot<QT, 2>(Wp, Sp, Xp, C, lane, d);
-            if (lane == 0u) y[r] = (h16)(silu_f(d[0]) * d[1]);
-        }
-    } else {
-        for (uint32_t r = r0 + wave; r < r1; r += 8u) {
-            const uint32_t rr = (r + 4u < r1) ? r + 4u : r;
-            const uint8_t *Wp[2] = {W + (size_t)r * rb, W + (size_t)rr * rb};
-            const h16 *Sp[2] = {S + (size_t)r * G, S + (size_t)rr * G};
-            const h16 *Xp[2] = {xs, xs};
-            float d[2];
-            rows_dot<QT, 2>(Wp, Sp, Xp, C, lane, d);
-            if (lane == 0u) {
-                if (EPI == EPI_RESID) {
-                    y[r] = (h16)(d[0] + (float)res[r]);
-                    if (rr != r) y[rr] = (h16)(d[1] + (float)res[rr]);
-                } else {
-                    y[r] = (h16)d[0];
-                    if (rr != r) y[rr] = (h16)d[1];
-                }
-            }
+            group_dot<QT, LPR, 8, 2>(Wp, Sp, Xp, C, sub, d);
+            if (r < r1 && sub == 0u) y[r] = (h16)(silu_f(d[0]) * d[1]);
+        } else {
+            const uint8_t *Wp[1] = {W + (size_t)rr * rb};
+            const h16 *Sp[1] = {S + (size_t)rr * G};
+            const h16 *Xp[1] = {xs};
+            float d[1];
+            group_dot<QT, LPR, 8, 1>(Wp, Sp, Xp, C, sub, d);
+            if (r < r1 && sub == 0u) y[r] = (h16)(EPI == EPI_RESID ? d[0] + (float)res[r] : d[0]);
         }
     }
 }
@@ -296,23 +356,28 @@ struct RopeTab {
     float f[UOCR_K_HEAD_DIM / 2];
 };
 
-/* Work item i (0..1919): matrix m = i/640 (q,k,v), head h, pair d; the wave
- * computes rows h*128+d and h*128+d+64 of matrix m. */
-template <int QT>
-__global__ __launch_bounds__(BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, uocr_qmat V, const h16 *__restrict__ hin,
-                                                    const h16 *__restrict__ nw, RopeTab rope,
-                                                    const uocr_step_state *__restrict__ st, h16 *__restrict__ qout,
-                                                    h16 *__restrict__ kc, h16 *__restrict__ vc, uint32_t cap,
-                                                    uint32_t ipb) {
+/* Work item i (0..1919): matrix m = i/640 (q,k,v), head h, pair d; a lane
+ * group computes rows h*128+d and h*128+d+64 of matrix m, rounds them to
+ * fp16, rotates q/k by the split-half RoPE at st->pos and stores q, or k/v
+ * into the cache slot st->cache_token. */
+template <int QT, int LPR>
+__global__ __launch_bounds__(GBLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, uocr_qmat V, const h16 *__restrict__ hin,
+                                                     const h16 *__restrict__ nw, RopeTab rope,
+                                                     const uocr_step_state *__restrict__ st, h16 *__restrict__ qout,
+                                                     h16 *__restrict__ kc, h16 *__restrict__ vc, uint32_t cap,
+                                                     uint32_t ipb) {
+    constexpr uint32_t R = 64u / LPR;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
     stage_x(xs, hin, nw, UOCR_K_HIDDEN, red);
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    const uint32_t sub = lane % LPR, grp = lane / LPR;
     const uint32_t K = UOCR_K_HIDDEN, rb = row_bytes<QT>(K), C = rb / 16u, G = K / 64u;
     const int32_t pos = st->pos;
     const uint32_t ct = (uint32_t)st->cache_token;
     const uint32_t i0 = blockIdx.x * ipb, i1 = min(1920u, i0 + ipb);
-    for (uint32_t it = i0 + wave; it < i1; it += 4u) {
+    for (uint32_t base = i0 + wave * R; base < i1; base += nwave * R) {
+        const uint32_t it = min(base + grp, i1 - 1u);
         const uint32_t m = it / 640u, rem = it % 640u, h = rem / 64u, d = rem % 64u;
         const uocr_qmat M = m == 0u ? Q : (m == 1u ? Km : V);
         const uint32_t ra = h * 128u + d, rbw = ra + 64u;
@@ -320,8 +385,8 @@ __global__ __launch_bounds__(BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, u
         const h16 *Sp[2] = {(const h16 *)M.s + (size_t)ra * G, (const h16 *)M.s + (size_t)rbw * G};
         const h16 *Xp[2] = {xs, xs};
         float dd[2];
-        rows_dot<QT, 2>(Wp, Sp, Xp, C, lane, dd);
-        if (lane == 0u) {
+        group_dot<QT, LPR, 8, 2>(Wp, Sp, Xp, C, sub, dd);
+        if (sub == 0u && base + grp < i1) {
             const h16 a = (h16)dd[0], b = (h16)dd[1];
             const size_t cix = ((size_t)h * cap + ct) * 128u + d;
             if (m == 2u) {
@@ -345,16 +410,19 @@ __global__ __launch_bounds__(BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, u
 }
 
 /* ------------------------------------------------------------------------ */
-/* split-K decode attention                                                  */
+/* split-K decode attention + merge                                          */
 /* ------------------------------------------------------------------------ */
 
+/* Block (s, h) covers attention indices [s*chunk, (s+1)*chunk) of head h:
+ * 16 lanes x 8 dims per cached token, 16 tokens per block in flight, an
+ * online softmax per 16-lane group, then a block merge into one (max, sum,
+ * acc[128]) partial.  Indices >= attn_prompt map into the 128-token ring
+ * (attention_decode.metal:25-33). */
 __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, const h16 *__restrict__ kc,
                                                      const h16 *__restrict__ vc, uint32_t cap,
-                                                     const uocr_step_state *__restrict__ st, float *part,
-                                                     uint32_t *cnt, h16 *__restrict__ ctx) {
+                                                     const uocr_step_state *__restrict__ st, float *__restrict__ part) {
     __shared__ float sm[16], sl[16];
     __shared__ float sacc[16][UOCR_K_HEAD_DIM];
-    __shared__ int is_last;
     const int h = blockIdx.y, s = blockIdx.x, S = gridDim.x;
     const int P = st->attn_prompt, L = st->attn_len, fg = st->first_gen;
     const int chunk = (L + S - 1) / S;
@@ -417,129 +485,139 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
             pp[0] = M;
             pp[1] = Ls;
         }
-        __threadfence();
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(&cnt[h], 1u);
-        is_last = (prev == (uint32_t)(S - 1));
+}
+
+/* Log-sum-exp merge of the S partials of one head -> fp16 context. */
+__global__ __launch_bounds__(UOCR_K_HEAD_DIM) void k_attention_merge(const float *__restrict__ part, uint32_t S,
+                                                                     h16 *__restrict__ ctx) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    const float *ph = part + (size_t)h * S * (UOCR_K_HEAD_DIM + 2);
+    float M = -INFINITY;
+    for (uint32_t k = 0; k < S; ++k) M = fmaxf(M, ph[(size_t)k * (UOCR_K_HEAD_DIM + 2)]);
+    float Ls = 0.0f, A = 0.0f;
+    for (uint32_t k = 0; k < S; ++k) {
+        const float *pk = ph + (size_t)k * (UOCR_K_HEAD_DIM + 2);
+        if (pk[0] == -INFINITY) continue;
+        const float f = expf(pk[0] - M);
+        Ls = fmaf(pk[1], f, Ls);
+        A = fmaf(pk[2 + d], f, A);
     }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    if (threadIdx.x < UOCR_K_HEAD_DIM) {
-        const int d = threadIdx.x;
-        const float *ph = part + (size_t)h * S * (UOCR_K_HEAD_DIM + 2);
-        float M = -INFINITY;
-        for (int k = 0; k < S; ++k) M = fmaxf(M, __builtin_nontemporal_load(ph + (size_t)k * (UOCR_K_HEAD_DIM + 2)));
-        float Ls = 0.0f, A = 0.0f;
-        for (int k = 0; k < S; ++k) {
-            const float *pk = ph + (size_t)k * (UOCR_K_HEAD_DIM + 2);
-            const float mk = __builtin_nontemporal_load(pk);
-            if (mk == -INFINITY) continue;
-            const float f = expf(mk - M);
-            Ls = fmaf(__builtin_nontemporal_load(pk + 1), f, Ls);
-            A = fmaf(__builtin_nontemporal_load(pk + 2 + d), f, A);
-        }
-        ctx[h * 128 + d] = (h16)(A / Ls);
-    }
-    if (threadIdx.x == 0) cnt[h] = 0u;
+    ctx[h * 128 + d] = (h16)(A / Ls);
 }
 
 /* ------------------------------------------------------------------------ */
-/* MoE router: one 1024-thread workgroup                                     */
+/* MoE: shared experts + router logits, routed gate/up, down-combine         */
 /* ------------------------------------------------------------------------ */
 
-__global__ __launch_bounds__(1024) void k_router(const h16 *__restrict__ R, const h16 *__restrict__ x,
-                                                 const h16 *__restrict__ nw, int norm_topk, uint32_t *ids,
-                                                 float *wts) {
+/* Blocks [0, nb_shared) compute the shared-expert SwiGLU rows (1792) and the
+ * remaining blocks the 64 router logits (fp16 rows, fp32 dot); both read the
+ * same RMSNorm'd input, so one launch serves both. */
+template <int QS, int LPRS>
+__global__ __launch_bounds__(GBLOCK) void k_moe_shared_router(uocr_qmat SG, uocr_qmat SU, const h16 *__restrict__ R,
+                                                              const h16 *__restrict__ x, const h16 *__restrict__ nw,
+                                                              h16 *__restrict__ smid, float *__restrict__ logits,
+                                                              uint32_t nb_shared, uint32_t rpb_shared,
+                                                              uint32_t rpb_router) {
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
-    __shared__ float logits[UOCR_K_EXPERTS];
     stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t rb = UOCR_K_HIDDEN * 2u, C = rb / 16u;
-    {
-        const uint32_t e0 = wave * 4u;
-        const uint8_t *Wp[4];
-        const h16 *Sp[4] = {nullptr, nullptr, nullptr, nullptr};
-        const h16 *Xp[4] = {xs, xs, xs, xs};
-        for (int j = 0; j < 4; ++j) Wp[j] = (const uint8_t *)R + (size_t)(e0 + j) * rb;
-        float d[4];
-        rows_dot<1, 4>(Wp, Sp, Xp, C, lane, d);
-        if (lane == 0u) {
-            for (int j = 0; j < 4; ++j) logits[e0 + j] = d[j];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    if (blockIdx.x < nb_shared) {
+        constexpr uint32_t RS = 64u / LPRS;
+        const uint32_t sub = lane % LPRS, grp = lane / LPRS;
+        const uint32_t rb = row_bytes<QS>(UOCR_K_HIDDEN), C = rb / 16u, G = UOCR_K_HIDDEN / 64u;
+        const uint32_t r0 = blockIdx.x * rpb_shared, r1 = min(1792u, r0 + rpb_shared);
+        for (uint32_t base = r0 + wave * RS; base < r1; base += nwave * RS) {
+            const uint32_t r = base + grp, rr = r < r1 ? r : r1 - 1u;
+            const uint8_t *Wp[2] = {(const uint8_t *)SG.w + (size_t)rr * rb, (const uint8_t *)SU.w + (size_t)rr * rb};
+            const h16 *Sp[2] = {(const h16 *)SG.s + (size_t)rr * G, (const h16 *)SU.s + (size_t)rr * G};
+            const h16 *Xp[2] = {xs, xs};
+            float d[2];
+            group_dot<QS, LPRS, 8, 2>(Wp, Sp, Xp, C, sub, d);
+            if (r < r1 && sub == 0u) smid[r] = (h16)(silu_f(d[0]) * d[1]);
         }
-    }
-    __syncthreads();
-    if (wave != 0u) return;
-    const float lg = logits[lane];
-    const float mx = wave_max(lg);
-    const float pe = expf(lg - mx);
-    const float den = wave_sum(pe);
-    const float prob = pe / den;
-    unsigned long long key = ((unsigned long long)__float_as_uint(prob) << 32) | (0xffffffffu - lane);
-    float sel_w[UOCR_K_TOPK];
-    uint32_t sel_id[UOCR_K_TOPK];
-    float tot = 0.0f;
-#pragma unroll
-    for (int r = 0; r < UOCR_K_TOPK; ++r) {
-        const unsigned long long best = wave_max_u64(key);
-        const uint32_t e = 0xffffffffu - (uint32_t)(best & 0xffffffffull);
-        sel_id[r] = e;
-        sel_w[r] = __uint_as_float((uint32_t)(best >> 32));
-        tot += sel_w[r];
-        if (lane == e) key = 0ull;
-    }
-    if (lane == 0u) {
-        for (int r = 0; r < UOCR_K_TOPK; ++r) {
-            ids[r] = sel_id[r];
-            wts[r] = norm_topk ? sel_w[r] / tot : sel_w[r];
+    } else {
+        constexpr uint32_t LPR = 32u, RR = 2u;
+        const uint32_t sub = lane % LPR, grp = lane / LPR;
+        const uint32_t rb = UOCR_K_HIDDEN * 2u, C = rb / 16u;
+        const uint32_t r0 = (blockIdx.x - nb_shared) * rpb_router, r1 = min(64u, r0 + rpb_router);
+        for (uint32_t base = r0 + wave * RR; base < r1; base += nwave * RR) {
+            const uint32_t r = base + grp, rr = r < r1 ? r : r1 - 1u;
+            const uint8_t *Wp[1] = {(const uint8_t *)R + (size_t)rr * rb};
+            const h16 *Sp[1] = {nullptr};
+            const h16 *Xp[1] = {xs};
+            float d[1];
+            group_dot<1, LPR, 8, 1>(Wp, Sp, Xp, C, sub, d);
+            if (r < r1 && sub == 0u) logits[r] = d[0];
         }
     }
 }
 
-/* ------------------------------------------------------------------------ */
-/* routed experts                                                            */
-/* ------------------------------------------------------------------------ */
+/* Router top-6 from logits (one wavefront). */
+__global__ __launch_bounds__(64) void k_router_topk(const float *__restrict__ logits, int norm_topk, uint32_t *ids,
+                                                    float *w) {
+    __shared__ uint32_t sid[UOCR_K_TOPK];
+    __shared__ float sw[UOCR_K_TOPK];
+    topk6_wave(logits, norm_topk, sid, sw);
+    __syncthreads();
+    if (threadIdx.x < UOCR_K_TOPK) {
+        ids[threadIdx.x] = sid[threadIdx.x];
+        w[threadIdx.x] = sw[threadIdx.x];
+    }
+}
 
-template <int QT>
-__global__ __launch_bounds__(BLOCK) void k_moe_gate_up(uocr_expert_slab sl, const uint32_t *__restrict__ ids,
-                                                       const h16 *__restrict__ x, const h16 *__restrict__ nw,
-                                                       h16 *__restrict__ mid, uint32_t rpb) {
+/* Routed gate/up: the block recomputes the top-6 from the logits, then
+ * mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = ids[r]. */
+template <int QT, int LPR>
+__global__ __launch_bounds__(GBLOCK) void k_moe_gate_up(uocr_expert_slab sl, const float *__restrict__ logits,
+                                                        int norm_topk, const h16 *__restrict__ x,
+                                                        const h16 *__restrict__ nw, h16 *__restrict__ mid,
+                                                        uint32_t *ids_out, float *w_out, uint32_t rpb) {
+    constexpr uint32_t R = 64u / LPR;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
+    __shared__ uint32_t sid[UOCR_K_TOPK];
+    __shared__ float sw[UOCR_K_TOPK];
+    if (threadIdx.x < 64u) topk6_wave(logits, norm_topk, sid, sw);
     stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    if (blockIdx.x == 0u && ids_out != nullptr && threadIdx.x < UOCR_K_TOPK) {
+        ids_out[threadIdx.x] = sid[threadIdx.x];
+        w_out[threadIdx.x] = sw[threadIdx.x];
+    }
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    const uint32_t sub = lane % LPR, grp = lane / LPR;
     const uint32_t I = 896u, K = UOCR_K_HIDDEN, rb = row_bytes<QT>(K), C = rb / 16u, G = K / 64u;
     const uint32_t rows = UOCR_K_TOPK * I;
     const uint32_t r0 = blockIdx.x * rpb, r1 = min(rows, r0 + rpb);
-    for (uint32_t r = r0 + wave; r < r1; r += 4u) {
-        const uint32_t rank = r / I, col = r % I;
-        const uint32_t e = ids[rank];
-        if (e >= UOCR_K_EXPERTS) {
-            if (lane == 0u) mid[r] = (h16)0.0f;
-            continue;
-        }
+    for (uint32_t base = r0 + wave * R; base < r1; base += nwave * R) {
+        const uint32_t r = base + grp, rr = r < r1 ? r : r1 - 1u;
+        const uint32_t rank = rr / I, col = rr % I;
+        const uint32_t e = sid[rank] < UOCR_K_EXPERTS ? sid[rank] : 0u;
         const uint8_t *Wp[2] = {(const uint8_t *)sl.gate.w + e * sl.gu_w_stride + (size_t)col * rb,
                                 (const uint8_t *)sl.up.w + e * sl.gu_w_stride + (size_t)col * rb};
         const h16 *Sp[2] = {(const h16 *)sl.gate.s + e * sl.gu_s_stride + (size_t)col * G,
                             (const h16 *)sl.up.s + e * sl.gu_s_stride + (size_t)col * G};
         const h16 *Xp[2] = {xs, xs};
         float d[2];
-        rows_dot<QT, 2>(Wp, Sp, Xp, C, lane, d);
-        if (lane == 0u) mid[r] = (h16)(silu_f(d[0]) * d[1]);
+        group_dot<QT, LPR, 8, 2>(Wp, Sp, Xp, C, sub, d);
+        if (r < r1 && sub == 0u) mid[r] = (h16)(silu_f(d[0]) * d[1]);
     }
 }
 
-template <int QT, int QS>
-__global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const uint32_t *__restrict__ ids,
-                                                    const float *__restrict__ wts, const h16 *__restrict__ mid,
-                                                    uocr_qmat SD, const h16 *__restrict__ smid,
-                                                    const h16 *__restrict__ res, h16 *__restrict__ out,
-                                                    uint32_t rpb) {
-    constexpr uint32_t I = 896u, SI = 1792u;
+/* Down projection of the 6 routed experts + weighted combine + shared-expert
+ * down + residual, one fp16 rounding:
+ * out[c] = f16(sum_r w_r * D_e[c].mid_r + f16(SD[c].smid) + res[c]). */
+template <int QT, int QS, int LPR>
+__global__ __launch_bounds__(GBLOCK) void k_moe_down(uocr_expert_slab sl, const float *__restrict__ logits,
+                                                     int norm_topk, const h16 *__restrict__ mid, uocr_qmat SD,
+                                                     const h16 *__restrict__ smid, const h16 *__restrict__ res,
+                                                     h16 *__restrict__ out, uint32_t rpb) {
+    constexpr uint32_t I = 896u, SI = 1792u, R = 64u / LPR;
     __shared__ __attribute__((aligned(16))) h16 ms[UOCR_K_TOPK * I + SI];
+    __shared__ uint32_t sid[UOCR_K_TOPK];
+    __shared__ float sw[UOCR_K_TOPK];
+    if (threadIdx.x < 64u) topk6_wave(logits, norm_topk, sid, sw);
     {
         const uint4 *a = (const uint4 *)mid;
         const uint4 *b = (const uint4 *)smid;
@@ -548,145 +626,42 @@ __global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const u
         for (uint32_t i = threadIdx.x; i < SI / 8u; i += blockDim.x) d[UOCR_K_TOPK * I / 8u + i] = b[i];
     }
     __syncthreads();
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    const uint32_t sub = lane % LPR, grp = lane / LPR;
     uint32_t e[UOCR_K_TOPK];
     float w[UOCR_K_TOPK];
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
-        const uint32_t id = ids[r];
-        e[r] = id < UOCR_K_EXPERTS ? id : 0u;
-        w[r] = id < UOCR_K_EXPERTS ? wts[r] : 0.0f;
+        e[r] = sid[r] < UOCR_K_EXPERTS ? sid[r] : 0u;
+        w[r] = sid[r] < UOCR_K_EXPERTS ? sw[r] : 0.0f;
     }
     const uint32_t rbD = row_bytes<QT>(I), CD = rbD / 16u, GD = I / 64u;
     const uint32_t rbS = row_bytes<QS>(SI), CS = rbS / 16u, GS = SI / 64u;
     const uint32_t r0 = blockIdx.x * rpb, r1 = min((uint32_t)UOCR_K_HIDDEN, r0 + rpb);
-    for (uint32_t c = r0 + wave; c < r1; c += 4u) {
+    for (uint32_t base = r0 + wave * R; base < r1; base += nwave * R) {
+        const uint32_t c = base + grp, cc = c < r1 ? c : r1 - 1u;
         const uint8_t *Wp[UOCR_K_TOPK];
         const h16 *Sp[UOCR_K_TOPK];
         const h16 *Xp[UOCR_K_TOPK];
 #pragma unroll
         for (int r = 0; r < UOCR_K_TOPK; ++r) {
-            Wp[r] = (const uint8_t *)sl.down.w + e[r] * sl.dn_w_stride + (size_t)c * rbD;
-            Sp[r] = (const h16 *)sl.down.s + e[r] * sl.dn_s_stride + (size_t)c * GD;
+            Wp[r] = (const uint8_t *)sl.down.w + e[r] * sl.dn_w_stride + (size_t)cc * rbD;
+            Sp[r] = (const h16 *)sl.down.s + e[r] * sl.dn_s_stride + (size_t)cc * GD;
             Xp[r] = ms + r * I;
         }
         float d[UOCR_K_TOPK];
-        rows_dot<QT, UOCR_K_TOPK>(Wp, Sp, Xp, CD, lane, d);
-        const uint8_t *Ws[1] = {(const uint8_t *)SD.w + (size_t)c * rbS};
-        const h16 *Ss[1] = {(const h16 *)SD.s + (size_t)c * GS};
+        group_dot<QT, LPR, 2, UOCR_K_TOPK>(Wp, Sp, Xp, CD, sub, d);
+        const uint8_t *Ws[1] = {(const uint8_t *)SD.w + (size_t)cc * rbS};
+        const h16 *Ss[1] = {(const h16 *)SD.s + (size_t)cc * GS};
         const h16 *Xs[1] = {ms + UOCR_K_TOPK * I};
         float sd[1];
-        rows_dot<QS, 1>(Ws, Ss, Xs, CS, lane, sd);
-        if (lane == 0u) {
+        group_dot<QS, LPR, 4, 1>(Ws, Ss, Xs, CS, sub, sd);
+        if (c < r1 && sub == 0u) {
             float acc = 0.0f;
 #pragma unroll
             for (int r = 0; r < UOCR_K_TOPK; ++r) acc = fmaf(w[r], d[r], acc);
             out[c] = (h16)(acc + (float)(h16)sd[0] + (float)res[c]);
         }
-    }
-}
-
-/* ------------------------------------------------------------------------ */
-/* LM head + argmax                                                          */
-/* ------------------------------------------------------------------------ */
-
-__device__ __forceinline__ bool better(float s, uint32_t id, float bs, uint32_t bid) {
-    return id != NONE_ID && (bid == NONE_ID || s > bs || (s == bs && id < bid));
-}
-
-template <int QT>
-__global__ __launch_bounds__(BLOCK) void k_lm_head(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
-                                                   uint32_t vocab, const h16 *__restrict__ x,
-                                                   const h16 *__restrict__ nw, uint32_t *part, uint32_t *cnt,
-                                                   uocr_step_state *st, int advance, int32_t *tokens,
-                                                   float *scores, uint32_t rpb) {
-    __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
-    __shared__ float red[16];
-    __shared__ float bsc[BLOCK];
-    __shared__ uint32_t bidv[BLOCK];
-    __shared__ int is_last;
-    stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t K = UOCR_K_HIDDEN, rb = row_bytes<QT>(K), C = rb / 16u, G = K / 64u;
-    const uint32_t r0 = blockIdx.x * rpb, r1 = min(vocab, r0 + rpb);
-    float bs = -INFINITY;
-    uint32_t bid = NONE_ID;
-    for (uint32_t r = r0 + wave; r < r1; r += 8u) {
-        const uint32_t rr = (r + 4u < r1) ? r + 4u : r;
-        const uint8_t *Wp[2] = {W + (size_t)r * rb, W + (size_t)rr * rb};
-        const h16 *Sp[2] = {S + (size_t)r * G, S + (size_t)rr * G};
-        const h16 *Xp[2] = {xs, xs};
-        float d[2];
-        rows_dot<QT, 2>(Wp, Sp, Xp, C, lane, d);
-        if (!isnan(d[0]) && better(d[0], r, bs, bid)) {
-            bs = d[0];
-            bid = r;
-        }
-        if (rr != r && !isnan(d[1]) && better(d[1], rr, bs, bid)) {
-            bs = d[1];
-            bid = rr;
-        }
-    }
-    if (lane == 0u) {
-        bsc[wave] = bs;
-        bidv[wave] = bid;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float b = -INFINITY;
-        uint32_t bi = NONE_ID;
-        for (int i = 0; i < BLOCK / 64; ++i) {
-            if (better(bsc[i], bidv[i], b, bi)) {
-                b = bsc[i];
-                bi = bidv[i];
-            }
-        }
-        part[2u * blockIdx.x] = __float_as_uint(b);
-        part[2u * blockIdx.x + 1u] = bi;
-        __threadfence();
-        const uint32_t prev = atomicAdd(cnt, 1u);
-        is_last = (prev == gridDim.x - 1u);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    float b = -INFINITY;
-    uint32_t bi = NONE_ID;
-    for (uint32_t i = threadIdx.x; i < gridDim.x; i += blockDim.x) {
-        const float s = __uint_as_float(__builtin_nontemporal_load(part + 2u * i));
-        const uint32_t id = __builtin_nontemporal_load(part + 2u * i + 1u);
-        if (better(s, id, b, bi)) {
-            b = s;
-            bi = id;
-        }
-    }
-    bsc[threadIdx.x] = b;
-    bidv[threadIdx.x] = bi;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int i = 1; i < BLOCK; ++i) {
-            if (better(bsc[i], bidv[i], b, bi)) {
-                b = bsc[i];
-                bi = bidv[i];
-            }
-        }
-        const int32_t id = bi == NONE_ID ? 0 : (int32_t)bi;
-        const int32_t t = st != nullptr ? st->t : 0;
-        tokens[t] = id;
-        if (scores != nullptr) scores[t] = bi == NONE_ID ? -INFINITY : b;
-        if (st != nullptr && advance) {
-            const int32_t P = st->prompt_len;
-            const int32_t gcount = t + 1;
-            const int32_t live = gcount < UOCR_K_RING ? gcount : UOCR_K_RING;
-            st->cur_token = id;
-            st->pos = P + t;
-            st->cache_token = P + (t % UOCR_K_RING);
-            st->attn_prompt = P;
-            st->attn_len = P + live;
-            st->first_gen = gcount - live;
-            st->t = t + 1;
-        }
-        *cnt = 0u;
     }
 }
 
@@ -777,6 +752,118 @@ __global__ void k_decode_state(uocr_step_state *st, int32_t P, int32_t t) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* LM head + argmax                                                          */
+/* ------------------------------------------------------------------------ */
+
+__device__ __forceinline__ bool better(float s, uint32_t id, float bs, uint32_t bid) {
+    return id != NONE_ID && (bid == NONE_ID || s > bs || (s == bs && id < bid));
+}
+
+/* Pass 1: fused final RMSNorm + GEMV over vocab rows; each block writes its
+ * best (score, id) with NaN rows skipped and ties to the lowest id. */
+template <int QT, int LPR>
+__global__ __launch_bounds__(GBLOCK) void k_lm_head(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
+                                                    uint32_t vocab, const h16 *__restrict__ x,
+                                                    const h16 *__restrict__ nw, uint32_t *__restrict__ part,
+                                                    uint32_t rpb) {
+    constexpr uint32_t R = 64u / LPR;
+    __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
+    __shared__ float red[16];
+    __shared__ float bsc[GBLOCK];
+    __shared__ uint32_t bidv[GBLOCK];
+    stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    const uint32_t sub = lane % LPR, grp = lane / LPR;
+    const uint32_t K = UOCR_K_HIDDEN, rb = row_bytes<QT>(K), C = rb / 16u, G = K / 64u;
+    const uint32_t r0 = blockIdx.x * rpb, r1 = min(vocab, r0 + rpb);
+    float bs = -INFINITY;
+    uint32_t bid = NONE_ID;
+    for (uint32_t base = r0 + wave * R; base < r1; base += nwave * R) {
+        const uint32_t r = base + grp, rr = r < r1 ? r : r1 - 1u;
+        const uint8_t *Wp[1] = {W + (size_t)rr * rb};
+        const h16 *Sp[1] = {S + (size_t)rr * G};
+        const h16 *Xp[1] = {xs};
+        float d[1];
+        group_dot<QT, LPR, 8, 1>(Wp, Sp, Xp, C, sub, d);
+        if (r < r1 && !isnan(d[0]) && better(d[0], r, bs, bid)) {
+            bs = d[0];
+            bid = r;
+        }
+    }
+    bsc[threadIdx.x] = bs;
+    bidv[threadIdx.x] = bid;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = -INFINITY;
+        uint32_t bi = NONE_ID;
+        for (uint32_t i = 0; i < blockDim.x; i += LPR) {
+            if (better(bsc[i], bidv[i], b, bi)) {
+                b = bsc[i];
+                bi = bidv[i];
+            }
+        }
+        part[2u * blockIdx.x] = __float_as_uint(b);
+        part[2u * blockIdx.x + 1u] = bi;
+    }
+}
+
+/* Pass 2 (one block): reduce the partials to the token id (none valid -> 0,
+ * score -inf), store it at tokens[state->t] (or [0] without state); with
+ * advance, write the next decode position into *state (uocr_metal.m:14239
+ * and the ring plan of attention_decode.metal:25-33) and gather the selected
+ * token's embedding row into h (embedding_q4.metal:21-56). */
+template <int QE>
+__global__ __launch_bounds__(BLOCK) void k_lm_finalize(const uint32_t *__restrict__ part, uint32_t nparts,
+                                                       uocr_step_state *st, int advance, int32_t *tokens,
+                                                       float *scores, const uint8_t *__restrict__ EW,
+                                                       const h16 *__restrict__ ES, uint32_t vocab,
+                                                       h16 *__restrict__ hout) {
+    __shared__ float bsc[BLOCK];
+    __shared__ uint32_t bidv[BLOCK];
+    __shared__ int32_t chosen;
+    float b = -INFINITY;
+    uint32_t bi = NONE_ID;
+    for (uint32_t i = threadIdx.x; i < nparts; i += blockDim.x) {
+        const float s = __uint_as_float(part[2u * i]);
+        const uint32_t id = part[2u * i + 1u];
+        if (better(s, id, b, bi)) {
+            b = s;
+            bi = id;
+        }
+    }
+    bsc[threadIdx.x] = b;
+    bidv[threadIdx.x] = bi;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t i = 1; i < blockDim.x; ++i) {
+            if (better(bsc[i], bidv[i], b, bi)) {
+                b = bsc[i];
+                bi = bidv[i];
+            }
+        }
+        const int32_t id = bi == NONE_ID ? 0 : (int32_t)bi;
+        const int32_t t = st != nullptr ? st->t : 0;
+        tokens[t] = id;
+        if (scores != nullptr) scores[t] = bi == NONE_ID ? -INFINITY : b;
+        if (st != nullptr && advance) {
+            const int32_t P = st->prompt_len;
+            const int32_t gcount = t + 1;
+            const int32_t live = gcount < UOCR_K_RING ? gcount : UOCR_K_RING;
+            st->cur_token = id;
+            st->pos = P + t;
+            st->cache_token = P + (t % UOCR_K_RING);
+            st->attn_prompt = P;
+            st->attn_len = P + live;
+            st->first_gen = gcount - live;
+            st->t = t + 1;
+        }
+        chosen = id;
+    }
+    __syncthreads();
+    if (advance && EW != nullptr) k_embed_row_body<QE>(EW, ES, vocab, chosen, hout);
+}
+
+/* ------------------------------------------------------------------------ */
 /* launchers                                                                 */
 /* ------------------------------------------------------------------------ */
 
@@ -788,11 +875,22 @@ static bool mat_ok(uocr_qmat m) {
     return m.w != nullptr && qt_ok(m.qtype) && (m.qtype == UOCR_QT_F16 || m.s != nullptr);
 }
 
-static uint32_t rows_per_block(uint32_t rows, uint32_t target_blocks) {
-    uint32_t rpb = (rows + target_blocks - 1u) / target_blocks;
-    rpb = (rpb + 3u) & ~3u;
-    return rpb < 4u ? 4u : rpb;
+static uint32_t chunks_of(uint32_t qt, uint32_t K) {
+    return (qt == UOCR_QT_Q4 ? K / 2u : (qt == UOCR_QT_Q8 ? K : 2u * K)) / 16u;
 }
+
+/* lanes per row: the smallest group that covers a row in at most 8 loads */
+static uint32_t pick_lpr(uint32_t C) {
+    for (uint32_t l = 4u; l < 64u; l *= 2u) {
+        if (C <= 8u * l) return l;
+    }
+    return 64u;
+}
+
+/* K = 1280 rows: Q4 -> 8 lanes, Q8 -> 16, f16 -> 32 (5 loads per lane) */
+#define LPR_1280(QT) ((QT) == 4 ? 8 : ((QT) == 3 ? 16 : 32))
+/* K = 896 with 2 loads per lane: Q4 -> 16, Q8 -> 32, f16 -> 64 */
+#define LPR_896(QT) ((QT) == 4 ? 16 : ((QT) == 3 ? 32 : 64))
 
 #define DISPATCH_QT(qt, F, ...)                                      \
     do {                                                             \
@@ -803,22 +901,36 @@ static uint32_t rows_per_block(uint32_t rows, uint32_t target_blocks) {
         }                                                            \
     } while (0)
 
-template <int QT>
-static void launch_gemv_qt(hipStream_t st, int epi, uocr_qmat W, uocr_qmat W2, uint32_t rows, uint32_t K,
-                           const uint16_t *x, const uint16_t *nw, const uint16_t *res, uint16_t *y) {
-    const uint32_t rpb = rows_per_block(rows, 512u);
+template <int QT, int LPR>
+static void launch_gemv_l(hipStream_t st, int epi, uocr_qmat W, uocr_qmat W2, uint32_t rows, uint32_t K,
+                          const uint16_t *x, const uint16_t *nw, const uint16_t *res, uint16_t *y) {
+    const uint32_t pass = 2u * (64u / LPR);
+    const uint32_t passes = (rows + pass * 1024u - 1u) / (pass * 1024u);
+    const uint32_t rpb = pass * passes;
     const dim3 grid((rows + rpb - 1u) / rpb);
     const uint8_t *w = (const uint8_t *)W.w, *w2 = (const uint8_t *)W2.w;
     const h16 *s = (const h16 *)W.s, *s2 = (const h16 *)W2.s;
     if (epi == EPI_SWIGLU) {
-        hipLaunchKernelGGL((k_gemv<QT, EPI_SWIGLU>), grid, dim3(BLOCK), 0, st, w, s, w2, s2, rows, K, (const h16 *)x,
-                           (const h16 *)nw, (const h16 *)res, (h16 *)y, rpb);
+        hipLaunchKernelGGL((k_gemv<QT, LPR, EPI_SWIGLU>), grid, dim3(GBLOCK), 0, st, w, s, w2, s2, rows, K,
+                           (const h16 *)x, (const h16 *)nw, (const h16 *)res, (h16 *)y, rpb);
     } else if (epi == EPI_RESID) {
-        hipLaunchKernelGGL((k_gemv<QT, EPI_RESID>), grid, dim3(BLOCK), 0, st, w, s, w2, s2, rows, K, (const h16 *)x,
-                           (const h16 *)nw, (const h16 *)res, (h16 *)y, rpb);
+        hipLaunchKernelGGL((k_gemv<QT, LPR, EPI_RESID>), grid, dim3(GBLOCK), 0, st, w, s, w2, s2, rows, K,
+                           (const h16 *)x, (const h16 *)nw, (const h16 *)res, (h16 *)y, rpb);
     } else {
-        hipLaunchKernelGGL((k_gemv<QT, EPI_STORE>), grid, dim3(BLOCK), 0, st, w, s, w2, s2, rows, K, (const h16 *)x,
-                           (const h16 *)nw, (const h16 *)res, (h16 *)y, rpb);
+        hipLaunchKernelGGL((k_gemv<QT, LPR, EPI_STORE>), grid, dim3(GBLOCK), 0, st, w, s, w2, s2, rows, K,
+                           (const h16 *)x, (const h16 *)nw, (const h16 *)res, (h16 *)y, rpb);
+    }
+}
+
+template <int QT>
+static void launch_gemv_qt(hipStream_t st, int epi, uocr_qmat W, uocr_qmat W2, uint32_t rows, uint32_t K,
+                           const uint16_t *x, const uint16_t *nw, const uint16_t *res, uint16_t *y) {
+    switch (pick_lpr(chunks_of(QT, K))) {
+        case 4: launch_gemv_l<QT, 4>(st, epi, W, W2, rows, K, x, nw, res, y); break;
+        case 8: launch_gemv_l<QT, 8>(st, epi, W, W2, rows, K, x, nw, res, y); break;
+        case 16: launch_gemv_l<QT, 16>(st, epi, W, W2, rows, K, x, nw, res, y); break;
+        case 32: launch_gemv_l<QT, 32>(st, epi, W, W2, rows, K, x, nw, res, y); break;
+        default: launch_gemv_l<QT, 64>(st, epi, W, W2, rows, K, x, nw, res, y); break;
     }
 }
 
@@ -853,9 +965,10 @@ template <int QT>
 static void launch_qkv_qt(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
                           const uint16_t *nw, const RopeTab &tab, const uocr_step_state *state, uint16_t *qout,
                           uint16_t *kc, uint16_t *vc, uint32_t cap) {
-    const uint32_t ipb = 8u;
-    hipLaunchKernelGGL((k_qkv_rope<QT>), dim3(1920u / ipb), dim3(BLOCK), 0, st, Q, K, V, (const h16 *)h,
-                       (const h16 *)nw, tab, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap, ipb);
+    constexpr int LPR = LPR_1280(QT);
+    const uint32_t ipb = 2u * (64u / LPR);
+    hipLaunchKernelGGL((k_qkv_rope<QT, LPR>), dim3((1920u + ipb - 1u) / ipb), dim3(GBLOCK), 0, st, Q, K, V,
+                       (const h16 *)h, (const h16 *)nw, tab, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap, ipb);
 }
 
 extern "C" hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
@@ -875,96 +988,140 @@ extern "C" hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qma
 
 extern "C" hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache,
                                             const uint16_t *vcache, uint32_t cache_capacity,
-                                            const uocr_step_state *state, float *partials, uint32_t *counters,
-                                            uint16_t *ctx) {
+                                            const uocr_step_state *state, float *partials, uint16_t *ctx) {
     if (q == nullptr || kcache == nullptr || vcache == nullptr || cache_capacity == 0u || state == nullptr ||
-        partials == nullptr || counters == nullptr || ctx == nullptr) {
+        partials == nullptr || ctx == nullptr) {
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(k_attention, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(BLOCK), 0, st, (const h16 *)q,
-                       (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials, counters,
-                       (h16 *)ctx);
+                       (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials);
+    hipLaunchKernelGGL(k_attention_merge, dim3(UOCR_K_HEADS), dim3(UOCR_K_HEAD_DIM), 0, st, (const float *)partials,
+                       (uint32_t)UOCR_K_ATTN_SPLITS, (h16 *)ctx);
+    return hipGetLastError();
+}
+
+template <int QS>
+static void launch_shared_router_qs(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R, const uint16_t *x,
+                                    const uint16_t *nw, uint16_t *smid, float *logits, bool with_shared) {
+    constexpr int LPRS = LPR_1280(QS);
+    const uint32_t rpb_s = 2u * (64u / LPRS);
+    const uint32_t nb_s = with_shared ? (1792u + rpb_s - 1u) / rpb_s : 0u;
+    const uint32_t rpb_r = 4u, nb_r = 64u / rpb_r;
+    hipLaunchKernelGGL((k_moe_shared_router<QS, LPRS>), dim3(nb_s + nb_r), dim3(GBLOCK), 0, st, SG, SU,
+                       (const h16 *)R, (const h16 *)x, (const h16 *)nw, (h16 *)smid, logits, nb_s, rpb_s, rpb_r);
+}
+
+extern "C" hipError_t uocr_launch_moe_shared_router(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R,
+                                                    const uint16_t *x, const uint16_t *nw, uint16_t *smid,
+                                                    float *logits) {
+    if (!mat_ok(SG) || !mat_ok(SU) || SG.qtype != SU.qtype || R == nullptr || x == nullptr || smid == nullptr ||
+        logits == nullptr) {
+        return hipErrorInvalidValue;
+    }
+    DISPATCH_QT(SG.qtype, launch_shared_router_qs, st, SG, SU, R, x, nw, smid, logits, true);
     return hipGetLastError();
 }
 
 extern "C" hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, const uint16_t *x, const uint16_t *nw,
-                                         int norm_topk, uint32_t *ids, float *weights) {
-    if (R == nullptr || x == nullptr || ids == nullptr || weights == nullptr) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_router, dim3(1), dim3(1024), 0, st, (const h16 *)R, (const h16 *)x, (const h16 *)nw,
-                       norm_topk, ids, weights);
+                                         int norm_topk, float *logits, uint32_t *ids, float *weights) {
+    if (R == nullptr || x == nullptr || logits == nullptr || ids == nullptr || weights == nullptr) {
+        return hipErrorInvalidValue;
+    }
+    uocr_qmat none = {R, nullptr, UOCR_QT_F16};
+    launch_shared_router_qs<1>(st, none, none, R, x, nw, nullptr, logits, false);
+    hipLaunchKernelGGL(k_router_topk, dim3(1), dim3(64), 0, st, (const float *)logits, norm_topk, ids, weights);
     return hipGetLastError();
 }
 
 template <int QT>
-static void launch_moe_gu_qt(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids, const uint16_t *x,
-                             const uint16_t *nw, uint16_t *mid) {
+static void launch_moe_gu_qt(hipStream_t st, const uocr_expert_slab *slab, const float *logits, int norm_topk,
+                             const uint16_t *x, const uint16_t *nw, uint16_t *mid, uint32_t *ids_out, float *w_out) {
+    constexpr int LPR = LPR_1280(QT);
     const uint32_t rows = UOCR_K_TOPK * 896u;
-    const uint32_t rpb = rows_per_block(rows, 512u);
-    hipLaunchKernelGGL((k_moe_gate_up<QT>), dim3((rows + rpb - 1u) / rpb), dim3(BLOCK), 0, st, *slab, ids,
-                       (const h16 *)x, (const h16 *)nw, (h16 *)mid, rpb);
+    const uint32_t rpb = 2u * (64u / LPR);
+    hipLaunchKernelGGL((k_moe_gate_up<QT, LPR>), dim3((rows + rpb - 1u) / rpb), dim3(GBLOCK), 0, st, *slab, logits,
+                       norm_topk, (const h16 *)x, (const h16 *)nw, (h16 *)mid, ids_out, w_out, rpb);
 }
 
-extern "C" hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
-                                              const uint16_t *x, const uint16_t *nw, uint16_t *mid) {
+extern "C" hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, const float *logits,
+                                              int norm_topk, const uint16_t *x, const uint16_t *nw, uint16_t *mid,
+                                              uint32_t *ids_out, float *weights_out) {
     if (slab == nullptr || !mat_ok(slab->gate) || !mat_ok(slab->up) || slab->gate.qtype != slab->up.qtype ||
-        ids == nullptr || x == nullptr || mid == nullptr) {
+        logits == nullptr || x == nullptr || mid == nullptr || ((ids_out == nullptr) != (weights_out == nullptr))) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(slab->gate.qtype, launch_moe_gu_qt, st, slab, ids, x, nw, mid);
+    DISPATCH_QT(slab->gate.qtype, launch_moe_gu_qt, st, slab, logits, norm_topk, x, nw, mid, ids_out, weights_out);
     return hipGetLastError();
 }
 
 template <int QT, int QS>
-static void launch_moe_down_qs(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids, const float *w,
+static void launch_moe_down_qs(hipStream_t st, const uocr_expert_slab *slab, const float *logits, int norm_topk,
                                const uint16_t *mid, uocr_qmat SD, const uint16_t *smid, const uint16_t *res,
                                uint16_t *out) {
-    const uint32_t rpb = 4u;
-    hipLaunchKernelGGL((k_moe_down<QT, QS>), dim3(UOCR_K_HIDDEN / rpb), dim3(BLOCK), 0, st, *slab, ids, w,
-                       (const h16 *)mid, SD, (const h16 *)smid, (const h16 *)res, (h16 *)out, rpb);
+    constexpr int LPR = LPR_896(QT);
+    const uint32_t rpb = 2u * (64u / LPR);
+    hipLaunchKernelGGL((k_moe_down<QT, QS, LPR>), dim3((UOCR_K_HIDDEN + rpb - 1u) / rpb), dim3(GBLOCK), 0, st, *slab,
+                       logits, norm_topk, (const h16 *)mid, SD, (const h16 *)smid, (const h16 *)res, (h16 *)out,
+                       rpb);
 }
 
 template <int QT>
-static void launch_moe_down_qt(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids, const float *w,
+static void launch_moe_down_qt(hipStream_t st, const uocr_expert_slab *slab, const float *logits, int norm_topk,
                                const uint16_t *mid, uocr_qmat SD, const uint16_t *smid, const uint16_t *res,
                                uint16_t *out) {
     switch (SD.qtype) {
-        case UOCR_QT_F16: launch_moe_down_qs<QT, 1>(st, slab, ids, w, mid, SD, smid, res, out); break;
-        case UOCR_QT_Q8: launch_moe_down_qs<QT, 3>(st, slab, ids, w, mid, SD, smid, res, out); break;
-        default: launch_moe_down_qs<QT, 4>(st, slab, ids, w, mid, SD, smid, res, out); break;
+        case UOCR_QT_F16: launch_moe_down_qs<QT, 1>(st, slab, logits, norm_topk, mid, SD, smid, res, out); break;
+        case UOCR_QT_Q8: launch_moe_down_qs<QT, 3>(st, slab, logits, norm_topk, mid, SD, smid, res, out); break;
+        default: launch_moe_down_qs<QT, 4>(st, slab, logits, norm_topk, mid, SD, smid, res, out); break;
     }
 }
 
-extern "C" hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
-                                           const float *weights, const uint16_t *mid, uocr_qmat SD,
-                                           const uint16_t *smid, const uint16_t *res, uint16_t *out) {
-    if (slab == nullptr || !mat_ok(slab->down) || !mat_ok(SD) || ids == nullptr || weights == nullptr ||
-        mid == nullptr || smid == nullptr || res == nullptr || out == nullptr) {
+extern "C" hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const float *logits,
+                                           int norm_topk, const uint16_t *mid, uocr_qmat SD, const uint16_t *smid,
+                                           const uint16_t *res, uint16_t *out) {
+    if (slab == nullptr || !mat_ok(slab->down) || !mat_ok(SD) || logits == nullptr || mid == nullptr ||
+        smid == nullptr || res == nullptr || out == nullptr) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(slab->down.qtype, launch_moe_down_qt, st, slab, ids, weights, mid, SD, smid, res, out);
+    DISPATCH_QT(slab->down.qtype, launch_moe_down_qt, st, slab, logits, norm_topk, mid, SD, smid, res, out);
     return hipGetLastError();
 }
 
 template <int QT>
-static void launch_lm_qt(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x, const uint16_t *nw,
-                         uint32_t *part, uint32_t *cnt, uocr_step_state *state, int advance, int32_t *tokens,
-                         float *scores) {
+static uint32_t launch_lm_qt(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x, const uint16_t *nw,
+                             uint32_t *part) {
+    constexpr int LPR = LPR_1280(QT);
+    const uint32_t pass = 2u * (64u / LPR);
     uint32_t rpb = (vocab + UOCR_K_LM_BLOCKS - 1u) / UOCR_K_LM_BLOCKS;
-    rpb = (rpb + 7u) & ~7u;
-    if (rpb < 8u) rpb = 8u;
-    hipLaunchKernelGGL((k_lm_head<QT>), dim3((vocab + rpb - 1u) / rpb), dim3(BLOCK), 0, st, (const uint8_t *)W.w,
-                       (const h16 *)W.s, vocab, (const h16 *)x, (const h16 *)nw, part, cnt, state, advance, tokens,
-                       scores, rpb);
+    rpb = (rpb + pass - 1u) / pass * pass;
+    const uint32_t nb = (vocab + rpb - 1u) / rpb;
+    hipLaunchKernelGGL((k_lm_head<QT, LPR>), dim3(nb), dim3(GBLOCK), 0, st, (const uint8_t *)W.w, (const h16 *)W.s,
+                       vocab, (const h16 *)x, (const h16 *)nw, part, rpb);
+    return nb;
+}
+
+template <int QE>
+static void launch_lm_fin(hipStream_t st, const uint32_t *part, uint32_t nb, uocr_step_state *state, int advance,
+                          int32_t *tokens, float *scores, uocr_qmat E, uint32_t vocab, uint16_t *hout) {
+    hipLaunchKernelGGL((k_lm_finalize<QE>), dim3(1), dim3(BLOCK), 0, st, part, nb, state, advance, tokens, scores,
+                       (const uint8_t *)E.w, (const h16 *)E.s, vocab, (h16 *)hout);
 }
 
 extern "C" hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x,
-                                          const uint16_t *nw, uint32_t *partials, uint32_t *counter,
-                                          uocr_step_state *state, int advance, int32_t *tokens, float *scores) {
-    if (!mat_ok(W) || vocab == 0u || x == nullptr || partials == nullptr || counter == nullptr ||
-        tokens == nullptr || (advance && state == nullptr)) {
+                                          const uint16_t *nw, uint32_t *partials, uocr_step_state *state, int advance,
+                                          int32_t *tokens, float *scores, uocr_qmat E, uint16_t *hout) {
+    if (!mat_ok(W) || vocab == 0u || x == nullptr || partials == nullptr || tokens == nullptr ||
+        (advance && state == nullptr) || (E.w != nullptr && (!mat_ok(E) || hout == nullptr))) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(W.qtype, launch_lm_qt, st, W, vocab, x, nw, partials, counter, state, advance, tokens, scores);
+    uint32_t nb = 0;
+    switch (W.qtype) {
+        case UOCR_QT_F16: nb = launch_lm_qt<1>(st, W, vocab, x, nw, partials); break;
+        case UOCR_QT_Q8: nb = launch_lm_qt<3>(st, W, vocab, x, nw, partials); break;
+        default: nb = launch_lm_qt<4>(st, W, vocab, x, nw, partials); break;
+    }
+    DISPATCH_QT(E.w != nullptr ? E.qtype : UOCR_QT_Q4, launch_lm_fin, st, partials, nb, state, advance, tokens, scores,
+                E, vocab, hout);
     return hipGetLastError();
 }
 
@@ -979,18 +1136,6 @@ extern "C" hipError_t uocr_launch_embed(hipStream_t st, uocr_qmat E, uint32_t vo
                                         const uocr_step_state *state, uint16_t *out) {
     if (!mat_ok(E) || out == nullptr || (token == nullptr && state == nullptr)) return hipErrorInvalidValue;
     DISPATCH_QT(E.qtype, launch_embed_qt, st, E, vocab, token, state, out);
-    return hipGetLastError();
-}
-
-extern "C" hipError_t uocr_launch_prefill_state(hipStream_t st, uocr_step_state *state, int32_t i) {
-    if (state == nullptr || i < 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_prefill_state, dim3(1), dim3(1), 0, st, state, i);
-    return hipGetLastError();
-}
-
-extern "C" hipError_t uocr_launch_decode_state(hipStream_t st, uocr_step_state *state, int32_t prompt_len, int32_t t) {
-    if (state == nullptr || prompt_len <= 0 || t < 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_decode_state, dim3(1), dim3(1), 0, st, state, prompt_len, t);
     return hipGetLastError();
 }
 
@@ -1012,5 +1157,17 @@ extern "C" hipError_t uocr_launch_prefill_next(hipStream_t st, uocr_step_state *
                                                uint16_t *h) {
     if (state == nullptr || prompt == nullptr || h == nullptr) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_prefill_next, dim3(1), dim3(BLOCK), 0, st, state, (const h16 *)prompt, (h16 *)h);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_prefill_state(hipStream_t st, uocr_step_state *state, int32_t i) {
+    if (state == nullptr || i < 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_prefill_state, dim3(1), dim3(1), 0, st, state, i);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_decode_state(hipStream_t st, uocr_step_state *state, int32_t prompt_len, int32_t t) {
+    if (state == nullptr || prompt_len <= 0 || t < 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_decode_state, dim3(1), dim3(1), 0, st, state, prompt_len, t);
     return hipGetLastError();
 }

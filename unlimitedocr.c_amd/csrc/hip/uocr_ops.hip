@@ -70,10 +70,9 @@ constexpr size_t A256(size_t v) {
 }
 constexpr size_t WS_STATE = 0;
 constexpr size_t WS_APART = WS_STATE + 256u;
-constexpr size_t WS_ACNT = WS_APART + A256(UOCR_ATTN_PARTIAL_FLOATS * 4u);
-constexpr size_t WS_LPART = WS_ACNT + 256u;
-constexpr size_t WS_LCNT = WS_LPART + A256(2u * UOCR_K_LM_BLOCKS * 4u);
-constexpr size_t WS_IDS = WS_LCNT + 256u;
+constexpr size_t WS_LOGITS = WS_APART + A256(UOCR_ATTN_PARTIAL_FLOATS * 4u);
+constexpr size_t WS_LPART = WS_LOGITS + 256u;
+constexpr size_t WS_IDS = WS_LPART + A256(UOCR_LM_PARTIAL_WORDS * 4u);
 constexpr size_t WS_WTS = WS_IDS + 256u;
 constexpr size_t WS_MID = WS_WTS + 256u;
 constexpr size_t WS_SMID = WS_MID + A256(6848u * 2u);
@@ -126,19 +125,18 @@ extern "C" int uocr_op_lm_head_argmax(uint32_t qtype, const void *w, const void 
         return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid lm_head_argmax arguments");
     }
     STREAM_OR_RETURN(st);
-    int r = hip_status(hipMemsetAsync(ws<uint8_t>(workspace, WS_LCNT), 0, 4u, st), "lm_head counter");
-    if (r != UOCR_OK) return r;
     return hip_status(uocr_launch_lm_head(st, qm(qtype, w, s), vocab, (const uint16_t *)x, (const uint16_t *)norm_w,
-                                          ws<uint32_t>(workspace, WS_LPART), ws<uint32_t>(workspace, WS_LCNT), nullptr,
-                                          0, token, score),
+                                          ws<uint32_t>(workspace, WS_LPART), nullptr, 0, token, score,
+                                          qm(qtype, nullptr, nullptr), nullptr),
                       "lm_head_argmax");
 }
 
-extern "C" int uocr_op_router(const void *router_w, const void *x, const void *norm_w, int norm_topk, uint32_t *ids,
-                              float *weights) {
+extern "C" int uocr_op_router(const void *router_w, const void *x, const void *norm_w, int norm_topk, void *workspace,
+                              uint32_t *ids, float *weights) {
+    if (workspace == nullptr) return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "router needs a workspace");
     STREAM_OR_RETURN(st);
     return hip_status(uocr_launch_router(st, (const uint16_t *)router_w, (const uint16_t *)x, (const uint16_t *)norm_w,
-                                         norm_topk, ids, weights),
+                                         norm_topk, ws<float>(workspace, WS_LOGITS), ids, weights),
                       "router");
 }
 
@@ -157,25 +155,22 @@ extern "C" int uocr_op_moe_ffn(const uocr_op_moe_weights *m, const void *x, cons
     sl.gu_s_stride = m->gu_s_stride;
     sl.dn_w_stride = m->dn_w_stride;
     sl.dn_s_stride = m->dn_s_stride;
-    uint32_t *wids = ws<uint32_t>(workspace, WS_IDS);
-    float *wwts = ws<float>(workspace, WS_WTS);
+    uint32_t *wids = ids != nullptr ? ids : ws<uint32_t>(workspace, WS_IDS);
+    float *wwts = weights != nullptr ? weights : ws<float>(workspace, WS_WTS);
+    float *logits = ws<float>(workspace, WS_LOGITS);
     uint16_t *mid = ws<uint16_t>(workspace, WS_MID), *smid = ws<uint16_t>(workspace, WS_SMID);
     const uint16_t *xx = (const uint16_t *)x, *nw = (const uint16_t *)norm_w;
-    int r = hip_status(uocr_launch_router(st, (const uint16_t *)m->router, xx, nw, norm_topk, wids, wwts), "moe router");
+    int r = hip_status(uocr_launch_moe_shared_router(st, qm(m->shared_qtype, m->sgate_w, m->sgate_s),
+                                                     qm(m->shared_qtype, m->sup_w, m->sup_s),
+                                                     (const uint16_t *)m->router, xx, nw, smid, logits),
+                       "moe shared gate/up + router");
     if (r == UOCR_OK) {
-        r = hip_status(uocr_launch_swiglu(st, qm(m->shared_qtype, m->sgate_w, m->sgate_s),
-                                          qm(m->shared_qtype, m->sup_w, m->sup_s), 1792u, 1280u, xx, nw, smid),
-                       "moe shared gate/up");
+        r = hip_status(uocr_launch_moe_gate_up(st, &sl, logits, norm_topk, xx, nw, mid, wids, wwts), "moe routed gate/up");
     }
-    if (r == UOCR_OK) r = hip_status(uocr_launch_moe_gate_up(st, &sl, wids, xx, nw, mid), "moe routed gate/up");
     if (r == UOCR_OK) {
-        r = hip_status(uocr_launch_moe_down(st, &sl, wids, wwts, mid, qm(m->shared_qtype, m->sdown_w, m->sdown_s), smid,
-                                            (const uint16_t *)residual, (uint16_t *)out),
+        r = hip_status(uocr_launch_moe_down(st, &sl, logits, norm_topk, mid, qm(m->shared_qtype, m->sdown_w, m->sdown_s),
+                                            smid, (const uint16_t *)residual, (uint16_t *)out),
                        "moe down/combine");
-    }
-    if (r == UOCR_OK && ids != nullptr) r = hip_status(hipMemcpyAsync(ids, wids, 24u, hipMemcpyDeviceToDevice, st), "ids copy");
-    if (r == UOCR_OK && weights != nullptr) {
-        r = hip_status(hipMemcpyAsync(weights, wwts, 24u, hipMemcpyDeviceToDevice, st), "weights copy");
     }
     return r;
 }
@@ -197,13 +192,11 @@ extern "C" int uocr_op_attention_decode(const void *q, const void *k_cache, cons
         return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid attention_decode arguments");
     }
     STREAM_OR_RETURN(st);
-    int r = hip_status(hipMemsetAsync(ws<uint8_t>(workspace, WS_ACNT), 0, UOCR_ATTN_COUNTER_INTS * 4u, st), "counters");
-    if (r == UOCR_OK) r = set_plan(st, workspace, cache_capacity, prompt_length, generated_count);
+    const int r = set_plan(st, workspace, cache_capacity, prompt_length, generated_count);
     if (r != UOCR_OK) return r;
     return hip_status(uocr_launch_attention(st, (const uint16_t *)q, (const uint16_t *)k_cache, (const uint16_t *)v_cache,
                                             cache_capacity, ws<uocr_step_state>(workspace, WS_STATE),
-                                            ws<float>(workspace, WS_APART), ws<uint32_t>(workspace, WS_ACNT),
-                                            (uint16_t *)out),
+                                            ws<float>(workspace, WS_APART), (uint16_t *)out),
                       "attention_decode");
 }
 
@@ -222,8 +215,7 @@ extern "C" int uocr_op_attention_block(uint32_t qtype, const void *wq, const voi
     for (int d = 0; d < UOCR_K_HEAD_DIM / 2; ++d) invf[d] = exp2f((float)d * freq_scale);
     uocr_step_state *state = ws<uocr_step_state>(workspace, WS_STATE);
     uint16_t *qb = ws<uint16_t>(workspace, WS_Q), *cb = ws<uint16_t>(workspace, WS_CTX);
-    int r = hip_status(hipMemsetAsync(ws<uint8_t>(workspace, WS_ACNT), 0, UOCR_ATTN_COUNTER_INTS * 4u, st), "counters");
-    if (r == UOCR_OK) r = set_plan(st, workspace, cache_capacity, prompt_length, generated_count);
+    int r = set_plan(st, workspace, cache_capacity, prompt_length, generated_count);
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_qkv_rope(st, qm(qtype, wq, sq), qm(qtype, wk, sk), qm(qtype, wv, sv),
                                             (const uint16_t *)hidden, (const uint16_t *)norm_w, invf, state, qb,
@@ -232,7 +224,7 @@ extern "C" int uocr_op_attention_block(uint32_t qtype, const void *wq, const voi
     }
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_attention(st, qb, (const uint16_t *)k_cache, (const uint16_t *)v_cache, cache_capacity,
-                                             state, ws<float>(workspace, WS_APART), ws<uint32_t>(workspace, WS_ACNT), cb),
+                                             state, ws<float>(workspace, WS_APART), cb),
                        "attention");
     }
     if (r == UOCR_OK) {

@@ -125,7 +125,7 @@ SIGNATURES = {
     "uocr_op_swiglu": ([_U32, _VP, _VP, _VP, _VP, _U32, _U32, _VP, _VP, _VP], ct.c_int),
     "uocr_op_rmsnorm": ([_VP, _VP, _U32, _VP], ct.c_int),
     "uocr_op_lm_head_argmax": ([_U32, _VP, _VP, _U32, _VP, _VP, _VP, _VP, _VP], ct.c_int),
-    "uocr_op_router": ([_VP, _VP, _VP, ct.c_int, _VP, _VP], ct.c_int),
+    "uocr_op_router": ([_VP, _VP, _VP, ct.c_int, _VP, _VP, _VP], ct.c_int),
     "uocr_op_moe_ffn": ([ct.POINTER(CMoeWeights), _VP, _VP, _VP, ct.c_int, _VP, _VP, _VP, _VP], ct.c_int),
     "uocr_op_attention_decode": ([_VP, _VP, _VP, _U32, _U32, _U32, _VP, _VP], ct.c_int),
     "uocr_op_attention_block": ([_U32, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _U32, _U32,
@@ -403,8 +403,8 @@ def op_lm_head_argmax(qtype, w, s, vocab, x, norm_w, ws, token, score) -> None:
                                                     _p(score)), "op_lm_head_argmax")
 
 
-def op_router(router, x, norm_w, norm_topk, ids, weights) -> None:
-    _check_op(load_library().uocr_op_router(_p(router), _p(x), _p(norm_w), norm_topk, _p(ids), _p(weights)),
+def op_router(router, x, norm_w, norm_topk, ws, ids, weights) -> None:
+    _check_op(load_library().uocr_op_router(_p(router), _p(x), _p(norm_w), norm_topk, _p(ws), _p(ids), _p(weights)),
               "op_router")
 
 
