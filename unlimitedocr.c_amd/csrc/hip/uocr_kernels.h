@@ -28,7 +28,10 @@
 #define UOCR_K_RING 128
 #define UOCR_K_MAX_K 6848          /* largest GEMV reduction length */
 #define UOCR_K_ATTN_SPLITS 32      /* split-K blocks per head in decode attention */
-#define UOCR_K_LM_BLOCKS 4096      /* upper bound on LM-head argmax partial blocks */
+#define UOCR_K_LM_BLOCKS 1024      /* upper bound on LM-head argmax partial blocks */
+#define UOCR_K_SYNC_WORDS 64       /* arrival counters of in-launch hand-offs */
+#define UOCR_SYNC_ATTN 0           /* UOCR_K_HEADS words */
+#define UOCR_SYNC_ROUTER 16        /* one word */
 
 /* Per-step decode state kept in device memory so one captured graph can be
  * replayed for every token.  Positions follow uocr_metal.m:14239 and the ring
@@ -80,30 +83,33 @@ hipError_t uocr_launch_rmsnorm(hipStream_t st, const uint16_t *x, const uint16_t
 hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
                                 const uint16_t *nw, const float *inv_freq, const uocr_step_state *state,
                                 uint16_t *qout, uint16_t *kcache, uint16_t *vcache, uint32_t cache_capacity);
-/* Split-K decode attention over the plan in *state (32 blocks per head) and
- * the log-sum-exp merge into ctx.  partials: UOCR_ATTN_PARTIAL_FLOATS. */
+/* Split-K decode attention over the plan in *state (32 blocks per head); the
+ * last block of each head merges the log-sum-exp partials into ctx.
+ * partials: UOCR_ATTN_PARTIAL_FLOATS; counters: UOCR_K_HEADS words of the
+ * zero-initialised sync area (left at zero on exit). */
 hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
                                  uint32_t cache_capacity, const uocr_step_state *state, float *partials,
-                                 uint16_t *ctx);
+                                 uint32_t *counters, uint16_t *ctx);
 /* One launch: shared-expert SwiGLU mid (1792 rows of SG/SU over rmsnorm(x))
- * and the 64 router logits (fp16 R, fp32 dot) of the same input. */
+ * and the 64 router logits (fp16 R, fp32 dot) of the same input; the router
+ * block finishing last runs softmax + greedy top-6 (ties to the lower id, raw
+ * probabilities unless norm_topk) into ids/weights.  counter: one word of the
+ * sync area. */
 hipError_t uocr_launch_moe_shared_router(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R,
-                                         const uint16_t *x, const uint16_t *nw, uint16_t *smid, float *logits);
-/* Router alone: logits, then softmax + greedy top-6 (ties to the lower id),
- * raw probabilities unless norm_topk. */
+                                         const uint16_t *x, const uint16_t *nw, int norm_topk, uint16_t *smid,
+                                         float *logits, uint32_t *counter, uint32_t *ids, float *weights);
+/* Router alone (same kernel without the shared experts). */
 hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, const uint16_t *x, const uint16_t *nw, int norm_topk,
-                              float *logits, uint32_t *ids, float *weights);
-/* Routed gate/up with the top-6 recomputed from logits:
- * mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = ids[r].
- * ids_out/weights_out (both or neither) receive the selection. */
-hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, const float *logits, int norm_topk,
-                                   const uint16_t *x, const uint16_t *nw, uint16_t *mid, uint32_t *ids_out,
-                                   float *weights_out);
-/* Routed down + weighted combine + shared down + residual (top-6 from logits):
+                              float *logits, uint32_t *counter, uint32_t *ids, float *weights);
+/* Routed gate/up of the experts in ids[0..5]:
+ * mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = ids[r]. */
+hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
+                                   const uint16_t *x, const uint16_t *nw, uint16_t *mid);
+/* Routed down + weighted combine + shared down + residual:
  * out[c] = f16(sum_r w_r * D_e[c].mid_r + f16(SD[c].smid) + res[c]). */
-hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const float *logits, int norm_topk,
-                                const uint16_t *mid, uocr_qmat SD, const uint16_t *smid, const uint16_t *res,
-                                uint16_t *out);
+hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
+                                const float *weights, const uint16_t *mid, uocr_qmat SD, const uint16_t *smid,
+                                const uint16_t *res, uint16_t *out);
 /* Fused final norm + LM-head argmax: per-block partials, then a one-block
  * finalize storing the winner at tokens[state->t] (tokens[0] without state);
  * with advance it also writes the next decode position into *state and, when

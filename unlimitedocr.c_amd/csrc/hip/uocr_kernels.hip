@@ -3,43 +3,60 @@
  * batch-1 decode token loop of the UnlimitedOCR language model.
  *
  * Design (MI355X-first, not a translation of the Metal kernels):
- *  - Batch-1 decode is HBM/latency-bound.  Every GEMV assigns a group of LPR
- *    lanes to a row; each lane owns 16-byte chunks sub, sub+LPR, ... of the
- *    row and issues all of its (up to 8) 128-bit loads and scale loads
- *    before any arithmetic, so a wavefront keeps 64 x 8 x 16 B of weights in
- *    flight.  LPR is chosen per (qtype, K) so a row takes at most 8 loads per
- *    lane (e.g. Q4 K=1280: 8 lanes x 5 loads, 8 rows per wavefront).
- *  - Dequantisation happens in registers (Q4_0 group-half-split nibbles,
- *    Q8_0, f16); the activation vector is staged once per workgroup in LDS as
- *    fp16, with the producing RMSNorm recomputed in the prologue instead of a
- *    separate launch.  Group sums use DPP row permutes (quad_perm,
- *    row_half_mirror, row_mirror) and lane swizzles beyond 16 lanes.
+ *  - Batch-1 decode is bound by HBM bandwidth and, at this model size, by
+ *    the latency of each launch's dependent memory round trips.  Every kernel
+ *    therefore issues its weight loads first (they depend on nothing), then
+ *    stages the activation vector (with the producing RMSNorm recomputed in
+ *    the prologue), so a kernel costs one memory round trip plus its
+ *    streaming time.  GEMVs that take several row passes per wavefront
+ *    double-buffer the next pass's loads behind the current pass's math.
+ *  - A GEMV row belongs to a group of LPR lanes; lane `sub` owns 16-byte
+ *    chunks sub, sub+LPR, ... (J of them, all loads in flight together).
+ *    LPR is the smallest power of two that covers a row in at most 7 chunks
+ *    per lane (K = 1280: Q4 8 lanes, Q8 16, f16 32).
+ *  - Dequantisation is exact and packed: a nibble n (or a biased int8 byte)
+ *    is placed under an fp16 exponent of 1024 with one byte permute, giving
+ *    the half 1024 + n; one packed fp16 subtract yields the integer weight
+ *    exactly, and v_dot2_f32_f16 accumulates weight x activation pairs in
+ *    fp32.  Each 16-byte chunk's sum is scaled by its group's fp16 scale.
+ *  - Group sums use DPP row permutes (quad_perm, row_half_mirror,
+ *    row_mirror) and lane swizzles beyond 16 lanes.
  *  - RoPE and the KV-cache write are fused into the QKV GEMV epilogue (one
  *    lane group owns rows d and d+64 of one head, the rotation pair).
- *  - Decode attention is split-K over the context (32 blocks per head, 16
- *    lanes x 8 dims per cached token) with an online softmax; a 10-block
- *    merge kernel combines the log-sum-exp partials.
+ *  - Decode attention is split-K over the context (32 blocks per head, a
+ *    16-lane group per cached token, 4 tokens' K/V in flight per group).  The
+ *    last split block of a head to finish merges the log-sum-exp partials.
  *  - The MoE router logits are computed by spare blocks of the shared-expert
- *    gate/up launch; the routed gate/up and down-combine kernels recompute
- *    the greedy top-6 from the 64 logits in one wavefront (64-bit keys of
- *    probability bits and inverted id, so ties go to the lower id).
+ *    gate/up launch; the last router block runs the greedy top-6 in one
+ *    wavefront (64-bit keys of probability bits and inverted id, so ties go to
+ *    the lower id) and publishes ids and weights for the routed kernels.
  *  - The down-combine kernel fuses the 6 routed down projections, their
  *    weighted sum, the shared-expert down GEMV and the residual add.
- *  - The LM head is a fused final-RMSNorm GEMV writing per-block argmax
- *    partials; a one-block finalize picks the token (NaN rows skipped, ties to
- *    the lowest id), advances the device-side step state and gathers the next
- *    token's embedding row, so a captured decode graph can be replayed.
- * No kernel waits on another block and none uses a device-scope fence
- * (on gfx950 one costs an L2 writeback and invalidate per wavefront); every
- * cross-block hand-off is a kernel boundary.
+ *  - The LM head is a streaming final-RMSNorm GEMV writing one argmax
+ *    partial per block; a one-block finalize picks the token (NaN rows
+ *    skipped, ties to the lowest id), advances the device-side step state and
+ *    gathers the next token's embedding row, so a captured decode graph can
+ *    be replayed.
+ *
+ * Cross-block hand-offs inside one launch (attention merge, router top-k)
+ * never use a device-scope fence: on gfx950 such a fence writes back and
+ * invalidates the whole L2 of the XCD.  The producer stores with agent-scope
+ * (sc1) stores, which are coherent across the XCDs' L2s, waits for them with
+ * s_waitcnt, then bumps an arrival counter with an agent-scope atomic; the
+ * block that arrives last reads the data with agent-scope loads and re-arms
+ * the counter to zero.  No block ever waits for another, so no launch can
+ * stall on co-residency.
  */
 #include "uocr_kernels.h"
 
 #include <math.h>
 
 typedef _Float16 h16;
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32;
 
 #define BLOCK 256
+#define NWAVE (BLOCK / 64)
 #define NONE_ID 0xffffffffu
 
 /* ------------------------------------------------------------------------ */
@@ -101,22 +118,75 @@ __device__ __forceinline__ float silu_f(float g) {
     return g / (1.0f + expf(-g));
 }
 
-/* Stage K fp16 activations into LDS; with nw, apply RMSNorm (eps 1e-6):
- * xs[i] = f16(x[i] * inv_rms * nw[i]) (norm.metal:12-40 arithmetic). */
+/* ------------------------------------------------------------------------ */
+/* agent-scope (cross-XCD coherent) exchange inside one launch                */
+/* ------------------------------------------------------------------------ */
+
+__device__ __forceinline__ void st_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void st_agent(u32 *p, u32 v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load((float *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Called by every thread of the block after its agent-scope stores.  Waits
+ * for those stores, counts the block in, and returns true in every thread of
+ * the block that arrives last of n; that block also re-arms the counter. */
+__device__ __forceinline__ bool arrive_last(u32 *counter, u32 n) {
+    __shared__ u32 last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const u32 prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = prev == n - 1u ? 1u : 0u;
+        if (last) st_agent(counter, 0u);
+    }
+    __syncthreads();
+    return last != 0u;
+}
+
+/* ------------------------------------------------------------------------ */
+/* activation staging                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* Stage K (multiple of 8) fp16 activations into LDS; with nw apply RMSNorm
+ * (eps 1e-6): xs[i] = f16(x[i] * inv_rms * nw[i]) (norm.metal:12-40
+ * arithmetic: fp32 sum of squares, then one rounding per element). */
 __device__ __forceinline__ void stage_x(h16 *xs, const h16 *x, const h16 *nw, int K, float *red) {
+    const uint4 *src = (const uint4 *)x;
+    uint4 *dst = (uint4 *)xs;
+    const int n8 = K / 8;
     if (nw != nullptr) {
         float ss = 0.0f;
-        for (int i = threadIdx.x; i < K; i += blockDim.x) {
-            const float v = (float)x[i];
-            ss = fmaf(v, v, ss);
+        for (int i = threadIdx.x; i < n8; i += blockDim.x) {
+            union {
+                uint4 u;
+                h16 h[8];
+            } v;
+            v.u = src[i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss = fmaf((float)v.h[j], (float)v.h[j], ss);
         }
         ss = block_sum(ss, red);
         const float inv = 1.0f / sqrtf(ss / (float)K + 1.0e-6f);
-        for (int i = threadIdx.x; i < K; i += blockDim.x) xs[i] = (h16)(((float)x[i] * inv) * (float)nw[i]);
+        for (int i = threadIdx.x; i < n8; i += blockDim.x) {
+            union {
+                uint4 u;
+                h16 h[8];
+            } v, w;
+            v.u = src[i];
+            w.u = ((const uint4 *)nw)[i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v.h[j] = (h16)(((float)v.h[j] * inv) * (float)w.h[j]);
+            dst[i] = v.u;
+        }
     } else {
-        const uint4 *src = (const uint4 *)x;
-        uint4 *dst = (uint4 *)xs;
-        for (int i = threadIdx.x; i < K / 8; i += blockDim.x) dst[i] = src[i];
+        for (int i = threadIdx.x; i < n8; i += blockDim.x) dst[i] = src[i];
     }
     __syncthreads();
 }
@@ -125,86 +195,89 @@ __device__ __forceinline__ void stage_x(h16 *xs, const h16 *x, const h16 *nw, in
 /* 16-byte chunk dequant-dots                                                */
 /* ------------------------------------------------------------------------ */
 
+/* Chunks per row and chunks per 64-column scale group. */
 template <int QT>
-__device__ __forceinline__ uint32_t row_bytes(uint32_t K) {
-    return QT == 4 ? K / 2u : (QT == 3 ? K : 2u * K);
+__host__ __device__ constexpr u32 chunks_per_row(u32 K) {
+    return QT == 4 ? K / 32u : (QT == 3 ? K / 16u : K / 8u);
+}
+template <int QT>
+__host__ __device__ constexpr u32 chunks_per_group() {
+    return QT == 4 ? 2u : 4u;
+}
+
+__device__ __forceinline__ h16x2 as_h2(u32 v) {
+    return __builtin_bit_cast(h16x2, v);
+}
+
+/* fp16 pair (1024 + b0, 1024 + b1) from bytes b0, b1 of v selected by SEL. */
+template <u32 SEL>
+__device__ __forceinline__ h16x2 magic_pair(u32 v) {
+    return as_h2(__builtin_amdgcn_perm(0x64646464u, v, SEL));
+}
+#define SEL01 0x04010400u /* bytes 0,1 */
+#define SEL23 0x04030402u /* bytes 2,3 */
+
+__device__ __forceinline__ float dot2(h16x2 a, u32 x, float acc) {
+    return __builtin_amdgcn_fdot2(a, as_h2(x), acc, false);
 }
 
 template <int QT>
-__device__ __forceinline__ uint32_t chunk_group(uint32_t c) {
-    return QT == 4 ? (c >> 1) : (c >> 2);
-}
+__device__ __forceinline__ float chunk_dot(const uint4 w, const h16 *xs, u32 c);
 
-union h16x8 {
-    uint4 u;
-    h16 h[8];
-};
-
-template <int QT>
-__device__ __forceinline__ float chunk_dot(const uint4 w, const h16 *xs, uint32_t c);
-
-/* Q4_0: chunk c is bytes 16*(c&1)..+15 of 64-column group c>>1; its low
- * nibbles are columns g*64+16*(c&1)+i and its high nibbles the same +32. */
+/* Q4_0: chunk c is bytes 16*(c&1)..+15 of 64-column group c>>1; byte i holds
+ * column g*64 + 16*(c&1) + i in its low nibble and the same + 32 in its high
+ * nibble, each stored as q + 8. */
 template <>
-__device__ __forceinline__ float chunk_dot<4>(const uint4 w, const h16 *xs, uint32_t c) {
-    const h16 *xl = xs + (c >> 1) * 64u + (c & 1u) * 16u;
-    h16x8 l0, l1, g0, g1;
-    l0.u = ((const uint4 *)xl)[0];
-    l1.u = ((const uint4 *)xl)[1];
-    g0.u = ((const uint4 *)(xl + 32))[0];
-    g1.u = ((const uint4 *)(xl + 32))[1];
-    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-    float s = 0.0f;
+__device__ __forceinline__ float chunk_dot<4>(const uint4 w, const h16 *xs, u32 c) {
+    const uint4 *xp = (const uint4 *)(xs + (c >> 1) * 64u + (c & 1u) * 16u);
+    const uint4 l0 = xp[0], l1 = xp[1], g0 = xp[4], g1 = xp[5];
+    const u32 xl[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+    const u32 xh[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const u32 wv[4] = {w.x, w.y, w.z, w.w};
+    const h16x2 bias = {(h16)1032.0f, (h16)1032.0f};
+    float d = 0.0f;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t byte = (wv[b] >> (8 * i)) & 0xffu;
-            const int k = 4 * b + i;
-            const float xlo = (float)(k < 8 ? l0.h[k] : l1.h[k - 8]);
-            const float xhi = (float)(k < 8 ? g0.h[k] : g1.h[k - 8]);
-            s = fmaf((float)((int)(byte & 15u) - 8), xlo, s);
-            s = fmaf((float)((int)(byte >> 4) - 8), xhi, s);
-        }
+        const u32 lo = wv[b] & 0x0F0F0F0Fu, hi = (wv[b] >> 4) & 0x0F0F0F0Fu;
+        d = dot2(magic_pair<SEL01>(lo) - bias, xl[2 * b], d);
+        d = dot2(magic_pair<SEL23>(lo) - bias, xl[2 * b + 1], d);
+        d = dot2(magic_pair<SEL01>(hi) - bias, xh[2 * b], d);
+        d = dot2(magic_pair<SEL23>(hi) - bias, xh[2 * b + 1], d);
     }
-    return s;
+    return d;
 }
 
-/* Q8_0: chunk c is columns 16c..16c+15 (group c>>2). */
+/* Q8_0: chunk c is columns 16c..16c+15; byte ^ 0x80 = q + 128. */
 template <>
-__device__ __forceinline__ float chunk_dot<3>(const uint4 w, const h16 *xs, uint32_t c) {
-    const h16 *xp = xs + 16u * c;
-    h16x8 a, b;
-    a.u = ((const uint4 *)xp)[0];
-    b.u = ((const uint4 *)xp)[1];
-    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-    float s = 0.0f;
+__device__ __forceinline__ float chunk_dot<3>(const uint4 w, const h16 *xs, u32 c) {
+    const uint4 *xp = (const uint4 *)(xs + 16u * c);
+    const uint4 a = xp[0], b4 = xp[1];
+    const u32 xv[8] = {a.x, a.y, a.z, a.w, b4.x, b4.y, b4.z, b4.w};
+    const u32 wv[4] = {w.x, w.y, w.z, w.w};
+    const h16x2 bias = {(h16)1152.0f, (h16)1152.0f};
+    float d = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int q = (int)(int8_t)((wv[j] >> (8 * i)) & 0xffu);
-            const int k = 4 * j + i;
-            s = fmaf((float)q, (float)(k < 8 ? a.h[k] : b.h[k - 8]), s);
-        }
+    for (int b = 0; b < 4; ++b) {
+        const u32 u = wv[b] ^ 0x80808080u;
+        d = dot2(magic_pair<SEL01>(u) - bias, xv[2 * b], d);
+        d = dot2(magic_pair<SEL23>(u) - bias, xv[2 * b + 1], d);
     }
-    return s;
+    return d;
 }
 
 /* f16: chunk c is columns 8c..8c+7. */
 template <>
-__device__ __forceinline__ float chunk_dot<1>(const uint4 w, const h16 *xs, uint32_t c) {
-    h16x8 a, b;
-    a.u = ((const uint4 *)(xs + 8u * c))[0];
-    b.u = w;
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s = fmaf((float)b.h[i], (float)a.h[i], s);
-    return s;
+__device__ __forceinline__ float chunk_dot<1>(const uint4 w, const h16 *xs, u32 c) {
+    const uint4 a = *(const uint4 *)(xs + 8u * c);
+    float d = 0.0f;
+    d = dot2(as_h2(w.x), a.x, d);
+    d = dot2(as_h2(w.y), a.y, d);
+    d = dot2(as_h2(w.z), a.z, d);
+    d = dot2(as_h2(w.w), a.w, d);
+    return d;
 }
 
-/* Sum over aligned groups of LPR lanes; every lane receives its group's sum.
- * DPP quad/half-row/row permutes inside 16-lane rows, then lane swizzles. */
+/* Sum over aligned groups of LPR lanes; every lane receives its group's sum. */
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
     if (LPR >= 2) v += dpp_f<0xB1>(v);
@@ -216,71 +289,67 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-/* Row dots by a group of LPR lanes: lane `sub` of the group owns the 16-byte
- * chunks sub, sub+LPR, ... of its row.  The first J chunks of every one of the
- * NM rows are loaded (with their scales) before any arithmetic, so a wave
- * keeps 64*J*NM loads in flight; chunks past J*LPR fall to a tail loop.  W, S,
- * X are per-lane pointers (row payload, row scales, activation in LDS).
- * Every lane receives the NM dot products of its group. */
-template <int QT, int LPR, int J, int NM>
-__device__ __forceinline__ void group_dot(const uint8_t *const *W, const h16 *const *S, const h16 *const *X,
-                                          uint32_t C, uint32_t sub, float *out) {
-    uint4 w[NM][J];
-    float sc[NM][J];
+/* In-flight loads of one row for one lane: chunks sub + LPR*j, j < J. */
+template <int J>
+struct RowFrag {
+    uint4 w[J];
+    h16 s[J];
+};
+
+template <int QT, int LPR, int J>
+__device__ __forceinline__ void frag_load(RowFrag<J> &f, const uint8_t *W, const h16 *S, u32 C, u32 sub) {
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const uint32_t c = sub + LPR * j;
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-            w[m][j] = c < C ? *(const uint4 *)(W[m] + 16u * c) : make_uint4(0u, 0u, 0u, 0u);
-            if (QT != 1) sc[m][j] = c < C ? (float)S[m][chunk_group<QT>(c)] : 0.0f;
-        }
+        const u32 c = sub + LPR * j;
+        const bool in = c < C;
+        f.w[j] = in ? *(const uint4 *)(W + 16u * c) : make_uint4(0u, 0u, 0u, 0u);
+        if (QT != 1) f.s[j] = in ? S[c / chunks_per_group<QT>()] : (h16)0.0f;
     }
-    float acc[NM];
-#pragma unroll
-    for (int m = 0; m < NM; ++m) acc[m] = 0.0f;
+}
+
+/* Lane-partial dot of a loaded row with the LDS activation xs. */
+template <int QT, int LPR, int J>
+__device__ __forceinline__ float frag_dot(const RowFrag<J> &f, const h16 *xs, u32 C, u32 sub) {
+    float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const uint32_t c = sub + LPR * j;
+        const u32 c = sub + LPR * j;
         if (c < C) {
-#pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                const float d = chunk_dot<QT>(w[m][j], X[m], c);
-                acc[m] = QT == 1 ? acc[m] + d : fmaf(d, sc[m][j], acc[m]);
-            }
+            const float d = chunk_dot<QT>(f.w[j], xs, c);
+            acc = QT == 1 ? acc + d : fmaf(d, (float)f.s[j], acc);
         }
     }
-    for (uint32_t c = sub + LPR * J; c < C; c += LPR) {
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-            const float d = chunk_dot<QT>(*(const uint4 *)(W[m] + 16u * c), X[m], c);
-            acc[m] = QT == 1 ? acc[m] + d : fmaf(d, (float)S[m][chunk_group<QT>(c)], acc[m]);
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < NM; ++m) out[m] = group_sum<LPR>(acc[m]);
+    return acc;
+}
+
+/* Lanes per row and chunk slots per lane for a row of C chunks: the smallest
+ * power of two >= 4 with C <= 7 * LPR (else 64 lanes, up to 16 slots). */
+__host__ __device__ constexpr u32 lpr_for(u32 C) {
+    return C <= 28u ? 4u : (C <= 56u ? 8u : (C <= 112u ? 16u : (C <= 224u ? 32u : 64u)));
+}
+__host__ __device__ constexpr u32 j_for(u32 C) {
+    return (C + lpr_for(C) - 1u) / lpr_for(C);
 }
 
 /* Greedy top-6 over 64 router logits by one wavefront (one expert per lane):
  * max-subtracted softmax, then 6 rounds of a 64-bit max over
  * (probability bits, inverted id) so ties go to the lower id
  * (uocr_cpu_ref.c:443-463, moe.metal:12-18).  Raw probabilities unless
- * norm_topk.  Results land in ids/w (LDS). */
-__device__ __forceinline__ void topk6_wave(const float *logits, int norm_topk, uint32_t *ids, float *w) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const float lg = logits[lane];
+ * norm_topk.  Lane 0 writes ids/w. */
+__device__ __forceinline__ void topk6_wave(float lg, int norm_topk, u32 *ids, float *w) {
+    const u32 lane = threadIdx.x & 63u;
     const float mx = wave_max(lg);
     const float pe = expf(lg - mx);
     const float prob = pe / wave_sum(pe);
     unsigned long long key = ((unsigned long long)__float_as_uint(prob) << 32) | (0xffffffffu - lane);
     float sel[UOCR_K_TOPK];
-    uint32_t sid[UOCR_K_TOPK];
+    u32 sid[UOCR_K_TOPK];
     float tot = 0.0f;
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
         const unsigned long long best = wave_max_u64(key);
-        sid[r] = 0xffffffffu - (uint32_t)(best & 0xffffffffull);
-        sel[r] = __uint_as_float((uint32_t)(best >> 32));
+        sid[r] = 0xffffffffu - (u32)(best & 0xffffffffull);
+        sel[r] = __uint_as_float((u32)(best >> 32));
         tot += sel[r];
         if (lane == sid[r]) key = 0ull;
     }
@@ -294,58 +363,118 @@ __device__ __forceinline__ void topk6_wave(const float *logits, int norm_topk, u
 }
 
 /* ------------------------------------------------------------------------ */
-/* GEMV family                                                               */
+/* streaming GEMV family                                                      */
 /* ------------------------------------------------------------------------ */
 
-#define GBLOCK 128 /* GEMV-family workgroup: 2 wavefronts */
+enum { EPI_LINEAR = 0, EPI_SWIGLU = 1, EPI_ARGMAX = 2 };
 
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+__device__ __forceinline__ bool better(float s, u32 id, float bs, u32 bid) {
+    return id != NONE_ID && (bid == NONE_ID || s > bs || (s == bs && id < bid));
+}
 
-template <int QT, int LPR, int EPI>
-__global__ __launch_bounds__(GBLOCK) void k_gemv(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
-                                                 const uint8_t *__restrict__ W2, const h16 *__restrict__ S2,
-                                                 uint32_t rows, uint32_t K, const h16 *__restrict__ x,
-                                                 const h16 *__restrict__ nw, const h16 *__restrict__ res,
-                                                 h16 *__restrict__ y, uint32_t rpb) {
-    constexpr uint32_t R = 64u / LPR;
+/* Row groups of R = 64/LPR rows are dealt to wavefronts round-robin over the
+ * grid; a wavefront loads its next group while it reduces the current one.
+ *  EPI_LINEAR: y[r] = f16(W_r.xin (+ res[r]))
+ *  EPI_SWIGLU: y[r] = f16(silu(W_r.xin) * (W2_r.xin))
+ *  EPI_ARGMAX: per-block best (score, row) into part[2*block] (NaN skipped,
+ *              ties to the lower row). */
+template <int QT, int LPR, int J, int EPI>
+__global__ __launch_bounds__(BLOCK) void k_stream(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
+                                                  const uint8_t *__restrict__ W2, const h16 *__restrict__ S2,
+                                                  u32 rows, u32 K, const h16 *__restrict__ x,
+                                                  const h16 *__restrict__ nw, const h16 *__restrict__ res,
+                                                  h16 *__restrict__ y, u32 *__restrict__ part) {
+    constexpr u32 R = 64u / LPR;
+    constexpr int NM = EPI == EPI_SWIGLU ? 2 : 1;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_MAX_K];
     __shared__ float red[16];
-    stage_x(xs, x, nw, (int)K, red);
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    const uint32_t sub = lane % LPR, grp = lane / LPR;
-    const uint32_t rb = row_bytes<QT>(K), C = rb / 16u, G = K / 64u;
-    const uint32_t r0 = blockIdx.x * rpb, r1 = min(rows, r0 + rpb);
-    for (uint32_t base = r0 + wave * R; base < r1; base += nwave * R) {
-        const uint32_t r = base + grp;
-        const uint32_t rr = r < r1 ? r : r1 - 1u;
+    __shared__ float bsc[NWAVE];
+    __shared__ u32 bidv[NWAVE];
+    const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const u32 sub = lane % LPR, grp = lane / LPR;
+    const u32 C = chunks_per_row<QT>(K), rb = 16u * C, G = K / 64u;
+    const u32 ngroups = (rows + R - 1u) / R;
+    const u32 stride = gridDim.x * NWAVE;
+    u32 g = blockIdx.x * NWAVE + wave;
+
+    RowFrag<J> fa[NM], fb[NM];
+    auto load = [&](RowFrag<J>(&f)[NM], u32 gg) {
+        const u32 r = min(gg * R + grp, rows - 1u);
+        frag_load<QT, LPR, J>(f[0], W + (size_t)r * rb, S + (size_t)r * G, C, sub);
+        if (NM == 2) frag_load<QT, LPR, J>(f[NM - 1], W2 + (size_t)r * rb, S2 + (size_t)r * G, C, sub);
+    };
+    float bs = -INFINITY;
+    u32 bid = NONE_ID;
+    auto finish = [&](const RowFrag<J>(&f)[NM], u32 gg) {
+        const u32 r = gg * R + grp;
+        const float d0 = group_sum<LPR>(frag_dot<QT, LPR, J>(f[0], xs, C, sub));
         if (EPI == EPI_SWIGLU) {
-            const uint8_t *Wp[2] = {W + (size_t)rr * rb, W2 + (size_t)rr * rb};
-            const h16 *Sp[2] = {S + (size_t)rr * G, S2 + (size_t)rr * G};
-            const h16 *Xp[2] = {xs, xs};
-            float d[2];
-            group_dot<QT, LPR, 8, 2>(Wp, Sp, Xp, C, sub, d);
-            if (r < r1 && sub == 0u) y[r] = (h16)(silu_f(d[0]) * d[1]);
+            const float d1 = group_sum<LPR>(frag_dot<QT, LPR, J>(f[NM - 1], xs, C, sub));
+            if (r < rows && sub == 0u) y[r] = (h16)(silu_f(d0) * d1);
+        } else if (EPI == EPI_LINEAR) {
+            if (r < rows && sub == 0u) y[r] = (h16)(res != nullptr ? d0 + (float)res[r] : d0);
         } else {
-            const uint8_t *Wp[1] = {W + (size_t)rr * rb};
-            const h16 *Sp[1] = {S + (size_t)rr * G};
-            const h16 *Xp[1] = {xs};
-            float d[1];
-            group_dot<QT, LPR, 8, 1>(Wp, Sp, Xp, C, sub, d);
-            if (r < r1 && sub == 0u) y[r] = (h16)(EPI == EPI_RESID ? d[0] + (float)res[r] : d[0]);
+            if (r < rows && !isnan(d0) && better(d0, r, bs, bid)) {
+                bs = d0;
+                bid = r;
+            }
+        }
+    };
+
+    if (g < ngroups) load(fa, g);
+    stage_x(xs, x, nw, (int)K, red);
+    while (g < ngroups) {
+        const u32 g1 = g + stride;
+        if (g1 < ngroups) load(fb, g1);
+        finish(fa, g);
+        if (g1 >= ngroups) break;
+        const u32 g2 = g1 + stride;
+        if (g2 < ngroups) load(fa, g2);
+        finish(fb, g1);
+        g = g2;
+    }
+
+    if (EPI == EPI_ARGMAX) {
+        /* wave argmax over the group leaders, then over the block's waves */
+#pragma unroll
+        for (int o = LPR; o < 64; o <<= 1) {
+            const float os = __shfl_xor(bs, o);
+            const u32 oid = (u32)__shfl_xor((int)bid, o);
+            if (better(os, oid, bs, bid)) {
+                bs = os;
+                bid = oid;
+            }
+        }
+        if (lane == 0u) {
+            bsc[wave] = bs;
+            bidv[wave] = bid;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float b = bsc[0];
+            u32 bi = bidv[0];
+            for (int i = 1; i < NWAVE; ++i) {
+                if (better(bsc[i], bidv[i], b, bi)) {
+                    b = bsc[i];
+                    bi = bidv[i];
+                }
+            }
+            part[2u * blockIdx.x] = __float_as_uint(b);
+            part[2u * blockIdx.x + 1u] = bi;
         }
     }
 }
 
-__global__ __launch_bounds__(BLOCK) void k_rmsnorm(const h16 *x, const h16 *nw, uint32_t n, h16 *y) {
+__global__ __launch_bounds__(BLOCK) void k_rmsnorm(const h16 *x, const h16 *nw, u32 n, h16 *y) {
     __shared__ float red[16];
     float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+    for (u32 i = threadIdx.x; i < n; i += blockDim.x) {
         const float v = (float)x[i];
         ss = fmaf(v, v, ss);
     }
     ss = block_sum(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)n + 1.0e-6f);
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) y[i] = (h16)(((float)x[i] * inv) * (float)nw[i]);
+    for (u32 i = threadIdx.x; i < n; i += blockDim.x) y[i] = (h16)(((float)x[i] * inv) * (float)nw[i]);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -359,81 +488,87 @@ struct RopeTab {
 /* Work item i (0..1919): matrix m = i/640 (q,k,v), head h, pair d; a lane
  * group computes rows h*128+d and h*128+d+64 of matrix m, rounds them to
  * fp16, rotates q/k by the split-half RoPE at st->pos and stores q, or k/v
- * into the cache slot st->cache_token. */
-template <int QT, int LPR>
-__global__ __launch_bounds__(GBLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, uocr_qmat V, const h16 *__restrict__ hin,
-                                                     const h16 *__restrict__ nw, RopeTab rope,
-                                                     const uocr_step_state *__restrict__ st, h16 *__restrict__ qout,
-                                                     h16 *__restrict__ kc, h16 *__restrict__ vc, uint32_t cap,
-                                                     uint32_t ipb) {
-    constexpr uint32_t R = 64u / LPR;
+ * into the cache slot st->cache_token.  One item per lane group. */
+template <int QT>
+__global__ __launch_bounds__(BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, uocr_qmat V, const h16 *__restrict__ hin,
+                                                    const h16 *__restrict__ nw, RopeTab rope,
+                                                    const uocr_step_state *__restrict__ st, h16 *__restrict__ qout,
+                                                    h16 *__restrict__ kc, h16 *__restrict__ vc, u32 cap) {
+    constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
+    constexpr u32 rb = 16u * C, G = K / 64u;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
-    stage_x(xs, hin, nw, UOCR_K_HIDDEN, red);
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    const uint32_t sub = lane % LPR, grp = lane / LPR;
-    const uint32_t K = UOCR_K_HIDDEN, rb = row_bytes<QT>(K), C = rb / 16u, G = K / 64u;
+    const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const u32 sub = lane % LPR, grp = lane / LPR;
+    const u32 item = (blockIdx.x * NWAVE + wave) * R + grp;
+    const u32 it = min(item, 1919u);
+    const u32 m = it / 640u, rem = it % 640u, h = rem / 64u, d = rem % 64u;
+    const uocr_qmat M = m == 0u ? Q : (m == 1u ? Km : V);
+    const u32 ra = h * 128u + d, rbw = ra + 64u;
+    RowFrag<J> fa, fb;
+    frag_load<QT, LPR, J>(fa, (const uint8_t *)M.w + (size_t)ra * rb, (const h16 *)M.s + (size_t)ra * G, C, sub);
+    frag_load<QT, LPR, J>(fb, (const uint8_t *)M.w + (size_t)rbw * rb, (const h16 *)M.s + (size_t)rbw * G, C, sub);
     const int32_t pos = st->pos;
-    const uint32_t ct = (uint32_t)st->cache_token;
-    const uint32_t i0 = blockIdx.x * ipb, i1 = min(1920u, i0 + ipb);
-    for (uint32_t base = i0 + wave * R; base < i1; base += nwave * R) {
-        const uint32_t it = min(base + grp, i1 - 1u);
-        const uint32_t m = it / 640u, rem = it % 640u, h = rem / 64u, d = rem % 64u;
-        const uocr_qmat M = m == 0u ? Q : (m == 1u ? Km : V);
-        const uint32_t ra = h * 128u + d, rbw = ra + 64u;
-        const uint8_t *Wp[2] = {(const uint8_t *)M.w + (size_t)ra * rb, (const uint8_t *)M.w + (size_t)rbw * rb};
-        const h16 *Sp[2] = {(const h16 *)M.s + (size_t)ra * G, (const h16 *)M.s + (size_t)rbw * G};
-        const h16 *Xp[2] = {xs, xs};
-        float dd[2];
-        group_dot<QT, LPR, 8, 2>(Wp, Sp, Xp, C, sub, dd);
-        if (sub == 0u && base + grp < i1) {
-            const h16 a = (h16)dd[0], b = (h16)dd[1];
-            const size_t cix = ((size_t)h * cap + ct) * 128u + d;
-            if (m == 2u) {
-                vc[cix] = a;
-                vc[cix + 64u] = b;
+    const u32 ct = (u32)st->cache_token;
+    stage_x(xs, hin, nw, UOCR_K_HIDDEN, red);
+    const float da = group_sum<LPR>(frag_dot<QT, LPR, J>(fa, xs, C, sub));
+    const float db = group_sum<LPR>(frag_dot<QT, LPR, J>(fb, xs, C, sub));
+    if (sub == 0u && item < 1920u) {
+        const h16 a = (h16)da, b = (h16)db;
+        const size_t cix = ((size_t)h * cap + ct) * 128u + d;
+        if (m == 2u) {
+            vc[cix] = a;
+            vc[cix + 64u] = b;
+        } else {
+            const float ang = (float)pos * rope.f[d];
+            const float cs = cosf(ang), sn = sinf(ang);
+            const float fa2 = (float)a, fb2 = (float)b;
+            const h16 na = (h16)(fa2 * cs - fb2 * sn), nb = (h16)(fa2 * sn + fb2 * cs);
+            if (m == 0u) {
+                qout[h * 128u + d] = na;
+                qout[h * 128u + d + 64u] = nb;
             } else {
-                const float ang = (float)pos * rope.f[d];
-                const float cs = cosf(ang), sn = sinf(ang);
-                const float fa = (float)a, fb = (float)b;
-                const h16 na = (h16)(fa * cs - fb * sn), nb = (h16)(fa * sn + fb * cs);
-                if (m == 0u) {
-                    qout[h * 128u + d] = na;
-                    qout[h * 128u + d + 64u] = nb;
-                } else {
-                    kc[cix] = na;
-                    kc[cix + 64u] = nb;
-                }
+                kc[cix] = na;
+                kc[cix + 64u] = nb;
             }
         }
     }
 }
 
 /* ------------------------------------------------------------------------ */
-/* split-K decode attention + merge                                          */
+/* split-K decode attention with last-block merge                            */
 /* ------------------------------------------------------------------------ */
 
+#define ATT_UNROLL 4
+
 /* Block (s, h) covers attention indices [s*chunk, (s+1)*chunk) of head h:
- * 16 lanes x 8 dims per cached token, 16 tokens per block in flight, an
- * online softmax per 16-lane group, then a block merge into one (max, sum,
- * acc[128]) partial.  Indices >= attn_prompt map into the 128-token ring
- * (attention_decode.metal:25-33). */
+ * a 16-lane group per cached token (8 dims per lane), ATT_UNROLL tokens'
+ * K/V rows loaded per group before the online-softmax updates, then a block
+ * merge into one (max, sum, acc[128]) partial.  Indices >= attn_prompt map
+ * into the 128-token ring (attention_decode.metal:25-33).  The last block of
+ * the head to finish merges the S partials into ctx (fp16). */
 __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, const h16 *__restrict__ kc,
-                                                     const h16 *__restrict__ vc, uint32_t cap,
-                                                     const uocr_step_state *__restrict__ st, float *__restrict__ part) {
+                                                     const h16 *__restrict__ vc, u32 cap,
+                                                     const uocr_step_state *__restrict__ st, float *__restrict__ part,
+                                                     u32 *__restrict__ counters, h16 *__restrict__ ctx) {
+    constexpr int S = UOCR_K_ATTN_SPLITS, PW = UOCR_K_HEAD_DIM + 2;
     __shared__ float sm[16], sl[16];
     __shared__ float sacc[16][UOCR_K_HEAD_DIM];
-    const int h = blockIdx.y, s = blockIdx.x, S = gridDim.x;
+    const int h = blockIdx.y, s = blockIdx.x;
     const int P = st->attn_prompt, L = st->attn_len, fg = st->first_gen;
     const int chunk = (L + S - 1) / S;
     const int i0 = s * chunk, i1 = min(L, i0 + chunk);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int g = lane >> 4, p = lane & 15;
+    const int gq = lane >> 4, p = lane & 15;
+    const int gid = wave * 4 + gq;
     const float scale = 0.08838834764831845f; /* 1/sqrt(128) */
 
     float qv[8];
     {
-        h16x8 t;
+        union {
+            uint4 u;
+            h16 h[8];
+        } t;
         t.u = *(const uint4 *)(q + h * 128 + 8 * p);
 #pragma unroll
         for (int j = 0; j < 8; ++j) qv[j] = (float)t.h[j];
@@ -443,23 +578,35 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
     const h16 *kh = kc + (size_t)h * cap * 128u;
     const h16 *vh = vc + (size_t)h * cap * 128u;
-    for (int i = i0 + wave * 4 + g; i < i1; i += 16) {
-        const int t = i < P ? i : P + (fg + i - P) % UOCR_K_RING;
-        h16x8 kk, vv;
-        kk.u = *(const uint4 *)(kh + (size_t)t * 128u + 8 * p);
-        vv.u = *(const uint4 *)(vh + (size_t)t * 128u + 8 * p);
-        float d = 0.0f;
+    for (int ib = i0 + gid; ib < i1; ib += 16 * ATT_UNROLL) {
+        union {
+            uint4 u;
+            h16 h[8];
+        } kk[ATT_UNROLL], vv[ATT_UNROLL];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) d = fmaf(qv[j], (float)kk.h[j], d);
-        const float sc = row16_sum(d) * scale;
-        const float mn = fmaxf(m, sc);
-        const float corr = expf(m - mn), e = expf(sc - mn);
-        l = l * corr + e;
+        for (int u = 0; u < ATT_UNROLL; ++u) {
+            const int i = ib + 16 * u;
+            const int ii = i < i1 ? i : ib;
+            const int t = ii < P ? ii : P + (fg + ii - P) % UOCR_K_RING;
+            kk[u].u = *(const uint4 *)(kh + (size_t)t * 128u + 8 * p);
+            vv[u].u = *(const uint4 *)(vh + (size_t)t * 128u + 8 * p);
+        }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = fmaf(e, (float)vv.h[j], acc[j] * corr);
-        m = mn;
+        for (int u = 0; u < ATT_UNROLL; ++u) {
+            if (ib + 16 * u < i1) {
+                float d = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) d = fmaf(qv[j], (float)kk[u].h[j], d);
+                const float sc = row16_sum(d) * scale;
+                const float mn = fmaxf(m, sc);
+                const float corr = expf(m - mn), e = expf(sc - mn);
+                l = l * corr + e;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = fmaf(e, (float)vv[u].h[j], acc[j] * corr);
+                m = mn;
+            }
+        }
     }
-    const int gid = wave * 4 + g;
     if (p == 0) {
         sm[gid] = m;
         sl[gid] = l;
@@ -467,202 +614,182 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
 #pragma unroll
     for (int j = 0; j < 8; ++j) sacc[gid][8 * p + j] = acc[j];
     __syncthreads();
+    float *ph = part + (size_t)h * S * PW;
     if (threadIdx.x < UOCR_K_HEAD_DIM) {
         const int d = threadIdx.x;
         float M = -INFINITY;
+#pragma unroll
         for (int k = 0; k < 16; ++k) M = fmaxf(M, sm[k]);
         float Ls = 0.0f, A = 0.0f;
         if (M != -INFINITY) {
+#pragma unroll
             for (int k = 0; k < 16; ++k) {
                 const float f = expf(sm[k] - M);
                 Ls = fmaf(sl[k], f, Ls);
                 A = fmaf(sacc[k][d], f, A);
             }
         }
-        float *pp = part + (size_t)(h * S + s) * (UOCR_K_HEAD_DIM + 2);
-        pp[2 + d] = A;
+        float *pp = ph + (size_t)s * PW;
+        st_agent(pp + 2 + d, A);
         if (d == 0) {
-            pp[0] = M;
-            pp[1] = Ls;
+            st_agent(pp, M);
+            st_agent(pp + 1, Ls);
         }
     }
-}
-
-/* Log-sum-exp merge of the S partials of one head -> fp16 context. */
-__global__ __launch_bounds__(UOCR_K_HEAD_DIM) void k_attention_merge(const float *__restrict__ part, uint32_t S,
-                                                                     h16 *__restrict__ ctx) {
-    const int h = blockIdx.x, d = threadIdx.x;
-    const float *ph = part + (size_t)h * S * (UOCR_K_HEAD_DIM + 2);
-    float M = -INFINITY;
-    for (uint32_t k = 0; k < S; ++k) M = fmaxf(M, ph[(size_t)k * (UOCR_K_HEAD_DIM + 2)]);
-    float Ls = 0.0f, A = 0.0f;
-    for (uint32_t k = 0; k < S; ++k) {
-        const float *pk = ph + (size_t)k * (UOCR_K_HEAD_DIM + 2);
-        if (pk[0] == -INFINITY) continue;
-        const float f = expf(pk[0] - M);
-        Ls = fmaf(pk[1], f, Ls);
-        A = fmaf(pk[2 + d], f, A);
+    if (!arrive_last(counters + h, (u32)S)) return;
+    if (threadIdx.x < UOCR_K_HEAD_DIM) {
+        const int d = threadIdx.x;
+        float Mk[S], Lk[S], Ak[S];
+#pragma unroll
+        for (int k = 0; k < S; ++k) {
+            Mk[k] = ld_agent(ph + (size_t)k * PW);
+            Lk[k] = ld_agent(ph + (size_t)k * PW + 1);
+            Ak[k] = ld_agent(ph + (size_t)k * PW + 2 + d);
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < S; ++k) M = fmaxf(M, Mk[k]);
+        float Ls = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int k = 0; k < S; ++k) {
+            if (Mk[k] != -INFINITY) {
+                const float f = expf(Mk[k] - M);
+                Ls = fmaf(Lk[k], f, Ls);
+                A = fmaf(Ak[k], f, A);
+            }
+        }
+        ctx[h * 128 + d] = (h16)(A / Ls);
     }
-    ctx[h * 128 + d] = (h16)(A / Ls);
 }
 
 /* ------------------------------------------------------------------------ */
-/* MoE: shared experts + router logits, routed gate/up, down-combine         */
+/* MoE: shared experts + router, routed gate/up, down-combine                */
 /* ------------------------------------------------------------------------ */
 
-/* Blocks [0, nb_shared) compute the shared-expert SwiGLU rows (1792) and the
- * remaining blocks the 64 router logits (fp16 rows, fp32 dot); both read the
- * same RMSNorm'd input, so one launch serves both. */
-template <int QS, int LPRS>
-__global__ __launch_bounds__(GBLOCK) void k_moe_shared_router(uocr_qmat SG, uocr_qmat SU, const h16 *__restrict__ R,
-                                                              const h16 *__restrict__ x, const h16 *__restrict__ nw,
-                                                              h16 *__restrict__ smid, float *__restrict__ logits,
-                                                              uint32_t nb_shared, uint32_t rpb_shared,
-                                                              uint32_t rpb_router) {
+#define ROUTER_BLOCKS 8u /* 64 router rows: 8 per block, 2 per wavefront */
+
+/* Blocks [0, nb_shared) compute the shared-expert SwiGLU rows (1792, one row
+ * per lane group) and the last ROUTER_BLOCKS blocks the 64 router logits
+ * (fp16 rows, fp32 dot); both read the same RMSNorm'd input.  The router
+ * block that finishes last runs the top-6 and writes ids/weights. */
+template <int QS>
+__global__ __launch_bounds__(BLOCK) void k_moe_shared_router(uocr_qmat SG, uocr_qmat SU, const h16 *__restrict__ Rw,
+                                                             const h16 *__restrict__ x, const h16 *__restrict__ nw,
+                                                             int norm_topk, h16 *__restrict__ smid,
+                                                             float *__restrict__ logits, u32 *__restrict__ counter,
+                                                             u32 *__restrict__ ids, float *__restrict__ weights,
+                                                             u32 nb_shared) {
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
-    stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     if (blockIdx.x < nb_shared) {
-        constexpr uint32_t RS = 64u / LPRS;
-        const uint32_t sub = lane % LPRS, grp = lane / LPRS;
-        const uint32_t rb = row_bytes<QS>(UOCR_K_HIDDEN), C = rb / 16u, G = UOCR_K_HIDDEN / 64u;
-        const uint32_t r0 = blockIdx.x * rpb_shared, r1 = min(1792u, r0 + rpb_shared);
-        for (uint32_t base = r0 + wave * RS; base < r1; base += nwave * RS) {
-            const uint32_t r = base + grp, rr = r < r1 ? r : r1 - 1u;
-            const uint8_t *Wp[2] = {(const uint8_t *)SG.w + (size_t)rr * rb, (const uint8_t *)SU.w + (size_t)rr * rb};
-            const h16 *Sp[2] = {(const h16 *)SG.s + (size_t)rr * G, (const h16 *)SU.s + (size_t)rr * G};
-            const h16 *Xp[2] = {xs, xs};
-            float d[2];
-            group_dot<QS, LPRS, 8, 2>(Wp, Sp, Xp, C, sub, d);
-            if (r < r1 && sub == 0u) smid[r] = (h16)(silu_f(d[0]) * d[1]);
-        }
-    } else {
-        constexpr uint32_t LPR = 32u, RR = 2u;
-        const uint32_t sub = lane % LPR, grp = lane / LPR;
-        const uint32_t rb = UOCR_K_HIDDEN * 2u, C = rb / 16u;
-        const uint32_t r0 = (blockIdx.x - nb_shared) * rpb_router, r1 = min(64u, r0 + rpb_router);
-        for (uint32_t base = r0 + wave * RR; base < r1; base += nwave * RR) {
-            const uint32_t r = base + grp, rr = r < r1 ? r : r1 - 1u;
-            const uint8_t *Wp[1] = {(const uint8_t *)R + (size_t)rr * rb};
-            const h16 *Sp[1] = {nullptr};
-            const h16 *Xp[1] = {xs};
-            float d[1];
-            group_dot<1, LPR, 8, 1>(Wp, Sp, Xp, C, sub, d);
-            if (r < r1 && sub == 0u) logits[r] = d[0];
-        }
+        constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QS>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
+        constexpr u32 rb = 16u * C, G = K / 64u;
+        const u32 sub = lane % LPR, grp = lane / LPR;
+        const u32 r = (blockIdx.x * NWAVE + wave) * R + grp, rr = min(r, 1791u);
+        RowFrag<J> fg, fu;
+        frag_load<QS, LPR, J>(fg, (const uint8_t *)SG.w + (size_t)rr * rb, (const h16 *)SG.s + (size_t)rr * G, C, sub);
+        frag_load<QS, LPR, J>(fu, (const uint8_t *)SU.w + (size_t)rr * rb, (const h16 *)SU.s + (size_t)rr * G, C, sub);
+        stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
+        const float dg = group_sum<LPR>(frag_dot<QS, LPR, J>(fg, xs, C, sub));
+        const float du = group_sum<LPR>(frag_dot<QS, LPR, J>(fu, xs, C, sub));
+        if (r < 1792u && sub == 0u) smid[r] = (h16)(silu_f(dg) * du);
+        return;
     }
+    constexpr u32 C = chunks_per_row<1>(UOCR_K_HIDDEN), LPR = 32u, J = (C + LPR - 1u) / LPR;
+    constexpr u32 rb = 16u * C;
+    const u32 sub = lane % LPR, grp = lane / LPR;
+    const u32 rblk = blockIdx.x - nb_shared;
+    const u32 r = rblk * 8u + wave * 2u + grp;
+    RowFrag<J> f;
+    frag_load<1, LPR, J>(f, (const uint8_t *)Rw + (size_t)r * rb, nullptr, C, sub);
+    stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
+    const float d = group_sum<LPR>(frag_dot<1, LPR, J>(f, xs, C, sub));
+    if (sub == 0u) st_agent(logits + r, d);
+    if (!arrive_last(counter, ROUTER_BLOCKS)) return;
+    if (threadIdx.x < 64u) topk6_wave(ld_agent(logits + threadIdx.x), norm_topk, ids, weights);
 }
 
-/* Router top-6 from logits (one wavefront). */
-__global__ __launch_bounds__(64) void k_router_topk(const float *__restrict__ logits, int norm_topk, uint32_t *ids,
-                                                    float *w) {
-    __shared__ uint32_t sid[UOCR_K_TOPK];
-    __shared__ float sw[UOCR_K_TOPK];
-    topk6_wave(logits, norm_topk, sid, sw);
-    __syncthreads();
-    if (threadIdx.x < UOCR_K_TOPK) {
-        ids[threadIdx.x] = sid[threadIdx.x];
-        w[threadIdx.x] = sw[threadIdx.x];
-    }
-}
-
-/* Routed gate/up: the block recomputes the top-6 from the logits, then
- * mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = ids[r]. */
-template <int QT, int LPR>
-__global__ __launch_bounds__(GBLOCK) void k_moe_gate_up(uocr_expert_slab sl, const float *__restrict__ logits,
-                                                        int norm_topk, const h16 *__restrict__ x,
-                                                        const h16 *__restrict__ nw, h16 *__restrict__ mid,
-                                                        uint32_t *ids_out, float *w_out, uint32_t rpb) {
-    constexpr uint32_t R = 64u / LPR;
+/* Routed gate/up: mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)),
+ * e = ids[r]; one row pair per lane group. */
+template <int QT>
+__global__ __launch_bounds__(BLOCK) void k_moe_gate_up(uocr_expert_slab sl, const u32 *__restrict__ ids,
+                                                       const h16 *__restrict__ x, const h16 *__restrict__ nw,
+                                                       h16 *__restrict__ mid) {
+    constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
+    constexpr u32 rb = 16u * C, G = K / 64u, I = 896u, ROWS = UOCR_K_TOPK * I;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
-    __shared__ uint32_t sid[UOCR_K_TOPK];
-    __shared__ float sw[UOCR_K_TOPK];
-    if (threadIdx.x < 64u) topk6_wave(logits, norm_topk, sid, sw);
+    const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const u32 sub = lane % LPR, grp = lane / LPR;
+    const u32 r = (blockIdx.x * NWAVE + wave) * R + grp, rr = min(r, ROWS - 1u);
+    const u32 rank = rr / I, col = rr % I;
+    const u32 e0 = ids[rank];
+    const u32 e = e0 < UOCR_K_EXPERTS ? e0 : 0u;
+    RowFrag<J> fg, fu;
+    frag_load<QT, LPR, J>(fg, (const uint8_t *)sl.gate.w + e * sl.gu_w_stride + (size_t)col * rb,
+                          (const h16 *)sl.gate.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
+    frag_load<QT, LPR, J>(fu, (const uint8_t *)sl.up.w + e * sl.gu_w_stride + (size_t)col * rb,
+                          (const h16 *)sl.up.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
     stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
-    if (blockIdx.x == 0u && ids_out != nullptr && threadIdx.x < UOCR_K_TOPK) {
-        ids_out[threadIdx.x] = sid[threadIdx.x];
-        w_out[threadIdx.x] = sw[threadIdx.x];
-    }
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    const uint32_t sub = lane % LPR, grp = lane / LPR;
-    const uint32_t I = 896u, K = UOCR_K_HIDDEN, rb = row_bytes<QT>(K), C = rb / 16u, G = K / 64u;
-    const uint32_t rows = UOCR_K_TOPK * I;
-    const uint32_t r0 = blockIdx.x * rpb, r1 = min(rows, r0 + rpb);
-    for (uint32_t base = r0 + wave * R; base < r1; base += nwave * R) {
-        const uint32_t r = base + grp, rr = r < r1 ? r : r1 - 1u;
-        const uint32_t rank = rr / I, col = rr % I;
-        const uint32_t e = sid[rank] < UOCR_K_EXPERTS ? sid[rank] : 0u;
-        const uint8_t *Wp[2] = {(const uint8_t *)sl.gate.w + e * sl.gu_w_stride + (size_t)col * rb,
-                                (const uint8_t *)sl.up.w + e * sl.gu_w_stride + (size_t)col * rb};
-        const h16 *Sp[2] = {(const h16 *)sl.gate.s + e * sl.gu_s_stride + (size_t)col * G,
-                            (const h16 *)sl.up.s + e * sl.gu_s_stride + (size_t)col * G};
-        const h16 *Xp[2] = {xs, xs};
-        float d[2];
-        group_dot<QT, LPR, 8, 2>(Wp, Sp, Xp, C, sub, d);
-        if (r < r1 && sub == 0u) mid[r] = (h16)(silu_f(d[0]) * d[1]);
-    }
+    const float dg = group_sum<LPR>(frag_dot<QT, LPR, J>(fg, xs, C, sub));
+    const float du = group_sum<LPR>(frag_dot<QT, LPR, J>(fu, xs, C, sub));
+    if (r < ROWS && sub == 0u) mid[r] = (h16)(silu_f(dg) * du);
+}
+
+/* Lanes per output row of the down-combine: Q4 16, Q8 32, f16 64 (2 chunk
+ * slots per routed row of K = 896). */
+__host__ __device__ constexpr u32 lpr_down(int QT) {
+    return QT == 4 ? 16u : (QT == 3 ? 32u : 64u);
 }
 
 /* Down projection of the 6 routed experts + weighted combine + shared-expert
  * down + residual, one fp16 rounding:
  * out[c] = f16(sum_r w_r * D_e[c].mid_r + f16(SD[c].smid) + res[c]). */
-template <int QT, int QS, int LPR>
-__global__ __launch_bounds__(GBLOCK) void k_moe_down(uocr_expert_slab sl, const float *__restrict__ logits,
-                                                     int norm_topk, const h16 *__restrict__ mid, uocr_qmat SD,
-                                                     const h16 *__restrict__ smid, const h16 *__restrict__ res,
-                                                     h16 *__restrict__ out, uint32_t rpb) {
-    constexpr uint32_t I = 896u, SI = 1792u, R = 64u / LPR;
+template <int QT, int QS>
+__global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const u32 *__restrict__ ids,
+                                                    const float *__restrict__ wts, const h16 *__restrict__ mid,
+                                                    uocr_qmat SD, const h16 *__restrict__ smid,
+                                                    const h16 *__restrict__ res, h16 *__restrict__ out) {
+    constexpr u32 I = 896u, SI = 1792u, LPR = lpr_down(QT), R = 64u / LPR;
+    constexpr u32 CD = chunks_per_row<QT>(I), JD = (CD + LPR - 1u) / LPR, GD = I / 64u;
+    constexpr u32 CS = chunks_per_row<QS>(SI), JS = (CS + LPR - 1u) / LPR, GS = SI / 64u;
     __shared__ __attribute__((aligned(16))) h16 ms[UOCR_K_TOPK * I + SI];
-    __shared__ uint32_t sid[UOCR_K_TOPK];
-    __shared__ float sw[UOCR_K_TOPK];
-    if (threadIdx.x < 64u) topk6_wave(logits, norm_topk, sid, sw);
+    const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const u32 sub = lane % LPR, grp = lane / LPR;
+    const u32 c = (blockIdx.x * NWAVE + wave) * R + grp, cc = min(c, (u32)UOCR_K_HIDDEN - 1u);
+    RowFrag<JS> fs;
+    frag_load<QS, LPR, JS>(fs, (const uint8_t *)SD.w + (size_t)cc * 16u * CS, (const h16 *)SD.s + (size_t)cc * GS, CS,
+                           sub);
+    u32 e[UOCR_K_TOPK];
+    float w[UOCR_K_TOPK];
+#pragma unroll
+    for (int r = 0; r < UOCR_K_TOPK; ++r) {
+        const u32 id = ids[r];
+        e[r] = id < UOCR_K_EXPERTS ? id : 0u;
+        w[r] = id < UOCR_K_EXPERTS ? wts[r] : 0.0f;
+    }
+    RowFrag<JD> fd[UOCR_K_TOPK];
+#pragma unroll
+    for (int r = 0; r < UOCR_K_TOPK; ++r) {
+        frag_load<QT, LPR, JD>(fd[r], (const uint8_t *)sl.down.w + e[r] * sl.dn_w_stride + (size_t)cc * 16u * CD,
+                               (const h16 *)sl.down.s + e[r] * sl.dn_s_stride + (size_t)cc * GD, CD, sub);
+    }
     {
         const uint4 *a = (const uint4 *)mid;
         const uint4 *b = (const uint4 *)smid;
         uint4 *d = (uint4 *)ms;
-        for (uint32_t i = threadIdx.x; i < UOCR_K_TOPK * I / 8u; i += blockDim.x) d[i] = a[i];
-        for (uint32_t i = threadIdx.x; i < SI / 8u; i += blockDim.x) d[UOCR_K_TOPK * I / 8u + i] = b[i];
+        for (u32 i = threadIdx.x; i < UOCR_K_TOPK * I / 8u; i += blockDim.x) d[i] = a[i];
+        for (u32 i = threadIdx.x; i < SI / 8u; i += blockDim.x) d[UOCR_K_TOPK * I / 8u + i] = b[i];
     }
     __syncthreads();
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    const uint32_t sub = lane % LPR, grp = lane / LPR;
-    uint32_t e[UOCR_K_TOPK];
-    float w[UOCR_K_TOPK];
+    float acc = 0.0f;
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
-        e[r] = sid[r] < UOCR_K_EXPERTS ? sid[r] : 0u;
-        w[r] = sid[r] < UOCR_K_EXPERTS ? sw[r] : 0.0f;
+        acc = fmaf(w[r], group_sum<LPR>(frag_dot<QT, LPR, JD>(fd[r], ms + r * I, CD, sub)), acc);
     }
-    const uint32_t rbD = row_bytes<QT>(I), CD = rbD / 16u, GD = I / 64u;
-    const uint32_t rbS = row_bytes<QS>(SI), CS = rbS / 16u, GS = SI / 64u;
-    const uint32_t r0 = blockIdx.x * rpb, r1 = min((uint32_t)UOCR_K_HIDDEN, r0 + rpb);
-    for (uint32_t base = r0 + wave * R; base < r1; base += nwave * R) {
-        const uint32_t c = base + grp, cc = c < r1 ? c : r1 - 1u;
-        const uint8_t *Wp[UOCR_K_TOPK];
-        const h16 *Sp[UOCR_K_TOPK];
-        const h16 *Xp[UOCR_K_TOPK];
-#pragma unroll
-        for (int r = 0; r < UOCR_K_TOPK; ++r) {
-            Wp[r] = (const uint8_t *)sl.down.w + e[r] * sl.dn_w_stride + (size_t)cc * rbD;
-            Sp[r] = (const h16 *)sl.down.s + e[r] * sl.dn_s_stride + (size_t)cc * GD;
-            Xp[r] = ms + r * I;
-        }
-        float d[UOCR_K_TOPK];
-        group_dot<QT, LPR, 2, UOCR_K_TOPK>(Wp, Sp, Xp, CD, sub, d);
-        const uint8_t *Ws[1] = {(const uint8_t *)SD.w + (size_t)cc * rbS};
-        const h16 *Ss[1] = {(const h16 *)SD.s + (size_t)cc * GS};
-        const h16 *Xs[1] = {ms + UOCR_K_TOPK * I};
-        float sd[1];
-        group_dot<QS, LPR, 4, 1>(Ws, Ss, Xs, CS, sub, sd);
-        if (c < r1 && sub == 0u) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int r = 0; r < UOCR_K_TOPK; ++r) acc = fmaf(w[r], d[r], acc);
-            out[c] = (h16)(acc + (float)(h16)sd[0] + (float)res[c]);
-        }
-    }
+    const float sd = group_sum<LPR>(frag_dot<QS, LPR, JS>(fs, ms + UOCR_K_TOPK * I, CS, sub));
+    if (c < UOCR_K_HIDDEN && sub == 0u) out[c] = (h16)(acc + (float)(h16)sd + (float)res[c]);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -670,12 +797,12 @@ __global__ __launch_bounds__(GBLOCK) void k_moe_down(uocr_expert_slab sl, const 
 /* ------------------------------------------------------------------------ */
 
 template <int QT>
-__device__ __forceinline__ void k_embed_row_body(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
-                                                 uint32_t vocab, int32_t tok, h16 *__restrict__ out) {
-    const uint32_t K = UOCR_K_HIDDEN;
-    for (uint32_t c = threadIdx.x; c < K; c += blockDim.x) {
+__device__ __forceinline__ void embed_row_body(const uint8_t *__restrict__ W, const h16 *__restrict__ S, u32 vocab,
+                                               int32_t tok, h16 *__restrict__ out) {
+    const u32 K = UOCR_K_HIDDEN;
+    for (u32 c = threadIdx.x; c < K; c += blockDim.x) {
         float v = 0.0f;
-        if (tok >= 0 && (uint32_t)tok < vocab) {
+        if (tok >= 0 && (u32)tok < vocab) {
             const size_t r = (size_t)tok;
             if (QT == 1) {
                 v = (float)((const h16 *)W)[r * K + c];
@@ -684,7 +811,7 @@ __device__ __forceinline__ void k_embed_row_body(const uint8_t *__restrict__ W, 
                 if (QT == 3) {
                     v = (float)((const int8_t *)W)[r * K + c] * sc;
                 } else {
-                    const uint32_t j = c % 64u;
+                    const u32 j = c % 64u;
                     const uint8_t b = W[r * (K / 2u) + (c / 64u) * 32u + (j & 31u)];
                     v = (float)((int)(j < 32u ? (b & 15u) : (b >> 4)) - 8) * sc;
                 }
@@ -695,21 +822,21 @@ __device__ __forceinline__ void k_embed_row_body(const uint8_t *__restrict__ W, 
 }
 
 template <int QT>
-__global__ __launch_bounds__(BLOCK) void k_embed(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
-                                                 uint32_t vocab, const int32_t *token,
-                                                 const uocr_step_state *st, h16 *__restrict__ out) {
-    k_embed_row_body<QT>(W, S, vocab, token != nullptr ? token[0] : st->cur_token, out);
+__global__ __launch_bounds__(BLOCK) void k_embed(const uint8_t *__restrict__ W, const h16 *__restrict__ S, u32 vocab,
+                                                 const int32_t *token, const uocr_step_state *st,
+                                                 h16 *__restrict__ out) {
+    embed_row_body<QT>(W, S, vocab, token != nullptr ? token[0] : st->cur_token, out);
 }
 
 /* Text rows of the prompt embedding: row b = dequant(E[ids[b]]) unless
  * mask[b] (image rows are placed by the host). */
 template <int QT>
 __global__ __launch_bounds__(BLOCK) void k_embed_rows(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
-                                                      uint32_t vocab, const int32_t *__restrict__ ids,
+                                                      u32 vocab, const int32_t *__restrict__ ids,
                                                       const uint8_t *__restrict__ mask, h16 *__restrict__ out) {
-    const uint32_t b = blockIdx.x;
+    const u32 b = blockIdx.x;
     if (mask != nullptr && mask[b] != 0u) return;
-    k_embed_row_body<QT>(W, S, vocab, ids[b], out + (size_t)b * UOCR_K_HIDDEN);
+    embed_row_body<QT>(W, S, vocab, ids[b], out + (size_t)b * UOCR_K_HIDDEN);
 }
 
 /* One replayable prefill step: position i = st->t; copy prompt row i into h
@@ -719,7 +846,7 @@ __global__ __launch_bounds__(BLOCK) void k_prefill_next(uocr_step_state *st, con
     const int32_t i = st->t;
     const uint4 *src = (const uint4 *)(prompt + (size_t)i * UOCR_K_HIDDEN);
     uint4 *dst = (uint4 *)h;
-    for (uint32_t c = threadIdx.x; c < UOCR_K_HIDDEN / 8u; c += blockDim.x) dst[c] = src[c];
+    for (u32 c = threadIdx.x; c < UOCR_K_HIDDEN / 8u; c += blockDim.x) dst[c] = src[c];
     __syncthreads();
     if (threadIdx.x == 0) {
         st->pos = i;
@@ -752,90 +879,57 @@ __global__ void k_decode_state(uocr_step_state *st, int32_t P, int32_t t) {
 }
 
 /* ------------------------------------------------------------------------ */
-/* LM head + argmax                                                          */
+/* LM head finalize                                                          */
 /* ------------------------------------------------------------------------ */
 
-__device__ __forceinline__ bool better(float s, uint32_t id, float bs, uint32_t bid) {
-    return id != NONE_ID && (bid == NONE_ID || s > bs || (s == bs && id < bid));
-}
-
-/* Pass 1: fused final RMSNorm + GEMV over vocab rows; each block writes its
- * best (score, id) with NaN rows skipped and ties to the lowest id. */
-template <int QT, int LPR>
-__global__ __launch_bounds__(GBLOCK) void k_lm_head(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
-                                                    uint32_t vocab, const h16 *__restrict__ x,
-                                                    const h16 *__restrict__ nw, uint32_t *__restrict__ part,
-                                                    uint32_t rpb) {
-    constexpr uint32_t R = 64u / LPR;
-    __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
-    __shared__ float red[16];
-    __shared__ float bsc[GBLOCK];
-    __shared__ uint32_t bidv[GBLOCK];
-    stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    const uint32_t sub = lane % LPR, grp = lane / LPR;
-    const uint32_t K = UOCR_K_HIDDEN, rb = row_bytes<QT>(K), C = rb / 16u, G = K / 64u;
-    const uint32_t r0 = blockIdx.x * rpb, r1 = min(vocab, r0 + rpb);
-    float bs = -INFINITY;
-    uint32_t bid = NONE_ID;
-    for (uint32_t base = r0 + wave * R; base < r1; base += nwave * R) {
-        const uint32_t r = base + grp, rr = r < r1 ? r : r1 - 1u;
-        const uint8_t *Wp[1] = {W + (size_t)rr * rb};
-        const h16 *Sp[1] = {S + (size_t)rr * G};
-        const h16 *Xp[1] = {xs};
-        float d[1];
-        group_dot<QT, LPR, 8, 1>(Wp, Sp, Xp, C, sub, d);
-        if (r < r1 && !isnan(d[0]) && better(d[0], r, bs, bid)) {
-            bs = d[0];
-            bid = r;
-        }
-    }
-    bsc[threadIdx.x] = bs;
-    bidv[threadIdx.x] = bid;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float b = -INFINITY;
-        uint32_t bi = NONE_ID;
-        for (uint32_t i = 0; i < blockDim.x; i += LPR) {
-            if (better(bsc[i], bidv[i], b, bi)) {
-                b = bsc[i];
-                bi = bidv[i];
-            }
-        }
-        part[2u * blockIdx.x] = __float_as_uint(b);
-        part[2u * blockIdx.x + 1u] = bi;
-    }
-}
-
-/* Pass 2 (one block): reduce the partials to the token id (none valid -> 0,
- * score -inf), store it at tokens[state->t] (or [0] without state); with
- * advance, write the next decode position into *state (uocr_metal.m:14239
- * and the ring plan of attention_decode.metal:25-33) and gather the selected
- * token's embedding row into h (embedding_q4.metal:21-56). */
+/* One block: reduce the nparts (<= 4 * BLOCK) argmax partials to the token
+ * id (none valid -> 0, score -inf), store it at tokens[state->t] (or [0]
+ * without state); with advance, write the next decode position into *state
+ * (uocr_metal.m:14239 and the ring plan of attention_decode.metal:25-33) and
+ * gather the selected token's embedding row into hout
+ * (embedding_q4.metal:21-56). */
 template <int QE>
-__global__ __launch_bounds__(BLOCK) void k_lm_finalize(const uint32_t *__restrict__ part, uint32_t nparts,
-                                                       uocr_step_state *st, int advance, int32_t *tokens,
-                                                       float *scores, const uint8_t *__restrict__ EW,
-                                                       const h16 *__restrict__ ES, uint32_t vocab,
-                                                       h16 *__restrict__ hout) {
-    __shared__ float bsc[BLOCK];
-    __shared__ uint32_t bidv[BLOCK];
+__global__ __launch_bounds__(BLOCK) void k_lm_finalize(const u32 *__restrict__ part, u32 nparts, uocr_step_state *st,
+                                                       int advance, int32_t *tokens, float *scores,
+                                                       const uint8_t *__restrict__ EW, const h16 *__restrict__ ES,
+                                                       u32 vocab, h16 *__restrict__ hout) {
+    __shared__ float bsc[NWAVE];
+    __shared__ u32 bidv[NWAVE];
     __shared__ int32_t chosen;
+    float ps[4];
+    u32 pid[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const u32 i = threadIdx.x + k * BLOCK;
+        ps[k] = i < nparts ? __uint_as_float(part[2u * i]) : -INFINITY;
+        pid[k] = i < nparts ? part[2u * i + 1u] : NONE_ID;
+    }
     float b = -INFINITY;
-    uint32_t bi = NONE_ID;
-    for (uint32_t i = threadIdx.x; i < nparts; i += blockDim.x) {
-        const float s = __uint_as_float(part[2u * i]);
-        const uint32_t id = part[2u * i + 1u];
-        if (better(s, id, b, bi)) {
-            b = s;
-            bi = id;
+    u32 bi = NONE_ID;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (better(ps[k], pid[k], b, bi)) {
+            b = ps[k];
+            bi = pid[k];
         }
     }
-    bsc[threadIdx.x] = b;
-    bidv[threadIdx.x] = bi;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float os = __shfl_xor(b, o);
+        const u32 oid = (u32)__shfl_xor((int)bi, o);
+        if (better(os, oid, b, bi)) {
+            b = os;
+            bi = oid;
+        }
+    }
+    const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    if (lane == 0u) {
+        bsc[wave] = b;
+        bidv[wave] = bi;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (uint32_t i = 1; i < blockDim.x; ++i) {
+        for (int i = 1; i < NWAVE; ++i) {
             if (better(bsc[i], bidv[i], b, bi)) {
                 b = bsc[i];
                 bi = bidv[i];
@@ -860,14 +954,14 @@ __global__ __launch_bounds__(BLOCK) void k_lm_finalize(const uint32_t *__restric
         chosen = id;
     }
     __syncthreads();
-    if (advance && EW != nullptr) k_embed_row_body<QE>(EW, ES, vocab, chosen, hout);
+    if (advance && EW != nullptr) embed_row_body<QE>(EW, ES, vocab, chosen, hout);
 }
 
 /* ------------------------------------------------------------------------ */
 /* launchers                                                                 */
 /* ------------------------------------------------------------------------ */
 
-static bool qt_ok(uint32_t q) {
+static bool qt_ok(u32 q) {
     return q == UOCR_QT_F16 || q == UOCR_QT_Q8 || q == UOCR_QT_Q4;
 }
 
@@ -875,22 +969,9 @@ static bool mat_ok(uocr_qmat m) {
     return m.w != nullptr && qt_ok(m.qtype) && (m.qtype == UOCR_QT_F16 || m.s != nullptr);
 }
 
-static uint32_t chunks_of(uint32_t qt, uint32_t K) {
-    return (qt == UOCR_QT_Q4 ? K / 2u : (qt == UOCR_QT_Q8 ? K : 2u * K)) / 16u;
+static u32 chunks_of(u32 qt, u32 K) {
+    return qt == UOCR_QT_Q4 ? K / 32u : (qt == UOCR_QT_Q8 ? K / 16u : K / 8u);
 }
-
-/* lanes per row: the smallest group that covers a row in at most 8 loads */
-static uint32_t pick_lpr(uint32_t C) {
-    for (uint32_t l = 4u; l < 64u; l *= 2u) {
-        if (C <= 8u * l) return l;
-    }
-    return 64u;
-}
-
-/* K = 1280 rows: Q4 -> 8 lanes, Q8 -> 16, f16 -> 32 (5 loads per lane) */
-#define LPR_1280(QT) ((QT) == 4 ? 8 : ((QT) == 3 ? 16 : 32))
-/* K = 896 with 2 loads per lane: Q4 -> 16, Q8 -> 32, f16 -> 64 */
-#define LPR_896(QT) ((QT) == 4 ? 16 : ((QT) == 3 ? 32 : 64))
 
 #define DISPATCH_QT(qt, F, ...)                                      \
     do {                                                             \
@@ -901,37 +982,55 @@ static uint32_t pick_lpr(uint32_t C) {
         }                                                            \
     } while (0)
 
-template <int QT, int LPR>
-static void launch_gemv_l(hipStream_t st, int epi, uocr_qmat W, uocr_qmat W2, uint32_t rows, uint32_t K,
-                          const uint16_t *x, const uint16_t *nw, const uint16_t *res, uint16_t *y) {
-    const uint32_t pass = 2u * (64u / LPR);
-    const uint32_t passes = (rows + pass * 1024u - 1u) / (pass * 1024u);
-    const uint32_t rpb = pass * passes;
-    const dim3 grid((rows + rpb - 1u) / rpb);
-    const uint8_t *w = (const uint8_t *)W.w, *w2 = (const uint8_t *)W2.w;
-    const h16 *s = (const h16 *)W.s, *s2 = (const h16 *)W2.s;
-    if (epi == EPI_SWIGLU) {
-        hipLaunchKernelGGL((k_gemv<QT, LPR, EPI_SWIGLU>), grid, dim3(GBLOCK), 0, st, w, s, w2, s2, rows, K,
-                           (const h16 *)x, (const h16 *)nw, (const h16 *)res, (h16 *)y, rpb);
-    } else if (epi == EPI_RESID) {
-        hipLaunchKernelGGL((k_gemv<QT, LPR, EPI_RESID>), grid, dim3(GBLOCK), 0, st, w, s, w2, s2, rows, K,
-                           (const h16 *)x, (const h16 *)nw, (const h16 *)res, (h16 *)y, rpb);
-    } else {
-        hipLaunchKernelGGL((k_gemv<QT, LPR, EPI_STORE>), grid, dim3(GBLOCK), 0, st, w, s, w2, s2, rows, K,
-                           (const h16 *)x, (const h16 *)nw, (const h16 *)res, (h16 *)y, rpb);
+/* Workgroups that fit on the device at once for a streaming kernel: waves
+ * per SIMD from its register use, 4 SIMDs per CU. */
+template <typename KFn>
+static u32 resident_blocks(KFn fn) {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+            cus = 256;
+        }
     }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, BLOCK, 0) != hipSuccess || per_cu <= 0) per_cu = 1;
+    return (u32)(cus * per_cu);
 }
 
-template <int QT>
-static void launch_gemv_qt(hipStream_t st, int epi, uocr_qmat W, uocr_qmat W2, uint32_t rows, uint32_t K,
-                           const uint16_t *x, const uint16_t *nw, const uint16_t *res, uint16_t *y) {
-    switch (pick_lpr(chunks_of(QT, K))) {
-        case 4: launch_gemv_l<QT, 4>(st, epi, W, W2, rows, K, x, nw, res, y); break;
-        case 8: launch_gemv_l<QT, 8>(st, epi, W, W2, rows, K, x, nw, res, y); break;
-        case 16: launch_gemv_l<QT, 16>(st, epi, W, W2, rows, K, x, nw, res, y); break;
-        case 32: launch_gemv_l<QT, 32>(st, epi, W, W2, rows, K, x, nw, res, y); break;
-        default: launch_gemv_l<QT, 64>(st, epi, W, W2, rows, K, x, nw, res, y); break;
+template <int QT, int LPR, int J, int EPI>
+static void launch_stream_lj(hipStream_t st, uocr_qmat W, uocr_qmat W2, u32 rows, u32 K, const uint16_t *x,
+                             const uint16_t *nw, const uint16_t *res, uint16_t *y, u32 *part, u32 max_blocks,
+                             u32 *nb_out) {
+    constexpr u32 R = 64u / LPR;
+    auto fn = k_stream<QT, LPR, J, EPI>;
+    const u32 groups = (rows + R - 1u) / R;
+    u32 nb = (groups + NWAVE - 1u) / NWAVE;
+    const u32 cap = resident_blocks(fn);
+    if (nb > cap) nb = cap;
+    if (nb > max_blocks) nb = max_blocks;
+    if (nb_out != nullptr) *nb_out = nb;
+    hipLaunchKernelGGL(fn, dim3(nb), dim3(BLOCK), 0, st, (const uint8_t *)W.w, (const h16 *)W.s,
+                       (const uint8_t *)W2.w, (const h16 *)W2.s, rows, K, (const h16 *)x, (const h16 *)nw,
+                       (const h16 *)res, (h16 *)y, part);
+}
+
+template <int QT, int EPI>
+static void launch_stream(hipStream_t st, uocr_qmat W, uocr_qmat W2, u32 rows, u32 K, const uint16_t *x,
+                          const uint16_t *nw, const uint16_t *res, uint16_t *y, u32 *part, u32 max_blocks,
+                          u32 *nb_out) {
+    const u32 C = chunks_of(QT, K);
+    const u32 lpr = lpr_for(C), j = (C + lpr - 1u) / lpr;
+#define LS(L, JJ) launch_stream_lj<QT, L, JJ, EPI>(st, W, W2, rows, K, x, nw, res, y, part, max_blocks, nb_out)
+    switch (lpr) {
+        case 4: if (j <= 5) LS(4, 5); else LS(4, 7); break;
+        case 8: if (j <= 5) LS(8, 5); else LS(8, 7); break;
+        case 16: if (j <= 5) LS(16, 5); else LS(16, 7); break;
+        case 32: if (j <= 5) LS(32, 5); else LS(32, 7); break;
+        default: if (j <= 7) LS(64, 7); else LS(64, 16); break;
     }
+#undef LS
 }
 
 extern "C" hipError_t uocr_launch_gemv(hipStream_t st, uocr_qmat W, uint32_t rows, uint32_t K, const uint16_t *x,
@@ -939,8 +1038,11 @@ extern "C" hipError_t uocr_launch_gemv(hipStream_t st, uocr_qmat W, uint32_t row
     if (!mat_ok(W) || x == nullptr || y == nullptr || rows == 0u || K == 0u || K % 64u != 0u || K > UOCR_K_MAX_K) {
         return hipErrorInvalidValue;
     }
-    const int epi = res != nullptr ? EPI_RESID : EPI_STORE;
-    DISPATCH_QT(W.qtype, launch_gemv_qt, st, epi, W, W, rows, K, x, nw, res, y);
+    switch (W.qtype) {
+        case UOCR_QT_F16: launch_stream<1, EPI_LINEAR>(st, W, W, rows, K, x, nw, res, y, nullptr, 0xffffffffu, nullptr); break;
+        case UOCR_QT_Q8: launch_stream<3, EPI_LINEAR>(st, W, W, rows, K, x, nw, res, y, nullptr, 0xffffffffu, nullptr); break;
+        default: launch_stream<4, EPI_LINEAR>(st, W, W, rows, K, x, nw, res, y, nullptr, 0xffffffffu, nullptr); break;
+    }
     return hipGetLastError();
 }
 
@@ -950,7 +1052,11 @@ extern "C" hipError_t uocr_launch_swiglu(hipStream_t st, uocr_qmat G, uocr_qmat 
         K == 0u || K % 64u != 0u || K > UOCR_K_MAX_K) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(G.qtype, launch_gemv_qt, st, EPI_SWIGLU, G, U, rows, K, x, nw, nullptr, mid);
+    switch (G.qtype) {
+        case UOCR_QT_F16: launch_stream<1, EPI_SWIGLU>(st, G, U, rows, K, x, nw, nullptr, mid, nullptr, 0xffffffffu, nullptr); break;
+        case UOCR_QT_Q8: launch_stream<3, EPI_SWIGLU>(st, G, U, rows, K, x, nw, nullptr, mid, nullptr, 0xffffffffu, nullptr); break;
+        default: launch_stream<4, EPI_SWIGLU>(st, G, U, rows, K, x, nw, nullptr, mid, nullptr, 0xffffffffu, nullptr); break;
+    }
     return hipGetLastError();
 }
 
@@ -964,11 +1070,11 @@ extern "C" hipError_t uocr_launch_rmsnorm(hipStream_t st, const uint16_t *x, con
 template <int QT>
 static void launch_qkv_qt(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
                           const uint16_t *nw, const RopeTab &tab, const uocr_step_state *state, uint16_t *qout,
-                          uint16_t *kc, uint16_t *vc, uint32_t cap) {
-    constexpr int LPR = LPR_1280(QT);
-    const uint32_t ipb = 2u * (64u / LPR);
-    hipLaunchKernelGGL((k_qkv_rope<QT, LPR>), dim3((1920u + ipb - 1u) / ipb), dim3(GBLOCK), 0, st, Q, K, V,
-                       (const h16 *)h, (const h16 *)nw, tab, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap, ipb);
+                          uint16_t *kc, uint16_t *vc, u32 cap) {
+    constexpr u32 R = 64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN));
+    constexpr u32 ipb = NWAVE * R;
+    hipLaunchKernelGGL((k_qkv_rope<QT>), dim3((1920u + ipb - 1u) / ipb), dim3(BLOCK), 0, st, Q, K, V, (const h16 *)h,
+                       (const h16 *)nw, tab, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap);
 }
 
 extern "C" hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
@@ -988,121 +1094,106 @@ extern "C" hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qma
 
 extern "C" hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache,
                                             const uint16_t *vcache, uint32_t cache_capacity,
-                                            const uocr_step_state *state, float *partials, uint16_t *ctx) {
+                                            const uocr_step_state *state, float *partials, uint32_t *counters,
+                                            uint16_t *ctx) {
     if (q == nullptr || kcache == nullptr || vcache == nullptr || cache_capacity == 0u || state == nullptr ||
-        partials == nullptr || ctx == nullptr) {
+        partials == nullptr || counters == nullptr || ctx == nullptr) {
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(k_attention, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(BLOCK), 0, st, (const h16 *)q,
-                       (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials);
-    hipLaunchKernelGGL(k_attention_merge, dim3(UOCR_K_HEADS), dim3(UOCR_K_HEAD_DIM), 0, st, (const float *)partials,
-                       (uint32_t)UOCR_K_ATTN_SPLITS, (h16 *)ctx);
+                       (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials, counters, (h16 *)ctx);
     return hipGetLastError();
 }
 
 template <int QS>
 static void launch_shared_router_qs(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R, const uint16_t *x,
-                                    const uint16_t *nw, uint16_t *smid, float *logits, bool with_shared) {
-    constexpr int LPRS = LPR_1280(QS);
-    const uint32_t rpb_s = 2u * (64u / LPRS);
-    const uint32_t nb_s = with_shared ? (1792u + rpb_s - 1u) / rpb_s : 0u;
-    const uint32_t rpb_r = 4u, nb_r = 64u / rpb_r;
-    hipLaunchKernelGGL((k_moe_shared_router<QS, LPRS>), dim3(nb_s + nb_r), dim3(GBLOCK), 0, st, SG, SU,
-                       (const h16 *)R, (const h16 *)x, (const h16 *)nw, (h16 *)smid, logits, nb_s, rpb_s, rpb_r);
+                                    const uint16_t *nw, int norm_topk, uint16_t *smid, float *logits, u32 *counter,
+                                    u32 *ids, float *weights, bool with_shared) {
+    constexpr u32 rpb = NWAVE * (64u / lpr_for(chunks_per_row<QS>(UOCR_K_HIDDEN)));
+    const u32 nb_s = with_shared ? (1792u + rpb - 1u) / rpb : 0u;
+    hipLaunchKernelGGL((k_moe_shared_router<QS>), dim3(nb_s + ROUTER_BLOCKS), dim3(BLOCK), 0, st, SG, SU,
+                       (const h16 *)R, (const h16 *)x, (const h16 *)nw, norm_topk, (h16 *)smid, logits, counter, ids,
+                       weights, nb_s);
 }
 
 extern "C" hipError_t uocr_launch_moe_shared_router(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R,
-                                                    const uint16_t *x, const uint16_t *nw, uint16_t *smid,
-                                                    float *logits) {
+                                                    const uint16_t *x, const uint16_t *nw, int norm_topk,
+                                                    uint16_t *smid, float *logits, uint32_t *counter, uint32_t *ids,
+                                                    float *weights) {
     if (!mat_ok(SG) || !mat_ok(SU) || SG.qtype != SU.qtype || R == nullptr || x == nullptr || smid == nullptr ||
-        logits == nullptr) {
+        logits == nullptr || counter == nullptr || ids == nullptr || weights == nullptr) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(SG.qtype, launch_shared_router_qs, st, SG, SU, R, x, nw, smid, logits, true);
+    DISPATCH_QT(SG.qtype, launch_shared_router_qs, st, SG, SU, R, x, nw, norm_topk, smid, logits, counter, ids, weights,
+                true);
     return hipGetLastError();
 }
 
 extern "C" hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, const uint16_t *x, const uint16_t *nw,
-                                         int norm_topk, float *logits, uint32_t *ids, float *weights) {
-    if (R == nullptr || x == nullptr || logits == nullptr || ids == nullptr || weights == nullptr) {
+                                         int norm_topk, float *logits, uint32_t *counter, uint32_t *ids,
+                                         float *weights) {
+    if (R == nullptr || x == nullptr || logits == nullptr || counter == nullptr || ids == nullptr ||
+        weights == nullptr) {
         return hipErrorInvalidValue;
     }
     uocr_qmat none = {R, nullptr, UOCR_QT_F16};
-    launch_shared_router_qs<1>(st, none, none, R, x, nw, nullptr, logits, false);
-    hipLaunchKernelGGL(k_router_topk, dim3(1), dim3(64), 0, st, (const float *)logits, norm_topk, ids, weights);
+    launch_shared_router_qs<1>(st, none, none, R, x, nw, norm_topk, nullptr, logits, counter, ids, weights, false);
     return hipGetLastError();
 }
 
 template <int QT>
-static void launch_moe_gu_qt(hipStream_t st, const uocr_expert_slab *slab, const float *logits, int norm_topk,
-                             const uint16_t *x, const uint16_t *nw, uint16_t *mid, uint32_t *ids_out, float *w_out) {
-    constexpr int LPR = LPR_1280(QT);
-    const uint32_t rows = UOCR_K_TOPK * 896u;
-    const uint32_t rpb = 2u * (64u / LPR);
-    hipLaunchKernelGGL((k_moe_gate_up<QT, LPR>), dim3((rows + rpb - 1u) / rpb), dim3(GBLOCK), 0, st, *slab, logits,
-                       norm_topk, (const h16 *)x, (const h16 *)nw, (h16 *)mid, ids_out, w_out, rpb);
+static void launch_moe_gu_qt(hipStream_t st, const uocr_expert_slab *slab, const u32 *ids, const uint16_t *x,
+                             const uint16_t *nw, uint16_t *mid) {
+    constexpr u32 rpb = NWAVE * (64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN)));
+    constexpr u32 rows = UOCR_K_TOPK * 896u;
+    hipLaunchKernelGGL((k_moe_gate_up<QT>), dim3((rows + rpb - 1u) / rpb), dim3(BLOCK), 0, st, *slab, ids,
+                       (const h16 *)x, (const h16 *)nw, (h16 *)mid);
 }
 
-extern "C" hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, const float *logits,
-                                              int norm_topk, const uint16_t *x, const uint16_t *nw, uint16_t *mid,
-                                              uint32_t *ids_out, float *weights_out) {
+extern "C" hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
+                                              const uint16_t *x, const uint16_t *nw, uint16_t *mid) {
     if (slab == nullptr || !mat_ok(slab->gate) || !mat_ok(slab->up) || slab->gate.qtype != slab->up.qtype ||
-        logits == nullptr || x == nullptr || mid == nullptr || ((ids_out == nullptr) != (weights_out == nullptr))) {
+        ids == nullptr || x == nullptr || mid == nullptr) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(slab->gate.qtype, launch_moe_gu_qt, st, slab, logits, norm_topk, x, nw, mid, ids_out, weights_out);
+    DISPATCH_QT(slab->gate.qtype, launch_moe_gu_qt, st, slab, ids, x, nw, mid);
     return hipGetLastError();
 }
 
 template <int QT, int QS>
-static void launch_moe_down_qs(hipStream_t st, const uocr_expert_slab *slab, const float *logits, int norm_topk,
+static void launch_moe_down_qs(hipStream_t st, const uocr_expert_slab *slab, const u32 *ids, const float *wts,
                                const uint16_t *mid, uocr_qmat SD, const uint16_t *smid, const uint16_t *res,
                                uint16_t *out) {
-    constexpr int LPR = LPR_896(QT);
-    const uint32_t rpb = 2u * (64u / LPR);
-    hipLaunchKernelGGL((k_moe_down<QT, QS, LPR>), dim3((UOCR_K_HIDDEN + rpb - 1u) / rpb), dim3(GBLOCK), 0, st, *slab,
-                       logits, norm_topk, (const h16 *)mid, SD, (const h16 *)smid, (const h16 *)res, (h16 *)out,
-                       rpb);
+    constexpr u32 rpb = NWAVE * (64u / lpr_down(QT));
+    hipLaunchKernelGGL((k_moe_down<QT, QS>), dim3((UOCR_K_HIDDEN + rpb - 1u) / rpb), dim3(BLOCK), 0, st, *slab, ids,
+                       wts, (const h16 *)mid, SD, (const h16 *)smid, (const h16 *)res, (h16 *)out);
 }
 
 template <int QT>
-static void launch_moe_down_qt(hipStream_t st, const uocr_expert_slab *slab, const float *logits, int norm_topk,
+static void launch_moe_down_qt(hipStream_t st, const uocr_expert_slab *slab, const u32 *ids, const float *wts,
                                const uint16_t *mid, uocr_qmat SD, const uint16_t *smid, const uint16_t *res,
                                uint16_t *out) {
     switch (SD.qtype) {
-        case UOCR_QT_F16: launch_moe_down_qs<QT, 1>(st, slab, logits, norm_topk, mid, SD, smid, res, out); break;
-        case UOCR_QT_Q8: launch_moe_down_qs<QT, 3>(st, slab, logits, norm_topk, mid, SD, smid, res, out); break;
-        default: launch_moe_down_qs<QT, 4>(st, slab, logits, norm_topk, mid, SD, smid, res, out); break;
+        case UOCR_QT_F16: launch_moe_down_qs<QT, 1>(st, slab, ids, wts, mid, SD, smid, res, out); break;
+        case UOCR_QT_Q8: launch_moe_down_qs<QT, 3>(st, slab, ids, wts, mid, SD, smid, res, out); break;
+        default: launch_moe_down_qs<QT, 4>(st, slab, ids, wts, mid, SD, smid, res, out); break;
     }
 }
 
-extern "C" hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const float *logits,
-                                           int norm_topk, const uint16_t *mid, uocr_qmat SD, const uint16_t *smid,
-                                           const uint16_t *res, uint16_t *out) {
-    if (slab == nullptr || !mat_ok(slab->down) || !mat_ok(SD) || logits == nullptr || mid == nullptr ||
-        smid == nullptr || res == nullptr || out == nullptr) {
+extern "C" hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
+                                           const float *weights, const uint16_t *mid, uocr_qmat SD,
+                                           const uint16_t *smid, const uint16_t *res, uint16_t *out) {
+    if (slab == nullptr || !mat_ok(slab->down) || !mat_ok(SD) || ids == nullptr || weights == nullptr ||
+        mid == nullptr || smid == nullptr || res == nullptr || out == nullptr) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(slab->down.qtype, launch_moe_down_qt, st, slab, logits, norm_topk, mid, SD, smid, res, out);
+    DISPATCH_QT(slab->down.qtype, launch_moe_down_qt, st, slab, ids, weights, mid, SD, smid, res, out);
     return hipGetLastError();
 }
 
-template <int QT>
-static uint32_t launch_lm_qt(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x, const uint16_t *nw,
-                             uint32_t *part) {
-    constexpr int LPR = LPR_1280(QT);
-    const uint32_t pass = 2u * (64u / LPR);
-    uint32_t rpb = (vocab + UOCR_K_LM_BLOCKS - 1u) / UOCR_K_LM_BLOCKS;
-    rpb = (rpb + pass - 1u) / pass * pass;
-    const uint32_t nb = (vocab + rpb - 1u) / rpb;
-    hipLaunchKernelGGL((k_lm_head<QT, LPR>), dim3(nb), dim3(GBLOCK), 0, st, (const uint8_t *)W.w, (const h16 *)W.s,
-                       vocab, (const h16 *)x, (const h16 *)nw, part, rpb);
-    return nb;
-}
-
 template <int QE>
-static void launch_lm_fin(hipStream_t st, const uint32_t *part, uint32_t nb, uocr_step_state *state, int advance,
-                          int32_t *tokens, float *scores, uocr_qmat E, uint32_t vocab, uint16_t *hout) {
+static void launch_lm_fin(hipStream_t st, const u32 *part, u32 nb, uocr_step_state *state, int advance,
+                          int32_t *tokens, float *scores, uocr_qmat E, u32 vocab, uint16_t *hout) {
     hipLaunchKernelGGL((k_lm_finalize<QE>), dim3(1), dim3(BLOCK), 0, st, part, nb, state, advance, tokens, scores,
                        (const uint8_t *)E.w, (const h16 *)E.s, vocab, (h16 *)hout);
 }
@@ -1114,11 +1205,12 @@ extern "C" hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t 
         (advance && state == nullptr) || (E.w != nullptr && (!mat_ok(E) || hout == nullptr))) {
         return hipErrorInvalidValue;
     }
-    uint32_t nb = 0;
+    u32 nb = 0;
+    const u32 maxb = 4u * BLOCK; /* finalize reduces at most 4 partials per thread */
     switch (W.qtype) {
-        case UOCR_QT_F16: nb = launch_lm_qt<1>(st, W, vocab, x, nw, partials); break;
-        case UOCR_QT_Q8: nb = launch_lm_qt<3>(st, W, vocab, x, nw, partials); break;
-        default: nb = launch_lm_qt<4>(st, W, vocab, x, nw, partials); break;
+        case UOCR_QT_F16: launch_stream<1, EPI_ARGMAX>(st, W, W, vocab, UOCR_K_HIDDEN, x, nw, nullptr, nullptr, partials, maxb, &nb); break;
+        case UOCR_QT_Q8: launch_stream<3, EPI_ARGMAX>(st, W, W, vocab, UOCR_K_HIDDEN, x, nw, nullptr, nullptr, partials, maxb, &nb); break;
+        default: launch_stream<4, EPI_ARGMAX>(st, W, W, vocab, UOCR_K_HIDDEN, x, nw, nullptr, nullptr, partials, maxb, &nb); break;
     }
     DISPATCH_QT(E.w != nullptr ? E.qtype : UOCR_QT_Q4, launch_lm_fin, st, partials, nb, state, advance, tokens, scores,
                 E, vocab, hout);
@@ -1126,7 +1218,7 @@ extern "C" hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t 
 }
 
 template <int QT>
-static void launch_embed_qt(hipStream_t st, uocr_qmat E, uint32_t vocab, const int32_t *token,
+static void launch_embed_qt(hipStream_t st, uocr_qmat E, u32 vocab, const int32_t *token,
                             const uocr_step_state *state, uint16_t *out) {
     hipLaunchKernelGGL((k_embed<QT>), dim3(1), dim3(BLOCK), 0, st, (const uint8_t *)E.w, (const h16 *)E.s, vocab,
                        token, state, (h16 *)out);
@@ -1140,8 +1232,8 @@ extern "C" hipError_t uocr_launch_embed(hipStream_t st, uocr_qmat E, uint32_t vo
 }
 
 template <int QT>
-static void launch_embed_rows_qt(hipStream_t st, uocr_qmat E, uint32_t vocab, const int32_t *ids,
-                                 const uint8_t *mask, uint32_t n, uint16_t *out) {
+static void launch_embed_rows_qt(hipStream_t st, uocr_qmat E, u32 vocab, const int32_t *ids, const uint8_t *mask,
+                                 u32 n, uint16_t *out) {
     hipLaunchKernelGGL((k_embed_rows<QT>), dim3(n), dim3(BLOCK), 0, st, (const uint8_t *)E.w, (const h16 *)E.s, vocab,
                        ids, mask, (h16 *)out);
 }
