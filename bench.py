@@ -142,7 +142,7 @@ def lm_head_roofline(log, iters: int = 60) -> dict:
             "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
             "traffic": None, "avg_launch_us": round(cold_ms * 1e3, 2), "hot_cache_achieved": round(
                 algo / (hot_ms / 1e3) / 1e9, 1), "algorithmic_bytes": algo, "launches": iters,
-            "note": "per-launch time includes the op's 4-byte counter reset (hipMemsetAsync)"}
+            "note": "one call = streaming GEMV+argmax kernel + one-block finalize"}
 
 
 def cpu_baseline(log, budget_s: float = 12.0) -> dict:
