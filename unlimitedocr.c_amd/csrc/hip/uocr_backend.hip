@@ -73,7 +73,7 @@ struct uocr_hip_ctx {
     uint64_t kv_bytes, scratch_bytes, moe_bytes, logits_bytes, prompt_bytes;
     uint16_t *kc, *vc, *h, *a, *q, *ctxv, *mid, *smid, *prompt;
     float *attn_part, *logits, *route_w;
-    uint32_t *sync, *route_ids;
+    uint32_t *route_ids;
     uint32_t *lm_part;
     uocr_step_state *state;
     int32_t *tokens;
@@ -319,7 +319,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_h = p.take(H_SIZE * 2u), o_a = p.take(H_SIZE * 2u), o_q = p.take(H_SIZE * 2u), o_c = p.take(H_SIZE * 2u);
     const uint64_t o_state = p.take(sizeof(uocr_step_state));
     const uint64_t o_apart = p.take(UOCR_ATTN_PARTIAL_FLOATS * 4u), o_logits = p.take(64u * 4u);
-    const uint64_t o_sync = p.take(UOCR_K_SYNC_WORDS * 4u), o_rids = p.take(64u), o_rwts = p.take(64u);
+    const uint64_t o_rids = p.take(64u), o_rwts = p.take(64u);
     const uint64_t scratch_end = p.off;
     const uint64_t o_mid = p.take(UOCR_DENSE_LAYER0_INTERMEDIATE * 2u), o_smid = p.take(UOCR_MOE_SHARED_INTERMEDIATE * 2u);
     const uint64_t moe_end = p.off;
@@ -341,7 +341,6 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->state = (uocr_step_state *)(b + o_state);
     ctx->attn_part = (float *)(b + o_apart);
     ctx->logits = (float *)(b + o_logits);
-    ctx->sync = (uint32_t *)(b + o_sync);
     ctx->route_ids = (uint32_t *)(b + o_rids);
     ctx->route_w = (float *)(b + o_rwts);
     ctx->mid = (uint16_t *)(b + o_mid);
@@ -391,14 +390,14 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c) {
         const dev_layer &L = c->L[l];
         uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
         ENQ(uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->invf, c->state, c->q, kc, vc, c->cache_cap));
-        ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part, c->sync + UOCR_SYNC_ATTN, c->ctxv));
-        ENQ(uocr_launch_gemv(s, L.o, H_SIZE, H_SIZE, c->ctxv, nullptr, c->h, c->a));
+        ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part));
+        ENQ(uocr_launch_attn_out(s, L.o, c->attn_part, c->h, c->a, nullptr));
         if (l == 0u) {
             ENQ(uocr_launch_swiglu(s, L.gate, L.up, UOCR_DENSE_LAYER0_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->mid));
             ENQ(uocr_launch_gemv(s, L.down, H_SIZE, UOCR_DENSE_LAYER0_INTERMEDIATE, c->mid, nullptr, c->a, c->h));
         } else {
             ENQ(uocr_launch_moe_shared_router(s, L.sgate, L.sup, L.router, c->a, L.post_norm, 0, c->smid, c->logits,
-                                              c->sync + UOCR_SYNC_ROUTER, c->route_ids, c->route_w));
+                                              c->route_ids, c->route_w));
             ENQ(uocr_launch_moe_gate_up(s, &L.slab, c->route_ids, c->a, L.post_norm, c->mid));
             ENQ(uocr_launch_moe_down(s, &L.slab, c->route_ids, c->route_w, c->mid, L.sdown, c->smid, c->a, c->h));
         }

@@ -27,11 +27,8 @@
 #define UOCR_K_TOPK 6
 #define UOCR_K_RING 128
 #define UOCR_K_MAX_K 6848          /* largest GEMV reduction length */
-#define UOCR_K_ATTN_SPLITS 32      /* split-K blocks per head in decode attention */
+#define UOCR_K_ATTN_SPLITS 16      /* split-K blocks per head in decode attention */
 #define UOCR_K_LM_BLOCKS 1024      /* upper bound on LM-head argmax partial blocks */
-#define UOCR_K_SYNC_WORDS 64       /* arrival counters of in-launch hand-offs */
-#define UOCR_SYNC_ATTN 0           /* UOCR_K_HEADS words */
-#define UOCR_SYNC_ROUTER 16        /* one word */
 
 /* Per-step decode state kept in device memory so one captured graph can be
  * replayed for every token.  Positions follow uocr_metal.m:14239 and the ring
@@ -83,24 +80,28 @@ hipError_t uocr_launch_rmsnorm(hipStream_t st, const uint16_t *x, const uint16_t
 hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
                                 const uint16_t *nw, const float *inv_freq, const uocr_step_state *state,
                                 uint16_t *qout, uint16_t *kcache, uint16_t *vcache, uint32_t cache_capacity);
-/* Split-K decode attention over the plan in *state (32 blocks per head); the
- * last block of each head merges the log-sum-exp partials into ctx.
- * partials: UOCR_ATTN_PARTIAL_FLOATS; counters: UOCR_K_HEADS words of the
- * zero-initialised sync area (left at zero on exit). */
+/* Split-K decode attention over the live slots [0, state->attn_len) of one
+ * layer's caches (UOCR_K_ATTN_SPLITS blocks per head, slots partitioned by
+ * cache_capacity): writes UOCR_ATTN_PARTIAL_FLOATS of per-split partials. */
 hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
-                                 uint32_t cache_capacity, const uocr_step_state *state, float *partials,
-                                 uint32_t *counters, uint16_t *ctx);
+                                 uint32_t cache_capacity, const uocr_step_state *state, float *partials);
+/* O projection with the attention merge in its prologue:
+ * out = f16(O . ctx + res), ctx = f16(merge(partials)); ctx_out (may be
+ * NULL) receives ctx. */
+hipError_t uocr_launch_attn_out(hipStream_t st, uocr_qmat O, const float *partials, const uint16_t *res,
+                                uint16_t *out, uint16_t *ctx_out);
+/* The merge alone: ctx = f16(merge(partials)). */
+hipError_t uocr_launch_attn_merge(hipStream_t st, const float *partials, uint16_t *ctx);
 /* One launch: shared-expert SwiGLU mid (1792 rows of SG/SU over rmsnorm(x))
- * and the 64 router logits (fp16 R, fp32 dot) of the same input; the router
- * block finishing last runs softmax + greedy top-6 (ties to the lower id, raw
- * probabilities unless norm_topk) into ids/weights.  counter: one word of the
- * sync area. */
+ * and, in one extra block, the 64 router logits (fp16 R, fp32 dot) of the
+ * same input followed by softmax + greedy top-6 (ties to the lower id, raw
+ * probabilities unless norm_topk) into ids/weights. */
 hipError_t uocr_launch_moe_shared_router(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R,
                                          const uint16_t *x, const uint16_t *nw, int norm_topk, uint16_t *smid,
-                                         float *logits, uint32_t *counter, uint32_t *ids, float *weights);
+                                         float *logits, uint32_t *ids, float *weights);
 /* Router alone (same kernel without the shared experts). */
 hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, const uint16_t *x, const uint16_t *nw, int norm_topk,
-                              float *logits, uint32_t *counter, uint32_t *ids, float *weights);
+                              float *logits, uint32_t *ids, float *weights);
 /* Routed gate/up of the experts in ids[0..5]:
  * mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = ids[r]. */
 hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,

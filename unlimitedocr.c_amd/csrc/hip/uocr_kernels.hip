@@ -23,13 +23,15 @@
  *    row_mirror) and lane swizzles beyond 16 lanes.
  *  - RoPE and the KV-cache write are fused into the QKV GEMV epilogue (one
  *    lane group owns rows d and d+64 of one head, the rotation pair).
- *  - Decode attention is split-K over the context (32 blocks per head, a
- *    16-lane group per cached token, 4 tokens' K/V in flight per group).  The
- *    last split block of a head to finish merges the log-sum-exp partials.
- *  - The MoE router logits are computed by spare blocks of the shared-expert
- *    gate/up launch; the last router block runs the greedy top-6 in one
- *    wavefront (64-bit keys of probability bits and inverted id, so ties go to
- *    the lower id) and publishes ids and weights for the routed kernels.
+ *  - Decode attention is split-K over the live KV slots (16 blocks per head,
+ *    slots partitioned by the cache capacity so the first K/V loads do not
+ *    wait for the step state; a 16-lane group per slot, 5 slots in flight per
+ *    group).  The log-sum-exp merge of the partials runs in the prologue of
+ *    the O projection, overlapped with that kernel's weight loads.
+ *  - The MoE router (64 fp16 rows) is one block of the shared-expert gate/up
+ *    launch; it runs the greedy top-6 in one wavefront (64-bit keys of
+ *    probability bits and inverted id, so ties go to the lower id) and
+ *    publishes ids and weights for the routed kernels.
  *  - The down-combine kernel fuses the 6 routed down projections, their
  *    weighted sum, the shared-expert down GEMV and the residual add.
  *  - The LM head is a streaming final-RMSNorm GEMV writing one argmax
@@ -38,14 +40,9 @@
  *    gathers the next token's embedding row, so a captured decode graph can
  *    be replayed.
  *
- * Cross-block hand-offs inside one launch (attention merge, router top-k)
- * never use a device-scope fence: on gfx950 such a fence writes back and
- * invalidates the whole L2 of the XCD.  The producer stores with agent-scope
- * (sc1) stores, which are coherent across the XCDs' L2s, waits for them with
- * s_waitcnt, then bumps an arrival counter with an agent-scope atomic; the
- * block that arrives last reads the data with agent-scope loads and re-arms
- * the counter to zero.  No block ever waits for another, so no launch can
- * stall on co-residency.
+ * Every cross-block hand-off is a kernel boundary: no kernel waits for
+ * another block and none uses a device-scope fence (on gfx950 such a fence
+ * writes back and invalidates the whole L2 of the XCD).
  */
 #include "uocr_kernels.h"
 
@@ -57,6 +54,7 @@ typedef uint32_t u32;
 
 #define BLOCK 256
 #define NWAVE (BLOCK / 64)
+#define SMALL_BLOCK 128 /* one-pass GEMVs with few rows: 2 wavefronts, more CUs */
 #define NONE_ID 0xffffffffu
 
 /* ------------------------------------------------------------------------ */
@@ -118,75 +116,97 @@ __device__ __forceinline__ float silu_f(float g) {
     return g / (1.0f + expf(-g));
 }
 
-/* ------------------------------------------------------------------------ */
-/* agent-scope (cross-XCD coherent) exchange inside one launch                */
-/* ------------------------------------------------------------------------ */
-
-__device__ __forceinline__ void st_agent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+/* Compiler-only fence on loaded values: every memory access before it stays
+ * before it, and v is consumed only after it.  Placed after a kernel's
+ * weight loads, it makes the compiler wait for an earlier-issued activation
+ * load with an in-order count that leaves the weight loads in flight
+ * (vector loads retire in issue order). */
+__device__ __forceinline__ void hold(uint4 &v) {
+    asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)::"memory");
 }
-
-__device__ __forceinline__ void st_agent(u32 *p, u32 v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void hold(float4 &v) {
+    asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)::"memory");
 }
-
-__device__ __forceinline__ float ld_agent(const float *p) {
-    return __hip_atomic_load((float *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-/* Called by every thread of the block after its agent-scope stores.  Waits
- * for those stores, counts the block in, and returns true in every thread of
- * the block that arrives last of n; that block also re-arms the counter. */
-__device__ __forceinline__ bool arrive_last(u32 *counter, u32 n) {
-    __shared__ u32 last;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const u32 prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = prev == n - 1u ? 1u : 0u;
-        if (last) st_agent(counter, 0u);
-    }
-    __syncthreads();
-    return last != 0u;
+__device__ __forceinline__ void hold(float2 &v) {
+    asm volatile("" : "+v"(v.x), "+v"(v.y)::"memory");
 }
 
 /* ------------------------------------------------------------------------ */
 /* activation staging                                                        */
 /* ------------------------------------------------------------------------ */
 
-/* Stage K (multiple of 8) fp16 activations into LDS; with nw apply RMSNorm
- * (eps 1e-6): xs[i] = f16(x[i] * inv_rms * nw[i]) (norm.metal:12-40
- * arithmetic: fp32 sum of squares, then one rounding per element). */
-__device__ __forceinline__ void stage_x(h16 *xs, const h16 *x, const h16 *nw, int K, float *red) {
-    const uint4 *src = (const uint4 *)x;
-    uint4 *dst = (uint4 *)xs;
-    const int n8 = K / 8;
+/* Activation staging in two halves so the activation loads are issued
+ * before a kernel's weight loads (vector loads retire in order: a load issued
+ * after the weights could only be consumed once every weight load is back).
+ * stage_load puts this thread's 16-byte pieces of x (and of the RMSNorm
+ * weight nw) in registers; stage_store, called after the weight loads are
+ * issued, applies RMSNorm (eps 1e-6) when nw is set,
+ *   xs[i] = f16(x[i] * inv_rms * nw[i])   (norm.metal:12-40 arithmetic:
+ *   fp32 sum of squares, one rounding per element),
+ * writes xs to LDS and synchronises the block.  KMAX and NT (threads) are
+ * compile-time; the runtime K (multiple of 8, <= KMAX) masks the pieces. */
+template <int KMAX, int NT>
+struct XStage {
+    static constexpr int PER = (KMAX / 8 + NT - 1) / NT;
+    uint4 x[PER], w[PER];
+};
+
+template <int KMAX, int NT>
+__device__ __forceinline__ void stage_load(XStage<KMAX, NT> &sx, const h16 *x, const h16 *nw, int K) {
+    /* branch-free (clamped index, nw aliased to x when absent) so the
+     * compiler keeps every load ahead of the first wait */
+    const uint4 *xp = (const uint4 *)x, *wp = (const uint4 *)(nw != nullptr ? nw : x);
+    const int last = K / 8 - 1;
+#pragma unroll
+    for (int p = 0; p < XStage<KMAX, NT>::PER; ++p) {
+        const int i = min((int)threadIdx.x + p * NT, last);
+        sx.x[p] = xp[i];
+        sx.w[p] = wp[i];
+    }
+}
+
+template <int KMAX, int NT>
+__device__ __forceinline__ void stage_store(XStage<KMAX, NT> &sx, h16 *xs, const h16 *nw, int K, float *red) {
+#pragma unroll
+    for (int p = 0; p < XStage<KMAX, NT>::PER; ++p) {
+        hold(sx.x[p]);
+        hold(sx.w[p]);
+    }
+    union h8 {
+        uint4 u;
+        h16 h[8];
+    };
     if (nw != nullptr) {
         float ss = 0.0f;
-        for (int i = threadIdx.x; i < n8; i += blockDim.x) {
-            union {
-                uint4 u;
-                h16 h[8];
-            } v;
-            v.u = src[i];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) ss = fmaf((float)v.h[j], (float)v.h[j], ss);
+        for (int p = 0; p < XStage<KMAX, NT>::PER; ++p) {
+            if ((int)threadIdx.x + p * NT < K / 8) {
+                h8 v;
+                v.u = sx.x[p];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) ss = fmaf((float)v.h[j], (float)v.h[j], ss);
+            }
         }
         ss = block_sum(ss, red);
         const float inv = 1.0f / sqrtf(ss / (float)K + 1.0e-6f);
-        for (int i = threadIdx.x; i < n8; i += blockDim.x) {
-            union {
-                uint4 u;
-                h16 h[8];
-            } v, w;
-            v.u = src[i];
-            w.u = ((const uint4 *)nw)[i];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v.h[j] = (h16)(((float)v.h[j] * inv) * (float)w.h[j]);
-            dst[i] = v.u;
+        for (int p = 0; p < XStage<KMAX, NT>::PER; ++p) {
+            const int i = threadIdx.x + p * NT;
+            if (i < K / 8) {
+                h8 v, w;
+                v.u = sx.x[p];
+                w.u = sx.w[p];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v.h[j] = (h16)(((float)v.h[j] * inv) * (float)w.h[j]);
+                ((uint4 *)xs)[i] = v.u;
+            }
         }
     } else {
-        for (int i = threadIdx.x; i < n8; i += blockDim.x) dst[i] = src[i];
+#pragma unroll
+        for (int p = 0; p < XStage<KMAX, NT>::PER; ++p) {
+            const int i = threadIdx.x + p * NT;
+            if (i < K / 8) ((uint4 *)xs)[i] = sx.x[p];
+        }
     }
     __syncthreads();
 }
@@ -298,12 +318,13 @@ struct RowFrag {
 
 template <int QT, int LPR, int J>
 __device__ __forceinline__ void frag_load(RowFrag<J> &f, const uint8_t *W, const h16 *S, u32 C, u32 sub) {
+    /* branch-free: chunks past the row re-read its last chunk and are
+     * dropped in frag_dot, so no wait lands between the loads */
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const u32 c = sub + LPR * j;
-        const bool in = c < C;
-        f.w[j] = in ? *(const uint4 *)(W + 16u * c) : make_uint4(0u, 0u, 0u, 0u);
-        if (QT != 1) f.s[j] = in ? S[c / chunks_per_group<QT>()] : (h16)0.0f;
+        const u32 c = min(sub + LPR * j, C - 1u);
+        f.w[j] = *(const uint4 *)(W + 16u * c);
+        if (QT != 1) f.s[j] = S[c / chunks_per_group<QT>()];
     }
 }
 
@@ -314,9 +335,10 @@ __device__ __forceinline__ float frag_dot(const RowFrag<J> &f, const h16 *xs, u3
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const u32 c = sub + LPR * j;
-        if (c < C) {
-            const float d = chunk_dot<QT>(f.w[j], xs, c);
-            acc = QT == 1 ? acc + d : fmaf(d, (float)f.s[j], acc);
+        if (LPR * (j + 1) <= C || c < C) {
+            const float d = chunk_dot<QT>(f.w[j], xs, min(c, C - 1u));
+            const float v = QT == 1 ? d : d * (float)f.s[j];
+            acc += c < C ? v : 0.0f;
         }
     }
     return acc;
@@ -421,8 +443,10 @@ __global__ __launch_bounds__(BLOCK) void k_stream(const uint8_t *__restrict__ W,
         }
     };
 
-    if (g < ngroups) load(fa, g);
-    stage_x(xs, x, nw, (int)K, red);
+    XStage<UOCR_K_MAX_K, BLOCK> sx;
+    stage_load(sx, x, nw, (int)K);
+    load(fa, min(g, ngroups - 1u));
+    stage_store(sx, xs, nw, (int)K, red);
     while (g < ngroups) {
         const u32 g1 = g + stride;
         if (g1 < ngroups) load(fb, g1);
@@ -490,7 +514,7 @@ struct RopeTab {
  * fp16, rotates q/k by the split-half RoPE at st->pos and stores q, or k/v
  * into the cache slot st->cache_token.  One item per lane group. */
 template <int QT>
-__global__ __launch_bounds__(BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, uocr_qmat V, const h16 *__restrict__ hin,
+__global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, uocr_qmat V, const h16 *__restrict__ hin,
                                                     const h16 *__restrict__ nw, RopeTab rope,
                                                     const uocr_step_state *__restrict__ st, h16 *__restrict__ qout,
                                                     h16 *__restrict__ kc, h16 *__restrict__ vc, u32 cap) {
@@ -500,17 +524,19 @@ __global__ __launch_bounds__(BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, u
     __shared__ float red[16];
     const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const u32 sub = lane % LPR, grp = lane / LPR;
-    const u32 item = (blockIdx.x * NWAVE + wave) * R + grp;
+    const u32 item = (blockIdx.x * (SMALL_BLOCK / 64) + wave) * R + grp;
     const u32 it = min(item, 1919u);
     const u32 m = it / 640u, rem = it % 640u, h = rem / 64u, d = rem % 64u;
     const uocr_qmat M = m == 0u ? Q : (m == 1u ? Km : V);
     const u32 ra = h * 128u + d, rbw = ra + 64u;
+    XStage<UOCR_K_HIDDEN, SMALL_BLOCK> sx;
+    stage_load(sx, hin, nw, UOCR_K_HIDDEN);
     RowFrag<J> fa, fb;
     frag_load<QT, LPR, J>(fa, (const uint8_t *)M.w + (size_t)ra * rb, (const h16 *)M.s + (size_t)ra * G, C, sub);
     frag_load<QT, LPR, J>(fb, (const uint8_t *)M.w + (size_t)rbw * rb, (const h16 *)M.s + (size_t)rbw * G, C, sub);
     const int32_t pos = st->pos;
     const u32 ct = (u32)st->cache_token;
-    stage_x(xs, hin, nw, UOCR_K_HIDDEN, red);
+    stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
     const float da = group_sum<LPR>(frag_dot<QT, LPR, J>(fa, xs, C, sub));
     const float db = group_sum<LPR>(frag_dot<QT, LPR, J>(fb, xs, C, sub));
     if (sub == 0u && item < 1920u) {
@@ -536,61 +562,67 @@ __global__ __launch_bounds__(BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, u
 }
 
 /* ------------------------------------------------------------------------ */
-/* split-K decode attention with last-block merge                            */
+/* split-K decode attention; merge in the O-projection prologue              */
 /* ------------------------------------------------------------------------ */
 
-#define ATT_UNROLL 4
+#define ATT_UNROLL 5
 
-/* Block (s, h) covers attention indices [s*chunk, (s+1)*chunk) of head h:
- * a 16-lane group per cached token (8 dims per lane), ATT_UNROLL tokens'
- * K/V rows loaded per group before the online-softmax updates, then a block
- * merge into one (max, sum, acc[128]) partial.  Indices >= attn_prompt map
- * into the 128-token ring (attention_decode.metal:25-33).  The last block of
- * the head to finish merges the S partials into ctx (fp16). */
+/* Live KV slots of a step are always [0, attn_len): the prompt slots
+ * [0, P) plus the ring slots [P, P + live) (before the ring wraps these hold
+ * generated tokens 0..live-1 in order; after it wraps all 128 slots are
+ * live).  Softmax over a set does not depend on the visiting order, so the
+ * kernel addresses slot i for attention index i and needs no ring
+ * arithmetic (attention_decode.metal:25-33 maps logical indices instead; the
+ * results differ only in fp32 summation order).
+ *
+ * Block (s, h) owns slots [s*chunk, (s+1)*chunk) with chunk fixed by the
+ * cache capacity, so its first K/V loads are issued before the step state
+ * (attention length) arrives; slots >= attn_len are masked afterwards.  A
+ * 16-lane group handles one slot (8 dims per lane), ATT_UNROLL slots in
+ * flight per group, with an online softmax; the block writes one partial
+ * (max, sum, acc[128]) per head:
+ *   acc at part[(h*S + s)*128 + d], (max, sum) at part[H*S*128 + (h*S + s)*2]. */
 __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, const h16 *__restrict__ kc,
                                                      const h16 *__restrict__ vc, u32 cap,
-                                                     const uocr_step_state *__restrict__ st, float *__restrict__ part,
-                                                     u32 *__restrict__ counters, h16 *__restrict__ ctx) {
-    constexpr int S = UOCR_K_ATTN_SPLITS, PW = UOCR_K_HEAD_DIM + 2;
+                                                     const uocr_step_state *__restrict__ st, float *__restrict__ part) {
+    constexpr int S = UOCR_K_ATTN_SPLITS;
     __shared__ float sm[16], sl[16];
     __shared__ float sacc[16][UOCR_K_HEAD_DIM];
     const int h = blockIdx.y, s = blockIdx.x;
-    const int P = st->attn_prompt, L = st->attn_len, fg = st->first_gen;
-    const int chunk = (L + S - 1) / S;
-    const int i0 = s * chunk, i1 = min(L, i0 + chunk);
+    const int chunk = ((int)cap + S - 1) / S;
+    const int i0 = s * chunk, iend = min((int)cap, i0 + chunk);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int gq = lane >> 4, p = lane & 15;
     const int gid = wave * 4 + gq;
     const float scale = 0.08838834764831845f; /* 1/sqrt(128) */
+    const h16 *kh = kc + (size_t)h * cap * 128u + 8 * p;
+    const h16 *vh = vc + (size_t)h * cap * 128u + 8 * p;
 
-    float qv[8];
-    {
-        union {
-            uint4 u;
-            h16 h[8];
-        } t;
-        t.u = *(const uint4 *)(q + h * 128 + 8 * p);
+    union h8 {
+        uint4 u;
+        h16 h[8];
+    };
+    h8 kk[ATT_UNROLL], vv[ATT_UNROLL];
+    auto load = [&](int ib) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qv[j] = (float)t.h[j];
-    }
+        for (int u = 0; u < ATT_UNROLL; ++u) {
+            const int t = min(ib + 16 * u, (int)cap - 1);
+            kk[u].u = *(const uint4 *)(kh + (size_t)t * 128u);
+            vv[u].u = *(const uint4 *)(vh + (size_t)t * 128u);
+        }
+    };
+    h8 qq;
+    qq.u = *(const uint4 *)(q + h * 128 + 8 * p);
+    load(i0 + gid);
+    hold(qq.u);
+    const int i1 = min(st->attn_len, iend);
+    float qv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qv[j] = (float)qq.h[j];
     float m = -INFINITY, l = 0.0f, acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-    const h16 *kh = kc + (size_t)h * cap * 128u;
-    const h16 *vh = vc + (size_t)h * cap * 128u;
-    for (int ib = i0 + gid; ib < i1; ib += 16 * ATT_UNROLL) {
-        union {
-            uint4 u;
-            h16 h[8];
-        } kk[ATT_UNROLL], vv[ATT_UNROLL];
-#pragma unroll
-        for (int u = 0; u < ATT_UNROLL; ++u) {
-            const int i = ib + 16 * u;
-            const int ii = i < i1 ? i : ib;
-            const int t = ii < P ? ii : P + (fg + ii - P) % UOCR_K_RING;
-            kk[u].u = *(const uint4 *)(kh + (size_t)t * 128u + 8 * p);
-            vv[u].u = *(const uint4 *)(vh + (size_t)t * 128u + 8 * p);
-        }
+    for (int ib = i0 + gid;;) {
 #pragma unroll
         for (int u = 0; u < ATT_UNROLL; ++u) {
             if (ib + 16 * u < i1) {
@@ -606,6 +638,9 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
                 m = mn;
             }
         }
+        ib += 16 * ATT_UNROLL;
+        if (ib >= i1) break;
+        load(ib);
     }
     if (p == 0) {
         sm[gid] = m;
@@ -614,7 +649,6 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
 #pragma unroll
     for (int j = 0; j < 8; ++j) sacc[gid][8 * p + j] = acc[j];
     __syncthreads();
-    float *ph = part + (size_t)h * S * PW;
     if (threadIdx.x < UOCR_K_HEAD_DIM) {
         const int d = threadIdx.x;
         float M = -INFINITY;
@@ -629,91 +663,188 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
                 A = fmaf(sacc[k][d], f, A);
             }
         }
-        float *pp = ph + (size_t)s * PW;
-        st_agent(pp + 2 + d, A);
+        part[(size_t)(h * S + s) * UOCR_K_HEAD_DIM + d] = A;
         if (d == 0) {
-            st_agent(pp, M);
-            st_agent(pp + 1, Ls);
+            float *ml = part + (size_t)UOCR_K_HEADS * S * UOCR_K_HEAD_DIM + (size_t)(h * S + s) * 2u;
+            ml[0] = M;
+            ml[1] = Ls;
         }
     }
-    if (!arrive_last(counters + h, (u32)S)) return;
-    if (threadIdx.x < UOCR_K_HEAD_DIM) {
-        const int d = threadIdx.x;
-        float Mk[S], Lk[S], Ak[S];
+}
+
+/* Log-sum-exp merge of the S attention partials into fp16 ctx[1280] in LDS
+ * (all threads of a BLOCK-thread block).  Threads t < H*S turn the (max,
+ * sum) pairs into per-split weights exp(M_k - M_h) / sum_k' L_k' exp(M_k' -
+ * M_h) in LDS; each thread then owns 4-dim quads of ctx and sums their S
+ * split accumulators (loads issued by merge_load, before the caller's
+ * weight loads). */
+struct MergeLoads {
+    static constexpr int NQ = (UOCR_K_HIDDEN / 4 + BLOCK - 1) / BLOCK;
+    float4 a[NQ][UOCR_K_ATTN_SPLITS];
+    float2 ml;
+};
+
+__device__ __forceinline__ void merge_load(MergeLoads &m, const float *__restrict__ part) {
+    constexpr int S = UOCR_K_ATTN_SPLITS, HD = UOCR_K_HEAD_DIM, Q = UOCR_K_HIDDEN / 4;
+    const int t = threadIdx.x;
 #pragma unroll
-        for (int k = 0; k < S; ++k) {
-            Mk[k] = ld_agent(ph + (size_t)k * PW);
-            Lk[k] = ld_agent(ph + (size_t)k * PW + 1);
-            Ak[k] = ld_agent(ph + (size_t)k * PW + 2 + d);
-        }
-        float M = -INFINITY;
+    for (int j = 0; j < MergeLoads::NQ; ++j) {
+        const int quad = min(t + j * BLOCK, Q - 1);
+        const int hh = quad / (HD / 4), dq = quad % (HD / 4);
 #pragma unroll
-        for (int k = 0; k < S; ++k) M = fmaxf(M, Mk[k]);
-        float Ls = 0.0f, A = 0.0f;
+        for (int k = 0; k < S; ++k) m.a[j][k] = *(const float4 *)(part + (size_t)(hh * S + k) * HD + 4 * dq);
+    }
+    m.ml = *(const float2 *)(part + (size_t)UOCR_K_HEADS * S * HD + 2u * min(t, UOCR_K_HEADS * S - 1));
+}
+
+__device__ __forceinline__ void merge_finish(MergeLoads &m, h16 *ctx, float *wk) {
+    constexpr int S = UOCR_K_ATTN_SPLITS, HD = UOCR_K_HEAD_DIM, Q = UOCR_K_HIDDEN / 4;
+    static_assert(S == 16, "weights use 16-lane DPP rows");
+    hold(m.ml);
 #pragma unroll
-        for (int k = 0; k < S; ++k) {
-            if (Mk[k] != -INFINITY) {
-                const float f = expf(Mk[k] - M);
-                Ls = fmaf(Lk[k], f, Ls);
-                A = fmaf(Ak[k], f, A);
+    for (int j = 0; j < MergeLoads::NQ; ++j) {
+#pragma unroll
+        for (int k = 0; k < S; ++k) hold(m.a[j][k]);
+    }
+    const int t = threadIdx.x;
+    if (t < UOCR_K_HEADS * S) {
+        /* lanes 16h..16h+15 of a row hold the splits of head h */
+        float M = m.ml.x;
+        M = fmaxf(M, __shfl_xor(M, 1));
+        M = fmaxf(M, __shfl_xor(M, 2));
+        M = fmaxf(M, __shfl_xor(M, 4));
+        M = fmaxf(M, __shfl_xor(M, 8));
+        const float f = m.ml.x == -INFINITY ? 0.0f : expf(m.ml.x - M);
+        const float Ls = row16_sum(m.ml.y * f);
+        wk[t] = f / Ls;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < MergeLoads::NQ; ++j) {
+        const int quad = t + j * BLOCK;
+        if (quad < Q) {
+            const int hh = quad / (HD / 4);
+            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                const float w = wk[hh * S + k];
+                acc.x = fmaf(m.a[j][k].x, w, acc.x);
+                acc.y = fmaf(m.a[j][k].y, w, acc.y);
+                acc.z = fmaf(m.a[j][k].z, w, acc.z);
+                acc.w = fmaf(m.a[j][k].w, w, acc.w);
             }
+            ctx[4 * quad] = (h16)acc.x;
+            ctx[4 * quad + 1] = (h16)acc.y;
+            ctx[4 * quad + 2] = (h16)acc.z;
+            ctx[4 * quad + 3] = (h16)acc.w;
         }
-        ctx[h * 128 + d] = (h16)(A / Ls);
     }
+    __syncthreads();
+}
+
+/* O projection with the attention merge in its prologue:
+ * out[r] = f16(O_r . ctx + res[r]), ctx = merge of the partials (fp16, the
+ * reference's attention-output rounding point).  Block 0 also stores ctx
+ * when ctx_out is set.  One row per lane group. */
+template <int QT>
+__global__ __launch_bounds__(BLOCK) void k_attn_out(uocr_qmat O, const float *__restrict__ part,
+                                                    const h16 *__restrict__ res, h16 *__restrict__ out,
+                                                    h16 *__restrict__ ctx_out) {
+    constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
+    constexpr u32 rb = 16u * C, G = K / 64u;
+    __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
+    __shared__ float wk[UOCR_K_HEADS * UOCR_K_ATTN_SPLITS];
+    const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const u32 sub = lane % LPR, grp = lane / LPR;
+    const u32 r = (blockIdx.x * NWAVE + wave) * R + grp, rr = min(r, K - 1u);
+    MergeLoads ml;
+    merge_load(ml, part);
+    RowFrag<J> f;
+    frag_load<QT, LPR, J>(f, (const uint8_t *)O.w + (size_t)rr * rb, (const h16 *)O.s + (size_t)rr * G, C, sub);
+    merge_finish(ml, xs, wk);
+    if (ctx_out != nullptr && blockIdx.x == 0) {
+        for (u32 i = threadIdx.x; i < K / 8u; i += blockDim.x) ((uint4 *)ctx_out)[i] = ((const uint4 *)xs)[i];
+    }
+    const float d = group_sum<LPR>(frag_dot<QT, LPR, J>(f, xs, C, sub));
+    if (r < K && sub == 0u) out[r] = (h16)(d + (float)res[r]);
+}
+
+/* Merge alone (operator API): ctx = merge of the partials. */
+__global__ __launch_bounds__(BLOCK) void k_attn_merge(const float *__restrict__ part, h16 *__restrict__ ctx) {
+    __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
+    __shared__ float wk[UOCR_K_HEADS * UOCR_K_ATTN_SPLITS];
+    MergeLoads ml;
+    merge_load(ml, part);
+    merge_finish(ml, xs, wk);
+    for (u32 i = threadIdx.x; i < UOCR_K_HIDDEN / 8u; i += blockDim.x) ((uint4 *)ctx)[i] = ((const uint4 *)xs)[i];
 }
 
 /* ------------------------------------------------------------------------ */
 /* MoE: shared experts + router, routed gate/up, down-combine                */
 /* ------------------------------------------------------------------------ */
 
-#define ROUTER_BLOCKS 8u /* 64 router rows: 8 per block, 2 per wavefront */
+#define MR_BLOCK 512 /* shared/router launch: 8 wavefronts per block */
 
 /* Blocks [0, nb_shared) compute the shared-expert SwiGLU rows (1792, one row
- * per lane group) and the last ROUTER_BLOCKS blocks the 64 router logits
- * (fp16 rows, fp32 dot); both read the same RMSNorm'd input.  The router
- * block that finishes last runs the top-6 and writes ids/weights. */
+ * per lane group); block nb_shared computes all 64 router logits (fp16
+ * rows, fp32 dot; 16 lanes x 10 chunks per row, every load in flight), then
+ * the top-6 of them in one wavefront, and writes ids/weights.  Both parts
+ * read the same RMSNorm'd input. */
 template <int QS>
-__global__ __launch_bounds__(BLOCK) void k_moe_shared_router(uocr_qmat SG, uocr_qmat SU, const h16 *__restrict__ Rw,
-                                                             const h16 *__restrict__ x, const h16 *__restrict__ nw,
-                                                             int norm_topk, h16 *__restrict__ smid,
-                                                             float *__restrict__ logits, u32 *__restrict__ counter,
-                                                             u32 *__restrict__ ids, float *__restrict__ weights,
-                                                             u32 nb_shared) {
+__global__ __launch_bounds__(MR_BLOCK) void k_moe_shared_router(uocr_qmat SG, uocr_qmat SU, const h16 *__restrict__ Rw,
+                                                                const h16 *__restrict__ x, const h16 *__restrict__ nw,
+                                                                int norm_topk, h16 *__restrict__ smid,
+                                                                float *__restrict__ logits, u32 *__restrict__ ids,
+                                                                float *__restrict__ weights, u32 nb_shared) {
+    constexpr u32 NW8 = MR_BLOCK / 64;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
+    __shared__ float lg[UOCR_K_EXPERTS];
     const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     if (blockIdx.x < nb_shared) {
         constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QS>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
         constexpr u32 rb = 16u * C, G = K / 64u;
         const u32 sub = lane % LPR, grp = lane / LPR;
-        const u32 r = (blockIdx.x * NWAVE + wave) * R + grp, rr = min(r, 1791u);
+        const u32 r = (blockIdx.x * NW8 + wave) * R + grp, rr = min(r, 1791u);
+        XStage<UOCR_K_HIDDEN, MR_BLOCK> sx;
+        stage_load(sx, x, nw, UOCR_K_HIDDEN);
         RowFrag<J> fg, fu;
         frag_load<QS, LPR, J>(fg, (const uint8_t *)SG.w + (size_t)rr * rb, (const h16 *)SG.s + (size_t)rr * G, C, sub);
         frag_load<QS, LPR, J>(fu, (const uint8_t *)SU.w + (size_t)rr * rb, (const h16 *)SU.s + (size_t)rr * G, C, sub);
-        stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
+        stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
         const float dg = group_sum<LPR>(frag_dot<QS, LPR, J>(fg, xs, C, sub));
         const float du = group_sum<LPR>(frag_dot<QS, LPR, J>(fu, xs, C, sub));
         if (r < 1792u && sub == 0u) smid[r] = (h16)(silu_f(dg) * du);
         return;
     }
-    constexpr u32 C = chunks_per_row<1>(UOCR_K_HIDDEN), LPR = 32u, J = (C + LPR - 1u) / LPR;
-    constexpr u32 rb = 16u * C;
+    constexpr u32 C = chunks_per_row<1>(UOCR_K_HIDDEN), LPR = 16u, J = C / LPR, RPW = 64u / LPR;
+    constexpr u32 rb = 16u * C, ROWS_PER_PASS = NW8 * RPW;
+    static_assert(UOCR_K_EXPERTS == 2 * ROWS_PER_PASS, "router block covers 64 rows in two row slots");
     const u32 sub = lane % LPR, grp = lane / LPR;
-    const u32 rblk = blockIdx.x - nb_shared;
-    const u32 r = rblk * 8u + wave * 2u + grp;
-    RowFrag<J> f;
-    frag_load<1, LPR, J>(f, (const uint8_t *)Rw + (size_t)r * rb, nullptr, C, sub);
-    stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
-    const float d = group_sum<LPR>(frag_dot<1, LPR, J>(f, xs, C, sub));
-    if (sub == 0u) st_agent(logits + r, d);
-    if (!arrive_last(counter, ROUTER_BLOCKS)) return;
-    if (threadIdx.x < 64u) topk6_wave(ld_agent(logits + threadIdx.x), norm_topk, ids, weights);
+    const u32 r0 = wave * RPW + grp, r1 = r0 + ROWS_PER_PASS;
+    XStage<UOCR_K_HIDDEN, MR_BLOCK> sx;
+    stage_load(sx, x, nw, UOCR_K_HIDDEN);
+    RowFrag<J> f0, f1;
+    frag_load<1, LPR, J>(f0, (const uint8_t *)Rw + (size_t)r0 * rb, nullptr, C, sub);
+    frag_load<1, LPR, J>(f1, (const uint8_t *)Rw + (size_t)r1 * rb, nullptr, C, sub);
+    stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
+    const float d0 = group_sum<LPR>(frag_dot<1, LPR, J>(f0, xs, C, sub));
+    const float d1 = group_sum<LPR>(frag_dot<1, LPR, J>(f1, xs, C, sub));
+    if (sub == 0u) {
+        lg[r0] = d0;
+        lg[r1] = d1;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64u) {
+        logits[threadIdx.x] = lg[threadIdx.x];
+        topk6_wave(lg[threadIdx.x], norm_topk, ids, weights);
+    }
 }
 
 /* Routed gate/up: mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)),
  * e = ids[r]; one row pair per lane group. */
 template <int QT>
-__global__ __launch_bounds__(BLOCK) void k_moe_gate_up(uocr_expert_slab sl, const u32 *__restrict__ ids,
+__global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl, const u32 *__restrict__ ids,
                                                        const h16 *__restrict__ x, const h16 *__restrict__ nw,
                                                        h16 *__restrict__ mid) {
     constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
@@ -722,7 +853,9 @@ __global__ __launch_bounds__(BLOCK) void k_moe_gate_up(uocr_expert_slab sl, cons
     __shared__ float red[16];
     const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const u32 sub = lane % LPR, grp = lane / LPR;
-    const u32 r = (blockIdx.x * NWAVE + wave) * R + grp, rr = min(r, ROWS - 1u);
+    const u32 r = (blockIdx.x * (SMALL_BLOCK / 64) + wave) * R + grp, rr = min(r, ROWS - 1u);
+    XStage<UOCR_K_HIDDEN, SMALL_BLOCK> sx;
+    stage_load(sx, x, nw, UOCR_K_HIDDEN);
     const u32 rank = rr / I, col = rr % I;
     const u32 e0 = ids[rank];
     const u32 e = e0 < UOCR_K_EXPERTS ? e0 : 0u;
@@ -731,16 +864,17 @@ __global__ __launch_bounds__(BLOCK) void k_moe_gate_up(uocr_expert_slab sl, cons
                           (const h16 *)sl.gate.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
     frag_load<QT, LPR, J>(fu, (const uint8_t *)sl.up.w + e * sl.gu_w_stride + (size_t)col * rb,
                           (const h16 *)sl.up.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
-    stage_x(xs, x, nw, UOCR_K_HIDDEN, red);
+    stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
     const float dg = group_sum<LPR>(frag_dot<QT, LPR, J>(fg, xs, C, sub));
     const float du = group_sum<LPR>(frag_dot<QT, LPR, J>(fu, xs, C, sub));
     if (r < ROWS && sub == 0u) mid[r] = (h16)(silu_f(dg) * du);
 }
 
-/* Lanes per output row of the down-combine: Q4 16, Q8 32, f16 64 (2 chunk
- * slots per routed row of K = 896). */
+/* Lanes per output row of the down-combine: Q4 32, Q8 and f16 64 (one or
+ * two chunk slots per routed row of K = 896), so 1280 rows spread over
+ * 160-320 workgroups. */
 __host__ __device__ constexpr u32 lpr_down(int QT) {
-    return QT == 4 ? 16u : (QT == 3 ? 32u : 64u);
+    return QT == 4 ? 32u : 64u;
 }
 
 /* Down projection of the 6 routed experts + weighted combine + shared-expert
@@ -758,6 +892,16 @@ __global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const u
     const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const u32 sub = lane % LPR, grp = lane / LPR;
     const u32 c = (blockIdx.x * NWAVE + wave) * R + grp, cc = min(c, (u32)UOCR_K_HIDDEN - 1u);
+    /* mids first (consumed first), then the shared-down row, then the routed
+     * rows once the expert ids are in */
+    constexpr u32 NMID = (UOCR_K_TOPK * I + SI) / 8u, PER = (NMID + BLOCK - 1u) / BLOCK;
+    uint4 mv[PER];
+#pragma unroll
+    for (u32 p = 0; p < PER; ++p) {
+        const u32 i = min(threadIdx.x + p * BLOCK, NMID - 1u);
+        const uint4 *src = i < UOCR_K_TOPK * I / 8u ? (const uint4 *)mid + i : (const uint4 *)smid + (i - UOCR_K_TOPK * I / 8u);
+        mv[p] = *src;
+    }
     RowFrag<JS> fs;
     frag_load<QS, LPR, JS>(fs, (const uint8_t *)SD.w + (size_t)cc * 16u * CS, (const h16 *)SD.s + (size_t)cc * GS, CS,
                            sub);
@@ -765,9 +909,13 @@ __global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const u
     float w[UOCR_K_TOPK];
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
-        const u32 id = ids[r];
-        e[r] = id < UOCR_K_EXPERTS ? id : 0u;
-        w[r] = id < UOCR_K_EXPERTS ? wts[r] : 0.0f;
+        e[r] = ids[r]; /* all 12 loads unconditional: one scalar round trip */
+        w[r] = wts[r];
+    }
+#pragma unroll
+    for (int r = 0; r < UOCR_K_TOPK; ++r) {
+        w[r] = e[r] < UOCR_K_EXPERTS ? w[r] : 0.0f;
+        e[r] = e[r] < UOCR_K_EXPERTS ? e[r] : 0u;
     }
     RowFrag<JD> fd[UOCR_K_TOPK];
 #pragma unroll
@@ -775,12 +923,12 @@ __global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const u
         frag_load<QT, LPR, JD>(fd[r], (const uint8_t *)sl.down.w + e[r] * sl.dn_w_stride + (size_t)cc * 16u * CD,
                                (const h16 *)sl.down.s + e[r] * sl.dn_s_stride + (size_t)cc * GD, CD, sub);
     }
-    {
-        const uint4 *a = (const uint4 *)mid;
-        const uint4 *b = (const uint4 *)smid;
-        uint4 *d = (uint4 *)ms;
-        for (u32 i = threadIdx.x; i < UOCR_K_TOPK * I / 8u; i += blockDim.x) d[i] = a[i];
-        for (u32 i = threadIdx.x; i < SI / 8u; i += blockDim.x) d[UOCR_K_TOPK * I / 8u + i] = b[i];
+#pragma unroll
+    for (u32 p = 0; p < PER; ++p) hold(mv[p]);
+#pragma unroll
+    for (u32 p = 0; p < PER; ++p) {
+        const u32 i = threadIdx.x + p * BLOCK;
+        if (i < NMID) ((uint4 *)ms)[i] = mv[p];
     }
     __syncthreads();
     float acc = 0.0f;
@@ -1072,8 +1220,8 @@ static void launch_qkv_qt(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V,
                           const uint16_t *nw, const RopeTab &tab, const uocr_step_state *state, uint16_t *qout,
                           uint16_t *kc, uint16_t *vc, u32 cap) {
     constexpr u32 R = 64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN));
-    constexpr u32 ipb = NWAVE * R;
-    hipLaunchKernelGGL((k_qkv_rope<QT>), dim3((1920u + ipb - 1u) / ipb), dim3(BLOCK), 0, st, Q, K, V, (const h16 *)h,
+    constexpr u32 ipb = (SMALL_BLOCK / 64) * R;
+    hipLaunchKernelGGL((k_qkv_rope<QT>), dim3((1920u + ipb - 1u) / ipb), dim3(SMALL_BLOCK), 0, st, Q, K, V, (const h16 *)h,
                        (const h16 *)nw, tab, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap);
 }
 
@@ -1094,59 +1242,74 @@ extern "C" hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qma
 
 extern "C" hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache,
                                             const uint16_t *vcache, uint32_t cache_capacity,
-                                            const uocr_step_state *state, float *partials, uint32_t *counters,
-                                            uint16_t *ctx) {
+                                            const uocr_step_state *state, float *partials) {
     if (q == nullptr || kcache == nullptr || vcache == nullptr || cache_capacity == 0u || state == nullptr ||
-        partials == nullptr || counters == nullptr || ctx == nullptr) {
+        partials == nullptr) {
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(k_attention, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(BLOCK), 0, st, (const h16 *)q,
-                       (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials, counters, (h16 *)ctx);
+                       (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials);
+    return hipGetLastError();
+}
+
+template <int QT>
+static void launch_attn_out_qt(hipStream_t st, uocr_qmat O, const float *partials, const uint16_t *res, uint16_t *out,
+                               uint16_t *ctx_out) {
+    constexpr u32 rpb = NWAVE * (64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN)));
+    hipLaunchKernelGGL((k_attn_out<QT>), dim3((UOCR_K_HIDDEN + rpb - 1u) / rpb), dim3(BLOCK), 0, st, O, partials,
+                       (const h16 *)res, (h16 *)out, (h16 *)ctx_out);
+}
+
+extern "C" hipError_t uocr_launch_attn_out(hipStream_t st, uocr_qmat O, const float *partials, const uint16_t *res,
+                                           uint16_t *out, uint16_t *ctx_out) {
+    if (!mat_ok(O) || partials == nullptr || res == nullptr || out == nullptr) return hipErrorInvalidValue;
+    DISPATCH_QT(O.qtype, launch_attn_out_qt, st, O, partials, res, out, ctx_out);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_attn_merge(hipStream_t st, const float *partials, uint16_t *ctx) {
+    if (partials == nullptr || ctx == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attn_merge, dim3(1), dim3(BLOCK), 0, st, partials, (h16 *)ctx);
     return hipGetLastError();
 }
 
 template <int QS>
 static void launch_shared_router_qs(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R, const uint16_t *x,
-                                    const uint16_t *nw, int norm_topk, uint16_t *smid, float *logits, u32 *counter,
-                                    u32 *ids, float *weights, bool with_shared) {
-    constexpr u32 rpb = NWAVE * (64u / lpr_for(chunks_per_row<QS>(UOCR_K_HIDDEN)));
+                                    const uint16_t *nw, int norm_topk, uint16_t *smid, float *logits, u32 *ids,
+                                    float *weights, bool with_shared) {
+    constexpr u32 rpb = (MR_BLOCK / 64) * (64u / lpr_for(chunks_per_row<QS>(UOCR_K_HIDDEN)));
     const u32 nb_s = with_shared ? (1792u + rpb - 1u) / rpb : 0u;
-    hipLaunchKernelGGL((k_moe_shared_router<QS>), dim3(nb_s + ROUTER_BLOCKS), dim3(BLOCK), 0, st, SG, SU,
-                       (const h16 *)R, (const h16 *)x, (const h16 *)nw, norm_topk, (h16 *)smid, logits, counter, ids,
-                       weights, nb_s);
+    hipLaunchKernelGGL((k_moe_shared_router<QS>), dim3(nb_s + 1u), dim3(MR_BLOCK), 0, st, SG, SU, (const h16 *)R,
+                       (const h16 *)x, (const h16 *)nw, norm_topk, (h16 *)smid, logits, ids, weights, nb_s);
 }
 
 extern "C" hipError_t uocr_launch_moe_shared_router(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R,
                                                     const uint16_t *x, const uint16_t *nw, int norm_topk,
-                                                    uint16_t *smid, float *logits, uint32_t *counter, uint32_t *ids,
-                                                    float *weights) {
+                                                    uint16_t *smid, float *logits, uint32_t *ids, float *weights) {
     if (!mat_ok(SG) || !mat_ok(SU) || SG.qtype != SU.qtype || R == nullptr || x == nullptr || smid == nullptr ||
-        logits == nullptr || counter == nullptr || ids == nullptr || weights == nullptr) {
+        logits == nullptr || ids == nullptr || weights == nullptr) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(SG.qtype, launch_shared_router_qs, st, SG, SU, R, x, nw, norm_topk, smid, logits, counter, ids, weights,
-                true);
+    DISPATCH_QT(SG.qtype, launch_shared_router_qs, st, SG, SU, R, x, nw, norm_topk, smid, logits, ids, weights, true);
     return hipGetLastError();
 }
 
 extern "C" hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, const uint16_t *x, const uint16_t *nw,
-                                         int norm_topk, float *logits, uint32_t *counter, uint32_t *ids,
-                                         float *weights) {
-    if (R == nullptr || x == nullptr || logits == nullptr || counter == nullptr || ids == nullptr ||
-        weights == nullptr) {
+                                         int norm_topk, float *logits, uint32_t *ids, float *weights) {
+    if (R == nullptr || x == nullptr || logits == nullptr || ids == nullptr || weights == nullptr) {
         return hipErrorInvalidValue;
     }
     uocr_qmat none = {R, nullptr, UOCR_QT_F16};
-    launch_shared_router_qs<1>(st, none, none, R, x, nw, norm_topk, nullptr, logits, counter, ids, weights, false);
+    launch_shared_router_qs<1>(st, none, none, R, x, nw, norm_topk, nullptr, logits, ids, weights, false);
     return hipGetLastError();
 }
 
 template <int QT>
 static void launch_moe_gu_qt(hipStream_t st, const uocr_expert_slab *slab, const u32 *ids, const uint16_t *x,
                              const uint16_t *nw, uint16_t *mid) {
-    constexpr u32 rpb = NWAVE * (64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN)));
+    constexpr u32 rpb = (SMALL_BLOCK / 64) * (64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN)));
     constexpr u32 rows = UOCR_K_TOPK * 896u;
-    hipLaunchKernelGGL((k_moe_gate_up<QT>), dim3((rows + rpb - 1u) / rpb), dim3(BLOCK), 0, st, *slab, ids,
+    hipLaunchKernelGGL((k_moe_gate_up<QT>), dim3((rows + rpb - 1u) / rpb), dim3(SMALL_BLOCK), 0, st, *slab, ids,
                        (const h16 *)x, (const h16 *)nw, (h16 *)mid);
 }
 

@@ -78,19 +78,11 @@ constexpr size_t WS_MID = WS_WTS + 256u;
 constexpr size_t WS_SMID = WS_MID + A256(6848u * 2u);
 constexpr size_t WS_Q = WS_SMID + A256(1792u * 2u);
 constexpr size_t WS_CTX = WS_Q + A256(1280u * 2u);
-constexpr size_t WS_SYNC = WS_CTX + A256(1280u * 2u);
-constexpr size_t WS_TOTAL = WS_SYNC + A256(UOCR_K_SYNC_WORDS * 4u);
+constexpr size_t WS_TOTAL = WS_CTX + A256(1280u * 2u);
 
 template <typename T>
 T *ws(void *base, size_t off) {
     return (T *)((uint8_t *)base + off);
-}
-
-/* The in-launch arrival counters start at zero; kernels leave them at zero,
- * but a caller's workspace may hold anything on its first use. */
-uint32_t *sync_area(hipStream_t st, void *workspace) {
-    uint32_t *p = ws<uint32_t>(workspace, WS_SYNC);
-    return hipMemsetAsync(p, 0, UOCR_K_SYNC_WORDS * 4u, st) == hipSuccess ? p : nullptr;
 }
 
 }  // namespace
@@ -143,11 +135,8 @@ extern "C" int uocr_op_router(const void *router_w, const void *x, const void *n
                               uint32_t *ids, float *weights) {
     if (workspace == nullptr) return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "router needs a workspace");
     STREAM_OR_RETURN(st);
-    uint32_t *sync = sync_area(st, workspace);
-    if (sync == nullptr) return op_fail(UOCR_ERROR_INTERNAL, "router: sync area clear failed");
     return hip_status(uocr_launch_router(st, (const uint16_t *)router_w, (const uint16_t *)x, (const uint16_t *)norm_w,
-                                         norm_topk, ws<float>(workspace, WS_LOGITS), sync + UOCR_SYNC_ROUTER, ids,
-                                         weights),
+                                         norm_topk, ws<float>(workspace, WS_LOGITS), ids, weights),
                       "router");
 }
 
@@ -171,12 +160,10 @@ extern "C" int uocr_op_moe_ffn(const uocr_op_moe_weights *m, const void *x, cons
     float *logits = ws<float>(workspace, WS_LOGITS);
     uint16_t *mid = ws<uint16_t>(workspace, WS_MID), *smid = ws<uint16_t>(workspace, WS_SMID);
     const uint16_t *xx = (const uint16_t *)x, *nw = (const uint16_t *)norm_w;
-    uint32_t *sync = sync_area(st, workspace);
-    if (sync == nullptr) return op_fail(UOCR_ERROR_INTERNAL, "moe_ffn: sync area clear failed");
     int r = hip_status(uocr_launch_moe_shared_router(st, qm(m->shared_qtype, m->sgate_w, m->sgate_s),
                                                      qm(m->shared_qtype, m->sup_w, m->sup_s),
                                                      (const uint16_t *)m->router, xx, nw, norm_topk, smid, logits,
-                                                     sync + UOCR_SYNC_ROUTER, wids, wwts),
+                                                     wids, wwts),
                        "moe shared gate/up + router");
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_moe_gate_up(st, &sl, wids, xx, nw, mid), "moe routed gate/up");
@@ -208,12 +195,12 @@ extern "C" int uocr_op_attention_decode(const void *q, const void *k_cache, cons
     STREAM_OR_RETURN(st);
     const int r = set_plan(st, workspace, cache_capacity, prompt_length, generated_count);
     if (r != UOCR_OK) return r;
-    uint32_t *sync = sync_area(st, workspace);
-    if (sync == nullptr) return op_fail(UOCR_ERROR_INTERNAL, "attention_decode: sync area clear failed");
-    return hip_status(uocr_launch_attention(st, (const uint16_t *)q, (const uint16_t *)k_cache, (const uint16_t *)v_cache,
-                                            cache_capacity, ws<uocr_step_state>(workspace, WS_STATE),
-                                            ws<float>(workspace, WS_APART), sync + UOCR_SYNC_ATTN, (uint16_t *)out),
-                      "attention_decode");
+    int r2 = hip_status(uocr_launch_attention(st, (const uint16_t *)q, (const uint16_t *)k_cache,
+                                              (const uint16_t *)v_cache, cache_capacity,
+                                              ws<uocr_step_state>(workspace, WS_STATE), ws<float>(workspace, WS_APART)),
+                        "attention_decode");
+    if (r2 != UOCR_OK) return r2;
+    return hip_status(uocr_launch_attn_merge(st, ws<float>(workspace, WS_APART), (uint16_t *)out), "attention merge");
 }
 
 extern "C" int uocr_op_attention_block(uint32_t qtype, const void *wq, const void *sq, const void *wk, const void *sk,
@@ -239,16 +226,13 @@ extern "C" int uocr_op_attention_block(uint32_t qtype, const void *wq, const voi
                        "qkv_rope");
     }
     if (r == UOCR_OK) {
-        uint32_t *sync = sync_area(st, workspace);
-        r = sync == nullptr ? op_fail(UOCR_ERROR_INTERNAL, "attention_block: sync area clear failed")
-                            : hip_status(uocr_launch_attention(st, qb, (const uint16_t *)k_cache,
-                                                               (const uint16_t *)v_cache, cache_capacity, state,
-                                                               ws<float>(workspace, WS_APART), sync + UOCR_SYNC_ATTN, cb),
-                                         "attention");
+        r = hip_status(uocr_launch_attention(st, qb, (const uint16_t *)k_cache, (const uint16_t *)v_cache,
+                                             cache_capacity, state, ws<float>(workspace, WS_APART)),
+                       "attention");
     }
     if (r == UOCR_OK) {
-        r = hip_status(uocr_launch_gemv(st, qm(qtype, wo, so), 1280u, 1280u, cb, nullptr, (const uint16_t *)hidden,
-                                        (uint16_t *)out),
+        r = hip_status(uocr_launch_attn_out(st, qm(qtype, wo, so), ws<float>(workspace, WS_APART),
+                                            (const uint16_t *)hidden, (uint16_t *)out, cb),
                        "o_proj");
     }
     return r;
