@@ -396,9 +396,9 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c) {
             ENQ(uocr_launch_swiglu(s, L.gate, L.up, UOCR_DENSE_LAYER0_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->mid));
             ENQ(uocr_launch_gemv(s, L.down, H_SIZE, UOCR_DENSE_LAYER0_INTERMEDIATE, c->mid, nullptr, c->a, c->h));
         } else {
-            ENQ(uocr_launch_moe_shared_router(s, L.sgate, L.sup, L.router, c->a, L.post_norm, 0, c->smid, c->logits,
-                                              c->route_ids, c->route_w));
-            ENQ(uocr_launch_moe_gate_up(s, &L.slab, c->route_ids, c->a, L.post_norm, c->mid));
+            ENQ(uocr_launch_router_logits(s, L.router, c->a, L.post_norm, c->logits));
+            ENQ(uocr_launch_moe_gate_up(s, &L.slab, L.sgate, L.sup, c->logits, 0, c->a, L.post_norm, c->mid, c->smid,
+                                        c->route_ids, c->route_w));
             ENQ(uocr_launch_moe_down(s, &L.slab, c->route_ids, c->route_w, c->mid, L.sdown, c->smid, c->a, c->h));
         }
     }

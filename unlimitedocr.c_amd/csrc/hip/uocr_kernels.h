@@ -92,20 +92,22 @@ hipError_t uocr_launch_attn_out(hipStream_t st, uocr_qmat O, const float *partia
                                 uint16_t *out, uint16_t *ctx_out);
 /* The merge alone: ctx = f16(merge(partials)). */
 hipError_t uocr_launch_attn_merge(hipStream_t st, const float *partials, uint16_t *ctx);
-/* One launch: shared-expert SwiGLU mid (1792 rows of SG/SU over rmsnorm(x))
- * and, in one extra block, the 64 router logits (fp16 R, fp32 dot) of the
- * same input followed by softmax + greedy top-6 (ties to the lower id, raw
+/* Router logits: logits[e] = R_e . rmsnorm(x) (fp16 R [64][1280], fp32 dot),
+ * one wavefront per expert row. */
+hipError_t uocr_launch_router_logits(hipStream_t st, const uint16_t *R, const uint16_t *x, const uint16_t *nw,
+                                     float *logits);
+/* Router logits + softmax + greedy top-6 (ties to the lower id; raw
  * probabilities unless norm_topk) into ids/weights. */
-hipError_t uocr_launch_moe_shared_router(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R,
-                                         const uint16_t *x, const uint16_t *nw, int norm_topk, uint16_t *smid,
-                                         float *logits, uint32_t *ids, float *weights);
-/* Router alone (same kernel without the shared experts). */
 hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, const uint16_t *x, const uint16_t *nw, int norm_topk,
                               float *logits, uint32_t *ids, float *weights);
-/* Routed gate/up of the experts in ids[0..5]:
- * mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = ids[r]. */
-hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
-                                   const uint16_t *x, const uint16_t *nw, uint16_t *mid);
+/* Gate/up of the routed experts (top-6 recomputed from logits per
+ * wavefront) and of the shared experts in one launch:
+ *   mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = rank-r expert,
+ *   smid[c]        = f16(silu(SG[c].xin) * (SU[c].xin)),  c < 1792,
+ * xin = x or rmsnorm(x, nw); ids/weights receive the selection. */
+hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG, uocr_qmat SU,
+                                   const float *logits, int norm_topk, const uint16_t *x, const uint16_t *nw,
+                                   uint16_t *mid, uint16_t *smid, uint32_t *ids, float *weights);
 /* Routed down + weighted combine + shared down + residual:
  * out[c] = f16(sum_r w_r * D_e[c].mid_r + f16(SD[c].smid) + res[c]). */
 hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,

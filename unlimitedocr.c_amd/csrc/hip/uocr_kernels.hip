@@ -353,34 +353,48 @@ __host__ __device__ constexpr u32 j_for(u32 C) {
     return (C + lpr_for(C) - 1u) / lpr_for(C);
 }
 
+/* Wave-uniform max of all 64 lanes with DPP row steps and readlanes. */
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
 /* Greedy top-6 over 64 router logits by one wavefront (one expert per lane):
- * max-subtracted softmax, then 6 rounds of a 64-bit max over
- * (probability bits, inverted id) so ties go to the lower id
- * (uocr_cpu_ref.c:443-463, moe.metal:12-18).  Raw probabilities unless
- * norm_topk.  Lane 0 writes ids/w. */
-__device__ __forceinline__ void topk6_wave(float lg, int norm_topk, u32 *ids, float *w) {
+ * max-subtracted softmax, then the greedy order of the keys (probability
+ * bits, inverted id), i.e. probability descending with ties to the lower id
+ * (uocr_cpu_ref.c:443-463, moe.metal:12-18).  Each lane counts the keys
+ * above its own (64 wave-uniform broadcasts, no dependent chain); the lanes
+ * of rank 0..5 are picked by ballot.  Raw probabilities unless norm_topk.
+ * The results are wave-uniform. */
+__device__ __forceinline__ void topk6(float lg, int norm_topk, u32 (&sid)[UOCR_K_TOPK], float (&sw)[UOCR_K_TOPK]) {
     const u32 lane = threadIdx.x & 63u;
-    const float mx = wave_max(lg);
+    const float mx = wave_max_dpp(lg);
     const float pe = expf(lg - mx);
     const float prob = pe / wave_sum(pe);
-    unsigned long long key = ((unsigned long long)__float_as_uint(prob) << 32) | (0xffffffffu - lane);
-    float sel[UOCR_K_TOPK];
-    u32 sid[UOCR_K_TOPK];
+    const u32 pb = __float_as_uint(prob);
+    const unsigned long long key = ((unsigned long long)pb << 32) | (0xffffffffu - lane);
+    u32 rank = 0;
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+        const unsigned long long kj =
+            ((unsigned long long)(u32)__builtin_amdgcn_readlane((int)pb, j) << 32) | (0xffffffffu - (u32)j);
+        rank += kj > key ? 1u : 0u;
+    }
     float tot = 0.0f;
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
-        const unsigned long long best = wave_max_u64(key);
-        sid[r] = 0xffffffffu - (u32)(best & 0xffffffffull);
-        sel[r] = __uint_as_float((u32)(best >> 32));
-        tot += sel[r];
-        if (lane == sid[r]) key = 0ull;
+        const unsigned long long m = __ballot(rank == (u32)r);
+        const u32 l = m != 0ull ? (u32)__builtin_ctzll(m) : 0u;
+        sid[r] = l;
+        sw[r] = __uint_as_float((u32)__builtin_amdgcn_readlane((int)pb, (int)l));
+        tot += sw[r];
     }
-    if (lane == 0u) {
+    if (norm_topk) {
 #pragma unroll
-        for (int r = 0; r < UOCR_K_TOPK; ++r) {
-            ids[r] = sid[r];
-            w[r] = norm_topk ? sel[r] / tot : sel[r];
-        }
+        for (int r = 0; r < UOCR_K_TOPK; ++r) sw[r] /= tot;
     }
 }
 
@@ -783,30 +797,65 @@ __global__ __launch_bounds__(BLOCK) void k_attn_merge(const float *__restrict__ 
 /* MoE: shared experts + router, routed gate/up, down-combine                */
 /* ------------------------------------------------------------------------ */
 
-#define MR_BLOCK 512 /* shared/router launch: 8 wavefronts per block */
-
-/* Blocks [0, nb_shared) compute the shared-expert SwiGLU rows (1792, one row
- * per lane group); block nb_shared computes all 64 router logits (fp16
- * rows, fp32 dot; 16 lanes x 10 chunks per row, every load in flight), then
- * the top-6 of them in one wavefront, and writes ids/weights.  Both parts
- * read the same RMSNorm'd input. */
-template <int QS>
-__global__ __launch_bounds__(MR_BLOCK) void k_moe_shared_router(uocr_qmat SG, uocr_qmat SU, const h16 *__restrict__ Rw,
-                                                                const h16 *__restrict__ x, const h16 *__restrict__ nw,
-                                                                int norm_topk, h16 *__restrict__ smid,
-                                                                float *__restrict__ logits, u32 *__restrict__ ids,
-                                                                float *__restrict__ weights, u32 nb_shared) {
-    constexpr u32 NW8 = MR_BLOCK / 64;
+/* Router logits: block r computes logit r = R_r . rmsnorm(x) (fp16 row,
+ * fp32 dot) with one wavefront, so the 64 rows (160 KB) stream through 64
+ * CUs. */
+__global__ __launch_bounds__(64) void k_router_logits(const h16 *__restrict__ Rw, const h16 *__restrict__ x,
+                                                      const h16 *__restrict__ nw, float *__restrict__ logits) {
+    constexpr u32 C = chunks_per_row<1>(UOCR_K_HIDDEN), LPR = 64u, J = (C + LPR - 1u) / LPR, rb = 16u * C;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
-    __shared__ float lg[UOCR_K_EXPERTS];
+    const u32 r = blockIdx.x, sub = threadIdx.x;
+    XStage<UOCR_K_HIDDEN, 64> sx;
+    stage_load(sx, x, nw, UOCR_K_HIDDEN);
+    RowFrag<J> f;
+    frag_load<1, LPR, J>(f, (const uint8_t *)Rw + (size_t)r * rb, nullptr, C, sub);
+    stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
+    const float d = group_sum<LPR>(frag_dot<1, LPR, J>(f, xs, C, sub));
+    if (sub == 0u) logits[r] = d;
+}
+
+/* Top-6 alone (operator API): one wavefront. */
+__global__ __launch_bounds__(64) void k_router_topk(const float *__restrict__ logits, int norm_topk, u32 *ids,
+                                                    float *weights) {
+    u32 sid[UOCR_K_TOPK];
+    float sw[UOCR_K_TOPK];
+    topk6(logits[threadIdx.x], norm_topk, sid, sw);
+    if (threadIdx.x < UOCR_K_TOPK) {
+#pragma unroll
+        for (int r = 0; r < UOCR_K_TOPK; ++r) {
+            if (threadIdx.x == (u32)r) {
+                ids[r] = sid[r];
+                weights[r] = sw[r];
+            }
+        }
+    }
+}
+
+/* Gate/up of the routed and the shared experts in one launch.
+ * Blocks [0, nb_routed): every wavefront recomputes the top-6 from the 64
+ * router logits (cheaper than another launch), then one row pair per lane
+ * group: mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = the
+ * rank-r expert; block 0 publishes ids/weights for the down kernel.
+ * Blocks [nb_routed, ...): smid[c] = f16(silu(SG[c].xin) * (SU[c].xin)),
+ * c < 1792.  xin = x or rmsnorm(x, nw). */
+template <int QT, int QS>
+__global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl, uocr_qmat SG, uocr_qmat SU,
+                                                             const float *__restrict__ logits, int norm_topk,
+                                                             const h16 *__restrict__ x, const h16 *__restrict__ nw,
+                                                             h16 *__restrict__ mid, h16 *__restrict__ smid,
+                                                             u32 *__restrict__ ids_out, float *__restrict__ w_out,
+                                                             u32 nb_routed) {
+    constexpr u32 K = UOCR_K_HIDDEN, G = K / 64u, I = 896u, ROWS = UOCR_K_TOPK * I, SI = 1792u;
+    constexpr u32 NWV = SMALL_BLOCK / 64u;
+    __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
+    __shared__ float red[16];
     const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    if (blockIdx.x < nb_shared) {
-        constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QS>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
-        constexpr u32 rb = 16u * C, G = K / 64u;
+    if (blockIdx.x >= nb_routed) {
+        constexpr u32 C = chunks_per_row<QS>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR, rb = 16u * C;
         const u32 sub = lane % LPR, grp = lane / LPR;
-        const u32 r = (blockIdx.x * NW8 + wave) * R + grp, rr = min(r, 1791u);
-        XStage<UOCR_K_HIDDEN, MR_BLOCK> sx;
+        const u32 r = ((blockIdx.x - nb_routed) * NWV + wave) * R + grp, rr = min(r, SI - 1u);
+        XStage<UOCR_K_HIDDEN, SMALL_BLOCK> sx;
         stage_load(sx, x, nw, UOCR_K_HIDDEN);
         RowFrag<J> fg, fu;
         frag_load<QS, LPR, J>(fg, (const uint8_t *)SG.w + (size_t)rr * rb, (const h16 *)SG.s + (size_t)rr * G, C, sub);
@@ -814,51 +863,32 @@ __global__ __launch_bounds__(MR_BLOCK) void k_moe_shared_router(uocr_qmat SG, uo
         stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
         const float dg = group_sum<LPR>(frag_dot<QS, LPR, J>(fg, xs, C, sub));
         const float du = group_sum<LPR>(frag_dot<QS, LPR, J>(fu, xs, C, sub));
-        if (r < 1792u && sub == 0u) smid[r] = (h16)(silu_f(dg) * du);
+        if (r < SI && sub == 0u) smid[r] = (h16)(silu_f(dg) * du);
         return;
     }
-    constexpr u32 C = chunks_per_row<1>(UOCR_K_HIDDEN), LPR = 16u, J = C / LPR, RPW = 64u / LPR;
-    constexpr u32 rb = 16u * C, ROWS_PER_PASS = NW8 * RPW;
-    static_assert(UOCR_K_EXPERTS == 2 * ROWS_PER_PASS, "router block covers 64 rows in two row slots");
+    constexpr u32 C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR, rb = 16u * C;
     const u32 sub = lane % LPR, grp = lane / LPR;
-    const u32 r0 = wave * RPW + grp, r1 = r0 + ROWS_PER_PASS;
-    XStage<UOCR_K_HIDDEN, MR_BLOCK> sx;
-    stage_load(sx, x, nw, UOCR_K_HIDDEN);
-    RowFrag<J> f0, f1;
-    frag_load<1, LPR, J>(f0, (const uint8_t *)Rw + (size_t)r0 * rb, nullptr, C, sub);
-    frag_load<1, LPR, J>(f1, (const uint8_t *)Rw + (size_t)r1 * rb, nullptr, C, sub);
-    stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
-    const float d0 = group_sum<LPR>(frag_dot<1, LPR, J>(f0, xs, C, sub));
-    const float d1 = group_sum<LPR>(frag_dot<1, LPR, J>(f1, xs, C, sub));
-    if (sub == 0u) {
-        lg[r0] = d0;
-        lg[r1] = d1;
-    }
-    __syncthreads();
-    if (threadIdx.x < 64u) {
-        logits[threadIdx.x] = lg[threadIdx.x];
-        topk6_wave(lg[threadIdx.x], norm_topk, ids, weights);
-    }
-}
-
-/* Routed gate/up: mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)),
- * e = ids[r]; one row pair per lane group. */
-template <int QT>
-__global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl, const u32 *__restrict__ ids,
-                                                       const h16 *__restrict__ x, const h16 *__restrict__ nw,
-                                                       h16 *__restrict__ mid) {
-    constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
-    constexpr u32 rb = 16u * C, G = K / 64u, I = 896u, ROWS = UOCR_K_TOPK * I;
-    __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
-    __shared__ float red[16];
-    const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const u32 sub = lane % LPR, grp = lane / LPR;
-    const u32 r = (blockIdx.x * (SMALL_BLOCK / 64) + wave) * R + grp, rr = min(r, ROWS - 1u);
+    const float lg = logits[lane];
     XStage<UOCR_K_HIDDEN, SMALL_BLOCK> sx;
     stage_load(sx, x, nw, UOCR_K_HIDDEN);
+    u32 sid[UOCR_K_TOPK];
+    float sw[UOCR_K_TOPK];
+    topk6(lg, norm_topk, sid, sw);
+    if (blockIdx.x == 0u && wave == 0u && lane < UOCR_K_TOPK) {
+#pragma unroll
+        for (int r = 0; r < UOCR_K_TOPK; ++r) {
+            if (lane == (u32)r) {
+                ids_out[r] = sid[r];
+                w_out[r] = sw[r];
+            }
+        }
+    }
+    const u32 r = (blockIdx.x * NWV + wave) * R + grp, rr = min(r, ROWS - 1u);
     const u32 rank = rr / I, col = rr % I;
-    const u32 e0 = ids[rank];
-    const u32 e = e0 < UOCR_K_EXPERTS ? e0 : 0u;
+    u32 e = sid[0];
+#pragma unroll
+    for (int k = 1; k < UOCR_K_TOPK; ++k) e = rank == (u32)k ? sid[k] : e;
+    e = e < UOCR_K_EXPERTS ? e : 0u;
     RowFrag<J> fg, fu;
     frag_load<QT, LPR, J>(fg, (const uint8_t *)sl.gate.w + e * sl.gu_w_stride + (size_t)col * rb,
                           (const h16 *)sl.gate.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
@@ -1273,53 +1303,57 @@ extern "C" hipError_t uocr_launch_attn_merge(hipStream_t st, const float *partia
     return hipGetLastError();
 }
 
-template <int QS>
-static void launch_shared_router_qs(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R, const uint16_t *x,
-                                    const uint16_t *nw, int norm_topk, uint16_t *smid, float *logits, u32 *ids,
-                                    float *weights, bool with_shared) {
-    constexpr u32 rpb = (MR_BLOCK / 64) * (64u / lpr_for(chunks_per_row<QS>(UOCR_K_HIDDEN)));
-    const u32 nb_s = with_shared ? (1792u + rpb - 1u) / rpb : 0u;
-    hipLaunchKernelGGL((k_moe_shared_router<QS>), dim3(nb_s + 1u), dim3(MR_BLOCK), 0, st, SG, SU, (const h16 *)R,
-                       (const h16 *)x, (const h16 *)nw, norm_topk, (h16 *)smid, logits, ids, weights, nb_s);
-}
-
-extern "C" hipError_t uocr_launch_moe_shared_router(hipStream_t st, uocr_qmat SG, uocr_qmat SU, const uint16_t *R,
-                                                    const uint16_t *x, const uint16_t *nw, int norm_topk,
-                                                    uint16_t *smid, float *logits, uint32_t *ids, float *weights) {
-    if (!mat_ok(SG) || !mat_ok(SU) || SG.qtype != SU.qtype || R == nullptr || x == nullptr || smid == nullptr ||
-        logits == nullptr || ids == nullptr || weights == nullptr) {
-        return hipErrorInvalidValue;
-    }
-    DISPATCH_QT(SG.qtype, launch_shared_router_qs, st, SG, SU, R, x, nw, norm_topk, smid, logits, ids, weights, true);
+extern "C" hipError_t uocr_launch_router_logits(hipStream_t st, const uint16_t *R, const uint16_t *x,
+                                                const uint16_t *nw, float *logits) {
+    if (R == nullptr || x == nullptr || logits == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_router_logits, dim3(UOCR_K_EXPERTS), dim3(64), 0, st, (const h16 *)R, (const h16 *)x,
+                       (const h16 *)nw, logits);
     return hipGetLastError();
 }
 
 extern "C" hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, const uint16_t *x, const uint16_t *nw,
                                          int norm_topk, float *logits, uint32_t *ids, float *weights) {
-    if (R == nullptr || x == nullptr || logits == nullptr || ids == nullptr || weights == nullptr) {
-        return hipErrorInvalidValue;
-    }
-    uocr_qmat none = {R, nullptr, UOCR_QT_F16};
-    launch_shared_router_qs<1>(st, none, none, R, x, nw, norm_topk, nullptr, logits, ids, weights, false);
+    if (ids == nullptr || weights == nullptr) return hipErrorInvalidValue;
+    const hipError_t e = uocr_launch_router_logits(st, R, x, nw, logits);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_router_topk, dim3(1), dim3(64), 0, st, (const float *)logits, norm_topk, ids, weights);
     return hipGetLastError();
 }
 
-template <int QT>
-static void launch_moe_gu_qt(hipStream_t st, const uocr_expert_slab *slab, const u32 *ids, const uint16_t *x,
-                             const uint16_t *nw, uint16_t *mid) {
-    constexpr u32 rpb = (SMALL_BLOCK / 64) * (64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN)));
-    constexpr u32 rows = UOCR_K_TOPK * 896u;
-    hipLaunchKernelGGL((k_moe_gate_up<QT>), dim3((rows + rpb - 1u) / rpb), dim3(SMALL_BLOCK), 0, st, *slab, ids,
-                       (const h16 *)x, (const h16 *)nw, (h16 *)mid);
+template <int QT, int QS>
+static void launch_moe_gu_qs(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG, uocr_qmat SU,
+                             const float *logits, int norm_topk, const uint16_t *x, const uint16_t *nw, uint16_t *mid,
+                             uint16_t *smid, u32 *ids, float *wts) {
+    constexpr u32 NWV = SMALL_BLOCK / 64u;
+    constexpr u32 rpb = NWV * (64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN)));
+    constexpr u32 rpb_s = NWV * (64u / lpr_for(chunks_per_row<QS>(UOCR_K_HIDDEN)));
+    constexpr u32 nbr = (UOCR_K_TOPK * 896u + rpb - 1u) / rpb, nbs = (1792u + rpb_s - 1u) / rpb_s;
+    hipLaunchKernelGGL((k_moe_gate_up<QT, QS>), dim3(nbr + nbs), dim3(SMALL_BLOCK), 0, st, *slab, SG, SU, logits,
+                       norm_topk, (const h16 *)x, (const h16 *)nw, (h16 *)mid, (h16 *)smid, ids, wts, nbr);
 }
 
-extern "C" hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
-                                              const uint16_t *x, const uint16_t *nw, uint16_t *mid) {
+template <int QT>
+static void launch_moe_gu_qt(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG, uocr_qmat SU,
+                             const float *logits, int norm_topk, const uint16_t *x, const uint16_t *nw, uint16_t *mid,
+                             uint16_t *smid, u32 *ids, float *wts) {
+    switch (SG.qtype) {
+        case UOCR_QT_F16: launch_moe_gu_qs<QT, 1>(st, slab, SG, SU, logits, norm_topk, x, nw, mid, smid, ids, wts); break;
+        case UOCR_QT_Q8: launch_moe_gu_qs<QT, 3>(st, slab, SG, SU, logits, norm_topk, x, nw, mid, smid, ids, wts); break;
+        default: launch_moe_gu_qs<QT, 4>(st, slab, SG, SU, logits, norm_topk, x, nw, mid, smid, ids, wts); break;
+    }
+}
+
+extern "C" hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG,
+                                              uocr_qmat SU, const float *logits, int norm_topk, const uint16_t *x,
+                                              const uint16_t *nw, uint16_t *mid, uint16_t *smid, uint32_t *ids,
+                                              float *weights) {
     if (slab == nullptr || !mat_ok(slab->gate) || !mat_ok(slab->up) || slab->gate.qtype != slab->up.qtype ||
-        ids == nullptr || x == nullptr || mid == nullptr) {
+        !mat_ok(SG) || !mat_ok(SU) || SG.qtype != SU.qtype || logits == nullptr || x == nullptr || mid == nullptr ||
+        smid == nullptr || ids == nullptr || weights == nullptr) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(slab->gate.qtype, launch_moe_gu_qt, st, slab, ids, x, nw, mid);
+    DISPATCH_QT(slab->gate.qtype, launch_moe_gu_qt, st, slab, SG, SU, logits, norm_topk, x, nw, mid, smid, ids,
+                weights);
     return hipGetLastError();
 }
 

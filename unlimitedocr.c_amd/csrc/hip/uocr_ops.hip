@@ -160,13 +160,12 @@ extern "C" int uocr_op_moe_ffn(const uocr_op_moe_weights *m, const void *x, cons
     float *logits = ws<float>(workspace, WS_LOGITS);
     uint16_t *mid = ws<uint16_t>(workspace, WS_MID), *smid = ws<uint16_t>(workspace, WS_SMID);
     const uint16_t *xx = (const uint16_t *)x, *nw = (const uint16_t *)norm_w;
-    int r = hip_status(uocr_launch_moe_shared_router(st, qm(m->shared_qtype, m->sgate_w, m->sgate_s),
-                                                     qm(m->shared_qtype, m->sup_w, m->sup_s),
-                                                     (const uint16_t *)m->router, xx, nw, norm_topk, smid, logits,
-                                                     wids, wwts),
-                       "moe shared gate/up + router");
+    int r = hip_status(uocr_launch_router_logits(st, (const uint16_t *)m->router, xx, nw, logits), "moe router");
     if (r == UOCR_OK) {
-        r = hip_status(uocr_launch_moe_gate_up(st, &sl, wids, xx, nw, mid), "moe routed gate/up");
+        r = hip_status(uocr_launch_moe_gate_up(st, &sl, qm(m->shared_qtype, m->sgate_w, m->sgate_s),
+                                               qm(m->shared_qtype, m->sup_w, m->sup_s), logits, norm_topk, xx, nw, mid,
+                                               smid, wids, wwts),
+                       "moe gate/up");
     }
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_moe_down(st, &sl, wids, wwts, mid, qm(m->shared_qtype, m->sdown_w, m->sdown_s),
