@@ -45,6 +45,7 @@ UOCR_API uocr_engine *uocr_engine_open_memory(const uocr_engine_opts *opts, cons
 
 #define UOCR_GEN_FLAG_IGNORE_EOS 1u  /* decode past EOS (benchmarks) */
 #define UOCR_GEN_FLAG_NO_GRAPH 2u    /* enqueue kernels directly, no hipGraph replay */
+#define UOCR_GEN_FLAG_TOKEN_PREFILL 4u /* prefill through the decode kernels, one prompt position at a time */
 
 /* Greedy generation from a prompt whose image positions (image_mask[i] == 1)
  * take the next row of image_rows_f16 ([n_image_rows][1280] fp16) instead of
@@ -150,6 +151,32 @@ UOCR_API int uocr_op_attention_block(uint32_t qtype, const void *wq, const void 
  * (kernels/embedding_q4.metal:21-56) and its Q8/f16 twins. */
 UOCR_API int uocr_op_embed(uint32_t qtype, const void *w, const void *s, uint32_t vocab, const int32_t *token,
                            void *out);
+
+/* ---- prefill operators (MFMA) ------------------------------------------- */
+
+/* y = f16(x . W^T (+ residual)) for m rows: x fp16 [m][k], W [n][k] in the
+ * .uocr layout (k % 64 == 0), residual/y fp16 [m][n].  The tiled MFMA GEMM of
+ * the prompt prefill.  Replaces uocr_decoder_gemm_residual_q4_0_to_f16
+ * (kernels/gemm_q4.metal:135-195) and its Q8 twin (kernels/gemm_q8.metal). */
+UOCR_API int uocr_op_gemm(uint32_t qtype, const void *w, const void *s, uint32_t m, uint32_t n, uint32_t k,
+                          const void *x, const void *residual, void *y);
+
+/* Causal attention of P prompt queries (fp16 [P][1280], RoPE applied) over
+ * cache slots 0..P-1 of caches laid out [10][cache_capacity][128]; ctx fp16
+ * [P][1280].  Replaces uocr_prefill_attention_flash_staged_f16_to_f16
+ * (kernels/attention_prefill.metal:105). */
+UOCR_API int uocr_op_prefill_attention(const void *q, const void *k_cache, const void *v_cache,
+                                       uint32_t cache_capacity, uint32_t prompt_length, void *ctx);
+
+/* Bytes of the workspace uocr_op_moe_ffn_rows needs for P rows. */
+UOCR_API size_t uocr_op_moe_rows_workspace_bytes(uint32_t rows);
+
+/* The MoE FFN of uocr_op_moe_ffn for P rows at once (x, residual, out fp16
+ * [P][1280]): router GEMM, per-row top-6, expert buckets, shared and
+ * expert-grouped SwiGLU GEMMs, combine.  Replaces the bucketed prefill MoE
+ * (kernels/gemm_q8.metal:462-919, gemm_q4.metal:260-339). */
+UOCR_API int uocr_op_moe_ffn_rows(const uocr_op_moe_weights *m, const void *x, const void *norm_w,
+                                  const void *residual, uint32_t rows, int norm_topk, void *workspace, void *out);
 
 /* ---- 3. device plumbing ---------------------------------------------------- */
 UOCR_API int uocr_hip_device_count(void);

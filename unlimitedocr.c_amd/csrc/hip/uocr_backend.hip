@@ -12,8 +12,13 @@
  * chunk of 8 steps, one chunk behind the GPU, and stops on EOS
  * (uocr_metal.m:15248-15358 semantics, without stalling the device).
  *
- * Prompt processing runs each prompt row through the same decoder-layer
- * kernels with a causal-prefix attention plan (a replayable prefill graph).
+ * Prompt processing (prefill) runs all P prompt rows through each layer at
+ * once on MFMA GEMMs (uocr_prefill.hip): QKV GEMM -> RoPE + KV scatter ->
+ * causal flash attention -> O GEMM + residual -> dense SwiGLU GEMMs (layer 0)
+ * or router GEMM -> per-token top-6 -> expert buckets -> shared and
+ * expert-grouped SwiGLU GEMMs -> combine.  The last row's hidden state seeds
+ * the decode loop.  UOCR_GEN_TOKEN_PREFILL instead replays the decode layer
+ * kernels once per prompt position (a replayable prefill graph).
  */
 #include "uocr_backend.h"
 
@@ -70,10 +75,16 @@ struct uocr_hip_ctx {
     uint32_t prompt_cap, cache_cap, max_gen;
     uint8_t *rarena;
     uint64_t rarena_bytes;
-    uint64_t kv_bytes, scratch_bytes, moe_bytes, logits_bytes, prompt_bytes;
+    uint64_t kv_bytes, scratch_bytes, moe_bytes, logits_bytes, prompt_bytes, prefill_bytes;
     uint16_t *kc, *vc, *h, *a, *q, *ctxv, *mid, *smid, *prompt;
     float *attn_part, *logits, *route_w;
     uint32_t *route_ids;
+    /* MFMA prefill scratch, sized for prompt_cap rows */
+    uint16_t *p_xn, *p_qkv, *p_q, *p_ctx, *p_a, *p_mid, *p_smid, *p_sout, *p_rmid;
+    float *p_logits, *p_wts, *p_y;
+    int32_t *p_ids, *p_counts, *p_offsets, *p_cursors, *p_tile_e, *p_tile_s0, *p_tile_s1, *p_ntiles, *p_list_tok,
+        *p_list_pair;
+    uint32_t p_max_tiles;
     uint32_t *lm_part;
     uocr_step_state *state;
     int32_t *tokens;
@@ -328,6 +339,19 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t logits_end = p.off;
     const uint64_t o_prompt = p.take((uint64_t)prompt_capacity * H_SIZE * 2u);
     const uint64_t o_dids = p.take((uint64_t)prompt_capacity * 4u), o_dmask = p.take(prompt_capacity);
+    const uint64_t prompt_end = p.off;
+    const uint64_t Pc = prompt_capacity, PK = Pc * UOCR_MOE_TOP_K;
+    const uint32_t max_tiles = (uint32_t)((PK + 63u) / 64u + UOCR_ROUTED_EXPERTS);
+    const uint64_t o_pxn = p.take(Pc * H_SIZE * 2u), o_pqkv = p.take(Pc * 3u * H_SIZE * 2u);
+    const uint64_t o_pq = p.take(Pc * H_SIZE * 2u), o_pctx = p.take(Pc * H_SIZE * 2u), o_pa = p.take(Pc * H_SIZE * 2u);
+    const uint64_t o_pmid = p.take(Pc * UOCR_DENSE_LAYER0_INTERMEDIATE * 2u);
+    const uint64_t o_psmid = p.take(Pc * UOCR_MOE_SHARED_INTERMEDIATE * 2u), o_psout = p.take(Pc * H_SIZE * 2u);
+    const uint64_t o_prmid = p.take(PK * UOCR_MOE_EXPERT_INTERMEDIATE * 2u);
+    const uint64_t o_plog = p.take(Pc * UOCR_ROUTED_EXPERTS * 4u), o_pwts = p.take(PK * 4u);
+    const uint64_t o_py = p.take(PK * H_SIZE * 4u), o_pids = p.take(PK * 4u);
+    const uint64_t o_pcnt = p.take(64u * 4u), o_poff = p.take(64u * 4u), o_pcur = p.take(64u * 4u);
+    const uint64_t o_pte = p.take(max_tiles * 4u), o_pts0 = p.take(max_tiles * 4u), o_pts1 = p.take(max_tiles * 4u);
+    const uint64_t o_pnt = p.take(4u), o_plt = p.take(PK * 4u), o_plp = p.take(PK * 4u);
     const uint64_t total = p.off;
     HIPCHK(hipMalloc((void **)&ctx->rarena, total), "runtime arena allocation");
     HIPCHK(hipMemset(ctx->rarena, 0, total), "runtime arena clear");
@@ -351,19 +375,43 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->prompt = (uint16_t *)(b + o_prompt);
     ctx->d_ids = (int32_t *)(b + o_dids);
     ctx->d_mask = (uint8_t *)(b + o_dmask);
+    ctx->p_xn = (uint16_t *)(b + o_pxn);
+    ctx->p_qkv = (uint16_t *)(b + o_pqkv);
+    ctx->p_q = (uint16_t *)(b + o_pq);
+    ctx->p_ctx = (uint16_t *)(b + o_pctx);
+    ctx->p_a = (uint16_t *)(b + o_pa);
+    ctx->p_mid = (uint16_t *)(b + o_pmid);
+    ctx->p_smid = (uint16_t *)(b + o_psmid);
+    ctx->p_sout = (uint16_t *)(b + o_psout);
+    ctx->p_rmid = (uint16_t *)(b + o_prmid);
+    ctx->p_logits = (float *)(b + o_plog);
+    ctx->p_wts = (float *)(b + o_pwts);
+    ctx->p_y = (float *)(b + o_py);
+    ctx->p_ids = (int32_t *)(b + o_pids);
+    ctx->p_counts = (int32_t *)(b + o_pcnt);
+    ctx->p_offsets = (int32_t *)(b + o_poff);
+    ctx->p_cursors = (int32_t *)(b + o_pcur);
+    ctx->p_tile_e = (int32_t *)(b + o_pte);
+    ctx->p_tile_s0 = (int32_t *)(b + o_pts0);
+    ctx->p_tile_s1 = (int32_t *)(b + o_pts1);
+    ctx->p_ntiles = (int32_t *)(b + o_pnt);
+    ctx->p_list_tok = (int32_t *)(b + o_plt);
+    ctx->p_list_pair = (int32_t *)(b + o_plp);
+    ctx->p_max_tiles = max_tiles;
     ctx->rarena_bytes = total;
     ctx->kv_bytes = 2u * kv_one;
     ctx->scratch_bytes = scratch_end - o_h;
     ctx->moe_bytes = moe_end - scratch_end;
     ctx->logits_bytes = logits_end - moe_end;
-    ctx->prompt_bytes = total - logits_end;
+    ctx->prompt_bytes = prompt_end - logits_end;
+    ctx->prefill_bytes = total - prompt_end;
     HIPCHK(hipHostMalloc((void **)&ctx->h_tokens, (size_t)max_gen * 4u, hipHostMallocDefault), "pinned token buffer");
     HIPCHK(hipHostMalloc((void **)&ctx->h_scores, (size_t)max_gen * 4u, hipHostMallocDefault), "pinned score buffer");
     HIPCHK(hipHostMalloc((void **)&ctx->h_prompt, (size_t)prompt_capacity * H_SIZE * 2u, hipHostMallocDefault),
            "pinned prompt staging");
     if (ctx->mem != nullptr) {
         uocr_memory_reserve(ctx->mem, UOCR_MEMORY_KV_CACHE, ctx->kv_bytes);
-        uocr_memory_reserve(ctx->mem, UOCR_MEMORY_DECODER_SCRATCH, ctx->scratch_bytes);
+        uocr_memory_reserve(ctx->mem, UOCR_MEMORY_DECODER_SCRATCH, ctx->scratch_bytes + ctx->prefill_bytes);
         uocr_memory_reserve(ctx->mem, UOCR_MEMORY_MOE_SCRATCH, ctx->moe_bytes);
         uocr_memory_reserve(ctx->mem, UOCR_MEMORY_LOGITS_READBACK, ctx->logits_bytes);
         uocr_memory_reserve(ctx->mem, UOCR_MEMORY_PROMPT_EMBEDDINGS, ctx->prompt_bytes);
@@ -424,6 +472,112 @@ static hipError_t enqueue_prefill_step(uocr_hip_ctx *c) {
     hipError_t e = uocr_launch_prefill_next(c->stream, c->state, c->prompt, c->h);
     if (e == hipSuccess) e = enqueue_layers(c);
     return e;
+}
+
+static uocr_gemm_desc gdesc(const uint16_t *A, uint32_t lda, uint32_t M, uint32_t N, uint32_t K, void *out,
+                           uint32_t ldo) {
+    uocr_gemm_desc d;
+    memset(&d, 0, sizeof(d));
+    d.A = A;
+    d.lda = lda;
+    d.M = M;
+    d.N = N;
+    d.K = K;
+    d.out = out;
+    d.ldo = ldo;
+    return d;
+}
+
+/* All P prompt rows (c->prompt, updated in place as the residual stream)
+ * through the 12 layers on MFMA GEMMs; K/V of positions 0..P-1 land in the
+ * cache slots 0..P-1 and the last row's hidden state in c->h. */
+static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
+    hipStream_t s = c->stream;
+    const uint64_t kv_layer = (uint64_t)UOCR_ATTENTION_HEADS * c->cache_cap * UOCR_HEAD_DIM;
+    uint16_t *H = c->prompt;
+    hipError_t e = hipSuccess;
+#define ENQ(x)                        \
+    do {                              \
+        e = (x);                      \
+        if (e != hipSuccess) return e; \
+    } while (0)
+    for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
+        const dev_layer &L = c->L[l];
+        uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
+        ENQ(uocr_launch_rows_rmsnorm(s, H, L.in_norm, P, c->p_xn));
+        uocr_gemm_desc d = gdesc(c->p_xn, H_SIZE, P, 3u * H_SIZE, H_SIZE, c->p_qkv, 3u * H_SIZE);
+        d.W[0] = L.q;
+        d.W[1] = L.k;
+        d.W[2] = L.v;
+        d.nseg = H_SIZE;
+        ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
+        ENQ(uocr_launch_rope_scatter(s, c->p_qkv, c->invf, P, c->p_q, kc, vc, c->cache_cap));
+        ENQ(uocr_launch_flash_attn(s, c->p_q, kc, vc, c->cache_cap, P, c->p_ctx));
+        d = gdesc(c->p_ctx, H_SIZE, P, H_SIZE, H_SIZE, c->p_a, H_SIZE);
+        d.W[0] = L.o;
+        d.res = H;
+        d.ldr = H_SIZE;
+        ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
+        ENQ(uocr_launch_rows_rmsnorm(s, c->p_a, L.post_norm, P, c->p_xn));
+        if (l == 0u) {
+            const uint32_t I0 = UOCR_DENSE_LAYER0_INTERMEDIATE;
+            d = gdesc(c->p_xn, H_SIZE, P, I0, H_SIZE, c->p_mid, I0);
+            d.W[0] = L.gate;
+            d.W[1] = L.up;
+            ENQ(uocr_launch_gemm(s, UOCR_GEMM_SWIGLU, &d));
+            d = gdesc(c->p_mid, I0, P, H_SIZE, I0, H, H_SIZE);
+            d.W[0] = L.down;
+            d.res = c->p_a;
+            d.ldr = H_SIZE;
+            ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
+            continue;
+        }
+        const uint32_t SI = UOCR_MOE_SHARED_INTERMEDIATE, EI = UOCR_MOE_EXPERT_INTERMEDIATE;
+        d = gdesc(c->p_xn, H_SIZE, P, UOCR_ROUTED_EXPERTS, H_SIZE, c->p_logits, UOCR_ROUTED_EXPERTS);
+        d.W[0].w = L.router;
+        d.W[0].s = nullptr;
+        d.W[0].qtype = UOCR_QT_F16;
+        ENQ(uocr_launch_gemm(s, UOCR_GEMM_F32, &d));
+        ENQ(uocr_launch_route_rows(s, c->p_logits, P, 0, c->p_ids, c->p_wts, c->p_counts, c->p_offsets, c->p_cursors,
+                                   c->p_tile_e, c->p_tile_s0, c->p_tile_s1, c->p_ntiles, c->p_list_tok,
+                                   c->p_list_pair));
+        d = gdesc(c->p_xn, H_SIZE, P, SI, H_SIZE, c->p_smid, SI);
+        d.W[0] = L.sgate;
+        d.W[1] = L.sup;
+        ENQ(uocr_launch_gemm(s, UOCR_GEMM_SWIGLU, &d));
+        d = gdesc(c->p_smid, SI, P, H_SIZE, SI, c->p_sout, H_SIZE);
+        d.W[0] = L.sdown;
+        ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
+        d = gdesc(c->p_xn, H_SIZE, 0, EI, H_SIZE, c->p_rmid, EI);
+        d.W[0] = L.slab.gate;
+        d.W[1] = L.slab.up;
+        d.w_stride = L.slab.gu_w_stride;
+        d.s_stride = L.slab.gu_s_stride;
+        d.a_idx = c->p_list_tok;
+        d.o_idx = c->p_list_pair;
+        d.tile_e = c->p_tile_e;
+        d.tile_s0 = c->p_tile_s0;
+        d.tile_s1 = c->p_tile_s1;
+        d.ntiles = c->p_ntiles;
+        d.max_tiles = c->p_max_tiles;
+        ENQ(uocr_launch_gemm(s, UOCR_GEMM_SWIGLU, &d));
+        uocr_gemm_desc dd = d;
+        dd.A = c->p_rmid;
+        dd.lda = EI;
+        dd.N = H_SIZE;
+        dd.K = EI;
+        dd.W[0] = L.slab.down;
+        dd.W[1] = uocr_qmat{nullptr, nullptr, 0};
+        dd.w_stride = L.slab.dn_w_stride;
+        dd.s_stride = L.slab.dn_s_stride;
+        dd.a_idx = c->p_list_pair;
+        dd.out = c->p_y;
+        dd.ldo = H_SIZE;
+        ENQ(uocr_launch_gemm(s, UOCR_GEMM_F32, &dd));
+        ENQ(uocr_launch_moe_combine(s, c->p_y, c->p_wts, c->p_sout, c->p_a, P, H));
+    }
+    return hipMemcpyAsync(c->h, H + (size_t)(P - 1u) * H_SIZE, H_SIZE * 2u, hipMemcpyDeviceToDevice, s);
+#undef ENQ
 }
 
 static int capture(uocr_hip_ctx *c, hipError_t (*fn)(uocr_hip_ctx *), hipGraphExec_t *out, char *err, size_t err_size) {
@@ -506,11 +660,15 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
 
     /* prefill */
     HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0), "state init");
-    for (uint32_t i = 0; i < P; ++i) {
-        if (use_graph) {
-            HIPCHK(hipGraphLaunch(c->g_prefill, s), "prefill graph launch");
-        } else {
-            HIPCHK(enqueue_prefill_step(c), "prefill step");
+    if ((req->flags & UOCR_GEN_TOKEN_PREFILL) == 0u) {
+        HIPCHK(enqueue_prefill_mfma(c, P), "MFMA prefill");
+    } else {
+        for (uint32_t i = 0; i < P; ++i) {
+            if (use_graph) {
+                HIPCHK(hipGraphLaunch(c->g_prefill, s), "prefill graph launch");
+            } else {
+                HIPCHK(enqueue_prefill_step(c), "prefill step");
+            }
         }
     }
     HIPCHK(hipStreamSynchronize(s), "prefill sync");

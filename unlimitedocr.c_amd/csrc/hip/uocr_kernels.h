@@ -135,6 +135,56 @@ hipError_t uocr_launch_prefill_state(hipStream_t st, uocr_step_state *state, int
 /* Sets *state for decode with explicit (prompt_len, gen_after_write). */
 hipError_t uocr_launch_decode_state(hipStream_t st, uocr_step_state *state, int32_t prompt_len, int32_t t);
 
+/* ---- prefill (MFMA) ------------------------------------------------------ */
+
+#define UOCR_GEMM_F16 0    /* out = f16(acc (+ res)) */
+#define UOCR_GEMM_F32 1    /* out = acc (fp32) */
+#define UOCR_GEMM_SWIGLU 2 /* out = f16(silu(acc(W[0])) * acc(W[1])) */
+
+/* C[m][n] = sum_k A[m][k] W[n][k]: fp16 activations A (row stride lda,
+ * multiple of 8), weights in the .uocr layout ([N][K], K % 64 == 0).
+ * Dense: rows 0..M-1 of A to rows 0..M-1 of out.  Grouped (tile_e set): a
+ * device tile table (tile_e, tile_s0, tile_s1, *ntiles <= max_tiles) maps
+ * launch tile i to expert tile_e[i] and slots [tile_s0[i], tile_s1[i]); slot
+ * s reads A row a_idx[s] and writes out row o_idx[s]; expert e's weights are
+ * at W.w + e * w_stride bytes and W.s + e * s_stride halves.  nseg != 0:
+ * columns [s*nseg, (s+1)*nseg) use W[s] (nseg a multiple of 128). */
+typedef struct uocr_gemm_desc {
+    const uint16_t *A;
+    uint32_t lda;
+    const int32_t *a_idx, *o_idx;
+    uint32_t M, N, K;
+    uocr_qmat W[3];
+    uint32_t nseg;
+    uint64_t w_stride, s_stride;
+    const int32_t *tile_e, *tile_s0, *tile_s1, *ntiles;
+    uint32_t max_tiles;
+    void *out;
+    uint32_t ldo;
+    const uint16_t *res;
+    uint32_t ldr;
+} uocr_gemm_desc;
+
+hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d);
+/* y[t] = rmsnorm(x[t], w) for P rows of 1280. */
+hipError_t uocr_launch_rows_rmsnorm(hipStream_t st, const uint16_t *x, const uint16_t *w, uint32_t P, uint16_t *y);
+/* qkv [P][3840] -> RoPE'd q [P][1280]; RoPE'd k and v into cache slots 0..P-1. */
+hipError_t uocr_launch_rope_scatter(hipStream_t st, const uint16_t *qkv, const float *inv_freq, uint32_t P,
+                                    uint16_t *qout, uint16_t *kcache, uint16_t *vcache, uint32_t cap);
+/* Causal attention of P prompt queries over cache slots 0..P-1 -> ctx [P][1280]. */
+hipError_t uocr_launch_flash_attn(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
+                                  uint32_t cap, uint32_t P, uint16_t *ctx);
+/* Per-token top-6 over logits [P][64] -> ids/wts [P][6]; expert buckets:
+ * counts, offsets, cursors (64 each), grouped-GEMM tile table (up to
+ * P*6/64 + 64 entries) and the (token, pair) slot lists [P*6]. */
+hipError_t uocr_launch_route_rows(hipStream_t st, const float *logits, uint32_t P, int norm_topk, int32_t *ids,
+                                  float *wts, int32_t *counts, int32_t *offsets, int32_t *cursors, int32_t *tile_e,
+                                  int32_t *tile_s0, int32_t *tile_s1, int32_t *ntiles, int32_t *list_tok,
+                                  int32_t *list_pair);
+/* out[t] = f16(sum_r wts[t][r] * Y[t*6+r] + shared[t] + res[t]). */
+hipError_t uocr_launch_moe_combine(hipStream_t st, const float *Y, const float *wts, const uint16_t *shared,
+                                   const uint16_t *res, uint32_t P, uint16_t *out);
+
 #ifdef __cplusplus
 }
 #endif

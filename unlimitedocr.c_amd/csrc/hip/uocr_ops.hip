@@ -244,6 +244,178 @@ extern "C" int uocr_op_embed(uint32_t qtype, const void *w, const void *s, uint3
     return hip_status(uocr_launch_embed(st, qm(qtype, w, s), vocab, token, nullptr, (uint16_t *)out), "embed");
 }
 
+/* ---- prefill operators ------------------------------------------------------ */
+
+extern "C" int uocr_op_gemm(uint32_t qtype, const void *w, const void *s, uint32_t m, uint32_t n, uint32_t k,
+                            const void *x, const void *residual, void *y) {
+    if (!qt_ok(qtype) || w == nullptr || x == nullptr || y == nullptr || m == 0u || n == 0u || k == 0u ||
+        k % 64u != 0u || (qtype != UOCR_QT_F16 && s == nullptr)) {
+        return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid gemm arguments (k must be a multiple of 64)");
+    }
+    STREAM_OR_RETURN(st);
+    uocr_gemm_desc d;
+    memset(&d, 0, sizeof(d));
+    d.A = (const uint16_t *)x;
+    d.lda = k;
+    d.M = m;
+    d.N = n;
+    d.K = k;
+    d.W[0] = qm(qtype, w, s);
+    d.out = y;
+    d.ldo = n;
+    d.res = (const uint16_t *)residual;
+    d.ldr = n;
+    return hip_status(uocr_launch_gemm(st, UOCR_GEMM_F16, &d), "gemm");
+}
+
+extern "C" int uocr_op_prefill_attention(const void *q, const void *k_cache, const void *v_cache,
+                                         uint32_t cache_capacity, uint32_t prompt_length, void *ctx) {
+    if (q == nullptr || k_cache == nullptr || v_cache == nullptr || ctx == nullptr || prompt_length == 0u ||
+        prompt_length > cache_capacity) {
+        return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid prefill_attention arguments");
+    }
+    STREAM_OR_RETURN(st);
+    return hip_status(uocr_launch_flash_attn(st, (const uint16_t *)q, (const uint16_t *)k_cache,
+                                             (const uint16_t *)v_cache, cache_capacity, prompt_length, (uint16_t *)ctx),
+                      "prefill_attention");
+}
+
+namespace {
+/* workspace layout of uocr_op_moe_ffn_rows for P rows */
+struct MoeRowsWs {
+    size_t xn, logits, ids, wts, counts, offsets, cursors, te, ts0, ts1, nt, ltok, lpair, smid, sout, rmid, y, total;
+    uint32_t max_tiles;
+    explicit MoeRowsWs(size_t P) {
+        const size_t PK = P * 6u;
+        max_tiles = (uint32_t)((PK + 63u) / 64u + 64u);
+        size_t o = 0;
+        auto take = [&](size_t bytes) {
+            const size_t r = o;
+            o += A256(bytes);
+            return r;
+        };
+        xn = take(P * 1280u * 2u);
+        logits = take(P * 64u * 4u);
+        ids = take(PK * 4u);
+        wts = take(PK * 4u);
+        counts = take(256u);
+        offsets = take(256u);
+        cursors = take(256u);
+        te = take(max_tiles * 4u);
+        ts0 = take(max_tiles * 4u);
+        ts1 = take(max_tiles * 4u);
+        nt = take(4u);
+        ltok = take(PK * 4u);
+        lpair = take(PK * 4u);
+        smid = take(P * 1792u * 2u);
+        sout = take(P * 1280u * 2u);
+        rmid = take(PK * 896u * 2u);
+        y = take(PK * 1280u * 4u);
+        total = o;
+    }
+};
+}  // namespace
+
+extern "C" size_t uocr_op_moe_rows_workspace_bytes(uint32_t rows) {
+    return MoeRowsWs(rows).total;
+}
+
+extern "C" int uocr_op_moe_ffn_rows(const uocr_op_moe_weights *m, const void *x, const void *norm_w,
+                                    const void *residual, uint32_t rows, int norm_topk, void *workspace, void *out) {
+    if (m == nullptr || x == nullptr || residual == nullptr || workspace == nullptr || out == nullptr || rows == 0u ||
+        !qt_ok(m->expert_qtype) || !qt_ok(m->shared_qtype) || m->router == nullptr) {
+        return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid moe_ffn_rows arguments");
+    }
+    STREAM_OR_RETURN(st);
+    const MoeRowsWs L(rows);
+    uint8_t *b = (uint8_t *)workspace;
+    const uint32_t P = rows;
+    uint16_t *xn = (uint16_t *)(b + L.xn);
+    int r = UOCR_OK;
+    if (norm_w != nullptr) {
+        r = hip_status(uocr_launch_rows_rmsnorm(st, (const uint16_t *)x, (const uint16_t *)norm_w, P, xn), "rmsnorm");
+    } else {
+        r = hip_status(hipMemcpyAsync(xn, x, (size_t)P * 1280u * 2u, hipMemcpyDeviceToDevice, st), "copy");
+    }
+    uocr_gemm_desc d;
+    memset(&d, 0, sizeof(d));
+    d.A = xn;
+    d.lda = 1280u;
+    d.M = P;
+    d.N = 64u;
+    d.K = 1280u;
+    d.W[0] = qm(UOCR_QT_F16, m->router, nullptr);
+    d.out = b + L.logits;
+    d.ldo = 64u;
+    if (r == UOCR_OK) r = hip_status(uocr_launch_gemm(st, UOCR_GEMM_F32, &d), "router gemm");
+    int32_t *ids = (int32_t *)(b + L.ids);
+    float *wts = (float *)(b + L.wts);
+    if (r == UOCR_OK) {
+        r = hip_status(uocr_launch_route_rows(st, (const float *)(b + L.logits), P, norm_topk, ids, wts,
+                                              (int32_t *)(b + L.counts), (int32_t *)(b + L.offsets),
+                                              (int32_t *)(b + L.cursors), (int32_t *)(b + L.te), (int32_t *)(b + L.ts0),
+                                              (int32_t *)(b + L.ts1), (int32_t *)(b + L.nt), (int32_t *)(b + L.ltok),
+                                              (int32_t *)(b + L.lpair)),
+                       "routing");
+    }
+    d.N = 1792u;
+    d.W[0] = qm(m->shared_qtype, m->sgate_w, m->sgate_s);
+    d.W[1] = qm(m->shared_qtype, m->sup_w, m->sup_s);
+    d.out = b + L.smid;
+    d.ldo = 1792u;
+    if (r == UOCR_OK) r = hip_status(uocr_launch_gemm(st, UOCR_GEMM_SWIGLU, &d), "shared gate/up gemm");
+    uocr_gemm_desc sd;
+    memset(&sd, 0, sizeof(sd));
+    sd.A = (const uint16_t *)(b + L.smid);
+    sd.lda = 1792u;
+    sd.M = P;
+    sd.N = 1280u;
+    sd.K = 1792u;
+    sd.W[0] = qm(m->shared_qtype, m->sdown_w, m->sdown_s);
+    sd.out = b + L.sout;
+    sd.ldo = 1280u;
+    if (r == UOCR_OK) r = hip_status(uocr_launch_gemm(st, UOCR_GEMM_F16, &sd), "shared down gemm");
+    uocr_gemm_desc gd;
+    memset(&gd, 0, sizeof(gd));
+    gd.A = xn;
+    gd.lda = 1280u;
+    gd.N = 896u;
+    gd.K = 1280u;
+    gd.W[0] = qm(m->expert_qtype, m->gate_w, m->gate_s);
+    gd.W[1] = qm(m->expert_qtype, m->up_w, m->up_s);
+    gd.w_stride = m->gu_w_stride;
+    gd.s_stride = m->gu_s_stride;
+    gd.a_idx = (const int32_t *)(b + L.ltok);
+    gd.o_idx = (const int32_t *)(b + L.lpair);
+    gd.tile_e = (const int32_t *)(b + L.te);
+    gd.tile_s0 = (const int32_t *)(b + L.ts0);
+    gd.tile_s1 = (const int32_t *)(b + L.ts1);
+    gd.ntiles = (const int32_t *)(b + L.nt);
+    gd.max_tiles = L.max_tiles;
+    gd.out = b + L.rmid;
+    gd.ldo = 896u;
+    if (r == UOCR_OK) r = hip_status(uocr_launch_gemm(st, UOCR_GEMM_SWIGLU, &gd), "routed gate/up gemm");
+    uocr_gemm_desc dd = gd;
+    dd.A = (const uint16_t *)(b + L.rmid);
+    dd.lda = 896u;
+    dd.N = 1280u;
+    dd.K = 896u;
+    dd.W[0] = qm(m->expert_qtype, m->down_w, m->down_s);
+    dd.W[1] = qm(0u, nullptr, nullptr);
+    dd.w_stride = m->dn_w_stride;
+    dd.s_stride = m->dn_s_stride;
+    dd.a_idx = (const int32_t *)(b + L.lpair);
+    dd.out = b + L.y;
+    dd.ldo = 1280u;
+    if (r == UOCR_OK) r = hip_status(uocr_launch_gemm(st, UOCR_GEMM_F32, &dd), "routed down gemm");
+    if (r == UOCR_OK) {
+        r = hip_status(uocr_launch_moe_combine(st, (const float *)(b + L.y), wts, (const uint16_t *)(b + L.sout),
+                                               (const uint16_t *)residual, P, (uint16_t *)out),
+                       "combine");
+    }
+    return r;
+}
+
 /* ---- plumbing -------------------------------------------------------------- */
 
 extern "C" int uocr_hip_device_count(void) {

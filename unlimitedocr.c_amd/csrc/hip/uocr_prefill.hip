@@ -1,0 +1,703 @@
+/*
+ * uocr_prefill.hip - MFMA prompt prefill for the UnlimitedOCR decoder on
+ * gfx950 (replaces the reference's prefill path, uocr_metal.m:14550-14908,
+ * with its tiled GEMMs gemm_q4.metal / gemm_q8.metal).
+ *
+ * All P prompt rows go through each layer together, so the projections are
+ * real GEMMs [P x K] x [K x N]:
+ *  - k_gemm: 64 x 128 output tiles, K in 64-column steps (one quantisation
+ *    group).  Activation tiles are staged in LDS as fp16; weight tiles are
+ *    dequantised into LDS as exact fp16 integers (Q4 nibble - 8, Q8 int8) so
+ *    v_mfma_f32_32x32x16_f16 forms sum_k x*q in fp32 per group and the group
+ *    scale is applied once per 64-column step, the same "group dot, then
+ *    scale" arithmetic as the decode GEMVs.  Epilogues: fp16 store with
+ *    optional residual, fp32 store, and SwiGLU over two weight matrices.  In
+ *    grouped mode a tile table maps each block to an expert's bucket of
+ *    (token, rank) pairs: rows are gathered through an index list and the
+ *    expert's weights are addressed by slab stride.
+ *  - k_flash_attn: causal attention over the prompt slots, one block per
+ *    (64-query tile, head): S = Q K^T and O += P V on MFMA, fp32 online
+ *    softmax in LDS.
+ *  - routing (top-6 per token, expert buckets), RoPE + KV scatter, MoE
+ *    combine and row RMSNorm kernels.
+ * fp16 rounding happens where the decode path rounds (norm, q/k/v, RoPE,
+ * attention output, O + residual, SwiGLU mids, shared output, layer output).
+ */
+#include "uocr_kernels.h"
+
+#include <math.h>
+
+typedef _Float16 h16;
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32;
+
+#define PB 256 /* threads per prefill block */
+#define TM 64  /* GEMM tile rows */
+#define TN 128 /* GEMM tile columns */
+#define TK 64  /* GEMM K step = one quantisation group */
+#define LDA (TK + 8) /* padded LDS row (halves) */
+
+__device__ __forceinline__ float silu_p(float g) {
+    return g / (1.0f + expf(-g));
+}
+
+union U4H8 {
+    uint4 u;
+    h16x8 v;
+    h16 h[8];
+};
+
+/* exact fp16 of bytes b0,b1 (each < 256) + 1024 */
+__device__ __forceinline__ u32 magic2(u32 v, u32 sel) {
+    return __builtin_amdgcn_perm(0x64646464u, v, sel);
+}
+
+/* ------------------------------------------------------------------------ */
+/* GEMM                                                                      */
+/* ------------------------------------------------------------------------ */
+
+enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2 };
+
+/* Dequantise this thread's share of a TN x TK weight tile (rows n0.., group
+ * g) into LDS as fp16 integers (f16: the values), and its row scales. */
+template <int QT>
+__device__ __forceinline__ void load_w_tile(h16 *ws, float *sc, const uint8_t *W, const h16 *S, u32 K, u32 n0, u32 nmax,
+                                            u32 g) {
+    const u32 t = threadIdx.x;
+    if (QT == 4) {
+        /* thread t: row t/2, bytes 16*(t&1)..+15 of the group: low nibbles
+         * are columns 16*(t&1)+i, high nibbles the same + 32 */
+        const u32 r = t >> 1, half = t & 1u, n = min(n0 + r, nmax - 1u);
+        const uint4 w = *(const uint4 *)(W + (size_t)n * (K / 2u) + g * 32u + 16u * half);
+        const u32 wv[4] = {w.x, w.y, w.z, w.w};
+        const u32 bias = 0x64086408u; /* (1032, 1032) */
+        union {
+            uint4 u[2];
+            u32 d[8];
+        } lo, hi;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const u32 l = wv[b] & 0x0F0F0F0Fu, h = (wv[b] >> 4) & 0x0F0F0F0Fu;
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            const h2 bb = __builtin_bit_cast(h2, bias);
+            lo.d[2 * b] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(l, 0x04010400u)) - bb);
+            lo.d[2 * b + 1] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(l, 0x04030402u)) - bb);
+            hi.d[2 * b] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(h, 0x04010400u)) - bb);
+            hi.d[2 * b + 1] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(h, 0x04030402u)) - bb);
+        }
+        uint4 *dl = (uint4 *)(ws + r * LDA + 16u * half);
+        uint4 *dh = (uint4 *)(ws + r * LDA + 32u + 16u * half);
+        dl[0] = lo.u[0];
+        dl[1] = lo.u[1];
+        dh[0] = hi.u[0];
+        dh[1] = hi.u[1];
+        if (t < TN) sc[t] = (float)S[(size_t)min(n0 + t, nmax - 1u) * (K / 64u) + g];
+    } else if (QT == 3) {
+        /* thread t: row t/2, bytes 32*(t&1)..+31 */
+        const u32 r = t >> 1, half = t & 1u, n = min(n0 + r, nmax - 1u);
+        const uint4 *src = (const uint4 *)(W + (size_t)n * K + g * 64u + 32u * half);
+        const uint4 w0 = src[0], w1 = src[1];
+        const u32 wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 bb = __builtin_bit_cast(h2, 0x64806480u); /* (1152, 1152) */
+        union {
+            uint4 u[4];
+            u32 d[16];
+        } o;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const u32 u = wv[b] ^ 0x80808080u;
+            o.d[2 * b] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(u, 0x04010400u)) - bb);
+            o.d[2 * b + 1] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(u, 0x04030402u)) - bb);
+        }
+        uint4 *d = (uint4 *)(ws + r * LDA + 32u * half);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d[i] = o.u[i];
+        if (t < TN) sc[t] = (float)S[(size_t)min(n0 + t, nmax - 1u) * (K / 64u) + g];
+    } else {
+        /* thread t: row t/2, columns 32*(t&1)..+31 */
+        const u32 r = t >> 1, half = t & 1u, n = min(n0 + r, nmax - 1u);
+        const uint4 *src = (const uint4 *)((const h16 *)W + (size_t)n * K + g * 64u + 32u * half);
+        uint4 *d = (uint4 *)(ws + r * LDA + 32u * half);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d[i] = src[i];
+    }
+}
+
+struct GemmArgs {
+    const h16 *A;        /* activations, row stride lda (halves) */
+    u32 lda;
+    const int32_t *a_idx;  /* grouped: A row of each slot */
+    const int32_t *o_idx;  /* grouped: output row of each slot */
+    u32 M, N, K;
+    uocr_qmat W[3];      /* W[0] (and W[1] for SwiGLU; W[seg] when nseg) */
+    u32 nseg;            /* when nonzero, columns [s*nseg, (s+1)*nseg) use W[s] */
+    uint64_t w_stride, s_stride; /* grouped: per-expert strides (bytes / halves) */
+    const int32_t *tile_e, *tile_s0, *tile_s1, *ntiles; /* grouped tile table */
+    void *out;
+    u32 ldo;
+    const h16 *res;      /* GE_F16: optional residual, row stride ldr */
+    u32 ldr;
+};
+
+/* C[m][n] = sum_k A[m][k] W[n][k] over one 64 x 128 tile per block; 4
+ * wavefronts, each 32 rows x 64 columns (two 32x32 MFMA tiles). */
+template <int QT, int EPI, bool GROUPED>
+__global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
+    constexpr int NMAT = EPI == GE_SWIGLU ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) h16 as[TM * LDA];
+    __shared__ __attribute__((aligned(16))) h16 wsm[NMAT][TN * LDA];
+    __shared__ float scs[NMAT][TN];
+    __shared__ int32_t arow[TM], orow[TM];
+    const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const u32 wm = wave & 1u, wn = wave >> 1;
+    u32 n0 = blockIdx.y * TN, rows = p.M, e = 0, s0 = 0;
+    if (GROUPED) {
+        if ((int)blockIdx.x >= *p.ntiles) return;
+        e = (u32)p.tile_e[blockIdx.x];
+        s0 = (u32)p.tile_s0[blockIdx.x];
+        rows = (u32)p.tile_s1[blockIdx.x] - s0;
+        if (t < TM) {
+            const u32 s = s0 + min(t, rows - 1u);
+            arow[t] = p.a_idx[s];
+            orow[t] = p.o_idx[s];
+        }
+    } else {
+        s0 = blockIdx.x * TM;
+        rows = min((u32)TM, p.M - s0);
+        if (t < TM) {
+            arow[t] = (int32_t)(s0 + min(t, rows - 1u));
+            orow[t] = arow[t];
+        }
+    }
+    uocr_qmat W0 = p.W[0], W1 = p.W[1];
+    u32 nbase = 0;
+    if (p.nseg != 0u) {
+        const u32 sgi = n0 / p.nseg;
+        W0 = p.W[sgi];
+        nbase = sgi * p.nseg;
+    }
+    const u32 nmax = (p.nseg != 0u ? p.nseg : p.N);
+    const uint8_t *w0 = (const uint8_t *)W0.w + (GROUPED ? e * p.w_stride : 0);
+    const h16 *s0p = (const h16 *)W0.s + (GROUPED ? e * p.s_stride : 0);
+    const uint8_t *w1 = NMAT == 2 ? (const uint8_t *)W1.w + (GROUPED ? e * p.w_stride : 0) : nullptr;
+    const h16 *s1p = NMAT == 2 ? (const h16 *)W1.s + (GROUPED ? e * p.s_stride : 0) : nullptr;
+    __syncthreads();
+
+    f32x16 acc[NMAT][2], tmp[NMAT][2];
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[m][j][i] = 0.0f;
+
+    const u32 G = p.K / TK;
+    for (u32 g = 0; g < G; ++g) {
+        /* A tile: 64 rows x 64 halves, 2 x 16 B per thread */
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const u32 idx = t + q * PB, r = idx >> 3, c8 = idx & 7u;
+            const uint4 v = *(const uint4 *)(p.A + (size_t)arow[r] * p.lda + g * TK + 8u * c8);
+            *(uint4 *)(as + r * LDA + 8u * c8) = v;
+        }
+        load_w_tile<QT>(wsm[0], scs[0], w0, s0p, p.K, n0 - nbase, nmax, g);
+        if (NMAT == 2) load_w_tile<QT>(wsm[NMAT - 1], scs[NMAT - 1], w1, s1p, p.K, n0 - nbase, nmax, g);
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) tmp[m][j][i] = 0.0f;
+#pragma unroll
+        for (u32 kk = 0; kk < TK; kk += 16) {
+            U4H8 a;
+            a.u = *(const uint4 *)(as + (32u * wm + (lane & 31u)) * LDA + kk + 8u * (lane >> 5));
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    U4H8 b;
+                    b.u = *(const uint4 *)(wsm[m] + (64u * wn + 32u * j + (lane & 31u)) * LDA + kk + 8u * (lane >> 5));
+                    tmp[m][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.v, b.v, tmp[m][j], 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float s = QT == 1 ? 1.0f : scs[m][64u * wn + 32u * j + (lane & 31u)];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[m][j][i] = fmaf(tmp[m][j][i], s, acc[m][j][i]);
+            }
+        }
+        __syncthreads();
+    }
+
+    /* C layout of a 32x32 MFMA tile: lane l, element i -> row 8*(i/4) +
+     * 4*(l/32) + i%4, column l%32 */
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const u32 col = n0 + 64u * wn + 32u * j + (lane & 31u);
+        if (col >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const u32 r = 32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4);
+            if (r >= rows) continue;
+            const size_t orw = (size_t)orow[r];
+            if (EPI == GE_F32) {
+                ((float *)p.out)[orw * p.ldo + col] = acc[0][j][i];
+            } else if (EPI == GE_SWIGLU) {
+                ((h16 *)p.out)[orw * p.ldo + col] = (h16)(silu_p(acc[0][j][i]) * acc[NMAT - 1][j][i]);
+            } else {
+                float v = acc[0][j][i];
+                if (p.res != nullptr) v += (float)p.res[orw * p.ldr + col];
+                ((h16 *)p.out)[orw * p.ldo + col] = (h16)v;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* row RMSNorm, RoPE + KV scatter                                            */
+/* ------------------------------------------------------------------------ */
+
+/* One wavefront per row of 1280: y = f16(x * inv_rms * w) (norm.metal:12-40). */
+__global__ __launch_bounds__(PB) void k_rows_rmsnorm(const h16 *__restrict__ x, const h16 *__restrict__ w, u32 P,
+                                                     h16 *__restrict__ y) {
+    const u32 row = blockIdx.x * (PB / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    if (row >= P) return;
+    const h16 *xr = x + (size_t)row * UOCR_K_HIDDEN;
+    U4H8 v[3];
+    float ss = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const u32 i = lane + 64u * q;
+        if (i < UOCR_K_HIDDEN / 8u) {
+            v[q].u = ((const uint4 *)xr)[i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss = fmaf((float)v[q].h[j], (float)v[q].h[j], ss);
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    const float inv = 1.0f / sqrtf(ss / (float)UOCR_K_HIDDEN + 1.0e-6f);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const u32 i = lane + 64u * q;
+        if (i < UOCR_K_HIDDEN / 8u) {
+            U4H8 wv;
+            wv.u = ((const uint4 *)w)[i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[q].h[j] = (h16)(((float)v[q].h[j] * inv) * (float)wv.h[j]);
+            ((uint4 *)(y + (size_t)row * UOCR_K_HIDDEN))[i] = v[q].u;
+        }
+    }
+}
+
+struct RopeTabP {
+    float f[UOCR_K_HEAD_DIM / 2];
+};
+
+/* qkv [P][3840] (q | k | v, fp16) -> q rotated into qout [P][1280]; k
+ * rotated and v copied into cache slots 0..P-1 ([head][cap][128]).  One
+ * thread per (token, head, pair d < 64). */
+__global__ __launch_bounds__(PB) void k_rope_scatter(const h16 *__restrict__ qkv, RopeTabP rope, u32 P,
+                                                     h16 *__restrict__ qout, h16 *__restrict__ kc,
+                                                     h16 *__restrict__ vc, u32 cap) {
+    const u32 idx = blockIdx.x * PB + threadIdx.x;
+    if (idx >= P * UOCR_K_HEADS * 64u) return;
+    const u32 t = idx / (UOCR_K_HEADS * 64u), rem = idx % (UOCR_K_HEADS * 64u), h = rem / 64u, d = rem % 64u;
+    const h16 *row = qkv + (size_t)t * 3u * UOCR_K_HIDDEN;
+    const float ang = (float)t * rope.f[d];
+    const float cs = cosf(ang), sn = sinf(ang);
+    const u32 c = h * 128u + d;
+    const float qa = (float)row[c], qb = (float)row[c + 64u];
+    const float ka = (float)row[UOCR_K_HIDDEN + c], kb = (float)row[UOCR_K_HIDDEN + c + 64u];
+    qout[(size_t)t * UOCR_K_HIDDEN + c] = (h16)(qa * cs - qb * sn);
+    qout[(size_t)t * UOCR_K_HIDDEN + c + 64u] = (h16)(qa * sn + qb * cs);
+    const size_t ci = ((size_t)h * cap + t) * 128u + d;
+    kc[ci] = (h16)(ka * cs - kb * sn);
+    kc[ci + 64u] = (h16)(ka * sn + kb * cs);
+    vc[ci] = row[2u * UOCR_K_HIDDEN + c];
+    vc[ci + 64u] = row[2u * UOCR_K_HIDDEN + c + 64u];
+}
+
+/* ------------------------------------------------------------------------ */
+/* causal flash attention over the prompt                                    */
+/* ------------------------------------------------------------------------ */
+
+#define AQ 64 /* queries per block */
+#define AK 64 /* keys per step */
+#define LDQ (UOCR_K_HEAD_DIM + 8)
+#define LDV (AK + 8)
+
+/* Block (qt, h): queries q0..q0+63 of head h attend to slots 0..q (causal),
+ * fp32 online softmax scaled by 1/sqrt(128), output fp16 into ctx [P][1280]
+ * (attention_decode.metal arithmetic per query). */
+__global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, const h16 *__restrict__ kc,
+                                                   const h16 *__restrict__ vc, u32 cap, u32 P,
+                                                   h16 *__restrict__ ctx) {
+    __shared__ __attribute__((aligned(16))) h16 qs[AQ * LDQ];
+    __shared__ __attribute__((aligned(16))) h16 ks[AK * LDQ];
+    __shared__ __attribute__((aligned(16))) h16 vt[UOCR_K_HEAD_DIM * LDV];
+    __shared__ float sS[AQ][AK + 1];
+    __shared__ __attribute__((aligned(16))) h16 ps[AQ * LDV];
+    __shared__ float rowm[AQ], rowl[AQ], rowc[AQ];
+    const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const u32 h = blockIdx.y, q0 = blockIdx.x * AQ;
+    const h16 *kh = kc + (size_t)h * cap * 128u, *vh = vc + (size_t)h * cap * 128u;
+    const float scale = 0.08838834764831845f;
+
+    /* Q tile */
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const u32 idx = t + q * PB, r = idx >> 4, c8 = idx & 15u;
+        const u32 qr = min(q0 + r, P - 1u);
+        *(uint4 *)(qs + r * LDQ + 8u * c8) = *(const uint4 *)(Q + (size_t)qr * UOCR_K_HIDDEN + h * 128u + 8u * c8);
+    }
+    if (t < AQ) {
+        rowm[t] = -INFINITY;
+        rowl[t] = 0.0f;
+    }
+    f32x16 o[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[j][i] = 0.0f;
+    const u32 wm = wave & 1u, wn = wave >> 1;
+    const u32 qlast = min(q0 + AQ, P) - 1u;
+    for (u32 k0 = 0; k0 <= qlast; k0 += AK) {
+        __syncthreads();
+        /* K tile (row-major) and V tile transposed to [dim][key] */
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32 idx = t + q * PB, r = idx >> 4, c8 = idx & 15u;
+            const u32 kr = min(k0 + r, P - 1u);
+            *(uint4 *)(ks + r * LDQ + 8u * c8) = *(const uint4 *)(kh + (size_t)kr * 128u + 8u * c8);
+            U4H8 v;
+            v.u = *(const uint4 *)(vh + (size_t)kr * 128u + 8u * c8);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) vt[(8u * c8 + j) * LDV + r] = v.h[j];
+        }
+        __syncthreads();
+        /* S = Q K^T: wave (wm, wn) computes rows 32wm.., keys 32wn.. */
+        {
+            f32x16 s;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+            for (u32 kk = 0; kk < UOCR_K_HEAD_DIM; kk += 16) {
+                U4H8 a, b;
+                a.u = *(const uint4 *)(qs + (32u * wm + (lane & 31u)) * LDQ + kk + 8u * (lane >> 5));
+                b.u = *(const uint4 *)(ks + (32u * wn + (lane & 31u)) * LDQ + kk + 8u * (lane >> 5));
+                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.v, b.v, s, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const u32 r = 32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4), c = 32u * wn + (lane & 31u);
+                const u32 qi = q0 + r, ki = k0 + c;
+                sS[r][c] = (ki <= qi && ki < P) ? s[i] * scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        /* online softmax: 4 threads per row, 16 keys each */
+        {
+            const u32 r = t >> 2, part = t & 3u;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < 16; ++c) mx = fmaxf(mx, sS[r][16u * part + c]);
+            mx = fmaxf(mx, __shfl_xor(mx, 1));
+            mx = fmaxf(mx, __shfl_xor(mx, 2));
+            const float mold = rowm[r], mnew = fmaxf(mold, mx);
+            float sum = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const float v = sS[r][16u * part + c];
+                const float e = v == -INFINITY ? 0.0f : expf(v - mnew);
+                sum += e;
+                ps[r * LDV + 16u * part + c] = (h16)e;
+            }
+            sum += __shfl_xor(sum, 1);
+            sum += __shfl_xor(sum, 2);
+            __syncthreads();
+            if (part == 0u) {
+                const float corr = mold == -INFINITY ? 0.0f : expf(mold - mnew);
+                rowc[r] = corr;
+                rowl[r] = rowl[r] * corr + sum;
+                rowm[r] = mnew;
+            }
+        }
+        __syncthreads();
+        /* O = O * corr + P V: wave (wm, wn) owns rows 32wm.., dims 64wn.. */
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[j][i] *= rowc[32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4)];
+        }
+#pragma unroll
+        for (u32 kk = 0; kk < AK; kk += 16) {
+            U4H8 a;
+            a.u = *(const uint4 *)(ps + (32u * wm + (lane & 31u)) * LDV + kk + 8u * (lane >> 5));
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                U4H8 b;
+                b.u = *(const uint4 *)(vt + (64u * wn + 32u * j + (lane & 31u)) * LDV + kk + 8u * (lane >> 5));
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.v, b.v, o[j], 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const u32 r = 32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4);
+            const u32 d = 64u * wn + 32u * j + (lane & 31u);
+            if (q0 + r < P) ctx[(size_t)(q0 + r) * UOCR_K_HIDDEN + h * 128u + d] = (h16)(o[j][i] / rowl[r]);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* MoE routing, buckets, combine                                             */
+/* ------------------------------------------------------------------------ */
+
+__device__ __forceinline__ float lane_fp(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+/* One wavefront per token: softmax over its 64 logits, greedy top-6 (ties to
+ * the lower id; same key order as the decode router), raw probabilities
+ * unless norm_topk; counts tokens per expert. */
+__global__ __launch_bounds__(PB) void k_route_rows(const float *__restrict__ logits, u32 P, int norm_topk,
+                                                   int32_t *__restrict__ ids, float *__restrict__ wts,
+                                                   int32_t *__restrict__ counts) {
+    const u32 tok = blockIdx.x * (PB / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    if (tok >= P) return;
+    const float lg = logits[(size_t)tok * 64u + lane];
+    float mx = lg;
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    const float pe = expf(lg - mx);
+    float sum = pe;
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    const float prob = pe / sum;
+    const u32 pb = __float_as_uint(prob);
+    const unsigned long long key = ((unsigned long long)pb << 32) | (0xffffffffu - lane);
+    u32 rank = 0;
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+        const unsigned long long kj =
+            ((unsigned long long)(u32)__builtin_amdgcn_readlane((int)pb, j) << 32) | (0xffffffffu - (u32)j);
+        rank += kj > key ? 1u : 0u;
+    }
+    float tot = 0.0f;
+    float sel[UOCR_K_TOPK];
+#pragma unroll
+    for (int r = 0; r < UOCR_K_TOPK; ++r) {
+        const unsigned long long m = __ballot(rank == (u32)r);
+        const u32 l = m != 0ull ? (u32)__builtin_ctzll(m) : 0u;
+        sel[r] = __uint_as_float((u32)__builtin_amdgcn_readlane((int)pb, (int)l));
+        tot += sel[r];
+    }
+    if (rank < (u32)UOCR_K_TOPK) {
+        ids[tok * UOCR_K_TOPK + rank] = (int32_t)lane;
+        wts[tok * UOCR_K_TOPK + rank] = norm_topk ? prob / tot : prob;
+        atomicAdd(&counts[lane], 1);
+    }
+}
+
+/* One block: exclusive scan of the 64 bucket sizes, the tile table of the
+ * grouped GEMMs (TM rows per tile) and the per-bucket cursors. */
+__global__ __launch_bounds__(64) void k_bucket_scan(const int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
+                                                    int32_t *__restrict__ cursors, int32_t *__restrict__ tile_e,
+                                                    int32_t *__restrict__ tile_s0, int32_t *__restrict__ tile_s1,
+                                                    int32_t *__restrict__ ntiles) {
+    __shared__ int32_t off[65], toff[65];
+    const u32 e = threadIdx.x;
+    if (e == 0) {
+        int32_t a = 0, b = 0;
+        for (int i = 0; i < 64; ++i) {
+            off[i] = a;
+            toff[i] = b;
+            a += counts[i];
+            b += (counts[i] + TM - 1) / TM;
+        }
+        off[64] = a;
+        toff[64] = b;
+        *ntiles = b;
+    }
+    __syncthreads();
+    offsets[e] = off[e];
+    cursors[e] = 0;
+    const int32_t n = counts[e];
+    for (int32_t k = 0; k * TM < n; ++k) {
+        const int32_t ti = toff[e] + k;
+        tile_e[ti] = (int32_t)e;
+        tile_s0[ti] = off[e] + k * TM;
+        tile_s1[ti] = off[e] + min(n, (k + 1) * TM);
+    }
+}
+
+/* Slot of every (token, rank) pair in its expert's bucket. */
+__global__ __launch_bounds__(PB) void k_bucket_place(const int32_t *__restrict__ ids, u32 P,
+                                                     const int32_t *__restrict__ offsets, int32_t *__restrict__ cursors,
+                                                     int32_t *__restrict__ list_tok, int32_t *__restrict__ list_pair) {
+    const u32 pr = blockIdx.x * PB + threadIdx.x;
+    if (pr >= P * UOCR_K_TOPK) return;
+    const int32_t e = ids[pr];
+    const int32_t s = offsets[e] + atomicAdd(&cursors[e], 1);
+    list_tok[s] = (int32_t)(pr / UOCR_K_TOPK);
+    list_pair[s] = (int32_t)pr;
+}
+
+/* h[t] = f16(sum_r w[t][r] * Y[t*6+r] + shared[t] + res[t]) (decode_gemv_q4.
+ * metal:185-224 order: routed sum in fp32, shared already fp16). */
+__global__ __launch_bounds__(PB) void k_moe_combine(const float *__restrict__ Y, const float *__restrict__ wts,
+                                                    const h16 *__restrict__ shared, const h16 *__restrict__ res, u32 P,
+                                                    h16 *__restrict__ out) {
+    const u32 idx = blockIdx.x * PB + threadIdx.x;
+    if (idx >= P * UOCR_K_HIDDEN) return;
+    const u32 t = idx / UOCR_K_HIDDEN, c = idx % UOCR_K_HIDDEN;
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < UOCR_K_TOPK; ++r) {
+        acc = fmaf(wts[t * UOCR_K_TOPK + r], Y[((size_t)t * UOCR_K_TOPK + r) * UOCR_K_HIDDEN + c], acc);
+    }
+    out[idx] = (h16)(acc + (float)shared[idx] + (float)res[idx]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* launchers                                                                 */
+/* ------------------------------------------------------------------------ */
+
+static bool pq_ok(u32 q) {
+    return q == UOCR_QT_F16 || q == UOCR_QT_Q8 || q == UOCR_QT_Q4;
+}
+
+static bool pmat_ok(uocr_qmat m) {
+    return m.w != nullptr && pq_ok(m.qtype) && (m.qtype == UOCR_QT_F16 || m.s != nullptr);
+}
+
+template <int EPI, bool GROUPED>
+static void gemm_dispatch(hipStream_t st, u32 qt, const GemmArgs &a, dim3 grid) {
+    switch (qt) {
+        case UOCR_QT_F16: hipLaunchKernelGGL((k_gemm<1, EPI, GROUPED>), grid, dim3(PB), 0, st, a); break;
+        case UOCR_QT_Q8: hipLaunchKernelGGL((k_gemm<3, EPI, GROUPED>), grid, dim3(PB), 0, st, a); break;
+        default: hipLaunchKernelGGL((k_gemm<4, EPI, GROUPED>), grid, dim3(PB), 0, st, a); break;
+    }
+}
+
+extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d) {
+    if (d == nullptr || d->A == nullptr || d->out == nullptr || d->N == 0u || d->K == 0u || d->K % 64u != 0u ||
+        d->lda % 8u != 0u || !pmat_ok(d->W[0]) || (epi == UOCR_GEMM_SWIGLU && (!pmat_ok(d->W[1]) || d->W[1].qtype != d->W[0].qtype)) ||
+        (d->nseg != 0u && (d->nseg % TN != 0u || d->N % d->nseg != 0u || d->N / d->nseg > 3u))) {
+        return hipErrorInvalidValue;
+    }
+    for (u32 s = 1; d->nseg != 0u && s < d->N / d->nseg; ++s) {
+        if (!pmat_ok(d->W[s]) || d->W[s].qtype != d->W[0].qtype) return hipErrorInvalidValue;
+    }
+    const bool grouped = d->tile_e != nullptr;
+    if (grouped ? (d->a_idx == nullptr || d->o_idx == nullptr || d->tile_s0 == nullptr || d->tile_s1 == nullptr ||
+                   d->ntiles == nullptr || d->max_tiles == 0u)
+                : d->M == 0u) {
+        return hipErrorInvalidValue;
+    }
+    GemmArgs a;
+    a.A = (const h16 *)d->A;
+    a.lda = d->lda;
+    a.a_idx = d->a_idx;
+    a.o_idx = d->o_idx;
+    a.M = d->M;
+    a.N = d->N;
+    a.K = d->K;
+    for (int i = 0; i < 3; ++i) a.W[i] = d->W[i];
+    a.nseg = d->nseg;
+    a.w_stride = d->w_stride;
+    a.s_stride = d->s_stride;
+    a.tile_e = d->tile_e;
+    a.tile_s0 = d->tile_s0;
+    a.tile_s1 = d->tile_s1;
+    a.ntiles = d->ntiles;
+    a.out = d->out;
+    a.ldo = d->ldo;
+    a.res = (const h16 *)d->res;
+    a.ldr = d->ldr;
+    const dim3 grid(grouped ? d->max_tiles : (d->M + TM - 1u) / TM, (d->N + TN - 1u) / TN);
+    const u32 qt = d->W[0].qtype;
+    if (epi == UOCR_GEMM_F32) {
+        if (grouped) gemm_dispatch<GE_F32, true>(st, qt, a, grid);
+        else gemm_dispatch<GE_F32, false>(st, qt, a, grid);
+    } else if (epi == UOCR_GEMM_SWIGLU) {
+        if (grouped) gemm_dispatch<GE_SWIGLU, true>(st, qt, a, grid);
+        else gemm_dispatch<GE_SWIGLU, false>(st, qt, a, grid);
+    } else {
+        if (grouped) gemm_dispatch<GE_F16, true>(st, qt, a, grid);
+        else gemm_dispatch<GE_F16, false>(st, qt, a, grid);
+    }
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_rows_rmsnorm(hipStream_t st, const uint16_t *x, const uint16_t *w, uint32_t P,
+                                               uint16_t *y) {
+    if (x == nullptr || w == nullptr || y == nullptr || P == 0u) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rows_rmsnorm, dim3((P + 3u) / 4u), dim3(PB), 0, st, (const h16 *)x, (const h16 *)w, P, (h16 *)y);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_rope_scatter(hipStream_t st, const uint16_t *qkv, const float *inv_freq, uint32_t P,
+                                               uint16_t *qout, uint16_t *kcache, uint16_t *vcache, uint32_t cap) {
+    if (qkv == nullptr || inv_freq == nullptr || qout == nullptr || kcache == nullptr || vcache == nullptr || P == 0u ||
+        P > cap) {
+        return hipErrorInvalidValue;
+    }
+    RopeTabP tab;
+    for (int i = 0; i < UOCR_K_HEAD_DIM / 2; ++i) tab.f[i] = inv_freq[i];
+    const u32 n = P * UOCR_K_HEADS * 64u;
+    hipLaunchKernelGGL(k_rope_scatter, dim3((n + PB - 1u) / PB), dim3(PB), 0, st, (const h16 *)qkv, tab, P, (h16 *)qout,
+                       (h16 *)kcache, (h16 *)vcache, cap);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_flash_attn(hipStream_t st, const uint16_t *q, const uint16_t *kcache,
+                                             const uint16_t *vcache, uint32_t cap, uint32_t P, uint16_t *ctx) {
+    if (q == nullptr || kcache == nullptr || vcache == nullptr || ctx == nullptr || P == 0u || P > cap) {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(k_flash_attn, dim3((P + AQ - 1u) / AQ, UOCR_K_HEADS), dim3(PB), 0, st, (const h16 *)q,
+                       (const h16 *)kcache, (const h16 *)vcache, cap, P, (h16 *)ctx);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_route_rows(hipStream_t st, const float *logits, uint32_t P, int norm_topk,
+                                             int32_t *ids, float *wts, int32_t *counts, int32_t *offsets,
+                                             int32_t *cursors, int32_t *tile_e, int32_t *tile_s0, int32_t *tile_s1,
+                                             int32_t *ntiles, int32_t *list_tok, int32_t *list_pair) {
+    if (logits == nullptr || P == 0u || ids == nullptr || wts == nullptr || counts == nullptr || offsets == nullptr ||
+        cursors == nullptr || tile_e == nullptr || tile_s0 == nullptr || tile_s1 == nullptr || ntiles == nullptr ||
+        list_tok == nullptr || list_pair == nullptr) {
+        return hipErrorInvalidValue;
+    }
+    hipError_t e = hipMemsetAsync(counts, 0, 64u * sizeof(int32_t), st);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_route_rows, dim3((P + 3u) / 4u), dim3(PB), 0, st, logits, P, norm_topk, ids, wts, counts);
+    hipLaunchKernelGGL(k_bucket_scan, dim3(1), dim3(64), 0, st, (const int32_t *)counts, offsets, cursors, tile_e,
+                       tile_s0, tile_s1, ntiles);
+    const u32 n = P * UOCR_K_TOPK;
+    hipLaunchKernelGGL(k_bucket_place, dim3((n + PB - 1u) / PB), dim3(PB), 0, st, (const int32_t *)ids, P,
+                       (const int32_t *)offsets, cursors, list_tok, list_pair);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_moe_combine(hipStream_t st, const float *Y, const float *wts, const uint16_t *shared,
+                                              const uint16_t *res, uint32_t P, uint16_t *out) {
+    if (Y == nullptr || wts == nullptr || shared == nullptr || res == nullptr || out == nullptr || P == 0u) {
+        return hipErrorInvalidValue;
+    }
+    const u32 n = P * UOCR_K_HIDDEN;
+    hipLaunchKernelGGL(k_moe_combine, dim3((n + PB - 1u) / PB), dim3(PB), 0, st, Y, wts, (const h16 *)shared,
+                       (const h16 *)res, P, (h16 *)out);
+    return hipGetLastError();
+}

@@ -36,7 +36,7 @@ UOCR_PROFILE_MAX_EVENTS = 256
 
 QT_F16, QT_Q8, QT_Q4 = 1, 3, 4
 QPROFILE_FP16, QPROFILE_Q8, QPROFILE_Q4 = 1, 2, 3
-GEN_IGNORE_EOS, GEN_NO_GRAPH = 1, 2
+GEN_IGNORE_EOS, GEN_NO_GRAPH, GEN_TOKEN_PREFILL = 1, 2, 4
 
 HIDDEN, VOCAB, HEADS, HEAD_DIM = 1280, 129280, 10, 128
 TOKEN_BOS, TOKEN_EOS, TOKEN_IMAGE = 0, 1, 128815
@@ -131,6 +131,10 @@ SIGNATURES = {
     "uocr_op_attention_block": ([_U32, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _U32, _U32,
                                  _U32, _VP, _VP], ct.c_int),
     "uocr_op_embed": ([_U32, _VP, _VP, _U32, _VP, _VP], ct.c_int),
+    "uocr_op_gemm": ([_U32, _VP, _VP, _U32, _U32, _U32, _VP, _VP, _VP], ct.c_int),
+    "uocr_op_prefill_attention": ([_VP, _VP, _VP, _U32, _U32, _VP], ct.c_int),
+    "uocr_op_moe_rows_workspace_bytes": ([_U32], _SZ),
+    "uocr_op_moe_ffn_rows": ([ct.POINTER(CMoeWeights), _VP, _VP, _VP, _U32, ct.c_int, _VP, _VP], ct.c_int),
     "uocr_hip_device_count": ([], ct.c_int),
     "uocr_hip_alloc": ([_SZ], _VP),
     "uocr_hip_free": ([_VP], ct.c_int),
@@ -427,6 +431,24 @@ def op_attention_block(qtype, wq, sq, wk, sk, wv, sv, wo, so, hidden, norm_w, kc
 
 def op_embed(qtype, w, s, vocab, token, out) -> None:
     _check_op(load_library().uocr_op_embed(qtype, _p(w), _p(s), vocab, _p(token), _p(out)), "op_embed")
+
+
+def op_gemm(qtype, w, s, m, n, k, x, residual, y) -> None:
+    _check_op(load_library().uocr_op_gemm(qtype, _p(w), _p(s), m, n, k, _p(x), _p(residual), _p(y)), "op_gemm")
+
+
+def op_prefill_attention(q, kc, vc, cap, prompt_len, ctx) -> None:
+    _check_op(load_library().uocr_op_prefill_attention(_p(q), _p(kc), _p(vc), cap, prompt_len, _p(ctx)),
+              "op_prefill_attention")
+
+
+def moe_rows_workspace(rows: int) -> DeviceBuffer:
+    return DeviceBuffer(load_library().uocr_op_moe_rows_workspace_bytes(rows))
+
+
+def op_moe_ffn_rows(weights: CMoeWeights, x, norm_w, residual, rows, norm_topk, ws, out) -> None:
+    _check_op(load_library().uocr_op_moe_ffn_rows(ct.byref(weights), _p(x), _p(norm_w), _p(residual), rows, norm_topk,
+                                                  _p(ws), _p(out)), "op_moe_ffn_rows")
 
 
 class Timer:
