@@ -456,6 +456,11 @@ extern "C" int uocr_hip_memset(void *dst, int value, size_t bytes) {
     return hip_status(hipMemsetAsync(dst, value, bytes, st), "memset");
 }
 
+extern "C" int uocr_hip_copy(void *dst, const void *src, size_t bytes) {
+    STREAM_OR_RETURN(st);
+    return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st), "copy");
+}
+
 extern "C" int uocr_hip_sync(void) {
     STREAM_OR_RETURN(st);
     return hip_status(hipStreamSynchronize(st), "sync");

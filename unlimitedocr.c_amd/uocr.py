@@ -141,6 +141,7 @@ SIGNATURES = {
     "uocr_hip_upload": ([_VP, _VP, _SZ], ct.c_int),
     "uocr_hip_download": ([_VP, _VP, _SZ], ct.c_int),
     "uocr_hip_memset": ([_VP, ct.c_int, _SZ], ct.c_int),
+    "uocr_hip_copy": ([_VP, _VP, _SZ], ct.c_int),
     "uocr_hip_sync": ([], ct.c_int),
     "uocr_hip_op_error": ([], ct.c_char_p),
     "uocr_hip_timer_begin": ([], ct.c_int),
@@ -379,6 +380,11 @@ def _p(buf) -> ct.c_void_p:
     if isinstance(buf, DeviceBuffer):
         return ct.c_void_p(buf.ptr)
     return ct.c_void_p(int(buf))
+
+
+def copy(dst, src, nbytes: int) -> None:
+    """Device-to-device copy on the operator stream."""
+    _check_op(load_library().uocr_hip_copy(_p(dst), _p(src), nbytes), "copy")
 
 
 def sync() -> None:
