@@ -353,6 +353,16 @@ __host__ __device__ constexpr u32 j_for(u32 C) {
     return (C + lpr_for(C) - 1u) / lpr_for(C);
 }
 
+/* One-pass GEMVs are latency-bound (about one wavefront per SIMD), so they
+ * spread a row over more lanes: at most 3 chunk slots per lane below 64
+ * lanes, which shortens each wavefront's dequant-dot stream. */
+__host__ __device__ constexpr u32 lpr_lat(u32 C) {
+    return C <= 12u ? 4u : (C <= 24u ? 8u : (C <= 48u ? 16u : (C <= 96u ? 32u : 64u)));
+}
+__host__ __device__ constexpr u32 j_lat(u32 C) {
+    return (C + lpr_lat(C) - 1u) / lpr_lat(C);
+}
+
 /* Wave-uniform max of all 64 lanes with DPP row steps and readlanes. */
 __device__ __forceinline__ float wave_max_dpp(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v));
@@ -532,7 +542,7 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
                                                     const h16 *__restrict__ nw, RopeTab rope,
                                                     const uocr_step_state *__restrict__ st, h16 *__restrict__ qout,
                                                     h16 *__restrict__ kc, h16 *__restrict__ vc, u32 cap) {
-    constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
+    constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_lat(C), J = j_lat(C), R = 64u / LPR;
     constexpr u32 rb = 16u * C, G = K / 64u;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
@@ -852,7 +862,7 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl
     __shared__ float red[16];
     const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     if (blockIdx.x >= nb_routed) {
-        constexpr u32 C = chunks_per_row<QS>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR, rb = 16u * C;
+        constexpr u32 C = chunks_per_row<QS>(K), LPR = lpr_lat(C), J = j_lat(C), R = 64u / LPR, rb = 16u * C;
         const u32 sub = lane % LPR, grp = lane / LPR;
         const u32 r = ((blockIdx.x - nb_routed) * NWV + wave) * R + grp, rr = min(r, SI - 1u);
         XStage<UOCR_K_HIDDEN, SMALL_BLOCK> sx;
@@ -866,7 +876,7 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl
         if (r < SI && sub == 0u) smid[r] = (h16)(silu_f(dg) * du);
         return;
     }
-    constexpr u32 C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR, rb = 16u * C;
+    constexpr u32 C = chunks_per_row<QT>(K), LPR = lpr_lat(C), J = j_lat(C), R = 64u / LPR, rb = 16u * C;
     const u32 sub = lane % LPR, grp = lane / LPR;
     const float lg = logits[lane];
     XStage<UOCR_K_HIDDEN, SMALL_BLOCK> sx;
@@ -1249,7 +1259,7 @@ template <int QT>
 static void launch_qkv_qt(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
                           const uint16_t *nw, const RopeTab &tab, const uocr_step_state *state, uint16_t *qout,
                           uint16_t *kc, uint16_t *vc, u32 cap) {
-    constexpr u32 R = 64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN));
+    constexpr u32 R = 64u / lpr_lat(chunks_per_row<QT>(UOCR_K_HIDDEN));
     constexpr u32 ipb = (SMALL_BLOCK / 64) * R;
     hipLaunchKernelGGL((k_qkv_rope<QT>), dim3((1920u + ipb - 1u) / ipb), dim3(SMALL_BLOCK), 0, st, Q, K, V, (const h16 *)h,
                        (const h16 *)nw, tab, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap);
@@ -1325,8 +1335,8 @@ static void launch_moe_gu_qs(hipStream_t st, const uocr_expert_slab *slab, uocr_
                              const float *logits, int norm_topk, const uint16_t *x, const uint16_t *nw, uint16_t *mid,
                              uint16_t *smid, u32 *ids, float *wts) {
     constexpr u32 NWV = SMALL_BLOCK / 64u;
-    constexpr u32 rpb = NWV * (64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN)));
-    constexpr u32 rpb_s = NWV * (64u / lpr_for(chunks_per_row<QS>(UOCR_K_HIDDEN)));
+    constexpr u32 rpb = NWV * (64u / lpr_lat(chunks_per_row<QT>(UOCR_K_HIDDEN)));
+    constexpr u32 rpb_s = NWV * (64u / lpr_lat(chunks_per_row<QS>(UOCR_K_HIDDEN)));
     constexpr u32 nbr = (UOCR_K_TOPK * 896u + rpb - 1u) / rpb, nbs = (1792u + rpb_s - 1u) / rpb_s;
     hipLaunchKernelGGL((k_moe_gate_up<QT, QS>), dim3(nbr + nbs), dim3(SMALL_BLOCK), 0, st, *slab, SG, SU, logits,
                        norm_topk, (const h16 *)x, (const h16 *)nw, (h16 *)mid, (h16 *)smid, ids, wts, nbr);
