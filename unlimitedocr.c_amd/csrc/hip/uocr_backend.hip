@@ -437,7 +437,7 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c) {
     for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
         const dev_layer &L = c->L[l];
         uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
-        ENQ(uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->invf, c->state, c->q, kc, vc, c->cache_cap));
+        ENQ(uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->state, c->q, kc, vc, c->cache_cap));
         ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part));
         ENQ(uocr_launch_attn_out(s, L.o, c->attn_part, c->h, c->a, nullptr));
         if (l == 0u) {
@@ -459,7 +459,7 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c) {
 static hipError_t enqueue_select(uocr_hip_ctx *c, bool embed) {
     uocr_qmat none = {nullptr, nullptr, UOCR_QT_Q4};
     return uocr_launch_lm_head(c->stream, c->lm_head, UOCR_VOCAB_SIZE, c->h, c->final_norm, c->lm_part, c->state, 1,
-                               c->tokens, c->scores, embed ? c->embed : none, c->h);
+                               c->tokens, c->scores, embed ? c->embed : none, c->h, c->invf);
 }
 
 static hipError_t enqueue_decode_step(uocr_hip_ctx *c) {
@@ -469,7 +469,7 @@ static hipError_t enqueue_decode_step(uocr_hip_ctx *c) {
 }
 
 static hipError_t enqueue_prefill_step(uocr_hip_ctx *c) {
-    hipError_t e = uocr_launch_prefill_next(c->stream, c->state, c->prompt, c->h);
+    hipError_t e = uocr_launch_prefill_next(c->stream, c->state, c->prompt, c->h, c->invf);
     if (e == hipSuccess) e = enqueue_layers(c);
     return e;
 }
@@ -659,7 +659,7 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
     HIPCHK(uocr_launch_embed_rows(s, c->embed, UOCR_VOCAB_SIZE, c->d_ids, dmask, P, c->prompt), "prompt embedding");
 
     /* prefill */
-    HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0), "state init");
+    HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf), "state init");
     if ((req->flags & UOCR_GEN_TOKEN_PREFILL) == 0u) {
         HIPCHK(enqueue_prefill_mfma(c, P), "MFMA prefill");
     } else {
@@ -676,7 +676,7 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
 
     /* decode: chunks of DECODE_CHUNK steps; the host scans chunk k-1 while
      * chunk k runs */
-    HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0), "decode state init");
+    HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf), "decode state init");
     const int ignore_eos = (req->flags & UOCR_GEN_IGNORE_EOS) != 0u;
     uint32_t count = 0, scanned = 0;
     int eos = 0;

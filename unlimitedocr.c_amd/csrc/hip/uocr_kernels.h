@@ -42,6 +42,8 @@ typedef struct uocr_step_state {
     int32_t attn_len;     /* attention length */
     int32_t first_gen;    /* logical index of the first live ring token */
     int32_t cur_token;    /* token id embedded this step */
+    float rope_cos[UOCR_K_HEAD_DIM / 2]; /* cos/sin(pos * inv_freq[d]) of this step's position */
+    float rope_sin[UOCR_K_HEAD_DIM / 2];
 } uocr_step_state;
 
 typedef struct uocr_qmat {
@@ -78,8 +80,8 @@ hipError_t uocr_launch_rmsnorm(hipStream_t st, const uint16_t *x, const uint16_t
  * at st->pos -> q to qout, k/v into the caches at st->cache_token.
  * Caches are [heads][cache_capacity][128] fp16 for one layer. */
 hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
-                                const uint16_t *nw, const float *inv_freq, const uocr_step_state *state,
-                                uint16_t *qout, uint16_t *kcache, uint16_t *vcache, uint32_t cache_capacity);
+                                const uint16_t *nw, const uocr_step_state *state, uint16_t *qout, uint16_t *kcache,
+                                uint16_t *vcache, uint32_t cache_capacity);
 /* Split-K decode attention over the live slots [0, state->attn_len) of one
  * layer's caches (UOCR_K_ATTN_SPLITS blocks per head, slots partitioned by
  * cache_capacity): writes UOCR_ATTN_PARTIAL_FLOATS of per-split partials. */
@@ -120,7 +122,7 @@ hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, co
  * partials: UOCR_LM_PARTIAL_WORDS words. */
 hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x, const uint16_t *nw,
                                uint32_t *partials, uocr_step_state *state, int advance, int32_t *tokens,
-                               float *scores, uocr_qmat E, uint16_t *hout);
+                               float *scores, uocr_qmat E, uint16_t *hout, const float *inv_freq);
 /* Embedding gather of tokens[0] (token == NULL: state->cur_token) -> fp16 row. */
 hipError_t uocr_launch_embed(hipStream_t st, uocr_qmat E, uint32_t vocab, const int32_t *token,
                              const uocr_step_state *state, uint16_t *out);
@@ -129,11 +131,13 @@ hipError_t uocr_launch_embed_rows(hipStream_t st, uocr_qmat E, uint32_t vocab, c
                                   const uint8_t *mask, uint32_t n, uint16_t *out);
 /* Replayable prefill step: copies prompt row state->t into h, sets the
  * causal-prefix plan for that position and increments state->t. */
-hipError_t uocr_launch_prefill_next(hipStream_t st, uocr_step_state *state, const uint16_t *prompt, uint16_t *h);
+hipError_t uocr_launch_prefill_next(hipStream_t st, uocr_step_state *state, const uint16_t *prompt, uint16_t *h,
+                                    const float *inv_freq);
 /* Sets *state for prompt position i (prefill through the decode kernels). */
-hipError_t uocr_launch_prefill_state(hipStream_t st, uocr_step_state *state, int32_t i);
+hipError_t uocr_launch_prefill_state(hipStream_t st, uocr_step_state *state, int32_t i, const float *inv_freq);
 /* Sets *state for decode with explicit (prompt_len, gen_after_write). */
-hipError_t uocr_launch_decode_state(hipStream_t st, uocr_step_state *state, int32_t prompt_len, int32_t t);
+hipError_t uocr_launch_decode_state(hipStream_t st, uocr_step_state *state, int32_t prompt_len, int32_t t,
+                                    const float *inv_freq);
 
 /* ---- prefill (MFMA) ------------------------------------------------------ */
 

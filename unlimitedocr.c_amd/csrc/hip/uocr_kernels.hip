@@ -372,35 +372,41 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
+/* Wave-uniform max of a 32-bit unsigned value over all 64 lanes (DPP row
+ * steps, then readlanes of the four row results). */
+__device__ __forceinline__ u32 wave_max_u32(u32 v) {
+    v = max(v, (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, true));
+    v = max(v, (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, true));
+    v = max(v, (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, true));
+    v = max(v, (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, true));
+    const u32 a = (u32)__builtin_amdgcn_readlane((int)v, 0), b = (u32)__builtin_amdgcn_readlane((int)v, 16);
+    const u32 c = (u32)__builtin_amdgcn_readlane((int)v, 32), d = (u32)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
+}
+
 /* Greedy top-6 over 64 router logits by one wavefront (one expert per lane):
- * max-subtracted softmax, then the greedy order of the keys (probability
- * bits, inverted id), i.e. probability descending with ties to the lower id
- * (uocr_cpu_ref.c:443-463, moe.metal:12-18).  Each lane counts the keys
- * above its own (64 wave-uniform broadcasts, no dependent chain); the lanes
- * of rank 0..5 are picked by ballot.  Raw probabilities unless norm_topk.
- * The results are wave-uniform. */
+ * max-subtracted softmax, then 6 rounds of "largest probability, lowest id
+ * among equals" (uocr_cpu_ref.c:443-463, moe.metal:12-18): a DPP wave max
+ * of the probability bits (non-negative floats order as unsigned integers)
+ * and a ballot of the lanes holding it.  Raw probabilities unless
+ * norm_topk.  The results are wave-uniform. */
 __device__ __forceinline__ void topk6(float lg, int norm_topk, u32 (&sid)[UOCR_K_TOPK], float (&sw)[UOCR_K_TOPK]) {
     const u32 lane = threadIdx.x & 63u;
     const float mx = wave_max_dpp(lg);
     const float pe = expf(lg - mx);
     const float prob = pe / wave_sum(pe);
-    const u32 pb = __float_as_uint(prob);
-    const unsigned long long key = ((unsigned long long)pb << 32) | (0xffffffffu - lane);
-    u32 rank = 0;
-#pragma unroll
-    for (int j = 0; j < 64; ++j) {
-        const unsigned long long kj =
-            ((unsigned long long)(u32)__builtin_amdgcn_readlane((int)pb, j) << 32) | (0xffffffffu - (u32)j);
-        rank += kj > key ? 1u : 0u;
-    }
+    u32 key = __float_as_uint(prob);
+    bool live = true;
     float tot = 0.0f;
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
-        const unsigned long long m = __ballot(rank == (u32)r);
-        const u32 l = m != 0ull ? (u32)__builtin_ctzll(m) : 0u;
+        const u32 best = wave_max_u32(live ? key : 0u);
+        const unsigned long long m = __ballot(live && key == best);
+        const u32 l = (u32)__builtin_ctzll(m);
         sid[r] = l;
-        sw[r] = __uint_as_float((u32)__builtin_amdgcn_readlane((int)pb, (int)l));
+        sw[r] = __uint_as_float(best);
         tot += sw[r];
+        live = live && lane != l;
     }
     if (norm_topk) {
 #pragma unroll
@@ -533,13 +539,25 @@ struct RopeTab {
     float f[UOCR_K_HEAD_DIM / 2];
 };
 
+/* cos/sin(pos * inv_freq[d]) of a step's position into the step state
+ * (threads d < 64), so the 12 QKV launches of the step read them instead of
+ * evaluating trig on their critical path (rope.metal:16-70 angle form). */
+__device__ __forceinline__ void set_rope(uocr_step_state *st, int32_t pos, const RopeTab &tab) {
+    const u32 d = threadIdx.x;
+    if (d < UOCR_K_HEAD_DIM / 2) {
+        const float ang = (float)pos * tab.f[d];
+        st->rope_cos[d] = cosf(ang);
+        st->rope_sin[d] = sinf(ang);
+    }
+}
+
 /* Work item i (0..1919): matrix m = i/640 (q,k,v), head h, pair d; a lane
  * group computes rows h*128+d and h*128+d+64 of matrix m, rounds them to
  * fp16, rotates q/k by the split-half RoPE at st->pos and stores q, or k/v
  * into the cache slot st->cache_token.  One item per lane group. */
 template <int QT>
 __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, uocr_qmat V, const h16 *__restrict__ hin,
-                                                    const h16 *__restrict__ nw, RopeTab rope,
+                                                    const h16 *__restrict__ nw,
                                                     const uocr_step_state *__restrict__ st, h16 *__restrict__ qout,
                                                     h16 *__restrict__ kc, h16 *__restrict__ vc, u32 cap) {
     constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_lat(C), J = j_lat(C), R = 64u / LPR;
@@ -558,8 +576,8 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
     RowFrag<J> fa, fb;
     frag_load<QT, LPR, J>(fa, (const uint8_t *)M.w + (size_t)ra * rb, (const h16 *)M.s + (size_t)ra * G, C, sub);
     frag_load<QT, LPR, J>(fb, (const uint8_t *)M.w + (size_t)rbw * rb, (const h16 *)M.s + (size_t)rbw * G, C, sub);
-    const int32_t pos = st->pos;
     const u32 ct = (u32)st->cache_token;
+    const float cs = st->rope_cos[d], sn = st->rope_sin[d];
     stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
     const float da = group_sum<LPR>(frag_dot<QT, LPR, J>(fa, xs, C, sub));
     const float db = group_sum<LPR>(frag_dot<QT, LPR, J>(fb, xs, C, sub));
@@ -570,8 +588,6 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
             vc[cix] = a;
             vc[cix + 64u] = b;
         } else {
-            const float ang = (float)pos * rope.f[d];
-            const float cs = cosf(ang), sn = sinf(ang);
             const float fa2 = (float)a, fb2 = (float)b;
             const h16 na = (h16)(fa2 * cs - fb2 * sn), nb = (h16)(fa2 * sn + fb2 * cs);
             if (m == 0u) {
@@ -647,20 +663,30 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
     for (int ib = i0 + gid;;) {
+        /* all slot scores first (independent), then one softmax update */
+        float sc[ATT_UNROLL];
+        float mn = m;
 #pragma unroll
         for (int u = 0; u < ATT_UNROLL; ++u) {
-            if (ib + 16 * u < i1) {
-                float d = 0.0f;
+            float d = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) d = fmaf(qv[j], (float)kk[u].h[j], d);
-                const float sc = row16_sum(d) * scale;
-                const float mn = fmaxf(m, sc);
-                const float corr = expf(m - mn), e = expf(sc - mn);
-                l = l * corr + e;
+            for (int j = 0; j < 8; ++j) d = fmaf(qv[j], (float)kk[u].h[j], d);
+            sc[u] = ib + 16 * u < i1 ? row16_sum(d) * scale : -INFINITY;
+            mn = fmaxf(mn, sc[u]);
+        }
+        if (mn != -INFINITY) {
+            const float corr = expf(m - mn);
+            l *= corr;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] = fmaf(e, (float)vv[u].h[j], acc[j] * corr);
-                m = mn;
+            for (int j = 0; j < 8; ++j) acc[j] *= corr;
+#pragma unroll
+            for (int u = 0; u < ATT_UNROLL; ++u) {
+                const float e = expf(sc[u] - mn);
+                l += e;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = fmaf(e, (float)vv[u].h[j], acc[j]);
             }
+            m = mn;
         }
         ib += 16 * ATT_UNROLL;
         if (ib >= i1) break;
@@ -1030,11 +1056,12 @@ __global__ __launch_bounds__(BLOCK) void k_embed_rows(const uint8_t *__restrict_
 /* One replayable prefill step: position i = st->t; copy prompt row i into h
  * and set the causal-prefix attention plan; then st->t = i + 1. */
 __global__ __launch_bounds__(BLOCK) void k_prefill_next(uocr_step_state *st, const h16 *__restrict__ prompt,
-                                                        h16 *__restrict__ h) {
+                                                        h16 *__restrict__ h, RopeTab tab) {
     const int32_t i = st->t;
     const uint4 *src = (const uint4 *)(prompt + (size_t)i * UOCR_K_HIDDEN);
     uint4 *dst = (uint4 *)h;
     for (u32 c = threadIdx.x; c < UOCR_K_HIDDEN / 8u; c += blockDim.x) dst[c] = src[c];
+    set_rope(st, i, tab);
     __syncthreads();
     if (threadIdx.x == 0) {
         st->pos = i;
@@ -1046,24 +1073,30 @@ __global__ __launch_bounds__(BLOCK) void k_prefill_next(uocr_step_state *st, con
     }
 }
 
-__global__ void k_prefill_state(uocr_step_state *st, int32_t i) {
-    st->pos = i;
-    st->cache_token = i;
-    st->attn_prompt = i + 1;
-    st->attn_len = i + 1;
-    st->first_gen = 0;
+__global__ void k_prefill_state(uocr_step_state *st, int32_t i, RopeTab tab) {
+    set_rope(st, i, tab);
+    if (threadIdx.x == 0) {
+        st->pos = i;
+        st->cache_token = i;
+        st->attn_prompt = i + 1;
+        st->attn_len = i + 1;
+        st->first_gen = 0;
+    }
 }
 
-__global__ void k_decode_state(uocr_step_state *st, int32_t P, int32_t t) {
-    const int32_t gcount = t + 1;
-    const int32_t live = gcount < UOCR_K_RING ? gcount : UOCR_K_RING;
-    st->t = t;
-    st->prompt_len = P;
-    st->pos = P + t;
-    st->cache_token = P + (t % UOCR_K_RING);
-    st->attn_prompt = P;
-    st->attn_len = P + live;
-    st->first_gen = gcount - live;
+__global__ void k_decode_state(uocr_step_state *st, int32_t P, int32_t t, RopeTab tab) {
+    set_rope(st, P + t, tab);
+    if (threadIdx.x == 0) {
+        const int32_t gcount = t + 1;
+        const int32_t live = gcount < UOCR_K_RING ? gcount : UOCR_K_RING;
+        st->t = t;
+        st->prompt_len = P;
+        st->pos = P + t;
+        st->cache_token = P + (t % UOCR_K_RING);
+        st->attn_prompt = P;
+        st->attn_len = P + live;
+        st->first_gen = gcount - live;
+    }
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1080,10 +1113,10 @@ template <int QE>
 __global__ __launch_bounds__(BLOCK) void k_lm_finalize(const u32 *__restrict__ part, u32 nparts, uocr_step_state *st,
                                                        int advance, int32_t *tokens, float *scores,
                                                        const uint8_t *__restrict__ EW, const h16 *__restrict__ ES,
-                                                       u32 vocab, h16 *__restrict__ hout) {
+                                                       u32 vocab, h16 *__restrict__ hout, RopeTab tab, int with_rope) {
     __shared__ float bsc[NWAVE];
     __shared__ u32 bidv[NWAVE];
-    __shared__ int32_t chosen;
+    __shared__ int32_t chosen, next_pos;
     float ps[4];
     u32 pid[4];
 #pragma unroll
@@ -1140,8 +1173,10 @@ __global__ __launch_bounds__(BLOCK) void k_lm_finalize(const u32 *__restrict__ p
             st->t = t + 1;
         }
         chosen = id;
+        next_pos = st != nullptr ? st->prompt_len + t : 0;
     }
     __syncthreads();
+    if (st != nullptr && advance && with_rope) set_rope(st, next_pos, tab);
     if (advance && EW != nullptr) embed_row_body<QE>(EW, ES, vocab, chosen, hout);
 }
 
@@ -1257,26 +1292,23 @@ extern "C" hipError_t uocr_launch_rmsnorm(hipStream_t st, const uint16_t *x, con
 
 template <int QT>
 static void launch_qkv_qt(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
-                          const uint16_t *nw, const RopeTab &tab, const uocr_step_state *state, uint16_t *qout,
+                          const uint16_t *nw, const uocr_step_state *state, uint16_t *qout,
                           uint16_t *kc, uint16_t *vc, u32 cap) {
     constexpr u32 R = 64u / lpr_lat(chunks_per_row<QT>(UOCR_K_HIDDEN));
     constexpr u32 ipb = (SMALL_BLOCK / 64) * R;
     hipLaunchKernelGGL((k_qkv_rope<QT>), dim3((1920u + ipb - 1u) / ipb), dim3(SMALL_BLOCK), 0, st, Q, K, V, (const h16 *)h,
-                       (const h16 *)nw, tab, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap);
+                       (const h16 *)nw, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap);
 }
 
 extern "C" hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
-                                           const uint16_t *nw, const float *inv_freq, const uocr_step_state *state,
-                                           uint16_t *qout, uint16_t *kcache, uint16_t *vcache,
-                                           uint32_t cache_capacity) {
+                                           const uint16_t *nw, const uocr_step_state *state, uint16_t *qout,
+                                           uint16_t *kcache, uint16_t *vcache, uint32_t cache_capacity) {
     if (!mat_ok(Q) || !mat_ok(K) || !mat_ok(V) || Q.qtype != K.qtype || Q.qtype != V.qtype || h == nullptr ||
-        nw == nullptr || inv_freq == nullptr || state == nullptr || qout == nullptr || kcache == nullptr ||
-        vcache == nullptr || cache_capacity == 0u) {
+        nw == nullptr || state == nullptr || qout == nullptr || kcache == nullptr || vcache == nullptr ||
+        cache_capacity == 0u) {
         return hipErrorInvalidValue;
     }
-    RopeTab tab;
-    for (int i = 0; i < UOCR_K_HEAD_DIM / 2; ++i) tab.f[i] = inv_freq[i];
-    DISPATCH_QT(Q.qtype, launch_qkv_qt, st, Q, K, V, h, nw, tab, state, qout, kcache, vcache, cache_capacity);
+    DISPATCH_QT(Q.qtype, launch_qkv_qt, st, Q, K, V, h, nw, state, qout, kcache, vcache, cache_capacity);
     return hipGetLastError();
 }
 
@@ -1398,16 +1430,25 @@ extern "C" hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_sla
     return hipGetLastError();
 }
 
+static RopeTab rope_tab(const float *inv_freq) {
+    RopeTab tab;
+    for (int i = 0; i < UOCR_K_HEAD_DIM / 2; ++i) tab.f[i] = inv_freq != nullptr ? inv_freq[i] : 0.0f;
+    return tab;
+}
+
 template <int QE>
 static void launch_lm_fin(hipStream_t st, const u32 *part, u32 nb, uocr_step_state *state, int advance,
-                          int32_t *tokens, float *scores, uocr_qmat E, u32 vocab, uint16_t *hout) {
+                          int32_t *tokens, float *scores, uocr_qmat E, u32 vocab, uint16_t *hout,
+                          const float *inv_freq) {
     hipLaunchKernelGGL((k_lm_finalize<QE>), dim3(1), dim3(BLOCK), 0, st, part, nb, state, advance, tokens, scores,
-                       (const uint8_t *)E.w, (const h16 *)E.s, vocab, (h16 *)hout);
+                       (const uint8_t *)E.w, (const h16 *)E.s, vocab, (h16 *)hout, rope_tab(inv_freq),
+                       inv_freq != nullptr ? 1 : 0);
 }
 
 extern "C" hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x,
                                           const uint16_t *nw, uint32_t *partials, uocr_step_state *state, int advance,
-                                          int32_t *tokens, float *scores, uocr_qmat E, uint16_t *hout) {
+                                          int32_t *tokens, float *scores, uocr_qmat E, uint16_t *hout,
+                                          const float *inv_freq) {
     if (!mat_ok(W) || vocab == 0u || x == nullptr || partials == nullptr || tokens == nullptr ||
         (advance && state == nullptr) || (E.w != nullptr && (!mat_ok(E) || hout == nullptr))) {
         return hipErrorInvalidValue;
@@ -1420,7 +1461,7 @@ extern "C" hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t 
         default: launch_stream<4, EPI_ARGMAX>(st, W, W, vocab, UOCR_K_HIDDEN, x, nw, nullptr, nullptr, partials, maxb, &nb); break;
     }
     DISPATCH_QT(E.w != nullptr ? E.qtype : UOCR_QT_Q4, launch_lm_fin, st, partials, nb, state, advance, tokens, scores,
-                E, vocab, hout);
+                E, vocab, hout, inv_freq);
     return hipGetLastError();
 }
 
@@ -1453,20 +1494,23 @@ extern "C" hipError_t uocr_launch_embed_rows(hipStream_t st, uocr_qmat E, uint32
 }
 
 extern "C" hipError_t uocr_launch_prefill_next(hipStream_t st, uocr_step_state *state, const uint16_t *prompt,
-                                               uint16_t *h) {
-    if (state == nullptr || prompt == nullptr || h == nullptr) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_prefill_next, dim3(1), dim3(BLOCK), 0, st, state, (const h16 *)prompt, (h16 *)h);
+                                               uint16_t *h, const float *inv_freq) {
+    if (state == nullptr || prompt == nullptr || h == nullptr || inv_freq == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_prefill_next, dim3(1), dim3(BLOCK), 0, st, state, (const h16 *)prompt, (h16 *)h,
+                       rope_tab(inv_freq));
     return hipGetLastError();
 }
 
-extern "C" hipError_t uocr_launch_prefill_state(hipStream_t st, uocr_step_state *state, int32_t i) {
-    if (state == nullptr || i < 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_prefill_state, dim3(1), dim3(1), 0, st, state, i);
+extern "C" hipError_t uocr_launch_prefill_state(hipStream_t st, uocr_step_state *state, int32_t i,
+                                                const float *inv_freq) {
+    if (state == nullptr || i < 0 || inv_freq == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_prefill_state, dim3(1), dim3(64), 0, st, state, i, rope_tab(inv_freq));
     return hipGetLastError();
 }
 
-extern "C" hipError_t uocr_launch_decode_state(hipStream_t st, uocr_step_state *state, int32_t prompt_len, int32_t t) {
-    if (state == nullptr || prompt_len <= 0 || t < 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_decode_state, dim3(1), dim3(1), 0, st, state, prompt_len, t);
+extern "C" hipError_t uocr_launch_decode_state(hipStream_t st, uocr_step_state *state, int32_t prompt_len, int32_t t,
+                                               const float *inv_freq) {
+    if (state == nullptr || prompt_len <= 0 || t < 0 || inv_freq == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_decode_state, dim3(1), dim3(64), 0, st, state, prompt_len, t, rope_tab(inv_freq));
     return hipGetLastError();
 }

@@ -69,7 +69,7 @@ constexpr size_t A256(size_t v) {
     return (v + 255u) & ~(size_t)255u;
 }
 constexpr size_t WS_STATE = 0;
-constexpr size_t WS_APART = WS_STATE + 256u;
+constexpr size_t WS_APART = WS_STATE + A256(sizeof(uocr_step_state));
 constexpr size_t WS_LOGITS = WS_APART + A256(UOCR_ATTN_PARTIAL_FLOATS * 4u);
 constexpr size_t WS_LPART = WS_LOGITS + 256u;
 constexpr size_t WS_IDS = WS_LPART + A256(UOCR_LM_PARTIAL_WORDS * 4u);
@@ -127,7 +127,7 @@ extern "C" int uocr_op_lm_head_argmax(uint32_t qtype, const void *w, const void 
     STREAM_OR_RETURN(st);
     return hip_status(uocr_launch_lm_head(st, qm(qtype, w, s), vocab, (const uint16_t *)x, (const uint16_t *)norm_w,
                                           ws<uint32_t>(workspace, WS_LPART), nullptr, 0, token, score,
-                                          qm(qtype, nullptr, nullptr), nullptr),
+                                          qm(qtype, nullptr, nullptr), nullptr, nullptr),
                       "lm_head_argmax");
 }
 
@@ -175,14 +175,21 @@ extern "C" int uocr_op_moe_ffn(const uocr_op_moe_weights *m, const void *x, cons
     return r;
 }
 
+static void rope_inv_freq(float *invf) {
+    const float freq_scale = -2.0f * log2f(10000.0f) / (float)UOCR_K_HEAD_DIM;
+    for (int d = 0; d < UOCR_K_HEAD_DIM / 2; ++d) invf[d] = exp2f((float)d * freq_scale);
+}
+
 static int set_plan(hipStream_t st, void *workspace, uint32_t cap, uint32_t P, uint32_t g) {
     if (P == 0u || (uint64_t)P + (g < UOCR_K_RING ? g : UOCR_K_RING) > cap) {
         return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "attention plan (prompt %u, generated %u) exceeds cache capacity %u", P,
                        g, cap);
     }
+    float invf[UOCR_K_HEAD_DIM / 2];
+    rope_inv_freq(invf);
     uocr_step_state *state = ws<uocr_step_state>(workspace, WS_STATE);
-    if (g == 0u) return hip_status(uocr_launch_prefill_state(st, state, (int32_t)P - 1), "attention plan");
-    return hip_status(uocr_launch_decode_state(st, state, (int32_t)P, (int32_t)g - 1), "attention plan");
+    if (g == 0u) return hip_status(uocr_launch_prefill_state(st, state, (int32_t)P - 1, invf), "attention plan");
+    return hip_status(uocr_launch_decode_state(st, state, (int32_t)P, (int32_t)g - 1, invf), "attention plan");
 }
 
 extern "C" int uocr_op_attention_decode(const void *q, const void *k_cache, const void *v_cache,
@@ -212,15 +219,12 @@ extern "C" int uocr_op_attention_block(uint32_t qtype, const void *wq, const voi
         return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid attention_block arguments");
     }
     STREAM_OR_RETURN(st);
-    float invf[UOCR_K_HEAD_DIM / 2];
-    const float freq_scale = -2.0f * log2f(10000.0f) / (float)UOCR_K_HEAD_DIM;
-    for (int d = 0; d < UOCR_K_HEAD_DIM / 2; ++d) invf[d] = exp2f((float)d * freq_scale);
     uocr_step_state *state = ws<uocr_step_state>(workspace, WS_STATE);
     uint16_t *qb = ws<uint16_t>(workspace, WS_Q), *cb = ws<uint16_t>(workspace, WS_CTX);
     int r = set_plan(st, workspace, cache_capacity, prompt_length, generated_count);
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_qkv_rope(st, qm(qtype, wq, sq), qm(qtype, wk, sk), qm(qtype, wv, sv),
-                                            (const uint16_t *)hidden, (const uint16_t *)norm_w, invf, state, qb,
+                                            (const uint16_t *)hidden, (const uint16_t *)norm_w, state, qb,
                                             (uint16_t *)k_cache, (uint16_t *)v_cache, cache_capacity),
                        "qkv_rope");
     }
