@@ -36,26 +36,8 @@ import uocr  # noqa: E402
 METRIC = "decode tok/s at batch 1 (Q4, Q8, fp16); achieved HBM GB/s vs 8 TB/s peak"
 PEAK_HBM = 8.0e12
 N_IMAGE, N_TEXT, N_NEW = 900, 32, 512
-ENTRY = np.dtype([("id", "<u4"), ("family", "<u4"), ("layer", "<i4"), ("expert", "<i4"), ("projection", "<u4"),
-                  ("usage", "<u4"), ("qtype", "<u4"), ("flags", "<u4"), ("rank", "<u4"), ("lshape", "<u4", 4),
-                  ("pshape", "<u4", 4), ("payload_offset", "<u8"), ("payload_size", "<u8"), ("block_size", "<u4"),
-                  ("row_size", "<u4"), ("scale_offset", "<u8"), ("scale_size", "<u8"), ("min_offset", "<u8"),
-                  ("min_size", "<u8"), ("reasons", "<u4", 2), ("source_name", "<u4", 2)])
-assert ENTRY.itemsize == 140
-
-
 def tensor_table(model: uocr.SynthModel) -> np.ndarray:
-    """Tensor directory of a .uocr image (uocr_format.h:268-299 layout)."""
-    v = model.view()
-    hdr = v[:112]
-    n_sec = int(hdr[24:28].view("<u4")[0])
-    sec_off = int(hdr[40:48].view("<u8")[0])
-    secs = v[sec_off:sec_off + 32 * n_sec].view(np.dtype([("type", "<u4"), ("flags", "<u4"), ("offset", "<u8"),
-                                                            ("size", "<u8"), ("alignment", "<u8")]))
-    d = secs[secs["type"] == 2][0]
-    count = int(v[d["offset"] + 12:d["offset"] + 16].view("<u4")[0])
-    start = int(d["offset"]) + 16
-    return v[start:start + 140 * count].view(ENTRY)
+    return uocr.tensor_table(model.view())
 
 
 def decode_bytes_per_token(model: uocr.SynthModel, prompt_len: int, n_new: int) -> float:

@@ -19,9 +19,11 @@
  *     selection :11360-11462, chunk loop :11487-11576) with fp16 rounding at
  *     the points of src/unlimitedocr_c/golden.py:381-666.
  * Each function cites the reference lines it follows.  How each one is
- * pinned (golden vectors, closed forms, brute force) is listed in the test
- * files that exercise it; functions with no independent pin are marked
- * "parity unpinned" at their declaration.
+ * pinned (golden vectors, closed forms, brute force, the reference's own
+ * compiled CPU ops) is listed in the test files that exercise it
+ * (tests/test_oracle.py, tests/test_oracle_compose.py for the decode-step
+ * and MoE compositions); functions with no independent pin would be marked
+ * "parity unpinned" at their declaration (none is).
  */
 #ifndef UOCR_ORACLE_H
 #define UOCR_ORACLE_H

@@ -322,6 +322,36 @@ class SynthModel:
             pass
 
 
+TENSOR_ENTRY = np.dtype([("id", "<u4"), ("family", "<u4"), ("layer", "<i4"), ("expert", "<i4"),
+                         ("projection", "<u4"), ("usage", "<u4"), ("qtype", "<u4"), ("flags", "<u4"), ("rank", "<u4"),
+                         ("lshape", "<u4", 4), ("pshape", "<u4", 4), ("payload_offset", "<u8"),
+                         ("payload_size", "<u8"), ("block_size", "<u4"), ("row_size", "<u4"),
+                         ("scale_offset", "<u8"), ("scale_size", "<u8"), ("min_offset", "<u8"), ("min_size", "<u8"),
+                         ("reasons", "<u4", 2), ("source_name", "<u4", 2)])
+assert TENSOR_ENTRY.itemsize == 140
+
+
+def tensor_table(image: np.ndarray) -> np.ndarray:
+    """Tensor directory of a .uocr image in memory (uint8 array), the entry
+    layout of include/uocr_format.h (uocr_format.h:268-299 in the reference)."""
+    hdr = image[:112]
+    n_sec = int(hdr[24:28].view("<u4")[0])
+    sec_off = int(hdr[40:48].view("<u8")[0])
+    secs = image[sec_off:sec_off + 32 * n_sec].view(np.dtype([("type", "<u4"), ("flags", "<u4"), ("offset", "<u8"),
+                                                                ("size", "<u8"), ("alignment", "<u8")]))
+    d = secs[secs["type"] == 2][0]
+    count = int(image[d["offset"] + 12:d["offset"] + 16].view("<u4")[0])
+    start = int(d["offset"]) + 16
+    return image[start:start + 140 * count].view(TENSOR_ENTRY)
+
+
+def f16_tensor(image: np.ndarray, entry, rows: int, cols: int) -> np.ndarray:
+    """fp16 payload of a tensor entry as a [rows][cols] float16 view."""
+    off, size = int(entry["payload_offset"]), int(entry["payload_size"])
+    assert size == rows * cols * 2, (int(entry["id"]), size, rows, cols)
+    return image[off:off + size].view(np.float16).reshape(rows, cols)
+
+
 def synth_model(qprofile: int, seed: int) -> SynthModel:
     return SynthModel(qprofile, seed)
 
