@@ -28,6 +28,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <vector>
 
 #include "uocr_kernels.h"
 
@@ -39,6 +40,7 @@ namespace {
 struct dev_layer {
     uocr_qmat q, k, v, o, gate, up, down, sgate, sup, sdown;
     const uint16_t *in_norm, *post_norm, *router;
+    const float *rfold; /* [1280][64] router * post_norm, or NULL (router kernel) */
     uocr_expert_slab slab;
 };
 
@@ -78,6 +80,7 @@ struct uocr_hip_ctx {
     uint64_t kv_bytes, scratch_bytes, moe_bytes, logits_bytes, prompt_bytes, prefill_bytes;
     uint16_t *kc, *vc, *h, *a, *q, *ctxv, *mid, *smid, *prompt;
     float *attn_part, *logits, *route_w;
+    int64_t *racc; /* un-normalised router logits, fixed point (k_attn_out -> k_moe_gate_up) */
     uint32_t *route_ids;
     /* MFMA prefill scratch, sized for prompt_cap rows */
     uint16_t *p_xn, *p_qkv, *p_q, *p_ctx, *p_a, *p_mid, *p_smid, *p_sout, *p_rmid;
@@ -223,6 +226,40 @@ static int upload(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor &t, uocr
     return 1;
 }
 
+/* The router folded into the post-attention norm weight, transposed:
+ * fold[i][e] = R[e][i] * nw[i] (exact in fp32: a product of two fp16
+ * values).  The O-projection kernel accumulates z[e] = sum_i fold[i][e] *
+ * a[i] in int64 fixed point (2^32 units), so the fold is used only when no
+ * sum can leave that range: max_e sum_i |fold[i][e]| * 65504 (the largest
+ * fp16 magnitude of a[i]) < 2^31.  Otherwise *out stays NULL and the layer
+ * keeps the separate router kernel. */
+static int upload_router_fold(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor &R, const uocr_bound_tensor &nw,
+                              const float **out, char *err, size_t err_size) {
+    constexpr uint32_t E = UOCR_ROUTED_EXPERTS;
+    *out = nullptr;
+    const uint64_t bytes = (uint64_t)H_SIZE * E * 4u;
+    const uint64_t off = p.take(bytes);
+    if (R.qtype != UOCR_QT_F16 || R.w_bytes < (uint64_t)E * H_SIZE * 2u || nw.w_bytes < (uint64_t)H_SIZE * 2u) {
+        return 1;
+    }
+    const _Float16 *r = (const _Float16 *)R.w, *w = (const _Float16 *)nw.w;
+    std::vector<float> fold((size_t)H_SIZE * E);
+    double worst = 0.0;
+    for (uint32_t e = 0; e < E; ++e) {
+        double tot = 0.0;
+        for (uint32_t i = 0; i < H_SIZE; ++i) {
+            const float f = (float)r[(size_t)e * H_SIZE + i] * (float)w[i];
+            fold[(size_t)i * E + e] = f;
+            tot += fabs((double)f);
+        }
+        worst = tot > worst ? tot : worst;
+    }
+    if (!(worst * 65504.0 < 2147483648.0)) return 1;
+    HIPCHK(hipMemcpy(ctx->warena + off, fold.data(), bytes, hipMemcpyHostToDevice), "router fold upload");
+    *out = (const float *)(ctx->warena + off);
+    return 1;
+}
+
 /* Uploads one projection of all 64 experts into an evenly strided slab. */
 static int upload_slab(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor *ex, uocr_qmat *out, uint64_t *w_stride,
                        uint64_t *s_stride, char *err, size_t err_size) {
@@ -264,6 +301,7 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
         } else {
             total += tensor_bytes(L.router) + tensor_bytes(L.sgate) + tensor_bytes(L.sup) + tensor_bytes(L.sdown);
             total += UOCR_ROUTED_EXPERTS * (tensor_bytes(L.egate[0]) + tensor_bytes(L.eup[0]) + tensor_bytes(L.edown[0]));
+            total += align256((uint64_t)H_SIZE * UOCR_ROUTED_EXPERTS * 4u);
         }
     }
     HIPCHK(hipMalloc((void **)&ctx->warena, total), "weight arena allocation");
@@ -300,6 +338,7 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
             return 0;
         }
         D.router = (const uint16_t *)r.w;
+        if (!upload_router_fold(ctx, p, S.router, S.post_norm, &D.rfold, err, err_size)) return 0;
         uocr_expert_slab &sl = D.slab;
         uint64_t ws2, ss2;
         if (!upload_slab(ctx, p, S.egate, &sl.gate, &sl.gu_w_stride, &sl.gu_s_stride, err, err_size) ||
@@ -330,7 +369,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_h = p.take(H_SIZE * 2u), o_a = p.take(H_SIZE * 2u), o_q = p.take(H_SIZE * 2u), o_c = p.take(H_SIZE * 2u);
     const uint64_t o_state = p.take(sizeof(uocr_step_state));
     const uint64_t o_apart = p.take(UOCR_ATTN_PARTIAL_FLOATS * 4u), o_logits = p.take(64u * 4u);
-    const uint64_t o_rids = p.take(64u), o_rwts = p.take(64u);
+    const uint64_t o_rids = p.take(64u), o_rwts = p.take(64u), o_racc = p.take(UOCR_ROUTER_ACC_WORDS * 8u);
     const uint64_t scratch_end = p.off;
     const uint64_t o_mid = p.take(UOCR_DENSE_LAYER0_INTERMEDIATE * 2u), o_smid = p.take(UOCR_MOE_SHARED_INTERMEDIATE * 2u);
     const uint64_t moe_end = p.off;
@@ -367,6 +406,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->logits = (float *)(b + o_logits);
     ctx->route_ids = (uint32_t *)(b + o_rids);
     ctx->route_w = (float *)(b + o_rwts);
+    ctx->racc = (int64_t *)(b + o_racc);
     ctx->mid = (uint16_t *)(b + o_mid);
     ctx->smid = (uint16_t *)(b + o_smid);
     ctx->lm_part = (uint32_t *)(b + o_lpart);
@@ -438,14 +478,16 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c) {
         const dev_layer &L = c->L[l];
         uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
         ENQ(uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->state, c->q, kc, vc, c->cache_cap));
-        ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part));
-        ENQ(uocr_launch_attn_out(s, L.o, c->attn_part, c->h, c->a, nullptr));
+        ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part, c->racc));
+        ENQ(uocr_launch_attn_out(s, L.o, c->attn_part, c->h, c->a, nullptr, L.rfold, c->racc));
         if (l == 0u) {
             ENQ(uocr_launch_swiglu(s, L.gate, L.up, UOCR_DENSE_LAYER0_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->mid));
             ENQ(uocr_launch_gemv(s, L.down, H_SIZE, UOCR_DENSE_LAYER0_INTERMEDIATE, c->mid, nullptr, c->a, c->h));
         } else {
-            ENQ(uocr_launch_router_logits(s, L.router, c->a, L.post_norm, c->logits));
-            ENQ(uocr_launch_moe_gate_up(s, &L.slab, L.sgate, L.sup, c->logits, 0, c->a, L.post_norm, c->mid, c->smid,
+            /* with the fold, attn_out has produced the un-normalised logits */
+            if (L.rfold == nullptr) ENQ(uocr_launch_router_logits(s, L.router, c->a, L.post_norm, c->logits));
+            ENQ(uocr_launch_moe_gate_up(s, &L.slab, L.sgate, L.sup, L.rfold == nullptr ? c->logits : nullptr,
+                                        L.rfold == nullptr ? nullptr : c->racc, 0, c->a, L.post_norm, c->mid, c->smid,
                                         c->route_ids, c->route_w));
             ENQ(uocr_launch_moe_down(s, &L.slab, c->route_ids, c->route_w, c->mid, L.sdown, c->smid, c->a, c->h));
         }

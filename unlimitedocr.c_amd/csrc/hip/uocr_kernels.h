@@ -29,6 +29,9 @@
 #define UOCR_K_MAX_K 6848          /* largest GEMV reduction length */
 #define UOCR_K_ATTN_SPLITS 16      /* split-K blocks per head in decode attention */
 #define UOCR_K_LM_BLOCKS 1024      /* upper bound on LM-head argmax partial blocks */
+#define UOCR_K_ROUTER_FIX_SHIFT 32 /* router fold accumulator: round(z * 2^32) in int64 */
+#define UOCR_K_ROUTER_ACC_COPIES 4 /* accumulator copies (block b adds into copy b % 4) */
+#define UOCR_ROUTER_ACC_WORDS (UOCR_K_ROUTER_ACC_COPIES * UOCR_K_EXPERTS) /* int64 words */
 
 /* Per-step decode state kept in device memory so one captured graph can be
  * replayed for every token.  Positions follow uocr_metal.m:14239 and the ring
@@ -84,14 +87,21 @@ hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_q
                                 uint16_t *vcache, uint32_t cache_capacity);
 /* Split-K decode attention over the live slots [0, state->attn_len) of one
  * layer's caches (UOCR_K_ATTN_SPLITS blocks per head, slots partitioned by
- * cache_capacity): writes UOCR_ATTN_PARTIAL_FLOATS of per-split partials. */
+ * cache_capacity): writes UOCR_ATTN_PARTIAL_FLOATS of per-split partials.
+ * router_acc (may be NULL) is cleared for the following attn_out. */
 hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
-                                 uint32_t cache_capacity, const uocr_step_state *state, float *partials);
+                                 uint32_t cache_capacity, const uocr_step_state *state, float *partials,
+                                 int64_t *router_acc);
 /* O projection with the attention merge in its prologue:
  * out = f16(O . ctx + res), ctx = f16(merge(partials)); ctx_out (may be
- * NULL) receives ctx. */
+ * NULL) receives ctx.  With router_fold (fp32 [1280][64], entry [i][e] =
+ * R[e][i] * post_norm[i]) each block also adds its rows' share of the
+ * un-normalised router logits z[e] = sum_i fold[i][e] * out[i] into
+ * router_acc (UOCR_ROUTER_ACC_WORDS, cleared beforehand) as fixed point,
+ * round(x * 2^32), so the sum is independent of the order of the
+ * additions. */
 hipError_t uocr_launch_attn_out(hipStream_t st, uocr_qmat O, const float *partials, const uint16_t *res,
-                                uint16_t *out, uint16_t *ctx_out);
+                                uint16_t *out, uint16_t *ctx_out, const float *router_fold, int64_t *router_acc);
 /* The merge alone: ctx = f16(merge(partials)). */
 hipError_t uocr_launch_attn_merge(hipStream_t st, const float *partials, uint16_t *ctx);
 /* Router logits: logits[e] = R_e . rmsnorm(x) (fp16 R [64][1280], fp32 dot),
@@ -106,10 +116,12 @@ hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, const uint16_t 
  * wavefront) and of the shared experts in one launch:
  *   mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = rank-r expert,
  *   smid[c]        = f16(silu(SG[c].xin) * (SU[c].xin)),  c < 1792,
- * xin = x or rmsnorm(x, nw); ids/weights receive the selection. */
+ * xin = x or rmsnorm(x, nw); ids/weights receive the selection.  Exactly
+ * one of logits (the router logits) and router_acc (the fixed-point
+ * un-normalised logits of attn_out; logits = z * inv_rms(x)) is set. */
 hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG, uocr_qmat SU,
-                                   const float *logits, int norm_topk, const uint16_t *x, const uint16_t *nw,
-                                   uint16_t *mid, uint16_t *smid, uint32_t *ids, float *weights);
+                                   const float *logits, const int64_t *router_acc, int norm_topk, const uint16_t *x,
+                                   const uint16_t *nw, uint16_t *mid, uint16_t *smid, uint32_t *ids, float *weights);
 /* Routed down + weighted combine + shared down + residual:
  * out[c] = f16(sum_r w_r * D_e[c].mid_r + f16(SD[c].smid) + res[c]). */
 hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,

@@ -143,7 +143,8 @@ __device__ __forceinline__ void hold(float2 &v) {
  * issued, applies RMSNorm (eps 1e-6) when nw is set,
  *   xs[i] = f16(x[i] * inv_rms * nw[i])   (norm.metal:12-40 arithmetic:
  *   fp32 sum of squares, one rounding per element),
- * writes xs to LDS and synchronises the block.  KMAX and NT (threads) are
+ * writes xs to LDS and synchronises the block, and returns inv_rms (1 without
+ * nw).  KMAX and NT (threads) are
  * compile-time; the runtime K (multiple of 8, <= KMAX) masks the pieces. */
 template <int KMAX, int NT>
 struct XStage {
@@ -166,7 +167,7 @@ __device__ __forceinline__ void stage_load(XStage<KMAX, NT> &sx, const h16 *x, c
 }
 
 template <int KMAX, int NT>
-__device__ __forceinline__ void stage_store(XStage<KMAX, NT> &sx, h16 *xs, const h16 *nw, int K, float *red) {
+__device__ __forceinline__ float stage_store(XStage<KMAX, NT> &sx, h16 *xs, const h16 *nw, int K, float *red) {
 #pragma unroll
     for (int p = 0; p < XStage<KMAX, NT>::PER; ++p) {
         hold(sx.x[p]);
@@ -176,6 +177,7 @@ __device__ __forceinline__ void stage_store(XStage<KMAX, NT> &sx, h16 *xs, const
         uint4 u;
         h16 h[8];
     };
+    float inv = 1.0f;
     if (nw != nullptr) {
         float ss = 0.0f;
 #pragma unroll
@@ -188,7 +190,7 @@ __device__ __forceinline__ void stage_store(XStage<KMAX, NT> &sx, h16 *xs, const
             }
         }
         ss = block_sum(ss, red);
-        const float inv = 1.0f / sqrtf(ss / (float)K + 1.0e-6f);
+        inv = 1.0f / sqrtf(ss / (float)K + 1.0e-6f);
 #pragma unroll
         for (int p = 0; p < XStage<KMAX, NT>::PER; ++p) {
             const int i = threadIdx.x + p * NT;
@@ -209,6 +211,7 @@ __device__ __forceinline__ void stage_store(XStage<KMAX, NT> &sx, h16 *xs, const
         }
     }
     __syncthreads();
+    return inv;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -384,29 +387,68 @@ __device__ __forceinline__ u32 wave_max_u32(u32 v) {
     return max(max(a, b), max(c, d));
 }
 
-/* Greedy top-6 over 64 router logits by one wavefront (one expert per lane):
- * max-subtracted softmax, then 6 rounds of "largest probability, lowest id
- * among equals" (uocr_cpu_ref.c:443-463, moe.metal:12-18): a DPP wave max
- * of the probability bits (non-negative floats order as unsigned integers)
- * and a ballot of the lanes holding it.  Raw probabilities unless
- * norm_topk.  The results are wave-uniform. */
-__device__ __forceinline__ void topk6(float lg, int norm_topk, u32 (&sid)[UOCR_K_TOPK], float (&sw)[UOCR_K_TOPK]) {
+/* Six rounds of "largest key, lowest lane among equals" over one wavefront
+ * (a DPP wave max of the key and a ballot of the lanes holding it); sid gets
+ * the lanes, best the keys.  Wave-uniform results. */
+__device__ __forceinline__ void top6_keys(u32 key, u32 (&sid)[UOCR_K_TOPK], u32 (&best)[UOCR_K_TOPK]) {
     const u32 lane = threadIdx.x & 63u;
+    bool live = true;
+#pragma unroll
+    for (int r = 0; r < UOCR_K_TOPK; ++r) {
+        best[r] = wave_max_u32(live ? key : 0u);
+        const unsigned long long m = __ballot(live && key == best[r]);
+        const u32 l = (u32)__builtin_ctzll(m);
+        sid[r] = l;
+        live = live && lane != l;
+    }
+}
+
+/* Max-subtracted softmax of the 64 router logits (one per lane). */
+__device__ __forceinline__ float router_prob(float lg) {
     const float mx = wave_max_dpp(lg);
     const float pe = expf(lg - mx);
-    const float prob = pe / wave_sum(pe);
-    u32 key = __float_as_uint(prob);
-    bool live = true;
+    return pe / wave_sum(pe);
+}
+
+/* Greedy top-6 over 64 router logits by one wavefront (one expert per lane):
+ * max-subtracted softmax, then 6 rounds of "largest probability, lowest id
+ * among equals" (uocr_cpu_ref.c:443-463, moe.metal:12-18); probabilities
+ * are non-negative, so their bits order as unsigned integers.  Raw
+ * probabilities unless norm_topk.  The results are wave-uniform. */
+__device__ __forceinline__ void topk6(float lg, int norm_topk, u32 (&sid)[UOCR_K_TOPK], float (&sw)[UOCR_K_TOPK]) {
+    u32 best[UOCR_K_TOPK];
+    top6_keys(__float_as_uint(router_prob(lg)), sid, best);
     float tot = 0.0f;
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
-        const u32 best = wave_max_u32(live ? key : 0u);
-        const unsigned long long m = __ballot(live && key == best);
-        const u32 l = (u32)__builtin_ctzll(m);
-        sid[r] = l;
-        sw[r] = __uint_as_float(best);
+        sw[r] = __uint_as_float(best[r]);
         tot += sw[r];
-        live = live && lane != l;
+    }
+    if (norm_topk) {
+#pragma unroll
+        for (int r = 0; r < UOCR_K_TOPK; ++r) sw[r] /= tot;
+    }
+}
+
+/* Top-6 ids from un-normalised logits z = logits / inv_rms: softmax is
+ * monotone and inv_rms > 0, so z orders the experts as the probabilities
+ * do.  The key maps floats to unsigned integers in the same order. */
+__device__ __forceinline__ void topk6_ids(float z, u32 (&sid)[UOCR_K_TOPK]) {
+    const u32 b = __float_as_uint(z);
+    u32 best[UOCR_K_TOPK];
+    top6_keys((b & 0x80000000u) ? ~b : (b | 0x80000000u), sid, best);
+}
+
+/* Probabilities of the selected experts sid from the logits (one per lane),
+ * with topk6's arithmetic. */
+__device__ __forceinline__ void topk6_weights(float lg, int norm_topk, const u32 (&sid)[UOCR_K_TOPK],
+                                              float (&sw)[UOCR_K_TOPK]) {
+    const float prob = router_prob(lg);
+    float tot = 0.0f;
+#pragma unroll
+    for (int r = 0; r < UOCR_K_TOPK; ++r) {
+        sw[r] = lane_f(prob, (int)sid[r]);
+        tot += sw[r];
     }
     if (norm_topk) {
 #pragma unroll
@@ -624,8 +666,12 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
  *   acc at part[(h*S + s)*128 + d], (max, sum) at part[H*S*128 + (h*S + s)*2]. */
 __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, const h16 *__restrict__ kc,
                                                      const h16 *__restrict__ vc, u32 cap,
-                                                     const uocr_step_state *__restrict__ st, float *__restrict__ part) {
+                                                     const uocr_step_state *__restrict__ st, float *__restrict__ part,
+                                                     long long *__restrict__ racc) {
     constexpr int S = UOCR_K_ATTN_SPLITS;
+    if (racc != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
+        for (int i = threadIdx.x; i < UOCR_ROUTER_ACC_WORDS; i += BLOCK) racc[i] = 0;
+    }
     __shared__ float sm[16], sl[16];
     __shared__ float sacc[16][UOCR_K_HEAD_DIM];
     const int h = blockIdx.y, s = blockIdx.x;
@@ -795,11 +841,17 @@ __device__ __forceinline__ void merge_finish(MergeLoads &m, h16 *ctx, float *wk)
 /* O projection with the attention merge in its prologue:
  * out[r] = f16(O_r . ctx + res[r]), ctx = merge of the partials (fp16, the
  * reference's attention-output rounding point).  Block 0 also stores ctx
- * when ctx_out is set.  One row per lane group. */
-template <int QT>
+ * when ctx_out is set.  One row per lane group.
+ * FOLD: the block also adds z[e] += sum over its rows i of fold[i][e] *
+ * out[i] to racc[e] as round(z * 2^32) (integer adds: the total does not
+ * depend on the order in which blocks arrive).  With fold = R * post_norm,
+ * z * inv_rms(out) are the router logits R . rmsnorm(out) of the MoE
+ * (moe.metal:53-189), less the fp16 rounding of the normalised vector. */
+template <int QT, bool FOLD>
 __global__ __launch_bounds__(BLOCK) void k_attn_out(uocr_qmat O, const float *__restrict__ part,
                                                     const h16 *__restrict__ res, h16 *__restrict__ out,
-                                                    h16 *__restrict__ ctx_out) {
+                                                    h16 *__restrict__ ctx_out, const float *__restrict__ fold,
+                                                    long long *__restrict__ racc) {
     constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
     constexpr u32 rb = 16u * C, G = K / 64u;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
@@ -811,12 +863,41 @@ __global__ __launch_bounds__(BLOCK) void k_attn_out(uocr_qmat O, const float *__
     merge_load(ml, part);
     RowFrag<J> f;
     frag_load<QT, LPR, J>(f, (const uint8_t *)O.w + (size_t)rr * rb, (const h16 *)O.s + (size_t)rr * G, C, sub);
+    const float rv = (float)res[rr];
+    const u32 row0 = (blockIdx.x * NWAVE + wave) * R;
+    float fw[FOLD ? R : 1];
+    if (FOLD) {
+#pragma unroll
+        for (u32 g = 0; g < R; ++g) fw[g] = fold[(size_t)min(row0 + g, K - 1u) * UOCR_K_EXPERTS + lane];
+    }
     merge_finish(ml, xs, wk);
     if (ctx_out != nullptr && blockIdx.x == 0) {
         for (u32 i = threadIdx.x; i < K / 8u; i += blockDim.x) ((uint4 *)ctx_out)[i] = ((const uint4 *)xs)[i];
     }
     const float d = group_sum<LPR>(frag_dot<QT, LPR, J>(f, xs, C, sub));
-    if (r < K && sub == 0u) out[r] = (h16)(d + (float)res[r]);
+    const h16 o = (h16)(d + rv);
+    if (r < K && sub == 0u) out[r] = o;
+    if (FOLD) {
+        __shared__ float zp[NWAVE][UOCR_K_EXPERTS];
+        float z = 0.0f;
+#pragma unroll
+        for (u32 g = 0; g < R; ++g) {
+            const float av = lane_f((float)o, (int)(g * LPR));
+            z = row0 + g < K ? fmaf(fw[g], av, z) : z;
+        }
+        zp[wave][lane] = z;
+        __syncthreads();
+        if (wave == 0u) {
+            float t = zp[0][lane];
+#pragma unroll
+            for (u32 w = 1; w < NWAVE; ++w) t += zp[w][lane];
+            const long long q = __float2ll_rn(t * (float)(1ull << UOCR_K_ROUTER_FIX_SHIFT));
+            /* blocks spread over the accumulator copies: fewer same-line
+             * atomics queue at the memory side */
+            atomicAdd((unsigned long long *)racc + (blockIdx.x % UOCR_K_ROUTER_ACC_COPIES) * UOCR_K_EXPERTS + lane,
+                      (unsigned long long)q);
+        }
+    }
 }
 
 /* Merge alone (operator API): ctx = merge of the partials. */
@@ -874,10 +955,15 @@ __global__ __launch_bounds__(64) void k_router_topk(const float *__restrict__ lo
  * group: mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = the
  * rank-r expert; block 0 publishes ids/weights for the down kernel.
  * Blocks [nb_routed, ...): smid[c] = f16(silu(SG[c].xin) * (SU[c].xin)),
- * c < 1792.  xin = x or rmsnorm(x, nw). */
-template <int QT, int QS>
+ * c < 1792.  xin = x or rmsnorm(x, nw).
+ * FOLD: racc holds the un-normalised logits z of k_attn_out (fixed point,
+ * summed over the accumulator copies);
+ * the top-6 is taken on z (same order), and block 0 turns z * inv_rms(x)
+ * into the probabilities once x is staged. */
+template <int QT, int QS, bool FOLD>
 __global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl, uocr_qmat SG, uocr_qmat SU,
-                                                             const float *__restrict__ logits, int norm_topk,
+                                                             const float *__restrict__ logits,
+                                                             const long long *__restrict__ racc, int norm_topk,
                                                              const h16 *__restrict__ x, const h16 *__restrict__ nw,
                                                              h16 *__restrict__ mid, h16 *__restrict__ smid,
                                                              u32 *__restrict__ ids_out, float *__restrict__ w_out,
@@ -904,13 +990,28 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl
     }
     constexpr u32 C = chunks_per_row<QT>(K), LPR = lpr_lat(C), J = j_lat(C), R = 64u / LPR, rb = 16u * C;
     const u32 sub = lane % LPR, grp = lane / LPR;
-    const float lg = logits[lane];
+    float lg;
+    if (FOLD) {
+        long long zq[UOCR_K_ROUTER_ACC_COPIES];
+#pragma unroll
+        for (int k = 0; k < UOCR_K_ROUTER_ACC_COPIES; ++k) zq[k] = racc[k * UOCR_K_EXPERTS + lane];
+        long long zt = 0;
+#pragma unroll
+        for (int k = 0; k < UOCR_K_ROUTER_ACC_COPIES; ++k) zt += zq[k];
+        lg = (float)zt * (1.0f / (float)(1ull << UOCR_K_ROUTER_FIX_SHIFT));
+    } else {
+        lg = logits[lane];
+    }
     XStage<UOCR_K_HIDDEN, SMALL_BLOCK> sx;
     stage_load(sx, x, nw, UOCR_K_HIDDEN);
     u32 sid[UOCR_K_TOPK];
     float sw[UOCR_K_TOPK];
-    topk6(lg, norm_topk, sid, sw);
-    if (blockIdx.x == 0u && wave == 0u && lane < UOCR_K_TOPK) {
+    if (FOLD) {
+        topk6_ids(lg, sid);
+    } else {
+        topk6(lg, norm_topk, sid, sw);
+    }
+    if (!FOLD && blockIdx.x == 0u && wave == 0u && lane < UOCR_K_TOPK) {
 #pragma unroll
         for (int r = 0; r < UOCR_K_TOPK; ++r) {
             if (lane == (u32)r) {
@@ -930,7 +1031,20 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl
                           (const h16 *)sl.gate.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
     frag_load<QT, LPR, J>(fu, (const uint8_t *)sl.up.w + e * sl.gu_w_stride + (size_t)col * rb,
                           (const h16 *)sl.up.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
-    stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
+    const float inv = stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
+    if (FOLD && blockIdx.x == 0u && wave == 0u) {
+        /* logits = z * inv_rms(x): the selection's probabilities */
+        topk6_weights(lg * inv, norm_topk, sid, sw);
+        if (lane < UOCR_K_TOPK) {
+#pragma unroll
+            for (int k = 0; k < UOCR_K_TOPK; ++k) {
+                if (lane == (u32)k) {
+                    ids_out[k] = sid[k];
+                    w_out[k] = sw[k];
+                }
+            }
+        }
+    }
     const float dg = group_sum<LPR>(frag_dot<QT, LPR, J>(fg, xs, C, sub));
     const float du = group_sum<LPR>(frag_dot<QT, LPR, J>(fu, xs, C, sub));
     if (r < ROWS && sub == 0u) mid[r] = (h16)(silu_f(dg) * du);
@@ -1314,28 +1428,39 @@ extern "C" hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qma
 
 extern "C" hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache,
                                             const uint16_t *vcache, uint32_t cache_capacity,
-                                            const uocr_step_state *state, float *partials) {
+                                            const uocr_step_state *state, float *partials, int64_t *router_acc) {
     if (q == nullptr || kcache == nullptr || vcache == nullptr || cache_capacity == 0u || state == nullptr ||
         partials == nullptr) {
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(k_attention, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(BLOCK), 0, st, (const h16 *)q,
-                       (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials);
+                       (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials,
+                       (long long *)router_acc);
     return hipGetLastError();
 }
 
 template <int QT>
 static void launch_attn_out_qt(hipStream_t st, uocr_qmat O, const float *partials, const uint16_t *res, uint16_t *out,
-                               uint16_t *ctx_out) {
+                               uint16_t *ctx_out, const float *fold, int64_t *racc) {
     constexpr u32 rpb = NWAVE * (64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN)));
-    hipLaunchKernelGGL((k_attn_out<QT>), dim3((UOCR_K_HIDDEN + rpb - 1u) / rpb), dim3(BLOCK), 0, st, O, partials,
-                       (const h16 *)res, (h16 *)out, (h16 *)ctx_out);
+    const dim3 grid((UOCR_K_HIDDEN + rpb - 1u) / rpb);
+    if (fold != nullptr) {
+        hipLaunchKernelGGL((k_attn_out<QT, true>), grid, dim3(BLOCK), 0, st, O, partials, (const h16 *)res,
+                           (h16 *)out, (h16 *)ctx_out, fold, (long long *)racc);
+    } else {
+        hipLaunchKernelGGL((k_attn_out<QT, false>), grid, dim3(BLOCK), 0, st, O, partials, (const h16 *)res,
+                           (h16 *)out, (h16 *)ctx_out, nullptr, nullptr);
+    }
 }
 
 extern "C" hipError_t uocr_launch_attn_out(hipStream_t st, uocr_qmat O, const float *partials, const uint16_t *res,
-                                           uint16_t *out, uint16_t *ctx_out) {
-    if (!mat_ok(O) || partials == nullptr || res == nullptr || out == nullptr) return hipErrorInvalidValue;
-    DISPATCH_QT(O.qtype, launch_attn_out_qt, st, O, partials, res, out, ctx_out);
+                                           uint16_t *out, uint16_t *ctx_out, const float *router_fold,
+                                           int64_t *router_acc) {
+    if (!mat_ok(O) || partials == nullptr || res == nullptr || out == nullptr ||
+        (router_fold != nullptr && router_acc == nullptr)) {
+        return hipErrorInvalidValue;
+    }
+    DISPATCH_QT(O.qtype, launch_attn_out_qt, st, O, partials, res, out, ctx_out, router_fold, router_acc);
     return hipGetLastError();
 }
 
@@ -1364,38 +1489,47 @@ extern "C" hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, cons
 
 template <int QT, int QS>
 static void launch_moe_gu_qs(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG, uocr_qmat SU,
-                             const float *logits, int norm_topk, const uint16_t *x, const uint16_t *nw, uint16_t *mid,
-                             uint16_t *smid, u32 *ids, float *wts) {
+                             const float *logits, const int64_t *racc, int norm_topk, const uint16_t *x,
+                             const uint16_t *nw, uint16_t *mid, uint16_t *smid, u32 *ids, float *wts) {
     constexpr u32 NWV = SMALL_BLOCK / 64u;
     constexpr u32 rpb = NWV * (64u / lpr_lat(chunks_per_row<QT>(UOCR_K_HIDDEN)));
     constexpr u32 rpb_s = NWV * (64u / lpr_lat(chunks_per_row<QS>(UOCR_K_HIDDEN)));
     constexpr u32 nbr = (UOCR_K_TOPK * 896u + rpb - 1u) / rpb, nbs = (1792u + rpb_s - 1u) / rpb_s;
-    hipLaunchKernelGGL((k_moe_gate_up<QT, QS>), dim3(nbr + nbs), dim3(SMALL_BLOCK), 0, st, *slab, SG, SU, logits,
-                       norm_topk, (const h16 *)x, (const h16 *)nw, (h16 *)mid, (h16 *)smid, ids, wts, nbr);
+    if (racc != nullptr) {
+        hipLaunchKernelGGL((k_moe_gate_up<QT, QS, true>), dim3(nbr + nbs), dim3(SMALL_BLOCK), 0, st, *slab, SG, SU,
+                           nullptr, (const long long *)racc, norm_topk, (const h16 *)x, (const h16 *)nw, (h16 *)mid,
+                           (h16 *)smid, ids, wts, nbr);
+    } else {
+        hipLaunchKernelGGL((k_moe_gate_up<QT, QS, false>), dim3(nbr + nbs), dim3(SMALL_BLOCK), 0, st, *slab, SG, SU,
+                           logits, nullptr, norm_topk, (const h16 *)x, (const h16 *)nw, (h16 *)mid, (h16 *)smid, ids,
+                           wts, nbr);
+    }
 }
 
 template <int QT>
 static void launch_moe_gu_qt(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG, uocr_qmat SU,
-                             const float *logits, int norm_topk, const uint16_t *x, const uint16_t *nw, uint16_t *mid,
-                             uint16_t *smid, u32 *ids, float *wts) {
+                             const float *logits, const int64_t *racc, int norm_topk, const uint16_t *x,
+                             const uint16_t *nw, uint16_t *mid, uint16_t *smid, u32 *ids, float *wts) {
+#define GU(QS) launch_moe_gu_qs<QT, QS>(st, slab, SG, SU, logits, racc, norm_topk, x, nw, mid, smid, ids, wts)
     switch (SG.qtype) {
-        case UOCR_QT_F16: launch_moe_gu_qs<QT, 1>(st, slab, SG, SU, logits, norm_topk, x, nw, mid, smid, ids, wts); break;
-        case UOCR_QT_Q8: launch_moe_gu_qs<QT, 3>(st, slab, SG, SU, logits, norm_topk, x, nw, mid, smid, ids, wts); break;
-        default: launch_moe_gu_qs<QT, 4>(st, slab, SG, SU, logits, norm_topk, x, nw, mid, smid, ids, wts); break;
+        case UOCR_QT_F16: GU(1); break;
+        case UOCR_QT_Q8: GU(3); break;
+        default: GU(4); break;
     }
+#undef GU
 }
 
 extern "C" hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG,
-                                              uocr_qmat SU, const float *logits, int norm_topk, const uint16_t *x,
-                                              const uint16_t *nw, uint16_t *mid, uint16_t *smid, uint32_t *ids,
-                                              float *weights) {
+                                              uocr_qmat SU, const float *logits, const int64_t *router_acc,
+                                              int norm_topk, const uint16_t *x, const uint16_t *nw, uint16_t *mid,
+                                              uint16_t *smid, uint32_t *ids, float *weights) {
     if (slab == nullptr || !mat_ok(slab->gate) || !mat_ok(slab->up) || slab->gate.qtype != slab->up.qtype ||
-        !mat_ok(SG) || !mat_ok(SU) || SG.qtype != SU.qtype || logits == nullptr || x == nullptr || mid == nullptr ||
-        smid == nullptr || ids == nullptr || weights == nullptr) {
+        !mat_ok(SG) || !mat_ok(SU) || SG.qtype != SU.qtype || (logits == nullptr) == (router_acc == nullptr) ||
+        x == nullptr || mid == nullptr || smid == nullptr || ids == nullptr || weights == nullptr) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(slab->gate.qtype, launch_moe_gu_qt, st, slab, SG, SU, logits, norm_topk, x, nw, mid, smid, ids,
-                weights);
+    DISPATCH_QT(slab->gate.qtype, launch_moe_gu_qt, st, slab, SG, SU, logits, router_acc, norm_topk, x, nw, mid, smid,
+                ids, weights);
     return hipGetLastError();
 }
 

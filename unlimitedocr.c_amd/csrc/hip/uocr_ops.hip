@@ -163,7 +163,7 @@ extern "C" int uocr_op_moe_ffn(const uocr_op_moe_weights *m, const void *x, cons
     int r = hip_status(uocr_launch_router_logits(st, (const uint16_t *)m->router, xx, nw, logits), "moe router");
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_moe_gate_up(st, &sl, qm(m->shared_qtype, m->sgate_w, m->sgate_s),
-                                               qm(m->shared_qtype, m->sup_w, m->sup_s), logits, norm_topk, xx, nw, mid,
+                                               qm(m->shared_qtype, m->sup_w, m->sup_s), logits, nullptr, norm_topk, xx, nw, mid,
                                                smid, wids, wwts),
                        "moe gate/up");
     }
@@ -203,7 +203,7 @@ extern "C" int uocr_op_attention_decode(const void *q, const void *k_cache, cons
     if (r != UOCR_OK) return r;
     int r2 = hip_status(uocr_launch_attention(st, (const uint16_t *)q, (const uint16_t *)k_cache,
                                               (const uint16_t *)v_cache, cache_capacity,
-                                              ws<uocr_step_state>(workspace, WS_STATE), ws<float>(workspace, WS_APART)),
+                                              ws<uocr_step_state>(workspace, WS_STATE), ws<float>(workspace, WS_APART), nullptr),
                         "attention_decode");
     if (r2 != UOCR_OK) return r2;
     return hip_status(uocr_launch_attn_merge(st, ws<float>(workspace, WS_APART), (uint16_t *)out), "attention merge");
@@ -230,12 +230,12 @@ extern "C" int uocr_op_attention_block(uint32_t qtype, const void *wq, const voi
     }
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_attention(st, qb, (const uint16_t *)k_cache, (const uint16_t *)v_cache,
-                                             cache_capacity, state, ws<float>(workspace, WS_APART)),
+                                             cache_capacity, state, ws<float>(workspace, WS_APART), nullptr),
                        "attention");
     }
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_attn_out(st, qm(qtype, wo, so), ws<float>(workspace, WS_APART),
-                                            (const uint16_t *)hidden, (uint16_t *)out, cb),
+                                            (const uint16_t *)hidden, (uint16_t *)out, cb, nullptr, nullptr),
                        "o_proj");
     }
     return r;
