@@ -81,6 +81,33 @@ def test_graph_and_eager_paths_agree(gpu):
     eng.close()
 
 
+def test_router_fold_matches_router_kernel(gpu, monkeypatch):
+    """The decode loop's folded router (logits accumulated by the O kernel,
+    selection on the un-normalised logits) against the separate router
+    kernel (UOCR_HIP_NO_ROUTER_FOLD=1): while the two id sequences agree,
+    every step's winning score agrees within the fp16 tolerance, and the
+    first disagreement can only be a near-tie."""
+    uocr = gpu
+    m = model(uocr, 3)
+    rng = np.random.default_rng(31)
+    ids, mask, rows = prompt(rng, 20, 8)
+    fold = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=128, max_gen_tokens=40)
+    monkeypatch.setenv("UOCR_HIP_NO_ROUTER_FOLD", "1")
+    plain = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=128, max_gen_tokens=40)
+    monkeypatch.delenv("UOCR_HIP_NO_ROUTER_FOLD")
+    a_ids, a_sc, _, _ = fold.generate_embeddings(ids, mask, rows, 24, flags=uocr.GEN_IGNORE_EOS)
+    b_ids, b_sc, _, _ = plain.generate_embeddings(ids, mask, rows, 24, flags=uocr.GEN_IGNORE_EOS)
+    fold.close()
+    plain.close()
+    steps = 0
+    for x, y, sx, sy in zip(a_ids.tolist(), b_ids.tolist(), a_sc.tolist(), b_sc.tolist()):
+        assert abs(sx - sy) <= 2e-2 + 1e-2 * abs(sy), f"step {steps}: scores {sx} vs {sy}"
+        if x != y:
+            break
+        steps += 1
+    assert steps >= 4
+
+
 def test_ring_window_wrap_matches_oracle(gpu, oracle):
     """More than 128 generated tokens: the KV ring overwrites its oldest slots."""
     uocr = gpu

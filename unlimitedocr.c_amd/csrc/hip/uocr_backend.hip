@@ -290,6 +290,9 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
         ctx->mapped = 0;
         release_graphs(ctx);
     }
+    /* UOCR_HIP_NO_ROUTER_FOLD=1 keeps the separate router kernel in every layer */
+    const char *nf = getenv("UOCR_HIP_NO_ROUTER_FOLD");
+    const bool no_fold = nf != nullptr && atoi(nf) != 0;
     /* size pass */
     uint64_t total = tensor_bytes(b->embed) + tensor_bytes(b->lm_head) + tensor_bytes(b->final_norm);
     for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
@@ -339,6 +342,7 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
         }
         D.router = (const uint16_t *)r.w;
         if (!upload_router_fold(ctx, p, S.router, S.post_norm, &D.rfold, err, err_size)) return 0;
+        if (no_fold) D.rfold = nullptr;
         uocr_expert_slab &sl = D.slab;
         uint64_t ws2, ss2;
         if (!upload_slab(ctx, p, S.egate, &sl.gate, &sl.gu_w_stride, &sl.gu_s_stride, err, err_size) ||
