@@ -27,7 +27,9 @@
 #define UOCR_K_TOPK 6
 #define UOCR_K_RING 128
 #define UOCR_K_MAX_K 6848          /* largest GEMV reduction length */
+#ifndef UOCR_K_ATTN_SPLITS
 #define UOCR_K_ATTN_SPLITS 16      /* split-K blocks per head in decode attention */
+#endif
 #define UOCR_K_LM_BLOCKS 1024      /* upper bound on LM-head argmax partial blocks */
 #define UOCR_K_ROUTER_FIX_SHIFT 32 /* router fold accumulator: round(z * 2^32) in int64 */
 #define UOCR_K_ROUTER_ACC_COPIES 4 /* accumulator copies (block b adds into copy b % 4) */

@@ -648,6 +648,10 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
 /* ------------------------------------------------------------------------ */
 
 #define ATT_UNROLL 5
+/* Threads of an attention block: 16-lane slot groups, 64 groups per head in
+ * all (so the per-wave work does not depend on the split count). */
+constexpr int ATT_THREADS = 64 * 64 / UOCR_K_ATTN_SPLITS;
+constexpr int ATT_GROUPS = ATT_THREADS / 16;
 
 /* Live KV slots of a step are always [0, attn_len): the prompt slots
  * [0, P) plus the ring slots [P, P + live) (before the ring wraps these hold
@@ -662,18 +666,20 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
  * (attention length) arrives; slots >= attn_len are masked afterwards.  A
  * 16-lane group handles one slot (8 dims per lane), ATT_UNROLL slots in
  * flight per group, with an online softmax; the block writes one partial
- * (max, sum, acc[128]) per head:
- *   acc at part[(h*S + s)*128 + d], (max, sum) at part[H*S*128 + (h*S + s)*2]. */
-__global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, const h16 *__restrict__ kc,
+ * (max, sum, acc[128] / sum) per head:
+ *   fp16 acc/sum at ((h16 *)part)[(h*S + s)*128 + d],
+ *   fp32 (max, sum) at part[H*S*128 + (h*S + s)*2]. */
+__global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict__ q, const h16 *__restrict__ kc,
                                                      const h16 *__restrict__ vc, u32 cap,
                                                      const uocr_step_state *__restrict__ st, float *__restrict__ part,
                                                      long long *__restrict__ racc) {
     constexpr int S = UOCR_K_ATTN_SPLITS;
     if (racc != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
-        for (int i = threadIdx.x; i < UOCR_ROUTER_ACC_WORDS; i += BLOCK) racc[i] = 0;
+        for (int i = threadIdx.x; i < UOCR_ROUTER_ACC_WORDS; i += ATT_THREADS) racc[i] = 0;
     }
-    __shared__ float sm[16], sl[16];
-    __shared__ float sacc[16][UOCR_K_HEAD_DIM];
+    constexpr int NW = ATT_THREADS / 64;
+    __shared__ float sm[NW], sl[NW];
+    __shared__ float sacc[NW][UOCR_K_HEAD_DIM];
     const int h = blockIdx.y, s = blockIdx.x;
     const int chunk = ((int)cap + S - 1) / S;
     const int i0 = s * chunk, iend = min((int)cap, i0 + chunk);
@@ -692,7 +698,7 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
     auto load = [&](int ib) {
 #pragma unroll
         for (int u = 0; u < ATT_UNROLL; ++u) {
-            const int t = min(ib + 16 * u, (int)cap - 1);
+            const int t = min(ib + ATT_GROUPS * u, (int)cap - 1);
             kk[u].u = *(const uint4 *)(kh + (size_t)t * 128u);
             vv[u].u = *(const uint4 *)(vh + (size_t)t * 128u);
         }
@@ -717,7 +723,7 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
             float d = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) d = fmaf(qv[j], (float)kk[u].h[j], d);
-            sc[u] = ib + 16 * u < i1 ? row16_sum(d) * scale : -INFINITY;
+            sc[u] = ib + ATT_GROUPS * u < i1 ? row16_sum(d) * scale : -INFINITY;
             mn = fmaxf(mn, sc[u]);
         }
         if (mn != -INFINITY) {
@@ -734,32 +740,51 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
             }
             m = mn;
         }
-        ib += 16 * ATT_UNROLL;
+        ib += ATT_GROUPS * ATT_UNROLL;
         if (ib >= i1) break;
         load(ib);
     }
-    if (p == 0) {
-        sm[gid] = m;
-        sl[gid] = l;
-    }
+    {
+        /* the wave's four slot groups (lanes p, p+16, p+32, p+48 hold the
+         * same dims) merged in registers */
+        float Mw = fmaxf(m, __shfl_xor(m, 16));
+        Mw = fmaxf(Mw, __shfl_xor(Mw, 32));
+        const float f = m == -INFINITY ? 0.0f : expf(m - Mw);
+        l *= f;
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sacc[gid][8 * p + j] = acc[j];
+        for (int j = 0; j < 8; ++j) {
+            acc[j] *= f;
+            acc[j] += __shfl_xor(acc[j], 16);
+            acc[j] += __shfl_xor(acc[j], 32);
+        }
+        if (gq == 0) {
+            if (p == 0) {
+                sm[wave] = Mw;
+                sl[wave] = l;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sacc[wave][8 * p + j] = acc[j];
+        }
+    }
     __syncthreads();
     if (threadIdx.x < UOCR_K_HEAD_DIM) {
         const int d = threadIdx.x;
         float M = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) M = fmaxf(M, sm[k]);
+        for (int k = 0; k < NW; ++k) M = fmaxf(M, sm[k]);
         float Ls = 0.0f, A = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
+            for (int k = 0; k < NW; ++k) {
                 const float f = expf(sm[k] - M);
                 Ls = fmaf(sl[k], f, Ls);
                 A = fmaf(sacc[k][d], f, A);
             }
         }
-        part[(size_t)(h * S + s) * UOCR_K_HEAD_DIM + d] = A;
+        /* normalised accumulator in fp16; (max, sum) in fp32 */
+        ((h16 *)part)[(size_t)(h * S + s) * UOCR_K_HEAD_DIM + d] = (h16)(Ls > 0.0f ? A / Ls : 0.0f);
         if (d == 0) {
             float *ml = part + (size_t)UOCR_K_HEADS * S * UOCR_K_HEAD_DIM + (size_t)(h * S + s) * 2u;
             ml[0] = M;
@@ -769,71 +794,64 @@ __global__ __launch_bounds__(BLOCK) void k_attention(const h16 *__restrict__ q, 
 }
 
 /* Log-sum-exp merge of the S attention partials into fp16 ctx[1280] in LDS
- * (all threads of a BLOCK-thread block).  Threads t < H*S turn the (max,
- * sum) pairs into per-split weights exp(M_k - M_h) / sum_k' L_k' exp(M_k' -
- * M_h) in LDS; each thread then owns 4-dim quads of ctx and sums their S
- * split accumulators (loads issued by merge_load, before the caller's
- * weight loads). */
+ * (all threads of a BLOCK-thread block).  Split k of head h left its
+ * normalised accumulator accn_k = acc_k / L_k in fp16 (a weighted mean of V
+ * rows, so within the V range) and (M_k, L_k) in fp32; then
+ *   ctx_h = sum_k w_k accn_k,  w_k = L_k exp(M_k - M_h) / sum_k' L_k' exp(M_k' - M_h).
+ * Threads t < H*S compute the weights into LDS; thread t < 160 owns dims
+ * 8t..8t+7 and sums their S split values (loads issued by merge_load,
+ * before the caller's weight loads). */
 struct MergeLoads {
-    static constexpr int NQ = (UOCR_K_HIDDEN / 4 + BLOCK - 1) / BLOCK;
-    float4 a[NQ][UOCR_K_ATTN_SPLITS];
+    uint4 a[UOCR_K_ATTN_SPLITS];
     float2 ml;
 };
 
 __device__ __forceinline__ void merge_load(MergeLoads &m, const float *__restrict__ part) {
-    constexpr int S = UOCR_K_ATTN_SPLITS, HD = UOCR_K_HEAD_DIM, Q = UOCR_K_HIDDEN / 4;
+    constexpr int S = UOCR_K_ATTN_SPLITS, HD = UOCR_K_HEAD_DIM, NO = UOCR_K_HIDDEN / 8;
     const int t = threadIdx.x;
+    const int o = min(t, NO - 1), hh = o / (HD / 8), d8 = o % (HD / 8);
+    const h16 *accn = (const h16 *)part;
 #pragma unroll
-    for (int j = 0; j < MergeLoads::NQ; ++j) {
-        const int quad = min(t + j * BLOCK, Q - 1);
-        const int hh = quad / (HD / 4), dq = quad % (HD / 4);
-#pragma unroll
-        for (int k = 0; k < S; ++k) m.a[j][k] = *(const float4 *)(part + (size_t)(hh * S + k) * HD + 4 * dq);
-    }
+    for (int k = 0; k < S; ++k) m.a[k] = *(const uint4 *)(accn + (size_t)(hh * S + k) * HD + 8 * d8);
     m.ml = *(const float2 *)(part + (size_t)UOCR_K_HEADS * S * HD + 2u * min(t, UOCR_K_HEADS * S - 1));
 }
 
 __device__ __forceinline__ void merge_finish(MergeLoads &m, h16 *ctx, float *wk) {
-    constexpr int S = UOCR_K_ATTN_SPLITS, HD = UOCR_K_HEAD_DIM, Q = UOCR_K_HIDDEN / 4;
-    static_assert(S == 16, "weights use 16-lane DPP rows");
+    constexpr int S = UOCR_K_ATTN_SPLITS, HD = UOCR_K_HEAD_DIM, NO = UOCR_K_HIDDEN / 8;
+    static_assert(S == 4 || S == 8 || S == 16, "split weights use aligned S-lane groups");
     hold(m.ml);
 #pragma unroll
-    for (int j = 0; j < MergeLoads::NQ; ++j) {
-#pragma unroll
-        for (int k = 0; k < S; ++k) hold(m.a[j][k]);
-    }
+    for (int k = 0; k < S; ++k) hold(m.a[k]);
     const int t = threadIdx.x;
     if (t < UOCR_K_HEADS * S) {
-        /* lanes 16h..16h+15 of a row hold the splits of head h */
+        /* lanes S*h..S*h+S-1 hold the splits of head h */
         float M = m.ml.x;
-        M = fmaxf(M, __shfl_xor(M, 1));
-        M = fmaxf(M, __shfl_xor(M, 2));
-        M = fmaxf(M, __shfl_xor(M, 4));
-        M = fmaxf(M, __shfl_xor(M, 8));
-        const float f = m.ml.x == -INFINITY ? 0.0f : expf(m.ml.x - M);
-        const float Ls = row16_sum(m.ml.y * f);
-        wk[t] = f / Ls;
+#pragma unroll
+        for (int o = 1; o < S; o <<= 1) M = fmaxf(M, __shfl_xor(M, o));
+        const float lf = m.ml.x == -INFINITY ? 0.0f : m.ml.y * expf(m.ml.x - M);
+        wk[t] = lf / group_sum<S>(lf);
     }
     __syncthreads();
+    if (t < NO) {
+        const int hh = t / (HD / 8);
+        float acc[8];
 #pragma unroll
-    for (int j = 0; j < MergeLoads::NQ; ++j) {
-        const int quad = t + j * BLOCK;
-        if (quad < Q) {
-            const int hh = quad / (HD / 4);
-            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
 #pragma unroll
-            for (int k = 0; k < S; ++k) {
-                const float w = wk[hh * S + k];
-                acc.x = fmaf(m.a[j][k].x, w, acc.x);
-                acc.y = fmaf(m.a[j][k].y, w, acc.y);
-                acc.z = fmaf(m.a[j][k].z, w, acc.z);
-                acc.w = fmaf(m.a[j][k].w, w, acc.w);
+        for (int k = 0; k < S; ++k) {
+            const float w = wk[hh * S + k];
+            const u32 u[4] = {m.a[k].x, m.a[k].y, m.a[k].z, m.a[k].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const h16x2 v = __builtin_bit_cast(h16x2, u[j]);
+                acc[2 * j] = fmaf((float)v.x, w, acc[2 * j]);
+                acc[2 * j + 1] = fmaf((float)v.y, w, acc[2 * j + 1]);
             }
-            ctx[4 * quad] = (h16)acc.x;
-            ctx[4 * quad + 1] = (h16)acc.y;
-            ctx[4 * quad + 2] = (h16)acc.z;
-            ctx[4 * quad + 3] = (h16)acc.w;
         }
+        h16x2 r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = h16x2{(h16)acc[2 * j], (h16)acc[2 * j + 1]};
+        ((uint4 *)ctx)[t] = __builtin_bit_cast(uint4, r);
     }
     __syncthreads();
 }
@@ -1433,7 +1451,7 @@ extern "C" hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, c
         partials == nullptr) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(k_attention, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(BLOCK), 0, st, (const h16 *)q,
+    hipLaunchKernelGGL(k_attention, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(ATT_THREADS), 0, st, (const h16 *)q,
                        (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials,
                        (long long *)router_acc);
     return hipGetLastError();
