@@ -62,7 +62,9 @@ UOCR_API int uocr_generate_embeddings(uocr_engine *engine, const int32_t *input_
 /* ---- 2. hot-path operators ----------------------------------------------- */
 
 /* Bytes of the device workspace every operator below takes (partials,
- * counters, routing ids, intermediates, step state). */
+ * counters, routing ids, intermediates, step state).  A workspace must be
+ * zero before its first use (uocr_hip_alloc returns zeroed memory); the
+ * operators leave their counters at zero. */
 UOCR_API size_t uocr_op_workspace_bytes(void);
 
 /* y[r] = fp16(sum_k W[r][k] * x[k] (+ residual[r])), r < rows, K % 64 == 0,
@@ -180,6 +182,8 @@ UOCR_API int uocr_op_moe_ffn_rows(const uocr_op_moe_weights *m, const void *x, c
 
 /* ---- 3. device plumbing ---------------------------------------------------- */
 UOCR_API int uocr_hip_device_count(void);
+/* Device memory on the library's device, zero-filled (a fresh operator
+ * workspace must start at zero). */
 UOCR_API void *uocr_hip_alloc(size_t bytes);
 UOCR_API int uocr_hip_free(void *p);
 UOCR_API int uocr_hip_upload(void *dst, const void *src, size_t bytes);

@@ -30,7 +30,7 @@
 #ifndef UOCR_K_ATTN_SPLITS
 #define UOCR_K_ATTN_SPLITS 16      /* split-K blocks per head in decode attention */
 #endif
-#define UOCR_K_LM_BLOCKS 1024      /* upper bound on LM-head argmax partial blocks */
+#define UOCR_K_LM_BLOCKS 1024      /* upper bound on LM-head blocks */
 #define UOCR_K_ROUTER_FIX_SHIFT 32 /* router fold accumulator: round(z * 2^32) in int64 */
 #define UOCR_K_ROUTER_ACC_COPIES 4 /* accumulator copies (block b adds into copy b % 4) */
 #define UOCR_ROUTER_ACC_WORDS (UOCR_K_ROUTER_ACC_COPIES * UOCR_K_EXPERTS) /* int64 words */
@@ -67,7 +67,8 @@ typedef struct uocr_expert_slab {
 
 /* Scratch sizes (bytes) the launchers expect. */
 #define UOCR_ATTN_PARTIAL_FLOATS (UOCR_K_HEADS * UOCR_K_ATTN_SPLITS * (UOCR_K_HEAD_DIM + 2))
-#define UOCR_LM_PARTIAL_WORDS (2 * UOCR_K_LM_BLOCKS)
+#define UOCR_LM_KEYS 16 /* LM-head argmax key copies (block b -> copy b % 16) */
+#define UOCR_LM_PARTIAL_WORDS (2 * UOCR_LM_KEYS + 1) /* keys + ticket counter */
 
 #ifdef __cplusplus
 extern "C" {
@@ -129,11 +130,13 @@ hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab,
 hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
                                 const float *weights, const uint16_t *mid, uocr_qmat SD, const uint16_t *smid,
                                 const uint16_t *res, uint16_t *out);
-/* Fused final norm + LM-head argmax: per-block partials, then a one-block
- * finalize storing the winner at tokens[state->t] (tokens[0] without state);
- * with advance it also writes the next decode position into *state and, when
- * E.w is set, gathers that token's embedding row into hout.
- * partials: UOCR_LM_PARTIAL_WORDS words. */
+/* Final norm + LM-head argmax + selection in one launch: blocks publish
+ * their best (score, row) by atomic max and the last block to finish stores
+ * the winner at tokens[state->t] (tokens[0] without state); with advance it
+ * also writes the next decode position into *state and, when E.w is set,
+ * gathers that token's embedding row into hout.
+ * partials: UOCR_LM_PARTIAL_WORDS words, zero before the first call; every
+ * call leaves them zero. */
 hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x, const uint16_t *nw,
                                uint32_t *partials, uocr_step_state *state, int advance, int32_t *tokens,
                                float *scores, uocr_qmat E, uint16_t *hout, const float *inv_freq);

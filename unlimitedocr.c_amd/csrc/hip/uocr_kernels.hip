@@ -473,11 +473,11 @@ __device__ __forceinline__ bool better(float s, u32 id, float bs, u32 bid) {
  *  EPI_ARGMAX: per-block best (score, row) into part[2*block] (NaN skipped,
  *              ties to the lower row). */
 template <int QT, int LPR, int J, int EPI>
-__global__ __launch_bounds__(BLOCK) void k_stream(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
-                                                  const uint8_t *__restrict__ W2, const h16 *__restrict__ S2,
-                                                  u32 rows, u32 K, const h16 *__restrict__ x,
-                                                  const h16 *__restrict__ nw, const h16 *__restrict__ res,
-                                                  h16 *__restrict__ y, u32 *__restrict__ part) {
+__device__ __forceinline__ void stream_rows(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
+                                            const uint8_t *__restrict__ W2, const h16 *__restrict__ S2, u32 rows,
+                                            u32 K, const h16 *__restrict__ x, const h16 *__restrict__ nw,
+                                            const h16 *__restrict__ res, h16 *__restrict__ y, float &best,
+                                            u32 &best_id) {
     constexpr u32 R = 64u / LPR;
     constexpr int NM = EPI == EPI_SWIGLU ? 2 : 1;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_MAX_K];
@@ -555,9 +555,24 @@ __global__ __launch_bounds__(BLOCK) void k_stream(const uint8_t *__restrict__ W,
                     bi = bidv[i];
                 }
             }
-            part[2u * blockIdx.x] = __float_as_uint(b);
-            part[2u * blockIdx.x + 1u] = bi;
+            best = b;
+            best_id = bi;
         }
+    }
+}
+
+template <int QT, int LPR, int J, int EPI>
+__global__ __launch_bounds__(BLOCK) void k_stream(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
+                                                  const uint8_t *__restrict__ W2, const h16 *__restrict__ S2,
+                                                  u32 rows, u32 K, const h16 *__restrict__ x,
+                                                  const h16 *__restrict__ nw, const h16 *__restrict__ res,
+                                                  h16 *__restrict__ y, u32 *__restrict__ part) {
+    float b = -INFINITY;
+    u32 bi = NONE_ID;
+    stream_rows<QT, LPR, J, EPI>(W, S, W2, S2, rows, K, x, nw, res, y, b, bi);
+    if (EPI == EPI_ARGMAX && threadIdx.x == 0) {
+        part[2u * blockIdx.x] = __float_as_uint(b);
+        part[2u * blockIdx.x + 1u] = bi;
     }
 }
 
@@ -1235,65 +1250,21 @@ __global__ void k_decode_state(uocr_step_state *st, int32_t P, int32_t t, RopeTa
 /* LM head finalize                                                          */
 /* ------------------------------------------------------------------------ */
 
-/* One block: reduce the nparts (<= 4 * BLOCK) argmax partials to the token
- * id (none valid -> 0, score -inf), store it at tokens[state->t] (or [0]
- * without state); with advance, write the next decode position into *state
- * (uocr_metal.m:14239 and the ring plan of attention_decode.metal:25-33) and
- * gather the selected token's embedding row into hout
- * (embedding_q4.metal:21-56). */
+/* The selection itself, by one whole block, with the winner (b, bi) and
+ * the step state's t and prompt_len (read early by the caller) in thread 0:
+ * store the token (and score), advance the step state, refresh the RoPE
+ * table, gather the token's embedding row. */
 template <int QE>
-__global__ __launch_bounds__(BLOCK) void k_lm_finalize(const u32 *__restrict__ part, u32 nparts, uocr_step_state *st,
-                                                       int advance, int32_t *tokens, float *scores,
-                                                       const uint8_t *__restrict__ EW, const h16 *__restrict__ ES,
-                                                       u32 vocab, h16 *__restrict__ hout, RopeTab tab, int with_rope) {
-    __shared__ float bsc[NWAVE];
-    __shared__ u32 bidv[NWAVE];
+__device__ __forceinline__ void lm_select_body(float b, u32 bi, int32_t t, int32_t P, uocr_step_state *st,
+                                               int advance, int32_t *tokens, float *scores,
+                                               const uint8_t *__restrict__ EW, const h16 *__restrict__ ES, u32 vocab,
+                                               h16 *__restrict__ hout, const RopeTab &tab, int with_rope) {
     __shared__ int32_t chosen, next_pos;
-    float ps[4];
-    u32 pid[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const u32 i = threadIdx.x + k * BLOCK;
-        ps[k] = i < nparts ? __uint_as_float(part[2u * i]) : -INFINITY;
-        pid[k] = i < nparts ? part[2u * i + 1u] : NONE_ID;
-    }
-    float b = -INFINITY;
-    u32 bi = NONE_ID;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        if (better(ps[k], pid[k], b, bi)) {
-            b = ps[k];
-            bi = pid[k];
-        }
-    }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const float os = __shfl_xor(b, o);
-        const u32 oid = (u32)__shfl_xor((int)bi, o);
-        if (better(os, oid, b, bi)) {
-            b = os;
-            bi = oid;
-        }
-    }
-    const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    if (lane == 0u) {
-        bsc[wave] = b;
-        bidv[wave] = bi;
-    }
-    __syncthreads();
     if (threadIdx.x == 0) {
-        for (int i = 1; i < NWAVE; ++i) {
-            if (better(bsc[i], bidv[i], b, bi)) {
-                b = bsc[i];
-                bi = bidv[i];
-            }
-        }
         const int32_t id = bi == NONE_ID ? 0 : (int32_t)bi;
-        const int32_t t = st != nullptr ? st->t : 0;
         tokens[t] = id;
         if (scores != nullptr) scores[t] = bi == NONE_ID ? -INFINITY : b;
         if (st != nullptr && advance) {
-            const int32_t P = st->prompt_len;
             const int32_t gcount = t + 1;
             const int32_t live = gcount < UOCR_K_RING ? gcount : UOCR_K_RING;
             st->cur_token = id;
@@ -1305,12 +1276,82 @@ __global__ __launch_bounds__(BLOCK) void k_lm_finalize(const u32 *__restrict__ p
             st->t = t + 1;
         }
         chosen = id;
-        next_pos = st != nullptr ? st->prompt_len + t : 0;
+        next_pos = P + t;
     }
     __syncthreads();
     if (st != nullptr && advance && with_rope) set_rope(st, next_pos, tab);
     if (advance && EW != nullptr) embed_row_body<QE>(EW, ES, vocab, chosen, hout);
 }
+
+/* Final norm + LM-head GEMV + argmax + selection in one launch.  Every block
+ * reduces its rows to a best (score, row) and publishes it as one 64-bit key,
+ *   key = (order(score) << 32) | (0xffffffff - row)   (0: no valid row),
+ * with a returning atomic max into keys[block % 16]; order() maps floats to
+ * unsigned integers in the same order, so the largest key is the highest
+ * score with the lowest row among equals (lm_head_q4.metal:48-97,
+ * sampling.metal:173-200: NaN rows skipped, ties to the lowest id, none
+ * valid -> 0).  The block then takes a ticket from a returning atomic
+ * counter; the block that draws the last ticket has every key in place,
+ * reads and clears the 16 keys with atomic exchanges, re-arms the counter
+ * and performs the selection (lm_select_body).  Only atomics cross blocks,
+ * so no device-scope fence is needed.  keys and counter start at zero and
+ * are left at zero. */
+template <int QT, int LPR, int J, int QE>
+__global__ __launch_bounds__(BLOCK) void k_lm_select(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
+                                                     u32 rows, const h16 *__restrict__ x,
+                                                     const h16 *__restrict__ nw, unsigned long long *keys,
+                                                     u32 *counter, uocr_step_state *st, int advance, int32_t *tokens,
+                                                     float *scores, const uint8_t *__restrict__ EW,
+                                                     const h16 *__restrict__ ES, h16 *__restrict__ hout, RopeTab tab,
+                                                     int with_rope) {
+    float b = -INFINITY;
+    u32 bi = NONE_ID;
+    /* the step fields the selection needs, read before the GEMV */
+    int32_t t0 = 0, P0 = 0;
+    if (st != nullptr && threadIdx.x == 0) {
+        t0 = st->t;
+        P0 = st->prompt_len;
+    }
+    stream_rows<QT, LPR, J, EPI_ARGMAX>(W, S, nullptr, nullptr, rows, UOCR_K_HIDDEN, x, nw, nullptr, nullptr, b, bi);
+    __shared__ int last;
+    if (threadIdx.x == 0) {
+        unsigned long long key = 0ull;
+        if (bi != NONE_ID) {
+            const u32 u = __float_as_uint(b == 0.0f ? 0.0f : b); /* -0 ranks as +0 */
+            const u32 o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+            key = ((unsigned long long)o << 32) | (unsigned long long)(0xffffffffu - bi);
+        }
+        unsigned long long old = __hip_atomic_fetch_max(keys + blockIdx.x % UOCR_LM_KEYS, key, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+        /* the ticket is drawn only after the key is in place: the fence needs
+         * the returned value, and the ticket atomic cannot move above it */
+        asm volatile("" : "+v"(old)::"memory");
+        const u32 ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = ticket == gridDim.x - 1u;
+    }
+    __syncthreads();
+    if (!last) return;
+    if (threadIdx.x == 0) {
+        unsigned long long best = 0ull;
+#pragma unroll
+        for (int k = 0; k < UOCR_LM_KEYS; ++k) {
+            const unsigned long long v = __hip_atomic_exchange(keys + k, 0ull, __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT);
+            best = v > best ? v : best;
+        }
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (best == 0ull) {
+            b = -INFINITY;
+            bi = NONE_ID;
+        } else {
+            const u32 o = (u32)(best >> 32);
+            b = __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+            bi = 0xffffffffu - (u32)best;
+        }
+    }
+    lm_select_body<QE>(b, bi, t0, P0, st, advance, tokens, scores, EW, ES, rows, hout, tab, with_rope);
+}
+
 
 /* ------------------------------------------------------------------------ */
 /* launchers                                                                 */
@@ -1588,13 +1629,32 @@ static RopeTab rope_tab(const float *inv_freq) {
     return tab;
 }
 
-template <int QE>
-static void launch_lm_fin(hipStream_t st, const u32 *part, u32 nb, uocr_step_state *state, int advance,
-                          int32_t *tokens, float *scores, uocr_qmat E, u32 vocab, uint16_t *hout,
-                          const float *inv_freq) {
-    hipLaunchKernelGGL((k_lm_finalize<QE>), dim3(1), dim3(BLOCK), 0, st, part, nb, state, advance, tokens, scores,
-                       (const uint8_t *)E.w, (const h16 *)E.s, vocab, (h16 *)hout, rope_tab(inv_freq),
-                       inv_freq != nullptr ? 1 : 0);
+template <int QT, int QE>
+static void launch_lm_select(hipStream_t st, uocr_qmat W, u32 vocab, const uint16_t *x, const uint16_t *nw,
+                             uint32_t *work, uocr_step_state *state, int advance, int32_t *tokens, float *scores,
+                             uocr_qmat E, uint16_t *hout, const float *inv_freq) {
+    constexpr u32 C = chunks_per_row<QT>(UOCR_K_HIDDEN), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
+    auto fn = k_lm_select<QT, LPR, J, QE>;
+    const u32 groups = (vocab + R - 1u) / R;
+    u32 nb = (groups + NWAVE - 1u) / NWAVE;
+    nb = min(nb, min(resident_blocks(fn), (u32)UOCR_K_LM_BLOCKS));
+    hipLaunchKernelGGL(fn, dim3(nb), dim3(BLOCK), 0, st, (const uint8_t *)W.w, (const h16 *)W.s, vocab,
+                       (const h16 *)x, (const h16 *)nw, (unsigned long long *)work, work + 2 * UOCR_LM_KEYS, state,
+                       advance, tokens, scores, (const uint8_t *)E.w, (const h16 *)E.s, (h16 *)hout,
+                       rope_tab(inv_freq), inv_freq != nullptr ? 1 : 0);
+}
+
+template <int QT>
+static void launch_lm_select_qt(hipStream_t st, uocr_qmat W, u32 vocab, const uint16_t *x, const uint16_t *nw,
+                                uint32_t *work, uocr_step_state *state, int advance, int32_t *tokens, float *scores,
+                                uocr_qmat E, uint16_t *hout, const float *inv_freq) {
+#define LMS(QE) launch_lm_select<QT, QE>(st, W, vocab, x, nw, work, state, advance, tokens, scores, E, hout, inv_freq)
+    switch (E.w != nullptr ? E.qtype : UOCR_QT_Q4) {
+        case UOCR_QT_F16: LMS(1); break;
+        case UOCR_QT_Q8: LMS(3); break;
+        default: LMS(4); break;
+    }
+#undef LMS
 }
 
 extern "C" hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x,
@@ -1605,15 +1665,8 @@ extern "C" hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t 
         (advance && state == nullptr) || (E.w != nullptr && (!mat_ok(E) || hout == nullptr))) {
         return hipErrorInvalidValue;
     }
-    u32 nb = 0;
-    const u32 maxb = 4u * BLOCK; /* finalize reduces at most 4 partials per thread */
-    switch (W.qtype) {
-        case UOCR_QT_F16: launch_stream<1, EPI_ARGMAX>(st, W, W, vocab, UOCR_K_HIDDEN, x, nw, nullptr, nullptr, partials, maxb, &nb); break;
-        case UOCR_QT_Q8: launch_stream<3, EPI_ARGMAX>(st, W, W, vocab, UOCR_K_HIDDEN, x, nw, nullptr, nullptr, partials, maxb, &nb); break;
-        default: launch_stream<4, EPI_ARGMAX>(st, W, W, vocab, UOCR_K_HIDDEN, x, nw, nullptr, nullptr, partials, maxb, &nb); break;
-    }
-    DISPATCH_QT(E.w != nullptr ? E.qtype : UOCR_QT_Q4, launch_lm_fin, st, partials, nb, state, advance, tokens, scores,
-                E, vocab, hout, inv_freq);
+    DISPATCH_QT(W.qtype, launch_lm_select_qt, st, W, vocab, x, nw, partials, state, advance, tokens, scores, E, hout,
+                inv_freq);
     return hipGetLastError();
 }
 

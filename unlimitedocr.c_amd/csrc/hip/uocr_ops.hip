@@ -435,6 +435,13 @@ extern "C" void *uocr_hip_alloc(size_t bytes) {
         op_fail(UOCR_ERROR_OUT_OF_MEMORY, "hipMalloc(%zu) failed", bytes);
         return nullptr;
     }
+    /* zeroed: operator workspaces rely on it (the LM-head selection's keys
+     * and ticket counter start at zero and are left at zero) */
+    if (hipMemset(p, 0, bytes) != hipSuccess) {
+        (void)hipFree(p);
+        op_fail(UOCR_ERROR_INTERNAL, "hipMemset(%zu) failed", bytes);
+        return nullptr;
+    }
     return p;
 }
 
