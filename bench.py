@@ -129,7 +129,7 @@ def lm_head_roofline(log, iters: int = 60) -> dict:
     traffic = None
     if TRAFFIC_FILE.exists():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
-    return {"kernel": "k_stream<Q4,EPI_ARGMAX> + k_lm_finalize (Q4 129280x1280 + argmax, config 2)", "bound": "hbm",
+    return {"kernel": "k_lm_select<Q4> (final norm + Q4 129280x1280 GEMV + argmax + selection, config 2)", "bound": "hbm",
             "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
             "traffic": traffic, "avg_launch_us": round(cold_ms * 1e3, 2),
             "hot_cache_achieved": round(algo / (hot_ms / 1e3) / 1e9, 1), "algorithmic_bytes": algo,
