@@ -27,6 +27,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 typedef _Float16 h16;
 typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -37,6 +39,7 @@ typedef uint32_t u32;
 #define TN 128 /* GEMM tile columns */
 #define TK 64  /* GEMM K step = one quantisation group */
 #define LDA (TK + 8) /* padded LDS row (halves) */
+#define GDEPTH 3 /* K steps in flight per GEMM block */
 
 __device__ __forceinline__ float silu_p(float g) {
     return g / (1.0f + expf(-g));
@@ -59,19 +62,49 @@ __device__ __forceinline__ u32 magic2(u32 v, u32 sel) {
 
 enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2 };
 
-/* Dequantise this thread's share of a TN x TK weight tile (rows n0.., group
- * g) into LDS as fp16 integers (f16: the values), and its row scales. */
+/* One K step's share of this thread: the activation tile piece (two 16-byte
+ * loads) and the weight tile piece of each matrix, loaded into registers
+ * (gemm_load) several steps ahead and dequantised into LDS (gemm_store)
+ * when the step comes up. */
 template <int QT>
-__device__ __forceinline__ void load_w_tile(h16 *ws, float *sc, const uint8_t *W, const h16 *S, u32 K, u32 n0, u32 nmax,
-                                            u32 g) {
-    const u32 t = threadIdx.x;
+struct WPiece {
+    static constexpr int NV = QT == 4 ? 1 : (QT == 3 ? 2 : 4);
+    uint4 w[NV];
+    u32 s; /* fp16 scale bits */
+};
+
+
+/* thread t: weight row t/2 of the tile; Q4 bytes 16*(t&1)..+15 of the group
+ * (low nibbles: columns 16*(t&1)+i, high nibbles the same + 32), Q8 bytes
+ * 32*(t&1)..+31, f16 columns 32*(t&1)..+31.  Threads t < TN also load the
+ * scale of row t. */
+template <int QT>
+__device__ __forceinline__ void w_load(WPiece<QT> &f, const uint8_t *W, const h16 *S, u32 K, u32 n0, u32 nmax,
+                                       u32 g) {
+    const u32 t = threadIdx.x, r = t >> 1, half = t & 1u, n = min(n0 + r, nmax - 1u);
     if (QT == 4) {
-        /* thread t: row t/2, bytes 16*(t&1)..+15 of the group: low nibbles
-         * are columns 16*(t&1)+i, high nibbles the same + 32 */
-        const u32 r = t >> 1, half = t & 1u, n = min(n0 + r, nmax - 1u);
-        const uint4 w = *(const uint4 *)(W + (size_t)n * (K / 2u) + g * 32u + 16u * half);
-        const u32 wv[4] = {w.x, w.y, w.z, w.w};
-        const u32 bias = 0x64086408u; /* (1032, 1032) */
+        f.w[0] = *(const uint4 *)(W + (size_t)n * (K / 2u) + g * 32u + 16u * half);
+    } else if (QT == 3) {
+        const uint4 *src = (const uint4 *)(W + (size_t)n * K + g * 64u + 32u * half);
+        f.w[0] = src[0];
+        f.w[1] = src[1];
+    } else {
+        const uint4 *src = (const uint4 *)((const h16 *)W + (size_t)n * K + g * 64u + 32u * half);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f.w[i] = src[i];
+    }
+    if (QT != 1) f.s = ((const unsigned short *)S)[(size_t)min(n0 + min(t, (u32)TN - 1u), nmax - 1u) * (K / 64u) + g];
+}
+
+/* Dequantise a loaded piece into the LDS tile as fp16 integers (Q4 nibble - 8,
+ * Q8 int8; f16: the values) and store the row scale. */
+template <int QT>
+__device__ __forceinline__ void w_store(const WPiece<QT> &f, h16 *ws, float *sc) {
+    const u32 t = threadIdx.x, r = t >> 1, half = t & 1u;
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    if (QT == 4) {
+        const u32 wv[4] = {f.w[0].x, f.w[0].y, f.w[0].z, f.w[0].w};
+        const h2 bb = __builtin_bit_cast(h2, 0x64086408u); /* (1032, 1032) */
         union {
             uint4 u[2];
             u32 d[8];
@@ -79,8 +112,6 @@ __device__ __forceinline__ void load_w_tile(h16 *ws, float *sc, const uint8_t *W
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const u32 l = wv[b] & 0x0F0F0F0Fu, h = (wv[b] >> 4) & 0x0F0F0F0Fu;
-            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-            const h2 bb = __builtin_bit_cast(h2, bias);
             lo.d[2 * b] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(l, 0x04010400u)) - bb);
             lo.d[2 * b + 1] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(l, 0x04030402u)) - bb);
             hi.d[2 * b] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(h, 0x04010400u)) - bb);
@@ -92,14 +123,8 @@ __device__ __forceinline__ void load_w_tile(h16 *ws, float *sc, const uint8_t *W
         dl[1] = lo.u[1];
         dh[0] = hi.u[0];
         dh[1] = hi.u[1];
-        if (t < TN) sc[t] = (float)S[(size_t)min(n0 + t, nmax - 1u) * (K / 64u) + g];
     } else if (QT == 3) {
-        /* thread t: row t/2, bytes 32*(t&1)..+31 */
-        const u32 r = t >> 1, half = t & 1u, n = min(n0 + r, nmax - 1u);
-        const uint4 *src = (const uint4 *)(W + (size_t)n * K + g * 64u + 32u * half);
-        const uint4 w0 = src[0], w1 = src[1];
-        const u32 wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const u32 wv[8] = {f.w[0].x, f.w[0].y, f.w[0].z, f.w[0].w, f.w[1].x, f.w[1].y, f.w[1].z, f.w[1].w};
         const h2 bb = __builtin_bit_cast(h2, 0x64806480u); /* (1152, 1152) */
         union {
             uint4 u[4];
@@ -114,15 +139,12 @@ __device__ __forceinline__ void load_w_tile(h16 *ws, float *sc, const uint8_t *W
         uint4 *d = (uint4 *)(ws + r * LDA + 32u * half);
 #pragma unroll
         for (int i = 0; i < 4; ++i) d[i] = o.u[i];
-        if (t < TN) sc[t] = (float)S[(size_t)min(n0 + t, nmax - 1u) * (K / 64u) + g];
     } else {
-        /* thread t: row t/2, columns 32*(t&1)..+31 */
-        const u32 r = t >> 1, half = t & 1u, n = min(n0 + r, nmax - 1u);
-        const uint4 *src = (const uint4 *)((const h16 *)W + (size_t)n * K + g * 64u + 32u * half);
         uint4 *d = (uint4 *)(ws + r * LDA + 32u * half);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) d[i] = src[i];
+        for (int i = 0; i < 4; ++i) d[i] = make_uint4(f.w[i].x, f.w[i].y, f.w[i].z, f.w[i].w);
     }
+    if (QT != 1 && t < TN) sc[t] = (float)__builtin_bit_cast(h16, (unsigned short)f.s);
 }
 
 struct GemmArgs {
@@ -193,18 +215,55 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[m][j][i] = 0.0f;
 
+    /* K steps run GDEPTH deep: step g's loads were issued GDEPTH steps
+     * earlier into a register ring (constant indices only, so the ring stays
+     * in registers), and the MFMAs of one step overlap the loads of the next
+     * ones */
     const u32 G = p.K / TK;
-    for (u32 g = 0; g < G; ++g) {
-        /* A tile: 64 rows x 64 halves, 2 x 16 B per thread */
+    constexpr int NV = WPiece<QT>::NV;
+    u32 ka[GDEPTH][2][4]; /* activation pieces as words: no struct copies, so they stay in registers */
+    uint4 kw[GDEPTH][NMAT][NV];
+    u32 kscale[GDEPTH][NMAT];
+    const uint8_t *wp[2] = {w0, w1};
+    const h16 *sp[2] = {s0p, s1p};
+    auto issue = [&](auto D, u32 g) {
+        constexpr int d = decltype(D)::value;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const u32 idx = t + q * PB, r = idx >> 3, c8 = idx & 7u;
             const uint4 v = *(const uint4 *)(p.A + (size_t)arow[r] * p.lda + g * TK + 8u * c8);
-            *(uint4 *)(as + r * LDA + 8u * c8) = v;
+            ka[d][q][0] = v.x;
+            ka[d][q][1] = v.y;
+            ka[d][q][2] = v.z;
+            ka[d][q][3] = v.w;
         }
-        load_w_tile<QT>(wsm[0], scs[0], w0, s0p, p.K, n0 - nbase, nmax, g);
-        if (NMAT == 2) load_w_tile<QT>(wsm[NMAT - 1], scs[NMAT - 1], w1, s1p, p.K, n0 - nbase, nmax, g);
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            WPiece<QT> f;
+            w_load<QT>(f, wp[m], sp[m], p.K, n0 - nbase, nmax, g);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) kw[d][m][v] = make_uint4(f.w[v].x, f.w[v].y, f.w[v].z, f.w[v].w);
+            kscale[d][m] = f.s;
+        }
+    };
+    auto step = [&](auto D, u32 g) {
+        constexpr int d = decltype(D)::value;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const u32 idx = t + q * PB, r = idx >> 3, c8 = idx & 7u;
+            *(uint4 *)(as + r * LDA + 8u * c8) = make_uint4(ka[d][q][0], ka[d][q][1], ka[d][q][2], ka[d][q][3]);
+        }
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            WPiece<QT> f;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) f.w[v] = make_uint4(kw[d][m][v].x, kw[d][m][v].y, kw[d][m][v].z, kw[d][m][v].w);
+            f.s = kscale[d][m];
+            w_store<QT>(f, wsm[m], scs[m]);
+        }
         __syncthreads();
+        /* refill this ring slot with step g + GDEPTH while the MFMAs run */
+        if (g + GDEPTH < G) issue(D, g + GDEPTH);
 #pragma unroll
         for (int m = 0; m < NMAT; ++m)
 #pragma unroll
@@ -235,6 +294,18 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
             }
         }
         __syncthreads();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    static_assert(GDEPTH == 3, "the ring below is written out for three slots");
+    issue(I0{}, 0u);
+    issue(I1{}, min(1u, G - 1u));
+    issue(I2{}, min(2u, G - 1u));
+    for (u32 g = 0; g < G; g += 3u) {
+        step(I0{}, g);
+        if (g + 1u < G) step(I1{}, g + 1u);
+        if (g + 2u < G) step(I2{}, g + 2u);
     }
 
     /* C layout of a 32x32 MFMA tile: lane l, element i -> row 8*(i/4) +
