@@ -440,20 +440,59 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
         for (int i = 0; i < 16; ++i) o[j][i] = 0.0f;
     const u32 wm = wave & 1u, wn = wave >> 1;
     const u32 qlast = min(q0 + AQ, P) - 1u;
-    for (u32 k0 = 0; k0 <= qlast; k0 += AK) {
-        __syncthreads();
-        /* K tile (row-major) and V tile transposed to [dim][key] */
+    /* next K/V tile in registers (words, so they stay in registers) */
+    u32 kr_[4][4], va_[2][4], vb_[2][4];
+    auto load_kv = [&](u32 k0n) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const u32 idx = t + q * PB, r = idx >> 4, c8 = idx & 15u;
-            const u32 kr = min(k0 + r, P - 1u);
-            *(uint4 *)(ks + r * LDQ + 8u * c8) = *(const uint4 *)(kh + (size_t)kr * 128u + 8u * c8);
-            U4H8 v;
-            v.u = *(const uint4 *)(vh + (size_t)kr * 128u + 8u * c8);
+            const uint4 v = *(const uint4 *)(kh + (size_t)min(k0n + r, P - 1u) * 128u + 8u * c8);
+            kr_[q][0] = v.x;
+            kr_[q][1] = v.y;
+            kr_[q][2] = v.z;
+            kr_[q][3] = v.w;
+        }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) vt[(8u * c8 + j) * LDV + r] = v.h[j];
+        for (int q = 0; q < 2; ++q) {
+            const u32 idx = t + q * PB, kp = idx & 31u, c8 = idx >> 5;
+            const uint4 a = *(const uint4 *)(vh + (size_t)min(k0n + 2u * kp, P - 1u) * 128u + 8u * c8);
+            const uint4 b = *(const uint4 *)(vh + (size_t)min(k0n + 2u * kp + 1u, P - 1u) * 128u + 8u * c8);
+            va_[q][0] = a.x;
+            va_[q][1] = a.y;
+            va_[q][2] = a.z;
+            va_[q][3] = a.w;
+            vb_[q][0] = b.x;
+            vb_[q][1] = b.y;
+            vb_[q][2] = b.z;
+            vb_[q][3] = b.w;
+        }
+    };
+    load_kv(0u);
+    for (u32 k0 = 0; k0 <= qlast; k0 += AK) {
+        __syncthreads();
+        /* K tile (row-major) and V tile transposed to [dim][key], from the
+         * registers loaded one tile ahead.  The transpose goes by key pairs:
+         * a thread holds 8 dims of keys 2i and 2i+1 and writes 8 dwords (dim
+         * d: key 2i | key 2i+1 << 16); the 32 lanes of a half-wavefront
+         * cover consecutive pairs, so each write touches consecutive banks. */
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32 idx = t + q * PB, r = idx >> 4, c8 = idx & 15u;
+            *(uint4 *)(ks + r * LDQ + 8u * c8) = make_uint4(kr_[q][0], kr_[q][1], kr_[q][2], kr_[q][3]);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const u32 idx = t + q * PB, kp = idx & 31u, c8 = idx >> 5;
+            u32 *dst = (u32 *)(vt + 8u * c8 * LDV + 2u * kp);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                /* dims 2j and 2j+1: low halves, then high halves */
+                dst[(2u * j) * (LDV / 2u)] = __builtin_amdgcn_perm(vb_[q][j], va_[q][j], 0x05040100u);
+                dst[(2u * j + 1u) * (LDV / 2u)] = __builtin_amdgcn_perm(vb_[q][j], va_[q][j], 0x07060302u);
+            }
         }
         __syncthreads();
+        if (k0 + AK <= qlast) load_kv(k0 + AK);
         /* S = Q K^T: wave (wm, wn) computes rows 32wm.., keys 32wn.. */
         {
             f32x16 s;
@@ -484,13 +523,17 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
             mx = fmaxf(mx, __shfl_xor(mx, 2));
             const float mold = rowm[r], mnew = fmaxf(mold, mx);
             float sum = 0.0f;
+            U4H8 pv[2];
 #pragma unroll
             for (int c = 0; c < 16; ++c) {
                 const float v = sS[r][16u * part + c];
                 const float e = v == -INFINITY ? 0.0f : expf(v - mnew);
                 sum += e;
-                ps[r * LDV + 16u * part + c] = (h16)e;
+                pv[c >> 3].h[c & 7] = (h16)e;
             }
+            /* the row's 16 probabilities as two 16-byte stores */
+            *(uint4 *)(ps + r * LDV + 16u * part) = pv[0].u;
+            *(uint4 *)(ps + r * LDV + 16u * part + 8u) = pv[1].u;
             sum += __shfl_xor(sum, 1);
             sum += __shfl_xor(sum, 2);
             __syncthreads();
