@@ -7,10 +7,9 @@
  * real GEMMs [P x K] x [K x N]:
  *  - k_gemm: 64 x 128 output tiles, K in 64-column steps (one quantisation
  *    group).  Activation tiles are staged in LDS as fp16; weight tiles are
- *    dequantised into LDS as exact fp16 integers (Q4 nibble - 8, Q8 int8) so
- *    v_mfma_f32_32x32x16_f16 forms sum_k x*q in fp32 per group and the group
- *    scale is applied once per 64-column step, the same "group dot, then
- *    scale" arithmetic as the decode GEMVs.  Epilogues: fp16 store with
+ *    dequantised into LDS as fp16(q * scale), the reference's prefill
+ *    staging (gemm_q4.metal:48-55: half(float(q) * scale)), and
+ *    v_mfma_f32_32x32x16_f16 accumulates in fp32.  Epilogues: fp16 store with
  *    optional residual, fp32 store, and SwiGLU over two weight matrices.  In
  *    grouped mode a tile table maps each block to an expert's bucket of
  *    (token, rank) pairs: rows are gathered through an index list and the
@@ -37,8 +36,9 @@ typedef uint32_t u32;
 #define PB 256 /* threads per prefill block */
 #define TM 64  /* GEMM tile rows */
 #define TN 128 /* GEMM tile columns */
-#define TK 64  /* GEMM K step = one quantisation group */
-#define LDA (TK + 8) /* padded LDS row (halves) */
+#define TK 64  /* one quantisation group */
+#define KG 1   /* quantisation groups per GEMM K step (2 was measured slower: LDS limits the grouped SwiGLU to one block per CU) */
+#define LDA (KG * TK + 8) /* padded LDS row (halves) */
 #define GDEPTH 3 /* K steps in flight per GEMM block */
 
 __device__ __forceinline__ float silu_p(float g) {
@@ -93,15 +93,19 @@ __device__ __forceinline__ void w_load(WPiece<QT> &f, const uint8_t *W, const h1
 #pragma unroll
         for (int i = 0; i < 4; ++i) f.w[i] = src[i];
     }
-    if (QT != 1) f.s = ((const unsigned short *)S)[(size_t)min(n0 + min(t, (u32)TN - 1u), nmax - 1u) * (K / 64u) + g];
+    if (QT != 1) f.s = ((const unsigned short *)S)[(size_t)n * (K / 64u) + g];
 }
 
-/* Dequantise a loaded piece into the LDS tile as fp16 integers (Q4 nibble - 8,
- * Q8 int8; f16: the values) and store the row scale. */
+/* Dequantise a loaded piece into the LDS tile as fp16(q * scale) (the
+ * product of two fp16 values rounded once, as half(float(q) * scale) in
+ * gemm_q4.metal:55; f16: the values). */
 template <int QT>
-__device__ __forceinline__ void w_store(const WPiece<QT> &f, h16 *ws, float *sc) {
+__device__ __forceinline__ void w_store(const WPiece<QT> &f, h16 *ws, bool live) {
     const u32 t = threadIdx.x, r = t >> 1, half = t & 1u;
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    /* a group past the end of K (odd group count) contributes zeros */
+    const h16 sv = live ? __builtin_bit_cast(h16, (unsigned short)f.s) : (h16)0.0f;
+    const h2 sc2 = {sv, sv};
     if (QT == 4) {
         const u32 wv[4] = {f.w[0].x, f.w[0].y, f.w[0].z, f.w[0].w};
         const h2 bb = __builtin_bit_cast(h2, 0x64086408u); /* (1032, 1032) */
@@ -112,10 +116,10 @@ __device__ __forceinline__ void w_store(const WPiece<QT> &f, h16 *ws, float *sc)
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const u32 l = wv[b] & 0x0F0F0F0Fu, h = (wv[b] >> 4) & 0x0F0F0F0Fu;
-            lo.d[2 * b] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(l, 0x04010400u)) - bb);
-            lo.d[2 * b + 1] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(l, 0x04030402u)) - bb);
-            hi.d[2 * b] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(h, 0x04010400u)) - bb);
-            hi.d[2 * b + 1] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(h, 0x04030402u)) - bb);
+            lo.d[2 * b] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(l, 0x04010400u)) - bb) * sc2);
+            lo.d[2 * b + 1] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(l, 0x04030402u)) - bb) * sc2);
+            hi.d[2 * b] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(h, 0x04010400u)) - bb) * sc2);
+            hi.d[2 * b + 1] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(h, 0x04030402u)) - bb) * sc2);
         }
         uint4 *dl = (uint4 *)(ws + r * LDA + 16u * half);
         uint4 *dh = (uint4 *)(ws + r * LDA + 32u + 16u * half);
@@ -133,8 +137,8 @@ __device__ __forceinline__ void w_store(const WPiece<QT> &f, h16 *ws, float *sc)
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const u32 u = wv[b] ^ 0x80808080u;
-            o.d[2 * b] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(u, 0x04010400u)) - bb);
-            o.d[2 * b + 1] = __builtin_bit_cast(u32, __builtin_bit_cast(h2, magic2(u, 0x04030402u)) - bb);
+            o.d[2 * b] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(u, 0x04010400u)) - bb) * sc2);
+            o.d[2 * b + 1] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(u, 0x04030402u)) - bb) * sc2);
         }
         uint4 *d = (uint4 *)(ws + r * LDA + 32u * half);
 #pragma unroll
@@ -142,9 +146,10 @@ __device__ __forceinline__ void w_store(const WPiece<QT> &f, h16 *ws, float *sc)
     } else {
         uint4 *d = (uint4 *)(ws + r * LDA + 32u * half);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) d[i] = make_uint4(f.w[i].x, f.w[i].y, f.w[i].z, f.w[i].w);
+        for (int i = 0; i < 4; ++i) {
+            d[i] = live ? make_uint4(f.w[i].x, f.w[i].y, f.w[i].z, f.w[i].w) : make_uint4(0u, 0u, 0u, 0u);
+        }
     }
-    if (QT != 1 && t < TN) sc[t] = (float)__builtin_bit_cast(h16, (unsigned short)f.s);
 }
 
 struct GemmArgs {
@@ -170,7 +175,6 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     constexpr int NMAT = EPI == GE_SWIGLU ? 2 : 1;
     __shared__ __attribute__((aligned(16))) h16 as[TM * LDA];
     __shared__ __attribute__((aligned(16))) h16 wsm[NMAT][TN * LDA];
-    __shared__ float scs[NMAT][TN];
     __shared__ int32_t arow[TM], orow[TM];
     const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6;
     const u32 wm = wave & 1u, wn = wave >> 1;
@@ -207,7 +211,7 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     const h16 *s1p = NMAT == 2 ? (const h16 *)W1.s + (GROUPED ? e * p.s_stride : 0) : nullptr;
     __syncthreads();
 
-    f32x16 acc[NMAT][2], tmp[NMAT][2];
+    f32x16 acc[NMAT][2];
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
@@ -215,23 +219,26 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[m][j][i] = 0.0f;
 
-    /* K steps run GDEPTH deep: step g's loads were issued GDEPTH steps
-     * earlier into a register ring (constant indices only, so the ring stays
-     * in registers), and the MFMAs of one step overlap the loads of the next
-     * ones */
-    const u32 G = p.K / TK;
-    constexpr int NV = WPiece<QT>::NV;
-    u32 ka[GDEPTH][2][4]; /* activation pieces as words: no struct copies, so they stay in registers */
-    uint4 kw[GDEPTH][NMAT][NV];
-    u32 kscale[GDEPTH][NMAT];
+    /* K steps of KG groups run GDEPTH deep: step s's loads were issued
+     * GDEPTH steps earlier into a register ring (constant indices only, so
+     * the ring stays in registers), and the MFMAs of one step overlap the
+     * loads of the next ones */
+    const u32 G = p.K / TK, NS = (G + KG - 1u) / KG;
+    constexpr int NV = WPiece<QT>::NV, NA = KG * 2; /* 16-byte activation pieces per thread */
+    u32 ka[GDEPTH][NA][4]; /* words, not uint4: no struct copies, so they stay in registers */
+    uint4 kw[GDEPTH][NMAT][KG][NV];
+    u32 kscale[GDEPTH][NMAT][KG];
     const uint8_t *wp[2] = {w0, w1};
     const h16 *sp[2] = {s0p, s1p};
-    auto issue = [&](auto D, u32 g) {
+    auto issue = [&](auto D, u32 st) {
         constexpr int d = decltype(D)::value;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const u32 idx = t + q * PB, r = idx >> 3, c8 = idx & 7u;
-            const uint4 v = *(const uint4 *)(p.A + (size_t)arow[r] * p.lda + g * TK + 8u * c8);
+        for (int q = 0; q < NA; ++q) {
+            const u32 idx = t + q * PB, r = idx / (KG * 8u), c8 = idx % (KG * 8u);
+            /* columns past K (odd group count) read the row's last piece;
+             * their weights are zero */
+            const u32 col = min(st * KG * TK + 8u * c8, p.K - 8u);
+            const uint4 v = *(const uint4 *)(p.A + (size_t)arow[r] * p.lda + col);
             ka[d][q][0] = v.x;
             ka[d][q][1] = v.y;
             ka[d][q][2] = v.z;
@@ -239,39 +246,41 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
         }
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
-            WPiece<QT> f;
-            w_load<QT>(f, wp[m], sp[m], p.K, n0 - nbase, nmax, g);
 #pragma unroll
-            for (int v = 0; v < NV; ++v) kw[d][m][v] = make_uint4(f.w[v].x, f.w[v].y, f.w[v].z, f.w[v].w);
-            kscale[d][m] = f.s;
+            for (int k = 0; k < KG; ++k) {
+                WPiece<QT> f;
+                w_load<QT>(f, wp[m], sp[m], p.K, n0 - nbase, nmax, min(st * KG + k, G - 1u));
+#pragma unroll
+                for (int v = 0; v < NV; ++v) kw[d][m][k][v] = make_uint4(f.w[v].x, f.w[v].y, f.w[v].z, f.w[v].w);
+                kscale[d][m][k] = f.s;
+            }
         }
     };
-    auto step = [&](auto D, u32 g) {
+    auto step = [&](auto D, u32 st) {
         constexpr int d = decltype(D)::value;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const u32 idx = t + q * PB, r = idx >> 3, c8 = idx & 7u;
+        for (int q = 0; q < NA; ++q) {
+            const u32 idx = t + q * PB, r = idx / (KG * 8u), c8 = idx % (KG * 8u);
             *(uint4 *)(as + r * LDA + 8u * c8) = make_uint4(ka[d][q][0], ka[d][q][1], ka[d][q][2], ka[d][q][3]);
         }
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
-            WPiece<QT> f;
 #pragma unroll
-            for (int v = 0; v < NV; ++v) f.w[v] = make_uint4(kw[d][m][v].x, kw[d][m][v].y, kw[d][m][v].z, kw[d][m][v].w);
-            f.s = kscale[d][m];
-            w_store<QT>(f, wsm[m], scs[m]);
+            for (int k = 0; k < KG; ++k) {
+                WPiece<QT> f;
+#pragma unroll
+                for (int v = 0; v < NV; ++v) {
+                    f.w[v] = make_uint4(kw[d][m][k][v].x, kw[d][m][k][v].y, kw[d][m][k][v].z, kw[d][m][k][v].w);
+                }
+                f.s = kscale[d][m][k];
+                w_store<QT>(f, wsm[m] + k * TK, st * KG + k < G);
+            }
         }
         __syncthreads();
-        /* refill this ring slot with step g + GDEPTH while the MFMAs run */
-        if (g + GDEPTH < G) issue(D, g + GDEPTH);
+        /* refill this ring slot with step st + GDEPTH while the MFMAs run */
+        if (st + GDEPTH < NS) issue(D, st + GDEPTH);
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) tmp[m][j][i] = 0.0f;
-#pragma unroll
-        for (u32 kk = 0; kk < TK; kk += 16) {
+        for (u32 kk = 0; kk < KG * TK; kk += 16) {
             U4H8 a;
             a.u = *(const uint4 *)(as + (32u * wm + (lane & 31u)) * LDA + kk + 8u * (lane >> 5));
 #pragma unroll
@@ -280,17 +289,8 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
                 for (int j = 0; j < 2; ++j) {
                     U4H8 b;
                     b.u = *(const uint4 *)(wsm[m] + (64u * wn + 32u * j + (lane & 31u)) * LDA + kk + 8u * (lane >> 5));
-                    tmp[m][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.v, b.v, tmp[m][j], 0, 0, 0);
+                    acc[m][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.v, b.v, acc[m][j], 0, 0, 0);
                 }
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float s = QT == 1 ? 1.0f : scs[m][64u * wn + 32u * j + (lane & 31u)];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[m][j][i] = fmaf(tmp[m][j][i], s, acc[m][j][i]);
             }
         }
         __syncthreads();
@@ -300,12 +300,12 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     using I2 = std::integral_constant<int, 2>;
     static_assert(GDEPTH == 3, "the ring below is written out for three slots");
     issue(I0{}, 0u);
-    issue(I1{}, min(1u, G - 1u));
-    issue(I2{}, min(2u, G - 1u));
-    for (u32 g = 0; g < G; g += 3u) {
-        step(I0{}, g);
-        if (g + 1u < G) step(I1{}, g + 1u);
-        if (g + 2u < G) step(I2{}, g + 2u);
+    issue(I1{}, min(1u, NS - 1u));
+    issue(I2{}, min(2u, NS - 1u));
+    for (u32 st = 0; st < NS; st += 3u) {
+        step(I0{}, st);
+        if (st + 1u < NS) step(I1{}, st + 1u);
+        if (st + 2u < NS) step(I2{}, st + 2u);
     }
 
     /* C layout of a 32x32 MFMA tile: lane l, element i -> row 8*(i/4) +
