@@ -470,8 +470,8 @@ __device__ __forceinline__ bool better(float s, u32 id, float bs, u32 bid) {
  * grid; a wavefront loads its next group while it reduces the current one.
  *  EPI_LINEAR: y[r] = f16(W_r.xin (+ res[r]))
  *  EPI_SWIGLU: y[r] = f16(silu(W_r.xin) * (W2_r.xin))
- *  EPI_ARGMAX: per-block best (score, row) into part[2*block] (NaN skipped,
- *              ties to the lower row). */
+ *  EPI_ARGMAX: the block's best (score, row) in thread 0's best/best_id
+ *              (NaN skipped, ties to the lower row). */
 template <int QT, int LPR, int J, int EPI>
 __device__ __forceinline__ void stream_rows(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
                                             const uint8_t *__restrict__ W2, const h16 *__restrict__ S2, u32 rows,
@@ -561,19 +561,18 @@ __device__ __forceinline__ void stream_rows(const uint8_t *__restrict__ W, const
     }
 }
 
+/* GEMV launch of stream_rows (EPI_LINEAR, EPI_SWIGLU; the LM head's
+ * EPI_ARGMAX runs inside k_lm_select). */
 template <int QT, int LPR, int J, int EPI>
 __global__ __launch_bounds__(BLOCK) void k_stream(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
                                                   const uint8_t *__restrict__ W2, const h16 *__restrict__ S2,
                                                   u32 rows, u32 K, const h16 *__restrict__ x,
                                                   const h16 *__restrict__ nw, const h16 *__restrict__ res,
-                                                  h16 *__restrict__ y, u32 *__restrict__ part) {
+                                                  h16 *__restrict__ y) {
+    static_assert(EPI != EPI_ARGMAX, "the argmax epilogue runs in k_lm_select");
     float b = -INFINITY;
     u32 bi = NONE_ID;
     stream_rows<QT, LPR, J, EPI>(W, S, W2, S2, rows, K, x, nw, res, y, b, bi);
-    if (EPI == EPI_ARGMAX && threadIdx.x == 0) {
-        part[2u * blockIdx.x] = __float_as_uint(b);
-        part[2u * blockIdx.x + 1u] = bi;
-    }
 }
 
 __global__ __launch_bounds__(BLOCK) void k_rmsnorm(const h16 *x, const h16 *nw, u32 n, h16 *y) {
@@ -1397,28 +1396,24 @@ static u32 resident_blocks(KFn fn) {
 
 template <int QT, int LPR, int J, int EPI>
 static void launch_stream_lj(hipStream_t st, uocr_qmat W, uocr_qmat W2, u32 rows, u32 K, const uint16_t *x,
-                             const uint16_t *nw, const uint16_t *res, uint16_t *y, u32 *part, u32 max_blocks,
-                             u32 *nb_out) {
+                             const uint16_t *nw, const uint16_t *res, uint16_t *y) {
     constexpr u32 R = 64u / LPR;
     auto fn = k_stream<QT, LPR, J, EPI>;
     const u32 groups = (rows + R - 1u) / R;
     u32 nb = (groups + NWAVE - 1u) / NWAVE;
     const u32 cap = resident_blocks(fn);
     if (nb > cap) nb = cap;
-    if (nb > max_blocks) nb = max_blocks;
-    if (nb_out != nullptr) *nb_out = nb;
     hipLaunchKernelGGL(fn, dim3(nb), dim3(BLOCK), 0, st, (const uint8_t *)W.w, (const h16 *)W.s,
                        (const uint8_t *)W2.w, (const h16 *)W2.s, rows, K, (const h16 *)x, (const h16 *)nw,
-                       (const h16 *)res, (h16 *)y, part);
+                       (const h16 *)res, (h16 *)y);
 }
 
 template <int QT, int EPI>
 static void launch_stream(hipStream_t st, uocr_qmat W, uocr_qmat W2, u32 rows, u32 K, const uint16_t *x,
-                          const uint16_t *nw, const uint16_t *res, uint16_t *y, u32 *part, u32 max_blocks,
-                          u32 *nb_out) {
+                          const uint16_t *nw, const uint16_t *res, uint16_t *y) {
     const u32 C = chunks_of(QT, K);
     const u32 lpr = lpr_for(C), j = (C + lpr - 1u) / lpr;
-#define LS(L, JJ) launch_stream_lj<QT, L, JJ, EPI>(st, W, W2, rows, K, x, nw, res, y, part, max_blocks, nb_out)
+#define LS(L, JJ) launch_stream_lj<QT, L, JJ, EPI>(st, W, W2, rows, K, x, nw, res, y)
     switch (lpr) {
         case 4: if (j <= 5) LS(4, 5); else LS(4, 7); break;
         case 8: if (j <= 5) LS(8, 5); else LS(8, 7); break;
@@ -1435,9 +1430,9 @@ extern "C" hipError_t uocr_launch_gemv(hipStream_t st, uocr_qmat W, uint32_t row
         return hipErrorInvalidValue;
     }
     switch (W.qtype) {
-        case UOCR_QT_F16: launch_stream<1, EPI_LINEAR>(st, W, W, rows, K, x, nw, res, y, nullptr, 0xffffffffu, nullptr); break;
-        case UOCR_QT_Q8: launch_stream<3, EPI_LINEAR>(st, W, W, rows, K, x, nw, res, y, nullptr, 0xffffffffu, nullptr); break;
-        default: launch_stream<4, EPI_LINEAR>(st, W, W, rows, K, x, nw, res, y, nullptr, 0xffffffffu, nullptr); break;
+        case UOCR_QT_F16: launch_stream<1, EPI_LINEAR>(st, W, W, rows, K, x, nw, res, y); break;
+        case UOCR_QT_Q8: launch_stream<3, EPI_LINEAR>(st, W, W, rows, K, x, nw, res, y); break;
+        default: launch_stream<4, EPI_LINEAR>(st, W, W, rows, K, x, nw, res, y); break;
     }
     return hipGetLastError();
 }
@@ -1449,9 +1444,9 @@ extern "C" hipError_t uocr_launch_swiglu(hipStream_t st, uocr_qmat G, uocr_qmat 
         return hipErrorInvalidValue;
     }
     switch (G.qtype) {
-        case UOCR_QT_F16: launch_stream<1, EPI_SWIGLU>(st, G, U, rows, K, x, nw, nullptr, mid, nullptr, 0xffffffffu, nullptr); break;
-        case UOCR_QT_Q8: launch_stream<3, EPI_SWIGLU>(st, G, U, rows, K, x, nw, nullptr, mid, nullptr, 0xffffffffu, nullptr); break;
-        default: launch_stream<4, EPI_SWIGLU>(st, G, U, rows, K, x, nw, nullptr, mid, nullptr, 0xffffffffu, nullptr); break;
+        case UOCR_QT_F16: launch_stream<1, EPI_SWIGLU>(st, G, U, rows, K, x, nw, nullptr, mid); break;
+        case UOCR_QT_Q8: launch_stream<3, EPI_SWIGLU>(st, G, U, rows, K, x, nw, nullptr, mid); break;
+        default: launch_stream<4, EPI_SWIGLU>(st, G, U, rows, K, x, nw, nullptr, mid); break;
     }
     return hipGetLastError();
 }
