@@ -104,6 +104,20 @@ def test_lm_head_argmax_bit_exact(gpu, oracle, qtype, vocab, seed):
     assert int(dtok.download(np.int32)[0]) == got
 
 
+def test_fresh_workspaces_read_zero(gpu):
+    """uocr_hip_alloc zero-fills on the library stream before returning, so
+    a new workspace reads as zero to the next operator even when its memory
+    was just released by a buffer full of non-zero bytes."""
+    uocr = gpu
+    nbytes = uocr.load_library().uocr_op_workspace_bytes()
+    for _ in range(4):
+        junk = uocr.DeviceBuffer(nbytes)
+        junk.upload(np.full(nbytes, 0xA5, np.uint8))
+        del junk
+        ws = uocr.workspace()
+        assert not ws.download(np.uint8).any()
+
+
 def test_lm_head_ties_and_nan_rows(gpu, oracle):
     uocr = gpu
     rng = np.random.default_rng(77)

@@ -353,6 +353,9 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
         if (ws2 != sl.gu_w_stride || ss2 != sl.gu_s_stride) return bfail(err, err_size, "expert gate/up slabs differ in stride");
     }
     if (p.off > total) return bfail(err, err_size, "weight arena overflow");
+    /* the uploads ran on the null stream; the engine's stream is non-blocking,
+     * so wait for them before any kernel can read the weights */
+    HIPCHK(hipDeviceSynchronize(), "weight upload sync");
     ctx->mapped = 1;
     return 1;
 }
@@ -397,7 +400,10 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_pnt = p.take(4u), o_plt = p.take(PK * 4u), o_plp = p.take(PK * 4u);
     const uint64_t total = p.off;
     HIPCHK(hipMalloc((void **)&ctx->rarena, total), "runtime arena allocation");
-    HIPCHK(hipMemset(ctx->rarena, 0, total), "runtime arena clear");
+    /* cleared on the engine's stream (non-blocking, so not ordered against a
+     * null-stream hipMemset) and waited for */
+    HIPCHK(hipMemsetAsync(ctx->rarena, 0, total, ctx->stream), "runtime arena clear");
+    HIPCHK(hipStreamSynchronize(ctx->stream), "runtime arena clear sync");
     uint8_t *b = ctx->rarena;
     ctx->kc = (uint16_t *)(b + o_kc);
     ctx->vc = (uint16_t *)(b + o_vc);

@@ -435,9 +435,11 @@ extern "C" void *uocr_hip_alloc(size_t bytes) {
         op_fail(UOCR_ERROR_OUT_OF_MEMORY, "hipMalloc(%zu) failed", bytes);
         return nullptr;
     }
-    /* zeroed: operator workspaces rely on it (the LM-head selection's keys
-     * and ticket counter start at zero and are left at zero) */
-    if (hipMemset(p, 0, bytes) != hipSuccess) {
+    /* zeroed on the library stream and waited for (a plain hipMemset runs on
+     * the null stream, which the non-blocking library stream does not order
+     * against): operator workspaces rely on it, the LM-head selection's keys
+     * and ticket counter start at zero */
+    if (hipMemsetAsync(p, 0, bytes, g_stream) != hipSuccess || hipStreamSynchronize(g_stream) != hipSuccess) {
         (void)hipFree(p);
         op_fail(UOCR_ERROR_INTERNAL, "hipMemset(%zu) failed", bytes);
         return nullptr;
