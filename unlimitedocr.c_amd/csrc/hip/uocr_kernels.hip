@@ -319,17 +319,29 @@ struct RowFrag {
     h16 s[J];
 };
 
-template <int QT, int LPR, int J>
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+
+/* NT: non-temporal loads, for weights read once per token (the LM head, the
+ * routed experts), so they do not displace reused weights from the caches. */
+template <int QT, int LPR, int J, bool NT = false>
 __device__ __forceinline__ void frag_load(RowFrag<J> &f, const uint8_t *W, const h16 *S, u32 C, u32 sub) {
     /* branch-free: chunks past the row re-read its last chunk and are
      * dropped in frag_dot, so no wait lands between the loads */
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const u32 c = min(sub + LPR * j, C - 1u);
-        f.w[j] = *(const uint4 *)(W + 16u * c);
-        if (QT != 1) f.s[j] = S[c / chunks_per_group<QT>()];
+        if (NT) {
+            f.w[j] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4v *)(W + 16u * c)));
+            if (QT != 1) f.s[j] = __builtin_nontemporal_load(S + c / chunks_per_group<QT>());
+        } else {
+            f.w[j] = *(const uint4 *)(W + 16u * c);
+            if (QT != 1) f.s[j] = S[c / chunks_per_group<QT>()];
+        }
     }
 }
+#ifndef UOCR_NT_STREAM
+#define UOCR_NT_STREAM true
+#endif
 
 /* Lane-partial dot of a loaded row with the LDS activation xs. */
 template <int QT, int LPR, int J>
@@ -494,7 +506,7 @@ __device__ __forceinline__ void stream_rows(const uint8_t *__restrict__ W, const
     RowFrag<J> fa[NM], fb[NM];
     auto load = [&](RowFrag<J>(&f)[NM], u32 gg) {
         const u32 r = min(gg * R + grp, rows - 1u);
-        frag_load<QT, LPR, J>(f[0], W + (size_t)r * rb, S + (size_t)r * G, C, sub);
+        frag_load<QT, LPR, J, EPI == EPI_ARGMAX && UOCR_NT_STREAM>(f[0], W + (size_t)r * rb, S + (size_t)r * G, C, sub);
         if (NM == 2) frag_load<QT, LPR, J>(f[NM - 1], W2 + (size_t)r * rb, S2 + (size_t)r * G, C, sub);
     };
     float bs = -INFINITY;
@@ -1059,9 +1071,9 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl
     for (int k = 1; k < UOCR_K_TOPK; ++k) e = rank == (u32)k ? sid[k] : e;
     e = e < UOCR_K_EXPERTS ? e : 0u;
     RowFrag<J> fg, fu;
-    frag_load<QT, LPR, J>(fg, (const uint8_t *)sl.gate.w + e * sl.gu_w_stride + (size_t)col * rb,
+    frag_load<QT, LPR, J, UOCR_NT_STREAM>(fg, (const uint8_t *)sl.gate.w + e * sl.gu_w_stride + (size_t)col * rb,
                           (const h16 *)sl.gate.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
-    frag_load<QT, LPR, J>(fu, (const uint8_t *)sl.up.w + e * sl.gu_w_stride + (size_t)col * rb,
+    frag_load<QT, LPR, J, UOCR_NT_STREAM>(fu, (const uint8_t *)sl.up.w + e * sl.gu_w_stride + (size_t)col * rb,
                           (const h16 *)sl.up.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
     const float inv = stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
     if (FOLD && blockIdx.x == 0u && wave == 0u) {
@@ -1132,7 +1144,7 @@ __global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const u
     RowFrag<JD> fd[UOCR_K_TOPK];
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
-        frag_load<QT, LPR, JD>(fd[r], (const uint8_t *)sl.down.w + e[r] * sl.dn_w_stride + (size_t)cc * 16u * CD,
+        frag_load<QT, LPR, JD, UOCR_NT_STREAM>(fd[r], (const uint8_t *)sl.down.w + e[r] * sl.dn_w_stride + (size_t)cc * 16u * CD,
                                (const h16 *)sl.down.s + e[r] * sl.dn_s_stride + (size_t)cc * GD, CD, sub);
     }
 #pragma unroll
