@@ -624,8 +624,10 @@ __global__ __launch_bounds__(PB) void k_route_rows(const float *__restrict__ log
 }
 
 /* One block: exclusive scan of the 64 bucket sizes, the tile table of the
- * grouped GEMMs (TM rows per tile) and the per-bucket cursors. */
-__global__ __launch_bounds__(64) void k_bucket_scan(const int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
+ * grouped GEMMs (TM rows per tile) and the per-bucket cursors.  The counts
+ * are cleared once read, so the next routing starts from zero without a
+ * memset (the prefill is replayed as a captured graph). */
+__global__ __launch_bounds__(64) void k_bucket_scan(int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                     int32_t *__restrict__ cursors, int32_t *__restrict__ tile_e,
                                                     int32_t *__restrict__ tile_s0, int32_t *__restrict__ tile_s1,
                                                     int32_t *__restrict__ ntiles) {
@@ -647,6 +649,7 @@ __global__ __launch_bounds__(64) void k_bucket_scan(const int32_t *__restrict__ 
     offsets[e] = off[e];
     cursors[e] = 0;
     const int32_t n = counts[e];
+    counts[e] = 0; /* thread 0's scan read every count before the barrier */
     for (int32_t k = 0; k * TM < n; ++k) {
         const int32_t ti = toff[e] + k;
         tile_e[ti] = (int32_t)e;
@@ -794,10 +797,10 @@ extern "C" hipError_t uocr_launch_route_rows(hipStream_t st, const float *logits
         list_tok == nullptr || list_pair == nullptr) {
         return hipErrorInvalidValue;
     }
-    hipError_t e = hipMemsetAsync(counts, 0, 64u * sizeof(int32_t), st);
-    if (e != hipSuccess) return e;
+    /* counts are zero on entry: zero-filled at allocation, cleared again by
+     * k_bucket_scan after every use */
     hipLaunchKernelGGL(k_route_rows, dim3((P + 3u) / 4u), dim3(PB), 0, st, logits, P, norm_topk, ids, wts, counts);
-    hipLaunchKernelGGL(k_bucket_scan, dim3(1), dim3(64), 0, st, (const int32_t *)counts, offsets, cursors, tile_e,
+    hipLaunchKernelGGL(k_bucket_scan, dim3(1), dim3(64), 0, st, counts, offsets, cursors, tile_e,
                        tile_s0, tile_s1, ntiles);
     const u32 n = P * UOCR_K_TOPK;
     hipLaunchKernelGGL(k_bucket_place, dim3((n + PB - 1u) / PB), dim3(PB), 0, st, (const int32_t *)ids, P,
