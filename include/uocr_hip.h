@@ -199,6 +199,16 @@ UOCR_API const char *uocr_hip_op_error(void);
  * error). */
 UOCR_API int uocr_hip_timer_begin(void);
 UOCR_API float uocr_hip_timer_end_ms(void);
+/* One hipGraph of operator calls, for callers that replay a fixed sequence
+ * (benchmarks): begin starts capturing the operator stream, the operator
+ * calls that follow are recorded instead of run, end instantiates the
+ * recording, replay launches it `times` times on the operator stream, release
+ * frees it.  One graph is held at a time; operators that synchronise cannot be
+ * captured. */
+UOCR_API int uocr_hip_capture_begin(void);
+UOCR_API int uocr_hip_capture_end(void);
+UOCR_API int uocr_hip_graph_replay(uint32_t times);
+UOCR_API int uocr_hip_graph_release(void);
 
 #ifdef __cplusplus
 }

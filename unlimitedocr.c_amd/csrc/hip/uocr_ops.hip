@@ -18,6 +18,8 @@ namespace {
 pthread_once_t g_once = PTHREAD_ONCE_INIT;
 hipStream_t g_stream = nullptr;
 hipEvent_t g_ev0 = nullptr, g_ev1 = nullptr;
+hipGraph_t g_graph = nullptr;
+hipGraphExec_t g_graph_exec = nullptr;
 hipError_t g_init_error = hipSuccess;
 thread_local char g_err[512] = "OK";
 
@@ -498,4 +500,36 @@ extern "C" float uocr_hip_timer_end_ms(void) {
         return -1.0f;
     }
     return ms;
+}
+
+extern "C" int uocr_hip_capture_begin(void) {
+    STREAM_OR_RETURN(st);
+    if (g_graph != nullptr || g_graph_exec != nullptr) return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "a graph is held");
+    return hip_status(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capture begin");
+}
+
+extern "C" int uocr_hip_capture_end(void) {
+    STREAM_OR_RETURN(st);
+    int r = hip_status(hipStreamEndCapture(st, &g_graph), "capture end");
+    if (r == UOCR_OK) r = hip_status(hipGraphInstantiate(&g_graph_exec, g_graph, nullptr, nullptr, 0), "instantiate");
+    if (r != UOCR_OK) uocr_hip_graph_release();
+    return r;
+}
+
+extern "C" int uocr_hip_graph_replay(uint32_t times) {
+    STREAM_OR_RETURN(st);
+    if (g_graph_exec == nullptr) return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "no captured graph");
+    for (uint32_t i = 0; i < times; ++i) {
+        int r = hip_status(hipGraphLaunch(g_graph_exec, st), "graph launch");
+        if (r != UOCR_OK) return r;
+    }
+    return UOCR_OK;
+}
+
+extern "C" int uocr_hip_graph_release(void) {
+    if (g_graph_exec != nullptr) (void)hipGraphExecDestroy(g_graph_exec);
+    if (g_graph != nullptr) (void)hipGraphDestroy(g_graph);
+    g_graph_exec = nullptr;
+    g_graph = nullptr;
+    return UOCR_OK;
 }

@@ -146,6 +146,10 @@ SIGNATURES = {
     "uocr_hip_op_error": ([], ct.c_char_p),
     "uocr_hip_timer_begin": ([], ct.c_int),
     "uocr_hip_timer_end_ms": ([], ct.c_float),
+    "uocr_hip_capture_begin": ([], ct.c_int),
+    "uocr_hip_capture_end": ([], ct.c_int),
+    "uocr_hip_graph_replay": ([ct.c_uint32], ct.c_int),
+    "uocr_hip_graph_release": ([], ct.c_int),
     "uocr_synth_model_build": ([_U32, ct.c_uint64, ct.POINTER(_VP), ct.POINTER(_SZ)], ct.c_int),
     "uocr_synth_model_write": ([ct.c_char_p, _U32, ct.c_uint64], ct.c_int),
     "uocr_synth_free": ([_VP], None),
@@ -496,3 +500,23 @@ class Timer:
 
     def __exit__(self, *exc) -> None:
         self.ms = float(load_library().uocr_hip_timer_end_ms())
+
+
+class Capture:
+    """Records the operator calls made inside the block into one hipGraph
+    (uocr_hip_capture_begin/end); `replay(n)` launches it n times."""
+
+    def __enter__(self) -> "Capture":
+        _check_op(load_library().uocr_hip_capture_begin(), "capture begin")
+        return self
+
+    def __exit__(self, exc_type, *exc) -> None:
+        status = load_library().uocr_hip_capture_end()
+        if exc_type is None:
+            _check_op(status, "capture end")
+
+    def replay(self, times: int = 1) -> None:
+        _check_op(load_library().uocr_hip_graph_replay(times), "graph replay")
+
+    def release(self) -> None:
+        load_library().uocr_hip_graph_release()
