@@ -152,10 +152,15 @@ def _q4(rng, rows, k):
     return w, s
 
 
+REPLAY_CAP = None  # --op-replays: fewer replays for counter-collection runs
+
+
 def _graph_time(log, calls, replays: int) -> float:
     """Captures `calls` (a list of zero-argument operator calls) into one
     hipGraph and returns the mean device time per call over `replays`
     replays, HIP events on the operator stream around the replays."""
+    if REPLAY_CAP is not None:
+        replays = max(1, min(replays, REPLAY_CAP))
     with uocr.Capture() as g:
         for c in calls:
             c()
@@ -397,6 +402,10 @@ def main() -> None:
                     help="run only the config-2 LM-head measurement and a copy probe (for rocprofv3 --pmc runs)")
     ap.add_argument("--no-ops", action="store_true", help="skip the config 1/3/4 operator measurements")
     ap.add_argument("--ops-only", action="store_true", help="run only the config 1/3/4 operator measurements")
+    ap.add_argument("--op-replays", type=int, default=None,
+                    help="cap the graph replays of the operator measurements (counter-collection runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the MFMA prefill of the config-5 prompt (Q4 profile, 1 generated token), twice")
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue decode kernels directly instead of replaying hipGraphs (for kernel tracing)")
     args = ap.parse_args()
@@ -415,8 +424,21 @@ def main() -> None:
         print(json.dumps({"roofline": lm_head_roofline(log)}), flush=True)
         copy_probe(log)
         return
+    global REPLAY_CAP
+    REPLAY_CAP = args.op_replays
+    if args.prefill_only:
+        model = uocr.synth_model(uocr.QPROFILE_Q4, 7)
+        ids, mask, rows = make_prompt()
+        with uocr.Engine.from_memory(model, backend="hip", max_prompt_tokens=1024, max_gen_tokens=8) as eng:
+            for _ in range(2):
+                _, _, p_ms, _ = eng.generate_embeddings(ids, mask, rows, 1, flags=uocr.GEN_IGNORE_EOS)
+        gf = prefill_flops(ids.size)
+        print(json.dumps({"prefill": {"ms": round(p_ms, 3), "gflop": round(gf / 1e9, 1),
+                                      "tflops": round(gf / (p_ms / 1e3) / 1e12, 1)}}), flush=True)
+        return
     if args.ops_only:
         print(json.dumps({"operators": operator_benchmarks(log, not args.no_cpu_baseline)}), flush=True)
+        copy_probe(log)
         return
     names = {"q4": uocr.QPROFILE_Q4, "q8": uocr.QPROFILE_Q8, "fp16": uocr.QPROFILE_FP16}
     wanted = ["q4"] + [p for p in args.profiles.split(",") if p in names and p != "q4"]

@@ -721,10 +721,14 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
         h16 h[8];
     };
     h8 kk[ATT_UNROLL], vv[ATT_UNROLL];
+    /* slots past the block's range (or, once the step state is in, past
+     * attn_len) re-read the range's last slot: the re-reads hit the caches
+     * instead of fetching the neighbouring split's slots */
+    int lim = max(iend - 1, 0);
     auto load = [&](int ib) {
 #pragma unroll
         for (int u = 0; u < ATT_UNROLL; ++u) {
-            const int t = min(ib + ATT_GROUPS * u, (int)cap - 1);
+            const int t = min(ib + ATT_GROUPS * u, lim);
             kk[u].u = *(const uint4 *)(kh + (size_t)t * 128u);
             vv[u].u = *(const uint4 *)(vh + (size_t)t * 128u);
         }
@@ -734,6 +738,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
     load(i0 + gid);
     hold(qq.u);
     const int i1 = min(st->attn_len, iend);
+    lim = max(min(i1, iend) - 1, 0);
     float qv[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) qv[j] = (float)qq.h[j];
