@@ -6,9 +6,10 @@
  * All P prompt rows go through each layer together, so the projections are
  * real GEMMs [P x K] x [K x N]:
  *  - k_gemm: 64 x 128 output tiles, K in 64-column steps (one quantisation
- *    group).  Activation tiles are staged in LDS as fp16; weight tiles are
- *    dequantised into LDS as fp16(q * scale), the reference's prefill
- *    staging (gemm_q4.metal:48-55: half(float(q) * scale)), and
+ *    group).  Activation tiles are staged in LDS as fp16 (double-buffered);
+ *    each wavefront dequantises its own 32 weight rows straight into MFMA
+ *    operand registers as fp16(q * scale), the reference's prefill staging
+ *    (gemm_q4.metal:48-55: half(float(q) * scale)), and
  *    v_mfma_f32_32x32x16_f16 accumulates in fp32.  Epilogues: fp16 store with
  *    optional residual, fp32 store, and SwiGLU over two weight matrices.  In
  *    grouped mode a tile table maps each block to an expert's bucket of
@@ -37,9 +38,10 @@ typedef uint32_t u32;
 #define TM 64  /* GEMM tile rows */
 #define TN 128 /* GEMM tile columns */
 #define TK 64  /* one quantisation group */
-#define KG 1   /* quantisation groups per GEMM K step (2 was measured slower: LDS limits the grouped SwiGLU to one block per CU) */
-#define LDA (KG * TK + 8) /* padded LDS row (halves) */
+#define LDA (TK + 8) /* padded LDS row of the activation tile (halves) */
+#ifndef GDEPTH
 #define GDEPTH 3 /* K steps in flight per GEMM block */
+#endif
 
 __device__ __forceinline__ float silu_p(float g) {
     return g / (1.0f + expf(-g));
@@ -60,95 +62,95 @@ __device__ __forceinline__ u32 magic2(u32 v, u32 sel) {
 /* GEMM                                                                      */
 /* ------------------------------------------------------------------------ */
 
-enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2 };
-
-/* One K step's share of this thread: the activation tile piece (two 16-byte
- * loads) and the weight tile piece of each matrix, loaded into registers
- * (gemm_load) several steps ahead and dequantised into LDS (gemm_store)
- * when the step comes up. */
-template <int QT>
-struct WPiece {
-    static constexpr int NV = QT == 4 ? 1 : (QT == 3 ? 2 : 4);
-    uint4 w[NV];
-    u32 s; /* fp16 scale bits */
-};
-
-
-/* thread t: weight row t/2 of the tile; Q4 bytes 16*(t&1)..+15 of the group
- * (low nibbles: columns 16*(t&1)+i, high nibbles the same + 32), Q8 bytes
- * 32*(t&1)..+31, f16 columns 32*(t&1)..+31.  Threads t < TN also load the
- * scale of row t. */
-template <int QT>
-__device__ __forceinline__ void w_load(WPiece<QT> &f, const uint8_t *W, const h16 *S, u32 K, u32 n0, u32 nmax,
-                                       u32 g) {
-    const u32 t = threadIdx.x, r = t >> 1, half = t & 1u, n = min(n0 + r, nmax - 1u);
-    if (QT == 4) {
-        f.w[0] = *(const uint4 *)(W + (size_t)n * (K / 2u) + g * 32u + 16u * half);
-    } else if (QT == 3) {
-        const uint4 *src = (const uint4 *)(W + (size_t)n * K + g * 64u + 32u * half);
-        f.w[0] = src[0];
-        f.w[1] = src[1];
-    } else {
-        const uint4 *src = (const uint4 *)((const h16 *)W + (size_t)n * K + g * 64u + 32u * half);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) f.w[i] = src[i];
+/* f(integral_constant<int, i>) for i = 0..N-1, in order, unrolled at compile
+ * time (register-ring slots need constant indices). */
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
     }
-    if (QT != 1) f.s = ((const unsigned short *)S)[(size_t)n * (K / 64u) + g];
 }
 
-/* Dequantise a loaded piece into the LDS tile as fp16(q * scale) (the
- * product of two fp16 values rounded once, as half(float(q) * scale) in
- * gemm_q4.metal:55; f16: the values). */
+enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2 };
+
+/* Weight piece of one K step (one 64-column quantisation group) for the
+ * weight row n = the output column of this lane, lane half h = lane / 32:
+ *   Q4: bytes 16h..16h+15 of the group (one uint4); f16 / Q8: columns
+ *   32h..32h+31 (Q8 two uint4, f16 four), plus the row's group scale.
+ * A K step is four 16-deep MFMA substeps; substep i takes 8 of these
+ * weights, at the group columns b_koff(i, h)..+7 (any order of the K sum
+ * works as long as the activation operand is read at the same columns):
+ *   Q4: i = 0, 1: low nibbles of bytes 8i..8i+7 (columns 16h + 8i ..);
+ *       i = 2, 3: high nibbles of the same bytes (columns + 32);
+ *   Q8 / f16: columns 32h + 8i ... */
 template <int QT>
-__device__ __forceinline__ void w_store(const WPiece<QT> &f, h16 *ws, bool live) {
-    const u32 t = threadIdx.x, r = t >> 1, half = t & 1u;
+struct BPiece {
+    static constexpr int NV = QT == 4 ? 1 : (QT == 3 ? 2 : 4); /* uint4 loads */
+    static constexpr int NW = 4 * NV;                          /* words */
+};
+
+template <int QT>
+__device__ __forceinline__ u32 b_koff(u32 i, u32 h) {
+    return QT == 4 ? ((i & 2u) << 4) + 16u * h + ((i & 1u) << 3) : 32u * h + 8u * i;
+}
+
+/* The piece is kept as plain words (no struct or vector copies), so the
+ * register ring stays in registers. */
+template <int QT>
+__device__ __forceinline__ void b_load(u32 (&w)[BPiece<QT>::NW], u32 &sc, const uint8_t *W, const h16 *S, u32 K,
+                                       u32 n, u32 g, u32 h) {
+    const uint4 *src = QT == 4 ? (const uint4 *)(W + (size_t)n * (K / 2u) + g * 32u + 16u * h)
+                               : (QT == 3 ? (const uint4 *)(W + (size_t)n * K + g * 64u + 32u * h)
+                                          : (const uint4 *)((const h16 *)W + (size_t)n * K + g * 64u + 32u * h));
+#pragma unroll
+    for (int v = 0; v < BPiece<QT>::NV; ++v) {
+        const uint4 x = src[v];
+        w[4 * v] = x.x;
+        w[4 * v + 1] = x.y;
+        w[4 * v + 2] = x.z;
+        w[4 * v + 3] = x.w;
+    }
+    if (QT != 1) sc = ((const unsigned short *)S)[(size_t)n * (K / 64u) + g];
+}
+
+/* The four B operands (8 fp16 each) of a loaded piece: fp16(q * scale), the
+ * product of two fp16 values rounded once, as half(float(q) * scale) in
+ * gemm_q4.metal:55 (the integer q is exact after the bias subtraction);
+ * f16: the values. */
+template <int QT>
+__device__ __forceinline__ void b_dequant(const u32 (&w)[BPiece<QT>::NW], u32 sc, h16x8 (&b)[4]) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    /* a group past the end of K (odd group count) contributes zeros */
-    const h16 sv = live ? __builtin_bit_cast(h16, (unsigned short)f.s) : (h16)0.0f;
+    const h16 sv = __builtin_bit_cast(h16, (unsigned short)sc);
     const h2 sc2 = {sv, sv};
-    if (QT == 4) {
-        const u32 wv[4] = {f.w[0].x, f.w[0].y, f.w[0].z, f.w[0].w};
-        const h2 bb = __builtin_bit_cast(h2, 0x64086408u); /* (1032, 1032) */
-        union {
-            uint4 u[2];
-            u32 d[8];
-        } lo, hi;
+    union {
+        h16x8 v;
+        u32 d[4];
+    } o;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const u32 l = wv[b] & 0x0F0F0F0Fu, h = (wv[b] >> 4) & 0x0F0F0F0Fu;
-            lo.d[2 * b] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(l, 0x04010400u)) - bb) * sc2);
-            lo.d[2 * b + 1] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(l, 0x04030402u)) - bb) * sc2);
-            hi.d[2 * b] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(h, 0x04010400u)) - bb) * sc2);
-            hi.d[2 * b + 1] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(h, 0x04030402u)) - bb) * sc2);
+    for (int i = 0; i < 4; ++i) {
+        if (QT == 4) {
+            const h2 bb = __builtin_bit_cast(h2, 0x64086408u); /* (1032, 1032) */
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const u32 x = w[2 * (i & 1) + q];
+                const u32 nb = (i & 2) ? (x >> 4) & 0x0F0F0F0Fu : x & 0x0F0F0F0Fu;
+                o.d[2 * q] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(nb, 0x04010400u)) - bb) * sc2);
+                o.d[2 * q + 1] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(nb, 0x04030402u)) - bb) * sc2);
+            }
+        } else if (QT == 3) {
+            const h2 bb = __builtin_bit_cast(h2, 0x64806480u); /* (1152, 1152) */
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const u32 u = w[2 * i + q] ^ 0x80808080u;
+                o.d[2 * q] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(u, 0x04010400u)) - bb) * sc2);
+                o.d[2 * q + 1] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(u, 0x04030402u)) - bb) * sc2);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o.d[q] = w[4 * i + q];
         }
-        uint4 *dl = (uint4 *)(ws + r * LDA + 16u * half);
-        uint4 *dh = (uint4 *)(ws + r * LDA + 32u + 16u * half);
-        dl[0] = lo.u[0];
-        dl[1] = lo.u[1];
-        dh[0] = hi.u[0];
-        dh[1] = hi.u[1];
-    } else if (QT == 3) {
-        const u32 wv[8] = {f.w[0].x, f.w[0].y, f.w[0].z, f.w[0].w, f.w[1].x, f.w[1].y, f.w[1].z, f.w[1].w};
-        const h2 bb = __builtin_bit_cast(h2, 0x64806480u); /* (1152, 1152) */
-        union {
-            uint4 u[4];
-            u32 d[16];
-        } o;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const u32 u = wv[b] ^ 0x80808080u;
-            o.d[2 * b] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(u, 0x04010400u)) - bb) * sc2);
-            o.d[2 * b + 1] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, magic2(u, 0x04030402u)) - bb) * sc2);
-        }
-        uint4 *d = (uint4 *)(ws + r * LDA + 32u * half);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d[i] = o.u[i];
-    } else {
-        uint4 *d = (uint4 *)(ws + r * LDA + 32u * half);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            d[i] = live ? make_uint4(f.w[i].x, f.w[i].y, f.w[i].z, f.w[i].w) : make_uint4(0u, 0u, 0u, 0u);
-        }
+        b[i] = o.v;
     }
 }
 
@@ -168,16 +170,17 @@ struct GemmArgs {
     u32 ldr;
 };
 
-/* C[m][n] = sum_k A[m][k] W[n][k] over one 64 x 128 tile per block; 4
- * wavefronts, each 32 rows x 64 columns (two 32x32 MFMA tiles). */
+/* C[m][n] = sum_k A[m][k] W[n][k] over one 64 x 128 tile per block.  Wave
+ * w owns output columns 32w..32w+31 (its weight rows, dequantised straight
+ * into MFMA B operands in registers) for all 64 rows (two 32x32 MFMA
+ * tiles); only the activation tile goes through LDS, double-buffered, so a
+ * K step has one barrier and LDS carries one activation read per MFMA. */
 template <int QT, int EPI, bool GROUPED>
 __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     constexpr int NMAT = EPI == GE_SWIGLU ? 2 : 1;
-    __shared__ __attribute__((aligned(16))) h16 as[TM * LDA];
-    __shared__ __attribute__((aligned(16))) h16 wsm[NMAT][TN * LDA];
+    __shared__ __attribute__((aligned(16))) h16 as[2][TM * LDA];
     __shared__ int32_t arow[TM], orow[TM];
-    const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    const u32 wm = wave & 1u, wn = wave >> 1;
+    const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6, hf = lane >> 5;
     u32 n0 = blockIdx.y * TN, rows = p.M, e = 0, s0 = 0;
     if (GROUPED) {
         if ((int)blockIdx.x >= *p.ntiles) return;
@@ -205,10 +208,12 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
         nbase = sgi * p.nseg;
     }
     const u32 nmax = (p.nseg != 0u ? p.nseg : p.N);
-    const uint8_t *w0 = (const uint8_t *)W0.w + (GROUPED ? e * p.w_stride : 0);
-    const h16 *s0p = (const h16 *)W0.s + (GROUPED ? e * p.s_stride : 0);
-    const uint8_t *w1 = NMAT == 2 ? (const uint8_t *)W1.w + (GROUPED ? e * p.w_stride : 0) : nullptr;
-    const h16 *s1p = NMAT == 2 ? (const h16 *)W1.s + (GROUPED ? e * p.s_stride : 0) : nullptr;
+    const uint8_t *wp[2] = {(const uint8_t *)W0.w + (GROUPED ? e * p.w_stride : 0),
+                            NMAT == 2 ? (const uint8_t *)W1.w + (GROUPED ? e * p.w_stride : 0) : nullptr};
+    const h16 *sp[2] = {(const h16 *)W0.s + (GROUPED ? e * p.s_stride : 0),
+                        NMAT == 2 ? (const h16 *)W1.s + (GROUPED ? e * p.s_stride : 0) : nullptr};
+    /* this lane's weight row (clamped; columns past N are not stored) */
+    const u32 nrow = min(n0 - nbase + 32u * wave + (lane & 31u), nmax - 1u);
     __syncthreads();
 
     f32x16 acc[NMAT][2];
@@ -219,104 +224,74 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[m][j][i] = 0.0f;
 
-    /* K steps of KG groups run GDEPTH deep: step s's loads were issued
-     * GDEPTH steps earlier into a register ring (constant indices only, so
-     * the ring stays in registers), and the MFMAs of one step overlap the
-     * loads of the next ones */
-    const u32 G = p.K / TK, NS = (G + KG - 1u) / KG;
-    constexpr int NV = WPiece<QT>::NV, NA = KG * 2; /* 16-byte activation pieces per thread */
-    u32 ka[GDEPTH][NA][4]; /* words, not uint4: no struct copies, so they stay in registers */
-    uint4 kw[GDEPTH][NMAT][KG][NV];
-    u32 kscale[GDEPTH][NMAT][KG];
-    const uint8_t *wp[2] = {w0, w1};
-    const h16 *sp[2] = {s0p, s1p};
+    /* K steps run GDEPTH deep: step s's loads were issued GDEPTH steps
+     * earlier into a register ring (constant indices only, so the ring stays
+     * in registers) */
+    /* the lambdas below see plain locals: a reference to the kernel
+     * argument struct would copy it to private memory */
+    const h16 *Ap = p.A;
+    const u32 lda = p.lda, Kd = p.K;
+    const u32 NS = Kd / TK;
+    u32 ka[GDEPTH][2][4]; /* words, not uint4: no struct copies, so they stay in registers */
+    u32 kb[GDEPTH][NMAT][BPiece<QT>::NW], ks[GDEPTH][NMAT];
     auto issue = [&](auto D, u32 st) {
         constexpr int d = decltype(D)::value;
 #pragma unroll
-        for (int q = 0; q < NA; ++q) {
-            const u32 idx = t + q * PB, r = idx / (KG * 8u), c8 = idx % (KG * 8u);
-            /* columns past K (odd group count) read the row's last piece;
-             * their weights are zero */
-            const u32 col = min(st * KG * TK + 8u * c8, p.K - 8u);
-            const uint4 v = *(const uint4 *)(p.A + (size_t)arow[r] * p.lda + col);
+        for (int q = 0; q < 2; ++q) {
+            const u32 idx = t + q * PB, r = idx >> 3, c8 = idx & 7u;
+            const uint4 v = *(const uint4 *)(Ap + (size_t)arow[r] * lda + st * TK + 8u * c8);
             ka[d][q][0] = v.x;
             ka[d][q][1] = v.y;
             ka[d][q][2] = v.z;
             ka[d][q][3] = v.w;
         }
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-#pragma unroll
-            for (int k = 0; k < KG; ++k) {
-                WPiece<QT> f;
-                w_load<QT>(f, wp[m], sp[m], p.K, n0 - nbase, nmax, min(st * KG + k, G - 1u));
-#pragma unroll
-                for (int v = 0; v < NV; ++v) kw[d][m][k][v] = make_uint4(f.w[v].x, f.w[v].y, f.w[v].z, f.w[v].w);
-                kscale[d][m][k] = f.s;
-            }
-        }
+        for (int m = 0; m < NMAT; ++m) b_load<QT>(kb[d][m], ks[d][m], wp[m], sp[m], Kd, nrow, st, hf);
     };
     auto step = [&](auto D, u32 st) {
         constexpr int d = decltype(D)::value;
+        h16 *ab = as[st & 1u];
 #pragma unroll
-        for (int q = 0; q < NA; ++q) {
-            const u32 idx = t + q * PB, r = idx / (KG * 8u), c8 = idx % (KG * 8u);
-            *(uint4 *)(as + r * LDA + 8u * c8) = make_uint4(ka[d][q][0], ka[d][q][1], ka[d][q][2], ka[d][q][3]);
+        for (int q = 0; q < 2; ++q) {
+            const u32 idx = t + q * PB, r = idx >> 3, c8 = idx & 7u;
+            *(uint4 *)(ab + r * LDA + 8u * c8) = make_uint4(ka[d][q][0], ka[d][q][1], ka[d][q][2], ka[d][q][3]);
         }
+        h16x8 bop[NMAT][4];
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-#pragma unroll
-            for (int k = 0; k < KG; ++k) {
-                WPiece<QT> f;
-#pragma unroll
-                for (int v = 0; v < NV; ++v) {
-                    f.w[v] = make_uint4(kw[d][m][k][v].x, kw[d][m][k][v].y, kw[d][m][k][v].z, kw[d][m][k][v].w);
-                }
-                f.s = kscale[d][m][k];
-                w_store<QT>(f, wsm[m] + k * TK, st * KG + k < G);
-            }
-        }
+        for (int m = 0; m < NMAT; ++m) b_dequant<QT>(kb[d][m], ks[d][m], bop[m]);
+        /* the other buffer's readers (step st - 1) all passed this barrier
+         * before anyone writes it again at step st + 1 */
         __syncthreads();
-        /* refill this ring slot with step st + GDEPTH while the MFMAs run */
         if (st + GDEPTH < NS) issue(D, st + GDEPTH);
 #pragma unroll
-        for (u32 kk = 0; kk < KG * TK; kk += 16) {
-            U4H8 a;
-            a.u = *(const uint4 *)(as + (32u * wm + (lane & 31u)) * LDA + kk + 8u * (lane >> 5));
+        for (u32 i = 0; i < 4; ++i) {
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m) {
+            for (int j = 0; j < 2; ++j) {
+                U4H8 a;
+                a.u = *(const uint4 *)(ab + (32u * j + (lane & 31u)) * LDA + b_koff<QT>(i, hf));
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    U4H8 b;
-                    b.u = *(const uint4 *)(wsm[m] + (64u * wn + 32u * j + (lane & 31u)) * LDA + kk + 8u * (lane >> 5));
-                    acc[m][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.v, b.v, acc[m][j], 0, 0, 0);
+                for (int m = 0; m < NMAT; ++m) {
+                    acc[m][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.v, bop[m][i], acc[m][j], 0, 0, 0);
                 }
             }
         }
-        __syncthreads();
     };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    static_assert(GDEPTH == 3, "the ring below is written out for three slots");
-    issue(I0{}, 0u);
-    issue(I1{}, min(1u, NS - 1u));
-    issue(I2{}, min(2u, NS - 1u));
-    for (u32 st = 0; st < NS; st += 3u) {
-        step(I0{}, st);
-        if (st + 1u < NS) step(I1{}, st + 1u);
-        if (st + 2u < NS) step(I2{}, st + 2u);
+    static_for<GDEPTH>([&](auto D) { issue(D, min((u32)decltype(D)::value, NS - 1u)); });
+    for (u32 st = 0; st < NS; st += GDEPTH) {
+        static_for<GDEPTH>([&](auto D) {
+            if (st + (u32)decltype(D)::value < NS) step(D, st + (u32)decltype(D)::value);
+        });
     }
 
     /* C layout of a 32x32 MFMA tile: lane l, element i -> row 8*(i/4) +
      * 4*(l/32) + i%4, column l%32 */
+    const u32 col = n0 + 32u * wave + (lane & 31u);
+    if (col >= p.N) return;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const u32 col = n0 + 64u * wn + 32u * j + (lane & 31u);
-        if (col >= p.N) continue;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const u32 r = 32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4);
+            const u32 r = 32u * j + 8u * (i / 4) + 4u * hf + (i % 4);
             if (r >= rows) continue;
             const size_t orw = (size_t)orow[r];
             if (EPI == GE_F32) {
