@@ -140,6 +140,24 @@ def lm_head_roofline(log, iters: int = 60) -> dict:
             "launches": iters}
 
 
+def algo_bytes_gemv_q8(rows: int = 6848, k: int = 1280) -> int:
+    """Config 1: Q8 payload + fp16 group scales + x + y."""
+    return rows * k + rows * (k // 64) * 2 + k * 2 + rows * 2
+
+
+def algo_bytes_moe_q4() -> int:
+    """Config 3 per token: fp16 router + merged shared gate/up/down (1792) +
+    6 routed experts (gate/up/down 896), Q4 with scales, + hidden in/out."""
+    E, I, H, SI = 64, 896, 1280, 1792
+    return E * H * 2 + 3 * (SI * H // 2 + SI * H // 64 * 2) + 6 * 3 * (I * H // 2 + I * H // 64 * 2) + 2 * H * 2
+
+
+def algo_bytes_attention_q8(context: int) -> int:
+    """Config 4: Q8 q/k/v/o (payload + scales) + K and V of `context` slots
+    (10 heads x 128 fp16 each) + hidden in/out and the new K/V row."""
+    return 4 * (1280 * 1280 + 1280 * 20 * 2) + 5120 * context + 10240
+
+
 def _q8(rng, rows, k):
     w = rng.integers(-127, 128, size=(rows, k), dtype=np.int8)
     s = (np.abs(rng.standard_normal((rows, k // 64))) * 0.02 / 127).astype(np.float16)
@@ -221,7 +239,7 @@ def operator_benchmarks(log, with_cpu: bool = True, cpu_budget_s: float = 2.0) -
     del copies
     xb = x.view(np.uint16)
     cpu_s, cpu_n = _cpu_time(lambda: oracle.gemv(3, w, s, 6848, 1280, xb), cpu_budget_s) if with_cpu else (0.0, 0)
-    algo = 6848 * 1280 + 6848 * 20 * 2 + 1280 * 2 + 6848 * 2
+    algo = algo_bytes_gemv_q8()
     out["config1_q8_gemv"] = _entry("Q8_0 GEMV 6848x1280 (k_stream)", algo, cold, hot, cpu_s, cpu_n, cores,
                                     f"{n_copy} weight copies (543 MB) for cold; 1020 calls")
     log(f"config 1: {out['config1_q8_gemv']}")
@@ -270,7 +288,7 @@ def operator_benchmarks(log, with_cpu: bool = True, cpu_budget_s: float = 2.0) -
     cold = _graph_time(log, [moe_call(t, mws[t % 5]) for t in range(n_tok)], 2)
     hot = _graph_time(log, [moe_call(t, mws[0]) for t in range(n_tok)], 2)
     del keep, mws
-    algo = E * H * 2 + 3 * (SI * H // 2 + SI * H // 64 * 2) + 6 * 3 * (I * H // 2 + I * H // 64 * 2) + 2 * H * 2
+    algo = algo_bytes_moe_q4()
     cpu_s, cpu_n = 0.0, 0
     if with_cpu:
         ev = oracle.ExpertView()
@@ -330,7 +348,7 @@ def operator_benchmarks(log, with_cpu: bool = True, cpu_budget_s: float = 2.0) -
                 oracle.gemv(3, W[3][0], W[3][1], 1280, 1280, ctx, h.view(np.uint16))
 
             cpu_s, cpu_n = _cpu_time(cpu_block, cpu_budget_s)
-        algo = 4 * (1280 * 1280 + 1280 * 20 * 2) + 5120 * L + 10240
+        algo = algo_bytes_attention_q8(L)
         key = f"config4_attention_L{L}"
         out[key] = _entry(f"attention decode layer, Q8 q/k/v/o, context {L}", algo, cold, hot, cpu_s, cpu_n, cores,
                           f"{n_copy} copies of weights + KV for cold")
