@@ -67,6 +67,44 @@ def test_generate_matches_oracle(gpu, oracle, qprofile):
     assert best >= 3
 
 
+def test_converted_model_matches_oracle(gpu, oracle):
+    """A checkpoint converted by uocr_convert (the fp16 synthetic model's
+    values as the source, mixed-q4 output) generates on the HIP engine with
+    the greedy ids the oracle computes on the same converted bytes."""
+    import sys
+    from pathlib import Path
+
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "unlimitedocr.c_amd"))
+    import uocr_convert
+
+    uocr = gpu
+    m = model(uocr, 1)
+    v = m.view()
+    by_id = {uocr_convert.decoder_entry(n)[0]: n for n in uocr_convert.decoder_tensor_names()}
+    src = {}
+    for e in uocr.tensor_table(v):
+        shape = (int(e["lshape"][0]),) if int(e["rank"]) == 1 else (int(e["lshape"][0]), int(e["lshape"][1]))
+        off, size = int(e["payload_offset"]), int(e["payload_size"])
+        src[by_id[int(e["id"])]] = v[off:off + size].view(np.float16).reshape(shape)
+    conv, summary = uocr_convert.convert(src, "mixed-q4")
+    assert summary["qtypes"]["q4_0"] == 2150
+    eng = uocr.Engine.from_memory(conv, backend="hip", max_prompt_tokens=64, max_gen_tokens=16)
+    orc = oracle.Model(conv.ptr, conv.size, conv, prompt_capacity=64)
+    best = 0
+    for seed in range(3):
+        rng = np.random.default_rng(700 + seed)
+        ids, mask, rows = prompt(rng, 10, 6)
+        got, _, _, _ = eng.generate_embeddings(ids, mask, rows, max_new_tokens=8, flags=uocr.GEN_IGNORE_EOS)
+        ref, margins = orc.generate(ids, mask, rows.view(np.uint16), max_new=8, ignore_eos=True)
+        best = max(best, compare_ids(got.tolist(), ref.tolist(), margins.tolist()))
+        if best >= 3:
+            break
+    orc.close()
+    eng.close()
+    conv.close()
+    assert best >= 3
+
+
 def test_graph_and_eager_paths_agree(gpu):
     uocr = gpu
     m = model(uocr, 3)

@@ -18,7 +18,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from conftest import dequant, q4_weights, q8_weights, rand_f16
+from conftest import convert_q4, convert_q8, dequant, q4_weights, q8_weights, rand_f16
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "cpu_ref_tiny_golden.json").read_text())
 
@@ -243,32 +243,6 @@ def test_against_reference_cpu_ref_build(oracle):
 # ---------------------------------------------------------------------------
 # quantised formats: the converter's algorithm, restated from convert.py
 # ---------------------------------------------------------------------------
-
-def convert_q8(values: np.ndarray):
-    """convert.py:2058-2063: scale = max|x|/127 (1.0 for an all-zero group), q = clip(rint(x/scale))."""
-    rows, cols = values.shape
-    g = values.reshape(rows, cols // 64, 64)
-    max_abs = np.max(np.abs(g), axis=2)
-    scales = np.where(max_abs == 0.0, np.float32(1.0), max_abs / np.float32(127)).astype(np.float32)
-    q = np.clip(np.rint(g / scales[:, :, None]), -127, 127).astype(np.int8)
-    return q.reshape(rows, cols), scales.astype(np.float16)
-
-
-def convert_q4(values: np.ndarray):
-    """convert.py:2249-2276: signed max / -8 -> fp16 scale, rint/clip to [-8,7], nibble q+8, half-split pack."""
-    rows, cols = values.shape
-    g = values.reshape(rows, cols // 64, 64)
-    idx = np.argmax(np.abs(g), axis=2)
-    signed_max = np.take_along_axis(g, idx[:, :, None], axis=2)[:, :, 0]
-    s16 = (signed_max / np.float32(-8)).astype(np.float16)
-    s32 = s16.astype(np.float32)
-    safe = np.where(s32 == 0.0, np.float32(1.0), s32)
-    q = np.clip(np.rint(g / safe[:, :, None]), -8, 7).astype(np.int8)
-    deq = (q.astype(np.float32) * s32[:, :, None]).reshape(rows, cols)
-    biased = (q.astype(np.int16) + 8).astype(np.uint8)
-    packed = (biased[:, :, :32] | (biased[:, :, 32:] << 4)).astype(np.uint8)
-    return packed.reshape(rows, cols // 2), s16, deq
-
 
 @pytest.mark.parametrize("qtype", [3, 4])
 def test_weight_storage_matches_converter(oracle, qtype):

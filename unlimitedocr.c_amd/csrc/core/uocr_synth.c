@@ -6,7 +6,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "uocr_convert.h"
 #include "uocr_format.h"
+#include "uocr_half.h"
 
 #define ROW_BLOCK 64u
 
@@ -35,26 +37,6 @@ static double unif(uint64_t *s) {
 static double gauss(uint64_t *s) {
     const double u1 = unif(s), u2 = unif(s);
     return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
-}
-
-/* fp32 -> fp16 bits, round to nearest even */
-static uint16_t to_half(float f) {
-    uint32_t x;
-    memcpy(&x, &f, 4);
-    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
-    const uint32_t ax = x & 0x7fffffffu;
-    if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
-    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
-    if (ax < 0x38800000u) {
-        float a;
-        memcpy(&a, &ax, 4);
-        return (uint16_t)(sign | (uint16_t)rintf(a * 16777216.0f));
-    }
-    const uint32_t m = ax & 0x7fffffu;
-    uint32_t h = (((ax >> 23) - 112u) << 10) | (m >> 13);
-    const uint32_t rem = m & 0x1fffu;
-    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
-    return (uint16_t)(sign | h);
 }
 
 static uint32_t qtype_for(uint32_t qprofile, uint32_t family) {
@@ -141,7 +123,7 @@ static void fill_block(uint8_t *img, const synth_tensor *t, uint32_t r0, uint32_
                                       (double)(u >> 48)) / 65536.0 - 2.0;
                     v = (float)(g * 1.7320508075688772 * (t->kind == 2u ? 0.03 : 0.01));
                 }
-                w[(size_t)r * K + c] = to_half(v);
+                w[(size_t)r * K + c] = uocr_half_bits(v);
             }
         }
         return;
@@ -174,11 +156,13 @@ static void fill_block(uint8_t *img, const synth_tensor *t, uint32_t r0, uint32_
     const uint32_t G = K / UOCR_QGROUP;
     const double div = t->qtype == UOCR_TENSOR_Q8_0 ? 127.0 : 7.0;
     for (uint32_t r = r0; r < r1; ++r) {
-        for (uint32_t g = 0; g < G; ++g) sc[(size_t)r * G + g] = to_half((float)(fabs(gauss(&s) * 0.02) / div));
+        for (uint32_t g = 0; g < G; ++g) sc[(size_t)r * G + g] = uocr_half_bits((float)(fabs(gauss(&s) * 0.02) / div));
     }
 }
 
-int uocr_synth_model_build(uint32_t qprofile, uint64_t seed, void **out_data, size_t *out_size) {
+/* The image of qprofile; with fill, every tensor takes its seeded synthetic
+ * values, else the tensor data stays zero (the converter's skeleton). */
+static int build_image(uint32_t qprofile, uint64_t seed, int fill, void **out_data, size_t *out_size) {
     if (out_data == NULL || out_size == NULL) return UOCR_ERROR_INVALID_ARGUMENT;
     *out_data = NULL;
     *out_size = 0u;
@@ -192,21 +176,40 @@ int uocr_synth_model_build(uint32_t qprofile, uint64_t seed, void **out_data, si
     const uint64_t dir_off = 512u;
     const uint64_t dir_size = sizeof(uocr_tensor_directory_header) + (uint64_t)n * sizeof(uocr_tensor_entry);
     const uint64_t data_off = up(dir_off + dir_size, UOCR_TENSOR_DATA_ALIGNMENT);
-    uint64_t off = data_off;
     for (uint32_t i = 0; i < n; ++i) {
         const uint64_t elems = (uint64_t)t[i].rows * t[i].cols;
-        t[i].w_off = off;
         if (t[i].qtype == UOCR_TENSOR_F16) {
             t[i].w_bytes = elems * 2u;
         } else {
             t[i].w_bytes = t[i].qtype == UOCR_TENSOR_Q8_0 ? elems : elems / 2u;
             t[i].s_bytes = (uint64_t)t[i].rows * (t[i].cols / UOCR_QGROUP) * 2u;
         }
-        off = up(off + t[i].w_bytes, 256u);
-        if (t[i].s_bytes != 0u) {
-            t[i].s_off = off;
-            off = up(off + t[i].s_bytes, 256u);
+    }
+    /* the reference converter's tensor-data layout (convert.py:928-1036):
+     * tensors in id order, payload then scales on 256-byte boundaries; the
+     * quantised routed experts of a layer form one group whose payloads are
+     * all laid out first, then all its scales */
+    uint64_t off = data_off;
+    for (uint32_t i = 0; i < n;) {
+        uint32_t end = i + 1u;
+        if (t[i].family == UOCR_TENSOR_FAMILY_MOE_EXPERT && t[i].qtype != UOCR_TENSOR_F16) {
+            while (end < n && t[end].family == UOCR_TENSOR_FAMILY_MOE_EXPERT && t[end].layer == t[i].layer &&
+                   t[end].qtype == t[i].qtype) {
+                ++end;
+            }
         }
+        for (uint32_t j = i; j < end; ++j) {
+            off = up(off, 256u);
+            t[j].w_off = off;
+            off += t[j].w_bytes;
+        }
+        for (uint32_t j = i; j < end; ++j) {
+            if (t[j].s_bytes == 0u) continue;
+            off = up(off, 256u);
+            t[j].s_off = off;
+            off += t[j].s_bytes;
+        }
+        i = end;
     }
     const uint64_t total = up(off, UOCR_FILE_ALIGNMENT);
     uint8_t *img = (uint8_t *)calloc(1, total);
@@ -224,7 +227,7 @@ int uocr_synth_model_build(uint32_t qprofile, uint64_t seed, void **out_data, si
     h->section_count = 3u;
     h->file_size = total;
     h->section_dir_offset = 128u;
-    for (int i = 0; i < 32; ++i) h->model_id_hash[i] = (uint8_t)(mix64(seed + (uint64_t)i) & 0xffu);
+    for (int i = 0; fill && i < 32; ++i) h->model_id_hash[i] = (uint8_t)(mix64(seed + (uint64_t)i) & 0xffu);
     uocr_section_entry *sec = (uocr_section_entry *)(void *)(img + 128u);
     sec[0].type = UOCR_SECTION_CONFIG;
     sec[0].offset = 256u;
@@ -278,6 +281,12 @@ int uocr_synth_model_build(uint32_t qprofile, uint64_t seed, void **out_data, si
             e->scale_size = t[i].s_bytes;
         }
     }
+    if (!fill) {
+        free(t);
+        *out_data = img;
+        *out_size = (size_t)total;
+        return UOCR_OK;
+    }
     /* value fill: one task per (tensor, 64-row block) */
     uint64_t ntask = 0;
     for (uint32_t i = 0; i < n; ++i) ntask += (t[i].rows + ROW_BLOCK - 1u) / ROW_BLOCK;
@@ -311,6 +320,14 @@ int uocr_synth_model_build(uint32_t qprofile, uint64_t seed, void **out_data, si
     *out_data = img;
     *out_size = (size_t)total;
     return UOCR_OK;
+}
+
+int uocr_synth_model_build(uint32_t qprofile, uint64_t seed, void **out_data, size_t *out_size) {
+    return build_image(qprofile, seed, 1, out_data, out_size);
+}
+
+int uocr_image_skeleton_build(uint32_t qprofile, void **out_data, size_t *out_size) {
+    return build_image(qprofile, 0u, 0, out_data, out_size);
 }
 
 int uocr_synth_model_write(const char *path, uint32_t qprofile, uint64_t seed) {

@@ -153,6 +153,8 @@ SIGNATURES = {
     "uocr_synth_model_build": ([_U32, ct.c_uint64, ct.POINTER(_VP), ct.POINTER(_SZ)], ct.c_int),
     "uocr_synth_model_write": ([ct.c_char_p, _U32, ct.c_uint64], ct.c_int),
     "uocr_synth_free": ([_VP], None),
+    "uocr_quantize_rows": ([_U32, _VP, _U32, _U32, _VP, _VP], ct.c_int),
+    "uocr_image_skeleton_build": ([_U32, ct.POINTER(_VP), ct.POINTER(_SZ)], ct.c_int),
 }
 
 _LIB: ct.CDLL | None = None
@@ -303,12 +305,17 @@ class Engine:
 class SynthModel:
     """A synthetic .uocr image in library-owned host memory."""
 
-    def __init__(self, qprofile: int, seed: int) -> None:
+    def __init__(self, qprofile: int, seed: int | None) -> None:
+        """seed None: the zero-filled skeleton the converter fills
+        (uocr_image_skeleton_build), else the seeded synthetic values."""
         self._lib = load_library()
         ptr, size = ct.c_void_p(), ct.c_size_t()
-        status = self._lib.uocr_synth_model_build(qprofile, seed, ct.byref(ptr), ct.byref(size))
+        if seed is None:
+            status = self._lib.uocr_image_skeleton_build(qprofile, ct.byref(ptr), ct.byref(size))
+        else:
+            status = self._lib.uocr_synth_model_build(qprofile, seed, ct.byref(ptr), ct.byref(size))
         if status != UOCR_OK:
-            raise RuntimeError(f"synthetic model build failed ({status})")
+            raise RuntimeError(f"model image build failed ({status})")
         self.ptr, self.size, self.qprofile, self.seed = ptr.value, size.value, qprofile, seed
 
     def view(self) -> np.ndarray:
