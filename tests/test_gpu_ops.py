@@ -331,3 +331,37 @@ def test_embed_matches_oracle(gpu, oracle, qtype):
         uocr.sync()
         ref = oracle.embed_row(qtype, w, s, 300, 1280, tok)
         assert np.array_equal(dout.download(np.uint16), ref)
+
+
+def test_captured_operators_replay_like_eager(gpu, oracle):
+    """uocr_hip_capture_begin/end + uocr_hip_graph_replay: a captured
+    sequence of operator calls (GEMV, then an RMSNorm of its output) gives
+    the eager result on every replay, with eager operator work and host
+    synchronisation between the replays."""
+    uocr = gpu
+    rng = np.random.default_rng(77)
+    w, s = weights_for(3, rng, 1280, 1280)
+    x = rand_f16(rng, 1280)
+    nw = rng.uniform(0.8, 1.2, 1280).astype(np.float16)
+    dw, ds, dx, dnw = dev(uocr, w), dev(uocr, s), dev(uocr, x), dev(uocr, nw)
+    dy, dz = uocr.DeviceBuffer(2560), uocr.DeviceBuffer(2560)
+    uocr.op_gemv(3, dw, ds, 1280, 1280, dx, None, dy)
+    uocr.op_rmsnorm(dy, dnw, 1280, dz)
+    uocr.sync()
+    ref_y, ref_z = dy.download(np.uint16), dz.download(np.uint16)
+    assert_f16_close(ref_y, oracle.gemv(3, w, s, 1280, 1280, x.view(np.uint16)))
+    with uocr.Capture() as g:
+        uocr.op_gemv(3, dw, ds, 1280, 1280, dx, None, dy)
+        uocr.op_rmsnorm(dy, dnw, 1280, dz)
+    try:
+        for _ in range(4):
+            dy.zero()
+            dz.zero()
+            uocr.op_rmsnorm(dx, dnw, 1280, dy)  # unrelated eager work on the same buffers
+            uocr.sync()
+            g.replay(1)
+            uocr.sync()
+            assert np.array_equal(dy.download(np.uint16), ref_y)
+            assert np.array_equal(dz.download(np.uint16), ref_z)
+    finally:
+        g.release()
