@@ -205,3 +205,39 @@ def test_engine_from_model_file(gpu, tmp_path):
     b = eng2.generate_prepared(np.array([0, 5, 6, 7], np.int32), max_new_tokens=4)
     eng2.close()
     assert a.tolist() == b.tolist()
+
+
+def test_separate_engines_on_separate_threads(gpu):
+    """include/unlimitedocr.h threading contract: separate engines may run on
+    separate threads at the same time.  Two engines generate concurrently
+    (ctypes releases the GIL during the call) and give the ids and scores
+    each gives alone."""
+    import threading
+
+    uocr = gpu
+    m = model(uocr, 3)
+    rng = np.random.default_rng(61)
+    prompts = [prompt(rng, 14, 5), prompt(rng, 9, 3)]
+    engines = [uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=64, max_gen_tokens=48) for _ in prompts]
+    serial = [e.generate_embeddings(*p, 40, flags=uocr.GEN_IGNORE_EOS) for e, p in zip(engines, prompts)]
+    results: list = [None, None]
+    errors: list = []
+
+    def run(i):
+        try:
+            for _ in range(3):
+                results[i] = engines[i].generate_embeddings(*prompts[i], 40, flags=uocr.GEN_IGNORE_EOS)
+        except Exception as exc:  # surfaced below
+            errors.append(exc)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    for e in engines:
+        e.close()
+    assert not errors, errors
+    for got, ref in zip(results, serial):
+        assert got[0].tolist() == ref[0].tolist()
+        assert np.array_equal(got[1], ref[1])
