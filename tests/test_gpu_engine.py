@@ -241,3 +241,43 @@ def test_separate_engines_on_separate_threads(gpu):
     for got, ref in zip(results, serial):
         assert got[0].tolist() == ref[0].tolist()
         assert np.array_equal(got[1], ref[1])
+
+
+def test_generation_stops_on_eos(gpu, oracle):
+    """Sequence rule (uocr_sequence.c:120-166, EOS id 1): generation stops at
+    the first EOS, which is returned as the last id.  LM-head row 1 (EOS) is
+    overwritten with the row of a token the model picks at some step, so EOS
+    ties with it there and wins on the lower id; ids before it are
+    unchanged."""
+    uocr = gpu
+    m = model(uocr, 3)
+    rng = np.random.default_rng(23)
+    ids, mask, rows = prompt(rng, 10, 4)
+    eng = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=64, max_gen_tokens=16)
+    base, _, _, _ = eng.generate_embeddings(ids, mask, rows, 12, flags=uocr.GEN_IGNORE_EOS)
+    eng.close()
+    base = base.tolist()
+    assert 1 not in base
+    stop = next(i for i in range(2, len(base)) if base[i] not in base[:i])  # first appearance of a token
+    target = base[stop]
+
+    class Image:
+        pass
+
+    buf = m.view().copy()
+    img = Image()
+    img.ptr, img.size, img.keep = buf.ctypes.data, buf.size, buf
+    lm = [e for e in uocr.tensor_table(buf) if int(e["id"]) == 2][0]
+    row_w, row_s = int(lm["row_size"]), (1280 // 64) * 2
+    w0, s0 = int(lm["payload_offset"]), int(lm["scale_offset"])
+    buf[w0 + row_w:w0 + 2 * row_w] = buf[w0 + target * row_w:w0 + (target + 1) * row_w]
+    buf[s0 + row_s:s0 + 2 * row_s] = buf[s0 + target * row_s:s0 + (target + 1) * row_s]
+
+    eng = uocr.Engine.from_memory(img, backend="hip", max_prompt_tokens=64, max_gen_tokens=16)
+    got, _, _, _ = eng.generate_embeddings(ids, mask, rows, 12)
+    eng.close()
+    orc = oracle.Model(img.ptr, img.size, img, prompt_capacity=64)
+    ref, _ = orc.generate(ids, mask, rows.view(np.uint16), max_new=12)
+    orc.close()
+    assert got.tolist() == base[:stop] + [1]
+    assert ref.tolist() == got.tolist()
