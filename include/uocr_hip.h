@@ -170,9 +170,8 @@ UOCR_API int uocr_op_gemm(uint32_t qtype, const void *w, const void *s, uint32_t
 UOCR_API int uocr_op_prefill_attention(const void *q, const void *k_cache, const void *v_cache,
                                        uint32_t cache_capacity, uint32_t prompt_length, void *ctx);
 
-/* Bytes of the workspace uocr_op_moe_ffn_rows needs for P rows (zero before
- * its first use, as from uocr_hip_alloc; the operator leaves its expert
- * counters at zero). */
+/* Bytes of the workspace uocr_op_moe_ffn_rows needs for P rows (any
+ * contents: the expert buckets are built in LDS on every call). */
 UOCR_API size_t uocr_op_moe_rows_workspace_bytes(uint32_t rows);
 
 /* The MoE FFN of uocr_op_moe_ffn for P rows at once (x, residual, out fp16

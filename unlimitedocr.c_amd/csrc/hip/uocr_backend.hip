@@ -85,7 +85,7 @@ struct uocr_hip_ctx {
     /* MFMA prefill scratch, sized for prompt_cap rows */
     uint16_t *p_xn, *p_qkv, *p_q, *p_ctx, *p_a, *p_mid, *p_smid, *p_sout, *p_rmid;
     float *p_logits, *p_wts, *p_y;
-    int32_t *p_ids, *p_counts, *p_offsets, *p_cursors, *p_tile_e, *p_tile_s0, *p_tile_s1, *p_ntiles, *p_list_tok,
+    int32_t *p_ids, *p_offsets, *p_tile_e, *p_tile_s0, *p_tile_s1, *p_ntiles, *p_list_tok,
         *p_list_pair;
     uint32_t p_max_tiles;
     uint32_t *lm_part;
@@ -395,7 +395,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_prmid = p.take(PK * UOCR_MOE_EXPERT_INTERMEDIATE * 2u);
     const uint64_t o_plog = p.take(Pc * UOCR_ROUTED_EXPERTS * 4u), o_pwts = p.take(PK * 4u);
     const uint64_t o_py = p.take(PK * H_SIZE * 4u), o_pids = p.take(PK * 4u);
-    const uint64_t o_pcnt = p.take(64u * 4u), o_poff = p.take(64u * 4u), o_pcur = p.take(64u * 4u);
+    const uint64_t o_poff = p.take(64u * 4u);
     const uint64_t o_pte = p.take(max_tiles * 4u), o_pts0 = p.take(max_tiles * 4u), o_pts1 = p.take(max_tiles * 4u);
     const uint64_t o_pnt = p.take(4u), o_plt = p.take(PK * 4u), o_plp = p.take(PK * 4u);
     const uint64_t total = p.off;
@@ -438,9 +438,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->p_wts = (float *)(b + o_pwts);
     ctx->p_y = (float *)(b + o_py);
     ctx->p_ids = (int32_t *)(b + o_pids);
-    ctx->p_counts = (int32_t *)(b + o_pcnt);
     ctx->p_offsets = (int32_t *)(b + o_poff);
-    ctx->p_cursors = (int32_t *)(b + o_pcur);
     ctx->p_tile_e = (int32_t *)(b + o_pte);
     ctx->p_tile_s0 = (int32_t *)(b + o_pts0);
     ctx->p_tile_s1 = (int32_t *)(b + o_pts1);
@@ -590,8 +588,7 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         d.W[0].s = nullptr;
         d.W[0].qtype = UOCR_QT_F16;
         ENQ(uocr_launch_gemm(s, UOCR_GEMM_F32, &d));
-        ENQ(uocr_launch_route_rows(s, c->p_logits, P, 0, c->p_ids, c->p_wts, c->p_counts, c->p_offsets, c->p_cursors,
-                                   c->p_tile_e, c->p_tile_s0, c->p_tile_s1, c->p_ntiles, c->p_list_tok,
+        ENQ(uocr_launch_route_rows(s, c->p_logits, P, 0, c->p_ids, c->p_wts, c->p_offsets, c->p_tile_e, c->p_tile_s0, c->p_tile_s1, c->p_ntiles, c->p_list_tok,
                                    c->p_list_pair));
         d = gdesc(c->p_xn, H_SIZE, P, SI, H_SIZE, c->p_smid, SI);
         d.W[0] = L.sgate;

@@ -196,12 +196,12 @@ hipError_t uocr_launch_rope_scatter(hipStream_t st, const uint16_t *qkv, const f
 hipError_t uocr_launch_flash_attn(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
                                   uint32_t cap, uint32_t P, uint16_t *ctx);
 /* Per-token top-6 over logits [P][64] -> ids/wts [P][6]; expert buckets:
- * counts, offsets, cursors (64 each), grouped-GEMM tile table (up to
- * P*6/64 + 64 entries) and the (token, pair) slot lists [P*6].  counts must
- * be zero on entry and is left at zero (no memset, so the call can be
- * captured into a graph). */
+ * offsets (64), grouped-GEMM tile table (up to P*6/64 + 64 entries) and the
+ * (token, pair) slot lists [P*6], built in LDS by one block (no global
+ * counters, nothing to clear between calls, so the call can be captured
+ * into a graph). */
 hipError_t uocr_launch_route_rows(hipStream_t st, const float *logits, uint32_t P, int norm_topk, int32_t *ids,
-                                  float *wts, int32_t *counts, int32_t *offsets, int32_t *cursors, int32_t *tile_e,
+                                  float *wts, int32_t *offsets, int32_t *tile_e,
                                   int32_t *tile_s0, int32_t *tile_s1, int32_t *ntiles, int32_t *list_tok,
                                   int32_t *list_pair);
 /* out[t] = f16(sum_r wts[t][r] * Y[t*6+r] + shared[t] + res[t]). */

@@ -289,7 +289,7 @@ extern "C" int uocr_op_prefill_attention(const void *q, const void *k_cache, con
 namespace {
 /* workspace layout of uocr_op_moe_ffn_rows for P rows */
 struct MoeRowsWs {
-    size_t xn, logits, ids, wts, counts, offsets, cursors, te, ts0, ts1, nt, ltok, lpair, smid, sout, rmid, y, total;
+    size_t xn, logits, ids, wts, offsets, te, ts0, ts1, nt, ltok, lpair, smid, sout, rmid, y, total;
     uint32_t max_tiles;
     explicit MoeRowsWs(size_t P) {
         const size_t PK = P * 6u;
@@ -304,9 +304,7 @@ struct MoeRowsWs {
         logits = take(P * 64u * 4u);
         ids = take(PK * 4u);
         wts = take(PK * 4u);
-        counts = take(256u);
         offsets = take(256u);
-        cursors = take(256u);
         te = take(max_tiles * 4u);
         ts0 = take(max_tiles * 4u);
         ts1 = take(max_tiles * 4u);
@@ -358,8 +356,7 @@ extern "C" int uocr_op_moe_ffn_rows(const uocr_op_moe_weights *m, const void *x,
     float *wts = (float *)(b + L.wts);
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_route_rows(st, (const float *)(b + L.logits), P, norm_topk, ids, wts,
-                                              (int32_t *)(b + L.counts), (int32_t *)(b + L.offsets),
-                                              (int32_t *)(b + L.cursors), (int32_t *)(b + L.te), (int32_t *)(b + L.ts0),
+                                              (int32_t *)(b + L.offsets), (int32_t *)(b + L.te), (int32_t *)(b + L.ts0),
                                               (int32_t *)(b + L.ts1), (int32_t *)(b + L.nt), (int32_t *)(b + L.ltok),
                                               (int32_t *)(b + L.lpair)),
                        "routing");

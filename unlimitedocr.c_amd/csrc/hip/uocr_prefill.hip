@@ -560,10 +560,9 @@ __device__ __forceinline__ float lane_fp(float v, int l) {
 
 /* One wavefront per token: softmax over its 64 logits, greedy top-6 (ties to
  * the lower id; same key order as the decode router), raw probabilities
- * unless norm_topk; counts tokens per expert. */
+ * unless norm_topk. */
 __global__ __launch_bounds__(PB) void k_route_rows(const float *__restrict__ logits, u32 P, int norm_topk,
-                                                   int32_t *__restrict__ ids, float *__restrict__ wts,
-                                                   int32_t *__restrict__ counts) {
+                                                   int32_t *__restrict__ ids, float *__restrict__ wts) {
     const u32 tok = blockIdx.x * (PB / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
     if (tok >= P) return;
     const float lg = logits[(size_t)tok * 64u + lane];
@@ -594,55 +593,63 @@ __global__ __launch_bounds__(PB) void k_route_rows(const float *__restrict__ log
     if (rank < (u32)UOCR_K_TOPK) {
         ids[tok * UOCR_K_TOPK + rank] = (int32_t)lane;
         wts[tok * UOCR_K_TOPK + rank] = norm_topk ? prob / tot : prob;
-        atomicAdd(&counts[lane], 1);
     }
 }
 
-/* One block: exclusive scan of the 64 bucket sizes, the tile table of the
- * grouped GEMMs (TM rows per tile) and the per-bucket cursors.  The counts
- * are cleared once read, so the next routing starts from zero without a
- * memset (the prefill is replayed as a captured graph). */
-__global__ __launch_bounds__(64) void k_bucket_scan(int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
-                                                    int32_t *__restrict__ cursors, int32_t *__restrict__ tile_e,
-                                                    int32_t *__restrict__ tile_s0, int32_t *__restrict__ tile_s1,
-                                                    int32_t *__restrict__ ntiles) {
-    __shared__ int32_t off[65], toff[65];
-    const u32 e = threadIdx.x;
-    if (e == 0) {
+/* One block builds the expert buckets of all P*6 (token, rank) pairs in
+ * LDS: the 64 bucket sizes (LDS atomics), their exclusive scan (offsets),
+ * the tile table of the grouped GEMMs (TM rows per tile) and every pair's
+ * slot in its bucket (list_tok, list_pair).  The order of pairs inside a
+ * bucket does not matter: each pair's row is computed on its own and the
+ * combine reads it by pair index.  Nothing is left in global memory that the
+ * next routing has to find cleared. */
+#define BUCKET_THREADS 1024
+__global__ __launch_bounds__(BUCKET_THREADS) void k_bucket_build(const int32_t *__restrict__ ids, u32 P,
+                                                                 int32_t *__restrict__ offsets,
+                                                                 int32_t *__restrict__ tile_e,
+                                                                 int32_t *__restrict__ tile_s0,
+                                                                 int32_t *__restrict__ tile_s1,
+                                                                 int32_t *__restrict__ ntiles,
+                                                                 int32_t *__restrict__ list_tok,
+                                                                 int32_t *__restrict__ list_pair) {
+    __shared__ int32_t cnt[64], off[65], toff[65], cur[64];
+    const u32 t = threadIdx.x, n = P * UOCR_K_TOPK;
+    if (t < 64u) {
+        cnt[t] = 0;
+        cur[t] = 0;
+    }
+    __syncthreads();
+    for (u32 pr = t; pr < n; pr += BUCKET_THREADS) atomicAdd(&cnt[ids[pr]], 1);
+    __syncthreads();
+    if (t == 0u) {
         int32_t a = 0, b = 0;
         for (int i = 0; i < 64; ++i) {
             off[i] = a;
             toff[i] = b;
-            a += counts[i];
-            b += (counts[i] + TM - 1) / TM;
+            a += cnt[i];
+            b += (cnt[i] + TM - 1) / TM;
         }
         off[64] = a;
         toff[64] = b;
         *ntiles = b;
     }
     __syncthreads();
-    offsets[e] = off[e];
-    cursors[e] = 0;
-    const int32_t n = counts[e];
-    counts[e] = 0; /* thread 0's scan read every count before the barrier */
-    for (int32_t k = 0; k * TM < n; ++k) {
-        const int32_t ti = toff[e] + k;
-        tile_e[ti] = (int32_t)e;
-        tile_s0[ti] = off[e] + k * TM;
-        tile_s1[ti] = off[e] + min(n, (k + 1) * TM);
+    if (t < 64u) {
+        offsets[t] = off[t];
+        const int32_t c = cnt[t];
+        for (int32_t k = 0; k * TM < c; ++k) {
+            const int32_t ti = toff[t] + k;
+            tile_e[ti] = (int32_t)t;
+            tile_s0[ti] = off[t] + k * TM;
+            tile_s1[ti] = off[t] + min(c, (k + 1) * TM);
+        }
     }
-}
-
-/* Slot of every (token, rank) pair in its expert's bucket. */
-__global__ __launch_bounds__(PB) void k_bucket_place(const int32_t *__restrict__ ids, u32 P,
-                                                     const int32_t *__restrict__ offsets, int32_t *__restrict__ cursors,
-                                                     int32_t *__restrict__ list_tok, int32_t *__restrict__ list_pair) {
-    const u32 pr = blockIdx.x * PB + threadIdx.x;
-    if (pr >= P * UOCR_K_TOPK) return;
-    const int32_t e = ids[pr];
-    const int32_t s = offsets[e] + atomicAdd(&cursors[e], 1);
-    list_tok[s] = (int32_t)(pr / UOCR_K_TOPK);
-    list_pair[s] = (int32_t)pr;
+    for (u32 pr = t; pr < n; pr += BUCKET_THREADS) {
+        const int32_t e = ids[pr];
+        const int32_t slot = off[e] + atomicAdd(&cur[e], 1);
+        list_tok[slot] = (int32_t)(pr / UOCR_K_TOPK);
+        list_pair[slot] = (int32_t)pr;
+    }
 }
 
 /* h[t] = f16(sum_r w[t][r] * Y[t*6+r] + shared[t] + res[t]) (decode_gemv_q4.
@@ -764,22 +771,16 @@ extern "C" hipError_t uocr_launch_flash_attn(hipStream_t st, const uint16_t *q, 
 }
 
 extern "C" hipError_t uocr_launch_route_rows(hipStream_t st, const float *logits, uint32_t P, int norm_topk,
-                                             int32_t *ids, float *wts, int32_t *counts, int32_t *offsets,
-                                             int32_t *cursors, int32_t *tile_e, int32_t *tile_s0, int32_t *tile_s1,
-                                             int32_t *ntiles, int32_t *list_tok, int32_t *list_pair) {
-    if (logits == nullptr || P == 0u || ids == nullptr || wts == nullptr || counts == nullptr || offsets == nullptr ||
-        cursors == nullptr || tile_e == nullptr || tile_s0 == nullptr || tile_s1 == nullptr || ntiles == nullptr ||
+                                             int32_t *ids, float *wts, int32_t *offsets, int32_t *tile_e,
+                                             int32_t *tile_s0, int32_t *tile_s1, int32_t *ntiles, int32_t *list_tok,
+                                             int32_t *list_pair) {
+    if (logits == nullptr || P == 0u || ids == nullptr || wts == nullptr || offsets == nullptr || tile_e == nullptr || tile_s0 == nullptr || tile_s1 == nullptr || ntiles == nullptr ||
         list_tok == nullptr || list_pair == nullptr) {
         return hipErrorInvalidValue;
     }
-    /* counts are zero on entry: zero-filled at allocation, cleared again by
-     * k_bucket_scan after every use */
-    hipLaunchKernelGGL(k_route_rows, dim3((P + 3u) / 4u), dim3(PB), 0, st, logits, P, norm_topk, ids, wts, counts);
-    hipLaunchKernelGGL(k_bucket_scan, dim3(1), dim3(64), 0, st, counts, offsets, cursors, tile_e,
-                       tile_s0, tile_s1, ntiles);
-    const u32 n = P * UOCR_K_TOPK;
-    hipLaunchKernelGGL(k_bucket_place, dim3((n + PB - 1u) / PB), dim3(PB), 0, st, (const int32_t *)ids, P,
-                       (const int32_t *)offsets, cursors, list_tok, list_pair);
+    hipLaunchKernelGGL(k_route_rows, dim3((P + 3u) / 4u), dim3(PB), 0, st, logits, P, norm_topk, ids, wts);
+    hipLaunchKernelGGL(k_bucket_build, dim3(1), dim3(BUCKET_THREADS), 0, st, (const int32_t *)ids, P, offsets,
+                       tile_e, tile_s0, tile_s1, ntiles, list_tok, list_pair);
     return hipGetLastError();
 }
 
