@@ -281,3 +281,25 @@ def test_generation_stops_on_eos(gpu, oracle):
     orc.close()
     assert got.tolist() == base[:stop] + [1]
     assert ref.tolist() == got.tolist()
+
+
+def test_config5_prompt_matches_oracle(gpu, oracle):
+    """BASELINE config 5's prompt at full size: 900 image-embedding rows
+    ~ N(0,1) after BOS, then 31 text ids (932 rows through the MFMA
+    prefill), then greedy steps; ids must match wherever the oracle's margin
+    exceeds 1e-2 (the oracle runs the prompt position by position)."""
+    uocr = gpu
+    m = model(uocr, 3)
+    rng = np.random.default_rng(0)
+    ids = np.concatenate([[0], np.full(900, 128815), rng.integers(2, 128000, 31)]).astype(np.int32)
+    mask = (ids == 128815).astype(np.uint8)
+    rows = rng.standard_normal((900, 1280)).astype(np.float16)
+    eng = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=1024, max_gen_tokens=16)
+    got, _, _, _ = eng.generate_embeddings(ids, mask, rows, 6, flags=uocr.GEN_IGNORE_EOS)
+    eng.close()
+    orc = oracle.Model(m.ptr, m.size, m, prompt_capacity=1024)
+    ref, margins = orc.generate(ids, mask, rows.view(np.uint16), max_new=6, ignore_eos=True)
+    orc.close()
+    assert got.shape == (6,)
+    assert margins[0] > 1e-2, "seed gives a first step without a clear winner"
+    assert compare_ids(got.tolist(), ref.tolist(), margins.tolist()) >= 1

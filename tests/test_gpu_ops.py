@@ -365,3 +365,37 @@ def test_captured_operators_replay_like_eager(gpu, oracle):
             assert np.array_equal(dz.download(np.uint16), ref_z)
     finally:
         g.release()
+
+
+def test_moe_ffn_512_consecutive_tokens(gpu, oracle):
+    """BASELINE config 3 at its stated length: 512 consecutive tokens, a fresh
+    hidden per token, through one set of Q4 expert weights (router fp16,
+    2 shared merged to 1792, 64 routed, top-6).  Expert ids equal the
+    oracle's wherever its logit margin exceeds 1e-2, and outputs stay within
+    the fp16 tolerance for every such token."""
+    uocr = gpu
+    rng = np.random.default_rng(3)
+    m, host, keep = _moe_setup(uocr, rng, 4, 4)
+    ws = uocr.workspace()
+    nw = rng.uniform(0.8, 1.2, 1280).astype(np.float16)
+    dnw = dev(uocr, nw)
+    xs = rand_f16(rng, (512, 1280))
+    res = rand_f16(rng, (512, 1280))
+    dxs, dres = dev(uocr, xs), dev(uocr, res)
+    dout = uocr.DeviceBuffer(512 * 2560)
+    dids, dwts = uocr.DeviceBuffer(512 * 24), uocr.DeviceBuffer(512 * 24)
+    for t in range(512):
+        uocr.op_moe_ffn(m, dxs.ptr + t * 2560, dnw, dres.ptr + t * 2560, 0, ws, dout.ptr + t * 2560,
+                        dids.ptr + t * 24, dwts.ptr + t * 24)
+    uocr.sync()
+    out = dout.download(np.uint16).reshape(512, 1280)
+    ids = dids.download(np.uint32).reshape(512, 6)
+    checked = 0
+    for t in range(512):
+        xn = oracle.rmsnorm_f16(xs[t].view(np.uint16), nw.view(np.uint16))
+        ref, ref_ids, _, margin = _oracle_moe(oracle, host, 4, 4, xn, res[t].view(np.uint16))
+        if margin > 1e-2:
+            assert ids[t].tolist() == ref_ids.tolist(), t
+            assert_f16_close(out[t], ref)
+            checked += 1
+    assert checked >= 256
