@@ -99,7 +99,7 @@ struct uocr_hip_ctx {
     uint16_t *h_prompt;
 
     float invf[UOCR_K_HEAD_DIM / 2];
-    hipGraphExec_t g_decode, g_prefill;
+    hipGraphExec_t g_decode, g_decode_chunk, g_prefill; /* one step, DECODE_CHUNK steps, one prompt position */
     int graphs_ready;
 };
 
@@ -144,6 +144,7 @@ extern "C" uocr_hip_ctx *uocr_hip_context_create(char *err, size_t err_size) {
 static void release_graphs(uocr_hip_ctx *ctx) {
     if (ctx->graphs_ready) {
         (void)hipGraphExecDestroy(ctx->g_decode);
+        (void)hipGraphExecDestroy(ctx->g_decode_chunk);
         (void)hipGraphExecDestroy(ctx->g_prefill);
         ctx->graphs_ready = 0;
     }
@@ -629,6 +630,16 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
 #undef ENQ
 }
 
+/* DECODE_CHUNK decode steps in one graph: the device-side step state
+ * advances from one step to the next, so the steps replay unchanged, and a
+ * chunk pays one graph launch instead of DECODE_CHUNK (a launch boundary
+ * between graphs costs about 6 us, between kernels of a graph about 1.4 us). */
+static hipError_t enqueue_decode_chunk(uocr_hip_ctx *c) {
+    hipError_t e = hipSuccess;
+    for (uint32_t i = 0; i < DECODE_CHUNK && e == hipSuccess; ++i) e = enqueue_decode_step(c);
+    return e;
+}
+
 static int capture(uocr_hip_ctx *c, hipError_t (*fn)(uocr_hip_ctx *), hipGraphExec_t *out, char *err, size_t err_size) {
     hipGraph_t g = nullptr;
     HIPCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
@@ -676,8 +687,13 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
     const int use_graph = (req->flags & UOCR_GEN_NO_GRAPH) == 0u;
     if (use_graph && !c->graphs_ready) {
         if (!capture(c, enqueue_decode_step, &c->g_decode, err, err_size)) return 0;
+        if (!capture(c, enqueue_decode_chunk, &c->g_decode_chunk, err, err_size)) {
+            (void)hipGraphExecDestroy(c->g_decode);
+            return 0;
+        }
         if (!capture(c, enqueue_prefill_step, &c->g_prefill, err, err_size)) {
             (void)hipGraphExecDestroy(c->g_decode);
+            (void)hipGraphExecDestroy(c->g_decode_chunk);
             return 0;
         }
         c->graphs_ready = 1;
@@ -736,7 +752,12 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
     int ok = 1;
     while (issued < N && !eos && ok) {
         const uint32_t end = issued + DECODE_CHUNK < N ? issued + DECODE_CHUNK : N;
-        for (uint32_t t = issued; t < end && ok; ++t) {
+        if (use_graph && end - issued == DECODE_CHUNK && end < N) {
+            /* a whole chunk of full decode steps: one graph launch */
+            const hipError_t e = hipGraphLaunch(c->g_decode_chunk, s);
+            if (e != hipSuccess) ok = bfail(err, err_size, "decode steps %u-%u: %s", issued, end - 1u, hipGetErrorString(e));
+        }
+        for (uint32_t t = issued; t < end && ok && !(use_graph && end - issued == DECODE_CHUNK && end < N); ++t) {
             hipError_t e;
             if (t + 1u < N) {
                 e = use_graph ? hipGraphLaunch(c->g_decode, s) : enqueue_decode_step(c);

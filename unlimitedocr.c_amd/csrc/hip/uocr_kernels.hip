@@ -57,6 +57,53 @@ typedef uint32_t u32;
 #define SMALL_BLOCK 128 /* one-pass GEMVs with few rows: 2 wavefronts, more CUs */
 #define NONE_ID 0xffffffffu
 
+
+/* ------------------------------------------------------------------------ */
+/* opt-in per-block timeline (builds with -DUOCR_TIMELINE only)              */
+/* ------------------------------------------------------------------------ */
+#ifdef UOCR_TIMELINE
+struct TlRec {
+    uint32_t kid, block, xcc, pad;
+    uint64_t t0, t1;
+};
+__device__ TlRec *g_tl_buf;
+__device__ unsigned g_tl_cap;
+__device__ unsigned g_tl_n[256]; /* records per region (block id % 256): few same-line atomics per launch */
+/* thread 0 of every block records (kernel, block, XCD, start, end) in
+ * s_memrealtime ticks (100 MHz) when the block leaves the kernel */
+struct TlScope {
+    uint64_t t0;
+    uint32_t kid;
+    __device__ explicit TlScope(uint32_t k) : kid(k) { t0 = __builtin_amdgcn_s_memrealtime(); }
+    __device__ ~TlScope() {
+        if (threadIdx.x == 0 && g_tl_buf != nullptr) {
+            const unsigned b = (blockIdx.x + blockIdx.y * gridDim.x) & 255u, per = g_tl_cap / 256u;
+            const unsigned j = atomicAdd(&g_tl_n[b], 1u), i = b * per + j;
+            if (j < per) {
+                TlRec r;
+                r.kid = kid;
+                r.block = blockIdx.x + blockIdx.y * gridDim.x;
+                r.xcc = (uint32_t)__builtin_amdgcn_s_getreg(20 | (3 << 11)) & 0xfu; /* HW_REG_XCC_ID */
+                r.pad = 0;
+                r.t0 = t0;
+                r.t1 = __builtin_amdgcn_s_memrealtime();
+                g_tl_buf[i] = r;
+            }
+        }
+    }
+};
+#define TL(k) TlScope tl_scope_(k)
+extern "C" __attribute__((visibility("default"))) int uocr_hip_timeline(void *buf, unsigned cap) {
+    static const unsigned zero[256] = {0};
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_tl_buf), &buf, sizeof(buf)) != hipSuccess) return -1;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_tl_cap), &cap, sizeof(cap)) != hipSuccess) return -1;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_tl_n), zero, sizeof(zero)) != hipSuccess) return -1;
+    return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}
+#else
+#define TL(k)
+#endif
+
 /* ------------------------------------------------------------------------ */
 /* wavefront / block reductions                                              */
 /* ------------------------------------------------------------------------ */
@@ -581,6 +628,7 @@ __global__ __launch_bounds__(BLOCK) void k_stream(const uint8_t *__restrict__ W,
                                                   u32 rows, u32 K, const h16 *__restrict__ x,
                                                   const h16 *__restrict__ nw, const h16 *__restrict__ res,
                                                   h16 *__restrict__ y) {
+    TL(7);
     static_assert(EPI != EPI_ARGMAX, "the argmax epilogue runs in k_lm_select");
     float b = -INFINITY;
     u32 bi = NONE_ID;
@@ -628,6 +676,7 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
                                                     const h16 *__restrict__ nw,
                                                     const uocr_step_state *__restrict__ st, h16 *__restrict__ qout,
                                                     h16 *__restrict__ kc, h16 *__restrict__ vc, u32 cap) {
+    TL(1);
     constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_lat(C), J = j_lat(C), R = 64u / LPR;
     constexpr u32 rb = 16u * C, G = K / 64u;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
@@ -699,6 +748,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
                                                      const h16 *__restrict__ vc, u32 cap,
                                                      const uocr_step_state *__restrict__ st, float *__restrict__ part,
                                                      long long *__restrict__ racc) {
+    TL(2);
     constexpr int S = UOCR_K_ATTN_SPLITS;
     if (racc != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
         for (int i = threadIdx.x; i < UOCR_ROUTER_ACC_WORDS; i += ATT_THREADS) racc[i] = 0;
@@ -901,6 +951,7 @@ __global__ __launch_bounds__(BLOCK) void k_attn_out(uocr_qmat O, const float *__
                                                     const h16 *__restrict__ res, h16 *__restrict__ out,
                                                     h16 *__restrict__ ctx_out, const float *__restrict__ fold,
                                                     long long *__restrict__ racc) {
+    TL(3);
     constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
     constexpr u32 rb = 16u * C, G = K / 64u;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
@@ -968,6 +1019,7 @@ __global__ __launch_bounds__(BLOCK) void k_attn_merge(const float *__restrict__ 
  * CUs. */
 __global__ __launch_bounds__(64) void k_router_logits(const h16 *__restrict__ Rw, const h16 *__restrict__ x,
                                                       const h16 *__restrict__ nw, float *__restrict__ logits) {
+    TL(8);
     constexpr u32 C = chunks_per_row<1>(UOCR_K_HIDDEN), LPR = 64u, J = (C + LPR - 1u) / LPR, rb = 16u * C;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
@@ -1017,6 +1069,7 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl
                                                              h16 *__restrict__ mid, h16 *__restrict__ smid,
                                                              u32 *__restrict__ ids_out, float *__restrict__ w_out,
                                                              u32 nb_routed) {
+    TL(4);
     constexpr u32 K = UOCR_K_HIDDEN, G = K / 64u, I = 896u, ROWS = UOCR_K_TOPK * I, SI = 1792u;
     constexpr u32 NWV = SMALL_BLOCK / 64u;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
@@ -1114,6 +1167,7 @@ __global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const u
                                                     const float *__restrict__ wts, const h16 *__restrict__ mid,
                                                     uocr_qmat SD, const h16 *__restrict__ smid,
                                                     const h16 *__restrict__ res, h16 *__restrict__ out) {
+    TL(5);
     constexpr u32 I = 896u, SI = 1792u, LPR = lpr_down(QT), R = 64u / LPR;
     constexpr u32 CD = chunks_per_row<QT>(I), JD = (CD + LPR - 1u) / LPR, GD = I / 64u;
     constexpr u32 CS = chunks_per_row<QS>(SI), JS = (CS + LPR - 1u) / LPR, GS = SI / 64u;
@@ -1320,6 +1374,7 @@ __global__ __launch_bounds__(BLOCK) void k_lm_select(const uint8_t *__restrict__
                                                      float *scores, const uint8_t *__restrict__ EW,
                                                      const h16 *__restrict__ ES, h16 *__restrict__ hout, RopeTab tab,
                                                      int with_rope) {
+    TL(6);
     float b = -INFINITY;
     u32 bi = NONE_ID;
     /* the step fields the selection needs, read before the GEMV */
