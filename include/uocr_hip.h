@@ -93,6 +93,17 @@ UOCR_API int uocr_op_rmsnorm(const void *x, const void *w, uint32_t n, void *y);
 UOCR_API int uocr_op_lm_head_argmax(uint32_t qtype, const void *w, const void *s, uint32_t vocab, const void *x,
                                     const void *norm_w, void *workspace, int32_t *token, float *score);
 
+/* The streaming part of uocr_op_lm_head_argmax alone (its first launch):
+ * [final RMSNorm +] LM-head GEMV + per-block argmax, each block adding its
+ * best (score, row) as a 64-bit key, (order(score) << 32) | (0xffffffff -
+ * row), by atomic max into keys[block % 16] (16 uint64 on the device; start
+ * them at zero; the largest key is the winner, 0: no valid row).  The
+ * decode loop chooses the token from these keys in its next launch.  No
+ * reference counterpart: it exposes the LM head's dominant kernel for
+ * measurement. */
+UOCR_API int uocr_op_lm_head_keys(uint32_t qtype, const void *w, const void *s, uint32_t vocab, const void *x,
+                                  const void *norm_w, uint64_t *keys);
+
 /* MoE router over 64 fp16 rows of K = 1280: softmax, greedy top-6 with ties
  * to the lower id, raw probabilities (renormalised when norm_topk != 0).
  * Replaces uocr_moe_router_decode_fused_f16 (kernels/moe.metal:53-189). */

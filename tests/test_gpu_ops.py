@@ -399,3 +399,25 @@ def test_moe_ffn_512_consecutive_tokens(gpu, oracle):
             assert_f16_close(out[t], ref)
             checked += 1
     assert checked >= 256
+
+
+def test_lm_head_keys_decode_to_the_argmax(gpu, oracle):
+    """uocr_op_lm_head_keys (the decode loop's LM-head launch): the largest
+    of the 16 keys decodes to the oracle's argmax row and its score."""
+    uocr = gpu
+    rng = np.random.default_rng(12)
+    vocab = 129280
+    w, s = q4_weights(rng, vocab, 1280)
+    x = rand_f16(rng, 1280)
+    tid, s1, s2 = oracle.lm_head_argmax(4, w, s, vocab, 1280, x.view(np.uint16))
+    keys = uocr.DeviceBuffer(16 * 8)
+    uocr.op_lm_head_keys(4, dev(uocr, w), dev(uocr, s), vocab, dev(uocr, x), None, keys)
+    uocr.sync()
+    best = int(keys.download(np.uint64).max())
+    row = 0xFFFFFFFF - (best & 0xFFFFFFFF)
+    o = best >> 32
+    bits = (o & 0x7FFFFFFF) if (o & 0x80000000) else (~o & 0xFFFFFFFF)
+    score = float(np.array([bits], np.uint32).view(np.float32)[0])
+    if s1 - s2 > 1e-2:
+        assert row == tid
+    assert abs(score - s1) <= 1e-3 * max(1.0, abs(s1))

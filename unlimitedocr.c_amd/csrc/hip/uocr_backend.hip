@@ -81,6 +81,7 @@ struct uocr_hip_ctx {
     uint16_t *kc, *vc, *h, *a, *q, *ctxv, *mid, *smid, *prompt;
     float *attn_part, *logits, *route_w;
     int64_t *racc; /* un-normalised router logits, fixed point (k_attn_out -> k_moe_gate_up) */
+    int fold_select; /* the token is chosen in layer 0's QKV launch (not a finalize launch) */
     uint32_t *route_ids;
     /* MFMA prefill scratch, sized for prompt_cap rows */
     uint16_t *p_xn, *p_qkv, *p_q, *p_ctx, *p_a, *p_mid, *p_smid, *p_sout, *p_rmid;
@@ -294,6 +295,9 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
     /* UOCR_HIP_NO_ROUTER_FOLD=1 keeps the separate router kernel in every layer */
     const char *nf = getenv("UOCR_HIP_NO_ROUTER_FOLD");
     const bool no_fold = nf != nullptr && atoi(nf) != 0;
+    /* UOCR_HIP_NO_SELECT_FOLD=1 chooses each token in a finalize launch after the LM head */
+    const char *ns = getenv("UOCR_HIP_NO_SELECT_FOLD");
+    ctx->fold_select = !(ns != nullptr && atoi(ns) != 0);
     /* size pass */
     uint64_t total = tensor_bytes(b->embed) + tensor_bytes(b->lm_head) + tensor_bytes(b->final_norm);
     for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
@@ -474,7 +478,10 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
 
 /* ---- step enqueue ----------------------------------------------------------- */
 
-static hipError_t enqueue_layers(uocr_hip_ctx *c) {
+/* sel: layer 0's QKV launch chooses the token from the LM-head keys and
+ * stages its embedding row (a decode step); else h already holds the
+ * layer input (a prompt position). */
+static hipError_t enqueue_layers(uocr_hip_ctx *c, bool sel) {
     hipStream_t s = c->stream;
     const uint64_t kv_layer = (uint64_t)UOCR_ATTENTION_HEADS * c->cache_cap * UOCR_HEAD_DIM;
     hipError_t e = hipSuccess;
@@ -486,8 +493,15 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c) {
     for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
         const dev_layer &L = c->L[l];
         uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
-        ENQ(uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->state, c->q, kc, vc, c->cache_cap));
-        ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part, c->racc));
+        if (sel && l == 0u) {
+            ENQ(uocr_launch_qkv_rope_select(s, L.q, L.k, L.v, L.in_norm, c->state, c->q, kc, vc, c->cache_cap,
+                                            (const uint64_t *)c->lm_part, c->embed, UOCR_VOCAB_SIZE, c->tokens,
+                                            c->scores, c->h));
+        } else {
+            ENQ(uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->state, c->q, kc, vc, c->cache_cap));
+        }
+        ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part, c->racc,
+                                  sel && l == 0u ? (uint64_t *)c->lm_part : nullptr));
         ENQ(uocr_launch_attn_out(s, L.o, c->attn_part, c->h, c->a, nullptr, L.rfold, c->racc));
         if (l == 0u) {
             ENQ(uocr_launch_swiglu(s, L.gate, L.up, UOCR_DENSE_LAYER0_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->mid));
@@ -505,23 +519,29 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c) {
 #undef ENQ
 }
 
-/* Selection of the next token; with embed, the finalize block also writes
- * that token's embedding row into h for the following decode step. */
-static hipError_t enqueue_select(uocr_hip_ctx *c, bool embed) {
+/* The LM head of a decode step: argmax keys and the step-state advance
+ * (k_lm_keys).  With fold_select the token is chosen by layer 0's QKV launch
+ * (enqueue_layers with sel); otherwise, or with last (the final step, no
+ * layers follow), a finalize launch chooses it and, unless last, gathers its
+ * embedding row into h. */
+static hipError_t enqueue_select(uocr_hip_ctx *c, bool last) {
+    hipError_t e = uocr_launch_lm_keys(c->stream, c->lm_head, UOCR_VOCAB_SIZE, c->h, c->final_norm,
+                                       (uint64_t *)c->lm_part, c->state, 1, c->invf);
+    if (e != hipSuccess || (c->fold_select && !last)) return e;
     uocr_qmat none = {nullptr, nullptr, UOCR_QT_Q4};
-    return uocr_launch_lm_head(c->stream, c->lm_head, UOCR_VOCAB_SIZE, c->h, c->final_norm, c->lm_part, c->state, 1,
-                               c->tokens, c->scores, embed ? c->embed : none, c->h, c->invf);
+    return uocr_launch_lm_finalize(c->stream, (uint64_t *)c->lm_part, c->state, 1, c->tokens, c->scores,
+                                   last ? none : c->embed, UOCR_VOCAB_SIZE, c->h);
 }
 
 static hipError_t enqueue_decode_step(uocr_hip_ctx *c) {
-    hipError_t e = enqueue_select(c, true);
-    if (e == hipSuccess) e = enqueue_layers(c);
+    hipError_t e = enqueue_select(c, false);
+    if (e == hipSuccess) e = enqueue_layers(c, c->fold_select != 0);
     return e;
 }
 
 static hipError_t enqueue_prefill_step(uocr_hip_ctx *c) {
     hipError_t e = uocr_launch_prefill_next(c->stream, c->state, c->prompt, c->h, c->invf);
-    if (e == hipSuccess) e = enqueue_layers(c);
+    if (e == hipSuccess) e = enqueue_layers(c, false);
     return e;
 }
 
@@ -762,7 +782,7 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
             if (t + 1u < N) {
                 e = use_graph ? hipGraphLaunch(c->g_decode, s) : enqueue_decode_step(c);
             } else {
-                e = enqueue_select(c, false);
+                e = enqueue_select(c, true);
             }
             if (e != hipSuccess) ok = bfail(err, err_size, "decode step %u: %s", t, hipGetErrorString(e));
         }

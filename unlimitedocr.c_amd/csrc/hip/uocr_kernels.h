@@ -91,10 +91,11 @@ hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_q
 /* Split-K decode attention over the live slots [0, state->attn_len) of one
  * layer's caches (UOCR_K_ATTN_SPLITS blocks per head, slots partitioned by
  * cache_capacity): writes UOCR_ATTN_PARTIAL_FLOATS of per-split partials.
- * router_acc (may be NULL) is cleared for the following attn_out. */
+ * router_acc (may be NULL) is cleared for the following attn_out, and the
+ * UOCR_LM_KEYS LM-head keys at clear_keys (may be NULL) for the next step. */
 hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
                                  uint32_t cache_capacity, const uocr_step_state *state, float *partials,
-                                 int64_t *router_acc);
+                                 int64_t *router_acc, uint64_t *clear_keys);
 /* O projection with the attention merge in its prologue:
  * out = f16(O . ctx + res), ctx = f16(merge(partials)); ctx_out (may be
  * NULL) receives ctx.  With router_fold (fp32 [1280][64], entry [i][e] =
@@ -130,11 +131,28 @@ hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab,
 hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
                                 const float *weights, const uint16_t *mid, uocr_qmat SD, const uint16_t *smid,
                                 const uint16_t *res, uint16_t *out);
-/* Final norm + LM-head argmax + selection in one launch: blocks publish
- * their best (score, row) by atomic max and the last block to finish stores
- * the winner at tokens[state->t] (tokens[0] without state); with advance it
- * also writes the next decode position into *state and, when E.w is set,
- * gathers that token's embedding row into hout.
+/* Final norm + LM-head GEMV + argmax keys (k_lm_keys): every block adds its
+ * best (score, row) as a 64-bit key by atomic max into keys[block % 16]
+ * (UOCR_LM_KEYS words, zero on entry); with advance, block 0 advances the
+ * step state (position, KV slot, attention length, t + 1, RoPE table). */
+hipError_t uocr_launch_lm_keys(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x, const uint16_t *nw,
+                               uint64_t *keys, uocr_step_state *state, int advance, const float *inv_freq);
+/* The selection from the keys (one wavefront): token and score at
+ * tokens[state->t - 1] with advance (the keys launch advanced t), else
+ * tokens[0]; state->cur_token; with E.w the token's embedding row into
+ * hout.  Leaves the keys zero. */
+hipError_t uocr_launch_lm_finalize(hipStream_t st, uint64_t *keys, uocr_step_state *state, int advance,
+                                   int32_t *tokens, float *scores, uocr_qmat E, uint32_t vocab, uint16_t *hout);
+/* Layer 0's QKV launch of a decode step with the selection folded in: the
+ * token is chosen from the keys, its embedding row (E) is the activation and
+ * is stored to hout (the hidden state), the token and score go to
+ * tokens[state->t - 1] and state->cur_token.  The keys are left for
+ * uocr_launch_attention's clear_keys. */
+hipError_t uocr_launch_qkv_rope_select(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *nw,
+                                       uocr_step_state *state, uint16_t *qout, uint16_t *kcache, uint16_t *vcache,
+                                       uint32_t cache_capacity, const uint64_t *keys, uocr_qmat E, uint32_t vocab,
+                                       int32_t *tokens, float *scores, uint16_t *hout);
+/* Keys launch followed by the finalize launch (the operator API's LM head).
  * partials: UOCR_LM_PARTIAL_WORDS words, zero before the first call; every
  * call leaves them zero. */
 hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x, const uint16_t *nw,

@@ -47,6 +47,7 @@
 #include "uocr_kernels.h"
 
 #include <math.h>
+#include <string.h>
 
 typedef _Float16 h16;
 typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
@@ -145,6 +146,28 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
         v = u > v ? u : v;
     }
     return v;
+}
+
+/* 64-bit argmax key of a (score, row) pair: the largest key is the highest
+ * score with the lowest row among equals; -0 ranks as +0; 0 means no valid
+ * row (lm_head_q4.metal:48-97, sampling.metal:173-200: NaN rows skipped,
+ * ties to the lowest id, none valid -> token 0). */
+__device__ __forceinline__ unsigned long long argmax_key(float b, u32 bi) {
+    if (bi == NONE_ID) return 0ull;
+    const u32 u = __float_as_uint(b == 0.0f ? 0.0f : b);
+    const u32 o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)o << 32) | (unsigned long long)(0xffffffffu - bi);
+}
+
+__device__ __forceinline__ void key_winner(unsigned long long best, float &b, u32 &bi) {
+    if (best == 0ull) {
+        b = -INFINITY;
+        bi = NONE_ID;
+    } else {
+        const u32 o = (u32)(best >> 32);
+        b = __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+        bi = 0xffffffffu - (u32)best;
+    }
 }
 
 /* Sum over the block; every thread receives the result. red: >= 16 floats. */
@@ -621,7 +644,7 @@ __device__ __forceinline__ void stream_rows(const uint8_t *__restrict__ W, const
 }
 
 /* GEMV launch of stream_rows (EPI_LINEAR, EPI_SWIGLU; the LM head's
- * EPI_ARGMAX runs inside k_lm_select). */
+ * EPI_ARGMAX runs inside k_lm_keys). */
 template <int QT, int LPR, int J, int EPI>
 __global__ __launch_bounds__(BLOCK) void k_stream(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
                                                   const uint8_t *__restrict__ W2, const h16 *__restrict__ S2,
@@ -629,7 +652,7 @@ __global__ __launch_bounds__(BLOCK) void k_stream(const uint8_t *__restrict__ W,
                                                   const h16 *__restrict__ nw, const h16 *__restrict__ res,
                                                   h16 *__restrict__ y) {
     TL(7);
-    static_assert(EPI != EPI_ARGMAX, "the argmax epilogue runs in k_lm_select");
+    static_assert(EPI != EPI_ARGMAX, "the argmax epilogue runs in k_lm_keys");
     float b = -INFINITY;
     u32 bi = NONE_ID;
     stream_rows<QT, LPR, J, EPI>(W, S, W2, S2, rows, K, x, nw, res, y, b, bi);
@@ -667,15 +690,66 @@ __device__ __forceinline__ void set_rope(uocr_step_state *st, int32_t pos, const
     }
 }
 
+/* Token selection folded into layer 0's QKV launch of a decode step
+ * (QE = the embedding's qtype; 0: plain QKV).  Every wavefront reads the 16
+ * argmax keys the LM-head launch left, takes the largest (the token; 0 when
+ * no row was valid) and stages the token's embedding row, dequantised as
+ * embed_row_body does, as its activation; block 0 also stores that row as
+ * the hidden state h (the residual of layer 0), the token and its score at
+ * tokens[st->t - 1] and st->cur_token.  The keys and weights are requested
+ * before the embedding row, so the row's dependent load overlaps the weight
+ * loads. */
+struct SelArgs {
+    const unsigned long long *keys;
+    const uint8_t *EW;
+    const h16 *ES;
+    u32 vocab;
+    int32_t *tokens;
+    float *scores;
+    uocr_step_state *stw;
+    h16 *hout;
+};
+
+/* 8 embedding values (columns 8i..8i+7) of row tok as fp16(q * scale). */
+template <int QE>
+__device__ __forceinline__ uint4 embed_piece(const SelArgs &sa, int32_t tok, u32 i) {
+    constexpr u32 K = UOCR_K_HIDDEN;
+    union h8 {
+        uint4 u;
+        h16 h[8];
+    } o;
+    o.u = make_uint4(0u, 0u, 0u, 0u);
+    if (tok < 0 || (u32)tok >= sa.vocab) return o.u;
+    const size_t r = (size_t)tok;
+    if (QE == 1) return ((const uint4 *)((const h16 *)sa.EW + r * K))[i];
+    const float sc = (float)sa.ES[r * (K / 64u) + i / 8u];
+    if (QE == 3) {
+        const uint2 v = *(const uint2 *)(sa.EW + r * K + 8u * i);
+        const u32 w[2] = {v.x, v.y};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o.h[j] = (h16)((float)(int8_t)((w[j / 4] >> (8 * (j % 4))) & 0xffu) * sc);
+    } else {
+        const u32 j0 = (i % 8u) * 8u;
+        const uint2 v = *(const uint2 *)(sa.EW + r * (K / 2u) + (i / 8u) * 32u + (j0 & 31u));
+        const u32 w[2] = {v.x, v.y}, sh = j0 < 32u ? 0u : 4u;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int q = (int)((w[j / 4] >> (8 * (j % 4) + sh)) & 15u) - 8;
+            o.h[j] = (h16)((float)q * sc);
+        }
+    }
+    return o.u;
+}
+
 /* Work item i (0..1919): matrix m = i/640 (q,k,v), head h, pair d; a lane
  * group computes rows h*128+d and h*128+d+64 of matrix m, rounds them to
  * fp16, rotates q/k by the split-half RoPE at st->pos and stores q, or k/v
  * into the cache slot st->cache_token.  One item per lane group. */
-template <int QT>
+template <int QT, int QE>
 __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, uocr_qmat V, const h16 *__restrict__ hin,
                                                     const h16 *__restrict__ nw,
                                                     const uocr_step_state *__restrict__ st, h16 *__restrict__ qout,
-                                                    h16 *__restrict__ kc, h16 *__restrict__ vc, u32 cap) {
+                                                    h16 *__restrict__ kc, h16 *__restrict__ vc, u32 cap, SelArgs sa) {
     TL(1);
     constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_lat(C), J = j_lat(C), R = 64u / LPR;
     constexpr u32 rb = 16u * C, G = K / 64u;
@@ -689,12 +763,42 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
     const uocr_qmat M = m == 0u ? Q : (m == 1u ? Km : V);
     const u32 ra = h * 128u + d, rbw = ra + 64u;
     XStage<UOCR_K_HIDDEN, SMALL_BLOCK> sx;
-    stage_load(sx, hin, nw, UOCR_K_HIDDEN);
+    constexpr int PER = XStage<UOCR_K_HIDDEN, SMALL_BLOCK>::PER;
+    unsigned long long key = 0ull;
+    if (QE == 0) {
+        stage_load(sx, hin, nw, UOCR_K_HIDDEN);
+    } else {
+        if (lane < UOCR_LM_KEYS) key = sa.keys[lane];
+#pragma unroll
+        for (int p = 0; p < PER; ++p) sx.w[p] = ((const uint4 *)nw)[min((int)threadIdx.x + p * SMALL_BLOCK, (int)K / 8 - 1)];
+    }
     RowFrag<J> fa, fb;
     frag_load<QT, LPR, J>(fa, (const uint8_t *)M.w + (size_t)ra * rb, (const h16 *)M.s + (size_t)ra * G, C, sub);
     frag_load<QT, LPR, J>(fb, (const uint8_t *)M.w + (size_t)rbw * rb, (const h16 *)M.s + (size_t)rbw * G, C, sub);
     const u32 ct = (u32)st->cache_token;
     const float cs = st->rope_cos[d], sn = st->rope_sin[d];
+    if (QE != 0) {
+        asm volatile("" : "+v"(key)::"memory");
+        float b;
+        u32 bi;
+        key_winner(wave_max_u64(key), b, bi);
+        const int32_t tok = bi == NONE_ID ? 0 : (int32_t)bi;
+#pragma unroll
+        for (int p = 0; p < PER; ++p) sx.x[p] = embed_piece<QE>(sa, tok, (u32)min((int)threadIdx.x + p * SMALL_BLOCK, (int)K / 8 - 1));
+        if (blockIdx.x == 0) {
+#pragma unroll
+            for (int p = 0; p < PER; ++p) {
+                const int i = (int)threadIdx.x + p * SMALL_BLOCK;
+                if (i < (int)K / 8) ((uint4 *)sa.hout)[i] = sx.x[p];
+            }
+            if (threadIdx.x == 0) {
+                const int32_t t = st->t - 1;
+                sa.tokens[t] = tok;
+                if (sa.scores != nullptr) sa.scores[t] = b;
+                sa.stw->cur_token = tok;
+            }
+        }
+    }
     stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
     const float da = group_sum<LPR>(frag_dot<QT, LPR, J>(fa, xs, C, sub));
     const float db = group_sum<LPR>(frag_dot<QT, LPR, J>(fb, xs, C, sub));
@@ -747,11 +851,17 @@ constexpr int ATT_GROUPS = ATT_THREADS / 16;
 __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict__ q, const h16 *__restrict__ kc,
                                                      const h16 *__restrict__ vc, u32 cap,
                                                      const uocr_step_state *__restrict__ st, float *__restrict__ part,
-                                                     long long *__restrict__ racc) {
+                                                     long long *__restrict__ racc,
+                                                     unsigned long long *__restrict__ clear_keys) {
     TL(2);
     constexpr int S = UOCR_K_ATTN_SPLITS;
     if (racc != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
         for (int i = threadIdx.x; i < UOCR_ROUTER_ACC_WORDS; i += ATT_THREADS) racc[i] = 0;
+    }
+    /* the LM-head keys, read by layer 0's QKV launch, are re-armed for the
+     * next step (kernel order: every reader has finished) */
+    if (clear_keys != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < UOCR_LM_KEYS) {
+        clear_keys[threadIdx.x] = 0ull;
     }
     constexpr int NW = ATT_THREADS / 64;
     __shared__ float sm[NW], sl[NW];
@@ -1320,107 +1430,73 @@ __global__ void k_decode_state(uocr_step_state *st, int32_t P, int32_t t, RopeTa
 /* LM head finalize                                                          */
 /* ------------------------------------------------------------------------ */
 
-/* The selection itself, by one whole block, with the winner (b, bi) and
- * the step state's t and prompt_len (read early by the caller) in thread 0:
- * store the token (and score), advance the step state, refresh the RoPE
- * table, gather the token's embedding row. */
-template <int QE>
-__device__ __forceinline__ void lm_select_body(float b, u32 bi, int32_t t, int32_t P, uocr_step_state *st,
-                                               int advance, int32_t *tokens, float *scores,
-                                               const uint8_t *__restrict__ EW, const h16 *__restrict__ ES, u32 vocab,
-                                               h16 *__restrict__ hout, const RopeTab &tab, int with_rope) {
-    __shared__ int32_t chosen, next_pos;
+/* Step-state advance for decode step t = st->t (thread 0 of one block, then
+ * the RoPE table by threads < 64): position P + t, its KV slot on the
+ * ring plan, attention length, t + 1.  It does not depend on the token, so
+ * the LM-head launch performs it; the token is chosen by the next kernel. */
+__device__ __forceinline__ void advance_state(uocr_step_state *st, const RopeTab &tab, int with_rope) {
+    __shared__ int32_t next_pos;
     if (threadIdx.x == 0) {
-        const int32_t id = bi == NONE_ID ? 0 : (int32_t)bi;
-        tokens[t] = id;
-        if (scores != nullptr) scores[t] = bi == NONE_ID ? -INFINITY : b;
-        if (st != nullptr && advance) {
-            const int32_t gcount = t + 1;
-            const int32_t live = gcount < UOCR_K_RING ? gcount : UOCR_K_RING;
-            st->cur_token = id;
-            st->pos = P + t;
-            st->cache_token = P + (t % UOCR_K_RING);
-            st->attn_prompt = P;
-            st->attn_len = P + live;
-            st->first_gen = gcount - live;
-            st->t = t + 1;
-        }
-        chosen = id;
+        const int32_t t = st->t, P = st->prompt_len;
+        const int32_t gcount = t + 1;
+        const int32_t live = gcount < UOCR_K_RING ? gcount : UOCR_K_RING;
+        st->pos = P + t;
+        st->cache_token = P + (t % UOCR_K_RING);
+        st->attn_prompt = P;
+        st->attn_len = P + live;
+        st->first_gen = gcount - live;
+        st->t = t + 1;
         next_pos = P + t;
     }
     __syncthreads();
-    if (st != nullptr && advance && with_rope) set_rope(st, next_pos, tab);
-    if (advance && EW != nullptr) embed_row_body<QE>(EW, ES, vocab, chosen, hout);
+    if (with_rope) set_rope(st, next_pos, tab);
 }
 
-/* Final norm + LM-head GEMV + argmax + selection in one launch.  Every block
- * reduces its rows to a best (score, row) and publishes it as one 64-bit key,
- *   key = (order(score) << 32) | (0xffffffff - row)   (0: no valid row),
- * with a returning atomic max into keys[block % 16]; order() maps floats to
- * unsigned integers in the same order, so the largest key is the highest
- * score with the lowest row among equals (lm_head_q4.metal:48-97,
- * sampling.metal:173-200: NaN rows skipped, ties to the lowest id, none
- * valid -> 0).  The block then takes a ticket from a returning atomic
- * counter; the block that draws the last ticket has every key in place,
- * reads and clears the 16 keys with atomic exchanges, re-arms the counter
- * and performs the selection (lm_select_body).  Only atomics cross blocks,
- * so no device-scope fence is needed.  keys and counter start at zero and
- * are left at zero. */
-template <int QT, int LPR, int J, int QE>
-__global__ __launch_bounds__(BLOCK) void k_lm_select(const uint8_t *__restrict__ W, const h16 *__restrict__ S,
-                                                     u32 rows, const h16 *__restrict__ x,
-                                                     const h16 *__restrict__ nw, unsigned long long *keys,
-                                                     u32 *counter, uocr_step_state *st, int advance, int32_t *tokens,
-                                                     float *scores, const uint8_t *__restrict__ EW,
-                                                     const h16 *__restrict__ ES, h16 *__restrict__ hout, RopeTab tab,
-                                                     int with_rope) {
+/* Final norm + LM-head GEMV + argmax: every block reduces its rows to a best
+ * (score, row) and adds its key with an atomic max into keys[block % 16]
+ * (non-returning: nothing in this launch waits for it).  With advance,
+ * block 0 also advances the step state after its rows.  The token itself is
+ * chosen from the 16 keys by the next launch (k_qkv_rope's SEL form in a
+ * decode step, or k_lm_finalize), after the kernel boundary. */
+template <int QT, int LPR, int J>
+__global__ __launch_bounds__(BLOCK) void k_lm_keys(const uint8_t *__restrict__ W, const h16 *__restrict__ S, u32 rows,
+                                                   const h16 *__restrict__ x, const h16 *__restrict__ nw,
+                                                   unsigned long long *keys, uocr_step_state *st, int advance,
+                                                   RopeTab tab, int with_rope) {
     TL(6);
     float b = -INFINITY;
     u32 bi = NONE_ID;
-    /* the step fields the selection needs, read before the GEMV */
-    int32_t t0 = 0, P0 = 0;
-    if (st != nullptr && threadIdx.x == 0) {
-        t0 = st->t;
-        P0 = st->prompt_len;
-    }
     stream_rows<QT, LPR, J, EPI_ARGMAX>(W, S, nullptr, nullptr, rows, UOCR_K_HIDDEN, x, nw, nullptr, nullptr, b, bi);
-    __shared__ int last;
     if (threadIdx.x == 0) {
-        unsigned long long key = 0ull;
-        if (bi != NONE_ID) {
-            const u32 u = __float_as_uint(b == 0.0f ? 0.0f : b); /* -0 ranks as +0 */
-            const u32 o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-            key = ((unsigned long long)o << 32) | (unsigned long long)(0xffffffffu - bi);
-        }
-        unsigned long long old = __hip_atomic_fetch_max(keys + blockIdx.x % UOCR_LM_KEYS, key, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-        /* the ticket is drawn only after the key is in place: the fence needs
-         * the returned value, and the ticket atomic cannot move above it */
-        asm volatile("" : "+v"(old)::"memory");
-        const u32 ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = ticket == gridDim.x - 1u;
+        __hip_atomic_fetch_max(keys + blockIdx.x % UOCR_LM_KEYS, argmax_key(b, bi), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
-    __syncthreads();
-    if (!last) return;
-    if (threadIdx.x == 0) {
-        unsigned long long best = 0ull;
-#pragma unroll
-        for (int k = 0; k < UOCR_LM_KEYS; ++k) {
-            const unsigned long long v = __hip_atomic_exchange(keys + k, 0ull, __ATOMIC_RELAXED,
-                                                               __HIP_MEMORY_SCOPE_AGENT);
-            best = v > best ? v : best;
-        }
-        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (best == 0ull) {
-            b = -INFINITY;
-            bi = NONE_ID;
-        } else {
-            const u32 o = (u32)(best >> 32);
-            b = __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
-            bi = 0xffffffffu - (u32)best;
-        }
+    if (advance && st != nullptr && blockIdx.x == 0) advance_state(st, tab, with_rope);
+}
+
+/* One wavefront: reads and clears the 16 keys, stores the token (and score)
+ * at tokens[st->t - 1] (advance; the LM-head launch already advanced t) or
+ * tokens[0], sets st->cur_token, and with EW gathers the token's embedding
+ * row into hout (all of the wavefront). */
+template <int QE>
+__global__ __launch_bounds__(64) void k_lm_finalize(unsigned long long *keys, uocr_step_state *st, int advance,
+                                                    int32_t *tokens, float *scores, const uint8_t *__restrict__ EW,
+                                                    const h16 *__restrict__ ES, u32 vocab, h16 *__restrict__ hout) {
+    const u32 lane = threadIdx.x;
+    unsigned long long k = 0ull;
+    if (lane < UOCR_LM_KEYS) k = __hip_atomic_exchange(keys + lane, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long best = wave_max_u64(k);
+    float b;
+    u32 bi;
+    key_winner(best, b, bi);
+    const int32_t id = bi == NONE_ID ? 0 : (int32_t)bi;
+    if (lane == 0) {
+        const int32_t t = advance && st != nullptr ? st->t - 1 : 0;
+        tokens[t] = id;
+        if (scores != nullptr) scores[t] = b;
+        if (advance && st != nullptr) st->cur_token = id;
     }
-    lm_select_body<QE>(b, bi, t0, P0, st, advance, tokens, scores, EW, ES, rows, hout, tab, with_rope);
+    if (EW != nullptr) embed_row_body<QE>(EW, ES, vocab, id, hout);
 }
 
 
@@ -1530,14 +1606,26 @@ extern "C" hipError_t uocr_launch_rmsnorm(hipStream_t st, const uint16_t *x, con
     return hipGetLastError();
 }
 
-template <int QT>
-static void launch_qkv_qt(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
-                          const uint16_t *nw, const uocr_step_state *state, uint16_t *qout,
-                          uint16_t *kc, uint16_t *vc, u32 cap) {
+template <int QT, int QE>
+static void launch_qkv_qe(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
+                          const uint16_t *nw, const uocr_step_state *state, uint16_t *qout, uint16_t *kc,
+                          uint16_t *vc, u32 cap, const SelArgs &sa) {
     constexpr u32 R = 64u / lpr_lat(chunks_per_row<QT>(UOCR_K_HIDDEN));
     constexpr u32 ipb = (SMALL_BLOCK / 64) * R;
-    hipLaunchKernelGGL((k_qkv_rope<QT>), dim3((1920u + ipb - 1u) / ipb), dim3(SMALL_BLOCK), 0, st, Q, K, V, (const h16 *)h,
-                       (const h16 *)nw, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap);
+    hipLaunchKernelGGL((k_qkv_rope<QT, QE>), dim3((1920u + ipb - 1u) / ipb), dim3(SMALL_BLOCK), 0, st, Q, K, V,
+                       (const h16 *)h, (const h16 *)nw, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap, sa);
+}
+
+template <int QT>
+static void launch_qkv_qt(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
+                          const uint16_t *nw, const uocr_step_state *state, uint16_t *qout, uint16_t *kc,
+                          uint16_t *vc, u32 cap, const SelArgs &sa, u32 qe) {
+    switch (qe) {
+        case 0u: launch_qkv_qe<QT, 0>(st, Q, K, V, h, nw, state, qout, kc, vc, cap, sa); break;
+        case UOCR_QT_F16: launch_qkv_qe<QT, 1>(st, Q, K, V, h, nw, state, qout, kc, vc, cap, sa); break;
+        case UOCR_QT_Q8: launch_qkv_qe<QT, 3>(st, Q, K, V, h, nw, state, qout, kc, vc, cap, sa); break;
+        default: launch_qkv_qe<QT, 4>(st, Q, K, V, h, nw, state, qout, kc, vc, cap, sa); break;
+    }
 }
 
 extern "C" hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
@@ -1548,20 +1636,47 @@ extern "C" hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qma
         cache_capacity == 0u) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(Q.qtype, launch_qkv_qt, st, Q, K, V, h, nw, state, qout, kcache, vcache, cache_capacity);
+    SelArgs sa;
+    memset(&sa, 0, sizeof(sa));
+    DISPATCH_QT(Q.qtype, launch_qkv_qt, st, Q, K, V, h, nw, state, qout, kcache, vcache, cache_capacity, sa, 0u);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_qkv_rope_select(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V,
+                                                  const uint16_t *nw, uocr_step_state *state, uint16_t *qout,
+                                                  uint16_t *kcache, uint16_t *vcache, uint32_t cache_capacity,
+                                                  const uint64_t *keys, uocr_qmat E, uint32_t vocab, int32_t *tokens,
+                                                  float *scores, uint16_t *hout) {
+    if (!mat_ok(Q) || !mat_ok(K) || !mat_ok(V) || Q.qtype != K.qtype || Q.qtype != V.qtype || nw == nullptr ||
+        state == nullptr || qout == nullptr || kcache == nullptr || vcache == nullptr || cache_capacity == 0u ||
+        keys == nullptr || !mat_ok(E) || vocab == 0u || tokens == nullptr || hout == nullptr) {
+        return hipErrorInvalidValue;
+    }
+    SelArgs sa;
+    sa.keys = (const unsigned long long *)keys;
+    sa.EW = (const uint8_t *)E.w;
+    sa.ES = (const h16 *)E.s;
+    sa.vocab = vocab;
+    sa.tokens = tokens;
+    sa.scores = scores;
+    sa.stw = state;
+    sa.hout = (h16 *)hout;
+    DISPATCH_QT(Q.qtype, launch_qkv_qt, st, Q, K, V, nullptr, nw, state, qout, kcache, vcache, cache_capacity, sa,
+                E.qtype);
     return hipGetLastError();
 }
 
 extern "C" hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache,
                                             const uint16_t *vcache, uint32_t cache_capacity,
-                                            const uocr_step_state *state, float *partials, int64_t *router_acc) {
+                                            const uocr_step_state *state, float *partials, int64_t *router_acc,
+                                            uint64_t *clear_keys) {
     if (q == nullptr || kcache == nullptr || vcache == nullptr || cache_capacity == 0u || state == nullptr ||
         partials == nullptr) {
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(k_attention, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(ATT_THREADS), 0, st, (const h16 *)q,
                        (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials,
-                       (long long *)router_acc);
+                       (long long *)router_acc, (unsigned long long *)clear_keys);
     return hipGetLastError();
 }
 
@@ -1696,32 +1811,46 @@ static RopeTab rope_tab(const float *inv_freq) {
     return tab;
 }
 
-template <int QT, int QE>
-static void launch_lm_select(hipStream_t st, uocr_qmat W, u32 vocab, const uint16_t *x, const uint16_t *nw,
-                             uint32_t *work, uocr_step_state *state, int advance, int32_t *tokens, float *scores,
-                             uocr_qmat E, uint16_t *hout, const float *inv_freq) {
+template <int QT>
+static void launch_lm_keys_qt(hipStream_t st, uocr_qmat W, u32 vocab, const uint16_t *x, const uint16_t *nw,
+                              uint64_t *keys, uocr_step_state *state, int advance, const float *inv_freq) {
     constexpr u32 C = chunks_per_row<QT>(UOCR_K_HIDDEN), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
-    auto fn = k_lm_select<QT, LPR, J, QE>;
+    auto fn = k_lm_keys<QT, LPR, J>;
     const u32 groups = (vocab + R - 1u) / R;
     u32 nb = (groups + NWAVE - 1u) / NWAVE;
     nb = min(nb, min(resident_blocks(fn), (u32)UOCR_K_LM_BLOCKS));
     hipLaunchKernelGGL(fn, dim3(nb), dim3(BLOCK), 0, st, (const uint8_t *)W.w, (const h16 *)W.s, vocab,
-                       (const h16 *)x, (const h16 *)nw, (unsigned long long *)work, work + 2 * UOCR_LM_KEYS, state,
-                       advance, tokens, scores, (const uint8_t *)E.w, (const h16 *)E.s, (h16 *)hout,
+                       (const h16 *)x, (const h16 *)nw, (unsigned long long *)keys, state, advance,
                        rope_tab(inv_freq), inv_freq != nullptr ? 1 : 0);
 }
 
-template <int QT>
-static void launch_lm_select_qt(hipStream_t st, uocr_qmat W, u32 vocab, const uint16_t *x, const uint16_t *nw,
-                                uint32_t *work, uocr_step_state *state, int advance, int32_t *tokens, float *scores,
-                                uocr_qmat E, uint16_t *hout, const float *inv_freq) {
-#define LMS(QE) launch_lm_select<QT, QE>(st, W, vocab, x, nw, work, state, advance, tokens, scores, E, hout, inv_freq)
-    switch (E.w != nullptr ? E.qtype : UOCR_QT_Q4) {
-        case UOCR_QT_F16: LMS(1); break;
-        case UOCR_QT_Q8: LMS(3); break;
-        default: LMS(4); break;
+extern "C" hipError_t uocr_launch_lm_keys(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x,
+                                          const uint16_t *nw, uint64_t *keys, uocr_step_state *state, int advance,
+                                          const float *inv_freq) {
+    if (!mat_ok(W) || vocab == 0u || x == nullptr || keys == nullptr || (advance && state == nullptr)) {
+        return hipErrorInvalidValue;
     }
-#undef LMS
+    DISPATCH_QT(W.qtype, launch_lm_keys_qt, st, W, vocab, x, nw, keys, state, advance, inv_freq);
+    return hipGetLastError();
+}
+
+template <int QE>
+static void launch_lm_finalize_qe(hipStream_t st, uint64_t *keys, uocr_step_state *state, int advance,
+                                  int32_t *tokens, float *scores, uocr_qmat E, u32 vocab, uint16_t *hout) {
+    hipLaunchKernelGGL((k_lm_finalize<QE>), dim3(1), dim3(64), 0, st, (unsigned long long *)keys, state, advance,
+                       tokens, scores, (const uint8_t *)E.w, (const h16 *)E.s, vocab, (h16 *)hout);
+}
+
+extern "C" hipError_t uocr_launch_lm_finalize(hipStream_t st, uint64_t *keys, uocr_step_state *state, int advance,
+                                              int32_t *tokens, float *scores, uocr_qmat E, uint32_t vocab,
+                                              uint16_t *hout) {
+    if (keys == nullptr || tokens == nullptr || (advance && state == nullptr) ||
+        (E.w != nullptr && (!mat_ok(E) || hout == nullptr))) {
+        return hipErrorInvalidValue;
+    }
+    DISPATCH_QT(E.w != nullptr ? E.qtype : UOCR_QT_Q4, launch_lm_finalize_qe, st, keys, state, advance, tokens,
+                scores, E, vocab, hout);
+    return hipGetLastError();
 }
 
 extern "C" hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t vocab, const uint16_t *x,
@@ -1732,9 +1861,9 @@ extern "C" hipError_t uocr_launch_lm_head(hipStream_t st, uocr_qmat W, uint32_t 
         (advance && state == nullptr) || (E.w != nullptr && (!mat_ok(E) || hout == nullptr))) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(W.qtype, launch_lm_select_qt, st, W, vocab, x, nw, partials, state, advance, tokens, scores, E, hout,
-                inv_freq);
-    return hipGetLastError();
+    const hipError_t e = uocr_launch_lm_keys(st, W, vocab, x, nw, (uint64_t *)partials, state, advance, inv_freq);
+    if (e != hipSuccess) return e;
+    return uocr_launch_lm_finalize(st, (uint64_t *)partials, state, advance, tokens, scores, E, vocab, hout);
 }
 
 template <int QT>

@@ -133,6 +133,17 @@ extern "C" int uocr_op_lm_head_argmax(uint32_t qtype, const void *w, const void 
                       "lm_head_argmax");
 }
 
+extern "C" int uocr_op_lm_head_keys(uint32_t qtype, const void *w, const void *s, uint32_t vocab, const void *x,
+                                    const void *norm_w, uint64_t *keys) {
+    if (!qt_ok(qtype) || keys == nullptr || vocab == 0u) {
+        return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid lm_head_keys arguments");
+    }
+    STREAM_OR_RETURN(st);
+    return hip_status(uocr_launch_lm_keys(st, qm(qtype, w, s), vocab, (const uint16_t *)x, (const uint16_t *)norm_w,
+                                          keys, nullptr, 0, nullptr),
+                      "lm_head_keys");
+}
+
 extern "C" int uocr_op_router(const void *router_w, const void *x, const void *norm_w, int norm_topk, void *workspace,
                               uint32_t *ids, float *weights) {
     if (workspace == nullptr) return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "router needs a workspace");
@@ -205,7 +216,8 @@ extern "C" int uocr_op_attention_decode(const void *q, const void *k_cache, cons
     if (r != UOCR_OK) return r;
     int r2 = hip_status(uocr_launch_attention(st, (const uint16_t *)q, (const uint16_t *)k_cache,
                                               (const uint16_t *)v_cache, cache_capacity,
-                                              ws<uocr_step_state>(workspace, WS_STATE), ws<float>(workspace, WS_APART), nullptr),
+                                              ws<uocr_step_state>(workspace, WS_STATE), ws<float>(workspace, WS_APART), nullptr,
+                                              nullptr),
                         "attention_decode");
     if (r2 != UOCR_OK) return r2;
     return hip_status(uocr_launch_attn_merge(st, ws<float>(workspace, WS_APART), (uint16_t *)out), "attention merge");
@@ -232,7 +244,7 @@ extern "C" int uocr_op_attention_block(uint32_t qtype, const void *wq, const voi
     }
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_attention(st, qb, (const uint16_t *)k_cache, (const uint16_t *)v_cache,
-                                             cache_capacity, state, ws<float>(workspace, WS_APART), nullptr),
+                                             cache_capacity, state, ws<float>(workspace, WS_APART), nullptr, nullptr),
                        "attention");
     }
     if (r == UOCR_OK) {

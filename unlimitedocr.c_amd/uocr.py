@@ -125,6 +125,7 @@ SIGNATURES = {
     "uocr_op_swiglu": ([_U32, _VP, _VP, _VP, _VP, _U32, _U32, _VP, _VP, _VP], ct.c_int),
     "uocr_op_rmsnorm": ([_VP, _VP, _U32, _VP], ct.c_int),
     "uocr_op_lm_head_argmax": ([_U32, _VP, _VP, _U32, _VP, _VP, _VP, _VP, _VP], ct.c_int),
+    "uocr_op_lm_head_keys": ([_U32, _VP, _VP, _U32, _VP, _VP, _VP], ct.c_int),
     "uocr_op_router": ([_VP, _VP, _VP, ct.c_int, _VP, _VP, _VP], ct.c_int),
     "uocr_op_moe_ffn": ([ct.POINTER(CMoeWeights), _VP, _VP, _VP, ct.c_int, _VP, _VP, _VP, _VP], ct.c_int),
     "uocr_op_attention_decode": ([_VP, _VP, _VP, _U32, _U32, _U32, _VP, _VP], ct.c_int),
@@ -452,6 +453,11 @@ def op_rmsnorm(x, w, n, y) -> None:
 def op_lm_head_argmax(qtype, w, s, vocab, x, norm_w, ws, token, score) -> None:
     _check_op(load_library().uocr_op_lm_head_argmax(qtype, _p(w), _p(s), vocab, _p(x), _p(norm_w), _p(ws), _p(token),
                                                     _p(score)), "op_lm_head_argmax")
+
+
+def op_lm_head_keys(qtype, w, s, vocab, x, norm_w, keys) -> None:
+    _check_op(load_library().uocr_op_lm_head_keys(qtype, _p(w), _p(s), vocab, _p(x), _p(norm_w), _p(keys)),
+              "op_lm_head_keys")
 
 
 def op_router(router, x, norm_w, norm_topk, ws, ids, weights) -> None:
