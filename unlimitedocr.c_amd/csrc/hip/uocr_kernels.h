@@ -68,7 +68,7 @@ typedef struct uocr_expert_slab {
 /* Scratch sizes (bytes) the launchers expect. */
 #define UOCR_ATTN_PARTIAL_FLOATS (UOCR_K_HEADS * UOCR_K_ATTN_SPLITS * (UOCR_K_HEAD_DIM + 2))
 #define UOCR_LM_KEYS 16 /* LM-head argmax key copies (block b -> copy b % 16) */
-#define UOCR_LM_PARTIAL_WORDS (2 * UOCR_LM_KEYS + 1) /* keys + ticket counter */
+#define UOCR_LM_PARTIAL_WORDS (2 * UOCR_LM_KEYS) /* the 64-bit argmax keys, in 32-bit words */
 
 #ifdef __cplusplus
 extern "C" {
