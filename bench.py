@@ -364,6 +364,56 @@ def operator_benchmarks(log, with_cpu: bool = True, cpu_budget_s: float = 2.0) -
     return out
 
 
+# Vision linears of one encoder block (uocr_metal.m:17111-17180 call sites):
+# SAM ViT-B over the 1024 x 1024 global view (64 x 64 = 4096 patches, width
+# 768, MLP 3072) and CLIP-L over one view (257 tokens, width 1024, MLP 4096).
+VISION_SHAPES = [
+    ("sam_qkv", 3, 4096, 768, 2304, 0, 768), ("sam_proj", 3, 4096, 768, 768, 0, 0),
+    ("sam_lin1_gelu", 3, 4096, 768, 3072, 2, 0), ("sam_lin2", 3, 4096, 3072, 768, 0, 0),
+    ("clip_qkv", 3, 257, 1024, 3072, 0, 1024), ("clip_fc1_quickgelu", 3, 257, 1024, 4096, 1, 0),
+    ("clip_fc2", 3, 257, 4096, 1024, 0, 0), ("sam_lin1_gelu_f16", 1, 4096, 768, 3072, 2, 0),
+]
+
+
+def vision_benchmarks(log, with_cpu: bool = True, calls: int = 20, replays: int = 10) -> dict:
+    """uocr_op_vision_linear at the SAM / CLIP block shapes: `calls` launches
+    captured into one hipGraph, HIP events around `replays` replays.  Bound:
+    MFMA (2 m n k flops against the 2.5 PFLOP/s fp16 dense peak).  The C oracle
+    computes up to 256 rows of the same linear on the host cores; its time is
+    scaled to all m rows."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    cores = int(oracle.lib().orc_get_threads())
+    out = {}
+    for name, qt, m, k, n, act, split in VISION_SHAPES:
+        rng = np.random.default_rng(m + k + n)
+        w, s = (_q8(rng, n, k) if qt == 3 else
+                ((rng.standard_normal((n, k)) * 0.02).astype(np.float16), None))
+        x = rng.standard_normal((m, k)).astype(np.float16)
+        bias = (rng.standard_normal(n) * 0.5).astype(np.float16)
+        dw, ds = uocr.DeviceBuffer.of(w), None if s is None else uocr.DeviceBuffer.of(s)
+        db, dx = uocr.DeviceBuffer.of(bias), uocr.DeviceBuffer.of(x)
+        width = split or n
+        outs = [uocr.DeviceBuffer(m * width * 2) for _ in range(3 if split else 1)]
+        ms = _graph_time(log, [lambda: uocr.op_vision_linear(qt, dw, ds, db, m, k, n, act, split, dx, *outs)] * calls,
+                         replays)
+        flops = 2.0 * m * n * k
+        tf = flops / (ms / 1e3) / 1e12
+        entry = {"qtype": {1: "f16", 3: "q8_0"}[qt], "m": m, "k": k, "n": n, "act": act, "split": split,
+                 "us": round(ms * 1e3, 2), "tflops": round(tf, 1), "frac_of_2500": round(tf / 2500.0, 4)}
+        if with_cpu:
+            rows = min(m, 256)
+            xs = np.ascontiguousarray(x[:rows]).view(np.uint16)
+            cpu_s, cpu_n = _cpu_time(lambda: oracle.vision_linear(qt, w, s, bias.view(np.uint16), rows, k, n, act,
+                                                                  split, xs), 1.0)
+            entry["cpu"] = {"us_all_rows": round(cpu_s * m / rows * 1e6, 1), "rows_timed": rows, "calls": cpu_n,
+                            "cores": cores, "kind": "port"}
+        out[name] = entry
+        log(f"vision {name}: {entry}")
+    return out
+
+
 def copy_probe(log, nbytes: int = 512 << 20, iters: int = 4) -> None:
     """A plain device-to-device copy of known size: the reference dispatch
     for scaling FETCH_SIZE / WRITE_SIZE counters to bytes."""
@@ -432,6 +482,9 @@ def main() -> None:
                     help="cap the graph replays of the operator measurements (counter-collection runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the MFMA prefill of the config-5 prompt (Q4 profile, 1 generated token), twice")
+    ap.add_argument("--vision-only", action="store_true",
+                    help="run only the vision linear (SAM / CLIP block shape) measurements")
+    ap.add_argument("--no-vision", action="store_true", help="skip the vision linear measurements")
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue decode kernels directly instead of replaying hipGraphs (for kernel tracing)")
     args = ap.parse_args()
@@ -462,6 +515,9 @@ def main() -> None:
         print(json.dumps({"prefill": {"ms": round(p_ms, 3), "gflop": round(gf / 1e9, 1),
                                       "tflops": round(gf / (p_ms / 1e3) / 1e12, 1)}}), flush=True)
         return
+    if args.vision_only:
+        print(json.dumps({"vision": vision_benchmarks(log, not args.no_cpu_baseline)}), flush=True)
+        return
     if args.ops_only:
         print(json.dumps({"operators": operator_benchmarks(log, not args.no_cpu_baseline)}), flush=True)
         copy_probe(log)
@@ -473,6 +529,7 @@ def main() -> None:
     roof = lm_head_roofline(log)
     cpu = None if args.no_cpu_baseline else cpu_baseline(log)
     ops = None if args.no_ops else operator_benchmarks(log, not args.no_cpu_baseline)
+    vision = None if args.no_vision else vision_benchmarks(log, not args.no_cpu_baseline)
     q4 = results["q4"]
     line = {
         "metric": METRIC,
@@ -499,6 +556,7 @@ def main() -> None:
                     "note": "fp16 MFMA GEMMs + flash attention over the 932-row prompt (Q4 profile); includes the "
                             "host-to-device prompt upload"},
         "operators": ops,
+        "vision": vision,
         "decode_hbm": {p: {"tok_s": round(r["tok_s"], 2), "hbm_gbs": round(r["hbm_gbs"], 1),
                            "frac_of_8tbs": round(r["frac"], 4), "roofline_tok_s": round(r["roofline_tok_s"], 1),
                            "bytes_per_token": int(r["bytes_per_token"]), "prefill_ms": round(r["prefill_ms"], 1),

@@ -174,6 +174,30 @@ UOCR_API int uocr_op_embed(uint32_t qtype, const void *w, const void *s, uint32_
 UOCR_API int uocr_op_gemm(uint32_t qtype, const void *w, const void *s, uint32_t m, uint32_t n, uint32_t k,
                           const void *x, const void *residual, void *y);
 
+/* ---- vision linear (MFMA) ------------------------------------------------ */
+
+#ifndef UOCR_VISION_ACT_NONE
+#define UOCR_VISION_ACT_NONE 0u      /* identity */
+#define UOCR_VISION_ACT_QUICKGELU 1u /* x * sigmoid(1.702 x), CLIP MLP fc1 */
+#define UOCR_VISION_ACT_GELU_ERF 2u  /* 0.5 x (1 + erf(x / sqrt 2)), SAM MLP lin1 */
+#endif
+
+/* dst = f16(act(x . W^T + bias)) for m rows: x fp16 [m][k], W [n][k] in the
+ * .uocr layout (qtype f16, Q8_0 or Q4_0; k % 64 == 0), bias fp16 [n].
+ * split == 0: dst0 fp16 [m][n] (dst1, dst2 ignored).  split != 0 (fused QKV):
+ * n == 3 * split and column c goes to (dst0, dst1, dst2)[c / split] at
+ * [row][c % split].  erf is Abramowitz & Stegun 7.1.26, as the reference's.
+ * Replaces metal_run_vision_gemm_q8_0 (src/backend/metal/uocr_metal.m:6321-
+ * 6396) with its kernels uocr_vision_gemm_q8_0_to_f16 (kernels/gemm_q8.metal:
+ * 161-221) and uocr_vision_gemm_q4_0_to_f16 (kernels/gemm_q4.metal:63-131),
+ * and the fp16 path MPS matmul + bias/activation (uocr_metal.m:17232-17250,
+ * kernels/dense.metal:68-79, kernels/sam.metal:93-104), which is fused here
+ * (one fp16 rounding instead of two).  Errors: UOCR_ERROR_INVALID_ARGUMENT for
+ * a bad qtype, act, shape or split, or a missing bias, scales or output. */
+UOCR_API int uocr_op_vision_linear(uint32_t qtype, const void *w, const void *s, const void *bias, uint32_t m,
+                                   uint32_t k, uint32_t n, uint32_t act, uint32_t split, const void *x, void *dst0,
+                                   void *dst1, void *dst2);
+
 /* Causal attention of P prompt queries (fp16 [P][1280], RoPE applied) over
  * cache slots 0..P-1 of caches laid out [10][cache_capacity][128]; ctx fp16
  * [P][1280].  Replaces uocr_prefill_attention_flash_staged_f16_to_f16

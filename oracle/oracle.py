@@ -65,6 +65,7 @@ _SIGS = {
     "orc_forward_token": ([_VP, _VP, _U32, _VP], ct.c_int),
     "orc_select": ([_VP, _VP, ct.POINTER(_I32), ct.POINTER(_F), ct.POINTER(_F)], ct.c_int),
     "orc_session_fill_kv": ([_VP, _U32, ct.c_uint64], ct.c_int),
+    "orc_vision_linear": ([_U32, _VP, _VP, _VP, _U32, _U32, _U32, _U32, _U32, _VP, _VP, _VP, _VP], ct.c_int),
     "orc_set_threads": ([ct.c_int], None),
     "orc_get_threads": ([], ct.c_int),
 }
@@ -107,6 +108,20 @@ def gemv(qtype, W, S, rows, K, x_bits, residual_bits=None) -> np.ndarray:
     y = np.zeros(rows, np.uint16)
     assert lib().orc_gemv(qtype, ptr(W), ptr(S), rows, K, ptr(x_bits), ptr(residual_bits), ptr(y)) == 1
     return y
+
+
+def vision_linear(qtype, W, S, bias_bits, m, K, N, act, split, x_bits):
+    """f16 bits [m][N] (split == 0) or a tuple of three [m][split] arrays."""
+    x_bits = np.ascontiguousarray(x_bits, np.uint16)
+    if split == 0:
+        out = np.zeros((m, N), np.uint16)
+        assert lib().orc_vision_linear(qtype, ptr(W), ptr(S), ptr(bias_bits), m, K, N, act, 0, ptr(x_bits), ptr(out),
+                                       None, None) == 1
+        return out
+    outs = [np.zeros((m, split), np.uint16) for _ in range(3)]
+    assert lib().orc_vision_linear(qtype, ptr(W), ptr(S), ptr(bias_bits), m, K, N, act, split, ptr(x_bits),
+                                   *[ptr(o) for o in outs]) == 1
+    return tuple(outs)
 
 
 def swiglu(qtype, G, Gs, U, Us, rows, K, x_bits) -> np.ndarray:

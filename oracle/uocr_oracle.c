@@ -693,6 +693,70 @@ int orc_embed_row(uint32_t qtype, const void *W, const uint16_t *S, uint32_t row
 }
 
 /* ------------------------------------------------------------------------ */
+/* vision linear                                                            */
+/* ------------------------------------------------------------------------ */
+
+/* Abramowitz & Stegun 7.1.26, as sam.metal:78-87 evaluates it. */
+static float erf_as(float x) {
+    const float sign = x < 0.0f ? -1.0f : 1.0f;
+    const float ax = fabsf(x);
+    const float t = 1.0f / (1.0f + 0.3275911f * ax);
+    const float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
+                            0.254829592f) * t * expf(-(ax * ax));
+    return sign * y;
+}
+
+static float vision_act(uint32_t act, float v) {
+    if (act == 1u) return v / (1.0f + expf(-1.702f * v));
+    if (act == 2u) return 0.5f * v * (1.0f + erf_as(v * 0.70710678118654752440f));
+    return v;
+}
+
+int orc_vision_linear(uint32_t qtype, const void *W, const uint16_t *S, const uint16_t *bias, uint32_t m,
+                      uint32_t K, uint32_t N, uint32_t act, uint32_t split, const uint16_t *x, uint16_t *dst0,
+                      uint16_t *dst1, uint16_t *dst2) {
+    if (!qtype_ok(qtype) || !W || !bias || !x || !dst0 || m == 0u || N == 0u || K == 0u || (K % UOCR_QGROUP) ||
+        act > 2u || (qtype != UOCR_TENSOR_F16 && !S) || (split && (N != 3u * split || !dst1 || !dst2))) {
+        return 0;
+    }
+    /* the fp16 weight tile as the GEMM stages it */
+    float *wf = (float *)malloc((size_t)N * K * sizeof(float));
+    float *xf = widen(x, (uint32_t)((size_t)m * K));
+    if (!wf || !xf) {
+        free(wf);
+        free(xf);
+        return 0;
+    }
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < (int64_t)N; ++n) {
+        for (uint32_t c = 0; c < K; ++c) {
+            wf[(size_t)n * K + c] = orc_f16_to_f32(orc_f32_to_f16(orc_weight_at(qtype, W, S, K, (uint32_t)n, c)));
+        }
+    }
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < (int64_t)m; ++r) {
+        const float *xr = xf + (size_t)r * K;
+        for (uint32_t n = 0; n < N; ++n) {
+            const float *wr = wf + (size_t)n * K;
+            float acc = 0.0f;
+            for (uint32_t c = 0; c < K; ++c) acc = fmaf(xr[c], wr[c], acc);
+            if (qtype == UOCR_TENSOR_F16) acc = orc_f16_to_f32(orc_f32_to_f16(acc));
+            const uint16_t v = orc_f32_to_f16(vision_act(act, acc + orc_f16_to_f32(bias[n])));
+            if (split == 0u) {
+                dst0[(size_t)r * N + n] = v;
+            } else {
+                const uint32_t pj = n / split;
+                uint16_t *d = pj == 0u ? dst0 : (pj == 1u ? dst1 : dst2);
+                d[(size_t)r * split + (n - pj * split)] = v;
+            }
+        }
+    }
+    free(wf);
+    free(xf);
+    return 1;
+}
+
+/* ------------------------------------------------------------------------ */
 /* model over a .uocr image                                                 */
 /* ------------------------------------------------------------------------ */
 

@@ -149,6 +149,24 @@ int orc_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint1
 int orc_embed_row(uint32_t qtype, const void *W, const uint16_t *S, uint32_t rows, uint32_t K,
                   int32_t token, uint16_t *out);
 
+/* ---- vision linear ------------------------------------------------------ */
+
+/* dst = f16(act(x . W^T + bias)) per row (kernels/gemm_q8.metal:161-221,
+ * gemm_q4.metal:63-131): each quantised weight is first rounded to fp16 as
+ * half(float(q) * scale) (gemm_q8.metal:58, the B-tile staging), products
+ * accumulate in fp32 over k in order, then bias, activation (act 1:
+ * x / (1 + exp(-1.702 x)), dense.metal:64-66; act 2: 0.5 x (1 + erf(x /
+ * sqrt 2)) with the Abramowitz & Stegun 7.1.26 erf, sam.metal:78-91) and one
+ * fp16 rounding.  qtype f16 follows the reference's MPS path
+ * (uocr_metal.m:17232-17250): the product is rounded to fp16, then bias and
+ * activation are applied in fp32 and rounded again (dense.metal:68-79).
+ * split != 0: n == 3 * split, column c to (dst0, dst1, dst2)[c / split] at
+ * [row][c % split] (gemm_q8.metal:208-219).  Pinned by brute-force fp64
+ * products and the closed forms of both activations (tests/test_oracle.py). */
+int orc_vision_linear(uint32_t qtype, const void *W, const uint16_t *S, const uint16_t *bias, uint32_t m,
+                      uint32_t K, uint32_t N, uint32_t act, uint32_t split, const uint16_t *x, uint16_t *dst0,
+                      uint16_t *dst1, uint16_t *dst2);
+
 /* ---- full model over a .uocr image in memory ---------------------------- */
 typedef struct orc_model orc_model;
 orc_model *orc_model_open(const uint8_t *bytes, size_t size, char *err, size_t err_size);

@@ -134,3 +134,55 @@ def test_batched_and_token_prefill_agree(gpu):
                                                 flags=uocr.GEN_IGNORE_EOS | uocr.GEN_TOKEN_PREFILL)
     eng.close()
     assert abs(float(a_sc[0]) - float(b_sc[0])) <= 2e-2 + 1e-2 * abs(float(b_sc[0]))
+
+
+# vision linear: (qtype, m, k, n, act, split) at the SAM ViT-B global view
+# (4096 tokens, 768 wide: qkv 2304 split 768, lin1 3072 + GELU, lin2), the
+# CLIP-L view (257 tokens, 1024 wide: qkv split 1024, fc1 4096 + QuickGELU,
+# fc2), the projector (2048 -> 1280), the Q4 and fp16 kernels, and ragged
+# tiles (m not a multiple of 64, n not a multiple of 128).
+VISION_CASES = [
+    (3, 4096, 768, 2304, 0, 768), (3, 4096, 768, 3072, 2, 0), (3, 4096, 3072, 768, 0, 0),
+    (3, 257, 1024, 3072, 0, 1024), (3, 257, 1024, 4096, 1, 0), (3, 257, 4096, 1024, 0, 0),
+    (3, 256, 2048, 1280, 0, 0), (4, 257, 1024, 4096, 1, 0), (1, 257, 1024, 4096, 1, 0),
+    (1, 4096, 768, 3072, 2, 0), (4, 4096, 768, 2304, 0, 768), (3, 1, 64, 96, 2, 0), (1, 65, 128, 40, 1, 0),
+    (4, 100, 192, 96, 2, 32),
+]
+
+
+@pytest.mark.parametrize("qtype,m,k,n,act,split", VISION_CASES)
+def test_vision_linear_matches_oracle(gpu, oracle, qtype, m, k, n, act, split):
+    """All m rows run on the GPU; the oracle checks the first and last 64 rows
+    and 32 random ones (rows are independent)."""
+    uocr = gpu
+    rng = np.random.default_rng(m + k + n + 10 * act + qtype)
+    w, s = weights_for(qtype, rng, n, k)
+    x = rand_f16(rng, (m, k))
+    bias = rand_f16(rng, n, 0.5)
+    dw, ds, db, dx = dev(uocr, w), None if s is None else dev(uocr, s), dev(uocr, bias), dev(uocr, x)
+    width = split or n
+    outs = [uocr.DeviceBuffer(m * width * 2) for _ in range(3 if split else 1)]
+    uocr.op_vision_linear(qtype, dw, ds, db, m, k, n, act, split, dx, *outs)
+    uocr.sync()
+    got = np.hstack([o.download(np.uint16).reshape(m, width) for o in outs])
+    rows = np.unique(np.concatenate([np.arange(min(m, 64)), np.arange(max(0, m - 64), m),
+                                     rng.integers(0, m, size=32)]))
+    ref = oracle.vision_linear(qtype, w, s, bias.view(np.uint16), rows.size, k, n, act, split,
+                               np.ascontiguousarray(x[rows]).view(np.uint16))
+    ref = np.hstack(ref) if split else ref
+    assert_f16_close(got[rows], ref)
+
+
+def test_vision_linear_rejects_bad_arguments(gpu):
+    uocr = gpu
+    buf = uocr.DeviceBuffer(1 << 16)
+    with pytest.raises(RuntimeError):
+        uocr.op_vision_linear(3, buf, buf, buf, 4, 100, 96, 0, 0, buf, buf)  # k not a multiple of 64
+    with pytest.raises(RuntimeError):
+        uocr.op_vision_linear(3, buf, buf, None, 4, 128, 96, 0, 0, buf, buf)  # bias is required
+    with pytest.raises(RuntimeError):
+        uocr.op_vision_linear(3, buf, buf, buf, 4, 128, 96, 3, 0, buf, buf)  # unknown activation
+    with pytest.raises(RuntimeError):
+        uocr.op_vision_linear(3, buf, buf, buf, 4, 128, 96, 0, 30, buf, buf, buf, buf)  # n != 3 * split
+    with pytest.raises(RuntimeError):
+        uocr.op_vision_linear(3, buf, buf, buf, 4, 128, 96, 0, 32, buf, buf)  # split needs three outputs

@@ -374,3 +374,68 @@ def test_rmsnorm_f16_and_embed(oracle):
         row = oracle.embed_row(qt, W, S, 20, 1280, 13)
         assert np.array_equal(row.view(np.float16), dequant(qt, W, S)[13].astype(np.float16))
         assert not oracle.embed_row(qt, W, S, 20, 1280, 20).any()  # out of range -> zeros
+
+
+# ---------------------------------------------------------------------------
+# vision linear (gemm_q8.metal:161-221, gemm_q4.metal:63-131, MPS fp16 path)
+# ---------------------------------------------------------------------------
+
+def _vision_float64(qtype, w, s, bias, x, act):
+    """float64 brute force: weights staged as fp16(q * scale), the fp16 path's
+    product rounded to fp16 (MPS), exact erf from scipy."""
+    from scipy.special import erf
+
+    from conftest import dequant
+    wd = dequant(qtype, w, s).astype(np.float16).astype(np.float64)
+    z = x.astype(np.float64) @ wd.T
+    if qtype == 1:
+        z = z.astype(np.float16).astype(np.float64)
+    z = z + bias.astype(np.float64)
+    if act == 1:
+        z = z / (1.0 + np.exp(-1.702 * z))
+    elif act == 2:
+        z = 0.5 * z * (1.0 + erf(z / math.sqrt(2.0)))
+    return z
+
+
+@pytest.mark.parametrize("qtype", [1, 3, 4])
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_vision_linear_vs_float64(oracle, qtype, act):
+    from conftest import weights_for
+    rng = np.random.default_rng(10 * qtype + act)
+    m, k, n = 5, 192, 48
+    w, s = weights_for(qtype, rng, n, k)
+    x = rand_f16(rng, (m, k))
+    bias = rand_f16(rng, n, 2.0)  # spreads the pre-activations over the curved part of both GELUs
+    got = oracle.vision_linear(qtype, w, s, bias.view(np.uint16), m, k, n, act, 0, x.view(np.uint16))
+    got = got.view(np.float16).astype(np.float64)
+    ref = _vision_float64(qtype, w, s, bias, x, act)
+    # fp16 half-ulp of the output (4.9e-4 relative) plus fp32 accumulation and,
+    # for the fp16 path, one product ulp when the two sums round differently
+    assert np.all(np.abs(got - ref) <= 1e-3 * np.abs(ref) + 5e-4), np.abs(got - ref).max()
+
+
+def test_vision_linear_split_is_column_thirds(oracle):
+    rng = np.random.default_rng(77)
+    m, k, split = 7, 128, 64
+    w, s = q8_weights(rng, 3 * split, k)
+    x = rand_f16(rng, (m, k)).view(np.uint16)
+    bias = rand_f16(rng, 3 * split).view(np.uint16)
+    whole = oracle.vision_linear(3, w, s, bias, m, k, 3 * split, 0, 0, x)
+    q, kk, v = oracle.vision_linear(3, w, s, bias, m, k, 3 * split, 0, split, x)
+    assert np.array_equal(np.hstack([q, kk, v]), whole)
+
+
+def test_vision_linear_rejects(oracle):
+    lib = oracle.lib()
+    p = oracle.ptr
+    w = np.zeros((96, 128), np.int8)
+    s = np.ones((96, 2), np.float16)
+    b = np.zeros(96, np.uint16)
+    x = np.zeros((2, 128), np.uint16)
+    o = np.zeros((2, 96), np.uint16)
+    assert lib.orc_vision_linear(3, p(w), p(s), p(b), 2, 128, 96, 0, 0, p(x), p(o), None, None) == 1
+    assert lib.orc_vision_linear(3, p(w), p(s), p(b), 2, 100, 96, 0, 0, p(x), p(o), None, None) == 0  # k % 64
+    assert lib.orc_vision_linear(3, p(w), p(s), None, 2, 128, 96, 0, 0, p(x), p(o), None, None) == 0  # bias
+    assert lib.orc_vision_linear(3, p(w), p(s), p(b), 2, 128, 96, 3, 0, p(x), p(o), None, None) == 0  # act
+    assert lib.orc_vision_linear(3, p(w), p(s), p(b), 2, 128, 96, 0, 30, p(x), p(o), p(o), p(o)) == 0  # n != 3 split

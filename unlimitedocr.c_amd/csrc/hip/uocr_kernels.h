@@ -179,6 +179,13 @@ hipError_t uocr_launch_decode_state(hipStream_t st, uocr_step_state *state, int3
 #define UOCR_GEMM_F16 0    /* out = f16(acc (+ res)) */
 #define UOCR_GEMM_F32 1    /* out = acc (fp32) */
 #define UOCR_GEMM_SWIGLU 2 /* out = f16(silu(acc(W[0])) * acc(W[1])) */
+#define UOCR_GEMM_VISION 3 /* out = f16(act(acc + bias)), optionally split into three outputs */
+
+#ifndef UOCR_VISION_ACT_NONE
+#define UOCR_VISION_ACT_NONE 0u      /* identity */
+#define UOCR_VISION_ACT_QUICKGELU 1u /* x * sigmoid(1.702 x), CLIP MLP */
+#define UOCR_VISION_ACT_GELU_ERF 2u  /* 0.5 x (1 + erf(x / sqrt 2)), SAM MLP */
+#endif
 
 /* C[m][n] = sum_k A[m][k] W[n][k]: fp16 activations A (row stride lda,
  * multiple of 8), weights in the .uocr layout ([N][K], K % 64 == 0).
@@ -202,6 +209,12 @@ typedef struct uocr_gemm_desc {
     uint32_t ldo;
     const uint16_t *res;
     uint32_t ldr;
+    /* UOCR_GEMM_VISION only: bias [N] (required), activation, and split: 0
+     * writes out [M][ldo]; else N == 3 * split and column c goes to
+     * (out, out1, out2)[c / split] at [row][c % split], row stride split */
+    const uint16_t *bias;
+    uint32_t act, split;
+    void *out1, *out2;
 } uocr_gemm_desc;
 
 hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d);

@@ -286,6 +286,34 @@ extern "C" int uocr_op_gemm(uint32_t qtype, const void *w, const void *s, uint32
     return hip_status(uocr_launch_gemm(st, UOCR_GEMM_F16, &d), "gemm");
 }
 
+extern "C" int uocr_op_vision_linear(uint32_t qtype, const void *w, const void *s, const void *bias, uint32_t m,
+                                     uint32_t k, uint32_t n, uint32_t act, uint32_t split, const void *x, void *dst0,
+                                     void *dst1, void *dst2) {
+    if (!qt_ok(qtype) || w == nullptr || bias == nullptr || x == nullptr || dst0 == nullptr || m == 0u || n == 0u ||
+        k == 0u || k % 64u != 0u || (qtype != UOCR_QT_F16 && s == nullptr) || act > UOCR_VISION_ACT_GELU_ERF ||
+        (split != 0u && (n != 3u * split || dst1 == nullptr || dst2 == nullptr))) {
+        return op_fail(UOCR_ERROR_INVALID_ARGUMENT,
+                       "invalid vision linear arguments (k % 64 == 0, bias required, split: n == 3 * split)");
+    }
+    STREAM_OR_RETURN(st);
+    uocr_gemm_desc d;
+    memset(&d, 0, sizeof(d));
+    d.A = (const uint16_t *)x;
+    d.lda = k;
+    d.M = m;
+    d.N = n;
+    d.K = k;
+    d.W[0] = qm(qtype, w, s);
+    d.out = dst0;
+    d.ldo = n;
+    d.bias = (const uint16_t *)bias;
+    d.act = act;
+    d.split = split;
+    d.out1 = dst1;
+    d.out2 = dst2;
+    return hip_status(uocr_launch_gemm(st, UOCR_GEMM_VISION, &d), "vision linear");
+}
+
 extern "C" int uocr_op_prefill_attention(const void *q, const void *k_cache, const void *v_cache,
                                          uint32_t cache_capacity, uint32_t prompt_length, void *ctx) {
     if (q == nullptr || k_cache == nullptr || v_cache == nullptr || ctx == nullptr || prompt_length == 0u ||

@@ -72,7 +72,24 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
-enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2 };
+enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2, GE_VISION = 3 };
+
+/* QuickGELU of the CLIP MLP: x * sigmoid(1.702 x) (dense.metal:63-66). */
+__device__ __forceinline__ float quick_gelu(float x) {
+    return x / (1.0f + expf(-1.702f * x));
+}
+
+/* GELU of the SAM MLP, 0.5 x (1 + erf(x / sqrt 2)), with erf from
+ * Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7), the approximation the
+ * reference's SAM kernels use (sam.metal:78-91). */
+__device__ __forceinline__ float gelu_erf_as(float x) {
+    const float z = x * 0.70710678118654752f;
+    const float az = fabsf(z);
+    const float t = 1.0f / (1.0f + 0.3275911f * az);
+    const float poly = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) * t;
+    const float e = 1.0f - poly * expf(-az * az);
+    return 0.5f * x * (1.0f + (z < 0.0f ? -e : e));
+}
 
 /* Weight piece of one K step (one 64-column quantisation group) for the
  * weight row n = the output column of this lane, lane half h = lane / 32:
@@ -168,6 +185,10 @@ struct GemmArgs {
     u32 ldo;
     const h16 *res;      /* GE_F16: optional residual, row stride ldr */
     u32 ldr;
+    const h16 *bias;     /* GE_VISION: per-column bias */
+    u32 act;             /* GE_VISION: UOCR_VISION_ACT_* */
+    u32 split;           /* GE_VISION: 0, or the width of each of out/out1/out2 */
+    void *out1, *out2;
 };
 
 /* C[m][n] = sum_k A[m][k] W[n][k] over one 64 x 128 tile per block.  Wave
@@ -298,6 +319,17 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
                 ((float *)p.out)[orw * p.ldo + col] = acc[0][j][i];
             } else if (EPI == GE_SWIGLU) {
                 ((h16 *)p.out)[orw * p.ldo + col] = (h16)(silu_p(acc[0][j][i]) * acc[NMAT - 1][j][i]);
+            } else if (EPI == GE_VISION) {
+                float v = acc[0][j][i] + (float)p.bias[col];
+                if (p.act == UOCR_VISION_ACT_QUICKGELU) v = quick_gelu(v);
+                else if (p.act == UOCR_VISION_ACT_GELU_ERF) v = gelu_erf_as(v);
+                if (p.split == 0u) {
+                    ((h16 *)p.out)[orw * p.ldo + col] = (h16)v;
+                } else {
+                    const u32 pj = col / p.split, lc = col - pj * p.split;
+                    h16 *dst = (h16 *)(pj == 0u ? p.out : (pj == 1u ? p.out1 : p.out2));
+                    dst[orw * p.split + lc] = (h16)v;
+                }
             } else {
                 float v = acc[0][j][i];
                 if (p.res != nullptr) v += (float)p.res[orw * p.ldr + col];
@@ -724,9 +756,20 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
     a.ldo = d->ldo;
     a.res = (const h16 *)d->res;
     a.ldr = d->ldr;
+    a.bias = (const h16 *)d->bias;
+    a.act = d->act;
+    a.split = d->split;
+    a.out1 = d->out1;
+    a.out2 = d->out2;
     const dim3 grid(grouped ? d->max_tiles : (d->M + TM - 1u) / TM, (d->N + TN - 1u) / TN);
     const u32 qt = d->W[0].qtype;
-    if (epi == UOCR_GEMM_F32) {
+    if (epi == UOCR_GEMM_VISION) {
+        if (grouped || d->bias == nullptr || d->act > UOCR_VISION_ACT_GELU_ERF ||
+            (d->split != 0u && (d->N != 3u * d->split || d->out1 == nullptr || d->out2 == nullptr))) {
+            return hipErrorInvalidValue;
+        }
+        gemm_dispatch<GE_VISION, false>(st, qt, a, grid);
+    } else if (epi == UOCR_GEMM_F32) {
         if (grouped) gemm_dispatch<GE_F32, true>(st, qt, a, grid);
         else gemm_dispatch<GE_F32, false>(st, qt, a, grid);
     } else if (epi == UOCR_GEMM_SWIGLU) {

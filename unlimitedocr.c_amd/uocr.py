@@ -133,6 +133,7 @@ SIGNATURES = {
                                  _U32, _VP, _VP], ct.c_int),
     "uocr_op_embed": ([_U32, _VP, _VP, _U32, _VP, _VP], ct.c_int),
     "uocr_op_gemm": ([_U32, _VP, _VP, _U32, _U32, _U32, _VP, _VP, _VP], ct.c_int),
+    "uocr_op_vision_linear": ([_U32, _VP, _VP, _VP, _U32, _U32, _U32, _U32, _U32, _VP, _VP, _VP, _VP], ct.c_int),
     "uocr_op_prefill_attention": ([_VP, _VP, _VP, _U32, _U32, _VP], ct.c_int),
     "uocr_op_moe_rows_workspace_bytes": ([_U32], _SZ),
     "uocr_op_moe_ffn_rows": ([ct.POINTER(CMoeWeights), _VP, _VP, _VP, _U32, ct.c_int, _VP, _VP], ct.c_int),
@@ -488,6 +489,15 @@ def op_embed(qtype, w, s, vocab, token, out) -> None:
 
 def op_gemm(qtype, w, s, m, n, k, x, residual, y) -> None:
     _check_op(load_library().uocr_op_gemm(qtype, _p(w), _p(s), m, n, k, _p(x), _p(residual), _p(y)), "op_gemm")
+
+
+VISION_ACT_NONE, VISION_ACT_QUICKGELU, VISION_ACT_GELU_ERF = 0, 1, 2
+
+
+def op_vision_linear(qtype, w, s, bias, m, k, n, act, split, x, dst0, dst1=None, dst2=None) -> None:
+    """dst = f16(act(x . W^T + bias)); split != 0 routes column thirds to dst0/dst1/dst2."""
+    _check_op(load_library().uocr_op_vision_linear(qtype, _p(w), _p(s), _p(bias), m, k, n, act, split, _p(x),
+                                                   _p(dst0), _p(dst1), _p(dst2)), "op_vision_linear")
 
 
 def op_prefill_attention(q, kc, vc, cap, prompt_len, ctx) -> None:
