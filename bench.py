@@ -396,8 +396,10 @@ def vision_benchmarks(log, with_cpu: bool = True, calls: int = 20, replays: int 
         db, dx = uocr.DeviceBuffer.of(bias), uocr.DeviceBuffer.of(x)
         width = split or n
         outs = [uocr.DeviceBuffer(m * width * 2) for _ in range(3 if split else 1)]
-        ms = _graph_time(log, [lambda: uocr.op_vision_linear(qt, dw, ds, db, m, k, n, act, split, dx, *outs)] * calls,
-                         replays)
+        call = lambda: uocr.op_vision_linear(qt, dw, ds, db, m, k, n, act, split, dx, *outs)
+        call()  # eager first call: sizes the split-K partials buffer outside the capture
+        uocr.sync()
+        ms = _graph_time(log, [call] * calls, replays)
         flops = 2.0 * m * n * k
         tf = flops / (ms / 1e3) / 1e12
         entry = {"qtype": {1: "f16", 3: "q8_0"}[qt], "m": m, "k": k, "n": n, "act": act, "split": split,

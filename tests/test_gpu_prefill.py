@@ -140,13 +140,15 @@ def test_batched_and_token_prefill_agree(gpu):
 # (4096 tokens, 768 wide: qkv 2304 split 768, lin1 3072 + GELU, lin2), the
 # CLIP-L view (257 tokens, 1024 wide: qkv split 1024, fc1 4096 + QuickGELU,
 # fc2), the projector (2048 -> 1280), the Q4 and fp16 kernels, and ragged
-# tiles (m not a multiple of 64, n not a multiple of 128).
+# tiles (m not a multiple of 64, n not a multiple of 128).  Grids of fewer
+# than 256 tiles split K (the CLIP shapes; 21 K steps in 4 splits of 6, 6, 6
+# and 3 in the 1344-wide case).
 VISION_CASES = [
     (3, 4096, 768, 2304, 0, 768), (3, 4096, 768, 3072, 2, 0), (3, 4096, 3072, 768, 0, 0),
     (3, 257, 1024, 3072, 0, 1024), (3, 257, 1024, 4096, 1, 0), (3, 257, 4096, 1024, 0, 0),
     (3, 256, 2048, 1280, 0, 0), (4, 257, 1024, 4096, 1, 0), (1, 257, 1024, 4096, 1, 0),
     (1, 4096, 768, 3072, 2, 0), (4, 4096, 768, 2304, 0, 768), (3, 1, 64, 96, 2, 0), (1, 65, 128, 40, 1, 0),
-    (4, 100, 192, 96, 2, 32),
+    (4, 100, 192, 96, 2, 32), (3, 100, 1344, 256, 2, 0),
 ]
 
 
@@ -186,3 +188,32 @@ def test_vision_linear_rejects_bad_arguments(gpu):
         uocr.op_vision_linear(3, buf, buf, buf, 4, 128, 96, 0, 30, buf, buf, buf, buf)  # n != 3 * split
     with pytest.raises(RuntimeError):
         uocr.op_vision_linear(3, buf, buf, buf, 4, 128, 96, 0, 32, buf, buf)  # split needs three outputs
+
+
+def test_vision_linear_split_k_in_a_graph(gpu, oracle):
+    """The CLIP fc2 shape (split K, partials reduced by a second kernel)
+    captured into a hipGraph: every replay equals the eager call."""
+    uocr = gpu
+    rng = np.random.default_rng(5)
+    m, k, n = 257, 4096, 1024
+    w, s = weights_for(3, rng, n, k)
+    x = rand_f16(rng, (m, k))
+    bias = rand_f16(rng, n, 0.5)
+    dw, ds, db, dx = dev(uocr, w), dev(uocr, s), dev(uocr, bias), dev(uocr, x)
+    eager, dy = uocr.DeviceBuffer(m * n * 2), uocr.DeviceBuffer(m * n * 2)
+    uocr.op_vision_linear(3, dw, ds, db, m, k, n, 0, 0, dx, eager)
+    uocr.sync()
+    ref = eager.download(np.uint16)
+    with uocr.Capture() as g:
+        uocr.op_vision_linear(3, dw, ds, db, m, k, n, 0, 0, dx, dy)
+    try:
+        for _ in range(3):
+            dy.zero()
+            g.replay(1)
+            uocr.sync()
+            assert np.array_equal(dy.download(np.uint16), ref)
+    finally:
+        g.release()
+    rows = np.arange(0, m, 16)
+    assert_f16_close(ref.reshape(m, n)[rows], oracle.vision_linear(3, w, s, bias.view(np.uint16), rows.size, k, n, 0,
+                                                                   0, np.ascontiguousarray(x[rows]).view(np.uint16)))

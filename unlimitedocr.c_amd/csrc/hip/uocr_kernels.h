@@ -215,6 +215,11 @@ typedef struct uocr_gemm_desc {
     const uint16_t *bias;
     uint32_t act, split;
     void *out1, *out2;
+    /* UOCR_GEMM_VISION only: ksplit > 1 splits K over that many blocks per
+     * tile, each writing fp32 partials into part ([ksplit][M][N] floats),
+     * reduced in order by a second kernel; ksplit <= 1 or part NULL: no split */
+    uint32_t ksplit;
+    float *part;
 } uocr_gemm_desc;
 
 hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d);

@@ -286,6 +286,21 @@ extern "C" int uocr_op_gemm(uint32_t qtype, const void *w, const void *s, uint32
     return hip_status(uocr_launch_gemm(st, UOCR_GEMM_F16, &d), "gemm");
 }
 
+/* Split-K partials of the vision linear: grown on demand, kept until the
+ * process ends (one buffer per process, so concurrent calls are not
+ * supported).  Grids under one block per CU split K (at least 4 K steps per
+ * split, at most 8 splits) so that the tile grid fills the chip. */
+static float *g_vision_part = nullptr;
+static size_t g_vision_part_bytes = 0;
+
+static uint32_t vision_ksplit(uint32_t m, uint32_t n, uint32_t k) {
+    const uint32_t blocks = ((m + 63u) / 64u) * ((n + 127u) / 128u), steps = k / 64u;
+    if (blocks >= 256u) return 1u;
+    uint32_t s = 1u;
+    while (s < 8u && blocks * s < 512u && steps / (2u * s) >= 4u) s *= 2u;
+    return s;
+}
+
 extern "C" int uocr_op_vision_linear(uint32_t qtype, const void *w, const void *s, const void *bias, uint32_t m,
                                      uint32_t k, uint32_t n, uint32_t act, uint32_t split, const void *x, void *dst0,
                                      void *dst1, void *dst2) {
@@ -311,6 +326,25 @@ extern "C" int uocr_op_vision_linear(uint32_t qtype, const void *w, const void *
     d.split = split;
     d.out1 = dst1;
     d.out2 = dst2;
+    d.ksplit = vision_ksplit(m, n, k);
+    if (d.ksplit > 1u) {
+        const size_t need = (size_t)d.ksplit * m * n * sizeof(float);
+        if (need > g_vision_part_bytes) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+                void *p = nullptr;
+                if (hipStreamSynchronize(st) == hipSuccess && hipMalloc(&p, need) == hipSuccess) {
+                    if (g_vision_part != nullptr) (void)hipFree(g_vision_part);
+                    g_vision_part = (float *)p;
+                    g_vision_part_bytes = need;
+                }
+            }
+        }
+        /* no room (or a capture in progress): the unsplit kernel, same result
+         * up to fp32 summation order */
+        if (need > g_vision_part_bytes) d.ksplit = 1u;
+        d.part = g_vision_part;
+    }
     return hip_status(uocr_launch_gemm(st, UOCR_GEMM_VISION, &d), "vision linear");
 }
 

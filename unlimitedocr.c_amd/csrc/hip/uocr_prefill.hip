@@ -72,7 +72,7 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
-enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2, GE_VISION = 3 };
+enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2, GE_VISION = 3, GE_PART = 4 };
 
 /* QuickGELU of the CLIP MLP: x * sigmoid(1.702 x) (dense.metal:63-66). */
 __device__ __forceinline__ float quick_gelu(float x) {
@@ -189,6 +189,7 @@ struct GemmArgs {
     u32 act;             /* GE_VISION: UOCR_VISION_ACT_* */
     u32 split;           /* GE_VISION: 0, or the width of each of out/out1/out2 */
     void *out1, *out2;
+    u32 kst;             /* split-K: K steps per blockIdx.z (0: all of K in one block) */
 };
 
 /* C[m][n] = sum_k A[m][k] W[n][k] over one 64 x 128 tile per block.  Wave
@@ -252,25 +253,35 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
      * argument struct would copy it to private memory */
     const h16 *Ap = p.A;
     const u32 lda = p.lda, Kd = p.K;
-    const u32 NS = Kd / TK;
+    const u32 NT = Kd / TK, kb0 = p.kst != 0u ? blockIdx.z * p.kst : 0u;
+    const u32 NS = p.kst != 0u ? min(p.kst, NT - kb0) : NT;
     u32 ka[GDEPTH][2][4]; /* words, not uint4: no struct copies, so they stay in registers */
     u32 kb[GDEPTH][NMAT][BPiece<QT>::NW], ks[GDEPTH][NMAT];
+    /* this thread's two activation rows, resolved once */
+    const h16 *arp[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const u32 idx = t + q * PB;
+        arp[q] = Ap + (size_t)arow[idx >> 3] * lda + (size_t)kb0 * TK + 8u * (idx & 7u);
+    }
     auto issue = [&](auto D, u32 st) {
         constexpr int d = decltype(D)::value;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            const u32 idx = t + q * PB, r = idx >> 3, c8 = idx & 7u;
-            const uint4 v = *(const uint4 *)(Ap + (size_t)arow[r] * lda + st * TK + 8u * c8);
+            const uint4 v = *(const uint4 *)(arp[q] + st * TK);
             ka[d][q][0] = v.x;
             ka[d][q][1] = v.y;
             ka[d][q][2] = v.z;
             ka[d][q][3] = v.w;
         }
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) b_load<QT>(kb[d][m], ks[d][m], wp[m], sp[m], Kd, nrow, st, hf);
+        for (int m = 0; m < NMAT; ++m) b_load<QT>(kb[d][m], ks[d][m], wp[m], sp[m], Kd, nrow, kb0 + st, hf);
     };
     auto step = [&](auto D, u32 st) {
         constexpr int d = decltype(D)::value;
+        /* keeps the scheduler from hoisting a later step's dequantisation
+         * (which waits for that step's loads) into this one */
+        __builtin_amdgcn_sched_barrier(0);
         h16 *ab = as[st & 1u];
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
@@ -283,7 +294,11 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
         /* the other buffer's readers (step st - 1) all passed this barrier
          * before anyone writes it again at step st + 1 */
         __syncthreads();
-        if (st + GDEPTH < NS) issue(D, st + GDEPTH);
+        /* unconditional (past the end it re-reads the last step into a slot
+         * no later step consumes): loads issued on every path keep the
+         * compiler's load counting exact, so the wait before a step covers
+         * only that step's loads and the later steps' stay in flight */
+        issue(D, min(st + GDEPTH, NS - 1u));
 #pragma unroll
         for (u32 i = 0; i < 4; ++i) {
 #pragma unroll
@@ -298,11 +313,13 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
         }
     };
     static_for<GDEPTH>([&](auto D) { issue(D, min((u32)decltype(D)::value, NS - 1u)); });
-    for (u32 st = 0; st < NS; st += GDEPTH) {
-        static_for<GDEPTH>([&](auto D) {
-            if (st + (u32)decltype(D)::value < NS) step(D, st + (u32)decltype(D)::value);
-        });
+    u32 st = 0;
+    for (; st + GDEPTH <= NS; st += GDEPTH) {
+        static_for<GDEPTH>([&](auto D) { step(D, st + (u32)decltype(D)::value); });
     }
+    static_for<GDEPTH>([&](auto D) {
+        if (st + (u32)decltype(D)::value < NS) step(D, st + (u32)decltype(D)::value);
+    });
 
     /* C layout of a 32x32 MFMA tile: lane l, element i -> row 8*(i/4) +
      * 4*(l/32) + i%4, column l%32 */
@@ -317,6 +334,8 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
             const size_t orw = (size_t)orow[r];
             if (EPI == GE_F32) {
                 ((float *)p.out)[orw * p.ldo + col] = acc[0][j][i];
+            } else if (EPI == GE_PART) {
+                ((float *)p.out)[((size_t)blockIdx.z * p.M + orw) * p.ldo + col] = acc[0][j][i];
             } else if (EPI == GE_SWIGLU) {
                 ((h16 *)p.out)[orw * p.ldo + col] = (h16)(silu_p(acc[0][j][i]) * acc[NMAT - 1][j][i]);
             } else if (EPI == GE_VISION) {
@@ -336,6 +355,28 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
                 ((h16 *)p.out)[orw * p.ldo + col] = (h16)v;
             }
         }
+    }
+}
+
+/* Split-K vision epilogue: out = f16(act(sum_z part[z] + bias)), the z
+ * partials summed in order (the result does not depend on block timing). */
+__global__ __launch_bounds__(PB) void k_vision_reduce(const float *__restrict__ part, u32 S, u32 M, u32 N,
+                                                      const h16 *__restrict__ bias, u32 act, u32 split,
+                                                      h16 *__restrict__ o0, h16 *__restrict__ o1,
+                                                      h16 *__restrict__ o2) {
+    const size_t i = (size_t)blockIdx.x * PB + threadIdx.x, MN = (size_t)M * N;
+    if (i >= MN) return;
+    float v = 0.0f;
+    for (u32 z = 0; z < S; ++z) v += part[z * MN + i];
+    const u32 row = (u32)(i / N), col = (u32)(i - (size_t)row * N);
+    v += (float)bias[col];
+    if (act == UOCR_VISION_ACT_QUICKGELU) v = quick_gelu(v);
+    else if (act == UOCR_VISION_ACT_GELU_ERF) v = gelu_erf_as(v);
+    if (split == 0u) {
+        o0[i] = (h16)v;
+    } else {
+        const u32 pj = col / split, lc = col - pj * split;
+        (pj == 0u ? o0 : (pj == 1u ? o1 : o2))[(size_t)row * split + lc] = (h16)v;
     }
 }
 
@@ -761,6 +802,7 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
     a.split = d->split;
     a.out1 = d->out1;
     a.out2 = d->out2;
+    a.kst = 0u;
     const dim3 grid(grouped ? d->max_tiles : (d->M + TM - 1u) / TM, (d->N + TN - 1u) / TN);
     const u32 qt = d->W[0].qtype;
     if (epi == UOCR_GEMM_VISION) {
@@ -768,7 +810,23 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
             (d->split != 0u && (d->N != 3u * d->split || d->out1 == nullptr || d->out2 == nullptr))) {
             return hipErrorInvalidValue;
         }
-        gemm_dispatch<GE_VISION, false>(st, qt, a, grid);
+        const u32 nt = d->K / TK;
+        if (d->ksplit > 1u && d->part != nullptr) {
+            /* split-K: blockIdx.z takes K steps [z*kst, (z+1)*kst) into an
+             * fp32 partial plane of part, then one ordered reduce applies
+             * bias, activation and split */
+            const u32 kst = (nt + d->ksplit - 1u) / d->ksplit, S = (nt + kst - 1u) / kst;
+            a.kst = kst;
+            a.out = d->part;
+            a.ldo = d->N;
+            gemm_dispatch<GE_PART, false>(st, qt, a, dim3(grid.x, grid.y, S));
+            const size_t mn = (size_t)d->M * d->N;
+            hipLaunchKernelGGL(k_vision_reduce, dim3((unsigned)((mn + PB - 1u) / PB)), dim3(PB), 0, st,
+                               (const float *)d->part, S, d->M, d->N, (const h16 *)d->bias, d->act, d->split,
+                               (h16 *)d->out, (h16 *)d->out1, (h16 *)d->out2);
+        } else {
+            gemm_dispatch<GE_VISION, false>(st, qt, a, grid);
+        }
     } else if (epi == UOCR_GEMM_F32) {
         if (grouped) gemm_dispatch<GE_F32, true>(st, qt, a, grid);
         else gemm_dispatch<GE_F32, false>(st, qt, a, grid);
