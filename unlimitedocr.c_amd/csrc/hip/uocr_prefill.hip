@@ -76,7 +76,9 @@ enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2, GE_VISION = 3, GE_PART = 4 };
 
 /* QuickGELU of the CLIP MLP: x * sigmoid(1.702 x) (dense.metal:63-66). */
 __device__ __forceinline__ float quick_gelu(float x) {
-    return x / (1.0f + expf(-1.702f * x));
+    /* hardware exp2 and reciprocal (about 1 ulp each in fp32; the result is
+     * rounded to fp16) instead of the full-precision expf and divide */
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.702f * 1.4426950408889634f * x));
 }
 
 /* GELU of the SAM MLP, 0.5 x (1 + erf(x / sqrt 2)), with erf from
@@ -85,9 +87,9 @@ __device__ __forceinline__ float quick_gelu(float x) {
 __device__ __forceinline__ float gelu_erf_as(float x) {
     const float z = x * 0.70710678118654752f;
     const float az = fabsf(z);
-    const float t = 1.0f / (1.0f + 0.3275911f * az);
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * az);
     const float poly = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) * t;
-    const float e = 1.0f - poly * expf(-az * az);
+    const float e = 1.0f - poly * __builtin_amdgcn_exp2f(-1.4426950408889634f * az * az);
     return 0.5f * x * (1.0f + (z < 0.0f ? -e : e));
 }
 
@@ -322,16 +324,32 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     });
 
     /* C layout of a 32x32 MFMA tile: lane l, element i -> row 8*(i/4) +
-     * 4*(l/32) + i%4, column l%32 */
+     * 4*(l/32) + i%4, column l%32.  Everything that depends only on the
+     * column (output pointer, split routing, bias) is resolved once per lane;
+     * rows of a plain GEMM are s0 + r (the row list is only read when
+     * grouped). */
     const u32 col = n0 + 32u * wave + (lane & 31u);
     if (col >= p.N) return;
+    auto out_row = [&](u32 r) -> size_t { return GROUPED ? (size_t)orow[r] : (size_t)(s0 + r); };
+    h16 *vdst = (h16 *)p.out + col;
+    size_t vld = p.ldo;
+    float bcol = 0.0f;
+    if (EPI == GE_VISION) {
+        bcol = (float)p.bias[col];
+        if (p.split != 0u) {
+            const u32 pj = col / p.split;
+            vdst = (h16 *)(pj == 0u ? p.out : (pj == 1u ? p.out1 : p.out2)) + (col - pj * p.split);
+            vld = p.split;
+        }
+    }
+    const u32 act = p.act;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const u32 r = 32u * j + 8u * (i / 4) + 4u * hf + (i % 4);
             if (r >= rows) continue;
-            const size_t orw = (size_t)orow[r];
+            const size_t orw = out_row(r);
             if (EPI == GE_F32) {
                 ((float *)p.out)[orw * p.ldo + col] = acc[0][j][i];
             } else if (EPI == GE_PART) {
@@ -339,16 +357,10 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
             } else if (EPI == GE_SWIGLU) {
                 ((h16 *)p.out)[orw * p.ldo + col] = (h16)(silu_p(acc[0][j][i]) * acc[NMAT - 1][j][i]);
             } else if (EPI == GE_VISION) {
-                float v = acc[0][j][i] + (float)p.bias[col];
-                if (p.act == UOCR_VISION_ACT_QUICKGELU) v = quick_gelu(v);
-                else if (p.act == UOCR_VISION_ACT_GELU_ERF) v = gelu_erf_as(v);
-                if (p.split == 0u) {
-                    ((h16 *)p.out)[orw * p.ldo + col] = (h16)v;
-                } else {
-                    const u32 pj = col / p.split, lc = col - pj * p.split;
-                    h16 *dst = (h16 *)(pj == 0u ? p.out : (pj == 1u ? p.out1 : p.out2));
-                    dst[orw * p.split + lc] = (h16)v;
-                }
+                float v = acc[0][j][i] + bcol;
+                if (act == UOCR_VISION_ACT_QUICKGELU) v = quick_gelu(v);
+                else if (act == UOCR_VISION_ACT_GELU_ERF) v = gelu_erf_as(v);
+                vdst[orw * vld] = (h16)v;
             } else {
                 float v = acc[0][j][i];
                 if (p.res != nullptr) v += (float)p.res[orw * p.ldr + col];
