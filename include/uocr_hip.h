@@ -192,8 +192,8 @@ UOCR_API int uocr_op_gemm(uint32_t qtype, const void *w, const void *s, uint32_t
  * 161-221) and uocr_vision_gemm_q4_0_to_f16 (kernels/gemm_q4.metal:63-131),
  * and the fp16 path MPS matmul + bias/activation (uocr_metal.m:17232-17250,
  * kernels/dense.metal:68-79, kernels/sam.metal:93-104), which is fused here
- * (one fp16 rounding instead of two).  Grids of fewer than 256 output tiles
- * split K over up to 8 blocks per tile through an fp32 partials buffer that
+ * (one fp16 rounding instead of two).  GEMMs with k >= 2048 on grids of
+ * fewer than 128 output tiles split K over up to 8 blocks per tile through an fp32 partials buffer that
  * the library allocates on first need (outside graph capture; under capture
  * without room the unsplit kernel runs) and keeps: calls must not overlap.
  * Errors: UOCR_ERROR_INVALID_ARGUMENT for

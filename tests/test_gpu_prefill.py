@@ -140,15 +140,15 @@ def test_batched_and_token_prefill_agree(gpu):
 # (4096 tokens, 768 wide: qkv 2304 split 768, lin1 3072 + GELU, lin2), the
 # CLIP-L view (257 tokens, 1024 wide: qkv split 1024, fc1 4096 + QuickGELU,
 # fc2), the projector (2048 -> 1280), the Q4 and fp16 kernels, and ragged
-# tiles (m not a multiple of 64, n not a multiple of 128).  Grids of fewer
-# than 256 tiles split K (the CLIP shapes; 21 K steps in 4 splits of 6, 6, 6
-# and 3 in the 1344-wide case).
+# tiles (m not a multiple of 64, n not a multiple of 128).  Long-K GEMMs on
+# grids of fewer than 128 tiles split K (CLIP fc2; 37 K steps in 4 splits of
+# 10, 10, 10 and 7 in the 2368-wide case).
 VISION_CASES = [
     (3, 4096, 768, 2304, 0, 768), (3, 4096, 768, 3072, 2, 0), (3, 4096, 3072, 768, 0, 0),
     (3, 257, 1024, 3072, 0, 1024), (3, 257, 1024, 4096, 1, 0), (3, 257, 4096, 1024, 0, 0),
     (3, 256, 2048, 1280, 0, 0), (4, 257, 1024, 4096, 1, 0), (1, 257, 1024, 4096, 1, 0),
     (1, 4096, 768, 3072, 2, 0), (4, 4096, 768, 2304, 0, 768), (3, 1, 64, 96, 2, 0), (1, 65, 128, 40, 1, 0),
-    (4, 100, 192, 96, 2, 32), (3, 100, 1344, 256, 2, 0),
+    (4, 100, 192, 96, 2, 32), (3, 100, 2368, 256, 2, 0),
 ]
 
 

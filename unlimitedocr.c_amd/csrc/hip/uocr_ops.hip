@@ -288,14 +288,17 @@ extern "C" int uocr_op_gemm(uint32_t qtype, const void *w, const void *s, uint32
 
 /* Split-K partials of the vision linear: grown on demand, kept until the
  * process ends (one buffer per process, so concurrent calls are not
- * supported).  Grids under one block per CU split K (at least 4 K steps per
- * split, at most 8 splits) so that the tile grid fills the chip. */
+ * supported).  Only long-K GEMMs on grids under half a block per CU split K
+ * (at least 4 K steps per split, at most 8 splits): the partials round trip
+ * and the reduce launch cost more than the unsplit kernel elsewhere (257 x
+ * 4096 -> 1024: 56 -> 20 us split; 640 x 1024 -> 3072: 28 us split against
+ * 14-20 us unsplit). */
 static float *g_vision_part = nullptr;
 static size_t g_vision_part_bytes = 0;
 
 static uint32_t vision_ksplit(uint32_t m, uint32_t n, uint32_t k) {
     const uint32_t blocks = ((m + 63u) / 64u) * ((n + 127u) / 128u), steps = k / 64u;
-    if (blocks >= 256u) return 1u;
+    if (blocks >= 128u || steps < 32u) return 1u;
     uint32_t s = 1u;
     while (s < 8u && blocks * s < 512u && steps / (2u * s) >= 4u) s *= 2u;
     return s;

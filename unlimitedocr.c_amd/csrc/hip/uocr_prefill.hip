@@ -376,19 +376,36 @@ __global__ __launch_bounds__(PB) void k_vision_reduce(const float *__restrict__ 
                                                       const h16 *__restrict__ bias, u32 act, u32 split,
                                                       h16 *__restrict__ o0, h16 *__restrict__ o1,
                                                       h16 *__restrict__ o2) {
-    const size_t i = (size_t)blockIdx.x * PB + threadIdx.x, MN = (size_t)M * N;
+    /* four consecutive columns per thread (N and split are multiples of 4,
+     * checked by the launcher), so every load is 16 bytes */
+    const size_t i = 4u * ((size_t)blockIdx.x * PB + threadIdx.x), MN = (size_t)M * N;
     if (i >= MN) return;
-    float v = 0.0f;
-    for (u32 z = 0; z < S; ++z) v += part[z * MN + i];
+    float4 v = *(const float4 *)(part + i);
+    for (u32 z = 1; z < S; ++z) {
+        const float4 w = *(const float4 *)(part + z * MN + i);
+        v.x += w.x;
+        v.y += w.y;
+        v.z += w.z;
+        v.w += w.w;
+    }
     const u32 row = (u32)(i / N), col = (u32)(i - (size_t)row * N);
-    v += (float)bias[col];
-    if (act == UOCR_VISION_ACT_QUICKGELU) v = quick_gelu(v);
-    else if (act == UOCR_VISION_ACT_GELU_ERF) v = gelu_erf_as(v);
+    float r[4] = {v.x, v.y, v.z, v.w};
+    union {
+        h16 h[4];
+        uint2 u;
+    } o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        float x = r[c] + (float)bias[col + c];
+        if (act == UOCR_VISION_ACT_QUICKGELU) x = quick_gelu(x);
+        else if (act == UOCR_VISION_ACT_GELU_ERF) x = gelu_erf_as(x);
+        o.h[c] = (h16)x;
+    }
     if (split == 0u) {
-        o0[i] = (h16)v;
+        *(uint2 *)(o0 + i) = o.u;
     } else {
         const u32 pj = col / split, lc = col - pj * split;
-        (pj == 0u ? o0 : (pj == 1u ? o1 : o2))[(size_t)row * split + lc] = (h16)v;
+        *(uint2 *)((pj == 0u ? o0 : (pj == 1u ? o1 : o2)) + (size_t)row * split + lc) = o.u;
     }
 }
 
@@ -823,7 +840,7 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
             return hipErrorInvalidValue;
         }
         const u32 nt = d->K / TK;
-        if (d->ksplit > 1u && d->part != nullptr) {
+        if (d->ksplit > 1u && d->part != nullptr && d->N % 4u == 0u && d->split % 4u == 0u) {
             /* split-K: blockIdx.z takes K steps [z*kst, (z+1)*kst) into an
              * fp32 partial plane of part, then one ordered reduce applies
              * bias, activation and split */
@@ -833,7 +850,7 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
             a.ldo = d->N;
             gemm_dispatch<GE_PART, false>(st, qt, a, dim3(grid.x, grid.y, S));
             const size_t mn = (size_t)d->M * d->N;
-            hipLaunchKernelGGL(k_vision_reduce, dim3((unsigned)((mn + PB - 1u) / PB)), dim3(PB), 0, st,
+            hipLaunchKernelGGL(k_vision_reduce, dim3((unsigned)((mn / 4u + PB - 1u) / PB)), dim3(PB), 0, st,
                                (const float *)d->part, S, d->M, d->N, (const h16 *)d->bias, d->act, d->split,
                                (h16 *)d->out, (h16 *)d->out1, (h16 *)d->out2);
         } else {
