@@ -461,12 +461,23 @@ def cpu_baseline(log, budget_s: float = 12.0) -> dict:
         n += 1
     dt = time.perf_counter() - t0
     cores = int(L.orc_get_threads())
+    # the same steps on one thread (bounded sample)
+    L.orc_set_threads(1)
+    n1, t1 = 0, time.perf_counter()
+    while n1 < 2 or time.perf_counter() - t1 < budget_s / 3:
+        L.orc_select(ct.c_void_p(orc.s), h.ctypes.data, ct.byref(tok), ct.byref(s1), ct.byref(s2))
+        L.orc_forward_token(ct.c_void_p(orc.s), h.ctypes.data, prompt_len + n + n1, None)
+        n1 += 1
+    dt1 = time.perf_counter() - t1
+    L.orc_set_threads(cores)
     orc.close()
     model.close()
-    log(f"cpu baseline: {n} tokens in {dt:.1f}s on {cores} threads")
+    log(f"cpu baseline: {n} tokens in {dt:.1f}s on {cores} threads; {n1} tokens in {dt1:.1f}s on 1 thread")
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "single_thread_value": round(n1 / dt1, 3),
             "sample": f"{n} decode steps (LM-head selection + 12 layers) of the mixed-Q4 model at context "
-                      f"{prompt_len}-{prompt_len + n}, C oracle with OpenMP over output rows, {dt:.1f} s"}
+                      f"{prompt_len}-{prompt_len + n}, C oracle with OpenMP over output rows, {dt:.1f} s; "
+                      f"then {n1} further steps on 1 thread, {dt1:.1f} s"}
 
 
 def main() -> None:
