@@ -118,7 +118,7 @@ __device__ __forceinline__ u32 b_koff(u32 i, u32 h) {
  * register ring stays in registers. */
 template <int QT>
 __device__ __forceinline__ void b_load(u32 (&w)[BPiece<QT>::NW], u32 &sc, const uint8_t *W, const h16 *S, u32 K,
-                                       u32 n, u32 g, u32 h) {
+                                       u32 n, u32 g, u32 h, bool with_scale = true) {
     const uint4 *src = QT == 4 ? (const uint4 *)(W + (size_t)n * (K / 2u) + g * 32u + 16u * h)
                                : (QT == 3 ? (const uint4 *)(W + (size_t)n * K + g * 64u + 32u * h)
                                           : (const uint4 *)((const h16 *)W + (size_t)n * K + g * 64u + 32u * h));
@@ -130,7 +130,7 @@ __device__ __forceinline__ void b_load(u32 (&w)[BPiece<QT>::NW], u32 &sc, const 
         w[4 * v + 2] = x.z;
         w[4 * v + 3] = x.w;
     }
-    if (QT != 1) sc = ((const unsigned short *)S)[(size_t)n * (K / 64u) + g];
+    if (QT != 1 && with_scale) sc = ((const unsigned short *)S)[(size_t)n * (K / 64u) + g];
 }
 
 /* The four B operands (8 fp16 each) of a loaded piece: fp16(q * scale), the
@@ -192,7 +192,14 @@ struct GemmArgs {
     u32 split;           /* GE_VISION: 0, or the width of each of out/out1/out2 */
     void *out1, *out2;
     u32 kst;             /* split-K: K steps per blockIdx.z (0: all of K in one block) */
+    u32 sc_lds;          /* the block's scale rows are preloaded into dynamic LDS */
 };
+
+/* Scale rows in LDS: a block's 128 weight rows x K/64 groups are one
+ * contiguous region of the scale tensor, loaded once with wide loads instead
+ * of one 2-byte load per row per K step (each of which touches a separate
+ * cache line).  Used while NMAT x K/64 <= SC_LDS_STEPS (28 KB). */
+#define SC_LDS_STEPS 112u
 
 /* C[m][n] = sum_k A[m][k] W[n][k] over one 64 x 128 tile per block.  Wave
  * w owns output columns 32w..32w+31 (its weight rows, dequantised straight
@@ -259,6 +266,10 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     const u32 NS = p.kst != 0u ? min(p.kst, NT - kb0) : NT;
     u32 ka[GDEPTH][2][4]; /* words, not uint4: no struct copies, so they stay in registers */
     u32 kb[GDEPTH][NMAT][BPiece<QT>::NW], ks[GDEPTH][NMAT];
+    extern __shared__ __attribute__((aligned(16))) unsigned short ssc[];
+    const bool scl = QT != 1 && p.sc_lds != 0u;
+    const u32 lrow0 = n0 - nbase, nvalid = min((u32)TN, nmax - lrow0);
+    const u32 lrow = nrow - lrow0; /* this lane's row within the block's scale rows */
     /* this thread's two activation rows, resolved once */
     const h16 *arp[2];
 #pragma unroll
@@ -277,7 +288,7 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
             ka[d][q][3] = v.w;
         }
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) b_load<QT>(kb[d][m], ks[d][m], wp[m], sp[m], Kd, nrow, kb0 + st, hf);
+        for (int m = 0; m < NMAT; ++m) b_load<QT>(kb[d][m], ks[d][m], wp[m], sp[m], Kd, nrow, kb0 + st, hf, !scl);
     };
     auto step = [&](auto D, u32 st) {
         constexpr int d = decltype(D)::value;
@@ -291,6 +302,10 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
             *(uint4 *)(ab + r * LDA + 8u * c8) = make_uint4(ka[d][q][0], ka[d][q][1], ka[d][q][2], ka[d][q][3]);
         }
         h16x8 bop[NMAT][4];
+        if (scl) {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) ks[d][m] = ssc[(m * TN + lrow) * NT + kb0 + st];
+        }
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) b_dequant<QT>(kb[d][m], ks[d][m], bop[m]);
         /* the other buffer's readers (step st - 1) all passed this barrier
@@ -315,6 +330,22 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
         }
     };
     static_for<GDEPTH>([&](auto D) { issue(D, min((u32)decltype(D)::value, NS - 1u)); });
+    if (scl) {
+        /* after the first steps' loads are in flight; rows past nmax are not
+         * loaded (their lanes read the last valid row, nrow is clamped) */
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            const unsigned short *src = (const unsigned short *)sp[m] + (size_t)lrow0 * NT;
+            unsigned short *dst = ssc + m * TN * NT;
+            const u32 cnt = nvalid * NT;
+            if ((((uintptr_t)src) & 15u) == 0u && cnt % 8u == 0u) {
+                for (u32 i = t; i < cnt / 8u; i += PB) ((uint4 *)dst)[i] = ((const uint4 *)src)[i];
+            } else {
+                for (u32 i = t; i < cnt; i += PB) dst[i] = src[i];
+            }
+        }
+        __syncthreads();
+    }
     u32 st = 0;
     for (; st + GDEPTH <= NS; st += GDEPTH) {
         static_for<GDEPTH>([&](auto D) { step(D, st + (u32)decltype(D)::value); });
@@ -783,11 +814,14 @@ static bool pmat_ok(uocr_qmat m) {
 }
 
 template <int EPI, bool GROUPED>
-static void gemm_dispatch(hipStream_t st, u32 qt, const GemmArgs &a, dim3 grid) {
+static void gemm_dispatch(hipStream_t st, u32 qt, GemmArgs a, dim3 grid) {
+    const u32 nm = EPI == GE_SWIGLU ? 2u : 1u, nt = a.K / TK;
+    a.sc_lds = qt != UOCR_QT_F16 && nm * nt <= SC_LDS_STEPS ? 1u : 0u;
+    const size_t shm = a.sc_lds ? (size_t)nm * TN * nt * sizeof(unsigned short) : 0;
     switch (qt) {
         case UOCR_QT_F16: hipLaunchKernelGGL((k_gemm<1, EPI, GROUPED>), grid, dim3(PB), 0, st, a); break;
-        case UOCR_QT_Q8: hipLaunchKernelGGL((k_gemm<3, EPI, GROUPED>), grid, dim3(PB), 0, st, a); break;
-        default: hipLaunchKernelGGL((k_gemm<4, EPI, GROUPED>), grid, dim3(PB), 0, st, a); break;
+        case UOCR_QT_Q8: hipLaunchKernelGGL((k_gemm<3, EPI, GROUPED>), grid, dim3(PB), shm, st, a); break;
+        default: hipLaunchKernelGGL((k_gemm<4, EPI, GROUPED>), grid, dim3(PB), shm, st, a); break;
     }
 }
 
