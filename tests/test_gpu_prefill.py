@@ -50,7 +50,7 @@ def test_gemm_rejects_bad_shapes(gpu):
         uocr.op_gemm(2, buf, buf, 4, 128, 128, buf, None, buf)  # unsupported qtype
 
 
-@pytest.mark.parametrize("P", [1, 63, 64, 150])
+@pytest.mark.parametrize("P", [1, 63, 64, 150, 600, 932])
 def test_prefill_attention_matches_oracle(gpu, oracle, P):
     """Causal attention: query i over slots 0..i equals the oracle's decode
     attention with prompt length i+1."""

@@ -85,6 +85,7 @@ struct uocr_hip_ctx {
     uint32_t *route_ids;
     /* MFMA prefill scratch, sized for prompt_cap rows */
     uint16_t *p_xn, *p_qkv, *p_q, *p_ctx, *p_a, *p_mid, *p_smid, *p_sout, *p_rmid;
+    float *p_fa_ws; /* prefill attention key-split partials */
     float *p_logits, *p_wts, *p_y;
     int32_t *p_ids, *p_offsets, *p_tile_e, *p_tile_s0, *p_tile_s1, *p_ntiles, *p_list_tok,
         *p_list_pair;
@@ -403,6 +404,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_poff = p.take(64u * 4u);
     const uint64_t o_pte = p.take(max_tiles * 4u), o_pts0 = p.take(max_tiles * 4u), o_pts1 = p.take(max_tiles * 4u);
     const uint64_t o_pnt = p.take(4u), o_plt = p.take(PK * 4u), o_plp = p.take(PK * 4u);
+    const uint64_t o_pfa = p.take(uocr_flash_attn_ws_bytes());
     const uint64_t total = p.off;
     HIPCHK(hipMalloc((void **)&ctx->rarena, total), "runtime arena allocation");
     /* cleared on the engine's stream (non-blocking, so not ordered against a
@@ -450,6 +452,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->p_ntiles = (int32_t *)(b + o_pnt);
     ctx->p_list_tok = (int32_t *)(b + o_plt);
     ctx->p_list_pair = (int32_t *)(b + o_plp);
+    ctx->p_fa_ws = (float *)(b + o_pfa);
     ctx->p_max_tiles = max_tiles;
     ctx->rarena_bytes = total;
     ctx->kv_bytes = 2u * kv_one;
@@ -583,7 +586,7 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         d.nseg = H_SIZE;
         ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
         ENQ(uocr_launch_rope_scatter(s, c->p_qkv, c->invf, P, c->p_q, kc, vc, c->cache_cap));
-        ENQ(uocr_launch_flash_attn(s, c->p_q, kc, vc, c->cache_cap, P, c->p_ctx));
+        ENQ(uocr_launch_flash_attn(s, c->p_q, kc, vc, c->cache_cap, P, c->p_ctx, c->p_fa_ws));
         d = gdesc(c->p_ctx, H_SIZE, P, H_SIZE, H_SIZE, c->p_a, H_SIZE);
         d.W[0] = L.o;
         d.res = H;

@@ -230,7 +230,10 @@ hipError_t uocr_launch_rope_scatter(hipStream_t st, const uint16_t *qkv, const f
                                     uint16_t *qout, uint16_t *kcache, uint16_t *vcache, uint32_t cap);
 /* Causal attention of P prompt queries over cache slots 0..P-1 -> ctx [P][1280]. */
 hipError_t uocr_launch_flash_attn(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
-                                  uint32_t cap, uint32_t P, uint16_t *ctx);
+                                  uint32_t cap, uint32_t P, uint16_t *ctx, float *ws);
+/* Workspace of uocr_launch_flash_attn's key split (partials of up to 512
+ * blocks); with ws NULL every query tile is one block (no split). */
+size_t uocr_flash_attn_ws_bytes(void);
 /* Per-token top-6 over logits [P][64] -> ids/wts [P][6]; expert buckets:
  * offsets (64), grouped-GEMM tile table (up to P*6/64 + 64 entries) and the
  * (token, pair) slot lists [P*6], built in LDS by one block (no global

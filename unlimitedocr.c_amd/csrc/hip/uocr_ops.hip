@@ -358,8 +358,19 @@ extern "C" int uocr_op_prefill_attention(const void *q, const void *k_cache, con
         return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid prefill_attention arguments");
     }
     STREAM_OR_RETURN(st);
+    /* key-split partials: allocated on first need outside graph capture and
+     * kept (calls must not overlap); without them the unsplit kernel runs */
+    static float *fa_ws = nullptr;
+    if (fa_ws == nullptr) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+            void *p = nullptr;
+            if (hipMalloc(&p, uocr_flash_attn_ws_bytes()) == hipSuccess) fa_ws = (float *)p;
+        }
+    }
     return hip_status(uocr_launch_flash_attn(st, (const uint16_t *)q, (const uint16_t *)k_cache,
-                                             (const uint16_t *)v_cache, cache_capacity, prompt_length, (uint16_t *)ctx),
+                                             (const uint16_t *)v_cache, cache_capacity, prompt_length, (uint16_t *)ctx,
+                                             fa_ws),
                       "prefill_attention");
 }
 

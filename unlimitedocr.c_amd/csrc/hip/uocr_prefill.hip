@@ -516,9 +516,29 @@ __global__ __launch_bounds__(PB) void k_rope_scatter(const h16 *__restrict__ qkv
 /* Block (qt, h): queries q0..q0+63 of head h attend to slots 0..q (causal),
  * fp32 online softmax scaled by 1/sqrt(128), output fp16 into ctx [P][1280]
  * (attention_decode.metal arithmetic per query). */
+/* KV split of the causal prefill attention.  Query tile qt (64 queries) sees
+ * qt + 1 key tiles; with chunks of CH key tiles it is nsplit(qt) = ceil((qt +
+ * 1) / CH) blocks.  Blocks enumerate (qt, head, split) with the split
+ * fastest, so the splits of one (qt, head) are consecutive block indices.
+ * Each split of a tile with more than one writes its unnormalised O and its
+ * row max / sum to its own partial slot; k_flash_merge combines them. */
+#define FA_PART_FLOATS (AQ * UOCR_K_HEAD_DIM + 2u * AQ)
+#define FA_MAX_SPLITS 16u /* splits of one query tile (the merge's weight table) */
+
+__device__ __forceinline__ u32 fa_nsplit(u32 qt, u32 ch) {
+    return (qt + ch) / ch;
+}
+
+/* first block index of query tile qt (all heads) */
+__device__ __forceinline__ u32 fa_tile_base(u32 qt, u32 ch) {
+    u32 b = 0;
+    for (u32 q = 0; q < qt; ++q) b += UOCR_K_HEADS * fa_nsplit(q, ch);
+    return b;
+}
+
 __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, const h16 *__restrict__ kc,
                                                    const h16 *__restrict__ vc, u32 cap, u32 P,
-                                                   h16 *__restrict__ ctx) {
+                                                   h16 *__restrict__ ctx, u32 ch, float *__restrict__ part) {
     __shared__ __attribute__((aligned(16))) h16 qs[AQ * LDQ];
     __shared__ __attribute__((aligned(16))) h16 ks[AK * LDQ];
     __shared__ __attribute__((aligned(16))) h16 vt[UOCR_K_HEAD_DIM * LDV];
@@ -526,7 +546,20 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
     __shared__ __attribute__((aligned(16))) h16 ps[AQ * LDV];
     __shared__ float rowm[AQ], rowl[AQ], rowc[AQ];
     const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    const u32 h = blockIdx.y, q0 = blockIdx.x * AQ;
+    /* which (query tile, head, key chunk) this block computes */
+    u32 qt = blockIdx.x, h = blockIdx.y, sp = 0, ns = 1;
+    if (ch != 0u) {
+        u32 b = blockIdx.x;
+        qt = 0;
+        while (b >= UOCR_K_HEADS * fa_nsplit(qt, ch)) {
+            b -= UOCR_K_HEADS * fa_nsplit(qt, ch);
+            ++qt;
+        }
+        ns = fa_nsplit(qt, ch);
+        h = b / ns;
+        sp = b - h * ns;
+    }
+    const u32 q0 = qt * AQ;
     const h16 *kh = kc + (size_t)h * cap * 128u, *vh = vc + (size_t)h * cap * 128u;
     const float scale = 0.08838834764831845f;
 
@@ -548,6 +581,9 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
         for (int i = 0; i < 16; ++i) o[j][i] = 0.0f;
     const u32 wm = wave & 1u, wn = wave >> 1;
     const u32 qlast = min(q0 + AQ, P) - 1u;
+    /* this block's keys: tiles [sp * ch, (sp + 1) * ch) of the causal range */
+    const u32 kbeg = ch != 0u ? sp * ch * AK : 0u;
+    const u32 klast = ch != 0u ? min(qlast, (sp + 1u) * ch * AK - 1u) : qlast;
     /* next K/V tile in registers (words, so they stay in registers) */
     u32 kr_[4][4], va_[2][4], vb_[2][4];
     auto load_kv = [&](u32 k0n) {
@@ -575,8 +611,8 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
             vb_[q][3] = b.w;
         }
     };
-    load_kv(0u);
-    for (u32 k0 = 0; k0 <= qlast; k0 += AK) {
+    load_kv(kbeg);
+    for (u32 k0 = kbeg; k0 <= klast; k0 += AK) {
         __syncthreads();
         /* K tile (row-major) and V tile transposed to [dim][key], from the
          * registers loaded one tile ahead.  The transpose goes by key pairs:
@@ -600,7 +636,7 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
             }
         }
         __syncthreads();
-        if (k0 + AK <= qlast) load_kv(k0 + AK);
+        if (k0 + AK <= klast) load_kv(k0 + AK);
         /* S = Q K^T: wave (wm, wn) computes rows 32wm.., keys 32wn.. */
         {
             f32x16 s;
@@ -672,6 +708,23 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
         }
     }
     __syncthreads();
+    if (ns > 1u) {
+        /* partial of a split tile: unnormalised O, row max and row sum */
+        float *po = part + (size_t)blockIdx.x * FA_PART_FLOATS;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const u32 r = 32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4);
+                po[r * UOCR_K_HEAD_DIM + 64u * wn + 32u * j + (lane & 31u)] = o[j][i];
+            }
+        }
+        if (t < AQ) {
+            po[AQ * UOCR_K_HEAD_DIM + t] = rowm[t];
+            po[AQ * UOCR_K_HEAD_DIM + AQ + t] = rowl[t];
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -679,6 +732,69 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
             const u32 r = 32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4);
             const u32 d = 64u * wn + 32u * j + (lane & 31u);
             if (q0 + r < P) ctx[(size_t)(q0 + r) * UOCR_K_HIDDEN + h * 128u + d] = (h16)(o[j][i] / rowl[r]);
+        }
+    }
+}
+
+/* Merge of the split tiles: block (x, h, z) takes rows 16z..16z+15 of query
+ * tile ch + x (every tile from ch on has at least two splits): ctx = sum_s
+ * O_s e^(m_s - M) / sum_s l_s e^(m_s - M), M = max_s m_s (split 0 holds key
+ * 0, so every row has L > 0).  Each thread owns two float4 of the 16 x 128
+ * block and issues the splits' loads four at a time. */
+__global__ __launch_bounds__(PB) void k_flash_merge(const float *__restrict__ part, u32 P, u32 ch,
+                                                    h16 *__restrict__ ctx) {
+    const u32 qt = ch + blockIdx.x, h = blockIdx.y, r0 = 16u * blockIdx.z, ns = fa_nsplit(qt, ch);
+    const float *pb = part + (size_t)(fa_tile_base(qt, ch) + h * ns) * FA_PART_FLOATS;
+    __shared__ float wgt[FA_MAX_SPLITS][16], linv[16];
+    if (threadIdx.x < 16u) {
+        const u32 r = r0 + threadIdx.x;
+        float M = -INFINITY;
+        for (u32 s = 0; s < ns; ++s) M = fmaxf(M, pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + r]);
+        float L = 0.0f;
+        for (u32 s = 0; s < ns; ++s) {
+            const float m = pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + r];
+            const float w = m == -INFINITY ? 0.0f : expf(m - M);
+            wgt[s][threadIdx.x] = w;
+            L += w * pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + AQ + r];
+        }
+        linv[threadIdx.x] = 1.0f / L;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const u32 e4 = threadIdx.x + q * PB;          /* float4 index within the 16 x 128 block */
+        const u32 rl = e4 / (UOCR_K_HEAD_DIM / 4u), d = 4u * (e4 % (UOCR_K_HEAD_DIM / 4u));
+        const size_t off = (size_t)(r0 + rl) * UOCR_K_HEAD_DIM + d;
+        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (u32 s0 = 0; s0 < ns; s0 += 4u) {
+            float4 v[4];
+#pragma unroll
+            for (u32 u = 0; u < 4u; ++u) {
+                if (s0 + u < ns) v[u] = *(const float4 *)(pb + (s0 + u) * FA_PART_FLOATS + off);
+            }
+#pragma unroll
+            for (u32 u = 0; u < 4u; ++u) {
+                if (s0 + u < ns) {
+                    const float w = wgt[s0 + u][rl];
+                    o.x += w * v[u].x;
+                    o.y += w * v[u].y;
+                    o.z += w * v[u].z;
+                    o.w += w * v[u].w;
+                }
+            }
+        }
+        const u32 row = qt * AQ + r0 + rl;
+        if (row < P) {
+            const float li = linv[rl];
+            union {
+                h16 hh[4];
+                uint2 u;
+            } pk;
+            pk.hh[0] = (h16)(o.x * li);
+            pk.hh[1] = (h16)(o.y * li);
+            pk.hh[2] = (h16)(o.z * li);
+            pk.hh[3] = (h16)(o.w * li);
+            *(uint2 *)(ctx + (size_t)row * UOCR_K_HIDDEN + h * 128u + d) = pk.u;
         }
     }
 }
@@ -924,13 +1040,44 @@ extern "C" hipError_t uocr_launch_rope_scatter(hipStream_t st, const uint16_t *q
     return hipGetLastError();
 }
 
+/* Resident blocks of k_flash_attn on the chip (about 80 KB of LDS each: two
+ * per CU).  The key chunk is the smallest whose (tile, head, chunk) blocks
+ * all fit at once; the longest block then walks ch key tiles instead of all
+ * of the last query tile's.  0: one block per (tile, head), no split. */
+#define FA_SLOTS 512u
+
+static u32 fa_chunk(u32 P) {
+    const u32 nq = (P + AQ - 1u) / AQ;
+    for (u32 ch = 1; ch < nq; ++ch) {
+        u32 blocks = 0;
+        for (u32 q = 0; q < nq; ++q) blocks += UOCR_K_HEADS * ((q + ch) / ch);
+        if (blocks <= FA_SLOTS && (nq + ch - 1u) / ch <= FA_MAX_SPLITS) return ch;
+    }
+    return 0u;
+}
+
+extern "C" size_t uocr_flash_attn_ws_bytes(void) {
+    return (size_t)FA_SLOTS * FA_PART_FLOATS * sizeof(float);
+}
+
 extern "C" hipError_t uocr_launch_flash_attn(hipStream_t st, const uint16_t *q, const uint16_t *kcache,
-                                             const uint16_t *vcache, uint32_t cap, uint32_t P, uint16_t *ctx) {
+                                             const uint16_t *vcache, uint32_t cap, uint32_t P, uint16_t *ctx,
+                                             float *ws) {
     if (q == nullptr || kcache == nullptr || vcache == nullptr || ctx == nullptr || P == 0u || P > cap) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(k_flash_attn, dim3((P + AQ - 1u) / AQ, UOCR_K_HEADS), dim3(PB), 0, st, (const h16 *)q,
-                       (const h16 *)kcache, (const h16 *)vcache, cap, P, (h16 *)ctx);
+    const u32 nq = (P + AQ - 1u) / AQ, ch = ws != nullptr ? fa_chunk(P) : 0u;
+    if (ch == 0u) {
+        hipLaunchKernelGGL(k_flash_attn, dim3(nq, UOCR_K_HEADS), dim3(PB), 0, st, (const h16 *)q,
+                           (const h16 *)kcache, (const h16 *)vcache, cap, P, (h16 *)ctx, 0u, (float *)nullptr);
+        return hipGetLastError();
+    }
+    u32 blocks = 0;
+    for (u32 qi = 0; qi < nq; ++qi) blocks += UOCR_K_HEADS * ((qi + ch) / ch);
+    hipLaunchKernelGGL(k_flash_attn, dim3(blocks), dim3(PB), 0, st, (const h16 *)q, (const h16 *)kcache,
+                       (const h16 *)vcache, cap, P, (h16 *)ctx, ch, ws);
+    hipLaunchKernelGGL(k_flash_merge, dim3(nq - ch, UOCR_K_HEADS, AQ / 16u), dim3(PB), 0, st, (const float *)ws, P,
+                       ch, (h16 *)ctx);
     return hipGetLastError();
 }
 
