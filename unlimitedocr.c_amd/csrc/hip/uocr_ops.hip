@@ -287,7 +287,8 @@ extern "C" int uocr_op_gemm(uint32_t qtype, const void *w, const void *s, uint32
 }
 
 /* Split-K partials of the vision linear: grown on demand, kept until the
- * process ends (one buffer per process, so concurrent calls are not
+ * process ends (outgrown buffers too, since captured graphs may reference
+ * them; one current buffer per process, so concurrent calls are not
  * supported).  Only long-K GEMMs on grids under half a block per CU split K
  * (at least 4 K steps per split, at most 8 splits): the partials round trip
  * and the reduce launch cost more than the unsplit kernel elsewhere (257 x
@@ -336,8 +337,9 @@ extern "C" int uocr_op_vision_linear(uint32_t qtype, const void *w, const void *
             hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
             if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
                 void *p = nullptr;
-                if (hipStreamSynchronize(st) == hipSuccess && hipMalloc(&p, need) == hipSuccess) {
-                    if (g_vision_part != nullptr) (void)hipFree(g_vision_part);
+                /* a smaller buffer is kept, not freed: a graph captured
+                 * earlier may still replay into it */
+                if (hipMalloc(&p, need) == hipSuccess) {
                     g_vision_part = (float *)p;
                     g_vision_part_bytes = need;
                 }
