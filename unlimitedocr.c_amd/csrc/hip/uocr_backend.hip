@@ -82,10 +82,12 @@ struct uocr_hip_ctx {
     float *attn_part, *logits, *route_w;
     int64_t *racc; /* un-normalised router logits, fixed point (k_attn_out -> k_moe_gate_up) */
     int fold_select; /* the token is chosen in layer 0's QKV launch (not a finalize launch) */
+    int prefill_ksplit; /* small-grid prefill GEMMs split K */
     uint32_t *route_ids;
     /* MFMA prefill scratch, sized for prompt_cap rows */
     uint16_t *p_xn, *p_qkv, *p_q, *p_ctx, *p_a, *p_mid, *p_smid, *p_sout, *p_rmid;
     float *p_fa_ws; /* prefill attention key-split partials */
+    float *p_kpart; /* prefill GEMM split-K partials */
     float *p_logits, *p_wts, *p_y;
     int32_t *p_ids, *p_offsets, *p_tile_e, *p_tile_s0, *p_tile_s1, *p_ntiles, *p_list_tok,
         *p_list_pair;
@@ -299,6 +301,9 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
     /* UOCR_HIP_NO_SELECT_FOLD=1 chooses each token in a finalize launch after the LM head */
     const char *ns = getenv("UOCR_HIP_NO_SELECT_FOLD");
     ctx->fold_select = !(ns != nullptr && atoi(ns) != 0);
+    /* UOCR_HIP_NO_PREFILL_KSPLIT=1 runs every prefill GEMM unsplit */
+    const char *nk = getenv("UOCR_HIP_NO_PREFILL_KSPLIT");
+    ctx->prefill_ksplit = !(nk != nullptr && atoi(nk) != 0);
     /* size pass */
     uint64_t total = tensor_bytes(b->embed) + tensor_bytes(b->lm_head) + tensor_bytes(b->final_norm);
     for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
@@ -405,6 +410,9 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_pte = p.take(max_tiles * 4u), o_pts0 = p.take(max_tiles * 4u), o_pts1 = p.take(max_tiles * 4u);
     const uint64_t o_pnt = p.take(4u), o_plt = p.take(PK * 4u), o_plp = p.take(PK * 4u);
     const uint64_t o_pfa = p.take(uocr_flash_attn_ws_bytes());
+    /* split-K partials of the O projection and the dense down (2 splits x
+     * P x 1280, fp32) */
+    const uint64_t o_pkp = p.take(Pc * H_SIZE * 2u * 4u);
     const uint64_t total = p.off;
     HIPCHK(hipMalloc((void **)&ctx->rarena, total), "runtime arena allocation");
     /* cleared on the engine's stream (non-blocking, so not ordered against a
@@ -453,6 +461,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->p_list_tok = (int32_t *)(b + o_plt);
     ctx->p_list_pair = (int32_t *)(b + o_plp);
     ctx->p_fa_ws = (float *)(b + o_pfa);
+    ctx->p_kpart = (float *)(b + o_pkp);
     ctx->p_max_tiles = max_tiles;
     ctx->rarena_bytes = total;
     ctx->kv_bytes = 2u * kv_one;
@@ -548,6 +557,20 @@ static hipError_t enqueue_prefill_step(uocr_hip_ctx *c) {
     return e;
 }
 
+/* Plain prefill GEMM with split K where its grid is small (the partials
+ * buffer holds 2 x P x 1280 floats: at most 2 splits at N = 1280).  Used for
+ * the O projection and layer 0's dense down (K = 6848): measured at P = 932,
+ * O 26.3 -> 16 + 5 us (reduce), while the router logits (11.4 -> 6.6 + 4.9)
+ * and the shared down (23.6 -> 19 + 5.2) gain nothing, an extra eager launch
+ * costing about 5 us. */
+static void with_ksplit(uocr_gemm_desc &d, float *part) {
+    const uint32_t s = uocr_gemm_ksplit(d.M, d.N, d.K);
+    if (s > 1u && (uint64_t)s * d.N <= 2u * H_SIZE) {
+        d.ksplit = s;
+        d.part = part;
+    }
+}
+
 static uocr_gemm_desc gdesc(const uint16_t *A, uint32_t lda, uint32_t M, uint32_t N, uint32_t K, void *out,
                            uint32_t ldo) {
     uocr_gemm_desc d;
@@ -591,6 +614,7 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         d.W[0] = L.o;
         d.res = H;
         d.ldr = H_SIZE;
+        if (c->prefill_ksplit) with_ksplit(d, c->p_kpart);
         ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
         ENQ(uocr_launch_rows_rmsnorm(s, c->p_a, L.post_norm, P, c->p_xn));
         if (l == 0u) {
@@ -603,6 +627,7 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
             d.W[0] = L.down;
             d.res = c->p_a;
             d.ldr = H_SIZE;
+            if (c->prefill_ksplit) with_ksplit(d, c->p_kpart);
             ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
             continue;
         }

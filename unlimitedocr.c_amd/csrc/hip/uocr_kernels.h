@@ -215,14 +215,18 @@ typedef struct uocr_gemm_desc {
     const uint16_t *bias;
     uint32_t act, split;
     void *out1, *out2;
-    /* UOCR_GEMM_VISION only: ksplit > 1 splits K over that many blocks per
-     * tile, each writing fp32 partials into part ([ksplit][M][N] floats),
-     * reduced in order by a second kernel; ksplit <= 1 or part NULL: no split */
+    /* UOCR_GEMM_VISION, F16 and F32 (not grouped): ksplit > 1 splits K over
+     * that many blocks per tile, each writing fp32 partials into part
+     * ([ksplit][M][N] floats), reduced in order by a second kernel that
+     * applies the epilogue; ksplit <= 1 or part NULL: no split */
     uint32_t ksplit;
     float *part;
 } uocr_gemm_desc;
 
 hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d);
+/* K splits (1: none) for a plain GEMM of M x N x K whose tile grid is under
+ * one block per CU; UOCR_GEMM_F16 / F32 / VISION honour desc ksplit + part. */
+uint32_t uocr_gemm_ksplit(uint32_t M, uint32_t N, uint32_t K);
 /* y[t] = rmsnorm(x[t], w) for P rows of 1280. */
 hipError_t uocr_launch_rows_rmsnorm(hipStream_t st, const uint16_t *x, const uint16_t *w, uint32_t P, uint16_t *y);
 /* qkv [P][3840] -> RoPE'd q [P][1280]; RoPE'd k and v into cache slots 0..P-1. */

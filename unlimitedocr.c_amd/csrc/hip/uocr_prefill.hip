@@ -401,30 +401,53 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     }
 }
 
-/* Split-K vision epilogue: out = f16(act(sum_z part[z] + bias)), the z
- * partials summed in order (the result does not depend on block timing). */
-__global__ __launch_bounds__(PB) void k_vision_reduce(const float *__restrict__ part, u32 S, u32 M, u32 N,
-                                                      const h16 *__restrict__ bias, u32 act, u32 split,
-                                                      h16 *__restrict__ o0, h16 *__restrict__ o1,
-                                                      h16 *__restrict__ o2) {
-    /* four consecutive columns per thread (N and split are multiples of 4,
-     * checked by the launcher), so every load is 16 bytes */
+/* Split-K epilogue: the z partials summed in order (the result does not
+ * depend on block timing), then
+ *   RD_VISION: out = f16(act(sum + bias)), split into o0/o1/o2 when split;
+ *   RD_F16:    out = f16(sum (+ res)), row stride ldo (res: ldr);
+ *   RD_F32:    out = sum (fp32), row stride ldo. */
+enum { RD_VISION = 0, RD_F16 = 1, RD_F32 = 2 };
+__global__ __launch_bounds__(PB) void k_split_reduce(const float *__restrict__ part, u32 S, u32 M, u32 N, u32 mode,
+                                                     const h16 *__restrict__ bias, u32 act, u32 split,
+                                                     const h16 *__restrict__ res, u32 ldr, void *__restrict__ o0,
+                                                     h16 *__restrict__ o1, h16 *__restrict__ o2, u32 ldo) {
+    /* four consecutive columns per thread (N, split, ldo and ldr are
+     * multiples of 4, checked by the launcher), so every load is 16 bytes */
     const size_t i = 4u * ((size_t)blockIdx.x * PB + threadIdx.x), MN = (size_t)M * N;
     if (i >= MN) return;
-    float4 v = *(const float4 *)(part + i);
-    for (u32 z = 1; z < S; ++z) {
-        const float4 w = *(const float4 *)(part + z * MN + i);
-        v.x += w.x;
-        v.y += w.y;
-        v.z += w.z;
-        v.w += w.w;
+    /* all planes' loads issued before the (ordered) sum; S <= 8 */
+    float4 w[8];
+#pragma unroll
+    for (u32 z = 0; z < 8u; ++z) {
+        if (z < S) w[z] = *(const float4 *)(part + z * MN + i);
+    }
+    float4 v = w[0];
+#pragma unroll
+    for (u32 z = 1; z < 8u; ++z) {
+        if (z < S) {
+            v.x += w[z].x;
+            v.y += w[z].y;
+            v.z += w[z].z;
+            v.w += w[z].w;
+        }
     }
     const u32 row = (u32)(i / N), col = (u32)(i - (size_t)row * N);
+    if (mode == RD_F32) {
+        *(float4 *)((float *)o0 + (size_t)row * ldo + col) = v;
+        return;
+    }
     float r[4] = {v.x, v.y, v.z, v.w};
     union {
         h16 h[4];
         uint2 u;
-    } o;
+    } o, rr;
+    if (mode == RD_F16) {
+        if (res != nullptr) rr.u = *(const uint2 *)(res + (size_t)row * ldr + col);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o.h[c] = (h16)(res != nullptr ? r[c] + (float)rr.h[c] : r[c]);
+        *(uint2 *)((h16 *)o0 + (size_t)row * ldo + col) = o.u;
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         float x = r[c] + (float)bias[col + c];
@@ -433,10 +456,10 @@ __global__ __launch_bounds__(PB) void k_vision_reduce(const float *__restrict__ 
         o.h[c] = (h16)x;
     }
     if (split == 0u) {
-        *(uint2 *)(o0 + i) = o.u;
+        *(uint2 *)((h16 *)o0 + (size_t)row * ldo + col) = o.u;
     } else {
         const u32 pj = col / split, lc = col - pj * split;
-        *(uint2 *)((pj == 0u ? o0 : (pj == 1u ? o1 : o2)) + (size_t)row * split + lc) = o.u;
+        *(uint2 *)((pj == 0u ? (h16 *)o0 : (pj == 1u ? o1 : o2)) + (size_t)row * split + lc) = o.u;
     }
 }
 
@@ -941,6 +964,17 @@ static void gemm_dispatch(hipStream_t st, u32 qt, GemmArgs a, dim3 grid) {
     }
 }
 
+/* K splits for a plain GEMM whose tile grid is under one block per CU: the
+ * largest power of two <= 8 that keeps the grid in one round of resident
+ * blocks (about 512) with at least 5 K steps per split. */
+extern "C" uint32_t uocr_gemm_ksplit(uint32_t M, uint32_t N, uint32_t K) {
+    const u32 blocks = ((M + TM - 1u) / TM) * ((N + TN - 1u) / TN), steps = K / TK;
+    if (blocks >= 256u) return 1u;
+    u32 s = 1u;
+    while (s < 8u && blocks * 2u * s <= 512u && steps / (2u * s) >= 5u) s *= 2u;
+    return s;
+}
+
 extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d) {
     if (d == nullptr || d->A == nullptr || d->out == nullptr || d->N == 0u || d->K == 0u || d->K % 64u != 0u ||
         d->lda % 8u != 0u || !pmat_ok(d->W[0]) || (epi == UOCR_GEMM_SWIGLU && (!pmat_ok(d->W[1]) || d->W[1].qtype != d->W[0].qtype)) ||
@@ -984,28 +1018,34 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
     a.kst = 0u;
     const dim3 grid(grouped ? d->max_tiles : (d->M + TM - 1u) / TM, (d->N + TN - 1u) / TN);
     const u32 qt = d->W[0].qtype;
-    if (epi == UOCR_GEMM_VISION) {
-        if (grouped || d->bias == nullptr || d->act > UOCR_VISION_ACT_GELU_ERF ||
-            (d->split != 0u && (d->N != 3u * d->split || d->out1 == nullptr || d->out2 == nullptr))) {
-            return hipErrorInvalidValue;
-        }
+    if (epi == UOCR_GEMM_VISION && (grouped || d->bias == nullptr || d->act > UOCR_VISION_ACT_GELU_ERF ||
+                                    (d->split != 0u && (d->N != 3u * d->split || d->out1 == nullptr ||
+                                                        d->out2 == nullptr)))) {
+        return hipErrorInvalidValue;
+    }
+    const bool splittable = !grouped && d->ksplit > 1u && d->part != nullptr && d->N % 4u == 0u &&
+                            (epi == UOCR_GEMM_VISION ? d->split % 4u == 0u
+                                                     : (epi == UOCR_GEMM_F16 || epi == UOCR_GEMM_F32) &&
+                                                           d->ldo % 4u == 0u &&
+                                                           (d->res == nullptr || d->ldr % 4u == 0u));
+    if (splittable) {
+        /* split-K: blockIdx.z takes K steps [z*kst, (z+1)*kst) into an fp32
+         * partial plane of part, then one ordered reduce applies the
+         * epilogue */
         const u32 nt = d->K / TK;
-        if (d->ksplit > 1u && d->part != nullptr && d->N % 4u == 0u && d->split % 4u == 0u) {
-            /* split-K: blockIdx.z takes K steps [z*kst, (z+1)*kst) into an
-             * fp32 partial plane of part, then one ordered reduce applies
-             * bias, activation and split */
-            const u32 kst = (nt + d->ksplit - 1u) / d->ksplit, S = (nt + kst - 1u) / kst;
-            a.kst = kst;
-            a.out = d->part;
-            a.ldo = d->N;
-            gemm_dispatch<GE_PART, false>(st, qt, a, dim3(grid.x, grid.y, S));
-            const size_t mn = (size_t)d->M * d->N;
-            hipLaunchKernelGGL(k_vision_reduce, dim3((unsigned)((mn / 4u + PB - 1u) / PB)), dim3(PB), 0, st,
-                               (const float *)d->part, S, d->M, d->N, (const h16 *)d->bias, d->act, d->split,
-                               (h16 *)d->out, (h16 *)d->out1, (h16 *)d->out2);
-        } else {
-            gemm_dispatch<GE_VISION, false>(st, qt, a, grid);
-        }
+        const u32 kst = (nt + min(d->ksplit, 8u) - 1u) / min(d->ksplit, 8u), S = (nt + kst - 1u) / kst;
+        a.kst = kst;
+        a.out = d->part;
+        a.ldo = d->N;
+        gemm_dispatch<GE_PART, false>(st, qt, a, dim3(grid.x, grid.y, S));
+        const size_t mn = (size_t)d->M * d->N;
+        const u32 mode = epi == UOCR_GEMM_VISION ? RD_VISION : (epi == UOCR_GEMM_F16 ? RD_F16 : RD_F32);
+        hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((mn / 4u + PB - 1u) / PB)), dim3(PB), 0, st,
+                           (const float *)d->part, S, d->M, d->N, mode, (const h16 *)d->bias, d->act, d->split,
+                           (const h16 *)d->res, d->ldr, d->out, (h16 *)d->out1, (h16 *)d->out2,
+                           epi == UOCR_GEMM_VISION ? d->N : d->ldo);
+    } else if (epi == UOCR_GEMM_VISION) {
+        gemm_dispatch<GE_VISION, false>(st, qt, a, grid);
     } else if (epi == UOCR_GEMM_F32) {
         if (grouped) gemm_dispatch<GE_F32, true>(st, qt, a, grid);
         else gemm_dispatch<GE_F32, false>(st, qt, a, grid);
