@@ -494,7 +494,7 @@ def main() -> None:
     ap.add_argument("--op-replays", type=int, default=None,
                     help="cap the graph replays of the operator measurements (counter-collection runs)")
     ap.add_argument("--prefill-only", action="store_true",
-                    help="run only the MFMA prefill of the config-5 prompt (Q4 profile, 1 generated token), twice")
+                    help="run only the MFMA prefill of the config-5 prompt (Q4 profile, 1 generated token), three times")
     ap.add_argument("--vision-only", action="store_true",
                     help="run only the vision linear (SAM / CLIP block shape) measurements")
     ap.add_argument("--no-vision", action="store_true", help="skip the vision linear measurements")
@@ -522,7 +522,9 @@ def main() -> None:
         model = uocr.synth_model(uocr.QPROFILE_Q4, 7)
         ids, mask, rows = make_prompt()
         with uocr.Engine.from_memory(model, backend="hip", max_prompt_tokens=1024, max_gen_tokens=8) as eng:
-            for _ in range(2):
+            # the first call runs the prefill eagerly, the second captures it
+            # (same prompt length), the third replays the graph
+            for _ in range(3):
                 _, _, p_ms, _ = eng.generate_embeddings(ids, mask, rows, 1, flags=uocr.GEN_IGNORE_EOS)
         gf = prefill_flops(ids.size)
         print(json.dumps({"prefill": {"ms": round(p_ms, 3), "gflop": round(gf / 1e9, 1),

@@ -110,12 +110,22 @@ def test_graph_and_eager_paths_agree(gpu):
     m = model(uocr, 3)
     rng = np.random.default_rng(5)
     ids, mask, rows = prompt(rng, 12, 4)
-    eng = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=128, max_gen_tokens=40)
+    eng = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=256, max_gen_tokens=40)
+    # prefill: eager (first length), eager (no graph), captured (same length
+    # again), replayed; then another length eagerly, and the first one again
     a = eng.generate_embeddings(ids, mask, rows, 20, flags=uocr.GEN_IGNORE_EOS)
     b = eng.generate_embeddings(ids, mask, rows, 20, flags=uocr.GEN_IGNORE_EOS | uocr.GEN_NO_GRAPH)
     c = eng.generate_embeddings(ids, mask, rows, 20, flags=uocr.GEN_IGNORE_EOS)
-    assert a[0].tolist() == b[0].tolist() == c[0].tolist()
-    assert np.array_equal(a[1], b[1])
+    d = eng.generate_embeddings(ids, mask, rows, 20, flags=uocr.GEN_IGNORE_EOS)
+    assert a[0].tolist() == b[0].tolist() == c[0].tolist() == d[0].tolist()
+    assert np.array_equal(a[1], b[1]) and np.array_equal(a[1], d[1])
+    ids2, mask2, rows2 = prompt(rng, 70, 90)  # 160 rows: three query tiles, split attention
+    e1 = eng.generate_embeddings(ids2, mask2, rows2, 8, flags=uocr.GEN_IGNORE_EOS | uocr.GEN_NO_GRAPH)
+    e2 = eng.generate_embeddings(ids2, mask2, rows2, 8, flags=uocr.GEN_IGNORE_EOS)
+    e3 = eng.generate_embeddings(ids2, mask2, rows2, 8, flags=uocr.GEN_IGNORE_EOS)
+    assert e1[0].tolist() == e2[0].tolist() == e3[0].tolist()
+    f = eng.generate_embeddings(ids, mask, rows, 20, flags=uocr.GEN_IGNORE_EOS)
+    assert f[0].tolist() == a[0].tolist()
     eng.close()
 
 
