@@ -206,9 +206,26 @@ struct GemmArgs {
  * into MFMA B operands in registers) for all 64 rows (two 32x32 MFMA
  * tiles); only the activation tile goes through LDS, double-buffered, so a
  * K step has one barrier and LDS carries one activation read per MFMA. */
+#ifndef UOCR_GEMM_BLDS
+#define UOCR_GEMM_BLDS 1
+#endif
+
 template <int QT, int EPI, bool GROUPED>
 __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     constexpr int NMAT = EPI == GE_SWIGLU ? 2 : 1;
+    /* f16 with one weight matrix: the block loads each K step's raw weight
+     * tile with eight lanes per row (whole 128-byte row pieces) into LDS, and
+     * each wavefront reads its 32 rows back in the MFMA operand layout; loads
+     * of one row per lane touched a cache line per lane (SAM lin1 with fp16
+     * weights 58.4 -> 48.5 us).  The same for Q8 (four lanes per 64-byte
+     * piece) measured -4.6% to +3.6% across the SAM / CLIP shapes, the extra
+     * 20 KB of LDS costing occupancy at long K, so Q8 keeps the per-lane
+     * loads; Q4 rows are 32 bytes per K step. */
+    constexpr bool BL = UOCR_GEMM_BLDS && QT == 1 && NMAT == 1;
+    constexpr u32 RB = QT == 3 ? 64u : 128u; /* raw bytes per row per K step */
+    constexpr u32 LDB = RB + 16u;            /* padded LDS row (bytes) */
+    constexpr u32 CPR = RB / 16u;            /* 16-byte pieces per row */
+    __shared__ __attribute__((aligned(16))) uint8_t bsm[BL ? 2u * TN * LDB : 16u];
     __shared__ __attribute__((aligned(16))) h16 as[2][TM * LDA];
     __shared__ int32_t arow[TM], orow[TM];
     const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6, hf = lane >> 5;
@@ -277,6 +294,15 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
         const u32 idx = t + q * PB;
         arp[q] = Ap + (size_t)arow[idx >> 3] * lda + (size_t)kb0 * TK + 8u * (idx & 7u);
     }
+    const uint8_t *bsrc[BPiece<QT>::NV];
+    if constexpr (BL) {
+        const u32 rowbytes = QT == 3 ? Kd : 2u * Kd;
+#pragma unroll
+        for (int v = 0; v < BPiece<QT>::NV; ++v) {
+            const u32 pidx = t + v * PB, r = pidx / CPR, c = pidx % CPR;
+            bsrc[v] = wp[0] + (size_t)min(lrow0 + r, nmax - 1u) * rowbytes + 16u * c;
+        }
+    }
     auto issue = [&](auto D, u32 st) {
         constexpr int d = decltype(D)::value;
 #pragma unroll
@@ -287,8 +313,22 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
             ka[d][q][2] = v.z;
             ka[d][q][3] = v.w;
         }
+        if constexpr (BL) {
+            /* piece v of this thread: row (t + v PB) / CPR of the block's
+             * rows, 16-byte piece (t + v PB) % CPR of its K step */
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) b_load<QT>(kb[d][m], ks[d][m], wp[m], sp[m], Kd, nrow, kb0 + st, hf, !scl);
+            for (int v = 0; v < BPiece<QT>::NV; ++v) {
+                const uint4 x = *(const uint4 *)(bsrc[v] + (size_t)(kb0 + st) * RB);
+                kb[d][0][4 * v] = x.x;
+                kb[d][0][4 * v + 1] = x.y;
+                kb[d][0][4 * v + 2] = x.z;
+                kb[d][0][4 * v + 3] = x.w;
+            }
+            if (!scl) ks[d][0] = ((const unsigned short *)sp[0])[(size_t)nrow * (Kd / 64u) + kb0 + st];
+        } else {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) b_load<QT>(kb[d][m], ks[d][m], wp[m], sp[m], Kd, nrow, kb0 + st, hf, !scl);
+        }
     };
     auto step = [&](auto D, u32 st) {
         constexpr int d = decltype(D)::value;
@@ -306,11 +346,35 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
 #pragma unroll
             for (int m = 0; m < NMAT; ++m) ks[d][m] = ssc[(m * TN + lrow) * NT + kb0 + st];
         }
+        uint8_t *bb = bsm + (st & 1u) * (BL ? TN * LDB : 0u);
+        if constexpr (BL) {
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) b_dequant<QT>(kb[d][m], ks[d][m], bop[m]);
+            for (int v = 0; v < BPiece<QT>::NV; ++v) {
+                const u32 pidx = t + v * PB;
+                *(uint4 *)(bb + (pidx / CPR) * LDB + 16u * (pidx % CPR)) =
+                    make_uint4(kb[d][0][4 * v], kb[d][0][4 * v + 1], kb[d][0][4 * v + 2], kb[d][0][4 * v + 3]);
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) b_dequant<QT>(kb[d][m], ks[d][m], bop[m]);
+        }
         /* the other buffer's readers (step st - 1) all passed this barrier
          * before anyone writes it again at step st + 1 */
         __syncthreads();
+        if constexpr (BL) {
+            /* this lane's MFMA piece of its row: bytes RB / 2 * h .. + RB / 2 */
+            u32 w[BPiece<QT>::NW];
+            const uint8_t *src = bb + (32u * wave + (lane & 31u)) * LDB + (RB / 2u) * hf;
+#pragma unroll
+            for (int v = 0; v < BPiece<QT>::NV; ++v) {
+                const uint4 x = *(const uint4 *)(src + 16u * v);
+                w[4 * v] = x.x;
+                w[4 * v + 1] = x.y;
+                w[4 * v + 2] = x.z;
+                w[4 * v + 3] = x.w;
+            }
+            b_dequant<QT>(w, ks[d][0], bop[0]);
+        }
         /* unconditional (past the end it re-reads the last step into a slot
          * no later step consumes): loads issued on every path keep the
          * compiler's load counting exact, so the wait before a step covers
