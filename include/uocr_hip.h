@@ -204,7 +204,11 @@ UOCR_API int uocr_op_vision_linear(uint32_t qtype, const void *w, const void *s,
 
 /* Causal attention of P prompt queries (fp16 [P][1280], RoPE applied) over
  * cache slots 0..P-1 of caches laid out [10][cache_capacity][128]; ctx fp16
- * [P][1280].  Replaces uocr_prefill_attention_flash_staged_f16_to_f16
+ * [P][1280].  Long causal key ranges are split over several blocks and
+ * merged by a second kernel, through a 17 MB partials buffer the library
+ * allocates on the first call made outside graph capture and keeps (without
+ * it the unsplit kernel runs; calls must not overlap).  Replaces
+ * uocr_prefill_attention_flash_staged_f16_to_f16
  * (kernels/attention_prefill.metal:105). */
 UOCR_API int uocr_op_prefill_attention(const void *q, const void *k_cache, const void *v_cache,
                                        uint32_t cache_capacity, uint32_t prompt_length, void *ctx);
