@@ -40,7 +40,7 @@ typedef uint32_t u32;
 #define TK 64  /* one quantisation group */
 #define LDA (TK + 8) /* padded LDS row of the activation tile (halves) */
 #ifndef GDEPTH
-#define GDEPTH 3 /* K steps in flight per GEMM block */
+#define GDEPTH 2 /* K steps in flight per GEMM block (2, 3 and 5 measured: 2 best on the SAM shapes, equal on the prefill) */
 #endif
 
 __device__ __forceinline__ float silu_p(float g) {
