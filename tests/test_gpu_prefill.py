@@ -142,13 +142,16 @@ def test_batched_and_token_prefill_agree(gpu):
 # fc2), the projector (2048 -> 1280), the Q4 and fp16 kernels, and ragged
 # tiles (m not a multiple of 64, n not a multiple of 128).  Long-K GEMMs on
 # grids of fewer than 128 tiles split K (CLIP fc2; 37 K steps in 4 splits of
-# 10, 10, 10 and 7 in the 2368-wide case).
+# 10, 10, 10 and 7 in the 2368-wide case).  n = 100 with k = 192 leaves the
+# block's scale region at 300 halves, which the LDS preload copies 2 bytes at
+# a time instead of 16.
 VISION_CASES = [
     (3, 4096, 768, 2304, 0, 768), (3, 4096, 768, 3072, 2, 0), (3, 4096, 3072, 768, 0, 0),
     (3, 257, 1024, 3072, 0, 1024), (3, 257, 1024, 4096, 1, 0), (3, 257, 4096, 1024, 0, 0),
     (3, 256, 2048, 1280, 0, 0), (4, 257, 1024, 4096, 1, 0), (1, 257, 1024, 4096, 1, 0),
     (1, 4096, 768, 3072, 2, 0), (4, 4096, 768, 2304, 0, 768), (3, 1, 64, 96, 2, 0), (1, 65, 128, 40, 1, 0),
     (4, 100, 192, 96, 2, 32), (3, 100, 2368, 256, 2, 0),
+    (3, 37, 192, 100, 0, 0), (4, 37, 192, 100, 1, 0),
 ]
 
 
