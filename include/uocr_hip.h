@@ -46,6 +46,7 @@ UOCR_API uocr_engine *uocr_engine_open_memory(const uocr_engine_opts *opts, cons
 #define UOCR_GEN_FLAG_IGNORE_EOS 1u  /* decode past EOS (benchmarks) */
 #define UOCR_GEN_FLAG_NO_GRAPH 2u    /* enqueue kernels directly, no hipGraph replay */
 #define UOCR_GEN_FLAG_TOKEN_PREFILL 4u /* prefill through the decode kernels, one prompt position at a time */
+#define UOCR_GEN_FLAG_NO_RUN 8u      /* decode with per-step kernel graphs instead of the persistent run */
 
 /* Greedy generation from a prompt whose image positions (image_mask[i] == 1)
  * take the next row of image_rows_f16 ([n_image_rows][1280] fp16) instead of

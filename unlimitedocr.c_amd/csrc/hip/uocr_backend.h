@@ -27,6 +27,7 @@ typedef struct uocr_hip_ctx uocr_hip_ctx;
 #define UOCR_GEN_IGNORE_EOS 1u   /* keep decoding past token 1 (benchmarks) */
 #define UOCR_GEN_NO_GRAPH 2u     /* enqueue kernels directly instead of replaying captured graphs */
 #define UOCR_GEN_TOKEN_PREFILL 4u /* prefill by replaying the decode layer kernels per prompt position */
+#define UOCR_GEN_NO_RUN 8u        /* decode with per-step graphs instead of the persistent run */
 
 typedef struct uocr_hip_decoder_request {
     const int32_t *input_ids;

@@ -28,9 +28,11 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <mutex>
 #include <vector>
 
 #include "uocr_kernels.h"
+#include "uocr_run.h"
 
 #define H_SIZE 1280u
 #define DECODE_CHUNK 8u
@@ -41,6 +43,7 @@ struct dev_layer {
     uocr_qmat q, k, v, o, gate, up, down, sgate, sup, sdown;
     const uint16_t *in_norm, *post_norm, *router;
     const float *rfold; /* [1280][64] router * post_norm, or NULL (router kernel) */
+    const float *rfold_all; /* the same fold whatever its range (the persistent run sums it in fp32) */
     uocr_expert_slab slab;
 };
 
@@ -109,7 +112,17 @@ struct uocr_hip_ctx {
      * twice in a row (its grids depend on the length) */
     hipGraphExec_t g_mfma;
     uint32_t g_mfma_P, last_mfma_P, cap_P;
+    /* persistent decode run (uocr_decode_run.hip) */
+    uocr_run_model run_model;
+    uocr_run_model *d_run_model; /* device copy, in the weight arena */
+    int run_ok;                  /* the model, device and environment allow the run */
+    uint8_t *run_arena;          /* packet arena, in the runtime arena */
+    uint32_t run_tag;            /* next unused packet tag */
 };
+
+/* Persistent runs need every CU of the device: runs of different engines in
+ * one process are serialised. */
+static std::mutex g_run_mutex;
 
 #define HIPCHK(expr, what)                                                                        \
     do {                                                                                          \
@@ -248,9 +261,10 @@ static int upload(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor &t, uocr
  * fp16 magnitude of a[i]) < 2^31.  Otherwise *out stays NULL and the layer
  * keeps the separate router kernel. */
 static int upload_router_fold(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor &R, const uocr_bound_tensor &nw,
-                              const float **out, char *err, size_t err_size) {
+                              const float **out, const float **all, char *err, size_t err_size) {
     constexpr uint32_t E = UOCR_ROUTED_EXPERTS;
     *out = nullptr;
+    *all = nullptr;
     const uint64_t bytes = (uint64_t)H_SIZE * E * 4u;
     const uint64_t off = p.take(bytes);
     if (R.qtype != UOCR_QT_F16 || R.w_bytes < (uint64_t)E * H_SIZE * 2u || nw.w_bytes < (uint64_t)H_SIZE * 2u) {
@@ -268,9 +282,9 @@ static int upload_router_fold(uocr_hip_ctx *ctx, placer &p, const uocr_bound_ten
         }
         worst = tot > worst ? tot : worst;
     }
-    if (!(worst * 65504.0 < 2147483648.0)) return 1;
     HIPCHK(hipMemcpy(ctx->warena + off, fold.data(), bytes, hipMemcpyHostToDevice), "router fold upload");
-    *out = (const float *)(ctx->warena + off);
+    *all = (const float *)(ctx->warena + off);
+    if (worst * 65504.0 < 2147483648.0) *out = *all;
     return 1;
 }
 
@@ -292,6 +306,81 @@ static int upload_slab(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor *ex
     out->qtype = ex[0].qtype;
     *w_stride = ws;
     *s_stride = ss / 2u;
+    return 1;
+}
+
+/* The persistent decode run's view of the model (device pointers of every
+ * layer) and whether this model, device and environment can use it:
+ * UOCR_HIP_RUN=1 selects it; the run needs a supported qtype mix, fp16
+ * routers (for the fold), 256 CUs and cooperative launch. */
+static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
+    uocr_run_model &m = ctx->run_model;
+    memset(&m, 0, sizeof(m));
+    bool ok = true;
+    for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
+        const dev_layer &D = ctx->L[l];
+        uocr_run_layer &R = m.L[l];
+        R.q = D.q.w;
+        R.k = D.k.w;
+        R.v = D.v.w;
+        R.o = D.o.w;
+        R.qs = D.q.s;
+        R.ks = D.k.s;
+        R.vs = D.v.s;
+        R.os = D.o.s;
+        R.in_norm = D.in_norm;
+        R.post_norm = D.post_norm;
+        ok = ok && D.q.qtype == D.k.qtype && D.q.qtype == D.v.qtype && D.q.qtype == D.o.qtype;
+        if (l == 0u) {
+            R.gate = D.gate.w;
+            R.up = D.up.w;
+            R.down = D.down.w;
+            R.gs = D.gate.s;
+            R.us = D.up.s;
+            R.ds = D.down.s;
+            ok = ok && D.gate.qtype == D.up.qtype && D.gate.qtype == D.down.qtype;
+            m.qf = D.gate.qtype;
+        } else {
+            R.fold = D.rfold_all;
+            R.sg = D.sgate.w;
+            R.su = D.sup.w;
+            R.sd = D.sdown.w;
+            R.sgs = D.sgate.s;
+            R.sus = D.sup.s;
+            R.sds = D.sdown.s;
+            R.eg = D.slab.gate.w;
+            R.eu = D.slab.up.w;
+            R.ed = D.slab.down.w;
+            R.egs = D.slab.gate.s;
+            R.eus = D.slab.up.s;
+            R.eds = D.slab.down.s;
+            R.gu_w_stride = D.slab.gu_w_stride;
+            R.gu_s_stride = D.slab.gu_s_stride;
+            R.dn_w_stride = D.slab.dn_w_stride;
+            R.dn_s_stride = D.slab.dn_s_stride;
+            ok = ok && R.fold != nullptr;
+            for (const uocr_qmat *q : {&D.sgate, &D.sup, &D.sdown, &D.slab.gate, &D.slab.up, &D.slab.down}) {
+                ok = ok && q->qtype == ctx->L[0].gate.qtype;
+            }
+        }
+        ok = ok && D.q.qtype == ctx->L[0].q.qtype;
+    }
+    m.qa = ctx->L[0].q.qtype;
+    m.lm = ctx->lm_head.w;
+    m.lms = ctx->lm_head.s;
+    m.emb = ctx->embed.w;
+    m.embs = ctx->embed.s;
+    m.final_norm = ctx->final_norm;
+    m.ql = ctx->lm_head.qtype;
+    m.qe = ctx->embed.qtype;
+    memcpy(m.invf, ctx->invf, sizeof(m.invf));
+    HIPCHK(hipMemcpy(ctx->d_run_model, &m, sizeof(m), hipMemcpyHostToDevice), "run model upload");
+    int cus = 0, coop = 0;
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
+    (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, ctx->device);
+    /* opt-in while the per-step graphs are faster: UOCR_HIP_RUN=1 */
+    const char *ru = getenv("UOCR_HIP_RUN");
+    ctx->run_ok = ok && uocr_run_supported(&m) && cus == (int)UOCR_RUN_BLOCKS && coop != 0 && ru != nullptr && atoi(ru) != 0;
     return 1;
 }
 
@@ -327,6 +416,8 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
             total += align256((uint64_t)H_SIZE * UOCR_ROUTED_EXPERTS * 4u);
         }
     }
+    const uint64_t run_model_off = total;
+    total += align256(sizeof(uocr_run_model));
     HIPCHK(hipMalloc((void **)&ctx->warena, total), "weight arena allocation");
     ctx->warena_bytes = total;
     placer p;
@@ -361,7 +452,7 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
             return 0;
         }
         D.router = (const uint16_t *)r.w;
-        if (!upload_router_fold(ctx, p, S.router, S.post_norm, &D.rfold, err, err_size)) return 0;
+        if (!upload_router_fold(ctx, p, S.router, S.post_norm, &D.rfold, &D.rfold_all, err, err_size)) return 0;
         if (no_fold) D.rfold = nullptr;
         uocr_expert_slab &sl = D.slab;
         uint64_t ws2, ss2;
@@ -372,7 +463,9 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
         }
         if (ws2 != sl.gu_w_stride || ss2 != sl.gu_s_stride) return bfail(err, err_size, "expert gate/up slabs differ in stride");
     }
-    if (p.off > total) return bfail(err, err_size, "weight arena overflow");
+    if (p.off > run_model_off) return bfail(err, err_size, "weight arena overflow");
+    ctx->d_run_model = (uocr_run_model *)(ctx->warena + run_model_off);
+    if (!setup_run(ctx, err, err_size)) return 0;
     /* the uploads ran on the null stream; the engine's stream is non-blocking,
      * so wait for them before any kernel can read the weights */
     HIPCHK(hipDeviceSynchronize(), "weight upload sync");
@@ -422,6 +515,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     /* split-K partials of the O projection and the dense down (2 splits x
      * P x 1280, fp32) */
     const uint64_t o_pkp = p.take(Pc * H_SIZE * 2u * 4u);
+    const uint64_t o_run = p.take(uocr_run_arena_bytes());
     const uint64_t total = p.off;
     HIPCHK(hipMalloc((void **)&ctx->rarena, total), "runtime arena allocation");
     /* cleared on the engine's stream (non-blocking, so not ordered against a
@@ -471,6 +565,8 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->p_list_pair = (int32_t *)(b + o_plp);
     ctx->p_fa_ws = (float *)(b + o_pfa);
     ctx->p_kpart = (float *)(b + o_pkp);
+    ctx->run_arena = b + o_run;
+    ctx->run_tag = 1u; /* the arena is zero: tag 0 never matches */
     ctx->p_max_tiles = max_tiles;
     ctx->rarena_bytes = total;
     ctx->kv_bytes = 2u * kv_one;
@@ -761,6 +857,79 @@ static int scan_chunk(uocr_hip_ctx *c, uint32_t from, uint32_t to, int ignore_eo
     return 1;
 }
 
+/* The decode loop on the persistent run: launches of DECODE_CHUNK steps,
+ * the first starting from the prefill's hidden state (published with a tag
+ * of its own), token ids read back one chunk behind the GPU. */
+static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, uint64_t t0, uint64_t t1,
+                      uocr_hip_decoder_result *res, char *err, size_t err_size) {
+    hipStream_t s = c->stream;
+    std::lock_guard<std::mutex> lock(g_run_mutex);
+    const uint32_t seed_tag = c->run_tag, tag0 = seed_tag + 1u;
+    c->run_tag = tag0 + N;
+    HIPCHK(uocr_run_reset(s, c->run_arena), "run reset");
+    HIPCHK(uocr_run_seed(s, c->run_arena, c->h, seed_tag), "run seed");
+    uint32_t count = 0, scanned = 0, issued = 0, chunk = 0;
+    int eos = 0, ok = 1;
+    hipEvent_t ev[2];
+    HIPCHK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming), "event create");
+    HIPCHK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming), "event create");
+    while (issued < N && !eos && ok) {
+        const uint32_t end = issued + DECODE_CHUNK < N ? issued + DECODE_CHUNK : N;
+        const hipError_t e = uocr_run_launch(s, c->d_run_model, &c->run_model, c->run_arena, c->kc, c->vc, c->cache_cap,
+                                             (int32_t)P, (int32_t)issued, (int32_t)(end - issued), end == N ? 1 : 0,
+                                             tag0 + issued, c->tokens, c->scores);
+        if (e != hipSuccess) {
+            ok = bfail(err, err_size, "decode run of steps %u-%u: %s", issued, end - 1u, hipGetErrorString(e));
+            break;
+        }
+        if (hipMemcpyAsync(c->h_tokens + issued, c->tokens + issued, (size_t)(end - issued) * 4u, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipEventRecord(ev[chunk & 1u], s) != hipSuccess) {
+            ok = bfail(err, err_size, "token readback failed");
+            break;
+        }
+        if (chunk > 0u) {
+            if (hipEventSynchronize(ev[(chunk - 1u) & 1u]) != hipSuccess) {
+                ok = bfail(err, err_size, "decode chunk wait failed");
+                break;
+            }
+            if (!scan_chunk(c, scanned, issued, ignore_eos, &count, &eos)) ok = bfail(err, err_size, "decode selected an invalid token id");
+            scanned = issued;
+        }
+        issued = end;
+        ++chunk;
+    }
+    const hipError_t se = hipStreamSynchronize(s);
+    (void)hipEventDestroy(ev[0]);
+    (void)hipEventDestroy(ev[1]);
+    if (se != hipSuccess) return bfail(err, err_size, "decode sync: %s", hipGetErrorString(se));
+    uint32_t ctl[4] = {0u, 0u, 0u, 0u};
+    HIPCHK(hipMemcpy(ctl, c->run_arena, sizeof(ctl), hipMemcpyDeviceToHost), "run status readback");
+    if (ctl[UOCR_RUN_CTL_ABORT] != 0u) {
+        return bfail(err, err_size, "decode run timed out waiting at stage %u of step %u (workgroup %u)",
+                     ctl[UOCR_RUN_CTL_WHERE], ctl[UOCR_RUN_CTL_STEP], ctl[UOCR_RUN_CTL_BLOCK]);
+    }
+    if (!ok) return 0;
+    if (!eos && !scan_chunk(c, scanned, issued, ignore_eos, &count, &eos)) {
+        return bfail(err, err_size, "decode selected an invalid token id");
+    }
+    const uint64_t t2 = uocr_now_ns();
+    memcpy(res->generated_ids, c->h_tokens, (size_t)count * 4u);
+    if (res->generated_scores != nullptr) {
+        HIPCHK(hipMemcpy(res->generated_scores, c->scores, (size_t)count * 4u, hipMemcpyDeviceToHost), "score readback");
+    }
+    res->generated_count = count;
+    res->stopped_on_eos = (uint32_t)eos;
+    res->prefill_ms = (double)(t1 - t0) / 1.0e6;
+    res->decode_ms = (double)(t2 - t1) / 1.0e6;
+    if (c->profile != nullptr) {
+        uocr_profile_add_ms(c->profile, "hip.prefill", res->prefill_ms);
+        uocr_profile_add_ms(c->profile, "hip.decode_loop", res->decode_ms);
+        c->profile->report.metal_command_buffer_count += chunk;
+        c->profile->report.metal_command_buffer_wait_count += chunk + 1u;
+    }
+    return 1;
+}
+
 extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder_request *req,
                                          uocr_hip_decoder_result *res, char *err, size_t err_size) {
     if (c == nullptr || req == nullptr || res == nullptr || req->input_ids == nullptr) {
@@ -831,9 +1000,12 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
     const uint64_t t1 = uocr_now_ns();
 
     /* decode: chunks of DECODE_CHUNK steps; the host scans chunk k-1 while
-     * chunk k runs */
-    HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf), "decode state init");
+     * chunk k runs.  A chunk is one persistent run launch, or (UOCR_GEN_NO_RUN,
+     * unsupported models) one replay of the captured 8-step graph. */
     const int ignore_eos = (req->flags & UOCR_GEN_IGNORE_EOS) != 0u;
+    const bool use_run = c->run_ok && use_graph && (req->flags & UOCR_GEN_NO_RUN) == 0u;
+    if (use_run) return decode_run(c, P, N, ignore_eos, t0, t1, res, err, err_size);
+    HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf), "decode state init");
     uint32_t count = 0, scanned = 0;
     int eos = 0;
     hipEvent_t ev[2];

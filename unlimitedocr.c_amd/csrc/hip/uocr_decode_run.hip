@@ -1,0 +1,1345 @@
+/*
+ * uocr_decode_run.hip - the persistent decode run (k_decode_run): greedy
+ * decode steps of the 12-layer decoder carried by 256 resident workgroups,
+ * one per CU, with no kernel boundary between stages.
+ *
+ * Op order and rounding points are the decode step of uocr_metal.m:14299-14518
+ * (the same as the per-stage kernels of uocr_kernels.hip):
+ *   LM head over the final-normed hidden state -> argmax (NaN rows skipped,
+ *   ties to the lowest id, none valid -> 0; lm_head_q4.metal:25-98,
+ *   sampling.metal:173-200) -> embedding row -> per layer:
+ *   rmsnorm -> q/k/v (f16) -> split-half RoPE (rope.metal:39-70) -> KV slot
+ *   write (kv_cache.metal:20-62) -> attention over the live slots
+ *   (attention_decode.metal:25-131) -> f16 context -> O + residual (f16) ->
+ *   rmsnorm -> layer 0: dense SwiGLU; layers 1-11: router top-6
+ *   (moe.metal:12-18, raw probabilities), routed + shared SwiGLU mids (f16),
+ *   down-combine f16(sum_r w_r D_r mid_r + f16(shared) + residual)
+ *   (decode_gemv_q4.metal:185-224).
+ *
+ * Stages and the workgroups that run them (b = workgroup index):
+ *   LM   all 256: rows [505b, 505b+505) of the LM head, one argmax packet each
+ *   QKV  b < 240: 8 (matrix, head, rotation pair) items of 2 rows each
+ *   ATT  176 <= b < 256: (head, split) of 10 x 8 over the live KV slots
+ *   O    136 <= b < 176: 32 rows of O each, plus the rows' share of the
+ *        un-normalised router logits z[e] = sum_i fold[i][e] a[i]
+ *   GU   all 256: b < 192 routed (rank b/32, 28 rows of that expert),
+ *        b >= 192 the shared experts' 1792 rows (layer 0: 27 dense rows each)
+ *   DN   b < 160: 8 output rows each
+ * Every block computes the top-6 itself from the O blocks' z partials (summed
+ * in a fixed order), so the DN blocks issue their routed down-projection
+ * loads as soon as the GU stage knows the experts.
+ *
+ * Hand-off (see uocr_run.h): packets {tag, 3 words}, device-coherent 16-byte
+ * stores into one copy per XCD, device-coherent polls on the block's own
+ * copy.  A stage's weight loads are issued before it polls for its inputs.
+ * Every wait is bounded: after UOCR_RUN_LIMIT_TICKS without its packet a
+ * block raises the abort word, every other waiting block sees it within a
+ * few polls, and all blocks leave the kernel; the host reports the failure.
+ */
+#include "uocr_run.h"
+
+#include "uocr_dev.h"
+
+namespace {
+
+typedef uint64_t u64;
+#define AS1 __attribute__((address_space(1))) /* global memory */
+#define AS4 __attribute__((address_space(4))) /* constant memory: scalar loads */
+
+/* Device view of uocr_run_model: the same layout, read through the constant
+ * address space (the descriptor does not change during a run, so its fields
+ * come through scalar loads), with global-memory pointer fields (so the
+ * weight loads are global, not flat, loads). */
+struct RunLayerD {
+    const AS1 uint8_t *q, *k, *v, *o;
+    const AS1 uint16_t *qs, *ks, *vs, *os;
+    const AS1 uint16_t *in_norm, *post_norm;
+    const AS1 float *fold;
+    const AS1 uint8_t *gate, *up, *down;
+    const AS1 uint16_t *gs, *us, *ds;
+    const AS1 uint8_t *sg, *su, *sd;
+    const AS1 uint16_t *sgs, *sus, *sds;
+    const AS1 uint8_t *eg, *eu, *ed;
+    const AS1 uint16_t *egs, *eus, *eds;
+    uint64_t gu_w_stride, gu_s_stride, dn_w_stride, dn_s_stride;
+};
+struct RunModelD {
+    RunLayerD L[UOCR_RUN_LAYERS];
+    const AS1 uint8_t *lm, *emb;
+    const AS1 uint16_t *lms, *embs, *final_norm;
+    float invf[UOCR_K_HEAD_DIM / 2];
+    uint32_t qa, qf, ql, qe;
+};
+static_assert(sizeof(RunModelD) == sizeof(uocr_run_model) && sizeof(RunLayerD) == sizeof(uocr_run_layer),
+              "device view of the run model");
+
+template <typename T, typename U>
+__device__ __forceinline__ const T *gp(const AS1 U *p) {
+    return (const T *)(const AS1 T *)p;
+}
+__device__ __forceinline__ const h16 *H(const AS1 uint16_t *p) { return gp<h16>(p); }
+/* threadIdx.x made opaque to the optimiser at each use, so per-lane values of
+ * one stage are recomputed there instead of being hoisted out of the step and
+ * layer loops and held in registers through every other stage */
+__device__ __forceinline__ u32 tid_() {
+    u32 t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+constexpr u32 NB = UOCR_RUN_BLOCKS, NT = UOCR_RUN_THREADS, NREP = UOCR_RUN_REPL;
+constexpr u32 HID = UOCR_K_HIDDEN, HDIM = UOCR_K_HEAD_DIM, NHEAD = UOCR_K_HEADS, NEXP = UOCR_K_EXPERTS;
+constexpr u32 TOPK = UOCR_K_TOPK, EI = 896u, SI = 1792u, DI = 6848u, VOCAB = 129280u, RING = UOCR_K_RING;
+
+constexpr u32 QKV_BLOCKS = 240u;  /* 1920 items / 8 */
+constexpr u32 ATT_SPLITS = 8u, ATT_BLOCKS = NHEAD * ATT_SPLITS, ATT0 = NB - ATT_BLOCKS;
+constexpr u32 O_BLOCKS = 40u, O_ROWS = 32u, O0 = ATT0 - O_BLOCKS;
+constexpr u32 GU_ROUTED = 192u, GU_ROWS = 28u, DGU_ROWS = 27u;
+constexpr u32 DN_BLOCKS = 160u, DN_ROWS = 8u;
+constexpr u32 LM_ROWS = VOCAB / NB;
+static_assert(LM_ROWS * NB == VOCAB, "LM rows split evenly");
+static_assert(GU_ROUTED * GU_ROWS == TOPK * EI && (NB - GU_ROUTED) * GU_ROWS == SI, "GU rows");
+static_assert(NB * DGU_ROWS >= DI, "dense rows");
+static_assert(O0 >= 0u && O0 + O_BLOCKS <= QKV_BLOCKS, "O blocks also gather h in the QKV stage");
+
+/* packets per copy */
+constexpr u32 PQKV_B = 3u, PQKV = QKV_BLOCKS * PQKV_B;
+constexpr u32 PATT_B = 23u, PATT = ATT_BLOCKS * PATT_B;
+constexpr u32 PO_A = 6u, PO_Z = 22u, PO_B = PO_A + PO_Z, PO = O_BLOCKS * PO_B;
+constexpr u32 PMID_B = 5u, PMID = NB * PMID_B;
+constexpr u32 PH_B = 2u, PH = DN_BLOCKS * PH_B;
+constexpr u32 PLM = NB;
+constexpr u32 PLAYER = PQKV + PATT + PO + PMID + PH;
+constexpr u32 CTL_PK = 16u; /* 256 bytes of control words */
+
+__host__ __device__ constexpr u64 off_lm() { return CTL_PK; }
+__host__ __device__ constexpr u64 off_layer(u32 l) { return CTL_PK + (u64)PLM * NREP + (u64)l * PLAYER * NREP; }
+__host__ __device__ constexpr u64 off_qkv(u32 l) { return off_layer(l); }
+__host__ __device__ constexpr u64 off_att(u32 l) { return off_layer(l) + (u64)PQKV * NREP; }
+__host__ __device__ constexpr u64 off_o(u32 l) { return off_att(l) + (u64)PATT * NREP; }
+__host__ __device__ constexpr u64 off_mid(u32 l) { return off_o(l) + (u64)PO * NREP; }
+__host__ __device__ constexpr u64 off_h(u32 l) { return off_mid(l) + (u64)PMID * NREP; }
+constexpr u64 ARENA_PK = off_layer(UOCR_RUN_LAYERS);
+
+#ifndef UOCR_RUN_LIMIT_TICKS
+#define UOCR_RUN_LIMIT_TICKS 5000000ull /* 50 ms of s_memrealtime (100 MHz) */
+#endif
+
+/* stage codes reported on a timeout */
+enum { W_LM = 1, W_SEL = 2, W_QKV = 3, W_ATT = 4, W_O = 5, W_GU = 6, W_DN = 7 };
+
+/* Hardware exp2 / reciprocal forms (about 1 ulp in fp32) for the run's
+ * softmax, SiLU, router probabilities and norms: with one wavefront per SIMD
+ * every instruction on a stage's path costs about 2 ns, and the precise
+ * library forms are several times longer.  Each result is rounded to fp16
+ * or compared at the 1e-2 margins of the parity contract afterwards. */
+__device__ __forceinline__ float fexp(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+__device__ __forceinline__ float frcp(float x) {
+    return __builtin_amdgcn_rcpf(x);
+}
+__device__ __forceinline__ float fsilu(float g) {
+    return g * frcp(1.0f + fexp(-g));
+}
+
+/* ---- device-coherent accesses ------------------------------------------- */
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, 0x7fffffff, 0x00020000);
+}
+/* sc1 loads are served from the memory side, never from a stale L2 line;
+ * the compiler barrier keeps a polling load inside its loop */
+__device__ __forceinline__ uint4 cload16(const void *base, u32 off) {
+    asm volatile("" ::: "memory");
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), off, 0, 16));
+}
+__device__ __forceinline__ u32 cload32(const void *base, u32 off) {
+    asm volatile("" ::: "memory");
+    return __builtin_amdgcn_raw_buffer_load_b32(rsrc(base), off, 0, 16);
+}
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void cstore16(void *base, u32 off, uint4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rsrc(base), off, 0, 16);
+}
+__device__ __forceinline__ void cstore32(void *base, u32 off, u32 v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, rsrc(base), off, 0, 16);
+}
+__device__ __forceinline__ void cstore_h16(void *base, u32 off, h16 v) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), rsrc(base), off, 0, 16);
+}
+
+/* ---- opt-in timeline (builds with -DUOCR_RUN_TIMELINE) ------------------- */
+
+#ifdef UOCR_RUN_TIMELINE
+/* s_memrealtime stamps of one chosen step: [block][event], event 2c when
+ * stage c's inputs were complete, 2c + 1 when its packets were stored
+ * (c = 0: LM head, 1 + 5l + s: stage s of layer l), 127 the step start;
+ * 128 + k: points inside the stages of layer 5 and the LM head */
+__device__ unsigned long long *g_run_tl;
+__device__ int g_run_tl_step;
+#define RUN_TL_EVENTS 256u
+#define TLR(ev)                                                                                    \
+    do {                                                                                           \
+        if (R.tl != nullptr && tid_() == 0u) R.tl[blockIdx.x * RUN_TL_EVENTS + (ev)] =             \
+            __builtin_amdgcn_s_memrealtime();                                                      \
+    } while (0)
+#define TLD(l, k)                      \
+    do {                               \
+        if ((l) == 5u) TLR(128u + (k)); \
+    } while (0)
+#else
+#define TLR(ev) \
+    do {        \
+    } while (0)
+#define TLD(l, k) \
+    do {          \
+    } while (0)
+#endif
+
+/* ---- packet hand-off ---------------------------------------------------- */
+
+struct Run {
+    const AS4 RunModelD *M;
+    uint4 *pk;
+    u32 *ctl;
+    h16 *kc, *vc;
+    u32 cap, xcc;
+    int32_t P;
+    int32_t *tokens;
+    float *scores;
+    unsigned long long *tl; /* timeline of this step, or NULL */
+};
+
+/* Raises the run's abort word with where/step/block; 1. */
+__device__ __attribute__((noinline)) int give_up(u32 *ctl, u32 where, u32 step) {
+    cstore32(ctl, UOCR_RUN_CTL_WHERE * 4u, where);
+    cstore32(ctl, UOCR_RUN_CTL_STEP * 4u, step);
+    cstore32(ctl, UOCR_RUN_CTL_BLOCK * 4u, blockIdx.x);
+    cstore32(ctl, UOCR_RUN_CTL_ABORT * 4u, 1u);
+    return 1;
+}
+
+/* Block-wide gather of n packets (logical index i -> physical phys(i)) of
+ * the block's copy: sink(i, packet) for each; false when the run aborted.
+ * A thread polls all of its packets that are not current yet in one round
+ * (one memory round trip per round whatever their number).  Ends with a
+ * barrier, so the sinks' LDS writes are visible. */
+/* Probe phase of a gather: thread p < nprod polls the last packet of
+ * producer p (physical base + p * per + per - 1) until it carries tag, so a
+ * block waiting for a long stage polls one packet per producer instead of
+ * every packet.  1 on abort or timeout. */
+__device__ __forceinline__ int probe(const Run &R, const uint4 *rep, u32 nprod, u32 per, u32 base, u32 tag, u32 where,
+                                     u32 step) {
+    const u32 t = tid_();
+    if (t >= nprod) return 0;
+    const u32 off = (base + t * per + per - 1u) * 16u;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (u32 it = 1;; ++it) {
+        if (cload16(rep, off).x == tag) return 0;
+        __builtin_amdgcn_s_sleep(2);
+        if ((it & 15u) == 0u) {
+            if (cload32(R.ctl, UOCR_RUN_CTL_ABORT * 4u) != 0u) return 1;
+            if (__builtin_amdgcn_s_memrealtime() - t0 > UOCR_RUN_LIMIT_TICKS) return give_up(R.ctl, where, step);
+        }
+    }
+}
+
+template <int MAXP, typename Phys, typename Sink>
+__device__ __forceinline__ bool gather(const Run &R, const uint4 *region, u32 per_copy, u32 n, u32 tag, u32 where,
+                                       u32 step, Phys phys, Sink sink, u32 nprod = 0u, u32 per = 1u, u32 base = 0u) {
+    const uint4 *rep = region + (size_t)R.xcc * per_copy;
+    const u32 t = tid_();
+    if (nprod != 0u &&
+        __builtin_amdgcn_readfirstlane(__syncthreads_or(probe(R, rep, nprod, per, base, tag, where, step))) != 0) {
+        return false;
+    }
+    uint4 v[MAXP];
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k) v[k] = cload16(rep, phys(min(t + (u32)k * NT, n - 1u)) * 16u);
+    u32 pend = 0u;
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k) pend |= (t + (u32)k * NT < n && v[k].x != tag) ? (1u << k) : 0u;
+    int bad = 0;
+    if (pend != 0u) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        for (u32 it = 1; pend != 0u; ++it) {
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int k = 0; k < MAXP; ++k) {
+                if (pend & (1u << k)) v[k] = cload16(rep, phys(t + (u32)k * NT) * 16u);
+            }
+#pragma unroll
+            for (int k = 0; k < MAXP; ++k) {
+                if ((pend & (1u << k)) && v[k].x == tag) pend &= ~(1u << k);
+            }
+            if (pend != 0u && (it & 15u) == 0u) {
+                if (cload32(R.ctl, UOCR_RUN_CTL_ABORT * 4u) != 0u ||
+                    __builtin_amdgcn_s_memrealtime() - t0 > UOCR_RUN_LIMIT_TICKS) {
+                    if (cload32(R.ctl, UOCR_RUN_CTL_ABORT * 4u) == 0u) give_up(R.ctl, where, step);
+                    bad = 1;
+                    break;
+                }
+            }
+        }
+    }
+    if (bad == 0) {
+#pragma unroll
+        for (int k = 0; k < MAXP; ++k) {
+            if (t + (u32)k * NT < n) sink(t + (u32)k * NT, v[k]);
+        }
+    }
+    /* readfirstlane: the result is block-uniform, and the compiler must know
+     * it, or every loop exit that depends on it turns the layer loop
+     * divergent (per-layer pointers then come through vector loads and
+     * full waits) */
+    return __builtin_amdgcn_readfirstlane(__syncthreads_or(bad)) == 0;
+}
+
+/* Threads t < npk * NREP store packet t / NREP of the block into copy
+ * t % NREP at first + p; payload(p) gives its three words. */
+template <typename Pay>
+__device__ __forceinline__ void publish(const Run &R, uint4 *region, u32 per_copy, u32 first, u32 npk, u32 tag,
+                                        Pay payload) {
+    const u32 t = tid_();
+    if (t < npk * NREP) {
+        const u32 p = t / NREP, r = t % NREP;
+        const uint3 d = payload(p);
+        cstore16(region, (r * per_copy + first + p) * 16u, make_uint4(tag, d.x, d.y, d.z));
+    }
+}
+
+__device__ __forceinline__ u32 pack2(h16 a, h16 b) {
+    return (u32)__builtin_bit_cast(unsigned short, a) | ((u32)__builtin_bit_cast(unsigned short, b) << 16);
+}
+__device__ __forceinline__ h16 lo16(u32 w) {
+    return __builtin_bit_cast(h16, (unsigned short)(w & 0xffffu));
+}
+__device__ __forceinline__ h16 hi16(u32 w) {
+    return __builtin_bit_cast(h16, (unsigned short)(w >> 16));
+}
+/* payload of 6 halves v[6p .. 6p+5], zero past n */
+__device__ __forceinline__ uint3 pay6(const h16 *v, u32 p, u32 n) {
+    h16 e[6];
+#pragma unroll
+    for (int j = 0; j < 6; ++j) e[j] = 6u * p + j < n ? v[6u * p + j] : (h16)0.0f;
+    return make_uint3(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]));
+}
+/* writes the 6 halves of packet v to dst[0..5], stopping at n - base */
+__device__ __forceinline__ void put6(h16 *dst, uint4 v, u32 base, u32 n) {
+    const h16 e[6] = {lo16(v.y), hi16(v.y), lo16(v.z), hi16(v.z), lo16(v.w), hi16(v.w)};
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+        if (base + j < n) dst[j] = e[j];
+    }
+}
+
+/* The norm weight's 8 values of thread t < 160 (columns 8t..8t+7), loaded
+ * before a stage polls for its inputs. */
+__device__ __forceinline__ uint4 norm_piece(const AS1 uint16_t *nw) {
+    return gp<uint4>(nw)[min(tid_(), HID / 8u - 1u)];
+}
+
+/* RMSNorm of the LDS vector x into xs with the weight piece w of norm_piece
+ * (eps 1e-6, fp32 sum of squares, one rounding per element;
+ * norm.metal:12-40); returns inv_rms. */
+__device__ __forceinline__ float rms_lds(const h16 *x, uint4 w, h16 *xs, float *red) {
+    union h8 {
+        uint4 u;
+        h16 h[8];
+    } xv, wv;
+    const u32 t = tid_();
+    float ss = 0.0f;
+    xv.u = ((const uint4 *)x)[min(t, HID / 8u - 1u)];
+    if (t < HID / 8u) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf((float)xv.h[j], (float)xv.h[j], ss);
+    }
+    ss = block_sum(ss, red);
+    const float inv = __builtin_amdgcn_rsqf(ss / (float)HID + 1.0e-6f);
+    if (t < HID / 8u) {
+        wv.u = w;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv.h[j] = (h16)(((float)xv.h[j] * inv) * (float)wv.h[j]);
+        ((uint4 *)xs)[t] = xv.u;
+    }
+    __syncthreads();
+    return inv;
+}
+
+/* Embedding row tok, columns 8i..8i+7, dequantised as f16(q * scale). */
+template <int QE>
+__device__ __forceinline__ uint4 embed8(const AS1 uint8_t *EW, const AS1 uint16_t *ES, int32_t tok, u32 i) {
+    union h8 {
+        uint4 u;
+        h16 h[8];
+    } o;
+    o.u = make_uint4(0u, 0u, 0u, 0u);
+    if (tok < 0 || (u32)tok >= VOCAB) return o.u;
+    const size_t r = (size_t)tok;
+    if (QE == 1) return ((const uint4 *)(gp<h16>(EW) + r * HID))[i];
+    const float sc = (float)gp<h16>(ES)[r * (HID / 64u) + i / 8u];
+    if (QE == 3) {
+        const uint2 v = *(const uint2 *)(gp<uint8_t>(EW) + r * HID + 8u * i);
+        const u32 w[2] = {v.x, v.y};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o.h[j] = (h16)((float)(int8_t)((w[j / 4] >> (8 * (j % 4))) & 0xffu) * sc);
+    } else {
+        const u32 j0 = (i % 8u) * 8u;
+        const uint2 v = *(const uint2 *)(gp<uint8_t>(EW) + r * (HID / 2u) + (i / 8u) * 32u + (j0 & 31u));
+        const u32 w[2] = {v.x, v.y}, sh = j0 < 32u ? 0u : 4u;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o.h[j] = (h16)((float)((int)((w[j / 4] >> (8 * (j % 4) + sh)) & 15u) - 8) * sc);
+    }
+    return o.u;
+}
+
+struct Lds {
+    h16 *xs, *hres, *outv;
+    float *red, *zout, *selw;
+    u32 *selid;
+    unsigned long long *keyw;
+    uint8_t *scr;
+};
+
+/* ---- LM head -------------------------------------------------------------- */
+
+template <int QL>
+struct LmCfg {
+    static constexpr u32 C = chunks_per_row<QL>(HID);
+    static constexpr u32 LPR = QL == 4 ? 8u : (QL == 3 ? 16u : 32u);
+    static constexpr u32 J = C / LPR;
+    static constexpr u32 GPP = NT / LPR;
+    static constexpr u32 NPASS = (LM_ROWS + GPP - 1u) / GPP;
+    static_assert(J * LPR == C, "LM lanes cover a row");
+};
+
+template <int QL>
+__device__ __forceinline__ void lm_load(const Run &R, RowFrag<LmCfg<QL>::J> &f, u32 pass) {
+    typedef LmCfg<QL> G;
+    const u32 grp = tid_() / G::LPR, sub = tid_() % G::LPR;
+    const u32 r = blockIdx.x * LM_ROWS + min(pass * G::GPP + grp, LM_ROWS - 1u);
+    frag_load<QL, G::LPR, G::J, true>(f, gp<uint8_t>(R.M->lm) + (size_t)r * 16u * G::C,
+                                      H(R.M->lms) + (size_t)r * (HID / 64u), G::C, sub);
+}
+
+/* LM head over the hidden state published with htag; publishes the block's
+ * argmax key with tag.  The caller issues the loads of passes 0 and 1 into
+ * f[0] and f[1]; each pass's dot is followed by the load of the pass two
+ * later into the same buffer (10 chunks per lane: 80 KB in flight per CU). */
+static_assert(NT % 64u == 0u && NT <= 1024u, "block of whole wavefronts");
+constexpr u32 LM_DEPTH = 2u;
+
+template <int QL>
+__device__ bool lm_stage(const Run &R, const Lds &S, u32 tag, u32 htag, int32_t step,
+                         RowFrag<LmCfg<QL>::J> (&f)[LM_DEPTH]) {
+    typedef LmCfg<QL> G;
+    const u32 grp = tid_() / G::LPR, sub = tid_() % G::LPR, lane = tid_() & 63u, wave = tid_() >> 6;
+    h16 *hres = S.hres;
+    const uint4 nwp = norm_piece(R.M->final_norm);
+    if (!gather<(PH + NT - 1u) / NT>(R, R.pk + off_h(UOCR_RUN_LAYERS - 1u), PH, PH, htag, W_LM, (u32)step, [](u32 i) { return i; },
+                   [&](u32 i, uint4 v) { put6(hres + (i / 2u) * DN_ROWS + (i % 2u) * 6u, v, (i % 2u) * 6u, DN_ROWS); })) {
+        return false;
+    }
+    TLR(0u);
+    rms_lds(S.hres, nwp, S.xs, S.red);
+    TLR(128u + 13u);
+    const u32 row0 = blockIdx.x * LM_ROWS;
+    float bs = -INFINITY;
+    u32 bid = NONE_ID;
+    auto finish = [&](const RowFrag<G::J> &fr, u32 pass) {
+        const u32 r = pass * G::GPP + grp;
+        const float d = group_sum<G::LPR>(frag_dot<QL, G::LPR, G::J>(fr, S.xs, G::C, sub));
+        if (r < LM_ROWS && !isnan(d) && better(d, row0 + r, bs, bid)) {
+            bs = d;
+            bid = row0 + r;
+        }
+    };
+#pragma unroll 1
+    for (u32 p = 0; p < G::NPASS; p += 2u) {
+        finish(f[0], p);
+        if (p + 2u < G::NPASS) lm_load<QL>(R, f[0], p + 2u);
+        if (p + 1u < G::NPASS) {
+            finish(f[1], p + 1u);
+            if (p + 3u < G::NPASS) lm_load<QL>(R, f[1], p + 3u);
+        }
+    }
+    TLR(128u + 14u);
+#pragma unroll
+    for (u32 o = G::LPR; o < 64u; o <<= 1) {
+        const float os = __shfl_xor(bs, (int)o);
+        const u32 oid = (u32)__shfl_xor((int)bid, (int)o);
+        if (better(os, oid, bs, bid)) {
+            bs = os;
+            bid = oid;
+        }
+    }
+    if (lane == 0u) S.keyw[wave] = argmax_key(bs, bid);
+    __syncthreads();
+    unsigned long long k = S.keyw[0];
+#pragma unroll
+    for (u32 w = 1; w < NT / 64u; ++w) k = S.keyw[w] > k ? S.keyw[w] : k;
+    publish(R, R.pk + off_lm(), PLM, blockIdx.x, 1u, tag,
+            [&](u32) { return make_uint3((u32)k, (u32)(k >> 32), 0u); });
+    TLR(1u);
+    return true;
+}
+
+/* The token of the step: the largest of the 256 argmax keys (0: no valid
+ * row -> token 0).  Every thread receives it. */
+__device__ bool select_token(const Run &R, const Lds &S, u32 tag, int32_t step, int32_t &tok, float &score) {
+    unsigned long long *kw = S.keyw;
+    unsigned long long mine = 0ull;
+    if (!gather<(PLM + NT - 1u) / NT>(R, R.pk + off_lm(), PLM, PLM, tag, W_SEL, (u32)step, [](u32 i) { return i; },
+                   [&](u32, uint4 v) { mine = ((unsigned long long)v.z << 32) | v.y; })) {
+        return false;
+    }
+    mine = wave_max_u64(mine);
+    if ((tid_() & 63u) == 0u) kw[tid_() >> 6] = mine;
+    __syncthreads();
+    unsigned long long k = kw[0];
+#pragma unroll
+    for (u32 w = 1; w < NT / 64u; ++w) k = kw[w] > k ? kw[w] : k;
+    u32 bi;
+    key_winner(k, score, bi);
+    tok = bi == NONE_ID ? 0 : (int32_t)bi;
+    __syncthreads(); /* keyw is reused */
+    return true;
+}
+
+/* ---- attention input: q/k/v + RoPE + KV write ---------------------------- */
+
+template <int QA>
+struct QkvCfg {
+    static constexpr u32 C = chunks_per_row<QA>(HID), LPR = 32u, J = (C + LPR - 1u) / LPR;
+};
+static_assert(NT / 64u == 8u, "QKV: one (matrix, head, pair) item per wavefront, 8 per block");
+
+template <int QA>
+struct QkvFrags {
+    RowFrag<QkvCfg<QA>::J> f;
+};
+
+/* Item of wavefront w of block b: matrix m = (b % 24) / 8 of q/k/v, head
+ * b / 24, rotation pair d = (b % 8) * 8 + w; lanes 0-31 hold row d of the
+ * head, lanes 32-63 row d + 64. */
+template <int QA>
+__device__ __forceinline__ void qkv_load(const Run &R, u32 l, QkvFrags<QA> &F) {
+    typedef QkvCfg<QA> G;
+    const u32 b = blockIdx.x;
+    if (b >= QKV_BLOCKS) return;
+    const AS4 RunLayerD &L = R.M->L[l];
+    const u32 head = b / 24u, m = (b % 24u) / 8u, lane = tid_() & 63u;
+    const u32 d = (b % 8u) * 8u + (tid_() >> 6), sub = lane % 32u;
+    const uint8_t *W = gp<uint8_t>(m == 0u ? L.q : (m == 1u ? L.k : L.v));
+    const h16 *Sc = m == 0u ? H(L.qs) : (m == 1u ? H(L.ks) : H(L.vs));
+    const u32 r = head * HDIM + d + (lane < 32u ? 0u : 64u);
+    frag_load<QA, G::LPR, G::J>(F.f, W + (size_t)r * 16u * G::C, Sc + (size_t)r * (HID / 64u), G::C, sub);
+}
+
+/* QKV stage of layer l at decode step t.  Layer 0 selects the token from
+ * the LM keys and stages its embedding row as the hidden state. */
+template <int QA, int QE>
+__device__ bool qkv_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, QkvFrags<QA> &F) {
+    typedef QkvCfg<QA> G;
+    const u32 b = blockIdx.x;
+    if (b >= QKV_BLOCKS) return true;
+    const AS4 RunLayerD &L = R.M->L[l];
+    const u32 w = tid_() >> 6, lane = tid_() & 63u;
+    const u32 head = b / 24u, m = (b % 24u) / 8u, d = (b % 8u) * 8u + w, sub = lane % 32u;
+    const int32_t pos = R.P + t;
+    const u32 slot = (u32)(R.P + t % (int32_t)RING);
+    float cs = 1.0f, sn = 0.0f;
+    if (m < 2u) {
+        const float ang = (float)pos * R.M->invf[d];
+        cs = cosf(ang);
+        sn = sinf(ang);
+    }
+    h16 *hres = S.hres;
+    const uint4 nwp = norm_piece(L.in_norm);
+    if (l == 0u) {
+        int32_t tok;
+        float score;
+        if (!select_token(R, S, tag, t, tok, score)) return false;
+        if (b == 0u && tid_() == 0u) {
+            R.tokens[t] = tok;
+            if (R.scores != nullptr) R.scores[t] = score;
+        }
+        if (tid_() < HID / 8u) ((uint4 *)hres)[tid_()] = embed8<QE>(R.M->emb, R.M->embs, tok, tid_());
+        __syncthreads();
+    } else {
+        if (!gather<(PH + NT - 1u) / NT>(R, R.pk + off_h(l - 1u), PH, PH, tag, W_QKV, (u32)t, [](u32 i) { return i; },
+                       [&](u32 i, uint4 v) { put6(hres + (i / 2u) * DN_ROWS + (i % 2u) * 6u, v, (i % 2u) * 6u, DN_ROWS); })) {
+            return false;
+        }
+    }
+    TLR(2u * (1u + 5u * l));
+    rms_lds(S.hres, nwp, S.xs, S.red);
+    TLD(l, 0u);
+    const float dd = group_sum<G::LPR>(frag_dot<QA, G::LPR, G::J>(F.f, S.xs, G::C, sub));
+    const float da = lane_f(dd, 0), db = lane_f(dd, 32);
+    TLD(l, 1u);
+    if (lane == 0u) {
+        const h16 a = (h16)da, bb = (h16)db;
+        h16 na = a, nb = bb;
+        if (m < 2u) {
+            const float fa2 = (float)a, fb2 = (float)bb;
+            na = (h16)(fa2 * cs - fb2 * sn);
+            nb = (h16)(fa2 * sn + fb2 * cs);
+        }
+        S.outv[w] = na;
+        S.outv[8u + w] = nb;
+        if (m >= 1u) {
+            h16 *cache = (m == 1u ? R.kc : R.vc) + (size_t)l * NHEAD * R.cap * HDIM;
+            const u32 off = ((head * R.cap + slot) * HDIM + d) * 2u;
+            cstore_h16(cache, off, na);
+            cstore_h16(cache, off + 128u, nb);
+        }
+    }
+    __syncthreads();
+    TLD(l, 2u);
+    publish(R, R.pk + off_qkv(l), PQKV, b * PQKV_B, PQKV_B, tag, [&](u32 p) { return pay6(S.outv, p, 16u); });
+    TLR(2u * (1u + 5u * l) + 1u);
+    return true;
+}
+
+/* ---- attention ------------------------------------------------------------ */
+
+constexpr u32 ATT_NG = NT / 16u; /* 16-lane slot groups per block */
+constexpr u32 ATT_PF = 4u;        /* ATT_NG-slot rounds whose K/V are loaded ahead */
+
+struct AttFrags {
+    uint4 k[ATT_PF], v[ATT_PF];
+};
+
+struct AttPlan {
+    u32 i0, i1, cs;
+};
+
+__device__ __forceinline__ AttPlan att_plan(const Run &R, int32_t t) {
+    const u32 a = blockIdx.x - ATT0, s = a % ATT_SPLITS;
+    const u32 live = (u32)min(t + 1, (int32_t)RING);
+    const u32 L = (u32)R.P + live;
+    const u32 chunk = (L + ATT_SPLITS - 1u) / ATT_SPLITS;
+    AttPlan p;
+    p.i0 = min(s * chunk, L);
+    p.i1 = min(L, p.i0 + chunk);
+    p.cs = (u32)(R.P + t % (int32_t)RING);
+    return p;
+}
+
+/* K/V pieces of rounds [u0, u0 + ATT_PF): slot i0 + g + ATT_NG * u, dims 8p..8p+7;
+ * slots past i1 and the current step's slot (taken from the packets) load
+ * slot i0 instead (a cache hit, dropped later). */
+__device__ __forceinline__ void att_load(const Run &R, u32 l, const AttPlan &pl, u32 u0, AttFrags &F) {
+    const u32 a = blockIdx.x - ATT0, head = a / ATT_SPLITS;
+    const u32 g = tid_() / 16u, p = tid_() % 16u;
+    const size_t lay = (size_t)l * NHEAD * R.cap * HDIM + (size_t)head * R.cap * HDIM;
+    const h16 *kb = R.kc + lay, *vb = R.vc + lay;
+#pragma unroll
+    for (u32 u = 0; u < ATT_PF; ++u) {
+        u32 slot = pl.i0 + g + ATT_NG * (u0 + u);
+        slot = slot < pl.i1 && slot != pl.cs ? slot : (pl.i1 > pl.i0 ? pl.i0 : 0u);
+        F.k[u] = cload16(kb, (slot * HDIM + 8u * p) * 2u);
+        F.v[u] = cload16(vb, (slot * HDIM + 8u * p) * 2u);
+    }
+}
+
+/* Split (head, s) of the attention over slots [i0, i1): online softmax per
+ * 16-lane slot group, merged over the block's 16 groups; publishes the
+ * normalised accumulator (f16) and (max, sum) (fp32). */
+__device__ bool att_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, AttFrags &F) {
+    const u32 b = blockIdx.x;
+    if (b < ATT0) return true;
+    const u32 a = b - ATT0, head = a / ATT_SPLITS;
+    const u32 g = tid_() / 16u, p = tid_() % 16u;
+    const AttPlan pl = att_plan(R, t);
+    h16 *qn = (h16 *)S.scr, *kn = qn + HDIM, *vn = kn + HDIM; /* [3][128] */
+    if (!gather<1>(R, R.pk + off_qkv(l), PQKV, 24u * PQKV_B, tag, W_ATT, (u32)t,
+                   [&](u32 i) { return head * 24u * PQKV_B + i; },
+                   [&](u32 i, uint4 v) {
+                       const u32 blk = i / PQKV_B, k = i % PQKV_B, m = blk / 8u, d0 = (blk % 8u) * 8u;
+                       h16 *dst = m == 0u ? qn : (m == 1u ? kn : vn);
+                       const h16 e[6] = {lo16(v.y), hi16(v.y), lo16(v.z), hi16(v.z), lo16(v.w), hi16(v.w)};
+#pragma unroll
+                       for (u32 j = 0; j < 6u; ++j) {
+                           const u32 idx = 6u * k + j;
+                           if (idx < 16u) dst[idx < 8u ? d0 + idx : d0 + 56u + idx] = e[j];
+                       }
+                   })) {
+        return false;
+    }
+    TLR(2u * (2u + 5u * l));
+    union h8 {
+        uint4 u;
+        h16 h[8];
+    };
+    const uint4 qq = ((const uint4 *)qn)[p];
+    const float scale = 0.08838834764831845f; /* 1/sqrt(128) */
+    float m = -INFINITY, lsum = 0.0f, acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    TLD(l, 3u);
+    const u32 nround = (pl.i1 - pl.i0 + ATT_NG - 1u) / ATT_NG;
+#pragma unroll 1
+    for (u32 u0 = 0;; u0 += ATT_PF) {
+        float sc[ATT_PF];
+        float mn = m;
+#pragma unroll
+        for (u32 u = 0; u < ATT_PF; ++u) {
+            const u32 slot = pl.i0 + g + ATT_NG * (u0 + u);
+            if (slot == pl.cs) {
+                F.k[u] = ((const uint4 *)kn)[p];
+                F.v[u] = ((const uint4 *)vn)[p];
+            }
+            float d = dot2(as_h2(qq.x), F.k[u].x, 0.0f);
+            d = dot2(as_h2(qq.y), F.k[u].y, d);
+            d = dot2(as_h2(qq.z), F.k[u].z, d);
+            d = dot2(as_h2(qq.w), F.k[u].w, d);
+            sc[u] = slot < pl.i1 ? row16_sum(d) * scale : -INFINITY;
+            mn = fmaxf(mn, sc[u]);
+        }
+        if (mn != -INFINITY) {
+            const float corr = fexp(m - mn);
+            lsum *= corr;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] *= corr;
+#pragma unroll
+            for (u32 u = 0; u < ATT_PF; ++u) {
+                const float e = fexp(sc[u] - mn);
+                lsum += e;
+                h8 vv;
+                vv.u = F.v[u];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = fmaf(e, (float)vv.h[j], acc[j]);
+            }
+            m = mn;
+        }
+        if (u0 + ATT_PF >= nround) break;
+        att_load(R, l, pl, u0 + ATT_PF, F);
+    }
+    TLD(l, 4u);
+    /* merge: the wave's four slot groups (lanes p, p+16, p+32, p+48 hold the
+     * same dims) in registers, then the block's waves through LDS */
+    constexpr u32 NWV = NT / 64u;
+    float *gm = (float *)(S.scr + 3u * HDIM * 2u), *gl = gm + NWV, *gacc = gl + NWV; /* gacc [NWV][128] */
+    {
+        float Mw = fmaxf(m, __shfl_xor(m, 16));
+        Mw = fmaxf(Mw, __shfl_xor(Mw, 32));
+        const float f = m == -INFINITY ? 0.0f : fexp(m - Mw);
+        lsum *= f;
+        lsum += __shfl_xor(lsum, 16);
+        lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            acc[j] *= f;
+            acc[j] += __shfl_xor(acc[j], 16);
+            acc[j] += __shfl_xor(acc[j], 32);
+        }
+        const u32 wv = tid_() >> 6;
+        if ((tid_() & 63u) < 16u) {
+            if (p == 0u) {
+                gm[wv] = Mw;
+                gl[wv] = lsum;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) gacc[wv * HDIM + 8u * p + j] = acc[j];
+        }
+    }
+    __syncthreads();
+    h16 *outa = (h16 *)(gacc + NWV * HDIM);
+    float *mlo = (float *)(outa + 132);
+    if (tid_() < HDIM) {
+        const u32 d = tid_();
+        float M = -INFINITY;
+#pragma unroll
+        for (u32 k = 0; k < NWV; ++k) M = fmaxf(M, gm[k]);
+        float Ls = 0.0f, A = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (u32 k = 0; k < NWV; ++k) {
+                const float f = fexp(gm[k] - M);
+                Ls = fmaf(gl[k], f, Ls);
+                A = fmaf(gacc[k * HDIM + d], f, A);
+            }
+        }
+        outa[d] = (h16)(Ls > 0.0f ? A * frcp(Ls) : 0.0f);
+        if (d == 0u) {
+            mlo[0] = M;
+            mlo[1] = Ls;
+        }
+    }
+    __syncthreads();
+    TLD(l, 5u);
+    publish(R, R.pk + off_att(l), PATT, a * PATT_B, PATT_B, tag, [&](u32 q) {
+        return q < PATT_B - 1u ? pay6(outa, q, HDIM) : make_uint3(__float_as_uint(mlo[0]), __float_as_uint(mlo[1]), 0u);
+    });
+    TLR(2u * (2u + 5u * l) + 1u);
+    return true;
+}
+
+/* ---- O projection + router fold -------------------------------------------- */
+
+template <int QA>
+struct OCfg {
+    static constexpr u32 C = chunks_per_row<QA>(HID), LPR = 32u, J = (C + LPR - 1u) / LPR;
+    static constexpr u32 NG = NT / LPR, RPG = O_ROWS / NG;
+    static constexpr u32 ZR = O_ROWS / (NT / 64u); /* rows per thread in the z partial */
+    static_assert(RPG * NG == O_ROWS && ZR * (NT / 64u) == O_ROWS, "O rows per group");
+};
+
+template <int QA>
+struct OFrags {
+    RowFrag<OCfg<QA>::J> f[OCfg<QA>::RPG];
+    float fw[OCfg<QA>::ZR];
+};
+
+template <int QA>
+__device__ __forceinline__ void o_load(const Run &R, u32 l, OFrags<QA> &F) {
+    typedef OCfg<QA> G;
+    const u32 b = blockIdx.x;
+    if (b < O0 || b >= O0 + O_BLOCKS) return;
+    const AS4 RunLayerD &L = R.M->L[l];
+    const u32 j = b - O0, g = tid_() / 32u, sub = tid_() % 32u;
+#pragma unroll
+    for (u32 k = 0; k < G::RPG; ++k) {
+        const u32 r = j * O_ROWS + g * G::RPG + k;
+        frag_load<QA, G::LPR, G::J>(F.f[k], gp<uint8_t>(L.o) + (size_t)r * 16u * G::C, H(L.os) + (size_t)r * (HID / 64u),
+                                    G::C, sub);
+    }
+    if (l > 0u) {
+        const u32 e = tid_() % 64u, q = tid_() / 64u;
+#pragma unroll
+        for (u32 k = 0; k < G::ZR; ++k) F.fw[k] = gp<float>(L.fold)[(size_t)(j * O_ROWS + G::ZR * q + k) * NEXP + e];
+    }
+}
+
+template <int QA>
+__device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, OFrags<QA> &F) {
+    typedef OCfg<QA> G;
+    const u32 b = blockIdx.x;
+    if (b < O0 || b >= O0 + O_BLOCKS) return true;
+    const u32 j = b - O0, g = tid_() / 32u, sub = tid_() % 32u;
+    h16 *accp = (h16 *)S.scr;                           /* [80][128] */
+    float *ml = (float *)(S.scr + ATT_BLOCKS * HDIM * 2u); /* [80][2] */
+    float *wk = ml + 2u * ATT_BLOCKS;                     /* [80] */
+    float *zq = wk + ATT_BLOCKS;                          /* [NT / 64][64] */
+    if (!gather<(PATT + NT - 1) / NT>(R, R.pk + off_att(l), PATT, PATT, tag, W_O, (u32)t, [](u32 i) { return i; },
+                                      [&](u32 i, uint4 v) {
+                                          const u32 a = i / PATT_B, k = i % PATT_B;
+                                          if (k < PATT_B - 1u) {
+                                              put6(accp + a * HDIM + 6u * k, v, 6u * k, HDIM);
+                                          } else {
+                                              ml[2u * a] = __uint_as_float(v.y);
+                                              ml[2u * a + 1u] = __uint_as_float(v.z);
+                                          }
+                                      })) {
+        return false;
+    }
+    TLR(2u * (3u + 5u * l));
+    /* merge weights: lanes 8h..8h+7 hold the splits of head h (the same
+     * arithmetic as k_attn_out's merge) */
+    if (tid_() < ATT_BLOCKS) {
+        const float mk = ml[2u * tid_()], lk = ml[2u * tid_() + 1u];
+        float M = mk;
+#pragma unroll
+        for (u32 o = 1; o < ATT_SPLITS; o <<= 1) M = fmaxf(M, __shfl_xor(M, (int)o));
+        const float lf = mk == -INFINITY ? 0.0f : lk * fexp(mk - M);
+        wk[tid_()] = lf * frcp(group_sum<ATT_SPLITS>(lf));
+    }
+    __syncthreads();
+    TLD(l, 6u);
+    if (tid_() < HID / 8u) {
+        const u32 hh = tid_() / (HDIM / 8u), d8 = tid_() % (HDIM / 8u);
+        float acc[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+#pragma unroll
+        for (u32 s = 0; s < ATT_SPLITS; ++s) {
+            const float w = wk[hh * ATT_SPLITS + s];
+            const uint4 u = ((const uint4 *)(accp + (hh * ATT_SPLITS + s) * HDIM))[d8];
+            const u32 uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc[2 * q] = fmaf((float)lo16(uu[q]), w, acc[2 * q]);
+                acc[2 * q + 1] = fmaf((float)hi16(uu[q]), w, acc[2 * q + 1]);
+            }
+        }
+        h16x2 r[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r[q] = h16x2{(h16)acc[2 * q], (h16)acc[2 * q + 1]};
+        ((uint4 *)S.xs)[tid_()] = __builtin_bit_cast(uint4, r);
+    }
+    __syncthreads();
+    TLD(l, 7u);
+#pragma unroll
+    for (u32 k = 0; k < G::RPG; ++k) {
+        const u32 rl = g * G::RPG + k, r = j * O_ROWS + rl;
+        const float d = group_sum<G::LPR>(frag_dot<QA, G::LPR, G::J>(F.f[k], S.xs, G::C, sub));
+        if (sub == 0u) S.outv[rl] = (h16)(d + (float)S.hres[r]);
+    }
+    __syncthreads();
+    TLD(l, 8u);
+    const bool moe = l > 0u;
+    if (moe) {
+        const u32 e = tid_() % 64u, q = tid_() / 64u;
+        float z = 0.0f;
+#pragma unroll
+        for (u32 k = 0; k < G::ZR; ++k) z = fmaf(F.fw[k], (float)S.outv[G::ZR * q + k], z);
+        zq[q * 64u + e] = z;
+        __syncthreads();
+        if (tid_() < 64u) {
+            const u32 e2 = tid_();
+            float zs = 0.0f;
+#pragma unroll
+            for (u32 k = 0; k < NT / 64u; ++k) zs += zq[k * 64u + e2];
+            S.zout[e2] = zs;
+        }
+        __syncthreads();
+    }
+    publish(R, R.pk + off_o(l), PO, j * PO_B, moe ? PO_B : PO_A, tag, [&](u32 p) {
+        if (p < PO_A) return pay6(S.outv, p, O_ROWS);
+        const u32 z0 = 3u * (p - PO_A);
+        return make_uint3(__float_as_uint(S.zout[z0]), __float_as_uint(z0 + 1u < NEXP ? S.zout[z0 + 1u] : 0.0f),
+                          __float_as_uint(z0 + 2u < NEXP ? S.zout[z0 + 2u] : 0.0f));
+    });
+    TLR(2u * (3u + 5u * l) + 1u);
+    return true;
+}
+
+/* ---- gate/up (dense layer 0, routed + shared experts) -------------------- */
+
+template <int QF>
+struct GuCfg {
+    static constexpr u32 C = chunks_per_row<QF>(HID);
+    static constexpr u32 LPR = 16u;
+    static constexpr u32 J = (C + LPR - 1u) / LPR;
+    static constexpr u32 NG = NT / LPR;                 /* lane groups */
+    static constexpr u32 RPG = (GU_ROWS + NG - 1u) / NG; /* row pairs per group */
+};
+
+template <int QF>
+struct GuFrags {
+    RowFrag<GuCfg<QF>::J> g[GuCfg<QF>::RPG], u[GuCfg<QF>::RPG];
+};
+
+template <int QF, bool NTL>
+__device__ __forceinline__ void gu_rows(GuFrags<QF> &F, const uint8_t *GW, const h16 *GS, const uint8_t *UW,
+                                        const h16 *US, u32 row0, u32 nrows, u32 maxrow) {
+    typedef GuCfg<QF> G;
+    const u32 grp = tid_() / G::LPR, sub = tid_() % G::LPR;
+#pragma unroll
+    for (u32 k = 0; k < G::RPG; ++k) {
+        const u32 r = row0 + min(grp + k * G::NG, nrows - 1u);
+        const u32 rr = min(r, maxrow - 1u);
+        frag_load<QF, G::LPR, G::J, NTL>(F.g[k], GW + (size_t)rr * 16u * G::C, GS + (size_t)rr * (HID / 64u), G::C, sub);
+        frag_load<QF, G::LPR, G::J, NTL>(F.u[k], UW + (size_t)rr * 16u * G::C, US + (size_t)rr * (HID / 64u), G::C, sub);
+    }
+}
+
+/* Loads that do not depend on the router: dense rows (layer 0) or the
+ * shared experts' rows (blocks >= GU_ROUTED). */
+template <int QF>
+__device__ __forceinline__ void gu_load_static(const Run &R, u32 l, GuFrags<QF> &F) {
+    const AS4 RunLayerD &L = R.M->L[l];
+    const u32 b = blockIdx.x;
+    if (l == 0u) {
+        gu_rows<QF, false>(F, gp<uint8_t>(L.gate), H(L.gs), gp<uint8_t>(L.up), H(L.us), b * DGU_ROWS,
+                           min(DGU_ROWS, DI - min(b * DGU_ROWS, DI - 1u)), DI);
+    } else if (b >= GU_ROUTED) {
+        gu_rows<QF, false>(F, gp<uint8_t>(L.sg), H(L.sgs), gp<uint8_t>(L.su), H(L.sus), (b - GU_ROUTED) * GU_ROWS,
+                           GU_ROWS, SI);
+    }
+}
+
+/* DN rows: wavefront w of block b owns output row 8b + w.  Its chunks are
+ * one list, the 6 routed experts' rows (CR chunks each) then the shared
+ * expert's row (CS chunks); lane l holds chunks l, l + 64, ... */
+template <int QF>
+struct DnCfg {
+    static constexpr u32 CR = chunks_per_row<QF>(EI), CS = chunks_per_row<QF>(SI), CT = TOPK * CR + CS;
+    static constexpr u32 J = (CT + 63u) / 64u;
+    static constexpr u32 CD = chunks_per_row<QF>(DI), JD = (CD + 63u) / 64u;
+};
+static_assert(NT / 64u == DN_ROWS, "DN: one output row per wavefront");
+
+template <int QF>
+struct DnFrags {
+    RowFrag<DnCfg<QF>::J> f;
+};
+
+template <int QF>
+struct DdFrags {
+    RowFrag<DnCfg<QF>::JD> f;
+};
+
+__device__ __forceinline__ u32 dn_row() {
+    return blockIdx.x * DN_ROWS + (tid_() >> 6);
+}
+
+/* Routed down rows of the selected experts (ids in LDS) and the shared down row. */
+template <int QF>
+__device__ __forceinline__ void dn_load(const Run &R, const Lds &S, u32 l, DnFrags<QF> &F) {
+    typedef DnCfg<QF> G;
+    if (blockIdx.x >= DN_BLOCKS) return;
+    const AS4 RunLayerD &L = R.M->L[l];
+    const u32 c = dn_row(), lane = tid_() & 63u;
+    constexpr u32 CPG = chunks_per_group<QF>();
+#pragma unroll
+    for (u32 j = 0; j < G::J; ++j) {
+        const u32 q = min(lane + 64u * j, G::CT - 1u);
+        if (q < TOPK * G::CR) {
+            const u32 r = q / G::CR, cc = q % G::CR, e = S.selid[r];
+            const uint8_t *W = gp<uint8_t>(L.ed) + e * L.dn_w_stride + (size_t)c * 16u * G::CR + 16u * cc;
+            F.f.w[j] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4v *)W));
+            if (QF != 1) F.f.s[j] = __builtin_nontemporal_load(H(L.eds) + e * L.dn_s_stride + (size_t)c * (EI / 64u) + cc / CPG);
+        } else {
+            const u32 cc = q - TOPK * G::CR;
+            F.f.w[j] = *(const uint4 *)(gp<uint8_t>(L.sd) + (size_t)c * 16u * G::CS + 16u * cc);
+            if (QF != 1) F.f.s[j] = H(L.sds)[(size_t)c * (SI / 64u) + cc / CPG];
+        }
+    }
+}
+
+template <int QF>
+__device__ __forceinline__ void dd_load(const Run &R, DdFrags<QF> &F) {
+    typedef DnCfg<QF> G;
+    if (blockIdx.x >= DN_BLOCKS) return;
+    const AS4 RunLayerD &L = R.M->L[0];
+    const u32 c = dn_row(), sub = tid_() & 63u;
+    frag_load<QF, 64u, G::JD>(F.f, gp<uint8_t>(L.down) + (size_t)c * 16u * G::CD, H(L.ds) + (size_t)c * (DI / 64u),
+                              G::CD, sub);
+}
+
+/* GU stage: gathers the O outputs (a, and the z partials in MoE layers),
+ * normalises a, selects the experts (MoE), and computes the block's mids.
+ * MoE layers also issue the DN stage's loads (dn) once the experts are known. */
+template <int QF>
+__device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, GuFrags<QF> &F, DnFrags<QF> &dn) {
+    typedef GuCfg<QF> G;
+    const AS4 RunLayerD &L = R.M->L[l];
+    const u32 b = blockIdx.x, grp = tid_() / G::LPR, sub = tid_() % G::LPR;
+    const bool moe = l > 0u;
+    float *zpart = (float *)S.scr; /* [40][64] */
+    h16 *hres = S.hres;
+    const u32 n = moe ? PO : O_BLOCKS * PO_A;
+    const uint4 nwp = norm_piece(L.post_norm);
+    if (!gather<(PO + NT - 1) / NT>(
+            R, R.pk + off_o(l), PO, n, tag, W_GU, (u32)t,
+            [&](u32 i) { return moe ? i : (i / PO_A) * PO_B + i % PO_A; },
+            [&](u32 i, uint4 v) {
+                const u32 j = moe ? i / PO_B : i / PO_A, k = moe ? i % PO_B : i % PO_A;
+                if (k < PO_A) {
+                    put6(hres + j * O_ROWS + 6u * k, v, 6u * k, O_ROWS);
+                } else {
+                    const u32 z0 = 3u * (k - PO_A);
+                    float *zp = zpart + j * NEXP + z0;
+                    zp[0] = __uint_as_float(v.y);
+                    if (z0 + 1u < NEXP) zp[1] = __uint_as_float(v.z);
+                    if (z0 + 2u < NEXP) zp[2] = __uint_as_float(v.w);
+                }
+            }, O_BLOCKS, PO_B, moe ? 0u : PO_A - PO_B)) {
+        return false;
+    }
+    TLR(2u * (4u + 5u * l));
+    float inv;
+    if (moe) {
+        /* wavefront 0: z in a fixed order over the O blocks, then the top-6
+         * on z (softmax is monotone and inv_rms > 0, so z orders the experts
+         * as the probabilities do); the expert loads are issued before the
+         * norm of a */
+        /* z partial sums: thread (e, q) adds blocks q*5 .. q*5+4 of expert e,
+         * then wavefront 0 adds the 8 sums, both in a fixed order */
+        constexpr u32 ZQ = NT / 64u, ZB = O_BLOCKS / ZQ;
+        static_assert(ZB * ZQ == O_BLOCKS, "z partials split evenly");
+        float *zsum = zpart + O_BLOCKS * NEXP; /* [ZQ][64] */
+        {
+            const u32 e = tid_() % 64u, q = tid_() / 64u;
+            float zz = 0.0f;
+#pragma unroll
+            for (u32 j = 0; j < ZB; ++j) zz += zpart[(q * ZB + j) * NEXP + e];
+            zsum[q * 64u + e] = zz;
+        }
+        __syncthreads();
+        float z = 0.0f;
+        if (tid_() < 64u) {
+            const u32 e = tid_();
+#pragma unroll
+            for (u32 q = 0; q < ZQ; ++q) z += zsum[q * 64u + e];
+            u32 sid[TOPK];
+            topk6_ids(z, sid);
+            if (e < TOPK) {
+#pragma unroll
+                for (u32 k = 0; k < TOPK; ++k) {
+                    if (e == k) S.selid[k] = sid[k] < NEXP ? sid[k] : 0u;
+                }
+            }
+        }
+        __syncthreads();
+        TLD(l, 9u);
+        if (b < GU_ROUTED) {
+            const u32 rank = b / 32u, e = S.selid[rank];
+            gu_rows<QF, true>(F, gp<uint8_t>(L.eg) + e * L.gu_w_stride, H(L.egs) + e * L.gu_s_stride,
+                              gp<uint8_t>(L.eu) + e * L.gu_w_stride, H(L.eus) + e * L.gu_s_stride, (b % 32u) * GU_ROWS,
+                              GU_ROWS, EI);
+        }
+        TLD(l, 10u);
+        inv = rms_lds(S.hres, nwp, S.xs, S.red);
+        if (tid_() < 64u) {
+            /* the selection's probabilities: softmax of z * inv_rms (raw, no
+             * renormalisation; max-subtracted) */
+            const float lg = z * inv;
+            const float mx = wave_max_dpp(lg);
+            const float pe = fexp(lg - mx);
+            const float p = pe * frcp(wave_sum(pe));
+            const u32 t = tid_();
+            const float ps = __shfl(p, (int)S.selid[min(t, TOPK - 1u)]); /* lane t < 6: p of expert selid[t] */
+            if (t < TOPK) S.selw[t] = ps;
+        }
+    } else {
+        inv = rms_lds(S.hres, nwp, S.xs, S.red);
+    }
+    (void)inv;
+    const u32 nrows = moe ? GU_ROWS : min(DGU_ROWS, DI - min(b * DGU_ROWS, DI));
+#pragma unroll
+    for (u32 k = 0; k < G::RPG; ++k) {
+        const u32 r = grp + k * G::NG;
+        const float dg = group_sum<G::LPR>(frag_dot<QF, G::LPR, G::J>(F.g[k], S.xs, G::C, sub));
+        const float du = group_sum<G::LPR>(frag_dot<QF, G::LPR, G::J>(F.u[k], S.xs, G::C, sub));
+        if (sub == 0u && r < nrows) S.outv[r] = (h16)(fsilu(dg) * du);
+    }
+    __syncthreads();
+    TLD(l, 11u);
+    publish(R, R.pk + off_mid(l), PMID, b * PMID_B, PMID_B, tag,
+            [&](u32 p) { return pay6(S.outv, p, moe ? GU_ROWS : nrows); });
+    /* the DN stage's rows of the selected experts, issued once this stage's
+     * own loads are consumed, so the two streams do not share bandwidth on
+     * the critical path */
+    if (moe) dn_load<QF>(R, S, l, dn);
+    TLR(2u * (4u + 5u * l) + 1u);
+    return true;
+}
+
+/* DN stage: gathers the mids; MoE: out = f16(sum_r w_r D_r.mid_r + f16(SD.smid)
+ * + a); layer 0: out = f16(D.mid + a). */
+template <int QF>
+__device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, DnFrags<QF> &dn, DdFrags<QF> &dd) {
+    typedef DnCfg<QF> G;
+    const u32 b = blockIdx.x;
+    if (b >= DN_BLOCKS) return true;
+    const bool moe = l > 0u;
+    const u32 rows_b = moe ? GU_ROWS : DGU_ROWS;
+    const u32 nmid = moe ? TOPK * EI + SI : DI;
+    h16 *mids = (h16 *)S.scr;
+    if (!gather<(PMID + NT - 1u) / NT>(R, R.pk + off_mid(l), PMID, PMID, tag, W_DN, (u32)t, [](u32 i) { return i; },
+                        [&](u32 i, uint4 v) {
+                            const u32 blk = i / PMID_B, k = i % PMID_B, base = blk * rows_b + 6u * k;
+                            if (6u * k < rows_b) put6(mids + base, v, 6u * k, rows_b);
+                            (void)nmid;
+                        }, NB, PMID_B)) {
+        return false;
+    }
+    TLR(2u * (5u + 5u * l));
+    const u32 c = dn_row(), lane = tid_() & 63u, rl = c - b * DN_ROWS;
+    float out;
+    if (moe) {
+        /* routed: sum over chunks of w_r * (scaled chunk dot); the shared
+         * expert's sum kept apart (rounded to fp16 before the combine) */
+        float acc = 0.0f, sh = 0.0f;
+#pragma unroll
+        for (u32 j = 0; j < G::J; ++j) {
+            const u32 q = lane + 64u * j;
+            if (64u * (j + 1u) <= G::CT || q < G::CT) {
+                const u32 qq = min(q, G::CT - 1u);
+                const bool routed = qq < TOPK * G::CR;
+                const u32 r = routed ? qq / G::CR : 0u, cc = routed ? qq % G::CR : qq - TOPK * G::CR;
+                const float d = chunk_dot<QF>(dn.f.w[j], mids + (routed ? r * EI : TOPK * EI), cc);
+                const float v = QF == 1 ? d : d * (float)dn.f.s[j];
+                if (q < G::CT) {
+                    if (routed) {
+                        acc = fmaf(S.selw[r], v, acc);
+                    } else {
+                        sh += v;
+                    }
+                }
+            }
+        }
+        acc = wave_sum(acc);
+        sh = wave_sum(sh);
+        out = acc + (float)(h16)sh + (float)S.hres[c];
+    } else {
+        const float d = wave_sum(frag_dot<QF, 64u, G::JD>(dd.f, mids, G::CD, lane));
+        out = d + (float)S.hres[c];
+    }
+    TLD(l, 12u);
+    if (lane == 0u) S.outv[rl] = (h16)out;
+    __syncthreads();
+    publish(R, R.pk + off_h(l), PH, b * PH_B, PH_B, tag, [&](u32 p) { return pay6(S.outv, p, DN_ROWS); });
+    TLR(2u * (5u + 5u * l) + 1u);
+    return true;
+}
+
+/* ---- the run --------------------------------------------------------------- */
+
+struct RunArgs {
+    const uocr_run_model *M;
+    uint4 *pk;
+    h16 *kc, *vc;
+    u32 cap;
+    int32_t P, t0, n, last;
+    u32 tag0;
+    int32_t *tokens;
+    float *scores;
+};
+
+template <int QA, int QF, int QL, int QE>
+__global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
+    __shared__ __attribute__((aligned(16))) h16 xs[HID];
+    __shared__ __attribute__((aligned(16))) h16 hres[HID];
+    __shared__ __attribute__((aligned(16))) h16 outv[64];
+    __shared__ __attribute__((aligned(16))) uint8_t scr[24576];
+    __shared__ float red[16], zout[64], selw[8];
+    __shared__ u32 selid[8];
+    __shared__ unsigned long long keyw[NT / 64u];
+    Lds S{xs, hres, outv, red, zout, selw, selid, keyw, scr};
+    Run R;
+    R.M = (const AS4 RunModelD *)A.M;
+    R.pk = A.pk;
+    R.ctl = (u32 *)A.pk;
+    R.kc = A.kc;
+    R.vc = A.vc;
+    R.cap = A.cap;
+    R.xcc = (u32)__builtin_amdgcn_s_getreg(20 | (3 << 11)) % NREP; /* HW_REG_XCC_ID */
+    R.P = A.P;
+    R.tokens = A.tokens;
+    R.scores = A.scores;
+    R.tl = nullptr;
+
+    RowFrag<LmCfg<QL>::J> lf[LM_DEPTH];
+#pragma unroll 1
+    for (int32_t i = 0; i < A.n; ++i) {
+        const int32_t t = A.t0 + i;
+        const u32 tag = A.tag0 + (u32)i;
+#ifdef UOCR_RUN_TIMELINE
+        R.tl = t == g_run_tl_step ? g_run_tl : nullptr;
+        TLR(127u);
+#endif
+#pragma unroll
+        for (u32 k = 0; k < LM_DEPTH; ++k) lm_load<QL>(R, lf[k], k);
+        if (!lm_stage<QL>(R, S, tag, tag - 1u, t, lf)) return;
+        if (A.last && i == A.n - 1) {
+            if (blockIdx.x == 0u) {
+                int32_t tok;
+                float score;
+                if (!select_token(R, S, tag, t, tok, score)) return;
+                if (tid_() == 0u) {
+                    R.tokens[t] = tok;
+                    if (R.scores != nullptr) R.scores[t] = score;
+                }
+            }
+            return;
+        }
+#pragma unroll 1
+        for (u32 l = 0; l < UOCR_RUN_LAYERS; ++l) {
+            QkvFrags<QA> qf;
+            qkv_load<QA>(R, l, qf);
+            AttFrags af;
+            if (blockIdx.x >= ATT0) att_load(R, l, att_plan(R, t), 0u, af);
+            if (!qkv_stage<QA, QE>(R, S, l, t, tag, qf)) return;
+            OFrags<QA> of;
+            o_load<QA>(R, l, of);
+            if (!att_stage(R, S, l, t, tag, af)) return;
+            GuFrags<QF> gf;
+            DnFrags<QF> dn;
+            DdFrags<QF> dd;
+            gu_load_static<QF>(R, l, gf);
+            if (!o_stage<QA>(R, S, l, t, tag, of)) return;
+            if (l == 0u) dd_load<QF>(R, dd);
+            if (!gu_stage<QF>(R, S, l, t, tag, gf, dn)) return;
+            if (!dn_stage<QF>(R, S, l, t, tag, dn, dd)) return;
+        }
+    }
+}
+
+/* Layer 11's output slot of h with the given tag (DN packet layout). */
+__global__ __launch_bounds__(NT) void k_run_seed(uint4 *pk, const h16 *__restrict__ h, u32 tag) {
+    const u32 t = blockIdx.x * NT + tid_();
+    if (t >= PH * NREP) return;
+    const u32 p = t % PH, r = t / PH;
+    const u32 base = (p / 2u) * DN_ROWS + (p % 2u) * 6u;
+    h16 e[6];
+#pragma unroll
+    for (u32 j = 0; j < 6u; ++j) e[j] = (p % 2u) * 6u + j < DN_ROWS ? h[base + j] : (h16)0.0f;
+    pk[off_h(UOCR_RUN_LAYERS - 1u) + (u64)r * PH + p] =
+        make_uint4(tag, pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]));
+}
+
+__global__ void k_run_reset(u32 *ctl) {
+    if (tid_() < 64u) ctl[tid_()] = 0u;
+}
+
+template <int QA, int QF, int QL, int QE>
+hipError_t launch_run(hipStream_t st, const RunArgs &a) {
+    void *args[] = {(void *)&a};
+    return hipLaunchCooperativeKernel((const void *)k_decode_run<QA, QF, QL, QE>, dim3(NB), dim3(NT), args, 0, st);
+}
+
+}  // namespace
+
+#ifdef UOCR_RUN_TIMELINE
+/* Records the stage timeline of decode step `step` into buf
+ * (256 x 256 u64, see g_run_tl); NULL stops recording. */
+extern "C" __attribute__((visibility("default"))) int uocr_run_timeline(void *buf, int step) {
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_run_tl), &buf, sizeof(buf)) != hipSuccess) return -1;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_run_tl_step), &step, sizeof(step)) != hipSuccess) return -1;
+    return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}
+#endif
+
+extern "C" uint64_t uocr_run_arena_bytes(void) {
+    return ARENA_PK * 16u;
+}
+
+extern "C" int uocr_run_supported(const uocr_run_model *m) {
+    if (m == nullptr) return 0;
+    return m->qa == UOCR_QT_Q8 && m->ql == m->qf && m->qe == m->qf && (m->qf == UOCR_QT_Q4 || m->qf == UOCR_QT_Q8);
+}
+
+extern "C" hipError_t uocr_run_seed(hipStream_t st, void *arena, const uint16_t *h, uint32_t tag) {
+    if (arena == nullptr || h == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_run_seed, dim3((PH * NREP + NT - 1u) / NT), dim3(NT), 0, st, (uint4 *)arena, (const h16 *)h, tag);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_run_reset(hipStream_t st, void *arena) {
+    if (arena == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_run_reset, dim3(1), dim3(64), 0, st, (u32 *)arena);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_run_launch(hipStream_t st, const uocr_run_model *model, const uocr_run_model *host_model,
+                                      void *arena, uint16_t *kc, uint16_t *vc, uint32_t cap, int32_t P, int32_t t0,
+                                      int32_t n, int last, uint32_t tag0, int32_t *tokens, float *scores) {
+    if (model == nullptr || host_model == nullptr || arena == nullptr || kc == nullptr || vc == nullptr ||
+        tokens == nullptr || n <= 0 || n > (int32_t)UOCR_RUN_MAX_STEPS || P <= 0 || t0 < 0 ||
+        cap < (uint32_t)P + RING || !uocr_run_supported(host_model)) {
+        return hipErrorInvalidValue;
+    }
+    /* byte offsets of one layer's cache fit the 32-bit buffer offsets */
+    if ((uint64_t)NHEAD * cap * HDIM * 2u >= (1ull << 31)) return hipErrorInvalidValue;
+    RunArgs a;
+    a.M = model;
+    a.pk = (uint4 *)arena;
+    a.kc = (h16 *)kc;
+    a.vc = (h16 *)vc;
+    a.cap = cap;
+    a.P = P;
+    a.t0 = t0;
+    a.n = n;
+    a.last = last;
+    a.tag0 = tag0;
+    a.tokens = tokens;
+    a.scores = scores;
+    if (host_model->qf == UOCR_QT_Q4) return launch_run<3, 4, 4, 4>(st, a);
+    return launch_run<3, 3, 3, 3>(st, a);
+}

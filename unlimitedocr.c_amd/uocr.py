@@ -36,7 +36,7 @@ UOCR_PROFILE_MAX_EVENTS = 256
 
 QT_F16, QT_Q8, QT_Q4 = 1, 3, 4
 QPROFILE_FP16, QPROFILE_Q8, QPROFILE_Q4 = 1, 2, 3
-GEN_IGNORE_EOS, GEN_NO_GRAPH, GEN_TOKEN_PREFILL = 1, 2, 4
+GEN_IGNORE_EOS, GEN_NO_GRAPH, GEN_TOKEN_PREFILL, GEN_NO_RUN = 1, 2, 4, 8
 
 HIDDEN, VOCAB, HEADS, HEAD_DIM = 1280, 129280, 10, 128
 TOKEN_BOS, TOKEN_EOS, TOKEN_IMAGE = 0, 1, 128815
