@@ -719,48 +719,55 @@ __device__ bool att_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag,
         att_load(R, l, pl, u0 + ATT_PF, F);
     }
     TLD(l, 4u);
-    /* merge: the wave's four slot groups (lanes p, p+16, p+32, p+48 hold the
-     * same dims) in registers, then the block's waves through LDS */
-    constexpr u32 NWV = NT / 64u;
-    float *gm = (float *)(S.scr + 3u * HDIM * 2u), *gl = gm + NWV, *gacc = gl + NWV; /* gacc [NWV][128] */
+    /* merge of the ATT_NG slot groups through LDS in two levels: thread
+     * (d, k) merges groups 8k..8k+7 for dim d, then threads d < 128 merge
+     * the NT / 128 results */
+    constexpr u32 GPK = 8u, NK = ATT_NG / GPK;
+    static_assert(NK * HDIM == NT, "ATT merge: one (dim, part) per thread");
+    float *gm = (float *)(S.scr + 3u * HDIM * 2u), *gl = gm + ATT_NG, *gacc = gl + ATT_NG; /* gacc [ATT_NG][128] */
+    float *pm = gacc + ATT_NG * HDIM, *psum = pm + NK, *pacc = psum + NK;                 /* pacc [NK][128] */
+    if (p == 0u) {
+        gm[g] = m;
+        gl[g] = lsum;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gacc[g * HDIM + 8u * p + j] = acc[j];
+    __syncthreads();
     {
-        float Mw = fmaxf(m, __shfl_xor(m, 16));
-        Mw = fmaxf(Mw, __shfl_xor(Mw, 32));
-        const float f = m == -INFINITY ? 0.0f : fexp(m - Mw);
-        lsum *= f;
-        lsum += __shfl_xor(lsum, 16);
-        lsum += __shfl_xor(lsum, 32);
+        const u32 d = tid_() % HDIM, k = tid_() / HDIM;
+        float M = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            acc[j] *= f;
-            acc[j] += __shfl_xor(acc[j], 16);
-            acc[j] += __shfl_xor(acc[j], 32);
-        }
-        const u32 wv = tid_() >> 6;
-        if ((tid_() & 63u) < 16u) {
-            if (p == 0u) {
-                gm[wv] = Mw;
-                gl[wv] = lsum;
+        for (u32 q = 0; q < GPK; ++q) M = fmaxf(M, gm[k * GPK + q]);
+        float Ls = 0.0f, A = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (u32 q = 0; q < GPK; ++q) {
+                const float f = fexp(gm[k * GPK + q] - M);
+                Ls = fmaf(gl[k * GPK + q], f, Ls);
+                A = fmaf(gacc[(k * GPK + q) * HDIM + d], f, A);
             }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) gacc[wv * HDIM + 8u * p + j] = acc[j];
+        }
+        pacc[k * HDIM + d] = A;
+        if (d == 0u) {
+            pm[k] = M;
+            psum[k] = Ls;
         }
     }
     __syncthreads();
-    h16 *outa = (h16 *)(gacc + NWV * HDIM);
+    h16 *outa = (h16 *)(pacc + NK * HDIM);
     float *mlo = (float *)(outa + 132);
     if (tid_() < HDIM) {
         const u32 d = tid_();
         float M = -INFINITY;
 #pragma unroll
-        for (u32 k = 0; k < NWV; ++k) M = fmaxf(M, gm[k]);
+        for (u32 k = 0; k < NK; ++k) M = fmaxf(M, pm[k]);
         float Ls = 0.0f, A = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (u32 k = 0; k < NWV; ++k) {
-                const float f = fexp(gm[k] - M);
-                Ls = fmaf(gl[k], f, Ls);
-                A = fmaf(gacc[k * HDIM + d], f, A);
+            for (u32 k = 0; k < NK; ++k) {
+                const float f = pm[k] == -INFINITY ? 0.0f : fexp(pm[k] - M);
+                Ls = fmaf(psum[k], f, Ls);
+                A = fmaf(pacc[k * HDIM + d], f, A);
             }
         }
         outa[d] = (h16)(Ls > 0.0f ? A * frcp(Ls) : 0.0f);
