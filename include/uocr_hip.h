@@ -225,6 +225,22 @@ UOCR_API size_t uocr_op_moe_rows_workspace_bytes(uint32_t rows);
 UOCR_API int uocr_op_moe_ffn_rows(const uocr_op_moe_weights *m, const void *x, const void *norm_w,
                                   const void *residual, uint32_t rows, int norm_topk, void *workspace, void *out);
 
+/* Maximum rows of uocr_op_moe_ffn_rows_static. */
+#define UOCR_OP_STATIC_MAX_ROWS 64u
+
+/* uocr_op_moe_ffn_rows without a workspace argument and without any device
+ * allocation: the workspace is a file-scope device array of the library
+ * (3,235,840 bytes: UOCR_OP_STATIC_MAX_ROWS rows), which every GPU the
+ * library runs on holds until the process ends.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Rejects
+ * rows > UOCR_OP_STATIC_MAX_ROWS with UOCR_ERROR_INVALID_ARGUMENT.  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * race.  The array needs no clearing (the expert buckets are rebuilt on
+ * every call) and keeps the last call's contents. */
+UOCR_API int uocr_op_moe_ffn_rows_static(const uocr_op_moe_weights *m, const void *x, const void *norm_w,
+                                         const void *residual, uint32_t rows, int norm_topk, void *out);
+
 /* ---- 3. device plumbing ---------------------------------------------------- */
 UOCR_API int uocr_hip_device_count(void);
 /* Device memory on the library's device, zero-filled (a fresh operator

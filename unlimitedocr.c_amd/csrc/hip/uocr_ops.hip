@@ -21,13 +21,18 @@ hipEvent_t g_ev0 = nullptr, g_ev1 = nullptr;
 hipGraph_t g_graph = nullptr;
 hipGraphExec_t g_graph_exec = nullptr;
 hipError_t g_init_error = hipSuccess;
+void *g_scratch_dev = nullptr; /* device address of `scratch` on device 0 */
+hipError_t g_scratch_err = hipSuccess;
 thread_local char g_err[512] = "OK";
+
+void take_scratch_address();
 
 void init_stream() {
     g_init_error = hipSetDevice(0);
     if (g_init_error == hipSuccess) g_init_error = hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking);
     if (g_init_error == hipSuccess) g_init_error = hipEventCreate(&g_ev0);
     if (g_init_error == hipSuccess) g_init_error = hipEventCreate(&g_ev1);
+    if (g_init_error == hipSuccess) take_scratch_address();
 }
 
 int op_fail(int status, const char *fmt, ...) {
@@ -379,9 +384,10 @@ extern "C" int uocr_op_prefill_attention(const void *q, const void *k_cache, con
 namespace {
 /* workspace layout of uocr_op_moe_ffn_rows for P rows */
 struct MoeRowsWs {
-    size_t xn, logits, ids, wts, offsets, te, ts0, ts1, nt, ltok, lpair, smid, sout, rmid, y, total;
-    uint32_t max_tiles;
-    explicit MoeRowsWs(size_t P) {
+    size_t xn = 0, logits = 0, ids = 0, wts = 0, offsets = 0, te = 0, ts0 = 0, ts1 = 0, nt = 0, ltok = 0, lpair = 0,
+           smid = 0, sout = 0, rmid = 0, y = 0, total = 0;
+    uint32_t max_tiles = 0;
+    explicit constexpr MoeRowsWs(size_t P) {
         const size_t PK = P * 6u;
         max_tiles = (uint32_t)((PK + 63u) / 64u + 64u);
         size_t o = 0;
@@ -414,13 +420,27 @@ extern "C" size_t uocr_op_moe_rows_workspace_bytes(uint32_t rows) {
     return MoeRowsWs(rows).total;
 }
 
-extern "C" int uocr_op_moe_ffn_rows(const uocr_op_moe_weights *m, const void *x, const void *norm_w,
-                                    const void *residual, uint32_t rows, int norm_topk, void *workspace, void *out) {
-    if (m == nullptr || x == nullptr || residual == nullptr || workspace == nullptr || out == nullptr || rows == 0u ||
-        !qt_ok(m->expert_qtype) || !qt_ok(m->shared_qtype) || m->router == nullptr) {
-        return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid moe_ffn_rows arguments");
-    }
-    STREAM_OR_RETURN(st);
+/* The static scratch of uocr_op_moe_ffn_rows_static: the workspace of
+ * UOCR_OP_STATIC_MAX_ROWS rows in a file-scope device array (each device
+ * holds its own copy until the process ends).  Host code never passes the
+ * array's name to a kernel: it is a host-side stand-in, not a device address.
+ * The device address comes from hipGetSymbolAddress, taken once per device
+ * with that device current (the operator stream runs on device 0: taken in
+ * init_stream). */
+constexpr size_t STATIC_SCRATCH_BYTES = 3235840u;
+static_assert(MoeRowsWs(UOCR_OP_STATIC_MAX_ROWS).total <= STATIC_SCRATCH_BYTES, "static scratch holds the maximum rows");
+static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
+
+namespace {
+void take_scratch_address() {
+    void *p = nullptr;
+    g_scratch_err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_dev = g_scratch_err == hipSuccess ? p : nullptr;
+}
+}  // namespace
+
+static int moe_rows(hipStream_t st, const uocr_op_moe_weights *m, const void *x, const void *norm_w,
+                    const void *residual, uint32_t rows, int norm_topk, void *workspace, void *out) {
     const MoeRowsWs L(rows);
     uint8_t *b = (uint8_t *)workspace;
     const uint32_t P = rows;
@@ -507,6 +527,35 @@ extern "C" int uocr_op_moe_ffn_rows(const uocr_op_moe_weights *m, const void *x,
                        "combine");
     }
     return r;
+}
+
+extern "C" int uocr_op_moe_ffn_rows(const uocr_op_moe_weights *m, const void *x, const void *norm_w,
+                                    const void *residual, uint32_t rows, int norm_topk, void *workspace, void *out) {
+    if (m == nullptr || x == nullptr || residual == nullptr || workspace == nullptr || out == nullptr || rows == 0u ||
+        !qt_ok(m->expert_qtype) || !qt_ok(m->shared_qtype) || m->router == nullptr) {
+        return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid moe_ffn_rows arguments");
+    }
+    STREAM_OR_RETURN(st);
+    return moe_rows(st, m, x, norm_w, residual, rows, norm_topk, workspace, out);
+}
+
+extern "C" int uocr_op_moe_ffn_rows_static(const uocr_op_moe_weights *m, const void *x, const void *norm_w,
+                                           const void *residual, uint32_t rows, int norm_topk, void *out) {
+    if (m == nullptr || x == nullptr || residual == nullptr || out == nullptr || rows == 0u ||
+        !qt_ok(m->expert_qtype) || !qt_ok(m->shared_qtype) || m->router == nullptr) {
+        return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid moe_ffn_rows_static arguments");
+    }
+    if (rows > UOCR_OP_STATIC_MAX_ROWS) {
+        return op_fail(UOCR_ERROR_INVALID_ARGUMENT,
+                       "moe_ffn_rows_static: %u rows exceed the static scratch's maximum of %u rows (use "
+                       "uocr_op_moe_ffn_rows with a workspace)",
+                       rows, UOCR_OP_STATIC_MAX_ROWS);
+    }
+    STREAM_OR_RETURN(st);
+    if (g_scratch_dev == nullptr) {
+        return op_fail(UOCR_ERROR_INTERNAL, "static scratch address unavailable: %s", hipGetErrorString(g_scratch_err));
+    }
+    return moe_rows(st, m, x, norm_w, residual, rows, norm_topk, g_scratch_dev, out);
 }
 
 /* ---- plumbing -------------------------------------------------------------- */

@@ -137,6 +137,7 @@ SIGNATURES = {
     "uocr_op_prefill_attention": ([_VP, _VP, _VP, _U32, _U32, _VP], ct.c_int),
     "uocr_op_moe_rows_workspace_bytes": ([_U32], _SZ),
     "uocr_op_moe_ffn_rows": ([ct.POINTER(CMoeWeights), _VP, _VP, _VP, _U32, ct.c_int, _VP, _VP], ct.c_int),
+    "uocr_op_moe_ffn_rows_static": ([ct.POINTER(CMoeWeights), _VP, _VP, _VP, _U32, ct.c_int, _VP], ct.c_int),
     "uocr_hip_device_count": ([], ct.c_int),
     "uocr_hip_alloc": ([_SZ], _VP),
     "uocr_hip_free": ([_VP], ct.c_int),
@@ -512,6 +513,16 @@ def moe_rows_workspace(rows: int) -> DeviceBuffer:
 def op_moe_ffn_rows(weights: CMoeWeights, x, norm_w, residual, rows, norm_topk, ws, out) -> None:
     _check_op(load_library().uocr_op_moe_ffn_rows(ct.byref(weights), _p(x), _p(norm_w), _p(residual), rows, norm_topk,
                                                   _p(ws), _p(out)), "op_moe_ffn_rows")
+
+
+STATIC_MAX_ROWS = 64
+
+
+def op_moe_ffn_rows_static(weights: CMoeWeights, x, norm_w, residual, rows, norm_topk, out) -> None:
+    """uocr_op_moe_ffn_rows on the library's static scratch (no workspace, no
+    device allocation; rows <= STATIC_MAX_ROWS)."""
+    _check_op(load_library().uocr_op_moe_ffn_rows_static(ct.byref(weights), _p(x), _p(norm_w), _p(residual), rows,
+                                                         norm_topk, _p(out)), "op_moe_ffn_rows_static")
 
 
 class Timer:
