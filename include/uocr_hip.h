@@ -249,7 +249,7 @@ UOCR_API void *uocr_hip_alloc(size_t bytes);
 UOCR_API int uocr_hip_free(void *p);
 UOCR_API int uocr_hip_upload(void *dst, const void *src, size_t bytes);
 UOCR_API int uocr_hip_download(void *dst, const void *src, size_t bytes);
-UOCR_API int uocr_hip_memset(void *dst, int value, size_t bytes);
+UOCR_API int uocr_hip_memset(void *dst, int value, size_t bytes); /* refused (INVALID_ARGUMENT) while capturing */
 UOCR_API int uocr_hip_copy(void *dst, const void *src, size_t bytes); /* device to device, on the operator stream */
 UOCR_API int uocr_hip_sync(void);
 UOCR_API const char *uocr_hip_op_error(void);

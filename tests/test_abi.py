@@ -46,12 +46,62 @@ def test_status_and_category_strings(uocr):
     assert lib.uocr_memory_category_name(99) == b"unknown"
 
 
-def test_struct_layouts_match_reference(uocr):
-    assert ct.sizeof(uocr.CEngineOpts) == 56  # sizeof(uocr_engine_opts) of the reference header
-    assert ct.sizeof(uocr.CPreparedRequest) == 48
-    assert ct.sizeof(uocr.CMemoryReport) == 8 * (20 + 19)
-    assert ct.sizeof(uocr.CProfileEvent) == 96
-    assert ct.sizeof(uocr.CProfileReport) == 24984
+_PUBLIC_STRUCTS = {"uocr_profile_event": "CProfileEvent", "uocr_memory_report": "CMemoryReport",
+                   "uocr_profile_report": "CProfileReport", "uocr_image_view": "CImageView",
+                   "uocr_prepared_request": "CPreparedRequest", "uocr_engine_opts": "CEngineOpts"}
+
+
+def _struct_fields(header: str) -> dict[str, list[str]]:
+    """Field names of every public struct of unlimitedocr.h, in order."""
+    import re
+    text = re.sub(r"/\*.*?\*/", "", Path(header).read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"typedef\s+struct\s+(\w+)\s*\{(.*?)\}\s*\1\s*;", text, flags=re.S):
+        names = []
+        for decl in m.group(2).split(";"):
+            decl = decl.strip()
+            if decl:
+                names.append(re.findall(r"(\w+)\s*(?:\[[^\]]*\])?\s*$", decl)[0])
+        out[m.group(1)] = names
+    return out
+
+
+def _layout(include_dir: str, fields: dict[str, list[str]], tmp: Path) -> dict[str, list[int]]:
+    """sizeof and offsetof of every field, compiled by gcc against the
+    unlimitedocr.h in include_dir."""
+    import subprocess
+    lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "unlimitedocr.h"', "int main(void) {"]
+    for st, names in fields.items():
+        lines.append(f'printf("{st} %zu", sizeof({st}));')
+        for n in names:
+            lines.append(f'printf(" %zu", offsetof({st}, {n}));')
+        lines.append('printf("\\n");')
+    lines += ["return 0;", "}"]
+    src, exe = tmp / "layout.c", tmp / f"layout_{abs(hash(include_dir))}"
+    src.write_text("\n".join(lines))
+    subprocess.run(["gcc", "-std=c11", "-I", include_dir, str(src), "-o", str(exe)], check=True)
+    res = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    return {ln.split()[0]: [int(v) for v in ln.split()[1:]] for ln in res if ln.strip()}
+
+
+def test_struct_layouts_match_reference(uocr, tmp_path):
+    """Every public struct: sizeof and the offset of every field, compiled
+    with offsetof against this build's unlimitedocr.h, equal those compiled
+    against the reference's header (where /root/reference is present) and
+    those of the ctypes mirror in uocr.py."""
+    ours_h = str(ROOT / "include")
+    fields = _struct_fields(ours_h + "/unlimitedocr.h")
+    assert set(_PUBLIC_STRUCTS) <= set(fields), set(_PUBLIC_STRUCTS) - set(fields)
+    ours = _layout(ours_h, fields, tmp_path)
+    ref_h = Path("/root/reference/include")
+    if (ref_h / "unlimitedocr.h").exists():
+        assert _struct_fields(str(ref_h / "unlimitedocr.h")) == fields
+        assert _layout(str(ref_h), fields, tmp_path) == ours
+    for st, cls in _PUBLIC_STRUCTS.items():
+        c = getattr(uocr, cls)
+        assert ct.sizeof(c) == ours[st][0], st
+        assert [f[0] for f in c._fields_] == fields[st], st
+        assert [getattr(c, n).offset for n in fields[st]] == ours[st][1:], st
 
 
 @pytest.fixture(scope="module")

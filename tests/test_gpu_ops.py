@@ -367,6 +367,21 @@ def test_captured_operators_replay_like_eager(gpu, oracle):
         g.release()
 
 
+def test_memset_refused_under_capture(gpu):
+    """uocr_hip_memset called while the operator stream captures a graph is
+    refused (a memset node in a captured graph has given wrong results on
+    replays after the first); outside a capture it still clears."""
+    uocr = gpu
+    buf = uocr.DeviceBuffer.of(np.full(256, 0x3C00, np.uint16))
+    with pytest.raises(RuntimeError, match="capturing"):
+        with uocr.Capture():
+            buf.zero()
+    uocr.Capture().release()
+    buf.zero()
+    uocr.sync()
+    assert not buf.download(np.uint16).any()
+
+
 def test_moe_ffn_512_consecutive_tokens(gpu, oracle):
     """BASELINE config 3 at its stated length: 512 consecutive tokens, a fresh
     hidden per token, through one set of Q4 expert weights (router fp16,

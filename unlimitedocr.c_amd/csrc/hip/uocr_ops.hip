@@ -604,6 +604,14 @@ extern "C" int uocr_hip_download(void *dst, const void *src, size_t bytes) {
 
 extern "C" int uocr_hip_memset(void *dst, int value, size_t bytes) {
     STREAM_OR_RETURN(st);
+    /* a memset recorded into a captured graph has given wrong results on
+     * replays after the first: refuse while the operator stream captures */
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t ce = hipStreamIsCapturing(st, &cs);
+    if (ce != hipSuccess) return hip_status(ce, "memset capture query");
+    if (cs != hipStreamCaptureStatusNone) {
+        return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "memset refused: the operator stream is capturing a graph");
+    }
     return hip_status(hipMemsetAsync(dst, value, bytes, st), "memset");
 }
 
