@@ -313,3 +313,27 @@ def test_config5_prompt_matches_oracle(gpu, oracle):
     assert got.shape == (6,)
     assert margins[0] > 1e-2, "seed gives a first step without a clear winner"
     assert compare_ids(got.tolist(), ref.tolist(), margins.tolist()) >= 1
+
+
+@pytest.mark.parametrize("where,run", [("prefill", "0"), ("decode", "0"), ("decode", "1")])
+def test_hot_path_allocation_fails_the_request(gpu, monkeypatch, where, run):
+    """The hot-path allocation guard (uocr_metal.m:8447-8486 semantics): a
+    device allocation inside the prompt prefill or the decode loop fails the
+    request with UOCR_ERROR_INTERNAL naming the region.  The allocation is
+    forced by the UOCR_HIP_FAULT_ALLOC test hook; without it the same request
+    succeeds (graph path, and the persistent run with UOCR_HIP_RUN=1)."""
+    uocr = gpu
+    m = model(uocr, 3)
+    rng = np.random.default_rng(11)
+    ids, mask, rows = prompt(rng, 8, 4)
+    monkeypatch.setenv("UOCR_HIP_RUN", run)
+    with uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=64, max_gen_tokens=16) as eng:
+        got, _, _, _ = eng.generate_embeddings(ids, mask, rows, max_new_tokens=4, flags=uocr.GEN_IGNORE_EOS)
+        assert got.shape == (4,)
+    monkeypatch.setenv("UOCR_HIP_FAULT_ALLOC", where)
+    with uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=64, max_gen_tokens=16) as eng:
+        with pytest.raises(RuntimeError) as ex:
+            eng.generate_embeddings(ids, mask, rows, max_new_tokens=4, flags=uocr.GEN_IGNORE_EOS)
+        assert ex.value.status == uocr.UOCR_ERROR_INTERNAL
+        assert "allocated device memory" in str(ex.value)
+        assert ("prefill" if where == "prefill" else "decode loop") in str(ex.value)

@@ -118,6 +118,10 @@ struct uocr_hip_ctx {
     int run_ok;                  /* the model, device and environment allow the run */
     uint8_t *run_arena;          /* packet arena, in the runtime arena */
     uint32_t run_tag;            /* next unused packet tag */
+    /* hot-path allocation guard (uocr_metal.m:8447-8486): every device and
+     * pinned allocation of the backend is counted */
+    uint64_t alloc_count, alloc_bytes;
+    int fault_alloc;             /* test hook (UOCR_HIP_FAULT_ALLOC): 1 prefill, 2 decode */
 };
 
 /* Persistent runs need every CU of the device: runs of different engines in
@@ -129,6 +133,51 @@ static std::mutex g_run_mutex;
         const hipError_t e_ = (expr);                                                             \
         if (e_ != hipSuccess) return bfail(err, err_size, "%s: %s", (what), hipGetErrorString(e_)); \
     } while (0)
+
+/* Counted allocations: the hot-path guard compares the counts. */
+static hipError_t counted_malloc(uocr_hip_ctx *c, void **p, size_t bytes) {
+    const hipError_t e = hipMalloc(p, bytes);
+    if (e == hipSuccess) {
+        ++c->alloc_count;
+        c->alloc_bytes += bytes;
+    }
+    return e;
+}
+
+static hipError_t counted_host_malloc(uocr_hip_ctx *c, void **p, size_t bytes) {
+    const hipError_t e = hipHostMalloc(p, bytes, hipHostMallocDefault);
+    if (e == hipSuccess) {
+        ++c->alloc_count;
+        c->alloc_bytes += bytes;
+    }
+    return e;
+}
+
+/* Hot-path allocation guard: generation fails when prefill or the decode
+ * loop allocated device or pinned memory, or the arenas changed size. */
+struct alloc_guard {
+    uint64_t count, bytes, warena, rarena;
+};
+
+static alloc_guard guard_begin(const uocr_hip_ctx *c) {
+    return alloc_guard{c->alloc_count, c->alloc_bytes, c->warena_bytes, c->rarena_bytes};
+}
+
+static int guard_end(const uocr_hip_ctx *c, const alloc_guard &g, const char *label, char *err, size_t err_size) {
+    if (c->alloc_count != g.count || c->warena_bytes != g.warena || c->rarena_bytes != g.rarena) {
+        return bfail(err, err_size, "%s allocated device memory (%llu allocation(s), %llu bytes)", label,
+                     (unsigned long long)(c->alloc_count - g.count), (unsigned long long)(c->alloc_bytes - g.bytes));
+    }
+    return 1;
+}
+
+/* UOCR_HIP_FAULT_ALLOC test hook: one counted 256-byte allocation inside the
+ * guarded region (freed at once), so tests can see the guard fail a request. */
+static void fault_alloc(uocr_hip_ctx *c, int where) {
+    if (c->fault_alloc != where) return;
+    void *p = nullptr;
+    if (counted_malloc(c, &p, 256u) == hipSuccess) (void)hipFree(p);
+}
 
 extern "C" int uocr_hip_is_available(char *why, size_t why_size) {
     int n = 0;
@@ -157,6 +206,8 @@ extern "C" uocr_hip_ctx *uocr_hip_context_create(char *err, size_t err_size) {
         return nullptr;
     }
     /* inv_freq[d] = 2^(d * (-2 log2(theta) / head_dim)), golden.py:410-414 */
+    const char *fa = getenv("UOCR_HIP_FAULT_ALLOC");
+    ctx->fault_alloc = fa == nullptr ? 0 : (strcmp(fa, "prefill") == 0 ? 1 : (strcmp(fa, "decode") == 0 ? 2 : 0));
     const float freq_scale = -2.0f * log2f((float)UOCR_ROPE_THETA) / (float)UOCR_HEAD_DIM;
     for (int d = 0; d < UOCR_K_HEAD_DIM / 2; ++d) ctx->invf[d] = exp2f((float)d * freq_scale);
     return ctx;
@@ -418,7 +469,7 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
     }
     const uint64_t run_model_off = total;
     total += align256(sizeof(uocr_run_model));
-    HIPCHK(hipMalloc((void **)&ctx->warena, total), "weight arena allocation");
+    HIPCHK(counted_malloc(ctx, (void **)&ctx->warena, total), "weight arena allocation");
     ctx->warena_bytes = total;
     placer p;
     uocr_qmat fn;
@@ -517,7 +568,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_pkp = p.take(Pc * H_SIZE * 2u * 4u);
     const uint64_t o_run = p.take(uocr_run_arena_bytes());
     const uint64_t total = p.off;
-    HIPCHK(hipMalloc((void **)&ctx->rarena, total), "runtime arena allocation");
+    HIPCHK(counted_malloc(ctx, (void **)&ctx->rarena, total), "runtime arena allocation");
     /* cleared on the engine's stream (non-blocking, so not ordered against a
      * null-stream hipMemset) and waited for */
     HIPCHK(hipMemsetAsync(ctx->rarena, 0, total, ctx->stream), "runtime arena clear");
@@ -575,9 +626,9 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->logits_bytes = logits_end - moe_end;
     ctx->prompt_bytes = prompt_end - logits_end;
     ctx->prefill_bytes = total - prompt_end;
-    HIPCHK(hipHostMalloc((void **)&ctx->h_tokens, (size_t)max_gen * 4u, hipHostMallocDefault), "pinned token buffer");
-    HIPCHK(hipHostMalloc((void **)&ctx->h_scores, (size_t)max_gen * 4u, hipHostMallocDefault), "pinned score buffer");
-    HIPCHK(hipHostMalloc((void **)&ctx->h_prompt, (size_t)prompt_capacity * H_SIZE * 2u, hipHostMallocDefault),
+    HIPCHK(counted_host_malloc(ctx, (void **)&ctx->h_tokens, (size_t)max_gen * 4u), "pinned token buffer");
+    HIPCHK(counted_host_malloc(ctx, (void **)&ctx->h_scores, (size_t)max_gen * 4u), "pinned score buffer");
+    HIPCHK(counted_host_malloc(ctx, (void **)&ctx->h_prompt, (size_t)prompt_capacity * H_SIZE * 2u),
            "pinned prompt staging");
     if (ctx->mem != nullptr) {
         uocr_memory_reserve(ctx->mem, UOCR_MEMORY_KV_CACHE, ctx->kv_bytes);
@@ -861,7 +912,7 @@ static int scan_chunk(uocr_hip_ctx *c, uint32_t from, uint32_t to, int ignore_eo
  * the first starting from the prefill's hidden state (published with a tag
  * of its own), token ids read back one chunk behind the GPU. */
 static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, uint64_t t0, uint64_t t1,
-                      uocr_hip_decoder_result *res, char *err, size_t err_size) {
+                      const alloc_guard &dg, uocr_hip_decoder_result *res, char *err, size_t err_size) {
     hipStream_t s = c->stream;
     std::lock_guard<std::mutex> lock(g_run_mutex);
     const uint32_t seed_tag = c->run_tag, tag0 = seed_tag + 1u;
@@ -912,6 +963,8 @@ static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, u
     if (!eos && !scan_chunk(c, scanned, issued, ignore_eos, &count, &eos)) {
         return bfail(err, err_size, "decode selected an invalid token id");
     }
+    fault_alloc(c, 2);
+    if (!guard_end(c, dg, "HIP decode loop", err, err_size)) return 0;
     const uint64_t t2 = uocr_now_ns();
     memcpy(res->generated_ids, c->h_tokens, (size_t)count * 4u);
     if (res->generated_scores != nullptr) {
@@ -960,6 +1013,7 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
     }
     hipStream_t s = c->stream;
     const uint64_t t0 = uocr_now_ns();
+    const alloc_guard pg = guard_begin(c);
 
     /* prompt assembly: image rows from the caller, text rows gathered on device */
     uint32_t n_img = 0;
@@ -996,7 +1050,10 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
             }
         }
     }
+    fault_alloc(c, 1);
     HIPCHK(hipStreamSynchronize(s), "prefill sync");
+    if (!guard_end(c, pg, "HIP prompt prefill", err, err_size)) return 0;
+    const alloc_guard dg = guard_begin(c);
     const uint64_t t1 = uocr_now_ns();
 
     /* decode: chunks of DECODE_CHUNK steps; the host scans chunk k-1 while
@@ -1004,7 +1061,7 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
      * unsupported models) one replay of the captured 8-step graph. */
     const int ignore_eos = (req->flags & UOCR_GEN_IGNORE_EOS) != 0u;
     const bool use_run = c->run_ok && use_graph && (req->flags & UOCR_GEN_NO_RUN) == 0u;
-    if (use_run) return decode_run(c, P, N, ignore_eos, t0, t1, res, err, err_size);
+    if (use_run) return decode_run(c, P, N, ignore_eos, t0, t1, dg, res, err, err_size);
     HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf), "decode state init");
     uint32_t count = 0, scanned = 0;
     int eos = 0;
@@ -1054,6 +1111,8 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
     if (!eos && !scan_chunk(c, scanned, issued, ignore_eos, &count, &eos)) {
         return bfail(err, err_size, "decode selected an invalid token id");
     }
+    fault_alloc(c, 2);
+    if (!guard_end(c, dg, "HIP decode loop", err, err_size)) return 0;
     const uint64_t t2 = uocr_now_ns();
     memcpy(res->generated_ids, c->h_tokens, (size_t)count * 4u);
     if (res->generated_scores != nullptr) {
