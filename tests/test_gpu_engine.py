@@ -337,3 +337,32 @@ def test_hot_path_allocation_fails_the_request(gpu, monkeypatch, where, run):
         assert ex.value.status == uocr.UOCR_ERROR_INTERNAL
         assert "allocated device memory" in str(ex.value)
         assert ("prefill" if where == "prefill" else "decode loop") in str(ex.value)
+
+
+def test_per_op_decode_profile_events(gpu, monkeypatch):
+    """Profiling on and UOCR_HIP_DECODER_PROFILE_DETAIL=3: the decode loop
+    runs eagerly with an event pair around each launch and reports
+    hip.decode.* roles (uocr_metal.m:14338-14496 names) with one call per
+    launch, the same greedy ids as the graph path, and per-launch times that
+    sum to no more than the decode loop's wall time."""
+    uocr = gpu
+    m = model(uocr, 3)
+    rng = np.random.default_rng(21)
+    ids, mask, rows = prompt(rng, 8, 4)
+    N = 4
+    with uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=64, max_gen_tokens=16) as eng:
+        ref, _, _, _ = eng.generate_embeddings(ids, mask, rows, max_new_tokens=N, flags=uocr.GEN_IGNORE_EOS)
+    monkeypatch.setenv("UOCR_HIP_DECODER_PROFILE_DETAIL", "3")
+    with uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=64, max_gen_tokens=16, profile=True) as eng:
+        got, _, _, dms = eng.generate_embeddings(ids, mask, rows, max_new_tokens=N, flags=uocr.GEN_IGNORE_EOS)
+        ev = eng.profile_events()
+    assert got.tolist() == ref.tolist()
+    steps = N - 1  # the last step runs the LM head only
+    assert ev["hip.decode.attention"][0] == 12 * steps
+    assert ev["hip.decode.attention_projections"][0] == 2 * 12 * steps
+    assert ev["hip.decode.dense_mlp"][0] == 2 * steps
+    assert ev["hip.decode.moe_routed_experts"][0] == 2 * 11 * steps
+    assert ev["hip.decode.layer"][0] == 12 * steps
+    assert ev["hip.decode.lm_head"][0] >= N
+    per_op = sum(v[1] for k, v in ev.items() if k.startswith("hip.decode.") and k != "hip.decode.layer")
+    assert 0.0 < per_op <= dms

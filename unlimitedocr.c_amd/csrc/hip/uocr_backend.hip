@@ -122,6 +122,18 @@ struct uocr_hip_ctx {
      * pinned allocation of the backend is counted */
     uint64_t alloc_count, alloc_bytes;
     int fault_alloc;             /* test hook (UOCR_HIP_FAULT_ALLOC): 1 prefill, 2 decode */
+    /* opt-in per-op decode timing (UOCR_HIP_DECODER_PROFILE_DETAIL >= 3 with
+     * profiling on): event pairs around every decode launch */
+    int profile_detail;
+    struct op_timer *tm;         /* active only inside the timed decode loop */
+};
+
+#define OP_TIMER_MAX 96
+struct op_timer {
+    hipEvent_t ev[2 * OP_TIMER_MAX];
+    const char *name[OP_TIMER_MAX];
+    int layer_first[UOCR_DECODER_LAYERS], layer_last[UOCR_DECODER_LAYERS];
+    int n;
 };
 
 /* Persistent runs need every CU of the device: runs of different engines in
@@ -206,6 +218,8 @@ extern "C" uocr_hip_ctx *uocr_hip_context_create(char *err, size_t err_size) {
         return nullptr;
     }
     /* inv_freq[d] = 2^(d * (-2 log2(theta) / head_dim)), golden.py:410-414 */
+    const char *pd = getenv("UOCR_HIP_DECODER_PROFILE_DETAIL");
+    ctx->profile_detail = pd != nullptr ? atoi(pd) : 0;
     const char *fa = getenv("UOCR_HIP_FAULT_ALLOC");
     ctx->fault_alloc = fa == nullptr ? 0 : (strcmp(fa, "prefill") == 0 ? 1 : (strcmp(fa, "decode") == 0 ? 2 : 0));
     const float freq_scale = -2.0f * log2f((float)UOCR_ROPE_THETA) / (float)UOCR_HEAD_DIM;
@@ -649,18 +663,69 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
 /* sel: layer 0's QKV launch chooses the token from the LM-head keys and
  * stages its embedding row (a decode step); else h already holds the
  * layer input (a prompt position). */
+/* Per-op decode timing: an event pair around one launch, named with the
+ * reference's decode roles (uocr_metal.m:14338-14496) under hip.decode.*;
+ * a fused launch carries the role of its first op:
+ *   attention_projections  QKV (+ attention norm, RoPE, KV write) and O
+ *                          (+ attention merge, router fold)
+ *   attention              split-K attention
+ *   dense_mlp              layer 0's SwiGLU and down
+ *   moe_router             router logits (layers without the fold)
+ *   moe_routed_experts     top-6 + routed and shared gate/up; routed and
+ *                          shared down + combine
+ *   lm_head                final norm + LM head + argmax (+ selection) */
+static void tm_begin(uocr_hip_ctx *c, const char *name) {
+    op_timer *t = c->tm;
+    if (t == nullptr || t->n >= OP_TIMER_MAX) return;
+    t->name[t->n] = name;
+    (void)hipEventRecord(t->ev[2 * t->n], c->stream);
+}
+
+static void tm_end(uocr_hip_ctx *c) {
+    op_timer *t = c->tm;
+    if (t == nullptr || t->n >= OP_TIMER_MAX) return;
+    (void)hipEventRecord(t->ev[2 * t->n + 1], c->stream);
+    ++t->n;
+}
+
+/* After the step's work is complete: every timed launch into the profile,
+ * and per layer the span from its first launch's start to its last's end. */
+static void tm_flush(uocr_hip_ctx *c) {
+    op_timer *t = c->tm;
+    if (t == nullptr || c->profile == nullptr) return;
+    for (int i = 0; i < t->n; ++i) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, t->ev[2 * i], t->ev[2 * i + 1]) == hipSuccess) uocr_profile_add_ms(c->profile, t->name[i], ms);
+    }
+    for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
+        const int a = t->layer_first[l], b = t->layer_last[l];
+        float ms = 0.0f;
+        if (a >= 0 && b >= a && hipEventElapsedTime(&ms, t->ev[2 * a], t->ev[2 * b + 1]) == hipSuccess) {
+            uocr_profile_add_ms(c->profile, "hip.decode.layer", ms);
+        }
+        t->layer_first[l] = t->layer_last[l] = -1;
+    }
+    t->n = 0;
+}
+
 static hipError_t enqueue_layers(uocr_hip_ctx *c, bool sel) {
     hipStream_t s = c->stream;
     const uint64_t kv_layer = (uint64_t)UOCR_ATTENTION_HEADS * c->cache_cap * UOCR_HEAD_DIM;
     hipError_t e = hipSuccess;
+    const char *role = nullptr;
 #define ENQ(x)                        \
     do {                              \
+        if (role != nullptr) tm_begin(c, role); \
         e = (x);                      \
         if (e != hipSuccess) return e; \
+        if (role != nullptr) tm_end(c); \
     } while (0)
+#define ROLE(r) role = c->tm != nullptr ? (r) : nullptr
     for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
         const dev_layer &L = c->L[l];
         uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
+        if (c->tm != nullptr) c->tm->layer_first[l] = c->tm->n;
+        ROLE("hip.decode.attention_projections");
         if (sel && l == 0u) {
             ENQ(uocr_launch_qkv_rope_select(s, L.q, L.k, L.v, L.in_norm, c->state, c->q, kc, vc, c->cache_cap,
                                             (const uint64_t *)c->lm_part, c->embed, UOCR_VOCAB_SIZE, c->tokens,
@@ -668,22 +733,29 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c, bool sel) {
         } else {
             ENQ(uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->state, c->q, kc, vc, c->cache_cap));
         }
+        ROLE("hip.decode.attention");
         ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part, c->racc,
                                   sel && l == 0u ? (uint64_t *)c->lm_part : nullptr));
+        ROLE("hip.decode.attention_projections");
         ENQ(uocr_launch_attn_out(s, L.o, c->attn_part, c->h, c->a, nullptr, L.rfold, c->racc));
         if (l == 0u) {
+            ROLE("hip.decode.dense_mlp");
             ENQ(uocr_launch_swiglu(s, L.gate, L.up, UOCR_DENSE_LAYER0_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->mid));
             ENQ(uocr_launch_gemv(s, L.down, H_SIZE, UOCR_DENSE_LAYER0_INTERMEDIATE, c->mid, nullptr, c->a, c->h));
         } else {
             /* with the fold, attn_out has produced the un-normalised logits */
+            ROLE("hip.decode.moe_router");
             if (L.rfold == nullptr) ENQ(uocr_launch_router_logits(s, L.router, c->a, L.post_norm, c->logits));
+            ROLE("hip.decode.moe_routed_experts");
             ENQ(uocr_launch_moe_gate_up(s, &L.slab, L.sgate, L.sup, L.rfold == nullptr ? c->logits : nullptr,
                                         L.rfold == nullptr ? nullptr : c->racc, 0, c->a, L.post_norm, c->mid, c->smid,
                                         c->route_ids, c->route_w));
             ENQ(uocr_launch_moe_down(s, &L.slab, c->route_ids, c->route_w, c->mid, L.sdown, c->smid, c->a, c->h));
         }
+        if (c->tm != nullptr) c->tm->layer_last[l] = c->tm->n - 1;
     }
     return e;
+#undef ROLE
 #undef ENQ
 }
 
@@ -693,12 +765,17 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c, bool sel) {
  * layers follow), a finalize launch chooses it and, unless last, gathers its
  * embedding row into h. */
 static hipError_t enqueue_select(uocr_hip_ctx *c, bool last) {
+    tm_begin(c, "hip.decode.lm_head");
     hipError_t e = uocr_launch_lm_keys(c->stream, c->lm_head, UOCR_VOCAB_SIZE, c->h, c->final_norm,
                                        (uint64_t *)c->lm_part, c->state, 1, c->invf);
+    if (e == hipSuccess) tm_end(c);
     if (e != hipSuccess || (c->fold_select && !last)) return e;
     uocr_qmat none = {nullptr, nullptr, UOCR_QT_Q4};
-    return uocr_launch_lm_finalize(c->stream, (uint64_t *)c->lm_part, c->state, 1, c->tokens, c->scores,
-                                   last ? none : c->embed, UOCR_VOCAB_SIZE, c->h);
+    tm_begin(c, "hip.decode.lm_head");
+    e = uocr_launch_lm_finalize(c->stream, (uint64_t *)c->lm_part, c->state, 1, c->tokens, c->scores,
+                                last ? none : c->embed, UOCR_VOCAB_SIZE, c->h);
+    if (e == hipSuccess) tm_end(c);
+    return e;
 }
 
 static hipError_t enqueue_decode_step(uocr_hip_ctx *c) {
@@ -983,6 +1060,55 @@ static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, u
     return 1;
 }
 
+/* The decode loop with per-op timing: eager launches with an event pair
+ * around each, the step synchronised and its times added to the profile
+ * report (hip.decode.*); the host scans every step for EOS. */
+static int decode_timed(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, uint64_t t0, uint64_t t1,
+                        const alloc_guard &dg, uocr_hip_decoder_result *res, char *err, size_t err_size) {
+    hipStream_t s = c->stream;
+    op_timer *t = (op_timer *)calloc(1, sizeof(op_timer));
+    if (t == nullptr) return bfail(err, err_size, "profile timer allocation failed");
+    int made = 0, ok = 1;
+    for (; made < 2 * OP_TIMER_MAX && hipEventCreate(&t->ev[made]) == hipSuccess; ++made) {
+    }
+    if (made < 2 * OP_TIMER_MAX) ok = bfail(err, err_size, "profile event creation failed");
+    for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) t->layer_first[l] = t->layer_last[l] = -1;
+    uint32_t count = 0;
+    int eos = 0;
+    if (ok && uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf) != hipSuccess) {
+        ok = bfail(err, err_size, "decode state init failed");
+    }
+    c->tm = t;
+    for (uint32_t step = 0; ok && step < N && !eos; ++step) {
+        const hipError_t e = step + 1u < N ? enqueue_decode_step(c) : enqueue_select(c, true);
+        if (e != hipSuccess || hipMemcpyAsync(c->h_tokens + step, c->tokens + step, 4u, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess) {
+            ok = bfail(err, err_size, "timed decode step %u failed", step);
+            break;
+        }
+        tm_flush(c);
+        if (!scan_chunk(c, step, step + 1u, ignore_eos, &count, &eos)) ok = bfail(err, err_size, "decode selected an invalid token id");
+    }
+    c->tm = nullptr;
+    for (int i = 0; i < made; ++i) (void)hipEventDestroy(t->ev[i]);
+    free(t);
+    if (!ok) return 0;
+    fault_alloc(c, 2);
+    if (!guard_end(c, dg, "HIP decode loop", err, err_size)) return 0;
+    const uint64_t t2 = uocr_now_ns();
+    memcpy(res->generated_ids, c->h_tokens, (size_t)count * 4u);
+    if (res->generated_scores != nullptr) {
+        HIPCHK(hipMemcpy(res->generated_scores, c->scores, (size_t)count * 4u, hipMemcpyDeviceToHost), "score readback");
+    }
+    res->generated_count = count;
+    res->stopped_on_eos = (uint32_t)eos;
+    res->prefill_ms = (double)(t1 - t0) / 1.0e6;
+    res->decode_ms = (double)(t2 - t1) / 1.0e6;
+    uocr_profile_add_ms(c->profile, "hip.prefill", res->prefill_ms);
+    uocr_profile_add_ms(c->profile, "hip.decode_loop", res->decode_ms);
+    return 1;
+}
+
 extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder_request *req,
                                          uocr_hip_decoder_result *res, char *err, size_t err_size) {
     if (c == nullptr || req == nullptr || res == nullptr || req->input_ids == nullptr) {
@@ -1060,8 +1186,10 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
      * chunk k runs.  A chunk is one persistent run launch, or (UOCR_GEN_NO_RUN,
      * unsupported models) one replay of the captured 8-step graph. */
     const int ignore_eos = (req->flags & UOCR_GEN_IGNORE_EOS) != 0u;
-    const bool use_run = c->run_ok && use_graph && (req->flags & UOCR_GEN_NO_RUN) == 0u;
+    const bool timed = c->profile_detail >= 3 && c->profile != nullptr && c->profile->report.enabled != 0u;
+    const bool use_run = c->run_ok && use_graph && !timed && (req->flags & UOCR_GEN_NO_RUN) == 0u;
     if (use_run) return decode_run(c, P, N, ignore_eos, t0, t1, dg, res, err, err_size);
+    if (timed) return decode_timed(c, P, N, ignore_eos, t0, t1, dg, res, err, err_size);
     HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf), "decode state init");
     uint32_t count = 0, scanned = 0;
     int eos = 0;
