@@ -9,10 +9,16 @@ decode-loop seconds (src/unlimitedocr_c/perf.py:97-102), weights resident in
 HBM before timing starts.  The Q8 and fp16 profiles run the same workload and
 are reported beside it.
 
-`roofline` is the dominant kernel by bytes (the Q4 LM-head GEMV + argmax
-keys: 87,912,964 algorithmic bytes per launch) timed
-with HIP events on the stream it runs on, rotating 6 weight copies (528 MB)
-so launches stream from HBM rather than the 256 MB Infinity Cache.
+`roofline` is the dominant kernel of the config-5 decode loop by time
+(k_moe_gate_up): its decode-shape launches captured into a hipGraph over
+expert-slab copies larger than the Infinity Cache, HIP events around the
+replays.  `roofline.decode_kernels` gives every decode kernel's share and
+fraction from one extra generation of the workload with per-launch HIP events
+on the engine stream (eager launches, dispatch included): algorithmic bytes
+per launch / mean launch time.  `lm_head_config2` times the Q4
+LM-head GEMV + argmax keys (87,912,964 algorithmic bytes
+per launch) rotating 6 weight copies (528 MB) so launches stream from HBM
+rather than the 256 MB Infinity Cache.
 `operators` times BASELINE configs 1, 3 and 4 as single operators through
 the C ABI (captured into one hipGraph, HIP events on the operator stream),
 weights rotated over copies larger than the Infinity Cache ("cold") and
@@ -98,6 +104,144 @@ def run_profile(qprofile: int, steps: int, warmup: int, log, flags: int = 0) -> 
             "roofline_tok_s": PEAK_HBM / bpt, "frac": bpt * tok_s / PEAK_HBM, "generated": gen}
 
 
+def _rowbytes(q: str, k: int) -> int:
+    """Bytes of one weight row of k inputs: q4_0 / q8_0 payload plus one
+    fp16 scale per 64 inputs, or fp16."""
+    return {"q4": k // 2 + k // 64 * 2, "q8": k + k // 64 * 2, "f16": 2 * k}[q]
+
+
+def decode_kernel_bytes(prompt_len: int, n_new: int) -> dict[str, float]:
+    """Algorithmic HBM bytes per launch of each config-5 decode kernel, mixed-Q4
+    profile (attention projections q8_0, FFN / LM head / embedding q4_0):
+    every weight byte the launch needs once, activations in and out once.
+    Layer-dependent kernels are averaged over their launches per step."""
+    H, I, SI, D0, V = 1280, 896, 1792, 6848, 129280
+    act = 2 * H  # one fp16 hidden vector
+    att_w = 3 * H * _rowbytes("q8", H)
+    # attention length of decode step t (t = 0 .. n_new-2 run the layers): P + min(t + 1, 128)
+    lens = [prompt_len + min(t + 1, 128) for t in range(n_new - 1)]
+    mean_len = float(np.mean(lens))
+    fold = H * 64 * 4  # fp32 router fold, MoE layers (11 of 12)
+    return {
+        # norm weights + h in, q out, the new K/V rows
+        "k_qkv_rope": att_w + 2 * act + act + 2 * act,
+        # K and V of every live slot (10 heads x 128 fp16 each) + q in + context out
+        "k_attention": 2 * 10 * 128 * 2 * mean_len + 2 * act,
+        # O projection + context and residual in, a out, the fold on MoE layers
+        "k_attn_out": H * _rowbytes("q8", H) + 3 * act + fold * 11 / 12,
+        # routed 6 x (gate, up) rows of 896 + shared merged (gate, up) 1792, a + post norm in, mid out
+        "k_moe_gate_up": 6 * 2 * I * _rowbytes("q4", H) + 2 * SI * _rowbytes("q4", H) + 2 * act
+                         + 2 * (6 * I + SI),
+        # routed 6 x down rows (K = 896) + shared down (K = 1792), mid in, a in, h out
+        "k_moe_down": 6 * H * _rowbytes("q4", I) + H * _rowbytes("q4", SI) + 2 * (6 * I + SI) + 2 * act,
+        "k_swiglu": 2 * D0 * _rowbytes("q4", H) + 2 * act + 2 * D0,
+        "k_gemv": H * _rowbytes("q4", D0) + 2 * D0 + 2 * act,
+        "k_lm_keys": V * _rowbytes("q4", H) + 2 * act,
+        "k_lm_finalize": _rowbytes("q4", H) + act,
+    }
+
+
+def decode_kernel_roofline(log) -> dict:
+    """Per-kernel HBM roofline of the config-5 decode loop (mixed-Q4), timed
+    live: one generation of the config-5 workload with the engine's per-launch
+    profile events (UOCR_HIP_DECODER_PROFILE_DETAIL=4: eager launches, each
+    bracketed by a HIP event pair on the engine's stream, added up per
+    kernel).  `achieved` = algorithmic bytes per launch / mean launch time.
+    The dominant kernel (largest share of decode time) is the roofline line."""
+    os.environ["UOCR_HIP_DECODER_PROFILE_DETAIL"] = "4"
+    try:
+        model = uocr.synth_model(uocr.QPROFILE_Q4, 7)
+        ids, mask, rows = make_prompt()
+        with uocr.Engine.from_memory(model, backend="hip", max_prompt_tokens=1024, max_gen_tokens=N_NEW,
+                                     profile=True) as eng:
+            eng.generate_embeddings(ids, mask, rows, N_NEW, flags=uocr.GEN_IGNORE_EOS)
+            eng.profile_reset()
+            out, _, _, dec_ms = eng.generate_embeddings(ids, mask, rows, N_NEW, flags=uocr.GEN_IGNORE_EOS)
+            ev = eng.profile_events()
+        model.close()
+    finally:
+        del os.environ["UOCR_HIP_DECODER_PROFILE_DETAIL"]
+    algo = decode_kernel_bytes(ids.size, N_NEW)
+    kern = {k[len("hip.kernel."):]: v for k, v in ev.items() if k.startswith("hip.kernel.")}
+    total_ms = sum(v[1] for v in kern.values())
+    table = {}
+    for name, (calls, ms) in sorted(kern.items(), key=lambda kv: -kv[1][1]):
+        us = ms * 1e3 / calls
+        gbs = algo[name] / (us * 1e-6) / 1e9
+        table[name] = {"launches": calls, "avg_us": round(us, 3), "share": round(ms / total_ms, 4),
+                       "algorithmic_bytes": int(algo[name]), "achieved_gbs": round(gbs, 1),
+                       "frac": round(gbs / 8000.0, 4)}
+    dom = next(iter(table))
+    log(f"decode kernels (eager, {out.size} tokens, {dec_ms:.1f} ms, kernel sum {total_ms:.1f} ms): "
+        + ", ".join(f"{k} {v['avg_us']:.1f}us x{v['launches']} {v['frac']:.2f}" for k, v in table.items()))
+    return {"dominant": dom, "decode_ms": round(dec_ms, 2), "kernel_sum_ms": round(total_ms, 2),
+            "timing": "HIP events on the engine stream around each eager launch of one config-5 generation; "
+                      "each interval includes the launch's dispatch (about 2 us on this path), so these "
+                      "fractions are lower bounds",
+            "per_kernel": table}
+
+
+def gate_up_roofline(log, n_copy: int = 5, per_copy: int = 12, replays: int = 40) -> dict:
+    """The dominant config-5 decode kernel, k_moe_gate_up (mixed-Q4: top-6 of
+    64 routed experts' gate/up rows 896 x 1280 + the merged shared 1792 x 1280,
+    q4_0), at its decode shape through uocr_op_moe_gate_up: n_copy copies of
+    the expert slabs (n_copy x 80 MB, more than the 256 MB Infinity Cache),
+    each call with fresh N(0,1) router logits (so the selected experts change
+    from call to call) and a fresh hidden; the calls are captured into one
+    hipGraph and timed with HIP events on the operator stream over `replays`
+    replays; mean launch time = elapsed / launches."""
+    rng = np.random.default_rng(5)
+    E, I, H, SI = 64, 896, 1280, 1792
+    keep = []
+
+    def put(a):
+        b = uocr.DeviceBuffer.of(np.ascontiguousarray(a))
+        keep.append(b)
+        return b.ptr
+
+    gw = rng.integers(0, 256, size=(E, I, H // 2), dtype=np.uint8)
+    gs = (np.abs(rng.standard_normal((E, I, H // 64))) * 0.02 / 7).astype(np.float16)
+    sgw = rng.integers(0, 256, size=(SI, H // 2), dtype=np.uint8)
+    sgs = (np.abs(rng.standard_normal((SI, H // 64))) * 0.02 / 7).astype(np.float16)
+    mws = []
+    for _ in range(n_copy):
+        m = uocr.CMoeWeights()
+        m.expert_qtype = m.shared_qtype = 4
+        m.gate_w, m.gate_s, m.up_w, m.up_s = put(gw), put(gs), put(gw[::-1]), put(gs[::-1])
+        m.down_w, m.down_s = m.gate_w, m.gate_s  # not read by the gate/up stage
+        m.gu_w_stride, m.gu_s_stride = gw[0].nbytes, gs[0].size
+        m.dn_w_stride, m.dn_s_stride = gw[0].nbytes, gs[0].size
+        m.sgate_w, m.sgate_s, m.sup_w, m.sup_s = put(sgw), put(sgs), put(sgw[::-1]), put(sgs[::-1])
+        m.sdown_w, m.sdown_s = m.sgate_w, m.sgate_s
+        mws.append(m)
+    n = n_copy * per_copy
+    logits = uocr.DeviceBuffer.of(rng.standard_normal((n, E)).astype(np.float32))
+    xs = uocr.DeviceBuffer.of(rng.standard_normal((n, H)).astype(np.float16))
+    nw = uocr.DeviceBuffer.of(rng.uniform(0.8, 1.2, H).astype(np.float16))
+    mid, smid = uocr.DeviceBuffer(n * 6 * I * 2), uocr.DeviceBuffer(n * SI * 2)
+    ids, wts = uocr.DeviceBuffer(n * 24), uocr.DeviceBuffer(n * 24)
+    calls = [lambda i=i: uocr.op_moe_gate_up(mws[i % n_copy], logits.ptr + i * E * 4, xs.ptr + i * H * 2, nw, 0,
+                                             mid.ptr + i * 6 * I * 2, smid.ptr + i * SI * 2, ids.ptr + i * 24,
+                                             wts.ptr + i * 24) for i in range(n)]
+    ms = _graph_time(log, calls, replays)
+    algo = decode_kernel_bytes(N_IMAGE + N_TEXT, N_NEW)["k_moe_gate_up"]
+    gbs = algo / (ms / 1e3) / 1e9
+    sel = ids.download(np.uint32).reshape(n, 6)
+    log(f"k_moe_gate_up (graph, {n} calls x {replays} replays, {n_copy} slab copies): {ms * 1e3:.2f} us/launch, "
+        f"{gbs:.0f} GB/s; {len(np.unique(sel))} distinct experts selected")
+    traffic = None
+    if DECODE_TRAFFIC_FILE.exists():
+        traffic = json.loads(DECODE_TRAFFIC_FILE.read_text()).get("k_moe_gate_up", {}).get("hbm_bytes_per_launch")
+    return {"kernel": "k_moe_gate_up<Q4, Q4, false> (router top-6 + routed and shared gate/up SwiGLU, config-5 decode "
+                      "shape, mixed-Q4)",
+            "bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s", "frac": round(gbs / 8000.0, 4),
+            "traffic": traffic, "avg_launch_us": round(ms * 1e3, 3), "algorithmic_bytes": int(algo),
+            "launches": n * replays,
+            "timing": f"hipGraph of {n} uocr_op_moe_gate_up calls over {n_copy} expert-slab copies "
+                      f"({n_copy * (gw.nbytes + gs.nbytes) * 2 / 1e6:.0f} MB), HIP events around {replays} replays"}
+
+
+DECODE_TRAFFIC_FILE = ROOT / "profiles" / "decode_q4_config5_traffic.json"
 TRAFFIC_FILE = ROOT / "profiles" / "lm_head_q4_traffic.json"
 
 
@@ -489,6 +633,11 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the config-2 LM-head measurement and a copy probe (for rocprofv3 --pmc runs)")
+    ap.add_argument("--decode-kernels-only", action="store_true",
+                    help="run only the per-kernel roofline of the config-5 decode loop (eager, event-timed)")
+    ap.add_argument("--gate-up-only", action="store_true",
+                    help="run only the dominant-kernel (k_moe_gate_up) graph measurement and a copy probe "
+                         "(for rocprofv3 runs)")
     ap.add_argument("--no-ops", action="store_true", help="skip the config 1/3/4 operator measurements")
     ap.add_argument("--ops-only", action="store_true", help="run only the config 1/3/4 operator measurements")
     ap.add_argument("--op-replays", type=int, default=None,
@@ -512,6 +661,13 @@ def main() -> None:
     if uocr.load_library().uocr_hip_device_count() <= 0:
         log("no HIP device visible")
         sys.exit(1)
+    if args.decode_kernels_only:
+        print(json.dumps({"decode_kernels": decode_kernel_roofline(log)}), flush=True)
+        return
+    if args.gate_up_only:
+        print(json.dumps({"roofline": gate_up_roofline(log)}), flush=True)
+        copy_probe(log)
+        return
     if args.roofline_only:
         print(json.dumps({"roofline": lm_head_roofline(log)}), flush=True)
         copy_probe(log)
@@ -541,7 +697,9 @@ def main() -> None:
     wanted = ["q4"] + [p for p in args.profiles.split(",") if p in names and p != "q4"]
     flags = uocr.GEN_NO_GRAPH if args.no_graph else 0
     results = {p: run_profile(names[p], args.steps, args.warmup, log, flags) for p in wanted}
-    roof = lm_head_roofline(log)
+    roof = gate_up_roofline(log)
+    roof["decode_kernels"] = decode_kernel_roofline(log)
+    lm = lm_head_roofline(log)
     cpu = None if args.no_cpu_baseline else cpu_baseline(log)
     ops = None if args.no_ops else operator_benchmarks(log, not args.no_cpu_baseline)
     vision = None if args.no_vision else vision_benchmarks(log, not args.no_cpu_baseline)
@@ -563,6 +721,7 @@ def main() -> None:
                                "512 greedy decode steps, batch 1, mixed-Q4 profile (attention Q8_0)",
                    "prompt_tokens": N_IMAGE + N_TEXT, "decode_steps": N_NEW},
         "roofline": roof,
+        "lm_head_config2": lm,
         "cpu_baseline": cpu,
         "prefill": {"ms": round(q4["prefill_ms"], 2), "gflop": round(prefill_flops(N_IMAGE + N_TEXT) / 1e9, 1),
                     "tflops": round(prefill_flops(N_IMAGE + N_TEXT) / (q4["prefill_ms"] / 1e3) / 1e12, 1),

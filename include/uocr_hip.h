@@ -60,6 +60,19 @@ UOCR_API int uocr_generate_embeddings(uocr_engine *engine, const int32_t *input_
                                       uint32_t max_new_tokens, uint32_t flags, int32_t *out_ids, float *out_scores,
                                       uint32_t *out_count, double *out_prefill_ms, double *out_decode_ms);
 
+/* Decode trace, for parity tests against a CPU restatement of the decoder
+ * (no counterpart in the reference; it reads the router selection of
+ * uocr_metal.m:14227-14548 and the hidden state fed to the LM head).  After
+ * uocr_engine_trace_enable(engine, steps), each generation records the
+ * expert ids the router selects in layers 1-11 while computing the hidden
+ * state of decode steps t < steps.  uocr_engine_trace_read copies them to
+ * expert_ids ([steps][11][6], 0xffffffff for steps not reached; may be NULL)
+ * and the final hidden state of the last generation (the fp16 [1280] input
+ * of its last token's final norm; may be NULL).  steps = 0 turns tracing off.
+ * Tracing switches the per-step graph path to eager launches. */
+UOCR_API int uocr_engine_trace_enable(uocr_engine *engine, uint32_t steps);
+UOCR_API int uocr_engine_trace_read(uocr_engine *engine, uint32_t *expert_ids, uint16_t *hidden);
+
 /* ---- 2. hot-path operators ----------------------------------------------- */
 
 /* Bytes of the device workspace every operator below takes (partials,
@@ -135,6 +148,18 @@ typedef struct uocr_op_moe_weights {
  * decode_gemv_q4.metal:138-180, down-combine :185-224); BASELINE config 3. */
 UOCR_API int uocr_op_moe_ffn(const uocr_op_moe_weights *m, const void *x, const void *norm_w, const void *residual,
                              int norm_topk, void *workspace, void *out, uint32_t *ids, float *weights);
+
+/* The gate/up stage of uocr_op_moe_ffn alone: from router logits (fp32[64],
+ * device) the top-6 experts and their softmax weights (renormalised when
+ * norm_topk), then mid[r] = fp16(silu(G_e xin) * U_e xin) for each selected
+ * expert e = ids[r] (mid: [6][896] fp16) and smid likewise for the merged
+ * shared experts ([1792] fp16), xin = x or rmsnorm(x, norm_w); all pointers
+ * device.  One kernel launch.  Replaces uocr_moe_router_softmax_topk_f32
+ * (kernels/moe.metal:194) followed by uocr_moe_decode_gate_up_gemv_q4_0_to_f16
+ * (kernels/decode_gemv_q4.metal:138-180) and the shared SwiGLU of
+ * uocr_metal.m:14433-14497. */
+UOCR_API int uocr_op_moe_gate_up(const uocr_op_moe_weights *m, const float *logits, const void *x, const void *norm_w,
+                                 int norm_topk, void *mid, void *smid, uint32_t *ids, float *weights);
 
 /* Decode attention of one query (fp16 [10][128]) over a KV cache laid out
  * [10 heads][cache_capacity][128] fp16, for prompt_length prompt slots plus

@@ -56,6 +56,7 @@ _SIGS = {
                      _VP, _VP, _U32, _VP, _VP, _VP, _VP], ct.c_int),
     "orc_attention_decode": ([_VP, _VP, _VP, _U32, _U32, ct.POINTER(Plan), _VP], ct.c_int),
     "orc_embed_row": ([_U32, _VP, _VP, _U32, _U32, _I32, _VP], ct.c_int),
+    "orc_session_embed": ([_VP, _I32, _VP], ct.c_int),
     "orc_model_open": ([_VP, ct.c_size_t, ct.c_char_p, ct.c_size_t], _VP),
     "orc_model_close": ([_VP], None),
     "orc_session_create": ([_VP, _U32], _VP),
@@ -63,6 +64,7 @@ _SIGS = {
     "orc_generate": ([_VP, _VP, _VP, _VP, _U32, _U32, ct.c_int, _VP, _VP], ct.c_int),
     "orc_session_reset": ([_VP, _U32], ct.c_int),
     "orc_forward_token": ([_VP, _VP, _U32, _VP], ct.c_int),
+    "orc_forward_token_traced": ([_VP, _VP, _U32, _VP, _VP], ct.c_int),
     "orc_select": ([_VP, _VP, ct.POINTER(_I32), ct.POINTER(_F), ct.POINTER(_F)], ct.c_int),
     "orc_session_fill_kv": ([_VP, _U32, ct.c_uint64], ct.c_int),
     "orc_vision_linear": ([_U32, _VP, _VP, _VP, _U32, _U32, _U32, _U32, _U32, _VP, _VP, _VP, _VP], ct.c_int),
@@ -204,6 +206,10 @@ class Model:
         if n < 0:
             raise RuntimeError("oracle generation failed")
         return out[:n], margins[:n]
+
+    def embed(self, token: int, out: np.ndarray) -> int:
+        """Embedding row of token into out (uint16 fp16 bits [1280]); 1 on success."""
+        return lib().orc_session_embed(ct.c_void_p(self.s), int(token), ptr(out))
 
     def close(self) -> None:
         if self.s:

@@ -939,7 +939,8 @@ int orc_session_fill_kv(orc_session *s, uint32_t n, uint64_t seed) {
 }
 
 /* One decoder token, uocr_metal.m:14299-14518 op order, golden.py rounding. */
-int orc_forward_token(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids) {
+static int forward_token(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids,
+                         float *trace_margins) {
     const uint32_t H = UOCR_HIDDEN_SIZE, NH = UOCR_ATTENTION_HEADS, HD = UOCR_HEAD_DIM;
     if (!s || !hidden || s->prompt_length == 0u) return 0;
     const uint32_t P = s->prompt_length, R = UOCR_GENERATED_RING_WINDOW;
@@ -984,11 +985,13 @@ int orc_forward_token(orc_session *s, uint16_t *hidden, uint32_t position, uint3
         } else {
             uint32_t ids[UOCR_MOE_TOP_K];
             float w[UOCR_MOE_TOP_K];
+            float margin = 0.0f;
             if (!orc_router_topk(n2, (const uint16_t *)L->router.w, UOCR_ROUTED_EXPERTS, H, UOCR_MOE_TOP_K, 0, ids, w,
-                                 NULL, NULL)) {
+                                 NULL, &margin)) {
                 return 0;
             }
             if (trace_ids) memcpy(trace_ids + (size_t)(l - 1u) * UOCR_MOE_TOP_K, ids, sizeof(ids));
+            if (trace_margins) trace_margins[l - 1u] = margin;
             const uint32_t SI = UOCR_MOE_SHARED_INTERMEDIATE, EI = UOCR_MOE_EXPERT_INTERMEDIATE;
             uint16_t smid[UOCR_MOE_SHARED_INTERMEDIATE], shared[UOCR_HIDDEN_SIZE];
             uint16_t mid[UOCR_MOE_TOP_K * UOCR_MOE_EXPERT_INTERMEDIATE];
@@ -1016,12 +1019,27 @@ int orc_forward_token(orc_session *s, uint16_t *hidden, uint32_t position, uint3
     return 1;
 }
 
+int orc_forward_token(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids) {
+    return forward_token(s, hidden, position, trace_ids, NULL);
+}
+
+int orc_forward_token_traced(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids,
+                             float *trace_margins) {
+    return forward_token(s, hidden, position, trace_ids, trace_margins);
+}
+
 int orc_select(orc_session *s, const uint16_t *hidden, int32_t *id, float *score, float *second) {
     uint16_t n[UOCR_HIDDEN_SIZE];
     const orc_model *m = s->m;
     if (!orc_rmsnorm_f16(hidden, (const uint16_t *)m->final_norm.w, UOCR_HIDDEN_SIZE, UOCR_RMS_NORM_EPS, n)) return 0;
     return orc_lm_head_argmax(m->lm_head.qtype, m->lm_head.w, m->lm_head.s, UOCR_VOCAB_SIZE, UOCR_HIDDEN_SIZE, n, id,
                               score, second);
+}
+
+int orc_session_embed(orc_session *s, int32_t token, uint16_t *out) {
+    if (!s || !out) return 0;
+    const orc_model *m = s->m;
+    return orc_embed_row(m->embed.qtype, m->embed.w, m->embed.s, UOCR_VOCAB_SIZE, UOCR_HIDDEN_SIZE, token, out);
 }
 
 int orc_generate(orc_session *s, const int32_t *ids, const uint8_t *image_mask, const uint16_t *image_rows,

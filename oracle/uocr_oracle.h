@@ -194,7 +194,15 @@ int orc_session_reset(orc_session *s, uint32_t prompt_length);
  * for that position; attention covers the plan implied by (prompt_length,
  * position).  Optional trace_ids receives the router ids [11][6]. */
 int orc_forward_token(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids);
+/* orc_forward_token that also writes, per MoE layer, the router's selection
+ * margin ([11] floats, orc_router_topk's margin: the smallest logit gap
+ * between consecutive ranks of the selection, the 6th against the best
+ * unselected expert included). */
+int orc_forward_token_traced(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids,
+                             float *trace_margins);
 int orc_select(orc_session *s, const uint16_t *hidden, int32_t *id, float *score, float *second);
+/* The model's embedding row of token (fp16 bits), as orc_generate stages it. */
+int orc_session_embed(orc_session *s, int32_t token, uint16_t *out);
 /* Fills the KV cache prefix [0, n) of every layer with fp16 values from a
  * seeded N(0,1) stream (for timing decode at a given context length). */
 int orc_session_fill_kv(orc_session *s, uint32_t n, uint64_t seed);

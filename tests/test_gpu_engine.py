@@ -366,3 +366,71 @@ def test_per_op_decode_profile_events(gpu, monkeypatch):
     assert ev["hip.decode.lm_head"][0] >= N
     per_op = sum(v[1] for k, v in ev.items() if k.startswith("hip.decode.") and k != "hip.decode.layer")
     assert 0.0 < per_op <= dms
+
+
+@pytest.mark.parametrize("profile,run", [("q4", "0"), ("q4", "1"), ("q8", "0"), ("q8", "1"), ("f16", "0")])
+def test_config5_full_decode_matches_oracle(gpu, monkeypatch, profile, run):
+    """BASELINE config 5 end to end: the 932-row prompt of
+    tests/golden/make_config5.py and 512 greedy steps, against the C oracle's
+    fixture for the same synthetic model (seed 7).
+
+    - ids: equal from step 0 until the first step where they differ, and that
+      step must be one the oracle decides by a margin of at most 1e-2; at
+      least 128 steps must agree;
+    - router: the expert ids of layers 1-11 for the first 16 steps, as sets
+      (only the set enters the sum), wherever the prefix of ids agrees and
+      the oracle's router margin exceeds 1e-2 (the fused router sums the
+      logits in another order and without the fp16 rounding of the normed
+      hidden, so a near-tie may resolve either way);
+    - hidden state (the input of the final norm) at each fixture checkpoint
+      reached on the oracle's token prefix: |got - ref| <= 2e-2 + 1e-2 |ref|.
+    run "1" takes the persistent cooperative decode (UOCR_HIP_RUN=1) where
+    the profile has one; "0" the per-step kernel path."""
+    import sys
+    from pathlib import Path
+
+    golden = Path(__file__).resolve().parent / "golden"
+    sys.path.insert(0, str(golden))
+    import make_config5
+
+    uocr = gpu
+    fx = np.load(golden / f"config5_{profile}.npz")
+    ref, margins, trace, rmargin = fx["ids"], fx["margins"], fx["trace"], fx["router_margin"]
+    steps = ref.size
+    monkeypatch.setenv("UOCR_HIP_RUN", run)
+    m = model(uocr, make_config5.PROFILES[profile])
+    ids, mask, rows = make_config5.config5_prompt()
+    with uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=1024, max_gen_tokens=steps) as eng:
+        eng.trace_enable(trace.shape[0])
+        got, _, _, _ = eng.generate_embeddings(ids, mask, rows, max_new_tokens=steps, flags=uocr.GEN_IGNORE_EOS)
+        sel, hidden = eng.trace_read()
+        assert got.shape == (steps,)
+        agree = int(np.argmin(got == ref)) if (got != ref).any() else steps
+        if agree < steps:
+            assert margins[agree] <= 1e-2, f"step {agree}: got {got[agree]}, oracle {ref[agree]} " \
+                                           f"(margin {margins[agree]:.4f})"
+        assert agree >= 128, f"ids agree for {agree} steps only"
+        routed = 0
+        for t in range(min(trace.shape[0], agree)):
+            for layer in range(11):
+                if rmargin[t, layer] > 1e-2:
+                    assert sorted(sel[t, layer]) == sorted(trace[t, layer]), f"step {t} layer {layer + 1}"
+                    routed += 1
+        assert routed >= 100
+        checked = 0
+        for k, href in zip(fx["hidden_steps"], fx["hidden"]):
+            k = int(k)
+            if k > agree:
+                continue
+            if k + 1 < steps:
+                part, _, _, _ = eng.generate_embeddings(ids, mask, rows, max_new_tokens=k + 1,
+                                                        flags=uocr.GEN_IGNORE_EOS)
+                assert part.tolist() == got[:k + 1].tolist()
+                _, h = eng.trace_read()
+            else:
+                h = hidden
+            want = href.view(np.float16).astype(np.float32)
+            np.testing.assert_allclose(h.astype(np.float32), want, atol=2e-2, rtol=1e-2,
+                                       err_msg=f"hidden state at step {k}")
+            checked += 1
+        assert checked >= 2

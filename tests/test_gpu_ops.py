@@ -253,6 +253,45 @@ def test_moe_ffn_matches_oracle(gpu, oracle, qtype, shared_qtype, norm_topk):
     assert checked >= 2
 
 
+@pytest.mark.parametrize("qtype,norm_topk", [(4, False), (3, True)])
+def test_moe_gate_up_matches_oracle(gpu, oracle, qtype, norm_topk):
+    """uocr_op_moe_gate_up: from fp32 router logits the top-6 ids and softmax
+    weights of the oracle's router (orc_router_topk on the same normalised
+    hidden), and per selected expert the oracle's SwiGLU mid; the shared mid
+    likewise.  Logits are the router product in float64, rounded to fp32."""
+    uocr = gpu
+    rng = np.random.default_rng(60 + qtype)
+    m, host, keep = _moe_setup(uocr, rng, qtype, qtype)
+    nw = rng.uniform(0.8, 1.2, 1280).astype(np.float16)
+    dnw = dev(uocr, nw)
+    gw, gs = host["gate"]
+    uw, us = host["up"]
+    sg, su = host["sg"], host["su"]
+    checked = 0
+    for t in range(6):
+        x = rand_f16(rng, 1280)
+        xn = oracle.rmsnorm_f16(x.view(np.uint16), nw.view(np.uint16))
+        ref_ids, ref_w, _, margin = oracle.router_topk(xn, host["router"].view(np.uint16), norm_topk=norm_topk)
+        logits = (host["router"].astype(np.float64) @ xn.view(np.float16).astype(np.float64)).astype(np.float32)
+        dmid, dsmid = uocr.DeviceBuffer(6 * 896 * 2), uocr.DeviceBuffer(1792 * 2)
+        dids, dw = uocr.DeviceBuffer(24), uocr.DeviceBuffer(24)
+        uocr.op_moe_gate_up(m, dev(uocr, logits), dev(uocr, x), dnw, int(norm_topk), dmid, dsmid, dids, dw)
+        uocr.sync()
+        ids = dids.download(np.uint32)
+        mid = dmid.download(np.uint16).reshape(6, 896)
+        assert_f16_close(dsmid.download(np.uint16), oracle.swiglu(qtype, sg[0], sg[1], su[0], su[1], 1792, 1280, xn))
+        if margin <= 1e-2:
+            continue
+        assert ids.tolist() == ref_ids.tolist()
+        assert np.allclose(dw.download(np.float32), ref_w, rtol=1e-3, atol=1e-5)
+        for r, e in enumerate(ids):
+            ref = oracle.swiglu(qtype, gw[e], None if gs is None else gs[e], uw[e], None if us is None else us[e], 896,
+                                1280, xn)
+            assert_f16_close(mid[r], ref)
+        checked += 1
+    assert checked >= 2
+
+
 def test_router_ties_lowest_id(gpu):
     uocr = gpu
     x = np.zeros(1280, np.float16)

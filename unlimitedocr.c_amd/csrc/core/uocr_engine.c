@@ -470,3 +470,35 @@ int uocr_generate_embeddings(uocr_engine *e, const int32_t *input_ids, const uin
     if (st == UOCR_OK) clear_error(e);
     return st;
 }
+
+static int hip_ready(uocr_engine *e) {
+    if (e == NULL) return set_error(NULL, UOCR_ERROR_INVALID_ARGUMENT, "engine is null");
+    clear_error(e);
+    if (e->hip == NULL || !e->decoder_ready) {
+        return set_error(e, UOCR_ERROR_NOT_IMPLEMENTED, "decode trace requires the HIP backend with a bound decoder");
+    }
+    return UOCR_OK;
+}
+
+int uocr_engine_trace_enable(uocr_engine *e, uint32_t steps) {
+    const int st = hip_ready(e);
+    if (st != UOCR_OK) return st;
+    if (steps > e->max_gen_tokens) {
+        return set_error(e, UOCR_ERROR_INVALID_ARGUMENT, "trace of %u steps exceeds max_gen_tokens %u", steps, e->max_gen_tokens);
+    }
+    char herr[512] = {0};
+    if (!uocr_hip_context_trace_enable(e->hip, steps, herr, sizeof(herr))) {
+        return set_error(e, UOCR_ERROR_INTERNAL, "decode trace setup failed: %s", herr);
+    }
+    return UOCR_OK;
+}
+
+int uocr_engine_trace_read(uocr_engine *e, uint32_t *expert_ids, uint16_t *hidden) {
+    const int st = hip_ready(e);
+    if (st != UOCR_OK) return st;
+    char herr[512] = {0};
+    if (!uocr_hip_context_trace_read(e->hip, expert_ids, hidden, herr, sizeof(herr))) {
+        return set_error(e, UOCR_ERROR_INTERNAL, "decode trace readback failed: %s", herr);
+    }
+    return UOCR_OK;
+}

@@ -63,6 +63,13 @@ int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t prompt_capacit
 int uocr_hip_context_generate(uocr_hip_ctx *ctx, const uocr_hip_decoder_request *req, uocr_hip_decoder_result *res,
                               char *err, size_t err_size);
 uint64_t uocr_hip_context_weight_bytes(const uocr_hip_ctx *ctx);
+/* Decode trace for parity tests: the following generations record, for
+ * decode steps t < steps, the expert ids of layers 1-11 ([steps][11][6]),
+ * and the final hidden state (the last step's LM-head input, fp16 [1280]).
+ * steps = 0 turns it off.  The graph path records through its eager per-step
+ * loop; the persistent run records in place. */
+int uocr_hip_context_trace_enable(uocr_hip_ctx *ctx, uint32_t steps, char *err, size_t err_size);
+int uocr_hip_context_trace_read(uocr_hip_ctx *ctx, uint32_t *expert_ids, uint16_t *hidden, char *err, size_t err_size);
 
 #ifdef __cplusplus
 }

@@ -126,12 +126,17 @@ struct uocr_hip_ctx {
      * profiling on): event pairs around every decode launch */
     int profile_detail;
     struct op_timer *tm;         /* active only inside the timed decode loop */
+    /* decode trace (uocr_hip_context_trace_enable) */
+    uint32_t trace_steps;
+    uint32_t *d_trace;           /* [trace_steps][11][6] expert ids */
+    int32_t trace_step;          /* step being enqueued by the eager loop (-1: none) */
 };
 
 #define OP_TIMER_MAX 96
 struct op_timer {
     hipEvent_t ev[2 * OP_TIMER_MAX];
     const char *name[OP_TIMER_MAX];
+    const char *kname[OP_TIMER_MAX]; /* the launch's kernel (hip.kernel.*), or NULL */
     int layer_first[UOCR_DECODER_LAYERS], layer_last[UOCR_DECODER_LAYERS];
     int n;
 };
@@ -218,6 +223,7 @@ extern "C" uocr_hip_ctx *uocr_hip_context_create(char *err, size_t err_size) {
         return nullptr;
     }
     /* inv_freq[d] = 2^(d * (-2 log2(theta) / head_dim)), golden.py:410-414 */
+    ctx->trace_step = -1;
     const char *pd = getenv("UOCR_HIP_DECODER_PROFILE_DETAIL");
     ctx->profile_detail = pd != nullptr ? atoi(pd) : 0;
     const char *fa = getenv("UOCR_HIP_FAULT_ALLOC");
@@ -269,6 +275,7 @@ extern "C" void uocr_hip_context_destroy(uocr_hip_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     release_runtime(ctx);
     if (ctx->warena != nullptr) (void)hipFree(ctx->warena);
+    if (ctx->d_trace != nullptr) (void)hipFree(ctx->d_trace);
     (void)hipStreamDestroy(ctx->stream);
     free(ctx);
 }
@@ -674,10 +681,11 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
  *   moe_routed_experts     top-6 + routed and shared gate/up; routed and
  *                          shared down + combine
  *   lm_head                final norm + LM head + argmax (+ selection) */
-static void tm_begin(uocr_hip_ctx *c, const char *name) {
+static void tm_begin(uocr_hip_ctx *c, const char *name, const char *kname) {
     op_timer *t = c->tm;
     if (t == nullptr || t->n >= OP_TIMER_MAX) return;
     t->name[t->n] = name;
+    t->kname[t->n] = c->profile_detail >= 4 ? kname : nullptr;
     (void)hipEventRecord(t->ev[2 * t->n], c->stream);
 }
 
@@ -695,7 +703,9 @@ static void tm_flush(uocr_hip_ctx *c) {
     if (t == nullptr || c->profile == nullptr) return;
     for (int i = 0; i < t->n; ++i) {
         float ms = 0.0f;
-        if (hipEventElapsedTime(&ms, t->ev[2 * i], t->ev[2 * i + 1]) == hipSuccess) uocr_profile_add_ms(c->profile, t->name[i], ms);
+        if (hipEventElapsedTime(&ms, t->ev[2 * i], t->ev[2 * i + 1]) != hipSuccess) continue;
+        uocr_profile_add_ms(c->profile, t->name[i], ms);
+        if (t->kname[i] != nullptr) uocr_profile_add_ms(c->profile, t->kname[i], ms);
     }
     for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
         const int a = t->layer_first[l], b = t->layer_last[l];
@@ -713,9 +723,9 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c, bool sel) {
     const uint64_t kv_layer = (uint64_t)UOCR_ATTENTION_HEADS * c->cache_cap * UOCR_HEAD_DIM;
     hipError_t e = hipSuccess;
     const char *role = nullptr;
-#define ENQ(x)                        \
+#define ENQK(k, x)                    \
     do {                              \
-        if (role != nullptr) tm_begin(c, role); \
+        if (role != nullptr) tm_begin(c, role, "hip.kernel." k); \
         e = (x);                      \
         if (e != hipSuccess) return e; \
         if (role != nullptr) tm_end(c); \
@@ -727,36 +737,42 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c, bool sel) {
         if (c->tm != nullptr) c->tm->layer_first[l] = c->tm->n;
         ROLE("hip.decode.attention_projections");
         if (sel && l == 0u) {
-            ENQ(uocr_launch_qkv_rope_select(s, L.q, L.k, L.v, L.in_norm, c->state, c->q, kc, vc, c->cache_cap,
+            ENQK("k_qkv_rope", uocr_launch_qkv_rope_select(s, L.q, L.k, L.v, L.in_norm, c->state, c->q, kc, vc, c->cache_cap,
                                             (const uint64_t *)c->lm_part, c->embed, UOCR_VOCAB_SIZE, c->tokens,
                                             c->scores, c->h));
         } else {
-            ENQ(uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->state, c->q, kc, vc, c->cache_cap));
+            ENQK("k_qkv_rope", uocr_launch_qkv_rope(s, L.q, L.k, L.v, c->h, L.in_norm, c->state, c->q, kc, vc, c->cache_cap));
         }
         ROLE("hip.decode.attention");
-        ENQ(uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part, c->racc,
+        ENQK("k_attention", uocr_launch_attention(s, c->q, kc, vc, c->cache_cap, c->state, c->attn_part, c->racc,
                                   sel && l == 0u ? (uint64_t *)c->lm_part : nullptr));
         ROLE("hip.decode.attention_projections");
-        ENQ(uocr_launch_attn_out(s, L.o, c->attn_part, c->h, c->a, nullptr, L.rfold, c->racc));
+        ENQK("k_attn_out", uocr_launch_attn_out(s, L.o, c->attn_part, c->h, c->a, nullptr, L.rfold, c->racc));
         if (l == 0u) {
             ROLE("hip.decode.dense_mlp");
-            ENQ(uocr_launch_swiglu(s, L.gate, L.up, UOCR_DENSE_LAYER0_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->mid));
-            ENQ(uocr_launch_gemv(s, L.down, H_SIZE, UOCR_DENSE_LAYER0_INTERMEDIATE, c->mid, nullptr, c->a, c->h));
+            ENQK("k_swiglu", uocr_launch_swiglu(s, L.gate, L.up, UOCR_DENSE_LAYER0_INTERMEDIATE, H_SIZE, c->a, L.post_norm, c->mid));
+            ENQK("k_gemv", uocr_launch_gemv(s, L.down, H_SIZE, UOCR_DENSE_LAYER0_INTERMEDIATE, c->mid, nullptr, c->a, c->h));
         } else {
             /* with the fold, attn_out has produced the un-normalised logits */
             ROLE("hip.decode.moe_router");
-            if (L.rfold == nullptr) ENQ(uocr_launch_router_logits(s, L.router, c->a, L.post_norm, c->logits));
+            if (L.rfold == nullptr) ENQK("k_router_logits", uocr_launch_router_logits(s, L.router, c->a, L.post_norm, c->logits));
             ROLE("hip.decode.moe_routed_experts");
-            ENQ(uocr_launch_moe_gate_up(s, &L.slab, L.sgate, L.sup, L.rfold == nullptr ? c->logits : nullptr,
+            ENQK("k_moe_gate_up", uocr_launch_moe_gate_up(s, &L.slab, L.sgate, L.sup, L.rfold == nullptr ? c->logits : nullptr,
                                         L.rfold == nullptr ? nullptr : c->racc, 0, c->a, L.post_norm, c->mid, c->smid,
                                         c->route_ids, c->route_w));
-            ENQ(uocr_launch_moe_down(s, &L.slab, c->route_ids, c->route_w, c->mid, L.sdown, c->smid, c->a, c->h));
+            if (c->trace_step >= 0 && (uint32_t)c->trace_step < c->trace_steps) {
+                role = nullptr; /* not a decode launch */
+                ENQK("trace", hipMemcpyAsync(c->d_trace + ((size_t)c->trace_step * 11u + (l - 1u)) * UOCR_MOE_TOP_K, c->route_ids,
+                                   UOCR_MOE_TOP_K * 4u, hipMemcpyDeviceToDevice, s));
+                ROLE("hip.decode.moe_routed_experts");
+            }
+            ENQK("k_moe_down", uocr_launch_moe_down(s, &L.slab, c->route_ids, c->route_w, c->mid, L.sdown, c->smid, c->a, c->h));
         }
         if (c->tm != nullptr) c->tm->layer_last[l] = c->tm->n - 1;
     }
     return e;
 #undef ROLE
-#undef ENQ
+#undef ENQK
 }
 
 /* The LM head of a decode step: argmax keys and the step-state advance
@@ -765,13 +781,13 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c, bool sel) {
  * layers follow), a finalize launch chooses it and, unless last, gathers its
  * embedding row into h. */
 static hipError_t enqueue_select(uocr_hip_ctx *c, bool last) {
-    tm_begin(c, "hip.decode.lm_head");
+    tm_begin(c, "hip.decode.lm_head", "hip.kernel.k_lm_keys");
     hipError_t e = uocr_launch_lm_keys(c->stream, c->lm_head, UOCR_VOCAB_SIZE, c->h, c->final_norm,
                                        (uint64_t *)c->lm_part, c->state, 1, c->invf);
     if (e == hipSuccess) tm_end(c);
     if (e != hipSuccess || (c->fold_select && !last)) return e;
     uocr_qmat none = {nullptr, nullptr, UOCR_QT_Q4};
-    tm_begin(c, "hip.decode.lm_head");
+    tm_begin(c, "hip.decode.lm_head", "hip.kernel.k_lm_finalize");
     e = uocr_launch_lm_finalize(c->stream, (uint64_t *)c->lm_part, c->state, 1, c->tokens, c->scores,
                                 last ? none : c->embed, UOCR_VOCAB_SIZE, c->h);
     if (e == hipSuccess) tm_end(c);
@@ -1005,7 +1021,7 @@ static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, u
         const uint32_t end = issued + DECODE_CHUNK < N ? issued + DECODE_CHUNK : N;
         const hipError_t e = uocr_run_launch(s, c->d_run_model, &c->run_model, c->run_arena, c->kc, c->vc, c->cache_cap,
                                              (int32_t)P, (int32_t)issued, (int32_t)(end - issued), end == N ? 1 : 0,
-                                             tag0 + issued, c->tokens, c->scores);
+                                             tag0 + issued, c->tokens, c->scores, c->h, c->d_trace, c->trace_steps);
         if (e != hipSuccess) {
             ok = bfail(err, err_size, "decode run of steps %u-%u: %s", issued, end - 1u, hipGetErrorString(e));
             break;
@@ -1060,11 +1076,12 @@ static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, u
     return 1;
 }
 
-/* The decode loop with per-op timing: eager launches with an event pair
- * around each, the step synchronised and its times added to the profile
- * report (hip.decode.*); the host scans every step for EOS. */
+/* The eager decode loop, one synchronised step at a time; the host scans
+ * every step for EOS.  With timed, an event pair brackets each launch and the
+ * step's times go to the profile report (hip.decode.*); with a decode trace
+ * on, the router's selections are copied out after each gate/up launch. */
 static int decode_timed(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, uint64_t t0, uint64_t t1,
-                        const alloc_guard &dg, uocr_hip_decoder_result *res, char *err, size_t err_size) {
+                        const alloc_guard &dg, bool timed, uocr_hip_decoder_result *res, char *err, size_t err_size) {
     hipStream_t s = c->stream;
     op_timer *t = (op_timer *)calloc(1, sizeof(op_timer));
     if (t == nullptr) return bfail(err, err_size, "profile timer allocation failed");
@@ -1078,8 +1095,9 @@ static int decode_timed(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos,
     if (ok && uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf) != hipSuccess) {
         ok = bfail(err, err_size, "decode state init failed");
     }
-    c->tm = t;
+    c->tm = timed ? t : nullptr;
     for (uint32_t step = 0; ok && step < N && !eos; ++step) {
+        c->trace_step = (int32_t)step;
         const hipError_t e = step + 1u < N ? enqueue_decode_step(c) : enqueue_select(c, true);
         if (e != hipSuccess || hipMemcpyAsync(c->h_tokens + step, c->tokens + step, 4u, hipMemcpyDeviceToHost, s) != hipSuccess ||
             hipStreamSynchronize(s) != hipSuccess) {
@@ -1090,6 +1108,7 @@ static int decode_timed(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos,
         if (!scan_chunk(c, step, step + 1u, ignore_eos, &count, &eos)) ok = bfail(err, err_size, "decode selected an invalid token id");
     }
     c->tm = nullptr;
+    c->trace_step = -1;
     for (int i = 0; i < made; ++i) (void)hipEventDestroy(t->ev[i]);
     free(t);
     if (!ok) return 0;
@@ -1104,8 +1123,10 @@ static int decode_timed(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos,
     res->stopped_on_eos = (uint32_t)eos;
     res->prefill_ms = (double)(t1 - t0) / 1.0e6;
     res->decode_ms = (double)(t2 - t1) / 1.0e6;
-    uocr_profile_add_ms(c->profile, "hip.prefill", res->prefill_ms);
-    uocr_profile_add_ms(c->profile, "hip.decode_loop", res->decode_ms);
+    if (c->profile != nullptr) {
+        uocr_profile_add_ms(c->profile, "hip.prefill", res->prefill_ms);
+        uocr_profile_add_ms(c->profile, "hip.decode_loop", res->decode_ms);
+    }
     return 1;
 }
 
@@ -1189,7 +1210,7 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
     const bool timed = c->profile_detail >= 3 && c->profile != nullptr && c->profile->report.enabled != 0u;
     const bool use_run = c->run_ok && use_graph && !timed && (req->flags & UOCR_GEN_NO_RUN) == 0u;
     if (use_run) return decode_run(c, P, N, ignore_eos, t0, t1, dg, res, err, err_size);
-    if (timed) return decode_timed(c, P, N, ignore_eos, t0, t1, dg, res, err, err_size);
+    if (timed || c->trace_steps != 0u) return decode_timed(c, P, N, ignore_eos, t0, t1, dg, timed, res, err, err_size);
     HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf), "decode state init");
     uint32_t count = 0, scanned = 0;
     int eos = 0;
@@ -1256,5 +1277,38 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
         c->profile->report.metal_command_buffer_count += use_graph ? (uint64_t)P + issued : 0u;
         c->profile->report.metal_command_buffer_wait_count += chunk + 1u;
     }
+    return 1;
+}
+
+/* ---- decode trace ----------------------------------------------------------- */
+
+extern "C" int uocr_hip_context_trace_enable(uocr_hip_ctx *c, uint32_t steps, char *err, size_t err_size) {
+    if (c == nullptr) return bfail(err, err_size, "invalid HIP context");
+    HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+    if (c->d_trace != nullptr) {
+        HIPCHK(hipStreamSynchronize(c->stream), "stream sync");
+        (void)hipFree(c->d_trace);
+        c->d_trace = nullptr;
+    }
+    c->trace_steps = 0u;
+    if (steps == 0u) return 1;
+    const size_t bytes = (size_t)steps * 11u * UOCR_MOE_TOP_K * 4u;
+    HIPCHK(counted_malloc(c, (void **)&c->d_trace, bytes), "trace buffer allocation");
+    HIPCHK(hipMemsetAsync(c->d_trace, 0xff, bytes, c->stream), "trace buffer clear");
+    HIPCHK(hipStreamSynchronize(c->stream), "trace buffer clear sync");
+    c->trace_steps = steps;
+    return 1;
+}
+
+extern "C" int uocr_hip_context_trace_read(uocr_hip_ctx *c, uint32_t *expert_ids, uint16_t *hidden, char *err,
+                                           size_t err_size) {
+    if (c == nullptr || !c->runtime_ready) return bfail(err, err_size, "HIP context has no runtime");
+    HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+    HIPCHK(hipStreamSynchronize(c->stream), "stream sync");
+    if (expert_ids != nullptr && c->trace_steps != 0u) {
+        HIPCHK(hipMemcpy(expert_ids, c->d_trace, (size_t)c->trace_steps * 11u * UOCR_MOE_TOP_K * 4u, hipMemcpyDeviceToHost),
+               "trace readback");
+    }
+    if (hidden != nullptr) HIPCHK(hipMemcpy(hidden, c->h, H_SIZE * 2u, hipMemcpyDeviceToHost), "hidden readback");
     return 1;
 }

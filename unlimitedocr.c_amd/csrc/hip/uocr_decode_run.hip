@@ -208,6 +208,9 @@ struct Run {
     int32_t P;
     int32_t *tokens;
     float *scores;
+    h16 *hout;      /* layer 11's output of every step (plain stores) */
+    u32 *trace;     /* expert ids [t][11][6] for t < trace_steps, or NULL */
+    u32 trace_steps;
     unsigned long long *tl; /* timeline of this step, or NULL */
 };
 
@@ -1083,6 +1086,9 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
             }
         }
         __syncthreads();
+        if (R.trace != nullptr && b == 0u && (u32)t < R.trace_steps && tid_() < TOPK) {
+            R.trace[((size_t)t * 11u + (l - 1u)) * TOPK + tid_()] = S.selid[tid_()];
+        }
         TLD(l, 9u);
         if (b < GU_ROUTED) {
             const u32 rank = b / 32u, e = S.selid[rank];
@@ -1179,7 +1185,10 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         out = d + (float)S.hres[c];
     }
     TLD(l, 12u);
-    if (lane == 0u) S.outv[rl] = (h16)out;
+    if (lane == 0u) {
+        S.outv[rl] = (h16)out;
+        if (l + 1u == UOCR_RUN_LAYERS) R.hout[c] = (h16)out;
+    }
     __syncthreads();
     publish(R, R.pk + off_h(l), PH, b * PH_B, PH_B, tag, [&](u32 p) { return pay6(S.outv, p, DN_ROWS); });
     TLR(2u * (5u + 5u * l) + 1u);
@@ -1197,6 +1206,9 @@ struct RunArgs {
     u32 tag0;
     int32_t *tokens;
     float *scores;
+    h16 *hout;
+    u32 *trace;
+    u32 trace_steps;
 };
 
 template <int QA, int QF, int QL, int QE>
@@ -1220,6 +1232,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
     R.P = A.P;
     R.tokens = A.tokens;
     R.scores = A.scores;
+    R.hout = A.hout;
+    R.trace = A.trace;
+    R.trace_steps = A.trace_steps;
     R.tl = nullptr;
 
     RowFrag<LmCfg<QL>::J> lf[LM_DEPTH];
@@ -1326,9 +1341,10 @@ extern "C" hipError_t uocr_run_reset(hipStream_t st, void *arena) {
 
 extern "C" hipError_t uocr_run_launch(hipStream_t st, const uocr_run_model *model, const uocr_run_model *host_model,
                                       void *arena, uint16_t *kc, uint16_t *vc, uint32_t cap, int32_t P, int32_t t0,
-                                      int32_t n, int last, uint32_t tag0, int32_t *tokens, float *scores) {
+                                      int32_t n, int last, uint32_t tag0, int32_t *tokens, float *scores,
+                                      uint16_t *hidden, uint32_t *trace, uint32_t trace_steps) {
     if (model == nullptr || host_model == nullptr || arena == nullptr || kc == nullptr || vc == nullptr ||
-        tokens == nullptr || n <= 0 || n > (int32_t)UOCR_RUN_MAX_STEPS || P <= 0 || t0 < 0 ||
+        tokens == nullptr || hidden == nullptr || (trace == nullptr && trace_steps != 0u) || n <= 0 || n > (int32_t)UOCR_RUN_MAX_STEPS || P <= 0 || t0 < 0 ||
         cap < (uint32_t)P + RING || !uocr_run_supported(host_model)) {
         return hipErrorInvalidValue;
     }
@@ -1347,6 +1363,9 @@ extern "C" hipError_t uocr_run_launch(hipStream_t st, const uocr_run_model *mode
     a.tag0 = tag0;
     a.tokens = tokens;
     a.scores = scores;
+    a.hout = (h16 *)hidden;
+    a.trace = trace;
+    a.trace_steps = trace_steps;
     if (host_model->qf == UOCR_QT_Q4) return launch_run<3, 4, 4, 4>(st, a);
     return launch_run<3, 3, 3, 3>(st, a);
 }

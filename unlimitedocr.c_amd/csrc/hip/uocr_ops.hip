@@ -193,6 +193,28 @@ extern "C" int uocr_op_moe_ffn(const uocr_op_moe_weights *m, const void *x, cons
     return r;
 }
 
+extern "C" int uocr_op_moe_gate_up(const uocr_op_moe_weights *m, const float *logits, const void *x, const void *norm_w,
+                                   int norm_topk, void *mid, void *smid, uint32_t *ids, float *weights) {
+    if (m == nullptr || logits == nullptr || x == nullptr || mid == nullptr || smid == nullptr || ids == nullptr ||
+        weights == nullptr || !qt_ok(m->expert_qtype) || !qt_ok(m->shared_qtype)) {
+        return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "invalid moe_gate_up arguments");
+    }
+    STREAM_OR_RETURN(st);
+    uocr_expert_slab sl;
+    sl.gate = qm(m->expert_qtype, m->gate_w, m->gate_s);
+    sl.up = qm(m->expert_qtype, m->up_w, m->up_s);
+    sl.down = qm(m->expert_qtype, m->down_w, m->down_s);
+    sl.gu_w_stride = m->gu_w_stride;
+    sl.gu_s_stride = m->gu_s_stride;
+    sl.dn_w_stride = m->dn_w_stride;
+    sl.dn_s_stride = m->dn_s_stride;
+    return hip_status(uocr_launch_moe_gate_up(st, &sl, qm(m->shared_qtype, m->sgate_w, m->sgate_s),
+                                              qm(m->shared_qtype, m->sup_w, m->sup_s), logits, nullptr, norm_topk,
+                                              (const uint16_t *)x, (const uint16_t *)norm_w, (uint16_t *)mid,
+                                              (uint16_t *)smid, ids, weights),
+                      "moe gate/up");
+}
+
 static void rope_inv_freq(float *invf) {
     const float freq_scale = -2.0f * log2f(10000.0f) / (float)UOCR_K_HEAD_DIM;
     for (int d = 0; d < UOCR_K_HEAD_DIM / 2; ++d) invf[d] = exp2f((float)d * freq_scale);

@@ -78,10 +78,13 @@ hipError_t uocr_run_reset(hipStream_t st, void *arena);
  * token t (tokens[t], scores[t]) from the LM head over the current hidden
  * state and, unless last and t is the final step, runs the 12 layers at
  * position P + t.  Step t0+i uses tag tag0+i.  model points to a device copy
- * of host_model.  kc/vc: [12][10][cap][128] fp16 caches. */
+ * of host_model.  kc/vc: [12][10][cap][128] fp16 caches.  hidden receives
+ * each step's final hidden state (layer 11's output); trace (may be NULL)
+ * the expert ids of layers 1-11 for steps t < trace_steps ([t][11][6]). */
 hipError_t uocr_run_launch(hipStream_t st, const uocr_run_model *model, const uocr_run_model *host_model,
                            void *arena, uint16_t *kc, uint16_t *vc, uint32_t cap, int32_t P, int32_t t0, int32_t n,
-                           int last, uint32_t tag0, int32_t *tokens, float *scores);
+                           int last, uint32_t tag0, int32_t *tokens, float *scores, uint16_t *hidden,
+                           uint32_t *trace, uint32_t trace_steps);
 
 #ifdef __cplusplus
 }

@@ -120,6 +120,8 @@ SIGNATURES = {
     "uocr_engine_open_memory": ([ct.POINTER(CEngineOpts), _VP, _SZ], _VP),
     "uocr_generate_embeddings": ([_VP, _VP, _VP, _VP, _U32, _U32, _U32, _U32, _VP, _VP, ct.POINTER(_U32),
                                   ct.POINTER(ct.c_double), ct.POINTER(ct.c_double)], ct.c_int),
+    "uocr_engine_trace_enable": ([_VP, _U32], ct.c_int),
+    "uocr_engine_trace_read": ([_VP, _VP, _VP], ct.c_int),
     "uocr_op_workspace_bytes": ([], _SZ),
     "uocr_op_gemv": ([_U32, _VP, _VP, _U32, _U32, _VP, _VP, _VP], ct.c_int),
     "uocr_op_swiglu": ([_U32, _VP, _VP, _VP, _VP, _U32, _U32, _VP, _VP, _VP], ct.c_int),
@@ -128,6 +130,7 @@ SIGNATURES = {
     "uocr_op_lm_head_keys": ([_U32, _VP, _VP, _U32, _VP, _VP, _VP], ct.c_int),
     "uocr_op_router": ([_VP, _VP, _VP, ct.c_int, _VP, _VP, _VP], ct.c_int),
     "uocr_op_moe_ffn": ([ct.POINTER(CMoeWeights), _VP, _VP, _VP, ct.c_int, _VP, _VP, _VP, _VP], ct.c_int),
+    "uocr_op_moe_gate_up": ([ct.POINTER(CMoeWeights), _VP, _VP, _VP, ct.c_int, _VP, _VP, _VP, _VP], ct.c_int),
     "uocr_op_attention_decode": ([_VP, _VP, _VP, _U32, _U32, _U32, _VP, _VP], ct.c_int),
     "uocr_op_attention_block": ([_U32, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _U32, _U32,
                                  _U32, _VP, _VP], ct.c_int),
@@ -256,6 +259,9 @@ class Engine:
         self._raise(self._lib.uocr_engine_profile_report(self._handle, ct.byref(rep)))
         return rep
 
+    def profile_reset(self) -> None:
+        self._raise(self._lib.uocr_engine_profile_reset(self._handle))
+
     def profile_events(self) -> dict[str, tuple[int, float]]:
         rep = self.profile_report()
         return {rep.events[i].name.decode(): (rep.events[i].calls, rep.events[i].total_ms)
@@ -299,6 +305,24 @@ class Engine:
                 None if rows is None else rows.ctypes.data, n_rows, ids.size, max_new_tokens, flags,
                 out.ctypes.data, scores.ctypes.data, ct.byref(count), ct.byref(pre), ct.byref(dec)))
         return out[:count.value], scores[:count.value], pre.value, dec.value
+
+    def trace_enable(self, steps: int) -> None:
+        """Record the router selections of the first `steps` decode steps of
+        each following generation (0 turns tracing off)."""
+        with self._lock:
+            self._raise(self._lib.uocr_engine_trace_enable(self._handle, steps))
+        self._trace_steps = steps
+
+    def trace_read(self) -> tuple[np.ndarray, np.ndarray]:
+        """(expert ids [steps][11][6] uint32, final hidden state fp16 [1280])
+        of the last generation."""
+        steps = getattr(self, "_trace_steps", 0)
+        ids = np.zeros((steps, 11, 6), np.uint32)
+        hidden = np.zeros(1280, np.float16)
+        with self._lock:
+            self._raise(self._lib.uocr_engine_trace_read(self._handle, ids.ctypes.data if steps else None,
+                                                         hidden.ctypes.data))
+        return ids, hidden
 
 
 # ---------------------------------------------------------------------------
@@ -470,6 +494,11 @@ def op_router(router, x, norm_w, norm_topk, ws, ids, weights) -> None:
 def op_moe_ffn(weights: CMoeWeights, x, norm_w, residual, norm_topk, ws, out, ids, wts) -> None:
     _check_op(load_library().uocr_op_moe_ffn(ct.byref(weights), _p(x), _p(norm_w), _p(residual), norm_topk, _p(ws),
                                              _p(out), _p(ids), _p(wts)), "op_moe_ffn")
+
+
+def op_moe_gate_up(weights: CMoeWeights, logits, x, norm_w, norm_topk, mid, smid, ids, wts) -> None:
+    _check_op(load_library().uocr_op_moe_gate_up(ct.byref(weights), _p(logits), _p(x), _p(norm_w), norm_topk,
+                                                 _p(mid), _p(smid), _p(ids), _p(wts)), "op_moe_gate_up")
 
 
 def op_attention_decode(q, kc, vc, cap, prompt_len, gen, ws, out) -> None:
