@@ -72,6 +72,14 @@ UOCR_API int uocr_generate_embeddings(uocr_engine *engine, const int32_t *input_
  * Tracing switches the per-step graph path to eager launches. */
 UOCR_API int uocr_engine_trace_enable(uocr_engine *engine, uint32_t steps);
 UOCR_API int uocr_engine_trace_read(uocr_engine *engine, uint32_t *expert_ids, uint16_t *hidden);
+/* Teacher forcing, also for parity tests (no counterpart in the reference):
+ * after uocr_engine_trace_force(engine, ids, n) each generation embeds ids[t]
+ * after decode step t < n instead of the token it selected, and still
+ * reports its own selection in out_ids.  Each step is then a function of the
+ * forced prefix alone, so a CPU restatement can be compared step by step
+ * over a whole generation.  n = 0 turns it off.  Forcing switches the
+ * per-step graph path to eager launches. */
+UOCR_API int uocr_engine_trace_force(uocr_engine *engine, const int32_t *ids, uint32_t n);
 
 /* ---- 2. hot-path operators ----------------------------------------------- */
 

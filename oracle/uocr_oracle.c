@@ -985,13 +985,23 @@ static int forward_token(orc_session *s, uint16_t *hidden, uint32_t position, ui
         } else {
             uint32_t ids[UOCR_MOE_TOP_K];
             float w[UOCR_MOE_TOP_K];
-            float margin = 0.0f;
+            float probs[UOCR_ROUTED_EXPERTS];
             if (!orc_router_topk(n2, (const uint16_t *)L->router.w, UOCR_ROUTED_EXPERTS, H, UOCR_MOE_TOP_K, 0, ids, w,
-                                 NULL, &margin)) {
+                                 probs, NULL)) {
                 return 0;
             }
             if (trace_ids) memcpy(trace_ids + (size_t)(l - 1u) * UOCR_MOE_TOP_K, ids, sizeof(ids));
-            if (trace_margins) trace_margins[l - 1u] = margin;
+            if (trace_margins) {
+                /* set margin in logit space: log p of the 6th choice over the
+                 * best unselected expert (softmax keeps logit differences) */
+                float next = 0.0f;
+                for (uint32_t e = 0; e < UOCR_ROUTED_EXPERTS; ++e) {
+                    int taken = 0;
+                    for (uint32_t j = 0; j < UOCR_MOE_TOP_K; ++j) taken |= ids[j] == e;
+                    if (!taken && probs[e] > next) next = probs[e];
+                }
+                trace_margins[l - 1u] = logf(probs[ids[UOCR_MOE_TOP_K - 1u]]) - logf(next);
+            }
             const uint32_t SI = UOCR_MOE_SHARED_INTERMEDIATE, EI = UOCR_MOE_EXPERT_INTERMEDIATE;
             uint16_t smid[UOCR_MOE_SHARED_INTERMEDIATE], shared[UOCR_HIDDEN_SIZE];
             uint16_t mid[UOCR_MOE_TOP_K * UOCR_MOE_EXPERT_INTERMEDIATE];

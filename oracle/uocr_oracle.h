@@ -194,10 +194,10 @@ int orc_session_reset(orc_session *s, uint32_t prompt_length);
  * for that position; attention covers the plan implied by (prompt_length,
  * position).  Optional trace_ids receives the router ids [11][6]. */
 int orc_forward_token(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids);
-/* orc_forward_token that also writes, per MoE layer, the router's selection
- * margin ([11] floats, orc_router_topk's margin: the smallest logit gap
- * between consecutive ranks of the selection, the 6th against the best
- * unselected expert included). */
+/* orc_forward_token that also writes, per MoE layer, the router's set
+ * margin ([11] floats): the logit gap between the 6th selected expert and
+ * the best unselected one (how far the selection, as a set, is from a
+ * tie). */
 int orc_forward_token_traced(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids,
                              float *trace_margins);
 int orc_select(orc_session *s, const uint16_t *hidden, int32_t *id, float *score, float *second);

@@ -3,11 +3,12 @@ BASELINE config 5 (900 N(0,1) fp16 image-embedding rows + 32 text ids, 512
 greedy steps) on the synthetic decoder of each quantisation profile
 (uocr.synth_model(profile, 7)).
 
-Each fixture holds, per step t < 512: the greedy id and the oracle's top-2
-logit margin; the router's expert ids of layers 1-11 while decoding the first
-TRACE_STEPS tokens, with the router's selection margin of each (the smallest
-logit gap between consecutive ranks, the 6th against the best unselected
-expert included); and the hidden state (fp16 bits, the input of step t's
+Each fixture holds, per step t < 512: the greedy id, its logit (`top`) and
+the oracle's top-2 logit margin; and for the forward pass of step t (which
+computes the hidden state step t + 1 selects from, t < 511) the router's
+expert ids in layers 1-11 (`trace`) with each selection's set margin
+(`router_gap`, the logit gap between the 6th chosen expert and the best
+unchosen one); and the hidden state (fp16 bits, the input of step t's
 final norm) at the checkpoint steps `hidden_steps`: 16, 128, 511 and the
 first step whose margin is at most 1e-2 (up to which a greedy decoder on the
 GPU must follow the oracle token for token).  The prompt is rebuilt from PROMPT_SEED by
@@ -31,7 +32,7 @@ for p in (ROOT / "unlimitedocr.c_amd", ROOT / "oracle"):
     sys.path.insert(0, str(p))
 
 PROMPT_SEED = 5
-N_IMAGE, N_TEXT, STEPS, TRACE_STEPS = 900, 32, 512, 16
+N_IMAGE, N_TEXT, STEPS = 900, 32, 512
 PROFILES = {"q4": 3, "q8": 2, "f16": 1}  # uocr.QPROFILE_*
 
 
@@ -75,29 +76,27 @@ def run(profile: str) -> None:
     print(f"{profile}: prefill {time.time() - t0:.0f} s", flush=True)
     out_ids = np.zeros(STEPS, np.int32)
     margins = np.zeros(STEPS, np.float32)
-    trace = np.zeros((TRACE_STEPS, 11, 6), np.uint32)
-    router_margin = np.zeros((TRACE_STEPS, 11), np.float32)
+    top = np.zeros(STEPS, np.float32)
+    trace = np.zeros((STEPS - 1, 11, 6), np.uint32)
+    router_gap = np.full((STEPS, 11), np.inf, np.float32)
     checkpoints = {16, 128, STEPS - 1}
     saved: dict[int, np.ndarray] = {}
     tok, s1, s2 = ct.c_int32(0), ct.c_float(0.0), ct.c_float(0.0)
     for t in range(STEPS):
         assert lib.orc_select(orc.s, oracle.ptr(h), ct.byref(tok), ct.byref(s1), ct.byref(s2)) == 1
-        out_ids[t], margins[t] = tok.value, s1.value - s2.value
+        out_ids[t], margins[t], top[t] = tok.value, s1.value - s2.value, s1.value
         if t in checkpoints or (margins[t] <= 1e-2 and not (margins[:t] <= 1e-2).any()):
             saved[t] = h.copy()
         if t + 1 == STEPS:
             break
         assert orc.embed(tok.value, emb) == 1
         h[:] = emb
-        if t < TRACE_STEPS:
-            assert lib.orc_forward_token_traced(orc.s, oracle.ptr(h), P + t, oracle.ptr(trace[t]),
-                                                oracle.ptr(router_margin[t])) == 1
-        else:
-            assert lib.orc_forward_token(orc.s, oracle.ptr(h), P + t, None) == 1
+        assert lib.orc_forward_token_traced(orc.s, oracle.ptr(h), P + t, oracle.ptr(trace[t]),
+                                            oracle.ptr(router_gap[t])) == 1
         if t % 64 == 0:
             print(f"{profile}: step {t} ({time.time() - t0:.0f} s)", flush=True)
-    np.savez_compressed(Path(__file__).with_name(f"config5_{profile}.npz"), ids=out_ids, margins=margins,
-                        trace=trace, router_margin=router_margin, hidden_steps=np.array(sorted(saved), np.int32),
+    np.savez_compressed(Path(__file__).with_name(f"config5_{profile}.npz"), ids=out_ids, margins=margins, top=top,
+                        trace=trace, router_gap=router_gap, hidden_steps=np.array(sorted(saved), np.int32),
                         hidden=np.stack([saved[k] for k in sorted(saved)]))
     orc.close()
     print(f"{profile}: done in {time.time() - t0:.0f} s; steps with margin <= 1e-2: "

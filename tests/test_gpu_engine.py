@@ -368,22 +368,32 @@ def test_per_op_decode_profile_events(gpu, monkeypatch):
     assert 0.0 < per_op <= dms
 
 
+ROUTER_TIE = 5e-3  # router set margins (logit units) at or below which the expert set may flip
+FLIP_WINDOW = 8    # steps after a routing difference whose ids are not compared
+
+
 @pytest.mark.parametrize("profile,run", [("q4", "0"), ("q4", "1"), ("q8", "0"), ("q8", "1"), ("f16", "0")])
 def test_config5_full_decode_matches_oracle(gpu, monkeypatch, profile, run):
     """BASELINE config 5 end to end: the 932-row prompt of
-    tests/golden/make_config5.py and 512 greedy steps, against the C oracle's
+    tests/golden/make_config5.py and 512 greedy steps against the C oracle's
     fixture for the same synthetic model (seed 7).
 
-    - ids: equal from step 0 until the first step where they differ, and that
-      step must be one the oracle decides by a margin of at most 1e-2; at
-      least 128 steps must agree;
-    - router: the expert ids of layers 1-11 for the first 16 steps, as sets
-      (only the set enters the sum), wherever the prefix of ids agrees and
-      the oracle's router margin exceeds 1e-2 (the fused router sums the
-      logits in another order and without the fp16 rounding of the normed
-      hidden, so a near-tie may resolve either way);
-    - hidden state (the input of the final norm) at each fixture checkpoint
-      reached on the oracle's token prefix: |got - ref| <= 2e-2 + 1e-2 |ref|.
+    Teacher-forced (the engine embeds the oracle's token after each step, so
+    every step is a function of the oracle's prefix):
+    - router: in each of the 511 forward passes, the first layer whose expert
+      set differs from the oracle's must be one where the oracle's set margin
+      is at most ROUTER_TIE (a near-tie; the later layers of that pass see a
+      different hidden state);
+    - ids and logits: at every step whose oracle margin exceeds 1e-2 and
+      whose last FLIP_WINDOW forward passes took the oracle's experts, the
+      engine's argmax equals the oracle's id and its logit is within
+      2e-2 + 1e-2 |logit| of the oracle's; at least 256 steps compared;
+    - hidden state (the final norm's input) at the fixture checkpoints with
+      no routing difference in the window before them:
+      |got - ref| <= 2e-2 + 1e-2 |ref|.
+    Free-running (the production path, no trace or forcing): ids equal the
+    oracle's up to the first step with a margin of at most 1e-2 or after a
+    router near-tie.
     run "1" takes the persistent cooperative decode (UOCR_HIP_RUN=1) where
     the profile has one; "0" the per-step kernel path."""
     import sys
@@ -395,37 +405,44 @@ def test_config5_full_decode_matches_oracle(gpu, monkeypatch, profile, run):
 
     uocr = gpu
     fx = np.load(golden / f"config5_{profile}.npz")
-    ref, margins, trace, rmargin = fx["ids"], fx["margins"], fx["trace"], fx["router_margin"]
+    ref, margins, top, trace, gap = fx["ids"], fx["margins"], fx["top"], fx["trace"], fx["router_gap"]
     steps = ref.size
     monkeypatch.setenv("UOCR_HIP_RUN", run)
     m = model(uocr, make_config5.PROFILES[profile])
     ids, mask, rows = make_config5.config5_prompt()
     with uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=1024, max_gen_tokens=steps) as eng:
-        eng.trace_enable(trace.shape[0])
-        got, _, _, _ = eng.generate_embeddings(ids, mask, rows, max_new_tokens=steps, flags=uocr.GEN_IGNORE_EOS)
+        free, _, _, _ = eng.generate_embeddings(ids, mask, rows, max_new_tokens=steps, flags=uocr.GEN_IGNORE_EOS)
+        # step t selects from the hidden state of forward pass t - 1
+        tie = np.concatenate([[False], gap[:-1].min(axis=1) <= ROUTER_TIE])
+        amb = (margins <= 1e-2) | np.maximum.accumulate(tie)
+        first_amb = int(np.argmax(amb)) if amb.any() else steps
+        assert free[:first_amb].tolist() == ref[:first_amb].tolist(), "free-running ids before the first ambiguous step"
+
+        eng.trace_force(ref)
+        eng.trace_enable(steps - 1)
+        got, score, _, _ = eng.generate_embeddings(ids, mask, rows, max_new_tokens=steps, flags=uocr.GEN_IGNORE_EOS)
         sel, hidden = eng.trace_read()
         assert got.shape == (steps,)
-        agree = int(np.argmin(got == ref)) if (got != ref).any() else steps
-        if agree < steps:
-            assert margins[agree] <= 1e-2, f"step {agree}: got {got[agree]}, oracle {ref[agree]} " \
-                                           f"(margin {margins[agree]:.4f})"
-        assert agree >= 128, f"ids agree for {agree} steps only"
-        routed = 0
-        for t in range(min(trace.shape[0], agree)):
-            for layer in range(11):
-                if rmargin[t, layer] > 1e-2:
-                    assert sorted(sel[t, layer]) == sorted(trace[t, layer]), f"step {t} layer {layer + 1}"
-                    routed += 1
-        assert routed >= 100
+        flipped = np.zeros(steps + FLIP_WINDOW, bool)
+        for t in range(steps - 1):
+            diff = [layer for layer in range(11) if sorted(sel[t, layer]) != sorted(trace[t, layer])]
+            if diff:
+                assert gap[t, diff[0]] <= ROUTER_TIE, \
+                    f"forward {t} layer {diff[0] + 1}: experts {sorted(sel[t, diff[0]])} vs oracle " \
+                    f"{sorted(trace[t, diff[0]])} at set margin {gap[t, diff[0]]:.4f}"
+                flipped[t + 1:t + 1 + FLIP_WINDOW] = True
+        comparable = (margins > 1e-2) & ~flipped[:steps]
+        bad = np.flatnonzero(comparable & (got != ref))
+        assert bad.size == 0, f"forced steps {bad[:8].tolist()}: got {got[bad[:8]].tolist()}, oracle {ref[bad[:8]].tolist()}"
+        np.testing.assert_allclose(score[comparable], top[comparable], atol=2e-2, rtol=1e-2)
+        assert int(comparable.sum()) >= 256, f"only {int(comparable.sum())} steps compared"
         checked = 0
         for k, href in zip(fx["hidden_steps"], fx["hidden"]):
             k = int(k)
-            if k > agree:
+            if flipped[k]:
                 continue
             if k + 1 < steps:
-                part, _, _, _ = eng.generate_embeddings(ids, mask, rows, max_new_tokens=k + 1,
-                                                        flags=uocr.GEN_IGNORE_EOS)
-                assert part.tolist() == got[:k + 1].tolist()
+                eng.generate_embeddings(ids, mask, rows, max_new_tokens=k + 1, flags=uocr.GEN_IGNORE_EOS)
                 _, h = eng.trace_read()
             else:
                 h = hidden

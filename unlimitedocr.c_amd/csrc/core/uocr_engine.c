@@ -502,3 +502,14 @@ int uocr_engine_trace_read(uocr_engine *e, uint32_t *expert_ids, uint16_t *hidde
     }
     return UOCR_OK;
 }
+
+int uocr_engine_trace_force(uocr_engine *e, const int32_t *ids, uint32_t n) {
+    const int st = hip_ready(e);
+    if (st != UOCR_OK) return st;
+    if (n > e->max_gen_tokens) return set_error(e, UOCR_ERROR_INVALID_ARGUMENT, "forcing %u ids exceeds max_gen_tokens", n);
+    char herr[512] = {0};
+    if (!uocr_hip_context_trace_force(e->hip, ids, n, herr, sizeof(herr))) {
+        return set_error(e, UOCR_ERROR_INVALID_ARGUMENT, "teacher forcing setup failed: %s", herr);
+    }
+    return UOCR_OK;
+}

@@ -69,6 +69,10 @@ uint64_t uocr_hip_context_weight_bytes(const uocr_hip_ctx *ctx);
  * steps = 0 turns it off.  The graph path records through its eager per-step
  * loop; the persistent run records in place. */
 int uocr_hip_context_trace_enable(uocr_hip_ctx *ctx, uint32_t steps, char *err, size_t err_size);
+/* Teacher forcing for parity tests: the following generations embed ids[t]
+ * after decode step t < n instead of the token they select (which they still
+ * report); n = 0 turns it off. */
+int uocr_hip_context_trace_force(uocr_hip_ctx *ctx, const int32_t *ids, uint32_t n, char *err, size_t err_size);
 int uocr_hip_context_trace_read(uocr_hip_ctx *ctx, uint32_t *expert_ids, uint16_t *hidden, char *err, size_t err_size);
 
 #ifdef __cplusplus

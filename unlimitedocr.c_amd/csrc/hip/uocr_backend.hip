@@ -44,6 +44,7 @@ struct dev_layer {
     const uint16_t *in_norm, *post_norm, *router;
     const float *rfold; /* [1280][64] router * post_norm, or NULL (router kernel) */
     const float *rfold_all; /* the same fold whatever its range (the persistent run sums it in fp32) */
+    const float *rfold_o;   /* [1280][64] O^T rfold_all (persistent run) */
     uocr_expert_slab slab;
 };
 
@@ -130,6 +131,8 @@ struct uocr_hip_ctx {
     uint32_t trace_steps;
     uint32_t *d_trace;           /* [trace_steps][11][6] expert ids */
     int32_t trace_step;          /* step being enqueued by the eager loop (-1: none) */
+    int32_t *d_force;            /* teacher-forced token ids (uocr_hip_context_trace_force) */
+    uint32_t force_n;
 };
 
 #define OP_TIMER_MAX 96
@@ -276,6 +279,7 @@ extern "C" void uocr_hip_context_destroy(uocr_hip_ctx *ctx) {
     release_runtime(ctx);
     if (ctx->warena != nullptr) (void)hipFree(ctx->warena);
     if (ctx->d_trace != nullptr) (void)hipFree(ctx->d_trace);
+    if (ctx->d_force != nullptr) (void)hipFree(ctx->d_force);
     (void)hipStreamDestroy(ctx->stream);
     free(ctx);
 }
@@ -414,6 +418,10 @@ static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
             m.qf = D.gate.qtype;
         } else {
             R.fold = D.rfold_all;
+            R.fold_o = D.rfold_o;
+            if (R.fold != nullptr && R.fold_o != nullptr) {
+                HIPCHK(uocr_run_fold_o(nullptr, D.o.qtype, D.o.w, D.o.s, R.fold, (float *)R.fold_o), "router fold_o");
+            }
             R.sg = D.sgate.w;
             R.su = D.sup.w;
             R.sd = D.sdown.w;
@@ -430,7 +438,7 @@ static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
             R.gu_s_stride = D.slab.gu_s_stride;
             R.dn_w_stride = D.slab.dn_w_stride;
             R.dn_s_stride = D.slab.dn_s_stride;
-            ok = ok && R.fold != nullptr;
+            ok = ok && R.fold != nullptr && R.fold_o != nullptr;
             for (const uocr_qmat *q : {&D.sgate, &D.sup, &D.sdown, &D.slab.gate, &D.slab.up, &D.slab.down}) {
                 ok = ok && q->qtype == ctx->L[0].gate.qtype;
             }
@@ -485,7 +493,7 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
         } else {
             total += tensor_bytes(L.router) + tensor_bytes(L.sgate) + tensor_bytes(L.sup) + tensor_bytes(L.sdown);
             total += UOCR_ROUTED_EXPERTS * (tensor_bytes(L.egate[0]) + tensor_bytes(L.eup[0]) + tensor_bytes(L.edown[0]));
-            total += align256((uint64_t)H_SIZE * UOCR_ROUTED_EXPERTS * 4u);
+            total += 2u * align256((uint64_t)H_SIZE * UOCR_ROUTED_EXPERTS * 4u); /* fold, fold_o */
         }
     }
     const uint64_t run_model_off = total;
@@ -534,6 +542,9 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
             return 0;
         }
         if (ws2 != sl.gu_w_stride || ss2 != sl.gu_s_stride) return bfail(err, err_size, "expert gate/up slabs differ in stride");
+    }
+    for (uint32_t l = 1; l < UOCR_DECODER_LAYERS; ++l) {
+        ctx->L[l].rfold_o = (const float *)(ctx->warena + p.take((uint64_t)H_SIZE * UOCR_ROUTED_EXPERTS * 4u));
     }
     if (p.off > run_model_off) return bfail(err, err_size, "weight arena overflow");
     ctx->d_run_model = (uocr_run_model *)(ctx->warena + run_model_off);
@@ -1021,7 +1032,8 @@ static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, u
         const uint32_t end = issued + DECODE_CHUNK < N ? issued + DECODE_CHUNK : N;
         const hipError_t e = uocr_run_launch(s, c->d_run_model, &c->run_model, c->run_arena, c->kc, c->vc, c->cache_cap,
                                              (int32_t)P, (int32_t)issued, (int32_t)(end - issued), end == N ? 1 : 0,
-                                             tag0 + issued, c->tokens, c->scores, c->h, c->d_trace, c->trace_steps);
+                                             tag0 + issued, c->tokens, c->scores, c->h, c->d_trace, c->trace_steps,
+                                             c->d_force, c->force_n);
         if (e != hipSuccess) {
             ok = bfail(err, err_size, "decode run of steps %u-%u: %s", issued, end - 1u, hipGetErrorString(e));
             break;
@@ -1096,9 +1108,22 @@ static int decode_timed(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos,
         ok = bfail(err, err_size, "decode state init failed");
     }
     c->tm = timed ? t : nullptr;
+    /* teacher forcing: the finalize launch selects and embeds the step's own
+     * token, then the forced token's row replaces it */
+    const int fold_select = c->fold_select;
+    if (c->force_n != 0u) c->fold_select = 0;
     for (uint32_t step = 0; ok && step < N && !eos; ++step) {
         c->trace_step = (int32_t)step;
-        const hipError_t e = step + 1u < N ? enqueue_decode_step(c) : enqueue_select(c, true);
+        hipError_t e;
+        if (step + 1u == N) {
+            e = enqueue_select(c, true);
+        } else if (step < c->force_n) {
+            e = enqueue_select(c, false);
+            if (e == hipSuccess) e = uocr_launch_embed(s, c->embed, UOCR_VOCAB_SIZE, c->d_force + step, nullptr, c->h);
+            if (e == hipSuccess) e = enqueue_layers(c, false);
+        } else {
+            e = enqueue_decode_step(c);
+        }
         if (e != hipSuccess || hipMemcpyAsync(c->h_tokens + step, c->tokens + step, 4u, hipMemcpyDeviceToHost, s) != hipSuccess ||
             hipStreamSynchronize(s) != hipSuccess) {
             ok = bfail(err, err_size, "timed decode step %u failed", step);
@@ -1109,6 +1134,7 @@ static int decode_timed(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos,
     }
     c->tm = nullptr;
     c->trace_step = -1;
+    c->fold_select = fold_select;
     for (int i = 0; i < made; ++i) (void)hipEventDestroy(t->ev[i]);
     free(t);
     if (!ok) return 0;
@@ -1210,7 +1236,7 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
     const bool timed = c->profile_detail >= 3 && c->profile != nullptr && c->profile->report.enabled != 0u;
     const bool use_run = c->run_ok && use_graph && !timed && (req->flags & UOCR_GEN_NO_RUN) == 0u;
     if (use_run) return decode_run(c, P, N, ignore_eos, t0, t1, dg, res, err, err_size);
-    if (timed || c->trace_steps != 0u) return decode_timed(c, P, N, ignore_eos, t0, t1, dg, timed, res, err, err_size);
+    if (timed || c->trace_steps != 0u || c->force_n != 0u) return decode_timed(c, P, N, ignore_eos, t0, t1, dg, timed, res, err, err_size);
     HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf), "decode state init");
     uint32_t count = 0, scanned = 0;
     int eos = 0;
@@ -1297,6 +1323,26 @@ extern "C" int uocr_hip_context_trace_enable(uocr_hip_ctx *c, uint32_t steps, ch
     HIPCHK(hipMemsetAsync(c->d_trace, 0xff, bytes, c->stream), "trace buffer clear");
     HIPCHK(hipStreamSynchronize(c->stream), "trace buffer clear sync");
     c->trace_steps = steps;
+    return 1;
+}
+
+extern "C" int uocr_hip_context_trace_force(uocr_hip_ctx *c, const int32_t *ids, uint32_t n, char *err,
+                                            size_t err_size) {
+    if (c == nullptr || (n != 0u && ids == nullptr)) return bfail(err, err_size, "invalid trace_force request");
+    HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+    HIPCHK(hipStreamSynchronize(c->stream), "stream sync");
+    if (c->d_force != nullptr) {
+        (void)hipFree(c->d_force);
+        c->d_force = nullptr;
+    }
+    c->force_n = 0u;
+    if (n == 0u) return 1;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (ids[i] < 0 || ids[i] >= (int32_t)UOCR_VOCAB_SIZE) return bfail(err, err_size, "forced id %u out of vocabulary", i);
+    }
+    HIPCHK(counted_malloc(c, (void **)&c->d_force, (size_t)n * 4u), "forced id allocation");
+    HIPCHK(hipMemcpy(c->d_force, ids, (size_t)n * 4u, hipMemcpyHostToDevice), "forced id upload");
+    c->force_n = n;
     return 1;
 }
 

@@ -54,7 +54,7 @@ struct RunLayerD {
     const AS1 uint8_t *q, *k, *v, *o;
     const AS1 uint16_t *qs, *ks, *vs, *os;
     const AS1 uint16_t *in_norm, *post_norm;
-    const AS1 float *fold;
+    const AS1 float *fold, *fold_o;
     const AS1 uint8_t *gate, *up, *down;
     const AS1 uint16_t *gs, *us, *ds;
     const AS1 uint8_t *sg, *su, *sd;
@@ -94,6 +94,7 @@ constexpr u32 TOPK = UOCR_K_TOPK, EI = 896u, SI = 1792u, DI = 6848u, VOCAB = 129
 constexpr u32 QKV_BLOCKS = 240u;  /* 1920 items / 8 */
 constexpr u32 ATT_SPLITS = 8u, ATT_BLOCKS = NHEAD * ATT_SPLITS, ATT0 = NB - ATT_BLOCKS;
 constexpr u32 O_BLOCKS = 40u, O_ROWS = 32u, O0 = ATT0 - O_BLOCKS;
+constexpr u32 Z_BLOCKS = 16u, Z_COLS = HID / Z_BLOCKS; /* O blocks j < 16 also publish z partials */
 constexpr u32 GU_ROUTED = 192u, GU_ROWS = 28u, DGU_ROWS = 27u;
 constexpr u32 DN_BLOCKS = 160u, DN_ROWS = 8u;
 constexpr u32 LM_ROWS = VOCAB / NB;
@@ -105,7 +106,7 @@ static_assert(O0 >= 0u && O0 + O_BLOCKS <= QKV_BLOCKS, "O blocks also gather h i
 /* packets per copy */
 constexpr u32 PQKV_B = 3u, PQKV = QKV_BLOCKS * PQKV_B;
 constexpr u32 PATT_B = 23u, PATT = ATT_BLOCKS * PATT_B;
-constexpr u32 PO_A = 6u, PO_Z = 22u, PO_B = PO_A + PO_Z, PO = O_BLOCKS * PO_B;
+constexpr u32 PO_A = 6u, PO_Z = 22u, PO_AR = O_BLOCKS * PO_A, PO = PO_AR + Z_BLOCKS * PO_Z;
 constexpr u32 PMID_B = 5u, PMID = NB * PMID_B;
 constexpr u32 PH_B = 2u, PH = DN_BLOCKS * PH_B;
 constexpr u32 PLM = NB;
@@ -121,6 +122,12 @@ __host__ __device__ constexpr u64 off_mid(u32 l) { return off_o(l) + (u64)PO * N
 __host__ __device__ constexpr u64 off_h(u32 l) { return off_mid(l) + (u64)PMID * NREP; }
 constexpr u64 ARENA_PK = off_layer(UOCR_RUN_LAYERS);
 
+#ifndef UOCR_RUN_SLEEP
+#define UOCR_RUN_SLEEP 1
+#endif
+#ifndef UOCR_RUN_ZPROBE
+#define UOCR_RUN_ZPROBE 0
+#endif
 #ifndef UOCR_RUN_LIMIT_TICKS
 #define UOCR_RUN_LIMIT_TICKS 5000000ull /* 50 ms of s_memrealtime (100 MHz) */
 #endif
@@ -211,6 +218,8 @@ struct Run {
     h16 *hout;      /* layer 11's output of every step (plain stores) */
     u32 *trace;     /* expert ids [t][11][6] for t < trace_steps, or NULL */
     u32 trace_steps;
+    const int32_t *force; /* teacher-forced ids for t < force_n, or NULL */
+    u32 force_n;
     unsigned long long *tl; /* timeline of this step, or NULL */
 };
 
@@ -267,7 +276,7 @@ __device__ __forceinline__ bool gather(const Run &R, const uint4 *region, u32 pe
     if (pend != 0u) {
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         for (u32 it = 1; pend != 0u; ++it) {
-            __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_s_sleep(UOCR_RUN_SLEEP);
 #pragma unroll
             for (int k = 0; k < MAXP; ++k) {
                 if (pend & (1u << k)) v[k] = cload16(rep, phys(t + (u32)k * NT) * 16u);
@@ -297,6 +306,74 @@ __device__ __forceinline__ bool gather(const Run &R, const uint4 *region, u32 pe
      * divergent (per-layer pointers then come through vector loads and
      * full waits) */
     return __builtin_amdgcn_readfirstlane(__syncthreads_or(bad)) == 0;
+}
+
+/* gather() by wavefront `wave` alone (the others pass straight through):
+ * its polls do not queue behind loads the other wavefronts have in flight.
+ * The polls are LDS-direct loads into stg ([MAXP][64] packets, 16-byte
+ * aligned LDS), so packets in flight take no registers.  No barrier: the
+ * caller synchronises before the sinks' LDS writes are read.  The result
+ * (false: the run aborted) is uniform in the wavefront. */
+template <int MAXP, typename Phys>
+__device__ __forceinline__ void gather_wave_issue(const Run &R, const uint4 *region, u32 per_copy, u32 n, u32 wave,
+                                                  uint4 *stg, Phys phys) {
+    if (__builtin_amdgcn_readfirstlane(tid_() / 64u) != wave) return;
+    const __amdgpu_buffer_rsrc_t rs = rsrc(region + (size_t)R.xcc * per_copy);
+    const u32 t = tid_() % 64u;
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k) {
+        if (t + (u32)k * 64u < n) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(stg + k * 64), 16u,
+                                                     phys(t + (u32)k * 64u) * 16u, 0u, 0u, 16u);
+        }
+    }
+}
+
+/* PRE: gather_wave_issue() has issued the first round of polls into stg. */
+template <int MAXP, bool PRE = false, typename Phys, typename Sink>
+__device__ __forceinline__ bool gather_wave(const Run &R, const uint4 *region, u32 per_copy, u32 n, u32 tag, u32 where,
+                                            u32 step, u32 wave, uint4 *stg, Phys phys, Sink sink) {
+    if (__builtin_amdgcn_readfirstlane(tid_() / 64u) != wave) return true;
+    const uint4 *rep = region + (size_t)R.xcc * per_copy;
+    const u32 t = tid_() % 64u;
+    const __amdgpu_buffer_rsrc_t rs = rsrc(rep);
+    u32 pend = 0u;
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k) pend |= t + (u32)k * 64u < n ? (1u << k) : 0u;
+    int bad = 0;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (u32 it = 1;; ++it) {
+#pragma unroll
+        for (int k = 0; k < MAXP; ++k) {
+            if (!(PRE && it == 1u) && (pend & (1u << k))) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(stg + k * 64),
+                                                         16u, phys(t + (u32)k * 64u) * 16u, 0u, 0u, 16u);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < MAXP; ++k) {
+            if ((pend & (1u << k)) && stg[k * 64 + t].x == tag) pend &= ~(1u << k);
+        }
+        if (__builtin_amdgcn_readfirstlane(__builtin_amdgcn_ballot_w64(pend != 0u) == 0ull)) break;
+        __builtin_amdgcn_s_sleep(1);
+        if ((it & 15u) == 0u) {
+            if (cload32(R.ctl, UOCR_RUN_CTL_ABORT * 4u) != 0u ||
+                __builtin_amdgcn_s_memrealtime() - t0 > UOCR_RUN_LIMIT_TICKS) {
+                if (cload32(R.ctl, UOCR_RUN_CTL_ABORT * 4u) == 0u && t == 0u) give_up(R.ctl, where, step);
+                bad = 1;
+                break;
+            }
+        }
+    }
+    bad = __builtin_amdgcn_readfirstlane(bad);
+    if (bad == 0) {
+#pragma unroll
+        for (int k = 0; k < MAXP; ++k) {
+            if (t + (u32)k * 64u < n) sink(t + (u32)k * 64u, stg[k * 64 + t]);
+        }
+    }
+    return bad == 0;
 }
 
 /* Threads t < npk * NREP store packet t / NREP of the block into copy
@@ -346,6 +423,38 @@ __device__ __forceinline__ uint4 norm_piece(const AS1 uint16_t *nw) {
 /* RMSNorm of the LDS vector x into xs with the weight piece w of norm_piece
  * (eps 1e-6, fp32 sum of squares, one rounding per element;
  * norm.metal:12-40); returns inv_rms. */
+/* Deferred RMSNorm: xs = fp16(x * w) and each wavefront's sum of x^2 in
+ * red[wave]; after the caller's barrier rms_inv(red) gives 1 / rms(x), and
+ * a dot over xs times it is the dot over the normalised row (the norm is
+ * linear in 1 / rms), so the dots do not wait for the block reduction. */
+__device__ __forceinline__ void rms_defer(const h16 *x, uint4 w, h16 *xs, float *red) {
+    union h8 {
+        uint4 u;
+        h16 h[8];
+    } xv, wv;
+    const u32 t = tid_();
+    float ss = 0.0f;
+    if (t < HID / 8u) {
+        xv.u = ((const uint4 *)x)[t];
+        wv.u = w;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float f = (float)xv.h[j];
+            ss = fmaf(f, f, ss);
+            xv.h[j] = (h16)(f * (float)wv.h[j]);
+        }
+        ((uint4 *)xs)[t] = xv.u;
+    }
+    ss = wave_sum(ss);
+    if ((t & 63u) == 0u) red[t >> 6] = ss;
+}
+__device__ __forceinline__ float rms_inv(const float *red) {
+    float s = 0.0f;
+#pragma unroll
+    for (u32 w = 0; w < NT / 64u; ++w) s += red[w];
+    return __builtin_amdgcn_rsqf(s / (float)HID + 1.0e-6f);
+}
+
 __device__ __forceinline__ float rms_lds(const h16 *x, uint4 w, h16 *xs, float *red) {
     union h8 {
         uint4 u;
@@ -399,7 +508,7 @@ __device__ __forceinline__ uint4 embed8(const AS1 uint8_t *EW, const AS1 uint16_
 
 struct Lds {
     h16 *xs, *hres, *outv;
-    float *red, *zout, *selw;
+    float *red, *zout, *selw, *zw;
     u32 *selid;
     unsigned long long *keyw;
     uint8_t *scr;
@@ -445,7 +554,8 @@ __device__ bool lm_stage(const Run &R, const Lds &S, u32 tag, u32 htag, int32_t 
         return false;
     }
     TLR(0u);
-    rms_lds(S.hres, nwp, S.xs, S.red);
+    rms_defer(S.hres, nwp, S.xs, S.red);
+    __syncthreads();
     TLR(128u + 13u);
     const u32 row0 = blockIdx.x * LM_ROWS;
     float bs = -INFINITY;
@@ -477,7 +587,9 @@ __device__ bool lm_stage(const Run &R, const Lds &S, u32 tag, u32 htag, int32_t 
             bid = oid;
         }
     }
-    if (lane == 0u) S.keyw[wave] = argmax_key(bs, bid);
+    /* the rows were compared before the positive factor 1 / rms, which
+     * scales the winner's logit */
+    if (lane == 0u) S.keyw[wave] = argmax_key(bs * rms_inv(S.red), bid);
     __syncthreads();
     unsigned long long k = S.keyw[0];
 #pragma unroll
@@ -568,7 +680,8 @@ __device__ bool qkv_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag,
             R.tokens[t] = tok;
             if (R.scores != nullptr) R.scores[t] = score;
         }
-        if (tid_() < HID / 8u) ((uint4 *)hres)[tid_()] = embed8<QE>(R.M->emb, R.M->embs, tok, tid_());
+        const int32_t etok = R.force != nullptr && (u32)t < R.force_n ? R.force[t] : tok;
+        if (tid_() < HID / 8u) ((uint4 *)hres)[tid_()] = embed8<QE>(R.M->emb, R.M->embs, etok, tid_());
         __syncthreads();
     } else {
         if (!gather<(PH + NT - 1u) / NT>(R, R.pk + off_h(l - 1u), PH, PH, tag, W_QKV, (u32)t, [](u32 i) { return i; },
@@ -577,9 +690,10 @@ __device__ bool qkv_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag,
         }
     }
     TLR(2u * (1u + 5u * l));
-    rms_lds(S.hres, nwp, S.xs, S.red);
+    rms_defer(S.hres, nwp, S.xs, S.red);
+    __syncthreads();
     TLD(l, 0u);
-    const float dd = group_sum<G::LPR>(frag_dot<QA, G::LPR, G::J>(F.f, S.xs, G::C, sub));
+    const float dd = group_sum<G::LPR>(frag_dot<QA, G::LPR, G::J>(F.f, S.xs, G::C, sub)) * rms_inv(S.red);
     const float da = lane_f(dd, 0), db = lane_f(dd, 32);
     TLD(l, 1u);
     if (lane == 0u) {
@@ -794,15 +908,40 @@ template <int QA>
 struct OCfg {
     static constexpr u32 C = chunks_per_row<QA>(HID), LPR = 32u, J = (C + LPR - 1u) / LPR;
     static constexpr u32 NG = NT / LPR, RPG = O_ROWS / NG;
-    static constexpr u32 ZR = O_ROWS / (NT / 64u); /* rows per thread in the z partial */
-    static_assert(RPG * NG == O_ROWS && ZR * (NT / 64u) == O_ROWS, "O rows per group");
+    static constexpr u32 ZC = Z_COLS / (NT / 64u); /* columns per thread in a z partial */
+    static_assert(RPG * NG == O_ROWS && ZC * (NT / 64u) == Z_COLS && Z_BLOCKS <= O_BLOCKS, "O rows per group");
 };
 
 template <int QA>
 struct OFrags {
     RowFrag<OCfg<QA>::J> f[OCfg<QA>::RPG];
-    float fw[OCfg<QA>::ZR];
 };
+
+/* z-partial weights of O block j < Z_BLOCKS (MoE layers): rows
+ * [80j, 80j + 80) of fold and of fold_o, two contiguous 20 KB ranges,
+ * copied into LDS (zw[0], zw[1]) by LDS-direct loads, so they take no
+ * registers while the O stage waits; complete once the issuing thread's
+ * later loads have returned (loads return in order). */
+constexpr u32 ZW_BYTES = Z_COLS * NEXP * 4u;
+static_assert(ZW_BYTES % (64u * 16u) == 0u, "z weights in whole wavefront copies");
+
+__device__ __forceinline__ void o_load_z(const Run &R, u32 l, float *zw) {
+    const u32 b = blockIdx.x;
+    if (l == 0u || b < O0 || b >= O0 + Z_BLOCKS) return;
+    const AS4 RunLayerD &L = R.M->L[l];
+    const u32 j = b - O0, wave = __builtin_amdgcn_readfirstlane(tid_() / 64u), lane = tid_() % 64u;
+    const AS1 uint8_t *src[2] = {(const AS1 uint8_t *)L.fold + (size_t)j * ZW_BYTES,
+                                 (const AS1 uint8_t *)L.fold_o + (size_t)j * ZW_BYTES};
+#pragma unroll
+    for (u32 a = 0; a < 2u; ++a) {
+#pragma unroll
+        for (u32 off = wave * 1024u; off < ZW_BYTES; off += NT * 16u) {
+            __builtin_amdgcn_global_load_lds((const AS1 void *)(src[a] + off + lane * 16u),
+                                             (__attribute__((address_space(3))) void *)((uint8_t *)zw + a * ZW_BYTES + off),
+                                             16u, 0, 0);
+        }
+    }
+}
 
 template <int QA>
 __device__ __forceinline__ void o_load(const Run &R, u32 l, OFrags<QA> &F) {
@@ -816,11 +955,6 @@ __device__ __forceinline__ void o_load(const Run &R, u32 l, OFrags<QA> &F) {
         const u32 r = j * O_ROWS + g * G::RPG + k;
         frag_load<QA, G::LPR, G::J>(F.f[k], gp<uint8_t>(L.o) + (size_t)r * 16u * G::C, H(L.os) + (size_t)r * (HID / 64u),
                                     G::C, sub);
-    }
-    if (l > 0u) {
-        const u32 e = tid_() % 64u, q = tid_() / 64u;
-#pragma unroll
-        for (u32 k = 0; k < G::ZR; ++k) F.fw[k] = gp<float>(L.fold)[(size_t)(j * O_ROWS + G::ZR * q + k) * NEXP + e];
     }
 }
 
@@ -857,6 +991,9 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
         const float lf = mk == -INFINITY ? 0.0f : lk * fexp(mk - M);
         wk[tid_()] = lf * frcp(group_sum<ATT_SPLITS>(lf));
     }
+    /* the z weights' LDS-direct loads (o_load_z) are complete in every
+     * wavefront before the barrier */
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     TLD(l, 6u);
     if (tid_() < HID / 8u) {
@@ -882,20 +1019,20 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
     }
     __syncthreads();
     TLD(l, 7u);
-#pragma unroll
-    for (u32 k = 0; k < G::RPG; ++k) {
-        const u32 rl = g * G::RPG + k, r = j * O_ROWS + rl;
-        const float d = group_sum<G::LPR>(frag_dot<QA, G::LPR, G::J>(F.f[k], S.xs, G::C, sub));
-        if (sub == 0u) S.outv[rl] = (h16)(d + (float)S.hres[r]);
-    }
-    __syncthreads();
-    TLD(l, 8u);
-    const bool moe = l > 0u;
-    if (moe) {
+    if (l > 0u && j < Z_BLOCKS) {
+        /* the router's pre-norm logits are linear in h and ctx:
+         * z = fold^T a = fold^T h + (O^T fold)^T ctx.  This block's partial
+         * over columns [80j, 80j + 80) goes out before the O rows, so the
+         * GU stage can choose the experts while the rows are computed. */
         const u32 e = tid_() % 64u, q = tid_() / 64u;
+        const float *zf = S.zw, *zo = S.zw + Z_COLS * NEXP;
         float z = 0.0f;
 #pragma unroll
-        for (u32 k = 0; k < G::ZR; ++k) z = fmaf(F.fw[k], (float)S.outv[G::ZR * q + k], z);
+        for (u32 k = 0; k < G::ZC; ++k) {
+            const u32 cl = G::ZC * q + k, c = j * Z_COLS + cl;
+            z = fmaf(zf[cl * NEXP + e], (float)S.hres[c], z);
+            z = fmaf(zo[cl * NEXP + e], (float)S.xs[c], z);
+        }
         zq[q * 64u + e] = z;
         __syncthreads();
         if (tid_() < 64u) {
@@ -906,13 +1043,21 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
             S.zout[e2] = zs;
         }
         __syncthreads();
+        publish(R, R.pk + off_o(l), PO, PO_AR + j * PO_Z, PO_Z, tag, [&](u32 p) {
+            const u32 z0 = 3u * p;
+            return make_uint3(__float_as_uint(S.zout[z0]), __float_as_uint(z0 + 1u < NEXP ? S.zout[z0 + 1u] : 0.0f),
+                              __float_as_uint(z0 + 2u < NEXP ? S.zout[z0 + 2u] : 0.0f));
+        });
     }
-    publish(R, R.pk + off_o(l), PO, j * PO_B, moe ? PO_B : PO_A, tag, [&](u32 p) {
-        if (p < PO_A) return pay6(S.outv, p, O_ROWS);
-        const u32 z0 = 3u * (p - PO_A);
-        return make_uint3(__float_as_uint(S.zout[z0]), __float_as_uint(z0 + 1u < NEXP ? S.zout[z0 + 1u] : 0.0f),
-                          __float_as_uint(z0 + 2u < NEXP ? S.zout[z0 + 2u] : 0.0f));
-    });
+#pragma unroll
+    for (u32 k = 0; k < G::RPG; ++k) {
+        const u32 rl = g * G::RPG + k, r = j * O_ROWS + rl;
+        const float d = group_sum<G::LPR>(frag_dot<QA, G::LPR, G::J>(F.f[k], S.xs, G::C, sub));
+        if (sub == 0u) S.outv[rl] = (h16)(d + (float)S.hres[r]);
+    }
+    __syncthreads();
+    TLD(l, 8u);
+    publish(R, R.pk + off_o(l), PO, j * PO_A, PO_A, tag, [&](u32 p) { return pay6(S.outv, p, O_ROWS); });
     TLR(2u * (3u + 5u * l) + 1u);
     return true;
 }
@@ -940,7 +1085,10 @@ __device__ __forceinline__ void gu_rows(GuFrags<QF> &F, const uint8_t *GW, const
     const u32 grp = tid_() / G::LPR, sub = tid_() % G::LPR;
 #pragma unroll
     for (u32 k = 0; k < G::RPG; ++k) {
-        const u32 r = row0 + min(grp + k * G::NG, nrows - 1u);
+        /* groups past the last row load nothing (their dots are discarded),
+         * which leaves the last wavefront free of loads in the MoE layers */
+        if (grp + k * G::NG >= nrows) continue;
+        const u32 r = row0 + grp + k * G::NG;
         const u32 rr = min(r, maxrow - 1u);
         frag_load<QF, G::LPR, G::J, NTL>(F.g[k], GW + (size_t)rr * 16u * G::C, GS + (size_t)rr * (HID / 64u), G::C, sub);
         frag_load<QF, G::LPR, G::J, NTL>(F.u[k], UW + (size_t)rr * 16u * G::C, US + (size_t)rr * (HID / 64u), G::C, sub);
@@ -960,6 +1108,40 @@ __device__ __forceinline__ void gu_load_static(const Run &R, u32 l, GuFrags<QF> 
         gu_rows<QF, false>(F, gp<uint8_t>(L.sg), H(L.sgs), gp<uint8_t>(L.su), H(L.sus), (b - GU_ROUTED) * GU_ROWS,
                            GU_ROWS, SI);
     }
+}
+
+/* A descriptor value read early and made opaque, so the compiler keeps it in
+ * a register instead of re-reading it (a scalar load that can miss the
+ * scalar cache) where it is used. */
+template <typename T>
+__device__ __forceinline__ T pin(T v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
+/* Expert slab pointers and strides of one layer, read at the GU stage's
+ * start, ahead of the loads that need them. */
+struct SlabD {
+    const AS1 uint8_t *eg, *eu, *ed, *sd;
+    const AS1 uint16_t *egs, *eus, *eds, *sds;
+    uint64_t gws, gss, dws, dss;
+};
+
+__device__ __forceinline__ SlabD slab_of(const AS4 RunLayerD &L) {
+    SlabD d;
+    d.eg = pin(L.eg);
+    d.eu = pin(L.eu);
+    d.ed = pin(L.ed);
+    d.sd = pin(L.sd);
+    d.egs = pin(L.egs);
+    d.eus = pin(L.eus);
+    d.eds = pin(L.eds);
+    d.sds = pin(L.sds);
+    d.gws = pin(L.gu_w_stride);
+    d.gss = pin(L.gu_s_stride);
+    d.dws = pin(L.dn_w_stride);
+    d.dss = pin(L.dn_s_stride);
+    return d;
 }
 
 /* DN rows: wavefront w of block b owns output row 8b + w.  Its chunks are
@@ -989,10 +1171,9 @@ __device__ __forceinline__ u32 dn_row() {
 
 /* Routed down rows of the selected experts (ids in LDS) and the shared down row. */
 template <int QF>
-__device__ __forceinline__ void dn_load(const Run &R, const Lds &S, u32 l, DnFrags<QF> &F) {
+__device__ __forceinline__ void dn_load(const Run &R, const Lds &S, const SlabD &L, DnFrags<QF> &F) {
     typedef DnCfg<QF> G;
     if (blockIdx.x >= DN_BLOCKS) return;
-    const AS4 RunLayerD &L = R.M->L[l];
     const u32 c = dn_row(), lane = tid_() & 63u;
     constexpr u32 CPG = chunks_per_group<QF>();
 #pragma unroll
@@ -1000,9 +1181,9 @@ __device__ __forceinline__ void dn_load(const Run &R, const Lds &S, u32 l, DnFra
         const u32 q = min(lane + 64u * j, G::CT - 1u);
         if (q < TOPK * G::CR) {
             const u32 r = q / G::CR, cc = q % G::CR, e = S.selid[r];
-            const uint8_t *W = gp<uint8_t>(L.ed) + e * L.dn_w_stride + (size_t)c * 16u * G::CR + 16u * cc;
+            const uint8_t *W = gp<uint8_t>(L.ed) + e * L.dws + (size_t)c * 16u * G::CR + 16u * cc;
             F.f.w[j] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4v *)W));
-            if (QF != 1) F.f.s[j] = __builtin_nontemporal_load(H(L.eds) + e * L.dn_s_stride + (size_t)c * (EI / 64u) + cc / CPG);
+            if (QF != 1) F.f.s[j] = __builtin_nontemporal_load(H(L.eds) + e * L.dss + (size_t)c * (EI / 64u) + cc / CPG);
         } else {
             const u32 cc = q - TOPK * G::CR;
             F.f.w[j] = *(const uint4 *)(gp<uint8_t>(L.sd) + (size_t)c * 16u * G::CS + 16u * cc);
@@ -1030,39 +1211,42 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     const AS4 RunLayerD &L = R.M->L[l];
     const u32 b = blockIdx.x, grp = tid_() / G::LPR, sub = tid_() % G::LPR;
     const bool moe = l > 0u;
-    float *zpart = (float *)S.scr; /* [40][64] */
+    const SlabD sd = moe ? slab_of(L) : SlabD{};
+    float *zpart = (float *)S.scr; /* [16][64] */
     h16 *hres = S.hres;
-    const u32 n = moe ? PO : O_BLOCKS * PO_A;
     const uint4 nwp = norm_piece(L.post_norm);
-    if (!gather<(PO + NT - 1) / NT>(
-            R, R.pk + off_o(l), PO, n, tag, W_GU, (u32)t,
-            [&](u32 i) { return moe ? i : (i / PO_A) * PO_B + i % PO_A; },
-            [&](u32 i, uint4 v) {
-                const u32 j = moe ? i / PO_B : i / PO_A, k = moe ? i % PO_B : i % PO_A;
-                if (k < PO_A) {
-                    put6(hres + j * O_ROWS + 6u * k, v, 6u * k, O_ROWS);
-                } else {
-                    const u32 z0 = 3u * (k - PO_A);
-                    float *zp = zpart + j * NEXP + z0;
-                    zp[0] = __uint_as_float(v.y);
-                    if (z0 + 1u < NEXP) zp[1] = __uint_as_float(v.z);
-                    if (z0 + 2u < NEXP) zp[2] = __uint_as_float(v.w);
-                }
-            }, O_BLOCKS, PO_B, moe ? 0u : PO_A - PO_B)) {
-        return false;
-    }
-    TLR(2u * (4u + 5u * l));
+    auto gather_a = [&]() {
+        return gather<(PO_AR + NT - 1) / NT>(R, R.pk + off_o(l), PO, PO_AR, tag, W_GU, (u32)t, [](u32 i) { return i; },
+                                             [&](u32 i, uint4 v) {
+                                                 const u32 j = i / PO_A, k = i % PO_A;
+                                                 put6(hres + j * O_ROWS + 6u * k, v, 6u * k, O_ROWS);
+                                             });
+    };
     float inv;
     if (moe) {
-        /* wavefront 0: z in a fixed order over the O blocks, then the top-6
-         * on z (softmax is monotone and inv_rms > 0, so z orders the experts
-         * as the probabilities do); the expert loads are issued before the
-         * norm of a */
-        /* z partial sums: thread (e, q) adds blocks q*5 .. q*5+4 of expert e,
+        /* the z partials first (published before the O rows), the top-6 on z
+         * (softmax is monotone and inv_rms > 0, so z orders the experts as
+         * the probabilities do) and the expert loads; then a and its norm */
+        if (!gather<(Z_BLOCKS * PO_Z + NT - 1) / NT>(R, R.pk + off_o(l), PO, Z_BLOCKS * PO_Z, tag, W_GU, (u32)t,
+                                                     [](u32 i) { return PO_AR + i; }, [&](u32 i, uint4 v) {
+                                                         const u32 j = i / PO_Z, z0 = 3u * (i % PO_Z);
+                                                         float *zp = zpart + j * NEXP + z0;
+                                                         zp[0] = __uint_as_float(v.y);
+                                                         if (z0 + 1u < NEXP) zp[1] = __uint_as_float(v.z);
+                                                         if (z0 + 2u < NEXP) zp[2] = __uint_as_float(v.w);
+                                                     }, UOCR_RUN_ZPROBE ? Z_BLOCKS : 0u, PO_Z, PO_AR)) {
+            return false;
+        }
+        TLR(2u * (4u + 5u * l));
+        /* the first round of a's polls, in flight while the experts are
+         * chosen and ahead of the expert loads */
+        uint4 *stg = (uint4 *)(S.scr + 8192u);
+        gather_wave_issue<(PO_AR + 63u) / 64u>(R, R.pk + off_o(l), PO, PO_AR, NT / 64u - 1u, stg, [](u32 i) { return i; });
+        /* z partial sums: thread (e, q) adds partials q*2, q*2+1 of expert e,
          * then wavefront 0 adds the 8 sums, both in a fixed order */
-        constexpr u32 ZQ = NT / 64u, ZB = O_BLOCKS / ZQ;
-        static_assert(ZB * ZQ == O_BLOCKS, "z partials split evenly");
-        float *zsum = zpart + O_BLOCKS * NEXP; /* [ZQ][64] */
+        constexpr u32 ZQ = NT / 64u, ZB = Z_BLOCKS / ZQ;
+        static_assert(ZB * ZQ == Z_BLOCKS, "z partials split evenly");
+        float *zsum = zpart + Z_BLOCKS * NEXP; /* [ZQ][64] */
         {
             const u32 e = tid_() % 64u, q = tid_() / 64u;
             float zz = 0.0f;
@@ -1071,6 +1255,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
             zsum[q * 64u + e] = zz;
         }
         __syncthreads();
+        TLD(l, 18u);
         float z = 0.0f;
         if (tid_() < 64u) {
             const u32 e = tid_();
@@ -1092,12 +1277,34 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         TLD(l, 9u);
         if (b < GU_ROUTED) {
             const u32 rank = b / 32u, e = S.selid[rank];
-            gu_rows<QF, true>(F, gp<uint8_t>(L.eg) + e * L.gu_w_stride, H(L.egs) + e * L.gu_s_stride,
-                              gp<uint8_t>(L.eu) + e * L.gu_w_stride, H(L.eus) + e * L.gu_s_stride, (b % 32u) * GU_ROWS,
-                              GU_ROWS, EI);
+            gu_rows<QF, true>(F, gp<uint8_t>(sd.eg) + e * sd.gws, H(sd.egs) + e * sd.gss, gp<uint8_t>(sd.eu) + e * sd.gws,
+                              H(sd.eus) + e * sd.gss, (b % 32u) * GU_ROWS, GU_ROWS, EI);
         }
         TLD(l, 10u);
-        inv = rms_lds(S.hres, nwp, S.xs, S.red);
+#ifdef UOCR_RUN_TIMELINE
+        if (l == 5u && tid_() == 0u) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            TLR(128u + 17u);
+        }
+#endif
+        /* a: polled by the last wavefront, which has no gate/up rows (28 rows
+         * of 16 lanes fill wavefronts 0-6), so its polls do not wait behind
+         * the expert loads in flight in the others */
+        static_assert(GU_ROWS * G::LPR <= NT - 64u && G::RPG == 1u, "the last wavefront holds no GU rows");
+        const bool ok_a = gather_wave<(PO_AR + 63u) / 64u, true>(
+            R, R.pk + off_o(l), PO, PO_AR, tag, W_GU, (u32)t, NT / 64u - 1u, stg, [](u32 i) { return i; },
+            [&](u32 i, uint4 v) {
+                const u32 j = i / PO_A, k = i % PO_A;
+                put6(hres + j * O_ROWS + 6u * k, v, 6u * k, O_ROWS);
+            });
+        if (tid_() == NT - 64u) S.red[15] = ok_a ? 1.0f : 0.0f;
+        __syncthreads();
+        if (S.red[15] == 0.0f) return false;
+        TLD(l, 15u);
+        rms_defer(S.hres, nwp, S.xs, S.red);
+        __syncthreads();
+        inv = rms_inv(S.red);
+        TLD(l, 16u);
         if (tid_() < 64u) {
             /* the selection's probabilities: softmax of z * inv_rms (raw, no
              * renormalisation; max-subtracted) */
@@ -1110,25 +1317,30 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
             if (t < TOPK) S.selw[t] = ps;
         }
     } else {
-        inv = rms_lds(S.hres, nwp, S.xs, S.red);
+        if (!gather_a()) return false;
+        TLR(2u * (4u + 5u * l));
+        rms_defer(S.hres, nwp, S.xs, S.red);
+        __syncthreads();
+        inv = rms_inv(S.red);
     }
-    (void)inv;
     const u32 nrows = moe ? GU_ROWS : min(DGU_ROWS, DI - min(b * DGU_ROWS, DI));
 #pragma unroll
     for (u32 k = 0; k < G::RPG; ++k) {
         const u32 r = grp + k * G::NG;
-        const float dg = group_sum<G::LPR>(frag_dot<QF, G::LPR, G::J>(F.g[k], S.xs, G::C, sub));
-        const float du = group_sum<G::LPR>(frag_dot<QF, G::LPR, G::J>(F.u[k], S.xs, G::C, sub));
+        const float dg = group_sum<G::LPR>(frag_dot<QF, G::LPR, G::J>(F.g[k], S.xs, G::C, sub)) * inv;
+        const float du = group_sum<G::LPR>(frag_dot<QF, G::LPR, G::J>(F.u[k], S.xs, G::C, sub)) * inv;
         if (sub == 0u && r < nrows) S.outv[r] = (h16)(fsilu(dg) * du);
     }
     __syncthreads();
     TLD(l, 11u);
     publish(R, R.pk + off_mid(l), PMID, b * PMID_B, PMID_B, tag,
             [&](u32 p) { return pay6(S.outv, p, moe ? GU_ROWS : nrows); });
+    TLD(l, 19u);
     /* the DN stage's rows of the selected experts, issued once this stage's
      * own loads are consumed, so the two streams do not share bandwidth on
      * the critical path */
-    if (moe) dn_load<QF>(R, S, l, dn);
+    if (moe) dn_load<QF>(R, S, sd, dn);
+    TLD(l, 20u);
     TLR(2u * (4u + 5u * l) + 1u);
     return true;
 }
@@ -1153,6 +1365,12 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         return false;
     }
     TLR(2u * (5u + 5u * l));
+#ifdef UOCR_RUN_TIMELINE
+    if (l == 5u && tid_() == 0u) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        TLR(128u + 21u);
+    }
+#endif
     const u32 c = dn_row(), lane = tid_() & 63u, rl = c - b * DN_ROWS;
     float out;
     if (moe) {
@@ -1209,6 +1427,8 @@ struct RunArgs {
     h16 *hout;
     u32 *trace;
     u32 trace_steps;
+    const int32_t *force;
+    u32 force_n;
 };
 
 template <int QA, int QF, int QL, int QE>
@@ -1218,9 +1438,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
     __shared__ __attribute__((aligned(16))) h16 outv[64];
     __shared__ __attribute__((aligned(16))) uint8_t scr[24576];
     __shared__ float red[16], zout[64], selw[8];
+    __shared__ __attribute__((aligned(16))) float zw[2u * Z_COLS * NEXP];
     __shared__ u32 selid[8];
     __shared__ unsigned long long keyw[NT / 64u];
-    Lds S{xs, hres, outv, red, zout, selw, selid, keyw, scr};
+    Lds S{xs, hres, outv, red, zout, selw, zw, selid, keyw, scr};
     Run R;
     R.M = (const AS4 RunModelD *)A.M;
     R.pk = A.pk;
@@ -1235,6 +1456,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
     R.hout = A.hout;
     R.trace = A.trace;
     R.trace_steps = A.trace_steps;
+    R.force = A.force;
+    R.force_n = A.force_n;
     R.tl = nullptr;
 
     RowFrag<LmCfg<QL>::J> lf[LM_DEPTH];
@@ -1275,6 +1498,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
             DnFrags<QF> dn;
             DdFrags<QF> dd;
             gu_load_static<QF>(R, l, gf);
+            o_load_z(R, l, S.zw);
             if (!o_stage<QA>(R, S, l, t, tag, of)) return;
             if (l == 0u) dd_load<QF>(R, dd);
             if (!gu_stage<QF>(R, S, l, t, tag, gf, dn)) return;
@@ -1294,6 +1518,28 @@ __global__ __launch_bounds__(NT) void k_run_seed(uint4 *pk, const h16 *__restric
     for (u32 j = 0; j < 6u; ++j) e[j] = (p % 2u) * 6u + j < DN_ROWS ? h[base + j] : (h16)0.0f;
     pk[off_h(UOCR_RUN_LAYERS - 1u) + (u64)r * PH + p] =
         make_uint4(tag, pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]));
+}
+
+/* fold_o[c][e] = sum_r fold[r][e] * O[r][c]: thread (c, e), rows in order. */
+template <int QT>
+__global__ __launch_bounds__(256) void k_fold_o(const uint8_t *__restrict__ ow, const h16 *__restrict__ os,
+                                                const float *__restrict__ fold, float *__restrict__ out) {
+    const u32 c = blockIdx.x * 4u + threadIdx.x / 64u, e = threadIdx.x % 64u;
+    float acc = 0.0f;
+    for (u32 r = 0; r < HID; ++r) {
+        float w;
+        if (QT == 1) {
+            w = (float)((const h16 *)ow)[(size_t)r * HID + c];
+        } else if (QT == 3) {
+            w = (float)(int8_t)ow[(size_t)r * HID + c] * (float)os[(size_t)r * (HID / 64u) + c / 64u];
+        } else {
+            const uint8_t byte = ow[(size_t)r * (HID / 2u) + (c / 64u) * 32u + (c % 32u)];
+            const int q = (int)((c % 64u) < 32u ? (byte & 15u) : (byte >> 4)) - 8;
+            w = (float)q * (float)os[(size_t)r * (HID / 64u) + c / 64u];
+        }
+        acc = fmaf(fold[(size_t)r * NEXP + e], w, acc);
+    }
+    out[(size_t)c * NEXP + e] = acc;
 }
 
 __global__ void k_run_reset(u32 *ctl) {
@@ -1327,6 +1573,23 @@ extern "C" int uocr_run_supported(const uocr_run_model *m) {
     return m->qa == UOCR_QT_Q8 && m->ql == m->qf && m->qe == m->qf && (m->qf == UOCR_QT_Q4 || m->qf == UOCR_QT_Q8);
 }
 
+extern "C" hipError_t uocr_run_fold_o(hipStream_t st, uint32_t qtype, const void *ow, const uint16_t *os,
+                                      const float *fold, float *out) {
+    if (ow == nullptr || fold == nullptr || out == nullptr || (qtype != UOCR_QT_F16 && os == nullptr)) {
+        return hipErrorInvalidValue;
+    }
+    const dim3 grid(HID / 4u), block(256u);
+    const uint8_t *w = (const uint8_t *)ow;
+    const h16 *s = (const h16 *)os;
+    switch (qtype) {
+    case UOCR_QT_F16: hipLaunchKernelGGL(k_fold_o<1>, grid, block, 0, st, w, s, fold, out); break;
+    case UOCR_QT_Q8: hipLaunchKernelGGL(k_fold_o<3>, grid, block, 0, st, w, s, fold, out); break;
+    case UOCR_QT_Q4: hipLaunchKernelGGL(k_fold_o<4>, grid, block, 0, st, w, s, fold, out); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 extern "C" hipError_t uocr_run_seed(hipStream_t st, void *arena, const uint16_t *h, uint32_t tag) {
     if (arena == nullptr || h == nullptr) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_run_seed, dim3((PH * NREP + NT - 1u) / NT), dim3(NT), 0, st, (uint4 *)arena, (const h16 *)h, tag);
@@ -1342,7 +1605,8 @@ extern "C" hipError_t uocr_run_reset(hipStream_t st, void *arena) {
 extern "C" hipError_t uocr_run_launch(hipStream_t st, const uocr_run_model *model, const uocr_run_model *host_model,
                                       void *arena, uint16_t *kc, uint16_t *vc, uint32_t cap, int32_t P, int32_t t0,
                                       int32_t n, int last, uint32_t tag0, int32_t *tokens, float *scores,
-                                      uint16_t *hidden, uint32_t *trace, uint32_t trace_steps) {
+                                      uint16_t *hidden, uint32_t *trace, uint32_t trace_steps, const int32_t *force,
+                                      uint32_t force_n) {
     if (model == nullptr || host_model == nullptr || arena == nullptr || kc == nullptr || vc == nullptr ||
         tokens == nullptr || hidden == nullptr || (trace == nullptr && trace_steps != 0u) || n <= 0 || n > (int32_t)UOCR_RUN_MAX_STEPS || P <= 0 || t0 < 0 ||
         cap < (uint32_t)P + RING || !uocr_run_supported(host_model)) {
@@ -1366,6 +1630,8 @@ extern "C" hipError_t uocr_run_launch(hipStream_t st, const uocr_run_model *mode
     a.hout = (h16 *)hidden;
     a.trace = trace;
     a.trace_steps = trace_steps;
+    a.force = force_n != 0u ? force : nullptr;
+    a.force_n = force_n;
     if (host_model->qf == UOCR_QT_Q4) return launch_run<3, 4, 4, 4>(st, a);
     return launch_run<3, 3, 3, 3>(st, a);
 }

@@ -38,6 +38,7 @@ typedef struct uocr_run_layer {
     const uint16_t *qs, *ks, *vs, *os;
     const uint16_t *in_norm, *post_norm;
     const float *fold;              /* [1280][64] router * post_norm (MoE layers) */
+    const float *fold_o;            /* [1280][64] O^T fold: z's weights on the attention context */
     const void *gate, *up, *down;   /* layer 0 dense SwiGLU */
     const uint16_t *gs, *us, *ds;
     const void *sg, *su, *sd;       /* shared experts (merged 1792) */
@@ -72,6 +73,11 @@ int uocr_run_supported(const uocr_run_model *m);
 /* Publishes the hidden state h (fp16[1280]) as layer 11's output with the
  * given tag, so a run whose first step carries tag + 1 starts from it. */
 hipError_t uocr_run_seed(hipStream_t st, void *arena, const uint16_t *h, uint32_t tag);
+/* out[c][e] = sum_r fold[r][e] * O[r][c] over the 1280 rows r of the O
+ * projection (qtype f16, q8_0 or q4_0; fp32, summed in row order), so the
+ * router's pre-norm logits are fold^T h + out^T ctx for a = h + O ctx. */
+hipError_t uocr_run_fold_o(hipStream_t st, uint32_t qtype, const void *ow, const uint16_t *os, const float *fold,
+                           float *out);
 /* Clears the control words (abort flag). */
 hipError_t uocr_run_reset(hipStream_t st, void *arena);
 /* Steps t0 .. t0+n-1 of a request with prompt length P: step t selects
@@ -80,11 +86,13 @@ hipError_t uocr_run_reset(hipStream_t st, void *arena);
  * position P + t.  Step t0+i uses tag tag0+i.  model points to a device copy
  * of host_model.  kc/vc: [12][10][cap][128] fp16 caches.  hidden receives
  * each step's final hidden state (layer 11's output); trace (may be NULL)
- * the expert ids of layers 1-11 for steps t < trace_steps ([t][11][6]). */
+ * the expert ids of layers 1-11 for steps t < trace_steps ([t][11][6]).
+ * force (may be NULL): step t < force_n embeds force[t] instead of the token
+ * it selects (teacher forcing for parity tests). */
 hipError_t uocr_run_launch(hipStream_t st, const uocr_run_model *model, const uocr_run_model *host_model,
                            void *arena, uint16_t *kc, uint16_t *vc, uint32_t cap, int32_t P, int32_t t0, int32_t n,
                            int last, uint32_t tag0, int32_t *tokens, float *scores, uint16_t *hidden,
-                           uint32_t *trace, uint32_t trace_steps);
+                           uint32_t *trace, uint32_t trace_steps, const int32_t *force, uint32_t force_n);
 
 #ifdef __cplusplus
 }

@@ -122,6 +122,7 @@ SIGNATURES = {
                                   ct.POINTER(ct.c_double), ct.POINTER(ct.c_double)], ct.c_int),
     "uocr_engine_trace_enable": ([_VP, _U32], ct.c_int),
     "uocr_engine_trace_read": ([_VP, _VP, _VP], ct.c_int),
+    "uocr_engine_trace_force": ([_VP, _VP, _U32], ct.c_int),
     "uocr_op_workspace_bytes": ([], _SZ),
     "uocr_op_gemv": ([_U32, _VP, _VP, _U32, _U32, _VP, _VP, _VP], ct.c_int),
     "uocr_op_swiglu": ([_U32, _VP, _VP, _VP, _VP, _U32, _U32, _VP, _VP, _VP], ct.c_int),
@@ -312,6 +313,14 @@ class Engine:
         with self._lock:
             self._raise(self._lib.uocr_engine_trace_enable(self._handle, steps))
         self._trace_steps = steps
+
+    def trace_force(self, ids) -> None:
+        """Embed ids[t] after decode step t of each following generation
+        (teacher forcing); an empty sequence turns it off."""
+        arr = np.ascontiguousarray(ids if ids is not None else [], dtype=np.int32)
+        with self._lock:
+            self._raise(self._lib.uocr_engine_trace_force(self._handle, arr.ctypes.data if arr.size else None,
+                                                          arr.size))
 
     def trace_read(self) -> tuple[np.ndarray, np.ndarray]:
         """(expert ids [steps][11][6] uint32, final hidden state fp16 [1280])
