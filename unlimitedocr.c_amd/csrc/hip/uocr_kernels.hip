@@ -388,10 +388,10 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
 /* split-K decode attention; merge in the O-projection prologue              */
 /* ------------------------------------------------------------------------ */
 
-#define ATT_UNROLL 5
-/* Threads of an attention block: 16-lane slot groups, 64 groups per head in
- * all (so the per-wave work does not depend on the split count). */
-constexpr int ATT_THREADS = 64 * 64 / UOCR_K_ATTN_SPLITS;
+/* Threads of an attention block: 32 slot groups of 16 lanes (8 dims per
+ * lane).  A group holds U slots in flight (the launch picks U so that one
+ * round of loads covers the block's range up to 4,608 slots of cache). */
+constexpr int ATT_THREADS = 512;
 constexpr int ATT_GROUPS = ATT_THREADS / 16;
 
 /* Live KV slots of a step are always [0, attn_len): the prompt slots
@@ -403,13 +403,16 @@ constexpr int ATT_GROUPS = ATT_THREADS / 16;
  * results differ only in fp32 summation order).
  *
  * Block (s, h) owns slots [s*chunk, (s+1)*chunk) with chunk fixed by the
- * cache capacity, so its first K/V loads are issued before the step state
- * (attention length) arrives; slots >= attn_len are masked afterwards.  A
- * 16-lane group handles one slot (8 dims per lane), ATT_UNROLL slots in
- * flight per group, with an online softmax; the block writes one partial
- * (max, sum, acc[128] / sum) per head:
+ * cache capacity.  Blocks whose range lies below the last UOCR_K_RING slots
+ * (live in every decode step whose prompt fills the cache) issue their first
+ * K/V loads before the step state (attention length) arrives; the others
+ * read it first, so ring slots not generated yet are not fetched.  Slots >=
+ * attn_len are masked.  A 16-lane group handles one slot (8 dims per lane),
+ * U slots in flight per group, with an online softmax; the block writes one
+ * partial (max, sum, acc[128] / sum) per head:
  *   fp16 acc/sum at ((h16 *)part)[(h*S + s)*128 + d],
  *   fp32 (max, sum) at part[H*S*128 + (h*S + s)*2]. */
+template <int ATT_UNROLL>
 __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict__ q, const h16 *__restrict__ kc,
                                                      const h16 *__restrict__ vc, u32 cap,
                                                      const uocr_step_state *__restrict__ st, float *__restrict__ part,
@@ -457,9 +460,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
     };
     h8 qq;
     qq.u = *(const uint4 *)(q + h * 128 + 8 * p);
+    const bool late = iend > (int)cap - min((int)cap, (int)UOCR_K_RING);
+    int i1 = iend;
+    if (late) {
+        i1 = min(st->attn_len, iend);
+        lim = max(i1 - 1, 0);
+    }
     load(i0 + gid);
     hold(qq.u);
-    const int i1 = min(st->attn_len, iend);
+    i1 = min(st->attn_len, iend);
     lim = max(min(i1, iend) - 1, 0);
     float qv[8];
 #pragma unroll
@@ -1236,7 +1245,10 @@ extern "C" hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, c
         partials == nullptr) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(k_attention, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(ATT_THREADS), 0, st, (const h16 *)q,
+    /* one round of loads per block where the range allows it */
+    const u32 chunk = (cache_capacity + UOCR_K_ATTN_SPLITS - 1u) / UOCR_K_ATTN_SPLITS;
+    auto *kern = chunk <= 3u * ATT_GROUPS ? k_attention<3> : (chunk <= 5u * ATT_GROUPS ? k_attention<5> : k_attention<9>);
+    hipLaunchKernelGGL(kern, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(ATT_THREADS), 0, st, (const h16 *)q,
                        (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials,
                        (long long *)router_acc, (unsigned long long *)clear_keys);
     return hipGetLastError();
