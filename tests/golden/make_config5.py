@@ -9,9 +9,8 @@ computes the hidden state step t + 1 selects from, t < 511) the router's
 expert ids in layers 1-11 (`trace`) with each selection's set margin
 (`router_gap`, the logit gap between the 6th chosen expert and the best
 unchosen one); and the hidden state (fp16 bits, the input of step t's
-final norm) at the checkpoint steps `hidden_steps`: 16, 128, 511 and the
-first step whose margin is at most 1e-2 (up to which a greedy decoder on the
-GPU must follow the oracle token for token).  The prompt is rebuilt from PROMPT_SEED by
+final norm) at the checkpoint steps `hidden_steps`: every 32nd step from 16, 511, and
+the first step whose margin is at most 1e-2.  The prompt is rebuilt from PROMPT_SEED by
 config5_prompt(), so the GPU test (tests/test_gpu_engine.py) feeds the HIP
 engine the same bytes.
 
@@ -79,7 +78,7 @@ def run(profile: str) -> None:
     top = np.zeros(STEPS, np.float32)
     trace = np.zeros((STEPS - 1, 11, 6), np.uint32)
     router_gap = np.full((STEPS, 11), np.inf, np.float32)
-    checkpoints = {16, 128, STEPS - 1}
+    checkpoints = set(range(16, STEPS, 32)) | {STEPS - 1}
     saved: dict[int, np.ndarray] = {}
     tok, s1, s2 = ct.c_int32(0), ct.c_float(0.0), ct.c_float(0.0)
     for t in range(STEPS):

@@ -106,7 +106,7 @@ static_assert(O0 >= 0u && O0 + O_BLOCKS <= QKV_BLOCKS, "O blocks also gather h i
 /* packets per copy */
 constexpr u32 PQKV_B = 3u, PQKV = QKV_BLOCKS * PQKV_B;
 constexpr u32 PATT_B = 23u, PATT = ATT_BLOCKS * PATT_B;
-constexpr u32 PO_A = 6u, PO_Z = 22u, PO_AR = O_BLOCKS * PO_A, PO = PO_AR + Z_BLOCKS * PO_Z;
+constexpr u32 PO_A = (O_ROWS + 5u) / 6u, PO_Z = 22u, PO_AR = O_BLOCKS * PO_A, PO = PO_AR + Z_BLOCKS * PO_Z;
 constexpr u32 PMID_B = 5u, PMID = NB * PMID_B;
 constexpr u32 PH_B = 2u, PH = DN_BLOCKS * PH_B;
 constexpr u32 PLM = NB;
@@ -906,15 +906,19 @@ __device__ bool att_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag,
 
 template <int QA>
 struct OCfg {
-    static constexpr u32 C = chunks_per_row<QA>(HID), LPR = 32u, J = (C + LPR - 1u) / LPR;
+    static constexpr u32 C = chunks_per_row<QA>(HID), LPR = 32u;
     static constexpr u32 NG = NT / LPR, RPG = O_ROWS / NG;
+    /* a lane group walks its RPG rows' chunks as one list, so every lane
+     * holds the same number of chunks */
+    static constexpr u32 J = (RPG * C + LPR - 1u) / LPR;
+    static_assert(J * LPR == RPG * C, "O chunks split evenly over the lane group");
     static constexpr u32 ZC = Z_COLS / (NT / 64u); /* columns per thread in a z partial */
     static_assert(RPG * NG == O_ROWS && ZC * (NT / 64u) == Z_COLS && Z_BLOCKS <= O_BLOCKS, "O rows per group");
 };
 
 template <int QA>
 struct OFrags {
-    RowFrag<OCfg<QA>::J> f[OCfg<QA>::RPG];
+    RowFrag<OCfg<QA>::J> f;
 };
 
 /* z-partial weights of O block j < Z_BLOCKS (MoE layers): rows
@@ -951,10 +955,11 @@ __device__ __forceinline__ void o_load(const Run &R, u32 l, OFrags<QA> &F) {
     const AS4 RunLayerD &L = R.M->L[l];
     const u32 j = b - O0, g = tid_() / 32u, sub = tid_() % 32u;
 #pragma unroll
-    for (u32 k = 0; k < G::RPG; ++k) {
+    for (u32 i = 0; i < G::J; ++i) {
+        const u32 q = sub + G::LPR * i, k = q / G::C, c = q % G::C;
         const u32 r = j * O_ROWS + g * G::RPG + k;
-        frag_load<QA, G::LPR, G::J>(F.f[k], gp<uint8_t>(L.o) + (size_t)r * 16u * G::C, H(L.os) + (size_t)r * (HID / 64u),
-                                    G::C, sub);
+        F.f.w[i] = *(const uint4 *)(gp<uint8_t>(L.o) + ((size_t)r * G::C + c) * 16u);
+        if (QA != 1) F.f.s[i] = H(L.os)[(size_t)r * (HID / 64u) + c / chunks_per_group<QA>()];
     }
 }
 
@@ -1049,10 +1054,21 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
                               __float_as_uint(z0 + 2u < NEXP ? S.zout[z0 + 2u] : 0.0f));
         });
     }
+    float part[G::RPG];
+#pragma unroll
+    for (u32 k = 0; k < G::RPG; ++k) part[k] = 0.0f;
+#pragma unroll
+    for (u32 i = 0; i < G::J; ++i) {
+        const u32 q = sub + G::LPR * i, kq = q / G::C;
+        const float d = chunk_dot<QA>(F.f.w[i], S.xs, q % G::C);
+        const float v = QA == 1 ? d : d * (float)F.f.s[i];
+#pragma unroll
+        for (u32 k = 0; k < G::RPG; ++k) part[k] += kq == k ? v : 0.0f;
+    }
 #pragma unroll
     for (u32 k = 0; k < G::RPG; ++k) {
         const u32 rl = g * G::RPG + k, r = j * O_ROWS + rl;
-        const float d = group_sum<G::LPR>(frag_dot<QA, G::LPR, G::J>(F.f[k], S.xs, G::C, sub));
+        const float d = group_sum<G::LPR>(part[k]);
         if (sub == 0u) S.outv[rl] = (h16)(d + (float)S.hres[r]);
     }
     __syncthreads();
@@ -1068,14 +1084,17 @@ template <int QF>
 struct GuCfg {
     static constexpr u32 C = chunks_per_row<QF>(HID);
     static constexpr u32 LPR = 16u;
-    static constexpr u32 J = (C + LPR - 1u) / LPR;
+    /* a lane group walks the gate row's C chunks then the up row's as one
+     * list of 2C, so every lane holds the same number of chunks */
+    static constexpr u32 J = (2u * C + LPR - 1u) / LPR;
+    static_assert(J * LPR == 2u * C, "gate and up chunks split evenly over the lane group");
     static constexpr u32 NG = NT / LPR;                 /* lane groups */
     static constexpr u32 RPG = (GU_ROWS + NG - 1u) / NG; /* row pairs per group */
 };
 
 template <int QF>
 struct GuFrags {
-    RowFrag<GuCfg<QF>::J> g[GuCfg<QF>::RPG], u[GuCfg<QF>::RPG];
+    RowFrag<GuCfg<QF>::J> f[GuCfg<QF>::RPG];
 };
 
 template <int QF, bool NTL>
@@ -1090,8 +1109,22 @@ __device__ __forceinline__ void gu_rows(GuFrags<QF> &F, const uint8_t *GW, const
         if (grp + k * G::NG >= nrows) continue;
         const u32 r = row0 + grp + k * G::NG;
         const u32 rr = min(r, maxrow - 1u);
-        frag_load<QF, G::LPR, G::J, NTL>(F.g[k], GW + (size_t)rr * 16u * G::C, GS + (size_t)rr * (HID / 64u), G::C, sub);
-        frag_load<QF, G::LPR, G::J, NTL>(F.u[k], UW + (size_t)rr * 16u * G::C, US + (size_t)rr * (HID / 64u), G::C, sub);
+        const uint8_t *gw = GW + (size_t)rr * 16u * G::C, *uw = UW + (size_t)rr * 16u * G::C;
+        const h16 *gs = GS + (size_t)rr * (HID / 64u), *us = US + (size_t)rr * (HID / 64u);
+#pragma unroll
+        for (u32 j = 0; j < G::J; ++j) {
+            const u32 q = sub + G::LPR * j;
+            const bool up = q >= G::C;
+            const u32 c = up ? q - G::C : q;
+            const uint8_t *w = (up ? uw : gw) + 16u * c;
+            if (NTL) {
+                F.f[k].w[j] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4v *)w));
+                if (QF != 1) F.f[k].s[j] = __builtin_nontemporal_load((up ? us : gs) + c / chunks_per_group<QF>());
+            } else {
+                F.f[k].w[j] = *(const uint4 *)w;
+                if (QF != 1) F.f[k].s[j] = (up ? us : gs)[c / chunks_per_group<QF>()];
+            }
+        }
     }
 }
 
@@ -1242,25 +1275,14 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
          * chosen and ahead of the expert loads */
         uint4 *stg = (uint4 *)(S.scr + 8192u);
         gather_wave_issue<(PO_AR + 63u) / 64u>(R, R.pk + off_o(l), PO, PO_AR, NT / 64u - 1u, stg, [](u32 i) { return i; });
-        /* z partial sums: thread (e, q) adds partials q*2, q*2+1 of expert e,
-         * then wavefront 0 adds the 8 sums, both in a fixed order */
-        constexpr u32 ZQ = NT / 64u, ZB = Z_BLOCKS / ZQ;
-        static_assert(ZB * ZQ == Z_BLOCKS, "z partials split evenly");
-        float *zsum = zpart + Z_BLOCKS * NEXP; /* [ZQ][64] */
-        {
-            const u32 e = tid_() % 64u, q = tid_() / 64u;
-            float zz = 0.0f;
-#pragma unroll
-            for (u32 j = 0; j < ZB; ++j) zz += zpart[(q * ZB + j) * NEXP + e];
-            zsum[q * 64u + e] = zz;
-        }
-        __syncthreads();
+        /* wavefront 0: z of expert e (lane e) over the 16 partials in a fixed
+         * order, then the top-6 */
         TLD(l, 18u);
         float z = 0.0f;
         if (tid_() < 64u) {
             const u32 e = tid_();
 #pragma unroll
-            for (u32 q = 0; q < ZQ; ++q) z += zsum[q * 64u + e];
+            for (u32 j = 0; j < Z_BLOCKS; ++j) z += zpart[j * NEXP + e];
             u32 sid[TOPK];
             topk6_ids(z, sid);
             if (e < TOPK) {
@@ -1327,8 +1349,18 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
 #pragma unroll
     for (u32 k = 0; k < G::RPG; ++k) {
         const u32 r = grp + k * G::NG;
-        const float dg = group_sum<G::LPR>(frag_dot<QF, G::LPR, G::J>(F.g[k], S.xs, G::C, sub)) * inv;
-        const float du = group_sum<G::LPR>(frag_dot<QF, G::LPR, G::J>(F.u[k], S.xs, G::C, sub)) * inv;
+        float pg = 0.0f, pu = 0.0f;
+#pragma unroll
+        for (u32 j = 0; j < G::J; ++j) {
+            const u32 q = sub + G::LPR * j;
+            const bool up = q >= G::C;
+            const float d = chunk_dot<QF>(F.f[k].w[j], S.xs, up ? q - G::C : q);
+            const float v = QF == 1 ? d : d * (float)F.f[k].s[j];
+            pg += up ? 0.0f : v;
+            pu += up ? v : 0.0f;
+        }
+        const float dg = group_sum<G::LPR>(pg) * inv;
+        const float du = group_sum<G::LPR>(pu) * inv;
         if (sub == 0u && r < nrows) S.outv[r] = (h16)(fsilu(dg) * du);
     }
     __syncthreads();
