@@ -46,6 +46,8 @@ struct dev_layer {
     const float *rfold_all; /* the same fold whatever its range (the persistent run sums it in fp32) */
     const float *rfold_o;   /* [1280][64] O^T rfold_all (persistent run) */
     uocr_expert_slab slab;
+    /* GEMM-packed payload copies for the MFMA prefill (Q4/Q8; NULL for fp16) */
+    const void *pq, *pk, *pv, *po, *pgate, *pup, *pdown, *psg, *psu, *psd, *peg, *peu, *ped;
 };
 
 int bfail(char *err, size_t n, const char *fmt, ...) {
@@ -496,6 +498,21 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
             total += 2u * align256((uint64_t)H_SIZE * UOCR_ROUTED_EXPERTS * 4u); /* fold, fold_o */
         }
     }
+    /* GEMM-packed copies of the Q4/Q8 layer payloads (MFMA prefill) */
+    auto packed_bytes = [](const uocr_bound_tensor &t, uint64_t count) -> uint64_t {
+        return t.qtype == UOCR_QT_F16 ? 0u : count * align256(t.w_bytes);
+    };
+    for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
+        const uocr_bound_layer &L = b->layers[l];
+        total += packed_bytes(L.q, 1) + packed_bytes(L.k, 1) + packed_bytes(L.v, 1) + packed_bytes(L.o, 1);
+        if (l == 0u) {
+            total += packed_bytes(L.gate, 1) + packed_bytes(L.up, 1) + packed_bytes(L.down, 1);
+        } else {
+            total += packed_bytes(L.sgate, 1) + packed_bytes(L.sup, 1) + packed_bytes(L.sdown, 1);
+            total += packed_bytes(L.egate[0], UOCR_ROUTED_EXPERTS) + packed_bytes(L.eup[0], UOCR_ROUTED_EXPERTS) +
+                     packed_bytes(L.edown[0], UOCR_ROUTED_EXPERTS);
+        }
+    }
     const uint64_t run_model_off = total;
     total += align256(sizeof(uocr_run_model));
     HIPCHK(counted_malloc(ctx, (void **)&ctx->warena, total), "weight arena allocation");
@@ -546,6 +563,40 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
     for (uint32_t l = 1; l < UOCR_DECODER_LAYERS; ++l) {
         ctx->L[l].rfold_o = (const float *)(ctx->warena + p.take((uint64_t)H_SIZE * UOCR_ROUTED_EXPERTS * 4u));
     }
+    /* GEMM-packed copies: rows x K per matrix, experts at the slab stride */
+    auto pack = [&](const uocr_qmat &m, uint32_t rows, uint32_t K, uint32_t count, uint64_t stride,
+                    uint64_t bytes) -> const void * {
+        if (m.qtype == UOCR_QT_F16) return nullptr;
+        uint8_t *dst = ctx->warena + p.take(count == 1u ? align256(bytes) : count * stride);
+        if (uocr_launch_pack_gemm_rows(nullptr, m.qtype, m.w, dst, rows, K, count, count == 1u ? 0u : stride) !=
+            hipSuccess) {
+            return nullptr;
+        }
+        return dst;
+    };
+    for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
+        dev_layer &D = ctx->L[l];
+        const uocr_bound_layer &S = b->layers[l];
+        const uint32_t H = H_SIZE, I0 = UOCR_DENSE_LAYER0_INTERMEDIATE, SI = UOCR_MOE_SHARED_INTERMEDIATE,
+                       EI = UOCR_MOE_EXPERT_INTERMEDIATE;
+        D.pq = pack(D.q, H, H, 1, 0, S.q.w_bytes);
+        D.pk = pack(D.k, H, H, 1, 0, S.k.w_bytes);
+        D.pv = pack(D.v, H, H, 1, 0, S.v.w_bytes);
+        D.po = pack(D.o, H, H, 1, 0, S.o.w_bytes);
+        if (l == 0u) {
+            D.pgate = pack(D.gate, I0, H, 1, 0, S.gate.w_bytes);
+            D.pup = pack(D.up, I0, H, 1, 0, S.up.w_bytes);
+            D.pdown = pack(D.down, H, I0, 1, 0, S.down.w_bytes);
+            continue;
+        }
+        D.psg = pack(D.sgate, SI, H, 1, 0, S.sgate.w_bytes);
+        D.psu = pack(D.sup, SI, H, 1, 0, S.sup.w_bytes);
+        D.psd = pack(D.sdown, H, SI, 1, 0, S.sdown.w_bytes);
+        D.peg = pack(D.slab.gate, EI, H, UOCR_ROUTED_EXPERTS, D.slab.gu_w_stride, 0);
+        D.peu = pack(D.slab.up, EI, H, UOCR_ROUTED_EXPERTS, D.slab.gu_w_stride, 0);
+        D.ped = pack(D.slab.down, H, EI, UOCR_ROUTED_EXPERTS, D.slab.dn_w_stride, 0);
+    }
+    HIPCHK(hipGetLastError(), "GEMM weight packing");
     if (p.off > run_model_off) return bfail(err, err_size, "weight arena overflow");
     ctx->d_run_model = (uocr_run_model *)(ctx->warena + run_model_off);
     if (!setup_run(ctx, err, err_size)) return 0;
@@ -848,6 +899,13 @@ static uocr_gemm_desc gdesc(const uint16_t *A, uint32_t lda, uint32_t M, uint32_
 /* All P prompt rows (c->prompt, updated in place as the residual stream)
  * through the 12 layers on MFMA GEMMs; K/V of positions 0..P-1 land in the
  * cache slots 0..P-1 and the last row's hidden state in c->h. */
+/* m with its payload replaced by the GEMM-packed copy (when there is one). */
+static uocr_qmat packed_of(const uocr_qmat &m, const void *pw) {
+    uocr_qmat r = m;
+    if (pw != nullptr) r.w = pw;
+    return r;
+}
+
 static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
     hipStream_t s = c->stream;
     const uint64_t kv_layer = (uint64_t)UOCR_ATTENTION_HEADS * c->cache_cap * UOCR_HEAD_DIM;
@@ -863,15 +921,22 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
         ENQ(uocr_launch_rows_rmsnorm(s, H, L.in_norm, P, c->p_xn));
         uocr_gemm_desc d = gdesc(c->p_xn, H_SIZE, P, 3u * H_SIZE, H_SIZE, c->p_qkv, 3u * H_SIZE);
-        d.W[0] = L.q;
-        d.W[1] = L.k;
-        d.W[2] = L.v;
+        d.W[0] = packed_of(L.q, L.pq);
+        d.W[1] = packed_of(L.k, L.pk);
+        d.W[2] = packed_of(L.v, L.pv);
+        d.packed = L.pq != nullptr && L.pk != nullptr && L.pv != nullptr;
+        if (!d.packed) {
+            d.W[0] = L.q;
+            d.W[1] = L.k;
+            d.W[2] = L.v;
+        }
         d.nseg = H_SIZE;
         ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
         ENQ(uocr_launch_rope_scatter(s, c->p_qkv, c->invf, P, c->p_q, kc, vc, c->cache_cap));
         ENQ(uocr_launch_flash_attn(s, c->p_q, kc, vc, c->cache_cap, P, c->p_ctx, c->p_fa_ws));
         d = gdesc(c->p_ctx, H_SIZE, P, H_SIZE, H_SIZE, c->p_a, H_SIZE);
-        d.W[0] = L.o;
+        d.W[0] = packed_of(L.o, L.po);
+        d.packed = L.po != nullptr;
         d.res = H;
         d.ldr = H_SIZE;
         if (c->prefill_ksplit) with_ksplit(d, c->p_kpart);
@@ -880,11 +945,13 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         if (l == 0u) {
             const uint32_t I0 = UOCR_DENSE_LAYER0_INTERMEDIATE;
             d = gdesc(c->p_xn, H_SIZE, P, I0, H_SIZE, c->p_mid, I0);
-            d.W[0] = L.gate;
-            d.W[1] = L.up;
+            d.packed = L.pgate != nullptr && L.pup != nullptr;
+            d.W[0] = d.packed ? packed_of(L.gate, L.pgate) : L.gate;
+            d.W[1] = d.packed ? packed_of(L.up, L.pup) : L.up;
             ENQ(uocr_launch_gemm(s, UOCR_GEMM_SWIGLU, &d));
             d = gdesc(c->p_mid, I0, P, H_SIZE, I0, H, H_SIZE);
-            d.W[0] = L.down;
+            d.W[0] = packed_of(L.down, L.pdown);
+            d.packed = L.pdown != nullptr;
             d.res = c->p_a;
             d.ldr = H_SIZE;
             if (c->prefill_ksplit) with_ksplit(d, c->p_kpart);
@@ -900,15 +967,18 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         ENQ(uocr_launch_route_rows(s, c->p_logits, P, 0, c->p_ids, c->p_wts, c->p_offsets, c->p_tile_e, c->p_tile_s0, c->p_tile_s1, c->p_ntiles, c->p_list_tok,
                                    c->p_list_pair));
         d = gdesc(c->p_xn, H_SIZE, P, SI, H_SIZE, c->p_smid, SI);
-        d.W[0] = L.sgate;
-        d.W[1] = L.sup;
+        d.packed = L.psg != nullptr && L.psu != nullptr;
+        d.W[0] = d.packed ? packed_of(L.sgate, L.psg) : L.sgate;
+        d.W[1] = d.packed ? packed_of(L.sup, L.psu) : L.sup;
         ENQ(uocr_launch_gemm(s, UOCR_GEMM_SWIGLU, &d));
         d = gdesc(c->p_smid, SI, P, H_SIZE, SI, c->p_sout, H_SIZE);
-        d.W[0] = L.sdown;
+        d.W[0] = packed_of(L.sdown, L.psd);
+        d.packed = L.psd != nullptr;
         ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
         d = gdesc(c->p_xn, H_SIZE, 0, EI, H_SIZE, c->p_rmid, EI);
-        d.W[0] = L.slab.gate;
-        d.W[1] = L.slab.up;
+        d.packed = L.peg != nullptr && L.peu != nullptr;
+        d.W[0] = d.packed ? packed_of(L.slab.gate, L.peg) : L.slab.gate;
+        d.W[1] = d.packed ? packed_of(L.slab.up, L.peu) : L.slab.up;
         d.w_stride = L.slab.gu_w_stride;
         d.s_stride = L.slab.gu_s_stride;
         d.a_idx = c->p_list_tok;
@@ -924,7 +994,8 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         dd.lda = EI;
         dd.N = H_SIZE;
         dd.K = EI;
-        dd.W[0] = L.slab.down;
+        dd.W[0] = packed_of(L.slab.down, L.ped);
+        dd.packed = L.ped != nullptr;
         dd.W[1] = uocr_qmat{nullptr, nullptr, 0};
         dd.w_stride = L.slab.dn_w_stride;
         dd.s_stride = L.slab.dn_s_stride;

@@ -221,9 +221,20 @@ typedef struct uocr_gemm_desc {
      * applies the epilogue; ksplit <= 1 or part NULL: no split */
     uint32_t ksplit;
     float *part;
+    /* Q4/Q8 weights: W[i].w (and each expert of a slab) holds the GEMM-packed
+     * copy of uocr_launch_pack_gemm_rows instead of the row-major payload */
+    uint32_t packed;
 } uocr_gemm_desc;
 
 hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d);
+/* GEMM-packed copy of a Q4_0 / Q8_0 payload of `rows` x K (rows % 32 == 0,
+ * K % 64 == 0), `count` matrices `stride` bytes apart (an expert slab; the
+ * copy keeps the stride).  Per 32-row block and 64-column step the block's
+ * bytes are stored as [half h][row r][RB/2], RB = 32 (Q4) or 64 (Q8) bytes
+ * per row and step, so the wavefront that owns the 32 rows reads one
+ * contiguous run per step (lane 32h + r takes row r's half h). */
+hipError_t uocr_launch_pack_gemm_rows(hipStream_t st, uint32_t qtype, const void *src, void *dst, uint32_t rows,
+                                      uint32_t K, uint32_t count, uint64_t stride);
 /* K splits (1: none) for a plain GEMM of M x N x K whose tile grid is under
  * one block per CU; UOCR_GEMM_F16 / F32 / VISION honour desc ksplit + part. */
 uint32_t uocr_gemm_ksplit(uint32_t M, uint32_t N, uint32_t K);

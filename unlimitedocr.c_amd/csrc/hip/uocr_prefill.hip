@@ -36,6 +36,7 @@ typedef uint32_t u32;
 
 #define PB 256 /* threads per prefill block */
 #define TM 64  /* GEMM tile rows */
+#define GTM TM /* tile rows of the grouped (expert-bucket) GEMMs */
 #define TN 128 /* GEMM tile columns */
 #define TK 64  /* one quantisation group */
 #define LDA (TK + 8) /* padded LDS row of the activation tile (halves) */
@@ -118,10 +119,16 @@ __device__ __forceinline__ u32 b_koff(u32 i, u32 h) {
  * register ring stays in registers. */
 template <int QT>
 __device__ __forceinline__ void b_load(u32 (&w)[BPiece<QT>::NW], u32 &sc, const uint8_t *W, const h16 *S, u32 K,
-                                       u32 n, u32 g, u32 h, bool with_scale = true) {
-    const uint4 *src = QT == 4 ? (const uint4 *)(W + (size_t)n * (K / 2u) + g * 32u + 16u * h)
-                               : (QT == 3 ? (const uint4 *)(W + (size_t)n * K + g * 64u + 32u * h)
-                                          : (const uint4 *)((const h16 *)W + (size_t)n * K + g * 64u + 32u * h));
+                                       u32 n, u32 g, u32 h, bool with_scale = true, bool packed = false) {
+    /* packed (Q4/Q8): the 32-row block's step is one run, half h of row r at
+     * (32h + r) * RB/2 */
+    constexpr u32 RB = QT == 4 ? 32u : 64u;
+    const uint4 *src =
+        packed && QT != 1
+            ? (const uint4 *)(W + ((size_t)(n / 32u) * (K / 64u) + g) * (32u * RB) + (32u * h + n % 32u) * (RB / 2u))
+            : (QT == 4 ? (const uint4 *)(W + (size_t)n * (K / 2u) + g * 32u + 16u * h)
+                       : (QT == 3 ? (const uint4 *)(W + (size_t)n * K + g * 64u + 32u * h)
+                                  : (const uint4 *)((const h16 *)W + (size_t)n * K + g * 64u + 32u * h)));
 #pragma unroll
     for (int v = 0; v < BPiece<QT>::NV; ++v) {
         const uint4 x = src[v];
@@ -193,6 +200,7 @@ struct GemmArgs {
     void *out1, *out2;
     u32 kst;             /* split-K: K steps per blockIdx.z (0: all of K in one block) */
     u32 sc_lds;          /* the block's scale rows are preloaded into dynamic LDS */
+    u32 packed;          /* Q4/Q8 payloads in the GEMM-packed layout */
 };
 
 /* Scale rows in LDS: a block's 128 weight rows x K/64 groups are one
@@ -210,8 +218,10 @@ struct GemmArgs {
 #define UOCR_GEMM_BLDS 1
 #endif
 
-template <int QT, int EPI, bool GROUPED>
+template <int QT, int EPI, bool GROUPED, int TMR>
 __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
+    constexpr int AQ4 = TMR * (TK / 8) / PB; /* activation pieces (8 halves) per thread per K step */
+    static_assert(TMR % 32 == 0 && TMR <= PB && AQ4 * PB == TMR * (TK / 8), "tile rows");
     constexpr int NMAT = EPI == GE_SWIGLU ? 2 : 1;
     /* f16 with one weight matrix: the block loads each K step's raw weight
      * tile with eight lanes per row (whole 128-byte row pieces) into LDS, and
@@ -226,8 +236,8 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     constexpr u32 LDB = RB + 16u;            /* padded LDS row (bytes) */
     constexpr u32 CPR = RB / 16u;            /* 16-byte pieces per row */
     __shared__ __attribute__((aligned(16))) uint8_t bsm[BL ? 2u * TN * LDB : 16u];
-    __shared__ __attribute__((aligned(16))) h16 as[2][TM * LDA];
-    __shared__ int32_t arow[TM], orow[TM];
+    __shared__ __attribute__((aligned(16))) h16 as[2][TMR * LDA];
+    __shared__ int32_t arow[TMR], orow[TMR];
     const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6, hf = lane >> 5;
     u32 n0 = blockIdx.y * TN, rows = p.M, e = 0, s0 = 0;
     if (GROUPED) {
@@ -235,15 +245,15 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
         e = (u32)p.tile_e[blockIdx.x];
         s0 = (u32)p.tile_s0[blockIdx.x];
         rows = (u32)p.tile_s1[blockIdx.x] - s0;
-        if (t < TM) {
+        if (t < TMR) {
             const u32 s = s0 + min(t, rows - 1u);
             arow[t] = p.a_idx[s];
             orow[t] = p.o_idx[s];
         }
     } else {
-        s0 = blockIdx.x * TM;
-        rows = min((u32)TM, p.M - s0);
-        if (t < TM) {
+        s0 = blockIdx.x * TMR;
+        rows = min((u32)TMR, p.M - s0);
+        if (t < TMR) {
             arow[t] = (int32_t)(s0 + min(t, rows - 1u));
             orow[t] = arow[t];
         }
@@ -264,11 +274,11 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     const u32 nrow = min(n0 - nbase + 32u * wave + (lane & 31u), nmax - 1u);
     __syncthreads();
 
-    f32x16 acc[NMAT][2];
+    f32x16 acc[NMAT][TMR / 32];
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TMR / 32; ++j)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[m][j][i] = 0.0f;
 
@@ -279,18 +289,19 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
      * argument struct would copy it to private memory */
     const h16 *Ap = p.A;
     const u32 lda = p.lda, Kd = p.K;
+    const bool pk = p.packed != 0u;
     const u32 NT = Kd / TK, kb0 = p.kst != 0u ? blockIdx.z * p.kst : 0u;
     const u32 NS = p.kst != 0u ? min(p.kst, NT - kb0) : NT;
-    u32 ka[GDEPTH][2][4]; /* words, not uint4: no struct copies, so they stay in registers */
+    u32 ka[GDEPTH][AQ4][4]; /* words, not uint4: no struct copies, so they stay in registers */
     u32 kb[GDEPTH][NMAT][BPiece<QT>::NW], ks[GDEPTH][NMAT];
     extern __shared__ __attribute__((aligned(16))) unsigned short ssc[];
     const bool scl = QT != 1 && p.sc_lds != 0u;
     const u32 lrow0 = n0 - nbase, nvalid = min((u32)TN, nmax - lrow0);
     const u32 lrow = nrow - lrow0; /* this lane's row within the block's scale rows */
     /* this thread's two activation rows, resolved once */
-    const h16 *arp[2];
+    const h16 *arp[AQ4];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < AQ4; ++q) {
         const u32 idx = t + q * PB;
         arp[q] = Ap + (size_t)arow[idx >> 3] * lda + (size_t)kb0 * TK + 8u * (idx & 7u);
     }
@@ -306,7 +317,7 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     auto issue = [&](auto D, u32 st) {
         constexpr int d = decltype(D)::value;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < AQ4; ++q) {
             const uint4 v = *(const uint4 *)(arp[q] + st * TK);
             ka[d][q][0] = v.x;
             ka[d][q][1] = v.y;
@@ -327,7 +338,7 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
             if (!scl) ks[d][0] = ((const unsigned short *)sp[0])[(size_t)nrow * (Kd / 64u) + kb0 + st];
         } else {
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m) b_load<QT>(kb[d][m], ks[d][m], wp[m], sp[m], Kd, nrow, kb0 + st, hf, !scl);
+            for (int m = 0; m < NMAT; ++m) b_load<QT>(kb[d][m], ks[d][m], wp[m], sp[m], Kd, nrow, kb0 + st, hf, !scl, pk);
         }
     };
     auto step = [&](auto D, u32 st) {
@@ -337,7 +348,7 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
         __builtin_amdgcn_sched_barrier(0);
         h16 *ab = as[st & 1u];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < AQ4; ++q) {
             const u32 idx = t + q * PB, r = idx >> 3, c8 = idx & 7u;
             *(uint4 *)(ab + r * LDA + 8u * c8) = make_uint4(ka[d][q][0], ka[d][q][1], ka[d][q][2], ka[d][q][3]);
         }
@@ -383,7 +394,7 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
 #pragma unroll
         for (u32 i = 0; i < 4; ++i) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < TMR / 32; ++j) {
                 U4H8 a;
                 a.u = *(const uint4 *)(ab + (32u * j + (lane & 31u)) * LDA + b_koff<QT>(i, hf));
 #pragma unroll
@@ -439,7 +450,7 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     }
     const u32 act = p.act;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < TMR / 32; ++j) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const u32 r = 32u * j + 8u * (i / 4) + 4u * hf + (i % 4);
@@ -963,7 +974,7 @@ __global__ __launch_bounds__(BUCKET_THREADS) void k_bucket_build(const int32_t *
             off[i] = a;
             toff[i] = b;
             a += cnt[i];
-            b += (cnt[i] + TM - 1) / TM;
+            b += (cnt[i] + GTM - 1) / GTM;
         }
         off[64] = a;
         toff[64] = b;
@@ -973,11 +984,11 @@ __global__ __launch_bounds__(BUCKET_THREADS) void k_bucket_build(const int32_t *
     if (t < 64u) {
         offsets[t] = off[t];
         const int32_t c = cnt[t];
-        for (int32_t k = 0; k * TM < c; ++k) {
+        for (int32_t k = 0; k * GTM < c; ++k) {
             const int32_t ti = toff[t] + k;
             tile_e[ti] = (int32_t)t;
-            tile_s0[ti] = off[t] + k * TM;
-            tile_s1[ti] = off[t] + min(c, (k + 1) * TM);
+            tile_s0[ti] = off[t] + k * GTM;
+            tile_s1[ti] = off[t] + min(c, (k + 1) * GTM);
         }
     }
     for (u32 pr = t; pr < n; pr += BUCKET_THREADS) {
@@ -1016,23 +1027,38 @@ static bool pmat_ok(uocr_qmat m) {
     return m.w != nullptr && pq_ok(m.qtype) && (m.qtype == UOCR_QT_F16 || m.s != nullptr);
 }
 
+/* Tile rows of a GEMM.  128-row tiles (each dequantised weight operand
+ * feeding four MFMAs instead of two) measured slower at the prefill shapes:
+ * 3.83 against 3.17 ms, the grouped gate/up dropping to one wavefront per
+ * SIMD; the kernel keeps the template parameter. */
+static inline u32 gemm_tm(bool, u32) {
+    return (u32)TM;
+}
+
+template <int EPI, bool GROUPED, int TMR>
+static void gemm_dispatch_tm(hipStream_t st, u32 qt, const GemmArgs &a, dim3 grid, size_t shm) {
+    switch (qt) {
+        case UOCR_QT_F16: hipLaunchKernelGGL((k_gemm<1, EPI, GROUPED, TMR>), grid, dim3(PB), 0, st, a); break;
+        case UOCR_QT_Q8: hipLaunchKernelGGL((k_gemm<3, EPI, GROUPED, TMR>), grid, dim3(PB), shm, st, a); break;
+        default: hipLaunchKernelGGL((k_gemm<4, EPI, GROUPED, TMR>), grid, dim3(PB), shm, st, a); break;
+    }
+}
+
 template <int EPI, bool GROUPED>
-static void gemm_dispatch(hipStream_t st, u32 qt, GemmArgs a, dim3 grid) {
+static void gemm_dispatch(hipStream_t st, u32 qt, GemmArgs a, dim3 grid, u32 tmr) {
     const u32 nm = EPI == GE_SWIGLU ? 2u : 1u, nt = a.K / TK;
     a.sc_lds = qt != UOCR_QT_F16 && nm * nt <= SC_LDS_STEPS ? 1u : 0u;
     const size_t shm = a.sc_lds ? (size_t)nm * TN * nt * sizeof(unsigned short) : 0;
-    switch (qt) {
-        case UOCR_QT_F16: hipLaunchKernelGGL((k_gemm<1, EPI, GROUPED>), grid, dim3(PB), 0, st, a); break;
-        case UOCR_QT_Q8: hipLaunchKernelGGL((k_gemm<3, EPI, GROUPED>), grid, dim3(PB), shm, st, a); break;
-        default: hipLaunchKernelGGL((k_gemm<4, EPI, GROUPED>), grid, dim3(PB), shm, st, a); break;
-    }
+    (void)tmr;
+    gemm_dispatch_tm<EPI, GROUPED, TM>(st, qt, a, grid, shm);
 }
 
 /* K splits for a plain GEMM whose tile grid is under one block per CU: the
  * largest power of two <= 8 that keeps the grid in one round of resident
  * blocks (about 512) with at least 5 K steps per split. */
 extern "C" uint32_t uocr_gemm_ksplit(uint32_t M, uint32_t N, uint32_t K) {
-    const u32 blocks = ((M + TM - 1u) / TM) * ((N + TN - 1u) / TN), steps = K / TK;
+    const u32 tm = gemm_tm(false, M);
+    const u32 blocks = ((M + tm - 1u) / tm) * ((N + TN - 1u) / TN), steps = K / TK;
     if (blocks >= 256u) return 1u;
     u32 s = 1u;
     while (s < 8u && blocks * 2u * s <= 512u && steps / (2u * s) >= 5u) s *= 2u;
@@ -1080,7 +1106,9 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
     a.out1 = d->out1;
     a.out2 = d->out2;
     a.kst = 0u;
-    const dim3 grid(grouped ? d->max_tiles : (d->M + TM - 1u) / TM, (d->N + TN - 1u) / TN);
+    a.packed = d->packed != 0u && d->W[0].qtype != UOCR_QT_F16 ? 1u : 0u;
+    const u32 tmr = gemm_tm(grouped, d->M);
+    const dim3 grid(grouped ? d->max_tiles : (d->M + tmr - 1u) / tmr, (d->N + TN - 1u) / TN);
     const u32 qt = d->W[0].qtype;
     if (epi == UOCR_GEMM_VISION && (grouped || d->bias == nullptr || d->act > UOCR_VISION_ACT_GELU_ERF ||
                                     (d->split != 0u && (d->N != 3u * d->split || d->out1 == nullptr ||
@@ -1101,7 +1129,7 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
         a.kst = kst;
         a.out = d->part;
         a.ldo = d->N;
-        gemm_dispatch<GE_PART, false>(st, qt, a, dim3(grid.x, grid.y, S));
+        gemm_dispatch<GE_PART, false>(st, qt, a, dim3(grid.x, grid.y, S), tmr);
         const size_t mn = (size_t)d->M * d->N;
         const u32 mode = epi == UOCR_GEMM_VISION ? RD_VISION : (epi == UOCR_GEMM_F16 ? RD_F16 : RD_F32);
         hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((mn / 4u + PB - 1u) / PB)), dim3(PB), 0, st,
@@ -1109,16 +1137,16 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
                            (const h16 *)d->res, d->ldr, d->out, (h16 *)d->out1, (h16 *)d->out2,
                            epi == UOCR_GEMM_VISION ? d->N : d->ldo);
     } else if (epi == UOCR_GEMM_VISION) {
-        gemm_dispatch<GE_VISION, false>(st, qt, a, grid);
+        gemm_dispatch<GE_VISION, false>(st, qt, a, grid, tmr);
     } else if (epi == UOCR_GEMM_F32) {
-        if (grouped) gemm_dispatch<GE_F32, true>(st, qt, a, grid);
-        else gemm_dispatch<GE_F32, false>(st, qt, a, grid);
+        if (grouped) gemm_dispatch<GE_F32, true>(st, qt, a, grid, tmr);
+        else gemm_dispatch<GE_F32, false>(st, qt, a, grid, tmr);
     } else if (epi == UOCR_GEMM_SWIGLU) {
-        if (grouped) gemm_dispatch<GE_SWIGLU, true>(st, qt, a, grid);
-        else gemm_dispatch<GE_SWIGLU, false>(st, qt, a, grid);
+        if (grouped) gemm_dispatch<GE_SWIGLU, true>(st, qt, a, grid, tmr);
+        else gemm_dispatch<GE_SWIGLU, false>(st, qt, a, grid, tmr);
     } else {
-        if (grouped) gemm_dispatch<GE_F16, true>(st, qt, a, grid);
-        else gemm_dispatch<GE_F16, false>(st, qt, a, grid);
+        if (grouped) gemm_dispatch<GE_F16, true>(st, qt, a, grid, tmr);
+        else gemm_dispatch<GE_F16, false>(st, qt, a, grid, tmr);
     }
     return hipGetLastError();
 }
@@ -1207,5 +1235,41 @@ extern "C" hipError_t uocr_launch_moe_combine(hipStream_t st, const float *Y, co
     const u32 n = P * UOCR_K_HIDDEN;
     hipLaunchKernelGGL(k_moe_combine, dim3((n + PB - 1u) / PB), dim3(PB), 0, st, Y, wts, (const h16 *)shared,
                        (const h16 *)res, P, (h16 *)out);
+    return hipGetLastError();
+}
+
+/* ---- GEMM-packed weight copies -------------------------------------------- */
+
+/* One 16-byte piece per thread: destination piece i of matrix blockIdx.y. */
+template <u32 RB>
+__global__ __launch_bounds__(PB) void k_pack_gemm_rows(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                       u32 rows, u32 K, uint64_t stride) {
+    const u32 steps = K / 64u, per = 32u * RB / 16u; /* pieces per (32-row block, step) */
+    const size_t i = (size_t)blockIdx.x * PB + threadIdx.x, total = (size_t)rows / 32u * steps * per;
+    if (i >= total) return;
+    const size_t blk = i / per;
+    const u32 in = (u32)(i % per), rb = (u32)(blk / steps), g = (u32)(blk % steps);
+    const u32 lanes = RB / 2u / 16u;                       /* pieces per lane */
+    const u32 l = in / lanes, v = in % lanes, h = l / 32u, r = l % 32u;
+    const size_t so = (size_t)(rb * 32u + r) * (K / 64u * RB) + (size_t)g * RB + h * (RB / 2u) + 16u * v;
+    const size_t m = (size_t)blockIdx.y * stride;
+    *(uint4 *)(dst + m + i * 16u) = *(const uint4 *)(src + m + so);
+}
+
+extern "C" hipError_t uocr_launch_pack_gemm_rows(hipStream_t st, uint32_t qtype, const void *src, void *dst,
+                                                 uint32_t rows, uint32_t K, uint32_t count, uint64_t stride) {
+    if (src == nullptr || dst == nullptr || rows == 0u || rows % 32u != 0u || K == 0u || K % 64u != 0u || count == 0u ||
+        (qtype != UOCR_QT_Q4 && qtype != UOCR_QT_Q8)) {
+        return hipErrorInvalidValue;
+    }
+    const size_t pieces = (size_t)rows * (qtype == UOCR_QT_Q4 ? K / 2u : K) / 16u;
+    const dim3 grid((unsigned)((pieces + PB - 1u) / PB), count);
+    if (qtype == UOCR_QT_Q4) {
+        hipLaunchKernelGGL(k_pack_gemm_rows<32u>, grid, dim3(PB), 0, st, (const uint8_t *)src, (uint8_t *)dst, rows, K,
+                           stride);
+    } else {
+        hipLaunchKernelGGL(k_pack_gemm_rows<64u>, grid, dim3(PB), 0, st, (const uint8_t *)src, (uint8_t *)dst, rows, K,
+                           stride);
+    }
     return hipGetLastError();
 }
