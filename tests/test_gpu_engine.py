@@ -105,7 +105,11 @@ def test_converted_model_matches_oracle(gpu, oracle):
     assert best >= 3
 
 
-def test_graph_and_eager_paths_agree(gpu):
+def test_graph_and_eager_paths_agree(gpu, monkeypatch):
+    """The per-step kernels replayed from captured graphs and enqueued
+    eagerly give bit-identical ids and scores (the persistent run, which
+    computes in another order, is switched off)."""
+    monkeypatch.setenv("UOCR_HIP_RUN", "0")
     uocr = gpu
     m = model(uocr, 3)
     rng = np.random.default_rng(5)

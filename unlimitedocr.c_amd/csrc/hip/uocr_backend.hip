@@ -389,7 +389,10 @@ static int upload_slab(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor *ex
 
 /* The persistent decode run's view of the model (device pointers of every
  * layer) and whether this model, device and environment can use it:
- * UOCR_HIP_RUN=1 selects it; the run needs a supported qtype mix, fp16
+ * it is the default decode of Q4 models (3,563 against 3,497 tok/s on
+ * config 5), while Q8 models keep the per-step graphs (their run kernel
+ * spills: 2,548 against 3,121 tok/s); UOCR_HIP_RUN=1 / 0 forces either.  The
+ * run needs a supported qtype mix, fp16
  * routers (for the fold), 256 CUs and cooperative launch. */
 static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
     uocr_run_model &m = ctx->run_model;
@@ -460,9 +463,9 @@ static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
     int cus = 0, coop = 0;
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
     (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, ctx->device);
-    /* opt-in while the per-step graphs are faster: UOCR_HIP_RUN=1 */
     const char *ru = getenv("UOCR_HIP_RUN");
-    ctx->run_ok = ok && uocr_run_supported(&m) && cus == (int)UOCR_RUN_BLOCKS && coop != 0 && ru != nullptr && atoi(ru) != 0;
+    const bool want = ru != nullptr ? atoi(ru) != 0 : m.qf == UOCR_QT_Q4;
+    ctx->run_ok = ok && uocr_run_supported(&m) && cus == (int)UOCR_RUN_BLOCKS && coop != 0 && want;
     return 1;
 }
 
