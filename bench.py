@@ -9,13 +9,14 @@ decode-loop seconds (src/unlimitedocr_c/perf.py:97-102), weights resident in
 HBM before timing starts.  The Q8 and fp16 profiles run the same workload and
 are reported beside it.
 
-`roofline` is the dominant kernel of the config-5 decode loop by time
-(k_moe_gate_up): its decode-shape launches captured into a hipGraph over
-expert-slab copies larger than the Infinity Cache, HIP events around the
-replays.  `roofline.decode_kernels` gives every decode kernel's share and
-fraction from one extra generation of the workload with per-launch HIP events
-on the engine stream (eager launches, dispatch included): algorithmic bytes
-per launch / mean launch time.  `lm_head_config2` times the Q4
+`roofline` is the dominant kernel of the default Q4 decode, k_decode_run
+(one cooperative launch per 8 steps): HIP events around each launch on the
+engine stream over one config-5 generation, algorithmic bytes = 8 x the
+decode bytes per token.  Beside it, for the per-step graph path (the Q8 /
+fp16 default): `graph_path_moe_gate_up`, its dominant kernel k_moe_gate_up at
+the decode shape in a hipGraph over expert-slab copies larger than the
+Infinity Cache, and `graph_path_kernels`, every per-step kernel's share from
+per-launch events (eager launches, dispatch included).  `lm_head_config2` times the Q4
 LM-head GEMV + argmax keys (87,912,964 algorithmic bytes
 per launch) rotating 6 weight copies (528 MB) so launches stream from HBM
 rather than the 256 MB Infinity Cache.
@@ -241,6 +242,47 @@ def gate_up_roofline(log, n_copy: int = 5, per_copy: int = 12, replays: int = 40
                       f"({n_copy * (gw.nbytes + gs.nbytes) * 2 / 1e6:.0f} MB), HIP events around {replays} replays"}
 
 
+def run_kernel_roofline(log) -> dict:
+    """The default Q4 decode: k_decode_run, one cooperative launch per 8 decode
+    steps (LM head + 12 layers each), timed with an event pair around every
+    launch on the engine's stream (UOCR_HIP_RUN_EVENTS=1 with profiling) over
+    one config-5 generation.  Algorithmic bytes per launch = 8 x the decode
+    bytes per token (decode_bytes_per_token: every weight byte a step reads,
+    6 of 64 experts per MoE layer, the KV cache over the attention length)."""
+    os.environ["UOCR_HIP_RUN_EVENTS"] = "1"
+    try:
+        model = uocr.synth_model(uocr.QPROFILE_Q4, 7)
+        ids, mask, rows = make_prompt()
+        with uocr.Engine.from_memory(model, backend="hip", max_prompt_tokens=1024, max_gen_tokens=N_NEW,
+                                     profile=True) as eng:
+            eng.generate_embeddings(ids, mask, rows, N_NEW, flags=uocr.GEN_IGNORE_EOS)
+            eng.profile_reset()
+            out, _, _, dec_ms = eng.generate_embeddings(ids, mask, rows, N_NEW, flags=uocr.GEN_IGNORE_EOS)
+            ev = eng.profile_events()
+        bpt = decode_bytes_per_token(model, ids.size, N_NEW)
+        model.close()
+    finally:
+        del os.environ["UOCR_HIP_RUN_EVENTS"]
+    if "hip.kernel.k_decode_run" not in ev:
+        return {}
+    launches, ms = ev["hip.kernel.k_decode_run"]
+    avg_us = ms * 1e3 / launches
+    algo = 8.0 * bpt
+    gbs = algo / (avg_us * 1e-6) / 1e9
+    log(f"k_decode_run: {launches} launches, {avg_us:.1f} us each ({avg_us / 8:.1f} us/step), {gbs:.0f} GB/s; "
+        f"decode loop {dec_ms:.1f} ms for {out.size} tokens")
+    traffic = None
+    if RUN_TRAFFIC_FILE.exists():
+        traffic = json.loads(RUN_TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    return {"kernel": "k_decode_run<Q8, Q4, Q4, Q4> (persistent cooperative decode: 8 steps of LM head + 12 layers "
+                      "per launch; the default Q4 decode)",
+            "bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s", "frac": round(gbs / 8000.0, 4),
+            "traffic": traffic, "avg_launch_us": round(avg_us, 2), "algorithmic_bytes": int(algo),
+            "launches": launches,
+            "timing": "HIP events around each cooperative launch on the engine stream, one config-5 generation"}
+
+
+RUN_TRAFFIC_FILE = ROOT / "profiles" / "decode_run_q4_traffic.json"
 DECODE_TRAFFIC_FILE = ROOT / "profiles" / "decode_q4_config5_traffic.json"
 TRAFFIC_FILE = ROOT / "profiles" / "lm_head_q4_traffic.json"
 
@@ -635,6 +677,9 @@ def main() -> None:
                     help="run only the config-2 LM-head measurement and a copy probe (for rocprofv3 --pmc runs)")
     ap.add_argument("--decode-kernels-only", action="store_true",
                     help="run only the per-kernel roofline of the config-5 decode loop (eager, event-timed)")
+    ap.add_argument("--run-only", action="store_true",
+                    help="run only the persistent decode kernel's measurement (one config-5 generation) and a copy "
+                         "probe (for rocprofv3 runs)")
     ap.add_argument("--gate-up-only", action="store_true",
                     help="run only the dominant-kernel (k_moe_gate_up) graph measurement and a copy probe "
                          "(for rocprofv3 runs)")
@@ -663,6 +708,10 @@ def main() -> None:
         sys.exit(1)
     if args.decode_kernels_only:
         print(json.dumps({"decode_kernels": decode_kernel_roofline(log)}), flush=True)
+        return
+    if args.run_only:
+        print(json.dumps({"roofline": run_kernel_roofline(log)}), flush=True)
+        copy_probe(log)
         return
     if args.gate_up_only:
         print(json.dumps({"roofline": gate_up_roofline(log)}), flush=True)
@@ -697,8 +746,13 @@ def main() -> None:
     wanted = ["q4"] + [p for p in args.profiles.split(",") if p in names and p != "q4"]
     flags = uocr.GEN_NO_GRAPH if args.no_graph else 0
     results = {p: run_profile(names[p], args.steps, args.warmup, log, flags) for p in wanted}
-    roof = gate_up_roofline(log)
-    roof["decode_kernels"] = decode_kernel_roofline(log)
+    roof = run_kernel_roofline(log)
+    gu = gate_up_roofline(log)
+    if not roof:  # no persistent run on this device: the per-step graphs' dominant kernel
+        roof = gu
+    else:
+        roof["graph_path_moe_gate_up"] = gu
+    roof["graph_path_kernels"] = decode_kernel_roofline(log)
     lm = lm_head_roofline(log)
     cpu = None if args.no_cpu_baseline else cpu_baseline(log)
     ops = None if args.no_ops else operator_benchmarks(log, not args.no_cpu_baseline)

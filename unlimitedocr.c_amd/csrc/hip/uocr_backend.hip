@@ -128,6 +128,7 @@ struct uocr_hip_ctx {
     /* opt-in per-op decode timing (UOCR_HIP_DECODER_PROFILE_DETAIL >= 3 with
      * profiling on): event pairs around every decode launch */
     int profile_detail;
+    int run_events;              /* UOCR_HIP_RUN_EVENTS=1: time each persistent-run launch (profiling on) */
     struct op_timer *tm;         /* active only inside the timed decode loop */
     /* decode trace (uocr_hip_context_trace_enable) */
     uint32_t trace_steps;
@@ -229,6 +230,8 @@ extern "C" uocr_hip_ctx *uocr_hip_context_create(char *err, size_t err_size) {
     }
     /* inv_freq[d] = 2^(d * (-2 log2(theta) / head_dim)), golden.py:410-414 */
     ctx->trace_step = -1;
+    const char *re = getenv("UOCR_HIP_RUN_EVENTS");
+    ctx->run_events = re != nullptr && atoi(re) != 0;
     const char *pd = getenv("UOCR_HIP_DECODER_PROFILE_DETAIL");
     ctx->profile_detail = pd != nullptr ? atoi(pd) : 0;
     const char *fa = getenv("UOCR_HIP_FAULT_ALLOC");
@@ -1102,8 +1105,18 @@ static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, u
     hipEvent_t ev[2];
     HIPCHK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming), "event create");
     HIPCHK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming), "event create");
+    /* per-launch timing (UOCR_HIP_RUN_EVENTS=1 with profiling): an event pair
+     * around each launch on the engine stream, reported as
+     * hip.kernel.k_decode_run once the loop has finished */
+    const bool kev = c->run_events != 0 && c->profile != nullptr && c->profile->report.enabled != 0u;
+    std::vector<hipEvent_t> kt;
+    if (kev) {
+        kt.resize(2u * ((N + DECODE_CHUNK - 1u) / DECODE_CHUNK));
+        for (hipEvent_t &x : kt) HIPCHK(hipEventCreate(&x), "event create");
+    }
     while (issued < N && !eos && ok) {
         const uint32_t end = issued + DECODE_CHUNK < N ? issued + DECODE_CHUNK : N;
+        if (kev) (void)hipEventRecord(kt[2u * chunk], s);
         const hipError_t e = uocr_run_launch(s, c->d_run_model, &c->run_model, c->run_arena, c->kc, c->vc, c->cache_cap,
                                              (int32_t)P, (int32_t)issued, (int32_t)(end - issued), end == N ? 1 : 0,
                                              tag0 + issued, c->tokens, c->scores, c->h, c->d_trace, c->trace_steps,
@@ -1112,6 +1125,7 @@ static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, u
             ok = bfail(err, err_size, "decode run of steps %u-%u: %s", issued, end - 1u, hipGetErrorString(e));
             break;
         }
+        if (kev) (void)hipEventRecord(kt[2u * chunk + 1u], s);
         if (hipMemcpyAsync(c->h_tokens + issued, c->tokens + issued, (size_t)(end - issued) * 4u, hipMemcpyDeviceToHost, s) != hipSuccess ||
             hipEventRecord(ev[chunk & 1u], s) != hipSuccess) {
             ok = bfail(err, err_size, "token readback failed");
@@ -1131,6 +1145,13 @@ static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, u
     const hipError_t se = hipStreamSynchronize(s);
     (void)hipEventDestroy(ev[0]);
     (void)hipEventDestroy(ev[1]);
+    for (uint32_t i = 0; kev && i < chunk; ++i) {
+        float ms = 0.0f;
+        if (se == hipSuccess && hipEventElapsedTime(&ms, kt[2u * i], kt[2u * i + 1u]) == hipSuccess) {
+            uocr_profile_add_ms(c->profile, "hip.kernel.k_decode_run", ms);
+        }
+    }
+    for (hipEvent_t x : kt) (void)hipEventDestroy(x);
     if (se != hipSuccess) return bfail(err, err_size, "decode sync: %s", hipGetErrorString(se));
     uint32_t ctl[4] = {0u, 0u, 0u, 0u};
     HIPCHK(hipMemcpy(ctl, c->run_arena, sizeof(ctl), hipMemcpyDeviceToHost), "run status readback");
