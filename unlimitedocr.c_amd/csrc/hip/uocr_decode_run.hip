@@ -125,9 +125,6 @@ constexpr u64 ARENA_PK = off_layer(UOCR_RUN_LAYERS);
 #ifndef UOCR_RUN_SLEEP
 #define UOCR_RUN_SLEEP 1
 #endif
-#ifndef UOCR_RUN_ZPROBE
-#define UOCR_RUN_ZPROBE 0
-#endif
 #ifndef UOCR_RUN_LIMIT_TICKS
 #define UOCR_RUN_LIMIT_TICKS 5000000ull /* 50 ms of s_memrealtime (100 MHz) */
 #endif
@@ -237,35 +234,11 @@ __device__ __attribute__((noinline)) int give_up(u32 *ctl, u32 where, u32 step) 
  * A thread polls all of its packets that are not current yet in one round
  * (one memory round trip per round whatever their number).  Ends with a
  * barrier, so the sinks' LDS writes are visible. */
-/* Probe phase of a gather: thread p < nprod polls the last packet of
- * producer p (physical base + p * per + per - 1) until it carries tag, so a
- * block waiting for a long stage polls one packet per producer instead of
- * every packet.  1 on abort or timeout. */
-__device__ __forceinline__ int probe(const Run &R, const uint4 *rep, u32 nprod, u32 per, u32 base, u32 tag, u32 where,
-                                     u32 step) {
-    const u32 t = tid_();
-    if (t >= nprod) return 0;
-    const u32 off = (base + t * per + per - 1u) * 16u;
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    for (u32 it = 1;; ++it) {
-        if (cload16(rep, off).x == tag) return 0;
-        __builtin_amdgcn_s_sleep(2);
-        if ((it & 15u) == 0u) {
-            if (cload32(R.ctl, UOCR_RUN_CTL_ABORT * 4u) != 0u) return 1;
-            if (__builtin_amdgcn_s_memrealtime() - t0 > UOCR_RUN_LIMIT_TICKS) return give_up(R.ctl, where, step);
-        }
-    }
-}
-
 template <int MAXP, typename Phys, typename Sink>
 __device__ __forceinline__ bool gather(const Run &R, const uint4 *region, u32 per_copy, u32 n, u32 tag, u32 where,
-                                       u32 step, Phys phys, Sink sink, u32 nprod = 0u, u32 per = 1u, u32 base = 0u) {
+                                       u32 step, Phys phys, Sink sink) {
     const uint4 *rep = region + (size_t)R.xcc * per_copy;
     const u32 t = tid_();
-    if (nprod != 0u &&
-        __builtin_amdgcn_readfirstlane(__syncthreads_or(probe(R, rep, nprod, per, base, tag, where, step))) != 0) {
-        return false;
-    }
     uint4 v[MAXP];
 #pragma unroll
     for (int k = 0; k < MAXP; ++k) v[k] = cload16(rep, phys(min(t + (u32)k * NT, n - 1u)) * 16u);
@@ -427,13 +400,13 @@ __device__ __forceinline__ uint4 norm_piece(const AS1 uint16_t *nw) {
  * red[wave]; after the caller's barrier rms_inv(red) gives 1 / rms(x), and
  * a dot over xs times it is the dot over the normalised row (the norm is
  * linear in 1 / rms), so the dots do not wait for the block reduction. */
-__device__ __forceinline__ void rms_defer(const h16 *x, uint4 w, h16 *xs, float *red) {
+__device__ __forceinline__ void rms_defer(const h16 *x, uint4 w, h16 *xs, float *red, float *x4, float *x8) {
     union h8 {
         uint4 u;
         h16 h[8];
     } xv, wv;
     const u32 t = tid_();
-    float ss = 0.0f;
+    float ss = 0.0f, ps = 0.0f;
     if (t < HID / 8u) {
         xv.u = ((const uint4 *)x)[t];
         wv.u = w;
@@ -442,11 +415,38 @@ __device__ __forceinline__ void rms_defer(const h16 *x, uint4 w, h16 *xs, float 
             const float f = (float)xv.h[j];
             ss = fmaf(f, f, ss);
             xv.h[j] = (h16)(f * (float)wv.h[j]);
+            ps += (float)xv.h[j];
         }
         ((uint4 *)xs)[t] = xv.u;
     }
+    /* the chunk sums of xs for the offset-free dots (LM head) */
+    if (x4 != nullptr || x8 != nullptr) piece_sums(ps, t, HID / 8u, x4, x8);
     ss = wave_sum(ss);
     if ((t & 63u) == 0u) red[t >> 6] = ss;
+}
+
+/* -bias * (activation sum) of chunk slot j of a lane (chunk sub + LPR j),
+ * for chunk_value() */
+template <int QT, int LPR, int J>
+__device__ __forceinline__ void frag_nx(float (&nx)[J], const float *x4, const float *x8, u32 C, u32 sub) {
+    static_assert(QT == 3 || QT == 4, "offset-free dots are Q4/Q8");
+#pragma unroll
+    for (int j = 0; j < J; ++j) nx[j] = -chunk_bias<QT>() * (QT == 4 ? x4 : x8)[min(sub + LPR * (u32)j, C - 1u)];
+}
+
+/* frag_dot() over offset-free chunk dots */
+template <int QT, int LPR, int J>
+__device__ __forceinline__ float frag_dot_x(const RowFrag<J> &f, const h16 *xs, const float (&nx)[J], u32 C, u32 sub) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const u32 c = sub + LPR * j;
+        if (LPR * (j + 1) <= (int)C || c < C) {
+            const float v = chunk_value(chunk_dot_u<QT>(f.w[j], xs, min(c, C - 1u)), (float)f.s[j], nx[j]);
+            acc += c < C ? v : 0.0f;
+        }
+    }
+    return acc;
 }
 __device__ __forceinline__ float rms_inv(const float *red) {
     float s = 0.0f;
@@ -512,6 +512,7 @@ struct Lds {
     u32 *selid;
     unsigned long long *keyw;
     uint8_t *scr;
+    float *xsum; /* chunk sums of the LM head's activation */
 };
 
 /* ---- LM head -------------------------------------------------------------- */
@@ -554,15 +555,17 @@ __device__ bool lm_stage(const Run &R, const Lds &S, u32 tag, u32 htag, int32_t 
         return false;
     }
     TLR(0u);
-    rms_defer(S.hres, nwp, S.xs, S.red);
+    rms_defer(S.hres, nwp, S.xs, S.red, QL == 4 ? S.xsum : nullptr, QL == 3 ? S.xsum : nullptr);
     __syncthreads();
     TLR(128u + 13u);
     const u32 row0 = blockIdx.x * LM_ROWS;
     float bs = -INFINITY;
     u32 bid = NONE_ID;
+    float nx[G::J];
+    frag_nx<QL, G::LPR, G::J>(nx, S.xsum, S.xsum, G::C, sub);
     auto finish = [&](const RowFrag<G::J> &fr, u32 pass) {
         const u32 r = pass * G::GPP + grp;
-        const float d = group_sum<G::LPR>(frag_dot<QL, G::LPR, G::J>(fr, S.xs, G::C, sub));
+        const float d = group_sum<G::LPR>(frag_dot_x<QL, G::LPR, G::J>(fr, S.xs, nx, G::C, sub));
         if (r < LM_ROWS && !isnan(d) && better(d, row0 + r, bs, bid)) {
             bs = d;
             bid = row0 + r;
@@ -690,7 +693,7 @@ __device__ bool qkv_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag,
         }
     }
     TLR(2u * (1u + 5u * l));
-    rms_defer(S.hres, nwp, S.xs, S.red);
+    rms_defer(S.hres, nwp, S.xs, S.red, nullptr, nullptr);
     __syncthreads();
     TLD(l, 0u);
     const float dd = group_sum<G::LPR>(frag_dot<QA, G::LPR, G::J>(F.f, S.xs, G::C, sub)) * rms_inv(S.red);
@@ -1267,7 +1270,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                                                          zp[0] = __uint_as_float(v.y);
                                                          if (z0 + 1u < NEXP) zp[1] = __uint_as_float(v.z);
                                                          if (z0 + 2u < NEXP) zp[2] = __uint_as_float(v.w);
-                                                     }, UOCR_RUN_ZPROBE ? Z_BLOCKS : 0u, PO_Z, PO_AR)) {
+                                                     })) {
             return false;
         }
         TLR(2u * (4u + 5u * l));
@@ -1323,7 +1326,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         __syncthreads();
         if (S.red[15] == 0.0f) return false;
         TLD(l, 15u);
-        rms_defer(S.hres, nwp, S.xs, S.red);
+        rms_defer(S.hres, nwp, S.xs, S.red, nullptr, nullptr);
         __syncthreads();
         inv = rms_inv(S.red);
         TLD(l, 16u);
@@ -1341,7 +1344,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     } else {
         if (!gather_a()) return false;
         TLR(2u * (4u + 5u * l));
-        rms_defer(S.hres, nwp, S.xs, S.red);
+        rms_defer(S.hres, nwp, S.xs, S.red, nullptr, nullptr);
         __syncthreads();
         inv = rms_inv(S.red);
     }
@@ -1393,7 +1396,7 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                             const u32 blk = i / PMID_B, k = i % PMID_B, base = blk * rows_b + 6u * k;
                             if (6u * k < rows_b) put6(mids + base, v, 6u * k, rows_b);
                             (void)nmid;
-                        }, NB, PMID_B)) {
+                        })) {
         return false;
     }
     TLR(2u * (5u + 5u * l));
@@ -1473,7 +1476,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
     __shared__ __attribute__((aligned(16))) float zw[2u * Z_COLS * NEXP];
     __shared__ u32 selid[8];
     __shared__ unsigned long long keyw[NT / 64u];
-    Lds S{xs, hres, outv, red, zout, selw, zw, selid, keyw, scr};
+    __shared__ float xsum[HID / 16u];
+    Lds S{xs, hres, outv, red, zout, selw, zw, selid, keyw, scr, xsum};
     Run R;
     R.M = (const AS4 RunModelD *)A.M;
     R.pk = A.pk;

@@ -241,17 +241,20 @@ __device__ __forceinline__ float chunk_dot<4>(const uint4 w, const h16 *xs, u32 
     const u32 xl[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
     const u32 xh[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
     const u32 wv[4] = {w.x, w.y, w.z, w.w};
-    const h16x2 bias = {(h16)1032.0f, (h16)1032.0f};
-    float d = 0.0f;
+    /* low nibbles: 1024 + q + 8 - 1032 = q; high nibbles stay in place
+     * (bytes 16 (q + 8)): 1024 + 16 (q + 8) - 1152 = 16 q, exact, summed in
+     * a second chain and scaled back by 1/16 (exact) */
+    const h16x2 bl = {(h16)1032.0f, (h16)1032.0f}, bh = {(h16)1152.0f, (h16)1152.0f};
+    float dl = 0.0f, dh = 0.0f;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-        const u32 lo = wv[b] & 0x0F0F0F0Fu, hi = (wv[b] >> 4) & 0x0F0F0F0Fu;
-        d = dot2(magic_pair<SEL01>(lo) - bias, xl[2 * b], d);
-        d = dot2(magic_pair<SEL23>(lo) - bias, xl[2 * b + 1], d);
-        d = dot2(magic_pair<SEL01>(hi) - bias, xh[2 * b], d);
-        d = dot2(magic_pair<SEL23>(hi) - bias, xh[2 * b + 1], d);
+        const u32 lo = wv[b] & 0x0F0F0F0Fu, hi = wv[b] & 0xF0F0F0F0u;
+        dl = dot2(magic_pair<SEL01>(lo) - bl, xl[2 * b], dl);
+        dh = dot2(magic_pair<SEL01>(hi) - bh, xh[2 * b], dh);
+        dl = dot2(magic_pair<SEL23>(lo) - bl, xl[2 * b + 1], dl);
+        dh = dot2(magic_pair<SEL23>(hi) - bh, xh[2 * b + 1], dh);
     }
-    return d;
+    return fmaf(dh, 0.0625f, dl);
 }
 
 /* Q8_0: chunk c is columns 16c..16c+15; byte ^ 0x80 = q + 128. */
@@ -282,6 +285,77 @@ __device__ __forceinline__ float chunk_dot<1>(const uint4 w, const h16 *xs, u32 
     d = dot2(as_h2(w.z), a.z, d);
     d = dot2(as_h2(w.w), a.w, d);
     return d;
+}
+
+/* Offset-free chunk dots.  Each weight byte is taken as the unsigned
+ * integer u it stores (Q4: q + 8 per nibble, Q8: q + 128 after flipping the
+ * sign bit) and placed in an fp16 subnormal, u * 2^-24 (exact), so a weight
+ * pair costs one v_perm and no bias subtraction; the returned raw dot is
+ * sum(u * x) * 2^-24.  chunk_value() restores q = u - bias with the sum of
+ * the chunk's activations:  scale * (2^24 raw - bias * xsum).  fp16
+ * subnormals are preserved by the dot instructions (the kernels run with
+ * fp16 denormals enabled, the compiler's default). */
+template <int QT>
+__device__ __forceinline__ float chunk_dot_u(const uint4 w, const h16 *xs, u32 c);
+
+template <>
+__device__ __forceinline__ float chunk_dot_u<4>(const uint4 w, const h16 *xs, u32 c) {
+    const uint4 *xp = (const uint4 *)(xs + (c >> 1) * 64u + (c & 1u) * 16u);
+    const uint4 l0 = xp[0], l1 = xp[1], g0 = xp[4], g1 = xp[5];
+    const u32 xl[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+    const u32 xh[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const u32 wv[4] = {w.x, w.y, w.z, w.w};
+    /* high nibbles stay in place (bytes 16 u): their chain is scaled by 1/16 */
+    float dl = 0.0f, dh = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const u32 lo = wv[b] & 0x0F0F0F0Fu, hi = wv[b] & 0xF0F0F0F0u;
+        dl = dot2(as_h2(__builtin_amdgcn_perm(0u, lo, SEL01)), xl[2 * b], dl);
+        dh = dot2(as_h2(__builtin_amdgcn_perm(0u, hi, SEL01)), xh[2 * b], dh);
+        dl = dot2(as_h2(__builtin_amdgcn_perm(0u, lo, SEL23)), xl[2 * b + 1], dl);
+        dh = dot2(as_h2(__builtin_amdgcn_perm(0u, hi, SEL23)), xh[2 * b + 1], dh);
+    }
+    return fmaf(dh, 0.0625f, dl);
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot_u<3>(const uint4 w, const h16 *xs, u32 c) {
+    const uint4 *xp = (const uint4 *)(xs + 16u * c);
+    const uint4 a = xp[0], b4 = xp[1];
+    const u32 xv[8] = {a.x, a.y, a.z, a.w, b4.x, b4.y, b4.z, b4.w};
+    const u32 wv[4] = {w.x, w.y, w.z, w.w};
+    float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const u32 u = wv[b] ^ 0x80808080u;
+        d0 = dot2(as_h2(__builtin_amdgcn_perm(0u, u, SEL01)), xv[2 * b], d0);
+        d1 = dot2(as_h2(__builtin_amdgcn_perm(0u, u, SEL23)), xv[2 * b + 1], d1);
+    }
+    return d0 + d1;
+}
+
+template <int QT>
+__host__ __device__ constexpr float chunk_bias() {
+    return QT == 4 ? 8.0f : 128.0f;
+}
+/* scale * (q . x) of a chunk from its raw dot and nx = -bias * xsum */
+__device__ __forceinline__ float chunk_value(float raw, float scale, float nx) {
+    return scale * fmaf(raw, 16777216.0f, nx);
+}
+
+/* Chunk sums of an activation row held as 8-element pieces, thread t of a
+ * wavefront-aligned range holding the fp32 sum p of piece t (0 past the
+ * row): Q4 chunk 2g + h is pieces 8g + 2h, +1, +4, +5 (columns 64g + 16h
+ * and + 32), a Q8 chunk pieces 2c, 2c + 1.  Every lane of the wavefront
+ * calls it. */
+__device__ __forceinline__ void piece_sums(float p, u32 t, u32 npieces, float *x4, float *x8) {
+    const float s1 = p + __shfl_xor(p, 1);
+    const float s2 = s1 + __shfl_xor(s1, 4);
+    if (t < npieces) {
+        if (x8 != nullptr && (t & 1u) == 0u) x8[t >> 1] = s1;
+        if (x4 != nullptr && (t & 7u) == 0u) x4[t >> 2] = s2;
+        if (x4 != nullptr && (t & 7u) == 2u) x4[(t >> 2) + 1u] = s2;
+    }
 }
 
 /* Sum over aligned groups of LPR lanes; every lane receives its group's sum. */
