@@ -1034,20 +1034,35 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
          * GU stage can choose the experts while the rows are computed. */
         const u32 e = tid_() % 64u, q = tid_() / 64u;
         const float *zf = S.zw, *zo = S.zw + Z_COLS * NEXP;
-        float z = 0.0f;
+        /* every operand read before the (ordered) sums, so the LDS round
+         * trips overlap */
+        float wf[G::ZC], wo[G::ZC], xh[G::ZC], xc[G::ZC];
 #pragma unroll
         for (u32 k = 0; k < G::ZC; ++k) {
             const u32 cl = G::ZC * q + k, c = j * Z_COLS + cl;
-            z = fmaf(zf[cl * NEXP + e], (float)S.hres[c], z);
-            z = fmaf(zo[cl * NEXP + e], (float)S.xs[c], z);
+            wf[k] = zf[cl * NEXP + e];
+            wo[k] = zo[cl * NEXP + e];
+            xh[k] = (float)S.hres[c];
+            xc[k] = (float)S.xs[c];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float z = 0.0f;
+#pragma unroll
+        for (u32 k = 0; k < G::ZC; ++k) {
+            z = fmaf(wf[k], xh[k], z);
+            z = fmaf(wo[k], xc[k], z);
         }
         zq[q * 64u + e] = z;
         __syncthreads();
         if (tid_() < 64u) {
             const u32 e2 = tid_();
+            float zk[NT / 64u];
+#pragma unroll
+            for (u32 k = 0; k < NT / 64u; ++k) zk[k] = zq[k * 64u + e2];
+            __builtin_amdgcn_sched_barrier(0);
             float zs = 0.0f;
 #pragma unroll
-            for (u32 k = 0; k < NT / 64u; ++k) zs += zq[k * 64u + e2];
+            for (u32 k = 0; k < NT / 64u; ++k) zs += zk[k];
             S.zout[e2] = zs;
         }
         __syncthreads();
@@ -1284,8 +1299,13 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         float z = 0.0f;
         if (tid_() < 64u) {
             const u32 e = tid_();
+            /* all partials read before the (ordered) sum: one LDS round trip */
+            float zp[Z_BLOCKS];
 #pragma unroll
-            for (u32 j = 0; j < Z_BLOCKS; ++j) z += zpart[j * NEXP + e];
+            for (u32 j = 0; j < Z_BLOCKS; ++j) zp[j] = zpart[j * NEXP + e];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (u32 j = 0; j < Z_BLOCKS; ++j) z += zp[j];
             u32 sid[TOPK];
             topk6_ids(z, sid);
             if (e < TOPK) {
