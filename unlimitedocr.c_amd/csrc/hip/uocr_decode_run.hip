@@ -1211,10 +1211,8 @@ struct DnFrags {
     RowFrag<DnCfg<QF>::J> f;
 };
 
-template <int QF>
-struct DdFrags {
-    RowFrag<DnCfg<QF>::JD> f;
-};
+/* layer 0's dense down row uses the same registers: as many chunk slots */
+static_assert(DnCfg<4>::JD == DnCfg<4>::J && DnCfg<3>::JD == DnCfg<3>::J, "dense down row fits the DN slots");
 
 __device__ __forceinline__ u32 dn_row() {
     return blockIdx.x * DN_ROWS + (tid_() >> 6);
@@ -1244,7 +1242,7 @@ __device__ __forceinline__ void dn_load(const Run &R, const Lds &S, const SlabD 
 }
 
 template <int QF>
-__device__ __forceinline__ void dd_load(const Run &R, DdFrags<QF> &F) {
+__device__ __forceinline__ void dd_load(const Run &R, DnFrags<QF> &F) {
     typedef DnCfg<QF> G;
     if (blockIdx.x >= DN_BLOCKS) return;
     const AS4 RunLayerD &L = R.M->L[0];
@@ -1391,10 +1389,15 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     publish(R, R.pk + off_mid(l), PMID, b * PMID_B, PMID_B, tag,
             [&](u32 p) { return pay6(S.outv, p, moe ? GU_ROWS : nrows); });
     TLD(l, 19u);
-    /* the DN stage's rows of the selected experts, issued once this stage's
-     * own loads are consumed, so the two streams do not share bandwidth on
-     * the critical path */
-    if (moe) dn_load<QF>(R, S, sd, dn);
+    /* the DN stage's rows of the selected experts (layer 0: the dense down
+     * row), issued once this stage's own loads are consumed, so the two
+     * streams do not share bandwidth on the critical path and no DN
+     * registers are live through the gate/up dots */
+    if (moe) {
+        dn_load<QF>(R, S, sd, dn);
+    } else {
+        dd_load<QF>(R, dn);
+    }
     TLD(l, 20u);
     TLR(2u * (4u + 5u * l) + 1u);
     return true;
@@ -1403,7 +1406,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
 /* DN stage: gathers the mids; MoE: out = f16(sum_r w_r D_r.mid_r + f16(SD.smid)
  * + a); layer 0: out = f16(D.mid + a). */
 template <int QF>
-__device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, DnFrags<QF> &dn, DdFrags<QF> &dd) {
+__device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, DnFrags<QF> &dn) {
     typedef DnCfg<QF> G;
     const u32 b = blockIdx.x;
     if (b >= DN_BLOCKS) return true;
@@ -1454,7 +1457,7 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         sh = wave_sum(sh);
         out = acc + (float)(h16)sh + (float)S.hres[c];
     } else {
-        const float d = wave_sum(frag_dot<QF, 64u, G::JD>(dd.f, mids, G::CD, lane));
+        const float d = wave_sum(frag_dot<QF, 64u, G::JD>(dn.f, mids, G::CD, lane));
         out = d + (float)S.hres[c];
     }
     TLD(l, 12u);
@@ -1552,13 +1555,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
             if (!att_stage(R, S, l, t, tag, af)) return;
             GuFrags<QF> gf;
             DnFrags<QF> dn;
-            DdFrags<QF> dd;
             gu_load_static<QF>(R, l, gf);
             o_load_z(R, l, S.zw);
             if (!o_stage<QA>(R, S, l, t, tag, of)) return;
-            if (l == 0u) dd_load<QF>(R, dd);
             if (!gu_stage<QF>(R, S, l, t, tag, gf, dn)) return;
-            if (!dn_stage<QF>(R, S, l, t, tag, dn, dd)) return;
+            if (!dn_stage<QF>(R, S, l, t, tag, dn)) return;
         }
     }
 }
