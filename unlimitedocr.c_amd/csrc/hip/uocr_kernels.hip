@@ -454,9 +454,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
 #pragma unroll
         for (int u = 0; u < ATT_UNROLL; ++u) {
             const int t = min(ib + ATT_GROUPS * u, lim);
-            /* non-temporal: a step reads each cached slot once */
-            kk[u].u = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4v *)(kh + (size_t)t * 128u)));
-            vv[u].u = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4v *)(vh + (size_t)t * 128u)));
+            /* plain loads: non-temporal ones measured slower on this
+             * two-stream pattern (4.57 against 3.87 us for the loads of a
+             * 4,224-slot cache, 240 blocks) */
+            kk[u].u = *(const uint4 *)(kh + (size_t)t * 128u);
+            vv[u].u = *(const uint4 *)(vh + (size_t)t * 128u);
         }
     };
     h8 qq;
@@ -471,9 +473,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
     hold(qq.u);
     i1 = min(st->attn_len, iend);
     lim = max(min(i1, iend) - 1, 0);
-    float qv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qv[j] = (float)qq.h[j];
     float m = -INFINITY, l = 0.0f, acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
@@ -483,9 +482,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
         float mn = m;
 #pragma unroll
         for (int u = 0; u < ATT_UNROLL; ++u) {
-            float d = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) d = fmaf(qv[j], (float)kk[u].h[j], d);
+            /* fp16 pair products are exact in fp32 */
+            float d = dot2(as_h2(qq.u.x), kk[u].u.x, 0.0f);
+            d = dot2(as_h2(qq.u.y), kk[u].u.y, d);
+            d = dot2(as_h2(qq.u.z), kk[u].u.z, d);
+            d = dot2(as_h2(qq.u.w), kk[u].u.w, d);
             sc[u] = ib + ATT_GROUPS * u < i1 ? row16_sum(d) * scale : -INFINITY;
             mn = fmaxf(mn, sc[u]);
         }
