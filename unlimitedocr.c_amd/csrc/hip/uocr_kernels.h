@@ -28,10 +28,7 @@
 #define UOCR_K_RING 128
 #define UOCR_K_MAX_K 6848          /* largest GEMV reduction length */
 #ifndef UOCR_K_ATTN_SPLITS
-/* split-K blocks per head in decode attention: 24 x 10 heads = 240 blocks,
- * about one per CU (a block's K/V stream is bounded by its CU's load
- * throughput, so the kernel is bounded by the CUs it occupies) */
-#define UOCR_K_ATTN_SPLITS 24
+#define UOCR_K_ATTN_SPLITS 16      /* split-K blocks per head in decode attention */
 #endif
 #define UOCR_K_LM_BLOCKS 1024      /* upper bound on LM-head blocks */
 #define UOCR_K_ROUTER_FIX_SHIFT 32 /* router fold accumulator: round(z * 2^32) in int64 */

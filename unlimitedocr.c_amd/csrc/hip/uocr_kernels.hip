@@ -390,7 +390,7 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
 
 /* Threads of an attention block: 32 slot groups of 16 lanes (8 dims per
  * lane).  A group holds U slots in flight (the launch picks U so that one
- * round of loads covers the block's range up to 6,912 slots of cache). */
+ * round of loads covers the block's range up to 4,608 slots of cache). */
 constexpr int ATT_THREADS = 512;
 constexpr int ATT_GROUPS = ATT_THREADS / 16;
 
@@ -454,9 +454,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
 #pragma unroll
         for (int u = 0; u < ATT_UNROLL; ++u) {
             const int t = min(ib + ATT_GROUPS * u, lim);
-            /* plain loads: non-temporal ones measured slower on this
-             * two-stream pattern (4.57 against 3.87 us for the loads of a
-             * 4,224-slot cache, 240 blocks) */
             kk[u].u = *(const uint4 *)(kh + (size_t)t * 128u);
             vv[u].u = *(const uint4 *)(vh + (size_t)t * 128u);
         }
@@ -473,6 +470,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
     hold(qq.u);
     i1 = min(st->attn_len, iend);
     lim = max(min(i1, iend) - 1, 0);
+    float qv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qv[j] = (float)qq.h[j];
     float m = -INFINITY, l = 0.0f, acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
@@ -482,11 +482,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
         float mn = m;
 #pragma unroll
         for (int u = 0; u < ATT_UNROLL; ++u) {
-            /* fp16 pair products are exact in fp32 */
-            float d = dot2(as_h2(qq.u.x), kk[u].u.x, 0.0f);
-            d = dot2(as_h2(qq.u.y), kk[u].u.y, d);
-            d = dot2(as_h2(qq.u.z), kk[u].u.z, d);
-            d = dot2(as_h2(qq.u.w), kk[u].u.w, d);
+            float d = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) d = fmaf(qv[j], (float)kk[u].h[j], d);
             sc[u] = ib + ATT_GROUPS * u < i1 ? row16_sum(d) * scale : -INFINITY;
             mn = fmaxf(mn, sc[u]);
         }
@@ -582,26 +580,18 @@ __device__ __forceinline__ void merge_load(MergeLoads &m, const float *__restric
 
 __device__ __forceinline__ void merge_finish(MergeLoads &m, h16 *ctx, float *wk) {
     constexpr int S = UOCR_K_ATTN_SPLITS, HD = UOCR_K_HEAD_DIM, NO = UOCR_K_HIDDEN / 8;
-    static_assert(UOCR_K_HEADS * S <= BLOCK, "one thread per (head, split) weight");
-    __shared__ float2 mls[UOCR_K_HEADS * S];
+    static_assert(S == 4 || S == 8 || S == 16, "split weights use aligned S-lane groups");
     hold(m.ml);
 #pragma unroll
     for (int k = 0; k < S; ++k) hold(m.a[k]);
     const int t = threadIdx.x;
-    if (t < UOCR_K_HEADS * S) mls[t] = m.ml;
-    __syncthreads();
     if (t < UOCR_K_HEADS * S) {
-        /* thread t: split t % S of head t / S; every thread of a head sums
-         * the head's splits in the same order */
-        const float2 *hm = mls + (t / S) * S;
-        float M = -INFINITY;
+        /* lanes S*h..S*h+S-1 hold the splits of head h */
+        float M = m.ml.x;
 #pragma unroll
-        for (int k = 0; k < S; ++k) M = fmaxf(M, hm[k].x);
-        float tot = 0.0f;
-#pragma unroll
-        for (int k = 0; k < S; ++k) tot += hm[k].x == -INFINITY ? 0.0f : hm[k].y * expf(hm[k].x - M);
+        for (int o = 1; o < S; o <<= 1) M = fmaxf(M, __shfl_xor(M, o));
         const float lf = m.ml.x == -INFINITY ? 0.0f : m.ml.y * expf(m.ml.x - M);
-        wk[t] = lf / tot;
+        wk[t] = lf / group_sum<S>(lf);
     }
     __syncthreads();
     if (t < NO) {
@@ -1257,7 +1247,7 @@ extern "C" hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, c
     }
     /* one round of loads per block where the range allows it */
     const u32 chunk = (cache_capacity + UOCR_K_ATTN_SPLITS - 1u) / UOCR_K_ATTN_SPLITS;
-    auto *kern = chunk <= 3u * ATT_GROUPS ? k_attention<3> : (chunk <= 6u * ATT_GROUPS ? k_attention<6> : k_attention<9>);
+    auto *kern = chunk <= 3u * ATT_GROUPS ? k_attention<3> : (chunk <= 5u * ATT_GROUPS ? k_attention<5> : k_attention<9>);
     hipLaunchKernelGGL(kern, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(ATT_THREADS), 0, st, (const h16 *)q,
                        (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials,
                        (long long *)router_acc, (unsigned long long *)clear_keys);
