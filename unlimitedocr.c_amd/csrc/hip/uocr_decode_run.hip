@@ -434,20 +434,6 @@ __device__ __forceinline__ void frag_nx(float (&nx)[J], const float *x4, const f
     for (int j = 0; j < J; ++j) nx[j] = -chunk_bias<QT>() * (QT == 4 ? x4 : x8)[min(sub + LPR * (u32)j, C - 1u)];
 }
 
-/* frag_dot() over offset-free chunk dots */
-template <int QT, int LPR, int J>
-__device__ __forceinline__ float frag_dot_x(const RowFrag<J> &f, const h16 *xs, const float (&nx)[J], u32 C, u32 sub) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const u32 c = sub + LPR * j;
-        if (LPR * (j + 1) <= (int)C || c < C) {
-            const float v = chunk_value(chunk_dot_u<QT>(f.w[j], xs, min(c, C - 1u)), (float)f.s[j], nx[j]);
-            acc += c < C ? v : 0.0f;
-        }
-    }
-    return acc;
-}
 __device__ __forceinline__ float rms_inv(const float *red) {
     float s = 0.0f;
 #pragma unroll
@@ -565,7 +551,7 @@ __device__ bool lm_stage(const Run &R, const Lds &S, u32 tag, u32 htag, int32_t 
     frag_nx<QL, G::LPR, G::J>(nx, S.xsum, S.xsum, G::C, sub);
     auto finish = [&](const RowFrag<G::J> &fr, u32 pass) {
         const u32 r = pass * G::GPP + grp;
-        const float d = group_sum<G::LPR>(frag_dot_x<QL, G::LPR, G::J>(fr, S.xs, nx, G::C, sub));
+        const float d = group_sum<G::LPR>(frag_dot_u<QL, G::LPR, G::J>(fr, S.xs, nx, G::C, sub));
         if (r < LM_ROWS && !isnan(d) && better(d, row0 + r, bs, bid)) {
             bs = d;
             bid = row0 + r;

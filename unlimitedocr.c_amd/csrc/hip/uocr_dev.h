@@ -417,6 +417,22 @@ __device__ __forceinline__ float frag_dot(const RowFrag<J> &f, const h16 *xs, u3
     return acc;
 }
 
+/* frag_dot() over offset-free chunk dots; nx[j] = -bias * (activation sum
+ * of the lane's chunk slot j). */
+template <int QT, int LPR, int J>
+__device__ __forceinline__ float frag_dot_u(const RowFrag<J> &f, const h16 *xs, const float (&nx)[J], u32 C, u32 sub) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const u32 c = sub + LPR * j;
+        if (LPR * (j + 1) <= (int)C || c < C) {
+            const float v = chunk_value(chunk_dot_u<QT>(f.w[j], xs, min(c, C - 1u)), (float)f.s[j], nx[j]);
+            acc += c < C ? v : 0.0f;
+        }
+    }
+    return acc;
+}
+
 /* Lanes per row and chunk slots per lane for a row of C chunks: the smallest
  * power of two >= 4 with C <= 7 * LPR (else 64 lanes, up to 16 slots). */
 __host__ __device__ constexpr u32 lpr_for(u32 C) {

@@ -143,9 +143,14 @@ __device__ __forceinline__ void stream_rows(const uint8_t *__restrict__ W, const
     };
     float bs = -INFINITY;
     u32 bid = NONE_ID;
+    /* LM head (Q4/Q8): offset-free chunk dots (chunk_dot_u), the bias back
+     * from the chunk sums of the staged activation */
+    constexpr bool XU = EPI == EPI_ARGMAX && QT != 1;
+    float nx[J];
     auto finish = [&](const RowFrag<J>(&f)[NM], u32 gg) {
         const u32 r = gg * R + grp;
-        const float d0 = group_sum<LPR>(frag_dot<QT, LPR, J>(f[0], xs, C, sub));
+        const float d0 = XU ? group_sum<LPR>(frag_dot_u<XU ? QT : 4, LPR, J>(f[0], xs, nx, C, sub))
+                            : group_sum<LPR>(frag_dot<QT, LPR, J>(f[0], xs, C, sub));
         if (EPI == EPI_SWIGLU) {
             const float d1 = group_sum<LPR>(frag_dot<QT, LPR, J>(f[NM - 1], xs, C, sub));
             if (r < rows && sub == 0u) y[r] = (h16)(silu_f(d0) * d1);
@@ -163,6 +168,29 @@ __device__ __forceinline__ void stream_rows(const uint8_t *__restrict__ W, const
     stage_load(sx, x, nw, (int)K);
     load(fa, min(g, ngroups - 1u));
     stage_store(sx, xs, nw, (int)K, red);
+    if constexpr (XU) {
+        /* chunk sums: a Q4 chunk is two runs of 16 columns (one per thread
+         * of a pair), a Q8 chunk one run */
+        __shared__ float xsum[UOCR_K_HIDDEN / 16u];
+        const u32 t = threadIdx.x, np = QT == 4 ? 2u * C : C;
+        float ps = 0.0f;
+        if (t < np && t < 2u * (UOCR_K_HIDDEN / 32u)) {
+            const u32 q = QT == 4 ? t >> 1 : t;
+            const u32 c0 = QT == 4 ? (q >> 1) * 64u + (q & 1u) * 16u + (t & 1u) * 32u : 16u * q;
+            const uint4 u0 = *(const uint4 *)(xs + c0), u1 = *(const uint4 *)(xs + c0 + 8u);
+            const u32 wv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const h16x2 v = __builtin_bit_cast(h16x2, wv[k]);
+                ps += (float)v.x + (float)v.y;
+            }
+        }
+        if (QT == 4) ps += __shfl_xor(ps, 1);
+        if (t < np && (QT != 4 || (t & 1u) == 0u)) xsum[QT == 4 ? t >> 1 : t] = ps;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < J; ++j) nx[j] = -chunk_bias<XU ? QT : 4>() * xsum[min(sub + LPR * (u32)j, C - 1u)];
+    }
     while (g < ngroups) {
         const u32 g1 = g + stride;
         if (g1 < ngroups) load(fb, g1);
