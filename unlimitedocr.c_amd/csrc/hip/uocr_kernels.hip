@@ -60,6 +60,14 @@
  * k_attn_out) are read non-temporally, so the Infinity Cache keeps the
  * weights that stay resident across steps with less pressure (measured:
  * Q8 decode 3,059 -> 3,103 tok/s, fp16 2,479 -> 2,560). */
+/* The shared experts stay resident across steps when quantised (Q4 40 MB,
+ * Q8 75 MB); in fp16 (138 MB) they do not fit beside the other resident
+ * weights and are read non-temporally (measured: fp16 decode 2,515 -> 2,561
+ * tok/s; Q8 with them non-temporal 3,105 -> 3,089). */
+template <int QS>
+__host__ __device__ constexpr bool shared_nt() {
+    return QS == 1;
+}
 #ifndef UOCR_ATT_W_NT
 #define UOCR_ATT_W_NT true
 #endif
@@ -799,8 +807,8 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl
         XStage<UOCR_K_HIDDEN, SMALL_BLOCK> sx;
         stage_load(sx, x, nw, UOCR_K_HIDDEN);
         RowFrag<J> fg, fu;
-        frag_load<QS, LPR, J>(fg, (const uint8_t *)SG.w + (size_t)rr * rb, (const h16 *)SG.s + (size_t)rr * G, C, sub);
-        frag_load<QS, LPR, J>(fu, (const uint8_t *)SU.w + (size_t)rr * rb, (const h16 *)SU.s + (size_t)rr * G, C, sub);
+        frag_load<QS, LPR, J, shared_nt<QS>()>(fg, (const uint8_t *)SG.w + (size_t)rr * rb, (const h16 *)SG.s + (size_t)rr * G, C, sub);
+        frag_load<QS, LPR, J, shared_nt<QS>()>(fu, (const uint8_t *)SU.w + (size_t)rr * rb, (const h16 *)SU.s + (size_t)rr * G, C, sub);
         stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
         const float dg = group_sum<LPR>(frag_dot<QS, LPR, J>(fg, xs, C, sub));
         const float du = group_sum<LPR>(frag_dot<QS, LPR, J>(fu, xs, C, sub));
@@ -903,7 +911,7 @@ __global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const u
         mv[p] = *src;
     }
     RowFrag<JS> fs;
-    frag_load<QS, LPR, JS>(fs, (const uint8_t *)SD.w + (size_t)cc * 16u * CS, (const h16 *)SD.s + (size_t)cc * GS, CS,
+    frag_load<QS, LPR, JS, shared_nt<QS>()>(fs, (const uint8_t *)SD.w + (size_t)cc * 16u * CS, (const h16 *)SD.s + (size_t)cc * GS, CS,
                            sub);
     u32 e[UOCR_K_TOPK];
     float w[UOCR_K_TOPK];
