@@ -122,13 +122,14 @@ __host__ __device__ constexpr u64 off_mid(u32 l) { return off_o(l) + (u64)PO * N
 __host__ __device__ constexpr u64 off_h(u32 l) { return off_mid(l) + (u64)PMID * NREP; }
 constexpr u64 ARENA_PK = off_layer(UOCR_RUN_LAYERS);
 
-/* Infinity Cache residency (256 MB) across decode steps: the LM head (88 MB)
+/* Infinity Cache residency (256 MB) across decode steps: a Q4 LM head (88 MB)
  * with plain loads stays resident beside the shared experts, dense layer 0,
  * the folds and the KV cache; the attention projections (81 MB of Q8) are
  * read non-temporally instead (measured: 3,831 against 3,814 tok/s; the LM
- * head plain with the attention plain too: 3,705). */
+ * head plain with the attention plain too: 3,705).  A Q8 LM head (170 MB)
+ * does not fit and is read non-temporally. */
 #ifndef UOCR_RUN_LM_NT
-#define UOCR_RUN_LM_NT false
+#define UOCR_RUN_LM_NT (QL != 4)
 #endif
 #ifndef UOCR_RUN_ATT_NT
 #define UOCR_RUN_ATT_NT true
