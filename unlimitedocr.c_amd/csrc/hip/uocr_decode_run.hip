@@ -87,6 +87,15 @@ __device__ __forceinline__ u32 tid_() {
     return t;
 }
 
+/* Block barrier for data exchanged through LDS by ordinary LDS stores: waits
+ * for this wavefront's LDS operations only.  Once a wavefront has issued
+ * LDS-direct loads, __syncthreads() also drains every global load in flight
+ * (vmcnt(0)), so a barrier placed while polls or weight rows are still
+ * arriving would hold the whole block for that round trip. */
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 constexpr u32 NB = UOCR_RUN_BLOCKS, NT = UOCR_RUN_THREADS, NREP = UOCR_RUN_REPL;
 constexpr u32 HID = UOCR_K_HIDDEN, HDIM = UOCR_K_HEAD_DIM, NHEAD = UOCR_K_HEADS, NEXP = UOCR_K_EXPERTS;
 constexpr u32 TOPK = UOCR_K_TOPK, EI = 896u, SI = 1792u, DI = 6848u, VOCAB = 129280u, RING = UOCR_K_RING;
@@ -1313,7 +1322,8 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                 }
             }
         }
-        __syncthreads();
+        /* the last wavefront's polls for a are in flight */
+        lds_barrier();
         if (R.trace != nullptr && b == 0u && (u32)t < R.trace_steps && tid_() < TOPK) {
             R.trace[((size_t)t * 11u + (l - 1u)) * TOPK + tid_()] = S.selid[tid_()];
         }
@@ -1341,11 +1351,12 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                 put6(hres + j * O_ROWS + 6u * k, v, 6u * k, O_ROWS);
             });
         if (tid_() == NT - 64u) S.red[15] = ok_a ? 1.0f : 0.0f;
-        __syncthreads();
+        /* the other wavefronts' expert rows may still be arriving */
+        lds_barrier();
         if (S.red[15] == 0.0f) return false;
         TLD(l, 15u);
         rms_defer(S.hres, nwp, S.xs, S.red, nullptr, nullptr);
-        __syncthreads();
+        lds_barrier();
         inv = rms_inv(S.red);
         TLD(l, 16u);
         if (tid_() < 64u) {
