@@ -12,8 +12,8 @@ are reported beside it.
 `roofline` is the dominant kernel of the default Q4 decode, k_decode_run
 (one cooperative launch per 8 steps): HIP events around each launch on the
 engine stream over one config-5 generation, algorithmic bytes = 8 x the
-decode bytes per token.  Beside it, for the per-step graph path (the Q8 /
-fp16 default): `graph_path_moe_gate_up`, its dominant kernel k_moe_gate_up at
+decode bytes per token.  The Q8 profile decodes through the same run; beside
+it, for the per-step graph path (the fp16 default): `graph_path_moe_gate_up`, its dominant kernel k_moe_gate_up at
 the decode shape in a hipGraph over expert-slab copies larger than the
 Infinity Cache, and `graph_path_kernels`, every per-step kernel's share from
 per-launch events (eager launches, dispatch included).  `lm_head_config2` times the Q4
@@ -275,7 +275,7 @@ def run_kernel_roofline(log) -> dict:
     if RUN_TRAFFIC_FILE.exists():
         traffic = json.loads(RUN_TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
     return {"kernel": "k_decode_run<Q8, Q4, Q4, Q4> (persistent cooperative decode: 8 steps of LM head + 12 layers "
-                      "per launch; the default Q4 decode)",
+                      "per launch; the default Q4 and Q8 decode)",
             "bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s", "frac": round(gbs / 8000.0, 4),
             "traffic": traffic, "avg_launch_us": round(avg_us, 2), "algorithmic_bytes": int(algo),
             "launches": launches,

@@ -392,11 +392,11 @@ static int upload_slab(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor *ex
 
 /* The persistent decode run's view of the model (device pointers of every
  * layer) and whether this model, device and environment can use it:
- * it is the default decode of Q4 models (3,563 against 3,497 tok/s on
- * config 5), while Q8 models keep the per-step graphs (their run kernel
- * spills: 2,548 against 3,121 tok/s); UOCR_HIP_RUN=1 / 0 forces either.  The
- * run needs a supported qtype mix, fp16
- * routers (for the fold), 256 CUs and cooperative launch. */
+ * it is the default decode wherever it is supported (config 5: Q4 3,873
+ * against about 3,500 tok/s for the per-step graphs, Q8 3,178 against
+ * 3,102); UOCR_HIP_RUN=1 / 0 forces either.  The run needs Q8 attention with
+ * Q4 or Q8 everywhere else (fp16 weights keep the graphs), fp16 routers (for
+ * the fold), 256 CUs and cooperative launch. */
 static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
     uocr_run_model &m = ctx->run_model;
     memset(&m, 0, sizeof(m));
@@ -467,7 +467,7 @@ static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
     (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, ctx->device);
     const char *ru = getenv("UOCR_HIP_RUN");
-    const bool want = ru != nullptr ? atoi(ru) != 0 : m.qf == UOCR_QT_Q4;
+    const bool want = ru != nullptr ? atoi(ru) != 0 : true;
     ctx->run_ok = ok && uocr_run_supported(&m) && cus == (int)UOCR_RUN_BLOCKS && coop != 0 && want;
     return 1;
 }

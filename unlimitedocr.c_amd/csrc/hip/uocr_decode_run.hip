@@ -1313,8 +1313,10 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (u32 j = 0; j < Z_BLOCKS; ++j) z += zp[j];
+            TLD(l, 22u);
             u32 sid[TOPK];
             topk6_ids(z, sid);
+            TLD(l, 23u);
             if (e < TOPK) {
 #pragma unroll
                 for (u32 k = 0; k < TOPK; ++k) {
