@@ -922,10 +922,13 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         e = (x);                      \
         if (e != hipSuccess) return e; \
     } while (0)
+    /* each layer's input norm comes out of the previous layer's last kernel
+     * (the combine, or layer 0's down reduce); only layer 0 launches it */
     for (uint32_t l = 0; l < UOCR_DECODER_LAYERS; ++l) {
         const dev_layer &L = c->L[l];
+        const uint16_t *next_norm = l + 1u < UOCR_DECODER_LAYERS ? c->L[l + 1u].in_norm : nullptr;
         uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
-        ENQ(uocr_launch_rows_rmsnorm(s, H, L.in_norm, P, c->p_xn));
+        if (l == 0u) ENQ(uocr_launch_rows_rmsnorm(s, H, L.in_norm, P, c->p_xn));
         uocr_gemm_desc d = gdesc(c->p_xn, H_SIZE, P, 3u * H_SIZE, H_SIZE, c->p_qkv, 3u * H_SIZE);
         d.W[0] = packed_of(L.q, L.pq);
         d.W[1] = packed_of(L.k, L.pk);
@@ -946,8 +949,9 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         d.res = H;
         d.ldr = H_SIZE;
         if (c->prefill_ksplit) with_ksplit(d, c->p_kpart);
+        d.norm_w = L.post_norm;
+        d.norm_out = c->p_xn;
         ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
-        ENQ(uocr_launch_rows_rmsnorm(s, c->p_a, L.post_norm, P, c->p_xn));
         if (l == 0u) {
             const uint32_t I0 = UOCR_DENSE_LAYER0_INTERMEDIATE;
             d = gdesc(c->p_xn, H_SIZE, P, I0, H_SIZE, c->p_mid, I0);
@@ -961,6 +965,8 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
             d.res = c->p_a;
             d.ldr = H_SIZE;
             if (c->prefill_ksplit) with_ksplit(d, c->p_kpart);
+            d.norm_w = next_norm;
+            d.norm_out = next_norm != nullptr ? c->p_xn : nullptr;
             ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
             continue;
         }
@@ -1009,7 +1015,11 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         dd.out = c->p_y;
         dd.ldo = H_SIZE;
         ENQ(uocr_launch_gemm(s, UOCR_GEMM_F32, &dd));
-        ENQ(uocr_launch_moe_combine(s, c->p_y, c->p_wts, c->p_sout, c->p_a, P, H));
+        if (next_norm != nullptr) {
+            ENQ(uocr_launch_moe_combine_norm(s, c->p_y, c->p_wts, c->p_sout, c->p_a, P, H, next_norm, c->p_xn));
+        } else {
+            ENQ(uocr_launch_moe_combine(s, c->p_y, c->p_wts, c->p_sout, c->p_a, P, H));
+        }
     }
     return hipMemcpyAsync(c->h, H + (size_t)(P - 1u) * H_SIZE, H_SIZE * 2u, hipMemcpyDeviceToDevice, s);
 #undef ENQ

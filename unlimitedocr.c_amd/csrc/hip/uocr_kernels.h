@@ -224,6 +224,10 @@ typedef struct uocr_gemm_desc {
     /* Q4/Q8 weights: W[i].w (and each expert of a slab) holds the GEMM-packed
      * copy of uocr_launch_pack_gemm_rows instead of the row-major payload */
     uint32_t packed;
+    /* UOCR_GEMM_F16, not grouped, N == ldo == 1280: norm_w set also writes
+     * norm_out = f16(rmsnorm(out) * norm_w) (fused into the split-K reduce) */
+    const uint16_t *norm_w;
+    uint16_t *norm_out;
 } uocr_gemm_desc;
 
 hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d);
@@ -259,6 +263,11 @@ hipError_t uocr_launch_route_rows(hipStream_t st, const float *logits, uint32_t 
                                   int32_t *tile_s0, int32_t *tile_s1, int32_t *ntiles, int32_t *list_tok,
                                   int32_t *list_pair);
 /* out[t] = f16(sum_r wts[t][r] * Y[t*6+r] + shared[t] + res[t]). */
+/* uocr_launch_moe_combine, then norm_out = f16(rmsnorm(out) * norm_w) of each
+ * row (the next layer's input norm), in one launch. */
+hipError_t uocr_launch_moe_combine_norm(hipStream_t st, const float *Y, const float *wts, const uint16_t *shared,
+                                        const uint16_t *res, uint32_t P, uint16_t *out, const uint16_t *norm_w,
+                                        uint16_t *norm_out);
 hipError_t uocr_launch_moe_combine(hipStream_t st, const float *Y, const float *wts, const uint16_t *shared,
                                    const uint16_t *res, uint32_t P, uint16_t *out);
 

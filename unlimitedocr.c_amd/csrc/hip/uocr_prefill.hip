@@ -542,19 +542,15 @@ __global__ __launch_bounds__(PB) void k_split_reduce(const float *__restrict__ p
 /* row RMSNorm, RoPE + KV scatter                                            */
 /* ------------------------------------------------------------------------ */
 
-/* One wavefront per row of 1280: y = f16(x * inv_rms * w) (norm.metal:12-40). */
-__global__ __launch_bounds__(PB) void k_rows_rmsnorm(const h16 *__restrict__ x, const h16 *__restrict__ w, u32 P,
-                                                     h16 *__restrict__ y) {
-    const u32 row = blockIdx.x * (PB / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
-    if (row >= P) return;
-    const h16 *xr = x + (size_t)row * UOCR_K_HIDDEN;
-    U4H8 v[3];
+/* RMSNorm of one row of 1280 held by a wavefront: lane l holds the 8-half
+ * pieces l, l + 64, l + 128 (< 160) in v.  Writes yr = f16(x * inv_rms * w)
+ * (norm.metal:12-40), the sum of squares in fp32 in a fixed order (lane
+ * pieces in order, then the butterfly), so every caller rounds alike. */
+__device__ __forceinline__ void row_norm_tail(U4H8 (&v)[3], u32 lane, const h16 *__restrict__ w, h16 *__restrict__ yr) {
     float ss = 0.0f;
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
-        const u32 i = lane + 64u * q;
-        if (i < UOCR_K_HIDDEN / 8u) {
-            v[q].u = ((const uint4 *)xr)[i];
+        if (lane + 64u * q < UOCR_K_HIDDEN / 8u) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) ss = fmaf((float)v[q].h[j], (float)v[q].h[j], ss);
         }
@@ -565,13 +561,66 @@ __global__ __launch_bounds__(PB) void k_rows_rmsnorm(const h16 *__restrict__ x, 
     for (int q = 0; q < 3; ++q) {
         const u32 i = lane + 64u * q;
         if (i < UOCR_K_HIDDEN / 8u) {
-            U4H8 wv;
+            U4H8 wv, y;
             wv.u = ((const uint4 *)w)[i];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[q].h[j] = (h16)(((float)v[q].h[j] * inv) * (float)wv.h[j]);
-            ((uint4 *)(y + (size_t)row * UOCR_K_HIDDEN))[i] = v[q].u;
+            for (int j = 0; j < 8; ++j) y.h[j] = (h16)(((float)v[q].h[j] * inv) * (float)wv.h[j]);
+            ((uint4 *)yr)[i] = y.u;
         }
     }
+}
+
+/* One wavefront per row of 1280: y = f16(x * inv_rms * w). */
+__global__ __launch_bounds__(PB) void k_rows_rmsnorm(const h16 *__restrict__ x, const h16 *__restrict__ w, u32 P,
+                                                     h16 *__restrict__ y) {
+    const u32 row = blockIdx.x * (PB / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    if (row >= P) return;
+    const h16 *xr = x + (size_t)row * UOCR_K_HIDDEN;
+    U4H8 v[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const u32 i = lane + 64u * q;
+        if (i < UOCR_K_HIDDEN / 8u) v[q].u = ((const uint4 *)xr)[i];
+    }
+    row_norm_tail(v, lane, w, y + (size_t)row * UOCR_K_HIDDEN);
+}
+
+/* Split-K reduce of a 1280-column fp16 GEMM output with its residual, fused
+ * with the RMSNorm that reads it: per row (one wavefront), out = f16(sum of
+ * the S planes in order + res) as k_split_reduce (RD_F16) rounds it, then
+ * y = rmsnorm(out) * w as k_rows_rmsnorm rounds it. */
+__global__ __launch_bounds__(PB) void k_reduce_norm(const float *__restrict__ part, u32 S, u32 M,
+                                                    const h16 *__restrict__ res, u32 ldr, h16 *__restrict__ out,
+                                                    u32 ldo, const h16 *__restrict__ w, h16 *__restrict__ y) {
+    const u32 row = blockIdx.x * (PB / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    if (row >= M) return;
+    const size_t MN = (size_t)M * UOCR_K_HIDDEN;
+    U4H8 v[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const u32 i = lane + 64u * q;
+        if (i >= UOCR_K_HIDDEN / 8u) continue;
+        const float *p0 = part + (size_t)row * UOCR_K_HIDDEN + 8u * i;
+        float4 a = *(const float4 *)p0, b = *(const float4 *)(p0 + 4);
+        for (u32 z = 1; z < S; ++z) {
+            const float4 c = *(const float4 *)(p0 + z * MN), d = *(const float4 *)(p0 + z * MN + 4);
+            a.x += c.x;
+            a.y += c.y;
+            a.z += c.z;
+            a.w += c.w;
+            b.x += d.x;
+            b.y += d.y;
+            b.z += d.z;
+            b.w += d.w;
+        }
+        const float r[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        U4H8 rr;
+        if (res != nullptr) rr.u = *(const uint4 *)(res + (size_t)row * ldr + 8u * i);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[q].h[j] = (h16)(res != nullptr ? r[j] + (float)rr.h[j] : r[j]);
+        *(uint4 *)(out + (size_t)row * ldo + 8u * i) = v[q].u;
+    }
+    row_norm_tail(v, lane, w, y + (size_t)row * UOCR_K_HIDDEN);
 }
 
 struct RopeTabP {
@@ -1015,6 +1064,43 @@ __global__ __launch_bounds__(PB) void k_moe_combine(const float *__restrict__ Y,
     out[idx] = (h16)(acc + (float)shared[idx] + (float)res[idx]);
 }
 
+/* k_moe_combine fused with the next layer's input RMSNorm: one wavefront
+ * per token row, the same per-element arithmetic, then y = rmsnorm(out) * w
+ * as k_rows_rmsnorm rounds it. */
+__global__ __launch_bounds__(PB) void k_moe_combine_norm(const float *__restrict__ Y, const float *__restrict__ wts,
+                                                         const h16 *__restrict__ shared, const h16 *__restrict__ res,
+                                                         u32 P, h16 *__restrict__ out, const h16 *__restrict__ w,
+                                                         h16 *__restrict__ y) {
+    const u32 t = blockIdx.x * (PB / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    if (t >= P) return;
+    float wr[UOCR_K_TOPK];
+#pragma unroll
+    for (int r = 0; r < UOCR_K_TOPK; ++r) wr[r] = wts[t * UOCR_K_TOPK + r];
+    U4H8 v[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const u32 i = lane + 64u * q;
+        if (i >= UOCR_K_HIDDEN / 8u) continue;
+        const size_t base = (size_t)t * UOCR_K_HIDDEN + 8u * i;
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int r = 0; r < UOCR_K_TOPK; ++r) {
+            const float *yr = Y + ((size_t)t * UOCR_K_TOPK + r) * UOCR_K_HIDDEN + 8u * i;
+            const float4 a = *(const float4 *)yr, b = *(const float4 *)(yr + 4);
+            const float e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = fmaf(wr[r], e[j], acc[j]);
+        }
+        U4H8 sh, rs;
+        sh.u = *(const uint4 *)(shared + base);
+        rs.u = *(const uint4 *)(res + base);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[q].h[j] = (h16)(acc[j] + (float)sh.h[j] + (float)rs.h[j]);
+        *(uint4 *)(out + base) = v[q].u;
+    }
+    row_norm_tail(v, lane, w, y + (size_t)t * UOCR_K_HIDDEN);
+}
+
 /* ------------------------------------------------------------------------ */
 /* launchers                                                                 */
 /* ------------------------------------------------------------------------ */
@@ -1120,6 +1206,14 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
                                                      : (epi == UOCR_GEMM_F16 || epi == UOCR_GEMM_F32) &&
                                                            d->ldo % 4u == 0u &&
                                                            (d->res == nullptr || d->ldr % 4u == 0u));
+    /* norm_w: the F16 output rows also go through the RMSNorm into norm_out
+     * (fused into the split-K reduce, else a row-norm launch after the GEMM) */
+    const bool want_norm = d->norm_w != nullptr;
+    if (want_norm && (epi != UOCR_GEMM_F16 || grouped || d->norm_out == nullptr || d->N != UOCR_K_HIDDEN ||
+                      d->ldo != UOCR_K_HIDDEN || (d->res != nullptr && d->ldr % 8u != 0u))) {
+        return hipErrorInvalidValue;
+    }
+    const bool fuse_norm = want_norm && splittable;
     if (splittable) {
         /* split-K: blockIdx.z takes K steps [z*kst, (z+1)*kst) into an fp32
          * partial plane of part, then one ordered reduce applies the
@@ -1132,6 +1226,12 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
         gemm_dispatch<GE_PART, false>(st, qt, a, dim3(grid.x, grid.y, S), tmr);
         const size_t mn = (size_t)d->M * d->N;
         const u32 mode = epi == UOCR_GEMM_VISION ? RD_VISION : (epi == UOCR_GEMM_F16 ? RD_F16 : RD_F32);
+        if (fuse_norm) {
+            hipLaunchKernelGGL(k_reduce_norm, dim3((d->M + 3u) / 4u), dim3(PB), 0, st, (const float *)d->part, S,
+                               d->M, (const h16 *)d->res, d->ldr, (h16 *)d->out, d->ldo, (const h16 *)d->norm_w,
+                               (h16 *)d->norm_out);
+            return hipGetLastError();
+        }
         hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((mn / 4u + PB - 1u) / PB)), dim3(PB), 0, st,
                            (const float *)d->part, S, d->M, d->N, mode, (const h16 *)d->bias, d->act, d->split,
                            (const h16 *)d->res, d->ldr, d->out, (h16 *)d->out1, (h16 *)d->out2,
@@ -1147,6 +1247,10 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
     } else {
         if (grouped) gemm_dispatch<GE_F16, true>(st, qt, a, grid, tmr);
         else gemm_dispatch<GE_F16, false>(st, qt, a, grid, tmr);
+        if (want_norm) {
+            hipLaunchKernelGGL(k_rows_rmsnorm, dim3((d->M + 3u) / 4u), dim3(PB), 0, st, (const h16 *)d->out,
+                               (const h16 *)d->norm_w, d->M, (h16 *)d->norm_out);
+        }
     }
     return hipGetLastError();
 }
@@ -1224,6 +1328,18 @@ extern "C" hipError_t uocr_launch_route_rows(hipStream_t st, const float *logits
     hipLaunchKernelGGL(k_route_rows, dim3((P + 3u) / 4u), dim3(PB), 0, st, logits, P, norm_topk, ids, wts);
     hipLaunchKernelGGL(k_bucket_build, dim3(1), dim3(BUCKET_THREADS), 0, st, (const int32_t *)ids, P, offsets,
                        tile_e, tile_s0, tile_s1, ntiles, list_tok, list_pair);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_moe_combine_norm(hipStream_t st, const float *Y, const float *wts,
+                                                   const uint16_t *shared, const uint16_t *res, uint32_t P,
+                                                   uint16_t *out, const uint16_t *norm_w, uint16_t *norm_out) {
+    if (Y == nullptr || wts == nullptr || shared == nullptr || res == nullptr || out == nullptr || norm_w == nullptr ||
+        norm_out == nullptr || P == 0u) {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(k_moe_combine_norm, dim3((P + 3u) / 4u), dim3(PB), 0, st, Y, wts, (const h16 *)shared,
+                       (const h16 *)res, P, (h16 *)out, (const h16 *)norm_w, (h16 *)norm_out);
     return hipGetLastError();
 }
 
