@@ -971,22 +971,22 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
             continue;
         }
         const uint32_t SI = UOCR_MOE_SHARED_INTERMEDIATE, EI = UOCR_MOE_EXPERT_INTERMEDIATE;
-        d = gdesc(c->p_xn, H_SIZE, P, UOCR_ROUTED_EXPERTS, H_SIZE, c->p_logits, UOCR_ROUTED_EXPERTS);
-        d.W[0].w = L.router;
-        d.W[0].s = nullptr;
-        d.W[0].qtype = UOCR_QT_F16;
-        ENQ(uocr_launch_gemm(s, UOCR_GEMM_F32, &d));
+        /* the router logits share a launch with the shared gate/up (both read
+         * xn), the shared down with the routed gate/up (after the routing) */
+        uocr_gemm_desc dr = gdesc(c->p_xn, H_SIZE, P, UOCR_ROUTED_EXPERTS, H_SIZE, c->p_logits, UOCR_ROUTED_EXPERTS);
+        dr.W[0].w = L.router;
+        dr.W[0].s = nullptr;
+        dr.W[0].qtype = UOCR_QT_F16;
+        uocr_gemm_desc dsg = gdesc(c->p_xn, H_SIZE, P, SI, H_SIZE, c->p_smid, SI);
+        dsg.packed = L.psg != nullptr && L.psu != nullptr;
+        dsg.W[0] = dsg.packed ? packed_of(L.sgate, L.psg) : L.sgate;
+        dsg.W[1] = dsg.packed ? packed_of(L.sup, L.psu) : L.sup;
+        ENQ(uocr_launch_gemm_pair(s, UOCR_GEMM_SWIGLU, &dsg, UOCR_GEMM_F32, &dr));
         ENQ(uocr_launch_route_rows(s, c->p_logits, P, 0, c->p_ids, c->p_wts, c->p_offsets, c->p_tile_e, c->p_tile_s0, c->p_tile_s1, c->p_ntiles, c->p_list_tok,
                                    c->p_list_pair));
-        d = gdesc(c->p_xn, H_SIZE, P, SI, H_SIZE, c->p_smid, SI);
-        d.packed = L.psg != nullptr && L.psu != nullptr;
-        d.W[0] = d.packed ? packed_of(L.sgate, L.psg) : L.sgate;
-        d.W[1] = d.packed ? packed_of(L.sup, L.psu) : L.sup;
-        ENQ(uocr_launch_gemm(s, UOCR_GEMM_SWIGLU, &d));
-        d = gdesc(c->p_smid, SI, P, H_SIZE, SI, c->p_sout, H_SIZE);
-        d.W[0] = packed_of(L.sdown, L.psd);
-        d.packed = L.psd != nullptr;
-        ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
+        uocr_gemm_desc dsd = gdesc(c->p_smid, SI, P, H_SIZE, SI, c->p_sout, H_SIZE);
+        dsd.W[0] = packed_of(L.sdown, L.psd);
+        dsd.packed = L.psd != nullptr;
         d = gdesc(c->p_xn, H_SIZE, 0, EI, H_SIZE, c->p_rmid, EI);
         d.packed = L.peg != nullptr && L.peu != nullptr;
         d.W[0] = d.packed ? packed_of(L.slab.gate, L.peg) : L.slab.gate;
@@ -1000,7 +1000,7 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         d.tile_s1 = c->p_tile_s1;
         d.ntiles = c->p_ntiles;
         d.max_tiles = c->p_max_tiles;
-        ENQ(uocr_launch_gemm(s, UOCR_GEMM_SWIGLU, &d));
+        ENQ(uocr_launch_gemm_pair(s, UOCR_GEMM_F16, &dsd, UOCR_GEMM_SWIGLU, &d));
         uocr_gemm_desc dd = d;
         dd.A = c->p_rmid;
         dd.lda = EI;

@@ -219,7 +219,7 @@ struct GemmArgs {
 #endif
 
 template <int QT, int EPI, bool GROUPED, int TMR>
-__global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
+__device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz) {
     constexpr int AQ4 = TMR * (TK / 8) / PB; /* activation pieces (8 halves) per thread per K step */
     static_assert(TMR % 32 == 0 && TMR <= PB && AQ4 * PB == TMR * (TK / 8), "tile rows");
     constexpr int NMAT = EPI == GE_SWIGLU ? 2 : 1;
@@ -239,19 +239,19 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) h16 as[2][TMR * LDA];
     __shared__ int32_t arow[TMR], orow[TMR];
     const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6, hf = lane >> 5;
-    u32 n0 = blockIdx.y * TN, rows = p.M, e = 0, s0 = 0;
+    u32 n0 = by * TN, rows = p.M, e = 0, s0 = 0;
     if (GROUPED) {
-        if ((int)blockIdx.x >= *p.ntiles) return;
-        e = (u32)p.tile_e[blockIdx.x];
-        s0 = (u32)p.tile_s0[blockIdx.x];
-        rows = (u32)p.tile_s1[blockIdx.x] - s0;
+        if ((int)bx >= *p.ntiles) return;
+        e = (u32)p.tile_e[bx];
+        s0 = (u32)p.tile_s0[bx];
+        rows = (u32)p.tile_s1[bx] - s0;
         if (t < TMR) {
             const u32 s = s0 + min(t, rows - 1u);
             arow[t] = p.a_idx[s];
             orow[t] = p.o_idx[s];
         }
     } else {
-        s0 = blockIdx.x * TMR;
+        s0 = bx * TMR;
         rows = min((u32)TMR, p.M - s0);
         if (t < TMR) {
             arow[t] = (int32_t)(s0 + min(t, rows - 1u));
@@ -290,7 +290,7 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     const h16 *Ap = p.A;
     const u32 lda = p.lda, Kd = p.K;
     const bool pk = p.packed != 0u;
-    const u32 NT = Kd / TK, kb0 = p.kst != 0u ? blockIdx.z * p.kst : 0u;
+    const u32 NT = Kd / TK, kb0 = p.kst != 0u ? bz * p.kst : 0u;
     const u32 NS = p.kst != 0u ? min(p.kst, NT - kb0) : NT;
     u32 ka[GDEPTH][AQ4][4]; /* words, not uint4: no struct copies, so they stay in registers */
     u32 kb[GDEPTH][NMAT][BPiece<QT>::NW], ks[GDEPTH][NMAT];
@@ -459,7 +459,7 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
             if (EPI == GE_F32) {
                 ((float *)p.out)[orw * p.ldo + col] = acc[0][j][i];
             } else if (EPI == GE_PART) {
-                ((float *)p.out)[((size_t)blockIdx.z * p.M + orw) * p.ldo + col] = acc[0][j][i];
+                ((float *)p.out)[((size_t)bz * p.M + orw) * p.ldo + col] = acc[0][j][i];
             } else if (EPI == GE_SWIGLU) {
                 ((h16 *)p.out)[orw * p.ldo + col] = (h16)(silu_p(acc[0][j][i]) * acc[NMAT - 1][j][i]);
             } else if (EPI == GE_VISION) {
@@ -473,6 +473,28 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
                 ((h16 *)p.out)[orw * p.ldo + col] = (h16)v;
             }
         }
+    }
+}
+
+template <int QT, int EPI, bool GROUPED, int TMR>
+__global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
+    gemm_body<QT, EPI, GROUPED, TMR>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+/* Two independent GEMMs in one launch: blocks [0, na) run A's tile grid
+ * (ax columns of tiles), the rest B's (bx columns).  For GEMMs that read the
+ * same input but not each other's output and that each leave most CUs idle
+ * or waiting (the router logits beside the shared gate/up, the shared down
+ * beside the routed gate/up): one launch overlaps them where a second
+ * stream would turn the captured graph into a slower parallel one. */
+template <int QA, int EA, bool GA, int QB, int EB, bool GB>
+__global__ __launch_bounds__(PB) void k_gemm_pair(GemmArgs a, u32 ax, u32 na, GemmArgs b, u32 bx) {
+    const u32 i = blockIdx.x;
+    if (i < na) {
+        gemm_body<QA, EA, GA, TM>(a, i % ax, i / ax, 0u);
+    } else {
+        const u32 j = i - na;
+        gemm_body<QB, EB, GB, TM>(b, j % bx, j / bx, 0u);
     }
 }
 
@@ -1151,21 +1173,25 @@ extern "C" uint32_t uocr_gemm_ksplit(uint32_t M, uint32_t N, uint32_t K) {
     return s;
 }
 
-extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d) {
+static bool gemm_desc_ok(int epi, const uocr_gemm_desc *d) {
     if (d == nullptr || d->A == nullptr || d->out == nullptr || d->N == 0u || d->K == 0u || d->K % 64u != 0u ||
         d->lda % 8u != 0u || !pmat_ok(d->W[0]) || (epi == UOCR_GEMM_SWIGLU && (!pmat_ok(d->W[1]) || d->W[1].qtype != d->W[0].qtype)) ||
         (d->nseg != 0u && (d->nseg % TN != 0u || d->N % d->nseg != 0u || d->N / d->nseg > 3u))) {
-        return hipErrorInvalidValue;
+        return false;
     }
     for (u32 s = 1; d->nseg != 0u && s < d->N / d->nseg; ++s) {
-        if (!pmat_ok(d->W[s]) || d->W[s].qtype != d->W[0].qtype) return hipErrorInvalidValue;
+        if (!pmat_ok(d->W[s]) || d->W[s].qtype != d->W[0].qtype) return false;
     }
     const bool grouped = d->tile_e != nullptr;
     if (grouped ? (d->a_idx == nullptr || d->o_idx == nullptr || d->tile_s0 == nullptr || d->tile_s1 == nullptr ||
                    d->ntiles == nullptr || d->max_tiles == 0u)
                 : d->M == 0u) {
-        return hipErrorInvalidValue;
+        return false;
     }
+    return true;
+}
+
+static GemmArgs gemm_args(const uocr_gemm_desc *d) {
     GemmArgs a;
     a.A = (const h16 *)d->A;
     a.lda = d->lda;
@@ -1193,6 +1219,14 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
     a.out2 = d->out2;
     a.kst = 0u;
     a.packed = d->packed != 0u && d->W[0].qtype != UOCR_QT_F16 ? 1u : 0u;
+    a.sc_lds = 0u;
+    return a;
+}
+
+extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d) {
+    if (!gemm_desc_ok(epi, d)) return hipErrorInvalidValue;
+    const bool grouped = d->tile_e != nullptr;
+    GemmArgs a = gemm_args(d);
     const u32 tmr = gemm_tm(grouped, d->M);
     const dim3 grid(grouped ? d->max_tiles : (d->M + tmr - 1u) / tmr, (d->N + TN - 1u) / TN);
     const u32 qt = d->W[0].qtype;
@@ -1250,6 +1284,73 @@ extern "C" hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_
         if (want_norm) {
             hipLaunchKernelGGL(k_rows_rmsnorm, dim3((d->M + 3u) / 4u), dim3(PB), 0, st, (const h16 *)d->out,
                                (const h16 *)d->norm_w, d->M, (h16 *)d->norm_out);
+        }
+    }
+    return hipGetLastError();
+}
+
+/* Scales in LDS for a paired GEMM (as gemm_dispatch decides them). */
+static size_t gemm_scales(u32 qt, u32 nmat, GemmArgs &a) {
+    const u32 nt = a.K / TK;
+    a.sc_lds = qt != UOCR_QT_F16 && nmat * nt <= SC_LDS_STEPS ? 1u : 0u;
+    return a.sc_lds ? (size_t)nmat * TN * nt * sizeof(unsigned short) : 0;
+}
+
+extern "C" hipError_t uocr_launch_gemm_pair(hipStream_t st, int epi_a, const uocr_gemm_desc *da, int epi_b,
+                                            const uocr_gemm_desc *db) {
+    if (!gemm_desc_ok(epi_a, da) || !gemm_desc_ok(epi_b, db)) return hipErrorInvalidValue;
+    static const int on = [] {
+        const char *e = getenv("UOCR_HIP_GEMM_PAIR");
+        return e == nullptr ? 1 : atoi(e);
+    }();
+    const u32 qa = da->W[0].qtype, qb = db->W[0].qtype;
+    auto simple = [](const uocr_gemm_desc *d) {
+        return !(d->ksplit > 1u && d->part != nullptr) && d->norm_w == nullptr && d->nseg == 0u;
+    };
+    const bool ok = on != 0 && simple(da) && simple(db) && da->tile_e == nullptr;
+    const bool router = ok && epi_a == UOCR_GEMM_SWIGLU && epi_b == UOCR_GEMM_F32 && db->tile_e == nullptr &&
+                        qb == UOCR_QT_F16;
+    const bool experts = ok && epi_a == UOCR_GEMM_F16 && epi_b == UOCR_GEMM_SWIGLU && db->tile_e != nullptr && qa == qb;
+    if (!router && !experts) {
+        const hipError_t e = uocr_launch_gemm(st, epi_a, da);
+        return e != hipSuccess ? e : uocr_launch_gemm(st, epi_b, db);
+    }
+    GemmArgs a = gemm_args(da), b = gemm_args(db);
+    const size_t sa = gemm_scales(qa, epi_a == UOCR_GEMM_SWIGLU ? 2u : 1u, a);
+    const size_t sb = gemm_scales(qb, epi_b == UOCR_GEMM_SWIGLU ? 2u : 1u, b);
+    const u32 ax = (da->M + TM - 1u) / TM, na = ax * ((da->N + TN - 1u) / TN);
+    const u32 bx = db->tile_e != nullptr ? db->max_tiles : (db->M + TM - 1u) / TM;
+    const dim3 grid(na + bx * ((db->N + TN - 1u) / TN));
+    const size_t shm = sa > sb ? sa : sb;
+    if (router) {
+        switch (qa) {
+            case UOCR_QT_F16:
+                hipLaunchKernelGGL((k_gemm_pair<1, GE_SWIGLU, false, 1, GE_F32, false>), grid, dim3(PB), shm, st, a, ax,
+                                   na, b, bx);
+                break;
+            case UOCR_QT_Q8:
+                hipLaunchKernelGGL((k_gemm_pair<3, GE_SWIGLU, false, 1, GE_F32, false>), grid, dim3(PB), shm, st, a, ax,
+                                   na, b, bx);
+                break;
+            default:
+                hipLaunchKernelGGL((k_gemm_pair<4, GE_SWIGLU, false, 1, GE_F32, false>), grid, dim3(PB), shm, st, a, ax,
+                                   na, b, bx);
+                break;
+        }
+    } else {
+        switch (qa) {
+            case UOCR_QT_F16:
+                hipLaunchKernelGGL((k_gemm_pair<1, GE_F16, false, 1, GE_SWIGLU, true>), grid, dim3(PB), shm, st, a, ax,
+                                   na, b, bx);
+                break;
+            case UOCR_QT_Q8:
+                hipLaunchKernelGGL((k_gemm_pair<3, GE_F16, false, 3, GE_SWIGLU, true>), grid, dim3(PB), shm, st, a, ax,
+                                   na, b, bx);
+                break;
+            default:
+                hipLaunchKernelGGL((k_gemm_pair<4, GE_F16, false, 4, GE_SWIGLU, true>), grid, dim3(PB), shm, st, a, ax,
+                                   na, b, bx);
+                break;
         }
     }
     return hipGetLastError();
