@@ -1039,17 +1039,26 @@ __global__ __launch_bounds__(BUCKET_THREADS) void k_bucket_build(const int32_t *
     __syncthreads();
     for (u32 pr = t; pr < n; pr += BUCKET_THREADS) atomicAdd(&cnt[ids[pr]], 1);
     __syncthreads();
-    if (t == 0u) {
-        int32_t a = 0, b = 0;
-        for (int i = 0; i < 64; ++i) {
-            off[i] = a;
-            toff[i] = b;
-            a += cnt[i];
-            b += (cnt[i] + GTM - 1) / GTM;
+    if (t < 64u) {
+        /* exclusive scans of the bucket sizes and tile counts: one wavefront,
+         * a lane per expert */
+        const int32_t c = cnt[t], tl = (c + GTM - 1) / GTM;
+        int32_t a = c, b = tl;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t x = __shfl_up(a, o), y = __shfl_up(b, o);
+            if ((int)t >= o) {
+                a += x;
+                b += y;
+            }
         }
-        off[64] = a;
-        toff[64] = b;
-        *ntiles = b;
+        off[t] = a - c;
+        toff[t] = b - tl;
+        if (t == 63u) {
+            off[64] = a;
+            toff[64] = b;
+            *ntiles = b;
+        }
     }
     __syncthreads();
     if (t < 64u) {
