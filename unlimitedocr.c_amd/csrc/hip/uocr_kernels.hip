@@ -739,17 +739,21 @@ __global__ __launch_bounds__(BLOCK) void k_attn_merge(const float *__restrict__ 
 /* MoE: shared experts + router, routed gate/up, down-combine                */
 /* ------------------------------------------------------------------------ */
 
-/* Router logits: block r computes logit r = R_r . rmsnorm(x) (fp16 row,
- * fp32 dot) with one wavefront, so the 64 rows (160 KB) stream through 64
- * CUs. */
-__global__ __launch_bounds__(64) void k_router_logits(const h16 *__restrict__ Rw, const h16 *__restrict__ x,
-                                                      const h16 *__restrict__ nw, float *__restrict__ logits) {
+/* Router logits: block b stages rmsnorm(x) once in LDS and its 8
+ * wavefronts compute logits 8b..8b+7 = R_r . rmsnorm(x) (fp16 rows, fp32
+ * dots): the input row and the norm weight are read by 8 blocks rather than
+ * by one block per logit. */
+#define ROUTER_ROWS 8u
+__global__ __launch_bounds__(64 * ROUTER_ROWS) void k_router_logits(const h16 *__restrict__ Rw,
+                                                                    const h16 *__restrict__ x,
+                                                                    const h16 *__restrict__ nw,
+                                                                    float *__restrict__ logits) {
     TL(8);
     constexpr u32 C = chunks_per_row<1>(UOCR_K_HIDDEN), LPR = 64u, J = (C + LPR - 1u) / LPR, rb = 16u * C;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
     __shared__ float red[16];
-    const u32 r = blockIdx.x, sub = threadIdx.x;
-    XStage<UOCR_K_HIDDEN, 64> sx;
+    const u32 r = blockIdx.x * ROUTER_ROWS + (threadIdx.x >> 6), sub = threadIdx.x & 63u;
+    XStage<UOCR_K_HIDDEN, 64 * ROUTER_ROWS> sx;
     stage_load(sx, x, nw, UOCR_K_HIDDEN);
     RowFrag<J> f;
     frag_load<1, LPR, J>(f, (const uint8_t *)Rw + (size_t)r * rb, nullptr, C, sub);
@@ -1332,8 +1336,8 @@ extern "C" hipError_t uocr_launch_attn_merge(hipStream_t st, const float *partia
 extern "C" hipError_t uocr_launch_router_logits(hipStream_t st, const uint16_t *R, const uint16_t *x,
                                                 const uint16_t *nw, float *logits) {
     if (R == nullptr || x == nullptr || logits == nullptr) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_router_logits, dim3(UOCR_K_EXPERTS), dim3(64), 0, st, (const h16 *)R, (const h16 *)x,
-                       (const h16 *)nw, logits);
+    hipLaunchKernelGGL(k_router_logits, dim3(UOCR_K_EXPERTS / ROUTER_ROWS), dim3(64 * ROUTER_ROWS), 0, st,
+                       (const h16 *)R, (const h16 *)x, (const h16 *)nw, logits);
     return hipGetLastError();
 }
 
