@@ -12,9 +12,9 @@
  *     sees the payload written with it;
  *   - readers poll with device-coherent loads (they never hit a stale L2
  *     line) until every packet they need carries the step's tag;
- *   - every packet is written in UOCR_RUN_REPL copies, one per XCD, and a
- *     block reads the copy of its own XCD, so no line is polled by more than
- *     the 32 CUs of one XCD.
+ *   - every packet is written in UOCR_RUN_REPL copies and a block reads copy
+ *     (its XCD) % UOCR_RUN_REPL, so no line is polled by more than the CUs of
+ *     8 / UOCR_RUN_REPL XCDs (4 copies measured faster than 8, 2 or 1).
  * A block issues the weight loads of its next stage before it polls for
  * that stage's inputs, so the weights stream while the hand-off completes.
  */
@@ -28,7 +28,9 @@
 
 #define UOCR_RUN_BLOCKS 256u  /* one workgroup per CU of an MI355X */
 #define UOCR_RUN_THREADS 512u
-#define UOCR_RUN_REPL 8u      /* packet copies: one per XCD */
+#ifndef UOCR_RUN_REPL
+#define UOCR_RUN_REPL 4u /* packet copies: XCD x polls copy x % 4 */
+#endif
 #define UOCR_RUN_LAYERS 12u
 #define UOCR_RUN_MAX_STEPS 64u
 
