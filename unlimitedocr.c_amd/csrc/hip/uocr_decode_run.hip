@@ -1263,6 +1263,9 @@ __device__ __forceinline__ void dd_load(const Run &R, DnFrags<QF> &F) {
 /* GU stage: gathers the O outputs (a, and the z partials in MoE layers),
  * normalises a, selects the experts (MoE), and computes the block's mids.
  * MoE layers also issue the DN stage's loads (dn) once the experts are known. */
+#ifndef UOCR_RUN_WAVE_TOPK
+#define UOCR_RUN_WAVE_TOPK (QF == 4) /* Q8: 3,180 against 3,196 tok/s with it */
+#endif
 template <int QF>
 __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, GuFrags<QF> &F, DnFrags<QF> &dn) {
     typedef GuCfg<QF> G;
@@ -1303,9 +1306,14 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         /* wavefront 0: z of expert e (lane e) over the 16 partials in a fixed
          * order, then the top-6 */
         TLD(l, 18u);
+        /* every wavefront sums z (lane e: expert e, the 16 partials in a fixed
+         * order) and takes the top-6 itself, so each issues its expert rows
+         * without a barrier; wavefront 0 also leaves the ids in LDS for the
+         * later readers (behind the barrier after the gather of a) */
         float z = 0.0f;
-        if (tid_() < 64u) {
-            const u32 e = tid_();
+        u32 mye = 0u;
+        if (UOCR_RUN_WAVE_TOPK || tid_() < 64u) {
+            const u32 e = tid_() % 64u;
             /* all partials read before the (ordered) sum: one LDS round trip */
             float zp[Z_BLOCKS];
 #pragma unroll
@@ -1317,21 +1325,26 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
             u32 sid[TOPK];
             topk6_ids(z, sid);
             TLD(l, 23u);
-            if (e < TOPK) {
+            if (tid_() < TOPK) {
 #pragma unroll
                 for (u32 k = 0; k < TOPK; ++k) {
                     if (e == k) S.selid[k] = sid[k] < NEXP ? sid[k] : 0u;
                 }
             }
+            const u32 rank = min(b / 32u, TOPK - 1u);
+#pragma unroll
+            for (u32 k = 0; k < TOPK; ++k) {
+                if (rank == k) mye = sid[k] < NEXP ? sid[k] : 0u;
+            }
         }
         /* the last wavefront's polls for a are in flight */
-        lds_barrier();
+        if (!UOCR_RUN_WAVE_TOPK) lds_barrier();
         if (R.trace != nullptr && b == 0u && (u32)t < R.trace_steps && tid_() < TOPK) {
             R.trace[((size_t)t * 11u + (l - 1u)) * TOPK + tid_()] = S.selid[tid_()];
         }
         TLD(l, 9u);
         if (b < GU_ROUTED) {
-            const u32 rank = b / 32u, e = S.selid[rank];
+            const u32 rank = b / 32u, e = UOCR_RUN_WAVE_TOPK ? mye : S.selid[rank];
             gu_rows<QF, true>(F, gp<uint8_t>(sd.eg) + e * sd.gws, H(sd.egs) + e * sd.gss, gp<uint8_t>(sd.eu) + e * sd.gws,
                               H(sd.eus) + e * sd.gss, (b % 32u) * GU_ROWS, GU_ROWS, EI);
         }
