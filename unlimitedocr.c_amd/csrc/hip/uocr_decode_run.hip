@@ -103,7 +103,10 @@ constexpr u32 TOPK = UOCR_K_TOPK, EI = 896u, SI = 1792u, DI = 6848u, VOCAB = 129
 constexpr u32 QKV_BLOCKS = 240u;  /* 1920 items / 8 */
 constexpr u32 ATT_SPLITS = 8u, ATT_BLOCKS = NHEAD * ATT_SPLITS, ATT0 = NB - ATT_BLOCKS;
 constexpr u32 O_BLOCKS = 40u, O_ROWS = 32u, O0 = ATT0 - O_BLOCKS;
-constexpr u32 Z_BLOCKS = 16u, Z_COLS = HID / Z_BLOCKS; /* O blocks j < 16 also publish z partials */
+#ifndef UOCR_RUN_Z_BLOCKS
+#define UOCR_RUN_Z_BLOCKS 16u
+#endif
+constexpr u32 Z_BLOCKS = UOCR_RUN_Z_BLOCKS, Z_COLS = HID / Z_BLOCKS; /* O blocks j < Z_BLOCKS also publish z partials */
 constexpr u32 GU_ROUTED = 192u, GU_ROWS = 28u, DGU_ROWS = 27u;
 constexpr u32 DN_BLOCKS = 160u, DN_ROWS = 8u;
 constexpr u32 LM_ROWS = VOCAB / NB;
