@@ -972,7 +972,7 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         }
         const uint32_t SI = UOCR_MOE_SHARED_INTERMEDIATE, EI = UOCR_MOE_EXPERT_INTERMEDIATE;
         /* the router logits share a launch with the shared gate/up (both read
-         * xn), the shared down with the routed gate/up (after the routing) */
+         * xn), the shared down with the routed down */
         uocr_gemm_desc dr = gdesc(c->p_xn, H_SIZE, P, UOCR_ROUTED_EXPERTS, H_SIZE, c->p_logits, UOCR_ROUTED_EXPERTS);
         dr.W[0].w = L.router;
         dr.W[0].s = nullptr;
@@ -1000,7 +1000,17 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         d.tile_s1 = c->p_tile_s1;
         d.ntiles = c->p_ntiles;
         d.max_tiles = c->p_max_tiles;
-        ENQ(uocr_launch_gemm_pair(s, UOCR_GEMM_F16, &dsd, UOCR_GEMM_SWIGLU, &d));
+        /* the shared down shares the routed down's launch (2.77 against 2.83 ms
+         * beside the routed gate/up; UOCR_HIP_SHARED_DOWN_WITH=gu for that) */
+        static const int sd_down = [] {
+            const char *e = getenv("UOCR_HIP_SHARED_DOWN_WITH");
+            return e != nullptr && strcmp(e, "gu") == 0 ? 0 : 1;
+        }();
+        if (sd_down) {
+            ENQ(uocr_launch_gemm(s, UOCR_GEMM_SWIGLU, &d));
+        } else {
+            ENQ(uocr_launch_gemm_pair(s, UOCR_GEMM_F16, &dsd, UOCR_GEMM_SWIGLU, &d));
+        }
         uocr_gemm_desc dd = d;
         dd.A = c->p_rmid;
         dd.lda = EI;
@@ -1014,7 +1024,11 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         dd.a_idx = c->p_list_pair;
         dd.out = c->p_y;
         dd.ldo = H_SIZE;
-        ENQ(uocr_launch_gemm(s, UOCR_GEMM_F32, &dd));
+        if (sd_down) {
+            ENQ(uocr_launch_gemm_pair(s, UOCR_GEMM_F16, &dsd, UOCR_GEMM_F32, &dd));
+        } else {
+            ENQ(uocr_launch_gemm(s, UOCR_GEMM_F32, &dd));
+        }
         if (next_norm != nullptr) {
             ENQ(uocr_launch_moe_combine_norm(s, c->p_y, c->p_wts, c->p_sout, c->p_a, P, H, next_norm, c->p_xn));
         } else {

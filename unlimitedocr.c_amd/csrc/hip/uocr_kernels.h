@@ -233,7 +233,8 @@ typedef struct uocr_gemm_desc {
 hipError_t uocr_launch_gemm(hipStream_t st, int epi, const uocr_gemm_desc *d);
 /* Two independent GEMMs in one launch (blocks split between their tile
  * grids): A plain SwiGLU with B the fp16 router (F32), or A plain F16 with B
- * grouped SwiGLU of the same qtype; neither split-K, fused norm nor nseg.
+ * grouped SwiGLU or grouped F32 of the same qtype; neither split-K, fused
+ * norm nor nseg.
  * Other pairs, or UOCR_HIP_GEMM_PAIR=0, run as two launches. */
 hipError_t uocr_launch_gemm_pair(hipStream_t st, int epi_a, const uocr_gemm_desc *da, int epi_b,
                                  const uocr_gemm_desc *db);

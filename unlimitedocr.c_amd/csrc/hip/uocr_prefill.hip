@@ -483,9 +483,9 @@ __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
 
 /* Two independent GEMMs in one launch: blocks [0, na) run A's tile grid
  * (ax columns of tiles), the rest B's (bx columns).  For GEMMs that read the
- * same input but not each other's output and that each leave most CUs idle
- * or waiting (the router logits beside the shared gate/up, the shared down
- * beside the routed gate/up): one launch overlaps them where a second
+ * same input or at least not each other's output, and that each leave most
+ * CUs idle or waiting (the router logits beside the shared gate/up, the
+ * shared down beside the routed down): one launch overlaps them where a second
  * stream would turn the captured graph into a slower parallel one. */
 template <int QA, int EA, bool GA, int QB, int EB, bool GB>
 __global__ __launch_bounds__(PB) void k_gemm_pair(GemmArgs a, u32 ax, u32 na, GemmArgs b, u32 bx) {
@@ -1320,7 +1320,8 @@ extern "C" hipError_t uocr_launch_gemm_pair(hipStream_t st, int epi_a, const uoc
     const bool router = ok && epi_a == UOCR_GEMM_SWIGLU && epi_b == UOCR_GEMM_F32 && db->tile_e == nullptr &&
                         qb == UOCR_QT_F16;
     const bool experts = ok && epi_a == UOCR_GEMM_F16 && epi_b == UOCR_GEMM_SWIGLU && db->tile_e != nullptr && qa == qb;
-    if (!router && !experts) {
+    const bool downs = ok && epi_a == UOCR_GEMM_F16 && epi_b == UOCR_GEMM_F32 && db->tile_e != nullptr && qa == qb;
+    if (!router && !experts && !downs) {
         const hipError_t e = uocr_launch_gemm(st, epi_a, da);
         return e != hipSuccess ? e : uocr_launch_gemm(st, epi_b, db);
     }
@@ -1344,6 +1345,21 @@ extern "C" hipError_t uocr_launch_gemm_pair(hipStream_t st, int epi_a, const uoc
             default:
                 hipLaunchKernelGGL((k_gemm_pair<4, GE_SWIGLU, false, 1, GE_F32, false>), grid, dim3(PB), shm, st, a, ax,
                                    na, b, bx);
+                break;
+        }
+    } else if (downs) {
+        switch (qa) {
+            case UOCR_QT_F16:
+                hipLaunchKernelGGL((k_gemm_pair<1, GE_F16, false, 1, GE_F32, true>), grid, dim3(PB), shm, st, a, ax, na,
+                                   b, bx);
+                break;
+            case UOCR_QT_Q8:
+                hipLaunchKernelGGL((k_gemm_pair<3, GE_F16, false, 3, GE_F32, true>), grid, dim3(PB), shm, st, a, ax, na,
+                                   b, bx);
+                break;
+            default:
+                hipLaunchKernelGGL((k_gemm_pair<4, GE_F16, false, 4, GE_F32, true>), grid, dim3(PB), shm, st, a, ax, na,
+                                   b, bx);
                 break;
         }
     } else {
