@@ -66,12 +66,28 @@ UOCR_API int uocr_generate_embeddings(uocr_engine *engine, const int32_t *input_
  * uocr_engine_trace_enable(engine, steps), each generation records the
  * expert ids the router selects in layers 1-11 while computing the hidden
  * state of decode steps t < steps.  uocr_engine_trace_read copies them to
- * expert_ids ([steps][11][6], 0xffffffff for steps not reached; may be NULL)
+ * expert_ids ([steps][11][6], 0xffffffff for steps the last generation did
+ * not reach; may be NULL)
  * and the final hidden state of the last generation (the fp16 [1280] input
  * of its last token's final norm; may be NULL).  steps = 0 turns tracing off.
  * Tracing switches the per-step graph path to eager launches. */
 UOCR_API int uocr_engine_trace_enable(uocr_engine *engine, uint32_t steps);
 UOCR_API int uocr_engine_trace_read(uocr_engine *engine, uint32_t *expert_ids, uint16_t *hidden);
+/* The routing weights of the traced selections ([steps][11][6] fp32, the raw
+ * softmax probabilities in the order of the ids uocr_engine_trace_read
+ * returns; NaN bits for steps the last generation did not reach). */
+UOCR_API int uocr_engine_trace_read_weights(uocr_engine *engine, float *weights);
+/* The router input of each traced selection: a = h + O ctx, the fp16
+ * [steps][11][1280] pre-norm input of the layer's router (0xffff bits for
+ * steps not reached), so a test can recompute the reference router on the
+ * engine's own input. */
+UOCR_API int uocr_engine_trace_read_router_inputs(uocr_engine *engine, uint16_t *inputs);
+/* Which decode loop served the engine's last generation (no counterpart in
+ * the reference; for tests and diagnostics): 1 the persistent cooperative
+ * run, 0 the per-step kernels, 2 the per-step kernels after the run gave up
+ * waiting on a workgroup and the request was served again, -1 none yet or
+ * not a HIP engine. */
+UOCR_API int uocr_engine_decode_path(uocr_engine *engine);
 /* Teacher forcing, also for parity tests (no counterpart in the reference):
  * after uocr_engine_trace_force(engine, ids, n) each generation embeds ids[t]
  * after decode step t < n instead of the token it selected, and still

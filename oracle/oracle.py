@@ -64,7 +64,7 @@ _SIGS = {
     "orc_generate": ([_VP, _VP, _VP, _VP, _U32, _U32, ct.c_int, _VP, _VP], ct.c_int),
     "orc_session_reset": ([_VP, _U32], ct.c_int),
     "orc_forward_token": ([_VP, _VP, _U32, _VP], ct.c_int),
-    "orc_forward_token_traced": ([_VP, _VP, _U32, _VP, _VP], ct.c_int),
+    "orc_forward_token_traced": ([_VP, _VP, _U32, _VP, _VP, _VP], ct.c_int),
     "orc_select": ([_VP, _VP, ct.POINTER(_I32), ct.POINTER(_F), ct.POINTER(_F)], ct.c_int),
     "orc_session_fill_kv": ([_VP, _U32, ct.c_uint64], ct.c_int),
     "orc_vision_linear": ([_U32, _VP, _VP, _VP, _U32, _U32, _U32, _U32, _U32, _VP, _VP, _VP, _VP], ct.c_int),

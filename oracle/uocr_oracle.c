@@ -940,7 +940,7 @@ int orc_session_fill_kv(orc_session *s, uint32_t n, uint64_t seed) {
 
 /* One decoder token, uocr_metal.m:14299-14518 op order, golden.py rounding. */
 static int forward_token(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids,
-                         float *trace_margins) {
+                         float *trace_margins, float *trace_weights) {
     const uint32_t H = UOCR_HIDDEN_SIZE, NH = UOCR_ATTENTION_HEADS, HD = UOCR_HEAD_DIM;
     if (!s || !hidden || s->prompt_length == 0u) return 0;
     const uint32_t P = s->prompt_length, R = UOCR_GENERATED_RING_WINDOW;
@@ -991,6 +991,7 @@ static int forward_token(orc_session *s, uint16_t *hidden, uint32_t position, ui
                 return 0;
             }
             if (trace_ids) memcpy(trace_ids + (size_t)(l - 1u) * UOCR_MOE_TOP_K, ids, sizeof(ids));
+            if (trace_weights) memcpy(trace_weights + (size_t)(l - 1u) * UOCR_MOE_TOP_K, w, sizeof(w));
             if (trace_margins) {
                 /* set margin in logit space: log p of the 6th choice over the
                  * best unselected expert (softmax keeps logit differences) */
@@ -1030,12 +1031,12 @@ static int forward_token(orc_session *s, uint16_t *hidden, uint32_t position, ui
 }
 
 int orc_forward_token(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids) {
-    return forward_token(s, hidden, position, trace_ids, NULL);
+    return forward_token(s, hidden, position, trace_ids, NULL, NULL);
 }
 
 int orc_forward_token_traced(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids,
-                             float *trace_margins) {
-    return forward_token(s, hidden, position, trace_ids, trace_margins);
+                             float *trace_margins, float *trace_weights) {
+    return forward_token(s, hidden, position, trace_ids, trace_margins, trace_weights);
 }
 
 int orc_select(orc_session *s, const uint16_t *hidden, int32_t *id, float *score, float *second) {

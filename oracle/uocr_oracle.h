@@ -197,9 +197,10 @@ int orc_forward_token(orc_session *s, uint16_t *hidden, uint32_t position, uint3
 /* orc_forward_token that also writes, per MoE layer, the router's set
  * margin ([11] floats): the logit gap between the 6th selected expert and
  * the best unselected one (how far the selection, as a set, is from a
- * tie). */
+ * tie); and (trace_weights, optional, [11][6]) the routing weights of the
+ * selected experts in selection order (raw softmax probabilities). */
 int orc_forward_token_traced(orc_session *s, uint16_t *hidden, uint32_t position, uint32_t *trace_ids,
-                             float *trace_margins);
+                             float *trace_margins, float *trace_weights);
 int orc_select(orc_session *s, const uint16_t *hidden, int32_t *id, float *score, float *second);
 /* The model's embedding row of token (fp16 bits), as orc_generate stages it. */
 int orc_session_embed(orc_session *s, int32_t token, uint16_t *out);

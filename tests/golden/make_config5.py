@@ -6,7 +6,8 @@ greedy steps) on the synthetic decoder of each quantisation profile
 Each fixture holds, per step t < 512: the greedy id, its logit (`top`) and
 the oracle's top-2 logit margin; and for the forward pass of step t (which
 computes the hidden state step t + 1 selects from, t < 511) the router's
-expert ids in layers 1-11 (`trace`) with each selection's set margin
+expert ids in layers 1-11 (`trace`), their routing weights (`weights`, raw
+softmax probabilities in selection order), each selection's set margin
 (`router_gap`, the logit gap between the 6th chosen expert and the best
 unchosen one); and the hidden state (fp16 bits, the input of step t's
 final norm) at the checkpoint steps `hidden_steps`: every 32nd step from 16, 511, and
@@ -52,7 +53,8 @@ def run(profile: str) -> None:
     lib = oracle.lib()
     lib.orc_session_reset.argtypes = [ct.c_void_p, ct.c_uint32]
     lib.orc_forward_token.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_uint32, ct.c_void_p]
-    lib.orc_forward_token_traced.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_uint32, ct.c_void_p, ct.c_void_p]
+    lib.orc_forward_token_traced.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_uint32, ct.c_void_p, ct.c_void_p,
+                                             ct.c_void_p]
     lib.orc_select.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p]
     lib.orc_embed_row.argtypes = [ct.c_uint32, ct.c_void_p, ct.c_void_p, ct.c_uint32, ct.c_uint32, ct.c_int32,
                                   ct.c_void_p]
@@ -77,6 +79,7 @@ def run(profile: str) -> None:
     margins = np.zeros(STEPS, np.float32)
     top = np.zeros(STEPS, np.float32)
     trace = np.zeros((STEPS - 1, 11, 6), np.uint32)
+    weights = np.zeros((STEPS - 1, 11, 6), np.float32)
     router_gap = np.full((STEPS, 11), np.inf, np.float32)
     checkpoints = set(range(16, STEPS, 32)) | {STEPS - 1}
     saved: dict[int, np.ndarray] = {}
@@ -91,11 +94,11 @@ def run(profile: str) -> None:
         assert orc.embed(tok.value, emb) == 1
         h[:] = emb
         assert lib.orc_forward_token_traced(orc.s, oracle.ptr(h), P + t, oracle.ptr(trace[t]),
-                                            oracle.ptr(router_gap[t])) == 1
+                                            oracle.ptr(router_gap[t]), oracle.ptr(weights[t])) == 1
         if t % 64 == 0:
             print(f"{profile}: step {t} ({time.time() - t0:.0f} s)", flush=True)
     np.savez_compressed(Path(__file__).with_name(f"config5_{profile}.npz"), ids=out_ids, margins=margins, top=top,
-                        trace=trace, router_gap=router_gap, hidden_steps=np.array(sorted(saved), np.int32),
+                        trace=trace, weights=weights, router_gap=router_gap, hidden_steps=np.array(sorted(saved), np.int32),
                         hidden=np.stack([saved[k] for k in sorted(saved)]))
     orc.close()
     print(f"{profile}: done in {time.time() - t0:.0f} s; steps with margin <= 1e-2: "

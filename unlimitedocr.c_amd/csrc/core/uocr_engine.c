@@ -503,6 +503,33 @@ int uocr_engine_trace_read(uocr_engine *e, uint32_t *expert_ids, uint16_t *hidde
     return UOCR_OK;
 }
 
+int uocr_engine_trace_read_weights(uocr_engine *e, float *weights) {
+    const int st = hip_ready(e);
+    if (st != UOCR_OK) return st;
+    if (weights == NULL) return set_error(e, UOCR_ERROR_INVALID_ARGUMENT, "weights is null");
+    char herr[512] = {0};
+    if (!uocr_hip_context_trace_read2(e->hip, NULL, weights, NULL, herr, sizeof(herr))) {
+        return set_error(e, UOCR_ERROR_INTERNAL, "decode trace readback failed: %s", herr);
+    }
+    return UOCR_OK;
+}
+
+int uocr_engine_trace_read_router_inputs(uocr_engine *e, uint16_t *inputs) {
+    const int st = hip_ready(e);
+    if (st != UOCR_OK) return st;
+    if (inputs == NULL) return set_error(e, UOCR_ERROR_INVALID_ARGUMENT, "inputs is null");
+    char herr[512] = {0};
+    if (!uocr_hip_context_trace_read_inputs(e->hip, inputs, herr, sizeof(herr))) {
+        return set_error(e, UOCR_ERROR_INTERNAL, "decode trace readback failed: %s", herr);
+    }
+    return UOCR_OK;
+}
+
+int uocr_engine_decode_path(uocr_engine *e) {
+    if (e == NULL || e->hip == NULL) return -1;
+    return uocr_hip_context_decode_path(e->hip);
+}
+
 int uocr_engine_trace_force(uocr_engine *e, const int32_t *ids, uint32_t n) {
     const int st = hip_ready(e);
     if (st != UOCR_OK) return st;

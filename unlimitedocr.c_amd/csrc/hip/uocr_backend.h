@@ -64,7 +64,8 @@ int uocr_hip_context_generate(uocr_hip_ctx *ctx, const uocr_hip_decoder_request 
                               char *err, size_t err_size);
 uint64_t uocr_hip_context_weight_bytes(const uocr_hip_ctx *ctx);
 /* Decode trace for parity tests: the following generations record, for
- * decode steps t < steps, the expert ids of layers 1-11 ([steps][11][6]),
+ * decode steps t < steps, the expert ids of layers 1-11 ([steps][11][6])
+ * and their routing weights,
  * and the final hidden state (the last step's LM-head input, fp16 [1280]).
  * steps = 0 turns it off.  The graph path records through its eager per-step
  * loop; the persistent run records in place. */
@@ -74,6 +75,17 @@ int uocr_hip_context_trace_enable(uocr_hip_ctx *ctx, uint32_t steps, char *err, 
  * report); n = 0 turns it off. */
 int uocr_hip_context_trace_force(uocr_hip_ctx *ctx, const int32_t *ids, uint32_t n, char *err, size_t err_size);
 int uocr_hip_context_trace_read(uocr_hip_ctx *ctx, uint32_t *expert_ids, uint16_t *hidden, char *err, size_t err_size);
+/* trace_read that also copies the routing weights of the traced selections
+ * ([steps][11][6] fp32, selection order; NaN bits for steps not reached) */
+int uocr_hip_context_trace_read2(uocr_hip_ctx *ctx, uint32_t *expert_ids, float *weights, uint16_t *hidden, char *err,
+                                 size_t err_size);
+/* The router inputs of the traced selections: a = h + O ctx (fp16
+ * [steps][11][1280], the pre-norm input of each MoE layer's router; 0xffff
+ * bits for steps not reached). */
+int uocr_hip_context_trace_read_inputs(uocr_hip_ctx *ctx, uint16_t *inputs, char *err, size_t err_size);
+/* Decode path of the last generation: 1 the persistent run, 0 the per-step
+ * kernels, 2 the per-step kernels after the run gave up waiting, -1 none. */
+int uocr_hip_context_decode_path(const uocr_hip_ctx *ctx);
 
 #ifdef __cplusplus
 }

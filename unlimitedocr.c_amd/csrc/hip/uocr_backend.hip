@@ -86,6 +86,7 @@ struct uocr_hip_ctx {
     uint64_t kv_bytes, scratch_bytes, moe_bytes, logits_bytes, prompt_bytes, prefill_bytes;
     uint16_t *kc, *vc, *h, *a, *q, *ctxv, *mid, *smid, *prompt;
     float *attn_part, *logits, *route_w;
+    float *lg_part; /* [4 x 64] quarters of the exact router logits (folded router) */
     int64_t *racc; /* un-normalised router logits, fixed point (k_attn_out -> k_moe_gate_up) */
     int fold_select; /* the token is chosen in layer 0's QKV launch (not a finalize launch) */
     int prefill_ksplit; /* small-grid prefill GEMMs split K */
@@ -119,6 +120,8 @@ struct uocr_hip_ctx {
     uocr_run_model run_model;
     uocr_run_model *d_run_model; /* device copy, in the weight arena */
     int run_ok;                  /* the model, device and environment allow the run */
+    int last_path;               /* decode path of the last generation (uocr_hip_context_decode_path) */
+    int run_aborted;             /* the last decode_run ended on a run timeout */
     uint8_t *run_arena;          /* packet arena, in the runtime arena */
     uint32_t run_tag;            /* next unused packet tag */
     /* hot-path allocation guard (uocr_metal.m:8447-8486): every device and
@@ -132,7 +135,8 @@ struct uocr_hip_ctx {
     struct op_timer *tm;         /* active only inside the timed decode loop */
     /* decode trace (uocr_hip_context_trace_enable) */
     uint32_t trace_steps;
-    uint32_t *d_trace;           /* [trace_steps][11][6] expert ids */
+    uint32_t *d_trace;           /* [trace_steps][11][6] expert ids, as many fp32 routing weights, then the
+                                  * router inputs a (fp16 [trace_steps][11][1280]) */
     int32_t trace_step;          /* step being enqueued by the eager loop (-1: none) */
     int32_t *d_force;            /* teacher-forced token ids (uocr_hip_context_trace_force) */
     uint32_t force_n;
@@ -230,6 +234,7 @@ extern "C" uocr_hip_ctx *uocr_hip_context_create(char *err, size_t err_size) {
     }
     /* inv_freq[d] = 2^(d * (-2 log2(theta) / head_dim)), golden.py:410-414 */
     ctx->trace_step = -1;
+    ctx->last_path = -1;
     const char *re = getenv("UOCR_HIP_RUN_EVENTS");
     ctx->run_events = re != nullptr && atoi(re) != 0;
     const char *pd = getenv("UOCR_HIP_DECODER_PROFILE_DETAIL");
@@ -396,7 +401,7 @@ static int upload_slab(uocr_hip_ctx *ctx, placer &p, const uocr_bound_tensor *ex
  * against about 3,500 tok/s for the per-step graphs, Q8 3,178 against
  * 3,102); UOCR_HIP_RUN=1 / 0 forces either.  The run needs Q8 attention with
  * Q4 or Q8 everywhere else (fp16 weights keep the graphs), fp16 routers (for
- * the fold), 256 CUs and cooperative launch. */
+ * the fold) and 256 CUs. */
 static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
     uocr_run_model &m = ctx->run_model;
     memset(&m, 0, sizeof(m));
@@ -427,6 +432,7 @@ static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
         } else {
             R.fold = D.rfold_all;
             R.fold_o = D.rfold_o;
+            R.router = D.router;
             if (R.fold != nullptr && R.fold_o != nullptr) {
                 HIPCHK(uocr_run_fold_o(nullptr, D.o.qtype, D.o.w, D.o.s, R.fold, (float *)R.fold_o), "router fold_o");
             }
@@ -446,7 +452,7 @@ static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
             R.gu_s_stride = D.slab.gu_s_stride;
             R.dn_w_stride = D.slab.dn_w_stride;
             R.dn_s_stride = D.slab.dn_s_stride;
-            ok = ok && R.fold != nullptr && R.fold_o != nullptr;
+            ok = ok && R.fold != nullptr && R.fold_o != nullptr && R.router != nullptr;
             for (const uocr_qmat *q : {&D.sgate, &D.sup, &D.sdown, &D.slab.gate, &D.slab.up, &D.slab.down}) {
                 ok = ok && q->qtype == ctx->L[0].gate.qtype;
             }
@@ -462,13 +468,26 @@ static int setup_run(uocr_hip_ctx *ctx, char *err, size_t err_size) {
     m.ql = ctx->lm_head.qtype;
     m.qe = ctx->embed.qtype;
     memcpy(m.invf, ctx->invf, sizeof(m.invf));
+    /* UOCR_HIP_RUN_LIMIT_US: the longest a run workgroup waits for a packet
+     * before the run gives up (default 50 ms; the request is then served
+     * again on the per-step kernels) */
+    const char *lu = getenv("UOCR_HIP_RUN_LIMIT_US");
+    m.limit_ticks = (lu != nullptr ? strtoull(lu, nullptr, 10) : 50000ull) * 100ull;
     HIPCHK(hipMemcpy(ctx->d_run_model, &m, sizeof(m), hipMemcpyHostToDevice), "run model upload");
-    int cus = 0, coop = 0;
+    int cus = 0;
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
-    (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, ctx->device);
     const char *ru = getenv("UOCR_HIP_RUN");
     const bool want = ru != nullptr ? atoi(ru) != 0 : true;
-    ctx->run_ok = ok && uocr_run_supported(&m) && cus == (int)UOCR_RUN_BLOCKS && coop != 0 && want;
+    const bool can = ok && uocr_run_supported(&m) && cus == (int)UOCR_RUN_BLOCKS;
+    /* UOCR_HIP_RUN=1 forces the run: a model or device without it fails the
+     * mapping instead of decoding on the per-step kernels */
+    if (ru != nullptr && want && !can) {
+        return bfail(err, err_size,
+                     "UOCR_HIP_RUN=1 but the persistent decode run is unavailable (%s)",
+                     !uocr_run_supported(&m) ? "qtype mix has no run kernel"
+                                             : "device CU count is not 256");
+    }
+    ctx->run_ok = can && want;
     return 1;
 }
 
@@ -569,13 +588,22 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
     for (uint32_t l = 1; l < UOCR_DECODER_LAYERS; ++l) {
         ctx->L[l].rfold_o = (const float *)(ctx->warena + p.take((uint64_t)H_SIZE * UOCR_ROUTED_EXPERTS * 4u));
     }
-    /* GEMM-packed copies: rows x K per matrix, experts at the slab stride */
+    /* GEMM-packed copies: rows x K per matrix, experts at the slab stride.
+     * Each copy's range is checked against the arena before its kernel
+     * writes it; a failed check or launch fails the mapping (pack_bad). */
+    const char *pack_bad = nullptr;
     auto pack = [&](const uocr_qmat &m, uint32_t rows, uint32_t K, uint32_t count, uint64_t stride,
                     uint64_t bytes) -> const void * {
-        if (m.qtype == UOCR_QT_F16) return nullptr;
-        uint8_t *dst = ctx->warena + p.take(count == 1u ? align256(bytes) : count * stride);
+        if (m.qtype == UOCR_QT_F16 || pack_bad != nullptr) return nullptr;
+        const uint64_t need = count == 1u ? align256(bytes) : count * stride;
+        if (p.off + need > run_model_off) {
+            pack_bad = "weight arena overflow (GEMM-packed copies)";
+            return nullptr;
+        }
+        uint8_t *dst = ctx->warena + p.take(need);
         if (uocr_launch_pack_gemm_rows(nullptr, m.qtype, m.w, dst, rows, K, count, count == 1u ? 0u : stride) !=
             hipSuccess) {
+            pack_bad = "GEMM weight packing launch failed";
             return nullptr;
         }
         return dst;
@@ -602,6 +630,7 @@ extern "C" int uocr_hip_context_map_model(uocr_hip_ctx *ctx, const uocr_decoder_
         D.peu = pack(D.slab.up, EI, H, UOCR_ROUTED_EXPERTS, D.slab.gu_w_stride, 0);
         D.ped = pack(D.slab.down, H, EI, UOCR_ROUTED_EXPERTS, D.slab.dn_w_stride, 0);
     }
+    if (pack_bad != nullptr) return bfail(err, err_size, "%s", pack_bad);
     HIPCHK(hipGetLastError(), "GEMM weight packing");
     if (p.off > run_model_off) return bfail(err, err_size, "weight arena overflow");
     ctx->d_run_model = (uocr_run_model *)(ctx->warena + run_model_off);
@@ -629,6 +658,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_h = p.take(H_SIZE * 2u), o_a = p.take(H_SIZE * 2u), o_q = p.take(H_SIZE * 2u), o_c = p.take(H_SIZE * 2u);
     const uint64_t o_state = p.take(sizeof(uocr_step_state));
     const uint64_t o_apart = p.take(UOCR_ATTN_PARTIAL_FLOATS * 4u), o_logits = p.take(64u * 4u);
+    const uint64_t o_lgpart = p.take(4u * 64u * 4u);
     const uint64_t o_rids = p.take(64u), o_rwts = p.take(64u), o_racc = p.take(UOCR_ROUTER_ACC_WORDS * 8u);
     const uint64_t scratch_end = p.off;
     const uint64_t o_mid = p.take(UOCR_DENSE_LAYER0_INTERMEDIATE * 2u), o_smid = p.take(UOCR_MOE_SHARED_INTERMEDIATE * 2u);
@@ -672,6 +702,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->state = (uocr_step_state *)(b + o_state);
     ctx->attn_part = (float *)(b + o_apart);
     ctx->logits = (float *)(b + o_logits);
+    ctx->lg_part = (float *)(b + o_lgpart);
     ctx->route_ids = (uint32_t *)(b + o_rids);
     ctx->route_w = (float *)(b + o_rwts);
     ctx->racc = (int64_t *)(b + o_racc);
@@ -827,14 +858,21 @@ static hipError_t enqueue_layers(uocr_hip_ctx *c, bool sel) {
             ROLE("hip.decode.moe_routed_experts");
             ENQK("k_moe_gate_up", uocr_launch_moe_gate_up(s, &L.slab, L.sgate, L.sup, L.rfold == nullptr ? c->logits : nullptr,
                                         L.rfold == nullptr ? nullptr : c->racc, 0, c->a, L.post_norm, c->mid, c->smid,
-                                        c->route_ids, c->route_w));
+                                        c->route_ids, c->route_w, L.router, L.rfold == nullptr ? nullptr : c->lg_part));
+            /* with the fold, the routing weights come from the exact logits'
+             * quarters of the gate/up launch, taken by the down launch */
+            ENQK("k_moe_down", uocr_launch_moe_down(s, &L.slab, c->route_ids, c->route_w, c->mid, L.sdown, c->smid, c->a, c->h,
+                                                    L.rfold == nullptr ? nullptr : c->lg_part, c->route_w));
             if (c->trace_step >= 0 && (uint32_t)c->trace_step < c->trace_steps) {
                 role = nullptr; /* not a decode launch */
                 ENQK("trace", hipMemcpyAsync(c->d_trace + ((size_t)c->trace_step * 11u + (l - 1u)) * UOCR_MOE_TOP_K, c->route_ids,
                                    UOCR_MOE_TOP_K * 4u, hipMemcpyDeviceToDevice, s));
-                ROLE("hip.decode.moe_routed_experts");
+                ENQK("trace", hipMemcpyAsync(c->d_trace + ((size_t)(c->trace_steps + c->trace_step) * 11u + (l - 1u)) * UOCR_MOE_TOP_K,
+                                   c->route_w, UOCR_MOE_TOP_K * 4u, hipMemcpyDeviceToDevice, s));
+                uint16_t *ta = (uint16_t *)(c->d_trace + 2u * (size_t)c->trace_steps * 11u * UOCR_MOE_TOP_K);
+                ENQK("trace", hipMemcpyAsync(ta + ((size_t)c->trace_step * 11u + (l - 1u)) * H_SIZE, c->a, H_SIZE * 2u,
+                                   hipMemcpyDeviceToDevice, s));
             }
-            ENQK("k_moe_down", uocr_launch_moe_down(s, &L.slab, c->route_ids, c->route_w, c->mid, L.sdown, c->smid, c->a, c->h));
         }
         if (c->tm != nullptr) c->tm->layer_last[l] = c->tm->n - 1;
     }
@@ -1100,6 +1138,15 @@ static int run_prefill_mfma(uocr_hip_ctx *c, uint32_t P, int use_graph, char *er
 
 /* ---- generation -------------------------------------------------------------- */
 
+__global__ void k_fill_u32(uint32_t *p, size_t n, uint32_t v) {
+    const size_t i = (size_t)blockIdx.x * 256u + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+extern "C" int uocr_hip_context_decode_path(const uocr_hip_ctx *c) {
+    return c != nullptr ? c->last_path : -1;
+}
+
 static int scan_chunk(uocr_hip_ctx *c, uint32_t from, uint32_t to, int ignore_eos, uint32_t *count, int *eos) {
     for (uint32_t i = from; i < to; ++i) {
         const int32_t id = c->h_tokens[i];
@@ -1180,6 +1227,7 @@ static int decode_run(uocr_hip_ctx *c, uint32_t P, uint32_t N, int ignore_eos, u
     uint32_t ctl[4] = {0u, 0u, 0u, 0u};
     HIPCHK(hipMemcpy(ctl, c->run_arena, sizeof(ctl), hipMemcpyDeviceToHost), "run status readback");
     if (ctl[UOCR_RUN_CTL_ABORT] != 0u) {
+        c->run_aborted = 1;
         return bfail(err, err_size, "decode run timed out waiting at stage %u of step %u (workgroup %u)",
                      ctl[UOCR_RUN_CTL_WHERE], ctl[UOCR_RUN_CTL_STEP], ctl[UOCR_RUN_CTL_BLOCK]);
     }
@@ -1354,7 +1402,27 @@ extern "C" int uocr_hip_context_generate(uocr_hip_ctx *c, const uocr_hip_decoder
     const int ignore_eos = (req->flags & UOCR_GEN_IGNORE_EOS) != 0u;
     const bool timed = c->profile_detail >= 3 && c->profile != nullptr && c->profile->report.enabled != 0u;
     const bool use_run = c->run_ok && use_graph && !timed && (req->flags & UOCR_GEN_NO_RUN) == 0u;
-    if (use_run) return decode_run(c, P, N, ignore_eos, t0, t1, dg, res, err, err_size);
+    if (c->trace_steps != 0u) {
+        /* steps this generation does not reach read as 0xffffffff */
+        const size_t n = 2u * (size_t)c->trace_steps * 11u * UOCR_MOE_TOP_K + (size_t)c->trace_steps * 11u * H_SIZE / 2u;
+        hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)((n + 255u) / 256u)), dim3(256), 0, s, c->d_trace, n, 0xffffffffu);
+        HIPCHK(hipGetLastError(), "trace clear");
+    }
+    if (use_run) {
+        c->last_path = 1;
+        c->run_aborted = 0;
+        if (decode_run(c, P, N, ignore_eos, t0, t1, dg, res, err, err_size)) return 1;
+        if (!c->run_aborted) return 0;
+        /* a run that gave up waiting (a workgroup not scheduled for 50 ms,
+         * e.g. CUs taken by another process) leaves the device usable: the
+         * request is served again, prefill included, on the per-step kernels */
+        uocr_hip_decoder_request again = *req;
+        again.flags |= UOCR_GEN_NO_RUN;
+        if (!uocr_hip_context_generate(c, &again, res, err, err_size)) return 0;
+        c->last_path = 2;
+        return 1;
+    }
+    c->last_path = 0;
     if (timed || c->trace_steps != 0u || c->force_n != 0u) return decode_timed(c, P, N, ignore_eos, t0, t1, dg, timed, res, err, err_size);
     HIPCHK(uocr_launch_decode_state(s, c->state, (int32_t)P, 0, c->invf), "decode state init");
     uint32_t count = 0, scanned = 0;
@@ -1437,10 +1505,8 @@ extern "C" int uocr_hip_context_trace_enable(uocr_hip_ctx *c, uint32_t steps, ch
     }
     c->trace_steps = 0u;
     if (steps == 0u) return 1;
-    const size_t bytes = (size_t)steps * 11u * UOCR_MOE_TOP_K * 4u;
+    const size_t bytes = 2u * (size_t)steps * 11u * UOCR_MOE_TOP_K * 4u + (size_t)steps * 11u * H_SIZE * 2u;
     HIPCHK(counted_malloc(c, (void **)&c->d_trace, bytes), "trace buffer allocation");
-    HIPCHK(hipMemsetAsync(c->d_trace, 0xff, bytes, c->stream), "trace buffer clear");
-    HIPCHK(hipStreamSynchronize(c->stream), "trace buffer clear sync");
     c->trace_steps = steps;
     return 1;
 }
@@ -1467,12 +1533,32 @@ extern "C" int uocr_hip_context_trace_force(uocr_hip_ctx *c, const int32_t *ids,
 
 extern "C" int uocr_hip_context_trace_read(uocr_hip_ctx *c, uint32_t *expert_ids, uint16_t *hidden, char *err,
                                            size_t err_size) {
+    return uocr_hip_context_trace_read2(c, expert_ids, nullptr, hidden, err, err_size);
+}
+
+extern "C" int uocr_hip_context_trace_read_inputs(uocr_hip_ctx *c, uint16_t *inputs, char *err, size_t err_size) {
+    if (c == nullptr || !c->runtime_ready || inputs == nullptr) return bfail(err, err_size, "invalid trace readback");
+    HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+    HIPCHK(hipStreamSynchronize(c->stream), "stream sync");
+    if (c->trace_steps != 0u) {
+        const size_t n = (size_t)c->trace_steps * 11u * UOCR_MOE_TOP_K;
+        HIPCHK(hipMemcpy(inputs, c->d_trace + 2u * n, (size_t)c->trace_steps * 11u * H_SIZE * 2u, hipMemcpyDeviceToHost),
+               "trace input readback");
+    }
+    return 1;
+}
+
+extern "C" int uocr_hip_context_trace_read2(uocr_hip_ctx *c, uint32_t *expert_ids, float *weights, uint16_t *hidden,
+                                            char *err, size_t err_size) {
     if (c == nullptr || !c->runtime_ready) return bfail(err, err_size, "HIP context has no runtime");
     HIPCHK(hipSetDevice(c->device), "hipSetDevice");
     HIPCHK(hipStreamSynchronize(c->stream), "stream sync");
+    const size_t n = (size_t)c->trace_steps * 11u * UOCR_MOE_TOP_K;
     if (expert_ids != nullptr && c->trace_steps != 0u) {
-        HIPCHK(hipMemcpy(expert_ids, c->d_trace, (size_t)c->trace_steps * 11u * UOCR_MOE_TOP_K * 4u, hipMemcpyDeviceToHost),
-               "trace readback");
+        HIPCHK(hipMemcpy(expert_ids, c->d_trace, n * 4u, hipMemcpyDeviceToHost), "trace readback");
+    }
+    if (weights != nullptr && c->trace_steps != 0u) {
+        HIPCHK(hipMemcpy(weights, c->d_trace + n, n * 4u, hipMemcpyDeviceToHost), "trace weight readback");
     }
     if (hidden != nullptr) HIPCHK(hipMemcpy(hidden, c->h, H_SIZE * 2u, hipMemcpyDeviceToHost), "hidden readback");
     return 1;

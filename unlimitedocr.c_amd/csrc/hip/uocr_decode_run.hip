@@ -32,7 +32,7 @@
  * Hand-off (see uocr_run.h): packets {tag, 3 words}, device-coherent 16-byte
  * stores into one copy per XCD, device-coherent polls on the block's own
  * copy.  A stage's weight loads are issued before it polls for its inputs.
- * Every wait is bounded: after UOCR_RUN_LIMIT_TICKS without its packet a
+ * Every wait is bounded: after the model's limit_ticks without its packet a
  * block raises the abort word, every other waiting block sees it within a
  * few polls, and all blocks leave the kernel; the host reports the failure.
  */
@@ -55,6 +55,7 @@ struct RunLayerD {
     const AS1 uint16_t *qs, *ks, *vs, *os;
     const AS1 uint16_t *in_norm, *post_norm;
     const AS1 float *fold, *fold_o;
+    const AS1 uint16_t *router;
     const AS1 uint8_t *gate, *up, *down;
     const AS1 uint16_t *gs, *us, *ds;
     const AS1 uint8_t *sg, *su, *sd;
@@ -69,6 +70,7 @@ struct RunModelD {
     const AS1 uint16_t *lms, *embs, *final_norm;
     float invf[UOCR_K_HEAD_DIM / 2];
     uint32_t qa, qf, ql, qe;
+    uint64_t limit_ticks;
 };
 static_assert(sizeof(RunModelD) == sizeof(uocr_run_model) && sizeof(RunLayerD) == sizeof(uocr_run_layer),
               "device view of the run model");
@@ -108,6 +110,12 @@ constexpr u32 O_BLOCKS = 40u, O_ROWS = 32u, O0 = ATT0 - O_BLOCKS;
 #endif
 constexpr u32 Z_BLOCKS = UOCR_RUN_Z_BLOCKS, Z_COLS = HID / Z_BLOCKS; /* O blocks j < Z_BLOCKS also publish z partials */
 constexpr u32 GU_ROUTED = 192u, GU_ROWS = 28u, DGU_ROWS = 27u;
+#ifndef UOCR_RUN_EXACT_WEIGHTS
+#define UOCR_RUN_EXACT_WEIGHTS 1
+#endif
+/* exact router logits: GU block b computes quarter b % 4 of logit b / 4 */
+constexpr u32 LG_Q = NB / NEXP, LG_COLS = HID / LG_Q;
+static_assert(LG_Q * NEXP == NB && LG_COLS % 64u == 0u && LG_COLS / 8u <= 64u, "logit quarters");
 constexpr u32 DN_BLOCKS = 160u, DN_ROWS = 8u;
 constexpr u32 LM_ROWS = VOCAB / NB;
 static_assert(LM_ROWS * NB == VOCAB, "LM rows split evenly");
@@ -148,9 +156,6 @@ constexpr u64 ARENA_PK = off_layer(UOCR_RUN_LAYERS);
 #endif
 #ifndef UOCR_RUN_SLEEP
 #define UOCR_RUN_SLEEP 1
-#endif
-#ifndef UOCR_RUN_LIMIT_TICKS
-#define UOCR_RUN_LIMIT_TICKS 5000000ull /* 50 ms of s_memrealtime (100 MHz) */
 #endif
 
 /* stage codes reported on a timeout */
@@ -237,7 +242,7 @@ struct Run {
     int32_t *tokens;
     float *scores;
     h16 *hout;      /* layer 11's output of every step (plain stores) */
-    u32 *trace;     /* expert ids [t][11][6] for t < trace_steps, or NULL */
+    u32 *trace;     /* expert ids [t][11][6] for t < trace_steps, their weights, the router inputs; or NULL */
     u32 trace_steps;
     const int32_t *force; /* teacher-forced ids for t < force_n, or NULL */
     u32 force_n;
@@ -284,7 +289,7 @@ __device__ __forceinline__ bool gather(const Run &R, const uint4 *region, u32 pe
             }
             if (pend != 0u && (it & 15u) == 0u) {
                 if (cload32(R.ctl, UOCR_RUN_CTL_ABORT * 4u) != 0u ||
-                    __builtin_amdgcn_s_memrealtime() - t0 > UOCR_RUN_LIMIT_TICKS) {
+                    __builtin_amdgcn_s_memrealtime() - t0 > R.M->limit_ticks) {
                     if (cload32(R.ctl, UOCR_RUN_CTL_ABORT * 4u) == 0u) give_up(R.ctl, where, step);
                     bad = 1;
                     break;
@@ -356,7 +361,7 @@ __device__ __forceinline__ bool gather_wave(const Run &R, const uint4 *region, u
         __builtin_amdgcn_s_sleep(1);
         if ((it & 15u) == 0u) {
             if (cload32(R.ctl, UOCR_RUN_CTL_ABORT * 4u) != 0u ||
-                __builtin_amdgcn_s_memrealtime() - t0 > UOCR_RUN_LIMIT_TICKS) {
+                __builtin_amdgcn_s_memrealtime() - t0 > R.M->limit_ticks) {
                 if (cload32(R.ctl, UOCR_RUN_CTL_ABORT * 4u) == 0u && t == 0u) give_up(R.ctl, where, step);
                 bad = 1;
                 break;
@@ -523,6 +528,7 @@ struct Lds {
     unsigned long long *keyw;
     uint8_t *scr;
     float *xsum; /* chunk sums of the LM head's activation */
+    uint8_t *lgw; /* the GU block's router row and norm weight quarter (2 x 640 bytes) */
 };
 
 /* ---- LM head -------------------------------------------------------------- */
@@ -1306,6 +1312,19 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
          * chosen and ahead of the expert loads */
         uint4 *stg = (uint4 *)(S.scr + 8192u);
         gather_wave_issue<(PO_AR + 63u) / 64u>(R, R.pk + off_o(l), PO, PO_AR, NT / 64u - 1u, stg, [](u32 i) { return i; });
+        /* the exact router logit's quarter this block owns (expert b / 4,
+         * columns [320 (b % 4), + 320)): its router row and norm weight
+         * pieces, by the polling wavefront behind its first polls */
+        if (UOCR_RUN_EXACT_WEIGHTS && __builtin_amdgcn_readfirstlane(tid_() / 64u) == NT / 64u - 1u) {
+            const u32 lane = tid_() % 64u, e = b / LG_Q, c0 = (b % LG_Q) * LG_COLS;
+            if (lane < LG_COLS / 8u) {
+                __builtin_amdgcn_global_load_lds((const AS1 void *)(L.router + (size_t)e * HID + c0 + 8u * lane),
+                                                 (__attribute__((address_space(3))) void *)S.lgw, 16u, 0, 0);
+                __builtin_amdgcn_global_load_lds((const AS1 void *)(L.post_norm + c0 + 8u * lane),
+                                                 (__attribute__((address_space(3))) void *)(S.lgw + 2u * LG_COLS), 16u,
+                                                 0, 0);
+            }
+        }
         /* wavefront 0: z of expert e (lane e) over the 16 partials in a fixed
          * order, then the top-6 */
         TLD(l, 18u);
@@ -1373,20 +1392,46 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         lds_barrier();
         if (S.red[15] == 0.0f) return false;
         TLD(l, 15u);
+        if (R.trace != nullptr && b == 0u && (u32)t < R.trace_steps && tid_() < HID / 8u) {
+            uint4 *ta = (uint4 *)(R.trace + 2u * (size_t)R.trace_steps * 11u * TOPK);
+            ta[((size_t)t * 11u + (l - 1u)) * (HID / 8u) + tid_()] = ((const uint4 *)S.hres)[tid_()];
+        }
         rms_defer(S.hres, nwp, S.xs, S.red, nullptr, nullptr);
         lds_barrier();
         inv = rms_inv(S.red);
         TLD(l, 16u);
-        if (tid_() < 64u) {
+        if (!UOCR_RUN_EXACT_WEIGHTS && tid_() < 64u) {
             /* the selection's probabilities: softmax of z * inv_rms (raw, no
              * renormalisation; max-subtracted) */
             const float lg = z * inv;
             const float mx = wave_max_dpp(lg);
             const float pe = fexp(lg - mx);
             const float p = pe * frcp(wave_sum(pe));
-            const u32 t = tid_();
-            const float ps = __shfl(p, (int)S.selid[min(t, TOPK - 1u)]); /* lane t < 6: p of expert selid[t] */
-            if (t < TOPK) S.selw[t] = ps;
+            const u32 k = tid_();
+            const float ps = __shfl(p, (int)S.selid[min(k, TOPK - 1u)]); /* lane k < 6: p of expert selid[k] */
+            if (k < TOPK) S.selw[k] = ps;
+        }
+        if (UOCR_RUN_EXACT_WEIGHTS && __builtin_amdgcn_readfirstlane(tid_() / 64u) == NT / 64u - 1u) {
+            /* the reference's router input, rounded as it rounds it:
+             * n[c] = f16(a[c] inv w[c]), inv = 1 / sqrt(mean a^2 + eps); this
+             * block's quarter of logit b / 4 = sum_c R[b / 4][c] n[c] goes to
+             * the DN stage with the mids (the experts were chosen from z, the
+             * weights come from these logits) */
+            float ss = 0.0f;
+#pragma unroll
+            for (u32 w = 0; w < NT / 64u; ++w) ss += S.red[w];
+            const float inve = 1.0f / __builtin_sqrtf(ss / (float)HID + 1.0e-6f);
+            const u32 lane = tid_() % 64u, c0 = (b % LG_Q) * LG_COLS;
+            const h16 *rw = (const h16 *)S.lgw, *nw = rw + LG_COLS;
+            float part = 0.0f;
+#pragma unroll
+            for (u32 k = 0; k < LG_COLS / 64u; ++k) {
+                const u32 c = lane * (LG_COLS / 64u) + k;
+                const h16 n = (h16)(((float)S.hres[c0 + c] * inve) * (float)nw[c]);
+                part = fmaf((float)n, (float)rw[c], part);
+            }
+            part = wave_sum(part);
+            if (lane == 0u) S.zout[0] = part;
         }
     } else {
         if (!gather_a()) return false;
@@ -1415,8 +1460,11 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     }
     __syncthreads();
     TLD(l, 11u);
-    publish(R, R.pk + off_mid(l), PMID, b * PMID_B, PMID_B, tag,
-            [&](u32 p) { return pay6(S.outv, p, moe ? GU_ROWS : nrows); });
+    publish(R, R.pk + off_mid(l), PMID, b * PMID_B, PMID_B, tag, [&](u32 p) {
+        uint3 v = pay6(S.outv, p, moe ? GU_ROWS : nrows);
+        if (moe && p == PMID_B - 1u) v.z = __float_as_uint(S.zout[0]); /* mids 28, 29 do not exist */
+        return v;
+    });
     TLD(l, 19u);
     /* the DN stage's rows of the selected experts (layer 0: the dense down
      * row), issued once this stage's own loads are consumed, so the two
@@ -1443,10 +1491,13 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     const u32 rows_b = moe ? GU_ROWS : DGU_ROWS;
     const u32 nmid = moe ? TOPK * EI + SI : DI;
     h16 *mids = (h16 *)S.scr;
+    float *lgp = (float *)(S.scr + (TOPK * EI + SI) * 2u); /* [256] the logit quarters */
+    static_assert((TOPK * EI + SI) * 2u + NB * 4u <= 24576u, "DN LDS");
     if (!gather<(PMID + NT - 1u) / NT>(R, R.pk + off_mid(l), PMID, PMID, tag, W_DN, (u32)t, [](u32 i) { return i; },
                         [&](u32 i, uint4 v) {
                             const u32 blk = i / PMID_B, k = i % PMID_B, base = blk * rows_b + 6u * k;
                             if (6u * k < rows_b) put6(mids + base, v, 6u * k, rows_b);
+                            if (moe && k == PMID_B - 1u) lgp[blk] = __uint_as_float(v.w);
                             (void)nmid;
                         })) {
         return false;
@@ -1461,6 +1512,34 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     const u32 c = dn_row(), lane = tid_() & 63u, rl = c - b * DN_ROWS;
     float out;
     if (moe) {
+        /* routing weights: every wavefront sums the logits (lane e: the four
+         * quarters of logit e in order) and takes the raw softmax
+         * probabilities of the selected experts (max-subtracted;
+         * moe.metal:53-193) */
+        float w6[TOPK];
+        if (!UOCR_RUN_EXACT_WEIGHTS) {
+#pragma unroll
+            for (u32 r = 0; r < TOPK; ++r) w6[r] = S.selw[r];
+        } else {
+            float q4[LG_Q];
+#pragma unroll
+            for (u32 q = 0; q < LG_Q; ++q) q4[q] = lgp[lane * LG_Q + q];
+            __builtin_amdgcn_sched_barrier(0);
+            float lg = q4[0];
+#pragma unroll
+            for (u32 q = 1; q < LG_Q; ++q) lg += q4[q];
+            const float mx = wave_max_dpp(lg);
+            const float pe = __expf(lg - mx);
+            const float p = pe / wave_sum(pe);
+#pragma unroll
+            for (u32 r = 0; r < TOPK; ++r) w6[r] = __shfl(p, (int)S.selid[r]);
+        }
+        if (R.trace != nullptr && b == 0u && lane < TOPK && tid_() < 64u && (u32)t < R.trace_steps) {
+            float mine = w6[0];
+#pragma unroll
+            for (u32 r = 1; r < TOPK; ++r) mine = lane == r ? w6[r] : mine;
+            R.trace[((size_t)(R.trace_steps + (u32)t) * 11u + (l - 1u)) * TOPK + lane] = __float_as_uint(mine);
+        }
         /* routed: sum over chunks of w_r * (scaled chunk dot); the shared
          * expert's sum kept apart (rounded to fp16 before the combine) */
         float acc = 0.0f, sh = 0.0f;
@@ -1475,7 +1554,10 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                 const float v = QF == 1 ? d : d * (float)dn.f.s[j];
                 if (q < G::CT) {
                     if (routed) {
-                        acc = fmaf(S.selw[r], v, acc);
+                        float wr = w6[0];
+#pragma unroll
+                        for (u32 k = 1; k < TOPK; ++k) wr = r == k ? w6[k] : wr;
+                        acc = fmaf(wr, v, acc);
                     } else {
                         sh += v;
                     }
@@ -1529,7 +1611,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
     __shared__ u32 selid[8];
     __shared__ unsigned long long keyw[NT / 64u];
     __shared__ float xsum[HID / 16u];
-    Lds S{xs, hres, outv, red, zout, selw, zw, selid, keyw, scr, xsum};
+    /* the exact-logit slices; sized so the block's LDS exceeds half a CU's
+     * 160 KB and no CU can hold two run workgroups whatever the register
+     * allocation (the run needs one workgroup on each of the 256 CUs) */
+    __shared__ __attribute__((aligned(16))) uint8_t lgw[10240];
+    Lds S{xs, hres, outv, red, zout, selw, zw, selid, keyw, scr, xsum, lgw};
     Run R;
     R.M = (const AS4 RunModelD *)A.M;
     R.pk = A.pk;
@@ -1632,10 +1718,19 @@ __global__ void k_run_reset(u32 *ctl) {
     if (tid_() < 64u) ctl[tid_()] = 0u;
 }
 
+/* An ordinary launch: the run needs its 256 workgroups resident together
+ * (one per CU: 512 threads at 256 VGPRs fill a CU's register file, and the
+ * block's LDS is above half a CU's), which an otherwise idle device gives;
+ * it uses none of the cooperative launch's grid synchronisation.  A
+ * workgroup that never gets a CU shows as a bounded wait that gives up, and
+ * the request is served again on the per-step kernels.  (The cooperative
+ * launch was replaced because every profiled process that made one ended in
+ * a segmentation fault in an exit handler after the profiler's
+ * finalisation, while profiled processes without one exited cleanly.) */
 template <int QA, int QF, int QL, int QE>
 hipError_t launch_run(hipStream_t st, const RunArgs &a) {
-    void *args[] = {(void *)&a};
-    return hipLaunchCooperativeKernel((const void *)k_decode_run<QA, QF, QL, QE>, dim3(NB), dim3(NT), args, 0, st);
+    hipLaunchKernelGGL((k_decode_run<QA, QF, QL, QE>), dim3(NB), dim3(NT), 0, st, a);
+    return hipGetLastError();
 }
 
 }  // namespace

@@ -120,17 +120,25 @@ hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, const uint16_t 
  * wavefront) and of the shared experts in one launch:
  *   mid[r*896 + c] = f16(silu(G_e[c].xin) * (U_e[c].xin)), e = rank-r expert,
  *   smid[c]        = f16(silu(SG[c].xin) * (SU[c].xin)),  c < 1792,
- * xin = x or rmsnorm(x, nw); ids/weights receive the selection.  Exactly
- * one of logits (the router logits) and router_acc (the fixed-point
- * un-normalised logits of attn_out; logits = z * inv_rms(x)) is set. */
+ * xin = x or rmsnorm(x, nw); ids receive the selection.  Exactly one of
+ * logits (the router logits; weights receive the selection's
+ * probabilities) and router_acc (the fixed-point un-normalised logits of
+ * attn_out, z = logits / inv_rms(x), which order the experts) is set.  With
+ * router_acc, router (the fp16 [64][1280] router) and lg_part (256 floats)
+ * give the exact logits: lg_part[4e + q] = the sum over columns [320 q,
+ * + 320) of router[e] times the normalised row, for uocr_launch_moe_down. */
 hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG, uocr_qmat SU,
                                    const float *logits, const int64_t *router_acc, int norm_topk, const uint16_t *x,
-                                   const uint16_t *nw, uint16_t *mid, uint16_t *smid, uint32_t *ids, float *weights);
+                                   const uint16_t *nw, uint16_t *mid, uint16_t *smid, uint32_t *ids, float *weights,
+                                   const uint16_t *router, float *lg_part);
 /* Routed down + weighted combine + shared down + residual:
- * out[c] = f16(sum_r w_r * D_e[c].mid_r + f16(SD[c].smid) + res[c]). */
+ * out[c] = f16(sum_r w_r * D_e[c].mid_r + f16(SD[c].smid) + res[c]).  The
+ * weights w_r come from weights, or (lg_part non-NULL) are the softmax
+ * probabilities of the exact logits sum_q lg_part[4e + q] of the selected
+ * experts, also written to w_out when it is non-NULL. */
 hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
                                 const float *weights, const uint16_t *mid, uocr_qmat SD, const uint16_t *smid,
-                                const uint16_t *res, uint16_t *out);
+                                const uint16_t *res, uint16_t *out, const float *lg_part, float *w_out);
 /* Final norm + LM-head GEMV + argmax keys (k_lm_keys): every block adds its
  * best (score, row) as a 64-bit key by atomic max into keys[block % 16]
  * (UOCR_LM_KEYS words, zero on entry); with advance, block 0 advances the

@@ -797,7 +797,8 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl
                                                              const h16 *__restrict__ x, const h16 *__restrict__ nw,
                                                              h16 *__restrict__ mid, h16 *__restrict__ smid,
                                                              u32 *__restrict__ ids_out, float *__restrict__ w_out,
-                                                             u32 nb_routed) {
+                                                             u32 nb_routed, const h16 *__restrict__ router,
+                                                             float *__restrict__ lg_part) {
     TL(4);
     constexpr u32 K = UOCR_K_HIDDEN, G = K / 64u, I = 896u, ROWS = UOCR_K_TOPK * I, SI = 1792u;
     constexpr u32 NWV = SMALL_BLOCK / 64u;
@@ -862,18 +863,32 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_moe_gate_up(uocr_expert_slab sl
                           (const h16 *)sl.gate.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
     frag_load<QT, LPR, J, UOCR_NT_STREAM>(fu, (const uint8_t *)sl.up.w + e * sl.gu_w_stride + (size_t)col * rb,
                           (const h16 *)sl.up.s + e * sl.gu_s_stride + (size_t)col * G, C, sub);
-    const float inv = stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
-    if (FOLD && blockIdx.x == 0u && wave == 0u) {
-        /* logits = z * inv_rms(x): the selection's probabilities */
-        topk6_weights(lg * inv, norm_topk, sid, sw);
-        if (lane < UOCR_K_TOPK) {
+    /* FOLD: the experts come from z; the routing weights from the exact
+     * logits, summed over the normalised row as the reference rounds it (xs):
+     * block b < 256 writes quarter b % 4 of logit b / 4 (columns [320 q,
+     * + 320) in order), and k_moe_down takes the softmax */
+    constexpr u32 LQ = 4u, LC = K / LQ, LPL = LC / 64u;
+    const bool lgb = FOLD && lg_part != nullptr && blockIdx.x < UOCR_K_EXPERTS * LQ && wave == 0u;
+    h16 rv[LPL];
+    if (lgb) {
+        const h16 *rr = router + (size_t)(blockIdx.x / LQ) * K + (blockIdx.x % LQ) * LC + lane * LPL;
 #pragma unroll
-            for (int k = 0; k < UOCR_K_TOPK; ++k) {
-                if (lane == (u32)k) {
-                    ids_out[k] = sid[k];
-                    w_out[k] = sw[k];
-                }
-            }
+        for (u32 k = 0; k < LPL; ++k) rv[k] = rr[k];
+    }
+    const float inv = stage_store(sx, xs, nw, UOCR_K_HIDDEN, red);
+    (void)inv;
+    if (lgb) {
+        const h16 *xr = xs + (blockIdx.x % LQ) * LC + lane * LPL;
+        float part = 0.0f;
+#pragma unroll
+        for (u32 k = 0; k < LPL; ++k) part = fmaf((float)xr[k], (float)rv[k], part);
+        part = wave_sum(part);
+        if (lane == 0u) lg_part[blockIdx.x] = part;
+    }
+    if (FOLD && blockIdx.x == 0u && wave == 0u && lane < UOCR_K_TOPK) {
+#pragma unroll
+        for (int k = 0; k < UOCR_K_TOPK; ++k) {
+            if (lane == (u32)k) ids_out[k] = sid[k];
         }
     }
     const float dg = group_sum<LPR>(frag_dot<QT, LPR, J>(fg, xs, C, sub));
@@ -895,7 +910,8 @@ template <int QT, int QS>
 __global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const u32 *__restrict__ ids,
                                                     const float *__restrict__ wts, const h16 *__restrict__ mid,
                                                     uocr_qmat SD, const h16 *__restrict__ smid,
-                                                    const h16 *__restrict__ res, h16 *__restrict__ out) {
+                                                    const h16 *__restrict__ res, h16 *__restrict__ out,
+                                                    const float *__restrict__ lg_part, float *__restrict__ w_out) {
     TL(5);
     constexpr u32 I = 896u, SI = 1792u, LPR = lpr_down(QT), R = 64u / LPR;
     constexpr u32 CD = chunks_per_row<QT>(I), JD = (CD + LPR - 1u) / LPR, GD = I / 64u;
@@ -923,6 +939,21 @@ __global__ __launch_bounds__(BLOCK) void k_moe_down(uocr_expert_slab sl, const u
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
         e[r] = ids[r]; /* all 12 loads unconditional: one scalar round trip */
         w[r] = wts[r];
+    }
+    if (lg_part != nullptr) {
+        /* routing weights from the gate/up kernel's logit quarters (lane e:
+         * the four quarters of logit e in order): raw softmax probabilities,
+         * max-subtracted (moe.metal:53-193); every wavefront takes them */
+        const float4 q = ((const float4 *)lg_part)[lane];
+        const float p = router_prob(((q.x + q.y) + q.z) + q.w);
+#pragma unroll
+        for (int r = 0; r < UOCR_K_TOPK; ++r) w[r] = __shfl(p, (int)(e[r] < UOCR_K_EXPERTS ? e[r] : 0u));
+        if (w_out != nullptr && blockIdx.x == 0u && wave == 0u && lane < UOCR_K_TOPK) {
+            float mine = w[0];
+#pragma unroll
+            for (int r = 1; r < UOCR_K_TOPK; ++r) mine = lane == (u32)r ? w[r] : mine;
+            w_out[lane] = mine;
+        }
     }
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
@@ -1353,7 +1384,8 @@ extern "C" hipError_t uocr_launch_router(hipStream_t st, const uint16_t *R, cons
 template <int QT, int QS>
 static void launch_moe_gu_qs(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG, uocr_qmat SU,
                              const float *logits, const int64_t *racc, int norm_topk, const uint16_t *x,
-                             const uint16_t *nw, uint16_t *mid, uint16_t *smid, u32 *ids, float *wts) {
+                             const uint16_t *nw, uint16_t *mid, uint16_t *smid, u32 *ids, float *wts,
+                             const uint16_t *router, float *lg_part) {
     constexpr u32 NWV = SMALL_BLOCK / 64u;
     constexpr u32 rpb = NWV * (64u / lpr_lat(chunks_per_row<QT>(UOCR_K_HIDDEN)));
     constexpr u32 rpb_s = NWV * (64u / lpr_lat(chunks_per_row<QS>(UOCR_K_HIDDEN)));
@@ -1361,19 +1393,20 @@ static void launch_moe_gu_qs(hipStream_t st, const uocr_expert_slab *slab, uocr_
     if (racc != nullptr) {
         hipLaunchKernelGGL((k_moe_gate_up<QT, QS, true>), dim3(nbr + nbs), dim3(SMALL_BLOCK), 0, st, *slab, SG, SU,
                            nullptr, (const long long *)racc, norm_topk, (const h16 *)x, (const h16 *)nw, (h16 *)mid,
-                           (h16 *)smid, ids, wts, nbr);
+                           (h16 *)smid, ids, wts, nbr, (const h16 *)router, lg_part);
     } else {
         hipLaunchKernelGGL((k_moe_gate_up<QT, QS, false>), dim3(nbr + nbs), dim3(SMALL_BLOCK), 0, st, *slab, SG, SU,
                            logits, nullptr, norm_topk, (const h16 *)x, (const h16 *)nw, (h16 *)mid, (h16 *)smid, ids,
-                           wts, nbr);
+                           wts, nbr, nullptr, nullptr);
     }
 }
 
 template <int QT>
 static void launch_moe_gu_qt(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG, uocr_qmat SU,
                              const float *logits, const int64_t *racc, int norm_topk, const uint16_t *x,
-                             const uint16_t *nw, uint16_t *mid, uint16_t *smid, u32 *ids, float *wts) {
-#define GU(QS) launch_moe_gu_qs<QT, QS>(st, slab, SG, SU, logits, racc, norm_topk, x, nw, mid, smid, ids, wts)
+                             const uint16_t *nw, uint16_t *mid, uint16_t *smid, u32 *ids, float *wts,
+                             const uint16_t *router, float *lg_part) {
+#define GU(QS) launch_moe_gu_qs<QT, QS>(st, slab, SG, SU, logits, racc, norm_topk, x, nw, mid, smid, ids, wts, router, lg_part)
     switch (SG.qtype) {
         case UOCR_QT_F16: GU(1); break;
         case UOCR_QT_Q8: GU(3); break;
@@ -1385,45 +1418,49 @@ static void launch_moe_gu_qt(hipStream_t st, const uocr_expert_slab *slab, uocr_
 extern "C" hipError_t uocr_launch_moe_gate_up(hipStream_t st, const uocr_expert_slab *slab, uocr_qmat SG,
                                               uocr_qmat SU, const float *logits, const int64_t *router_acc,
                                               int norm_topk, const uint16_t *x, const uint16_t *nw, uint16_t *mid,
-                                              uint16_t *smid, uint32_t *ids, float *weights) {
+                                              uint16_t *smid, uint32_t *ids, float *weights, const uint16_t *router,
+                                              float *lg_part) {
     if (slab == nullptr || !mat_ok(slab->gate) || !mat_ok(slab->up) || slab->gate.qtype != slab->up.qtype ||
         !mat_ok(SG) || !mat_ok(SU) || SG.qtype != SU.qtype || (logits == nullptr) == (router_acc == nullptr) ||
-        x == nullptr || mid == nullptr || smid == nullptr || ids == nullptr || weights == nullptr) {
+        x == nullptr || mid == nullptr || smid == nullptr || ids == nullptr || weights == nullptr ||
+        (lg_part != nullptr && (router == nullptr || router_acc == nullptr || nw == nullptr))) {
         return hipErrorInvalidValue;
     }
     DISPATCH_QT(slab->gate.qtype, launch_moe_gu_qt, st, slab, SG, SU, logits, router_acc, norm_topk, x, nw, mid, smid,
-                ids, weights);
+                ids, weights, router, lg_part);
     return hipGetLastError();
 }
 
 template <int QT, int QS>
 static void launch_moe_down_qs(hipStream_t st, const uocr_expert_slab *slab, const u32 *ids, const float *wts,
                                const uint16_t *mid, uocr_qmat SD, const uint16_t *smid, const uint16_t *res,
-                               uint16_t *out) {
+                               uint16_t *out, const float *lg_part, float *w_out) {
     constexpr u32 rpb = NWAVE * (64u / lpr_down(QT));
     hipLaunchKernelGGL((k_moe_down<QT, QS>), dim3((UOCR_K_HIDDEN + rpb - 1u) / rpb), dim3(BLOCK), 0, st, *slab, ids,
-                       wts, (const h16 *)mid, SD, (const h16 *)smid, (const h16 *)res, (h16 *)out);
+                       wts, (const h16 *)mid, SD, (const h16 *)smid, (const h16 *)res, (h16 *)out, lg_part, w_out);
 }
 
 template <int QT>
 static void launch_moe_down_qt(hipStream_t st, const uocr_expert_slab *slab, const u32 *ids, const float *wts,
                                const uint16_t *mid, uocr_qmat SD, const uint16_t *smid, const uint16_t *res,
-                               uint16_t *out) {
+                               uint16_t *out, const float *lg_part, float *w_out) {
     switch (SD.qtype) {
-        case UOCR_QT_F16: launch_moe_down_qs<QT, 1>(st, slab, ids, wts, mid, SD, smid, res, out); break;
-        case UOCR_QT_Q8: launch_moe_down_qs<QT, 3>(st, slab, ids, wts, mid, SD, smid, res, out); break;
-        default: launch_moe_down_qs<QT, 4>(st, slab, ids, wts, mid, SD, smid, res, out); break;
+        case UOCR_QT_F16: launch_moe_down_qs<QT, 1>(st, slab, ids, wts, mid, SD, smid, res, out, lg_part, w_out); break;
+        case UOCR_QT_Q8: launch_moe_down_qs<QT, 3>(st, slab, ids, wts, mid, SD, smid, res, out, lg_part, w_out); break;
+        default: launch_moe_down_qs<QT, 4>(st, slab, ids, wts, mid, SD, smid, res, out, lg_part, w_out); break;
     }
 }
 
 extern "C" hipError_t uocr_launch_moe_down(hipStream_t st, const uocr_expert_slab *slab, const uint32_t *ids,
                                            const float *weights, const uint16_t *mid, uocr_qmat SD,
-                                           const uint16_t *smid, const uint16_t *res, uint16_t *out) {
-    if (slab == nullptr || !mat_ok(slab->down) || !mat_ok(SD) || ids == nullptr || weights == nullptr ||
-        mid == nullptr || smid == nullptr || res == nullptr || out == nullptr) {
+                                           const uint16_t *smid, const uint16_t *res, uint16_t *out,
+                                           const float *lg_part, float *w_out) {
+    if (slab == nullptr || !mat_ok(slab->down) || !mat_ok(SD) || ids == nullptr ||
+        (weights == nullptr && lg_part == nullptr) || mid == nullptr || smid == nullptr || res == nullptr ||
+        out == nullptr) {
         return hipErrorInvalidValue;
     }
-    DISPATCH_QT(slab->down.qtype, launch_moe_down_qt, st, slab, ids, weights, mid, SD, smid, res, out);
+    DISPATCH_QT(slab->down.qtype, launch_moe_down_qt, st, slab, ids, weights, mid, SD, smid, res, out, lg_part, w_out);
     return hipGetLastError();
 }
 

@@ -182,12 +182,12 @@ extern "C" int uocr_op_moe_ffn(const uocr_op_moe_weights *m, const void *x, cons
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_moe_gate_up(st, &sl, qm(m->shared_qtype, m->sgate_w, m->sgate_s),
                                                qm(m->shared_qtype, m->sup_w, m->sup_s), logits, nullptr, norm_topk, xx, nw, mid,
-                                               smid, wids, wwts),
+                                               smid, wids, wwts, nullptr, nullptr),
                        "moe gate/up");
     }
     if (r == UOCR_OK) {
         r = hip_status(uocr_launch_moe_down(st, &sl, wids, wwts, mid, qm(m->shared_qtype, m->sdown_w, m->sdown_s),
-                                            smid, (const uint16_t *)residual, (uint16_t *)out),
+                                            smid, (const uint16_t *)residual, (uint16_t *)out, nullptr, nullptr),
                        "moe down/combine");
     }
     return r;
@@ -211,7 +211,7 @@ extern "C" int uocr_op_moe_gate_up(const uocr_op_moe_weights *m, const float *lo
     return hip_status(uocr_launch_moe_gate_up(st, &sl, qm(m->shared_qtype, m->sgate_w, m->sgate_s),
                                               qm(m->shared_qtype, m->sup_w, m->sup_s), logits, nullptr, norm_topk,
                                               (const uint16_t *)x, (const uint16_t *)norm_w, (uint16_t *)mid,
-                                              (uint16_t *)smid, ids, weights),
+                                              (uint16_t *)smid, ids, weights, nullptr, nullptr),
                       "moe gate/up");
 }
 
@@ -323,6 +323,15 @@ extern "C" int uocr_op_gemm(uint32_t qtype, const void *w, const void *s, uint32
  * 14-20 us unsplit). */
 static float *g_vision_part = nullptr;
 static size_t g_vision_part_bytes = 0;
+/* Guards the lazily allocated operator buffers (g_vision_part, the prefill
+ * attention partials): held from the size check through the launch, so two
+ * threads never allocate twice or launch into a buffer being replaced; the
+ * launches then serialise on the operator stream. */
+static pthread_mutex_t g_lazy_mu = PTHREAD_MUTEX_INITIALIZER;
+struct lazy_lock {
+    lazy_lock() { pthread_mutex_lock(&g_lazy_mu); }
+    ~lazy_lock() { pthread_mutex_unlock(&g_lazy_mu); }
+};
 
 static uint32_t vision_ksplit(uint32_t m, uint32_t n, uint32_t k) {
     const uint32_t blocks = ((m + 63u) / 64u) * ((n + 127u) / 128u), steps = k / 64u;
@@ -358,6 +367,7 @@ extern "C" int uocr_op_vision_linear(uint32_t qtype, const void *w, const void *
     d.out1 = dst1;
     d.out2 = dst2;
     d.ksplit = vision_ksplit(m, n, k);
+    lazy_lock lk;
     if (d.ksplit > 1u) {
         const size_t need = (size_t)d.ksplit * m * n * sizeof(float);
         if (need > g_vision_part_bytes) {
@@ -390,6 +400,7 @@ extern "C" int uocr_op_prefill_attention(const void *q, const void *k_cache, con
     /* key-split partials: allocated on first need outside graph capture and
      * kept (calls must not overlap); without them the unsplit kernel runs */
     static float *fa_ws = nullptr;
+    lazy_lock lk;
     if (fa_ws == nullptr) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {

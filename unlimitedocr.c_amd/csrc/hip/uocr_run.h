@@ -1,5 +1,5 @@
 /*
- * uocr_run.h - the persistent decode run: one cooperative launch that
+ * uocr_run.h - the persistent decode run: one launch of 256 resident workgroups that
  * carries several greedy decode steps (LM head + selection + 12 decoder
  * layers per step) through the whole GPU.
  *
@@ -41,6 +41,7 @@ typedef struct uocr_run_layer {
     const uint16_t *in_norm, *post_norm;
     const float *fold;              /* [1280][64] router * post_norm (MoE layers) */
     const float *fold_o;            /* [1280][64] O^T fold: z's weights on the attention context */
+    const uint16_t *router;         /* [64][1280] fp16 router rows (exact logits for the routing weights) */
     const void *gate, *up, *down;   /* layer 0 dense SwiGLU */
     const uint16_t *gs, *us, *ds;
     const void *sg, *su, *sd;       /* shared experts (merged 1792) */
@@ -56,6 +57,7 @@ typedef struct uocr_run_model {
     const uint16_t *lms, *embs, *final_norm;
     float invf[UOCR_K_HEAD_DIM / 2];
     uint32_t qa, qf, ql, qe;        /* qtypes: attention, FFN, LM head, embedding */
+    uint64_t limit_ticks;           /* longest wait for a packet (s_memrealtime ticks, 100 MHz) */
 } uocr_run_model;
 
 /* Run-control words at the start of the packet arena. */
@@ -88,7 +90,9 @@ hipError_t uocr_run_reset(hipStream_t st, void *arena);
  * position P + t.  Step t0+i uses tag tag0+i.  model points to a device copy
  * of host_model.  kc/vc: [12][10][cap][128] fp16 caches.  hidden receives
  * each step's final hidden state (layer 11's output); trace (may be NULL)
- * the expert ids of layers 1-11 for steps t < trace_steps ([t][11][6]).
+ * the expert ids of layers 1-11 for steps t < trace_steps ([t][11][6]),
+ * followed by their routing weights (fp32, [trace_steps][11][6]) and the
+ * router inputs a (fp16, [trace_steps][11][1280]).
  * force (may be NULL): step t < force_n embeds force[t] instead of the token
  * it selects (teacher forcing for parity tests). */
 hipError_t uocr_run_launch(hipStream_t st, const uocr_run_model *model, const uocr_run_model *host_model,

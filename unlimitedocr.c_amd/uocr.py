@@ -123,6 +123,9 @@ SIGNATURES = {
     "uocr_engine_trace_enable": ([_VP, _U32], ct.c_int),
     "uocr_engine_trace_read": ([_VP, _VP, _VP], ct.c_int),
     "uocr_engine_trace_force": ([_VP, _VP, _U32], ct.c_int),
+    "uocr_engine_trace_read_weights": ([_VP, _VP], ct.c_int),
+    "uocr_engine_trace_read_router_inputs": ([_VP, _VP], ct.c_int),
+    "uocr_engine_decode_path": ([_VP], ct.c_int),
     "uocr_op_workspace_bytes": ([], _SZ),
     "uocr_op_gemv": ([_U32, _VP, _VP, _U32, _U32, _VP, _VP, _VP], ct.c_int),
     "uocr_op_swiglu": ([_U32, _VP, _VP, _VP, _VP, _U32, _U32, _VP, _VP, _VP], ct.c_int),
@@ -332,6 +335,33 @@ class Engine:
             self._raise(self._lib.uocr_engine_trace_read(self._handle, ids.ctypes.data if steps else None,
                                                          hidden.ctypes.data))
         return ids, hidden
+
+    def trace_read_weights(self) -> np.ndarray:
+        """Routing weights [steps][11][6] float32 of the traced selections
+        (selection order, NaN for steps the last generation did not reach)."""
+        steps = getattr(self, "_trace_steps", 0)
+        w = np.zeros((steps, 11, 6), np.float32)
+        if steps:
+            with self._lock:
+                self._raise(self._lib.uocr_engine_trace_read_weights(self._handle, w.ctypes.data))
+        return w
+
+    def trace_read_router_inputs(self) -> np.ndarray:
+        """Router inputs [steps][11][1280] (fp16 bits as uint16) of the traced
+        selections: the pre-norm input a = h + O ctx of each MoE layer."""
+        steps = getattr(self, "_trace_steps", 0)
+        a = np.zeros((steps, 11, 1280), np.uint16)
+        if steps:
+            with self._lock:
+                self._raise(self._lib.uocr_engine_trace_read_router_inputs(self._handle, a.ctypes.data))
+        return a
+
+    def decode_path(self) -> int:
+        """1: the last generation decoded on the persistent run; 0: on the
+        per-step kernels; 2: per-step kernels after the run gave up waiting;
+        -1: no generation yet."""
+        with self._lock:
+            return int(self._lib.uocr_engine_decode_path(self._handle))
 
 
 # ---------------------------------------------------------------------------
