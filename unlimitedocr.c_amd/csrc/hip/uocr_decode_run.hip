@@ -1294,6 +1294,19 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     };
     float inv;
     if (moe) {
+        /* the exact router logit's quarter this block owns (expert b / 4,
+         * columns [320 (b % 4), + 320)): its router row and norm weight
+         * pieces, by wavefront 0 ahead of its polls (used after the dots) */
+        if (UOCR_RUN_EXACT_WEIGHTS && __builtin_amdgcn_readfirstlane(tid_() / 64u) == 0u) {
+            const u32 lane = tid_() % 64u, e = b / LG_Q, c0 = (b % LG_Q) * LG_COLS;
+            if (lane < LG_COLS / 8u) {
+                __builtin_amdgcn_global_load_lds((const AS1 void *)(L.router + (size_t)e * HID + c0 + 8u * lane),
+                                                 (__attribute__((address_space(3))) void *)S.lgw, 16u, 0, 0);
+                __builtin_amdgcn_global_load_lds((const AS1 void *)(L.post_norm + c0 + 8u * lane),
+                                                 (__attribute__((address_space(3))) void *)(S.lgw + 2u * LG_COLS), 16u,
+                                                 0, 0);
+            }
+        }
         /* the z partials first (published before the O rows), the top-6 on z
          * (softmax is monotone and inv_rms > 0, so z orders the experts as
          * the probabilities do) and the expert loads; then a and its norm */
@@ -1312,19 +1325,6 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
          * chosen and ahead of the expert loads */
         uint4 *stg = (uint4 *)(S.scr + 8192u);
         gather_wave_issue<(PO_AR + 63u) / 64u>(R, R.pk + off_o(l), PO, PO_AR, NT / 64u - 1u, stg, [](u32 i) { return i; });
-        /* the exact router logit's quarter this block owns (expert b / 4,
-         * columns [320 (b % 4), + 320)): its router row and norm weight
-         * pieces, by the polling wavefront behind its first polls */
-        if (UOCR_RUN_EXACT_WEIGHTS && __builtin_amdgcn_readfirstlane(tid_() / 64u) == NT / 64u - 1u) {
-            const u32 lane = tid_() % 64u, e = b / LG_Q, c0 = (b % LG_Q) * LG_COLS;
-            if (lane < LG_COLS / 8u) {
-                __builtin_amdgcn_global_load_lds((const AS1 void *)(L.router + (size_t)e * HID + c0 + 8u * lane),
-                                                 (__attribute__((address_space(3))) void *)S.lgw, 16u, 0, 0);
-                __builtin_amdgcn_global_load_lds((const AS1 void *)(L.post_norm + c0 + 8u * lane),
-                                                 (__attribute__((address_space(3))) void *)(S.lgw + 2u * LG_COLS), 16u,
-                                                 0, 0);
-            }
-        }
         /* wavefront 0: z of expert e (lane e) over the 16 partials in a fixed
          * order, then the top-6 */
         TLD(l, 18u);
@@ -1411,28 +1411,6 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
             const float ps = __shfl(p, (int)S.selid[min(k, TOPK - 1u)]); /* lane k < 6: p of expert selid[k] */
             if (k < TOPK) S.selw[k] = ps;
         }
-        if (UOCR_RUN_EXACT_WEIGHTS && __builtin_amdgcn_readfirstlane(tid_() / 64u) == NT / 64u - 1u) {
-            /* the reference's router input, rounded as it rounds it:
-             * n[c] = f16(a[c] inv w[c]), inv = 1 / sqrt(mean a^2 + eps); this
-             * block's quarter of logit b / 4 = sum_c R[b / 4][c] n[c] goes to
-             * the DN stage with the mids (the experts were chosen from z, the
-             * weights come from these logits) */
-            float ss = 0.0f;
-#pragma unroll
-            for (u32 w = 0; w < NT / 64u; ++w) ss += S.red[w];
-            const float inve = 1.0f / __builtin_sqrtf(ss / (float)HID + 1.0e-6f);
-            const u32 lane = tid_() % 64u, c0 = (b % LG_Q) * LG_COLS;
-            const h16 *rw = (const h16 *)S.lgw, *nw = rw + LG_COLS;
-            float part = 0.0f;
-#pragma unroll
-            for (u32 k = 0; k < LG_COLS / 64u; ++k) {
-                const u32 c = lane * (LG_COLS / 64u) + k;
-                const h16 n = (h16)(((float)S.hres[c0 + c] * inve) * (float)nw[c]);
-                part = fmaf((float)n, (float)rw[c], part);
-            }
-            part = wave_sum(part);
-            if (lane == 0u) S.zout[0] = part;
-        }
     } else {
         if (!gather_a()) return false;
         TLR(2u * (4u + 5u * l));
@@ -1458,11 +1436,37 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         const float du = group_sum<G::LPR>(pu) * inv;
         if (sub == 0u && r < nrows) S.outv[r] = (h16)(fsilu(dg) * du);
     }
+    constexpr u32 LG_W = 7u, LG_PER = (LG_COLS + LG_W - 1u) / LG_W; /* the 7 row wavefronts' shares */
+    if (moe && UOCR_RUN_EXACT_WEIGHTS) {
+        /* the reference's router input, rounded as it rounds it:
+         * n[c] = f16(a[c] inv w[c]); this block's quarter of logit b / 4 =
+         * sum_c R[b / 4][c] n[c] (the experts were chosen from z, the routing
+         * weights come from these logits): wavefront w < 7 sums columns
+         * [46 w, 46 w + 46) of the quarter, one per lane */
+        static_assert(LG_PER <= 64u, "one column per lane");
+        const u32 wave = __builtin_amdgcn_readfirstlane(tid_() / 64u), lane = tid_() % 64u;
+        if (wave < LG_W) {
+            const u32 k = wave * LG_PER + lane;
+            float x = 0.0f;
+            if (lane < LG_PER && k < LG_COLS) {
+                const h16 *rw = (const h16 *)S.lgw, *nw = rw + LG_COLS;
+                const h16 n = (h16)(((float)S.hres[(b % LG_Q) * LG_COLS + k] * inv) * (float)nw[k]);
+                x = (float)n * (float)rw[k];
+            }
+            x = wave_sum(x);
+            if (lane == 0u) S.zout[wave] = x;
+        }
+    }
     __syncthreads();
     TLD(l, 11u);
     publish(R, R.pk + off_mid(l), PMID, b * PMID_B, PMID_B, tag, [&](u32 p) {
         uint3 v = pay6(S.outv, p, moe ? GU_ROWS : nrows);
-        if (moe && p == PMID_B - 1u) v.z = __float_as_uint(S.zout[0]); /* mids 28, 29 do not exist */
+        if (moe && p == PMID_B - 1u && UOCR_RUN_EXACT_WEIGHTS) {
+            float q = S.zout[0]; /* mids 28, 29 do not exist: the quarter, its 7 shares in order */
+#pragma unroll
+            for (u32 w = 1; w < LG_W; ++w) q += S.zout[w];
+            v.z = __float_as_uint(q);
+        }
         return v;
     });
     TLD(l, 19u);
@@ -1521,18 +1525,16 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
 #pragma unroll
             for (u32 r = 0; r < TOPK; ++r) w6[r] = S.selw[r];
         } else {
-            float q4[LG_Q];
-#pragma unroll
-            for (u32 q = 0; q < LG_Q; ++q) q4[q] = lgp[lane * LG_Q + q];
-            __builtin_amdgcn_sched_barrier(0);
-            float lg = q4[0];
-#pragma unroll
-            for (u32 q = 1; q < LG_Q; ++q) lg += q4[q];
+            const float4 q4 = ((const float4 *)lgp)[lane];
+            const float lg = ((q4.x + q4.y) + q4.z) + q4.w;
             const float mx = wave_max_dpp(lg);
             const float pe = __expf(lg - mx);
-            const float p = pe / wave_sum(pe);
+            const float p = pe * frcp(wave_sum(pe));
 #pragma unroll
-            for (u32 r = 0; r < TOPK; ++r) w6[r] = __shfl(p, (int)S.selid[r]);
+            for (u32 r = 0; r < TOPK; ++r) {
+                w6[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p),
+                                                                 (int)__builtin_amdgcn_readfirstlane(S.selid[r])));
+            }
         }
         if (R.trace != nullptr && b == 0u && lane < TOPK && tid_() < 64u && (u32)t < R.trace_steps) {
             float mine = w6[0];
