@@ -10,7 +10,7 @@ HBM before timing starts.  The Q8 and fp16 profiles run the same workload and
 are reported beside it.
 
 `roofline` is the dominant kernel of the default Q4 decode, k_decode_run
-(one cooperative launch per 8 steps): HIP events around each launch on the
+(one launch of 256 resident workgroups per 8 steps): HIP events around each launch on the
 engine stream over one config-5 generation, algorithmic bytes = 8 x the
 decode bytes per token.  The Q8 profile decodes through the same run; beside
 it, for the per-step graph path (the fp16 default): `graph_path_moe_gate_up`, its dominant kernel k_moe_gate_up at
@@ -243,7 +243,7 @@ def gate_up_roofline(log, n_copy: int = 5, per_copy: int = 12, replays: int = 40
 
 
 def run_kernel_roofline(log) -> dict:
-    """The default Q4 decode: k_decode_run, one cooperative launch per 8 decode
+    """The default Q4 decode: k_decode_run, one launch per 8 decode
     steps (LM head + 12 layers each), timed with an event pair around every
     launch on the engine's stream (UOCR_HIP_RUN_EVENTS=1 with profiling) over
     one config-5 generation.  Algorithmic bytes per launch = 8 x the decode
@@ -274,12 +274,12 @@ def run_kernel_roofline(log) -> dict:
     traffic = None
     if RUN_TRAFFIC_FILE.exists():
         traffic = json.loads(RUN_TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
-    return {"kernel": "k_decode_run<Q8, Q4, Q4, Q4> (persistent cooperative decode: 8 steps of LM head + 12 layers "
+    return {"kernel": "k_decode_run<Q8, Q4, Q4, Q4> (persistent decode run: 8 steps of LM head + 12 layers "
                       "per launch; the default Q4 and Q8 decode)",
             "bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s", "frac": round(gbs / 8000.0, 4),
             "traffic": traffic, "avg_launch_us": round(avg_us, 2), "algorithmic_bytes": int(algo),
             "launches": launches,
-            "timing": "HIP events around each cooperative launch on the engine stream, one config-5 generation"}
+            "timing": "HIP events around each launch on the engine stream, one config-5 generation"}
 
 
 RUN_TRAFFIC_FILE = ROOT / "profiles" / "decode_run_q4_traffic.json"

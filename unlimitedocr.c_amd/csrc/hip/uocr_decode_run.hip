@@ -1496,6 +1496,10 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     const u32 nmid = moe ? TOPK * EI + SI : DI;
     h16 *mids = (h16 *)S.scr;
     float *lgp = (float *)(S.scr + (TOPK * EI + SI) * 2u); /* [256] the logit quarters */
+    /* the selected experts (this block's GU stage), read before the gather */
+    u32 sel[TOPK];
+#pragma unroll
+    for (u32 r = 0; r < TOPK; ++r) sel[r] = moe ? __builtin_amdgcn_readfirstlane(S.selid[r]) : 0u;
     static_assert((TOPK * EI + SI) * 2u + NB * 4u <= 24576u, "DN LDS");
     if (!gather<(PMID + NT - 1u) / NT>(R, R.pk + off_mid(l), PMID, PMID, tag, W_DN, (u32)t, [](u32 i) { return i; },
                         [&](u32 i, uint4 v) {
@@ -1528,13 +1532,10 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
             const float4 q4 = ((const float4 *)lgp)[lane];
             const float lg = ((q4.x + q4.y) + q4.z) + q4.w;
             const float mx = wave_max_dpp(lg);
-            const float pe = __expf(lg - mx);
+            const float pe = fexp(lg - mx);
             const float p = pe * frcp(wave_sum(pe));
 #pragma unroll
-            for (u32 r = 0; r < TOPK; ++r) {
-                w6[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p),
-                                                                 (int)__builtin_amdgcn_readfirstlane(S.selid[r])));
-            }
+            for (u32 r = 0; r < TOPK; ++r) w6[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), (int)sel[r]));
         }
         if (R.trace != nullptr && b == 0u && lane < TOPK && tid_() < 64u && (u32)t < R.trace_steps) {
             float mine = w6[0];
