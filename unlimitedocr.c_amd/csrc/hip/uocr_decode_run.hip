@@ -529,6 +529,7 @@ struct Lds {
     uint8_t *scr;
     float *xsum; /* chunk sums of the LM head's activation */
     uint8_t *lgw; /* the GU block's router row and norm weight quarter (2 x 640 bytes) */
+    uint4 *dnw;   /* the DN rows' weight chunks: [wavefront][slot][lane] */
 };
 
 /* ---- LM head -------------------------------------------------------------- */
@@ -1224,9 +1225,24 @@ struct DnCfg {
 };
 static_assert(NT / 64u == DN_ROWS, "DN: one output row per wavefront");
 
+/* Where the DN rows' 16-byte weight chunks wait for the DN stage (the
+ * scales always stay in registers):
+ *   - Q4: in registers, loaded once the GU stage's own loads are consumed;
+ *   - Q8: in LDS (S.dnw: [wavefront][slot][lane] uint4), by LDS-direct loads
+ *     issued during the GU stage right after its gather of a, so the DN
+ *     stage polls for the mids with no row loads in flight and finds its
+ *     rows resident, and no DN registers are live through the GU stage.
+ * Measured on config 5: Q8 3,370 (LDS, early) against 3,199 tok/s (registers,
+ * late; the Q8 kernel then spilled 21 VGPRs); Q4 3,810 (registers, late)
+ * against 3,736 (LDS, late) and 3,648 (LDS, early). */
+template <int QF>
+constexpr bool dn_in_lds() {
+    return QF == 3;
+}
 template <int QF>
 struct DnFrags {
-    RowFrag<DnCfg<QF>::J> f;
+    uint4 w[dn_in_lds<QF>() ? 1u : DnCfg<QF>::J];
+    h16 s[DnCfg<QF>::J];
 };
 
 /* layer 0's dense down row uses the same registers: as many chunk slots */
@@ -1236,42 +1252,74 @@ __device__ __forceinline__ u32 dn_row() {
     return blockIdx.x * DN_ROWS + (tid_() >> 6);
 }
 
-/* Routed down rows of the selected experts (ids in LDS) and the shared down row. */
+__device__ __forceinline__ void lds16(const void *src, uint4 *dst, bool nt) {
+    if (nt) {
+        __builtin_amdgcn_global_load_lds((const AS1 void *)src, (__attribute__((address_space(3))) void *)dst, 16u, 0,
+                                         2 /* nt */);
+    } else {
+        __builtin_amdgcn_global_load_lds((const AS1 void *)src, (__attribute__((address_space(3))) void *)dst, 16u, 0,
+                                         0);
+    }
+}
+
+/* Routed down rows of the selected experts (ids in LDS, non-temporal) and
+ * the shared down row (plain: it stays in the Infinity Cache). */
 template <int QF>
 __device__ __forceinline__ void dn_load(const Run &R, const Lds &S, const SlabD &L, DnFrags<QF> &F) {
     typedef DnCfg<QF> G;
     if (blockIdx.x >= DN_BLOCKS) return;
-    const u32 c = dn_row(), lane = tid_() & 63u;
+    const u32 c = dn_row(), lane = tid_() & 63u, wave = __builtin_amdgcn_readfirstlane(tid_() >> 6);
     constexpr u32 CPG = chunks_per_group<QF>();
+    uint4 *dst = S.dnw + (size_t)wave * G::J * 64u;
 #pragma unroll
     for (u32 j = 0; j < G::J; ++j) {
         const u32 q = min(lane + 64u * j, G::CT - 1u);
         if (q < TOPK * G::CR) {
             const u32 r = q / G::CR, cc = q % G::CR, e = S.selid[r];
             const uint8_t *W = gp<uint8_t>(L.ed) + e * L.dws + (size_t)c * 16u * G::CR + 16u * cc;
-            F.f.w[j] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4v *)W));
-            if (QF != 1) F.f.s[j] = __builtin_nontemporal_load(H(L.eds) + e * L.dss + (size_t)c * (EI / 64u) + cc / CPG);
+            if (dn_in_lds<QF>()) {
+                lds16(W, dst + j * 64u, true);
+            } else {
+                F.w[j] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4v *)W));
+            }
+            if (QF != 1) F.s[j] = __builtin_nontemporal_load(H(L.eds) + e * L.dss + (size_t)c * (EI / 64u) + cc / CPG);
         } else {
             const u32 cc = q - TOPK * G::CR;
-            F.f.w[j] = *(const uint4 *)(gp<uint8_t>(L.sd) + (size_t)c * 16u * G::CS + 16u * cc);
-            if (QF != 1) F.f.s[j] = H(L.sds)[(size_t)c * (SI / 64u) + cc / CPG];
+            const uint8_t *W = gp<uint8_t>(L.sd) + (size_t)c * 16u * G::CS + 16u * cc;
+            if (dn_in_lds<QF>()) {
+                lds16(W, dst + j * 64u, false);
+            } else {
+                F.w[j] = *(const uint4 *)W;
+            }
+            if (QF != 1) F.s[j] = H(L.sds)[(size_t)c * (SI / 64u) + cc / CPG];
         }
     }
 }
 
 template <int QF>
-__device__ __forceinline__ void dd_load(const Run &R, DnFrags<QF> &F) {
+__device__ __forceinline__ void dd_load(const Run &R, const Lds &S, DnFrags<QF> &F) {
     typedef DnCfg<QF> G;
     if (blockIdx.x >= DN_BLOCKS) return;
     const AS4 RunLayerD &L = R.M->L[0];
-    const u32 c = dn_row(), sub = tid_() & 63u;
-    frag_load<QF, 64u, G::JD>(F.f, gp<uint8_t>(L.down) + (size_t)c * 16u * G::CD, H(L.ds) + (size_t)c * (DI / 64u),
-                              G::CD, sub);
+    const u32 c = dn_row(), lane = tid_() & 63u, wave = __builtin_amdgcn_readfirstlane(tid_() >> 6);
+    uint4 *dst = S.dnw + (size_t)wave * G::J * 64u;
+#pragma unroll
+    for (u32 j = 0; j < G::JD; ++j) {
+        const u32 q = min(lane + 64u * j, G::CD - 1u);
+        const uint8_t *W = gp<uint8_t>(L.down) + (size_t)c * 16u * G::CD + 16u * q;
+        if (dn_in_lds<QF>()) {
+            lds16(W, dst + j * 64u, false);
+        } else {
+            F.w[j] = *(const uint4 *)W;
+        }
+        if (QF != 1) F.s[j] = H(L.ds)[(size_t)c * (DI / 64u) + q / chunks_per_group<QF>()];
+    }
 }
 
 /* GU stage: gathers the O outputs (a, and the z partials in MoE layers),
  * normalises a, selects the experts (MoE), and computes the block's mids.
  * MoE layers also issue the DN stage's loads (dn) once the experts are known. */
+#define UOCR_RUN_DN_EARLY dn_in_lds<QF>()
 #ifndef UOCR_RUN_WAVE_TOPK
 #define UOCR_RUN_WAVE_TOPK (QF == 4) /* Q8: 3,180 against 3,196 tok/s with it */
 #endif
@@ -1391,6 +1439,9 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         /* the other wavefronts' expert rows may still be arriving */
         lds_barrier();
         if (S.red[15] == 0.0f) return false;
+        /* the DN stage's rows of the selected experts into LDS, now that no
+         * poll of this stage is left behind them */
+        if (UOCR_RUN_DN_EARLY) dn_load<QF>(R, S, sd, dn);
         TLD(l, 15u);
         if (R.trace != nullptr && b == 0u && (u32)t < R.trace_steps && tid_() < HID / 8u) {
             uint4 *ta = (uint4 *)(R.trace + 2u * (size_t)R.trace_steps * 11u * TOPK);
@@ -1414,6 +1465,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     } else {
         if (!gather_a()) return false;
         TLR(2u * (4u + 5u * l));
+        if (UOCR_RUN_DN_EARLY) dd_load<QF>(R, S, dn);
         rms_defer(S.hres, nwp, S.xs, S.red, nullptr, nullptr);
         __syncthreads();
         inv = rms_inv(S.red);
@@ -1470,14 +1522,13 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         return v;
     });
     TLD(l, 19u);
-    /* the DN stage's rows of the selected experts (layer 0: the dense down
-     * row), issued once this stage's own loads are consumed, so the two
-     * streams do not share bandwidth on the critical path and no DN
-     * registers are live through the gate/up dots */
-    if (moe) {
-        dn_load<QF>(R, S, sd, dn);
-    } else {
-        dd_load<QF>(R, dn);
+    if (!UOCR_RUN_DN_EARLY) {
+        /* the DN rows after this stage's own loads are consumed */
+        if (moe) {
+            dn_load<QF>(R, S, sd, dn);
+        } else {
+            dd_load<QF>(R, S, dn);
+        }
     }
     TLD(l, 20u);
     TLR(2u * (4u + 5u * l) + 1u);
@@ -1518,6 +1569,10 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     }
 #endif
     const u32 c = dn_row(), lane = tid_() & 63u, rl = c - b * DN_ROWS;
+    /* the rows: registers, or this wavefront's LDS-direct loads */
+    if (dn_in_lds<QF>()) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint4 *dnw = S.dnw + (size_t)(tid_() >> 6) * G::J * 64u;
+    auto dnrow = [&](u32 j) { return dn_in_lds<QF>() ? dnw[j * 64u + tid_() % 64u] : dn.w[dn_in_lds<QF>() ? 0u : j]; };
     float out;
     if (moe) {
         /* routing weights: every wavefront sums the logits (lane e: the four
@@ -1553,8 +1608,8 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                 const u32 qq = min(q, G::CT - 1u);
                 const bool routed = qq < TOPK * G::CR;
                 const u32 r = routed ? qq / G::CR : 0u, cc = routed ? qq % G::CR : qq - TOPK * G::CR;
-                const float d = chunk_dot<QF>(dn.f.w[j], mids + (routed ? r * EI : TOPK * EI), cc);
-                const float v = QF == 1 ? d : d * (float)dn.f.s[j];
+                const float d = chunk_dot<QF>(dnrow(j), mids + (routed ? r * EI : TOPK * EI), cc);
+                const float v = QF == 1 ? d : d * (float)dn.s[j];
                 if (q < G::CT) {
                     if (routed) {
                         float wr = w6[0];
@@ -1571,7 +1626,17 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         sh = wave_sum(sh);
         out = acc + (float)(h16)sh + (float)S.hres[c];
     } else {
-        const float d = wave_sum(frag_dot<QF, 64u, G::JD>(dn.f, mids, G::CD, lane));
+        float acc = 0.0f;
+#pragma unroll
+        for (u32 j = 0; j < G::JD; ++j) {
+            const u32 q = lane + 64u * j;
+            if (64u * (j + 1u) <= G::CD || q < G::CD) {
+                const float dj = chunk_dot<QF>(dnrow(j), mids, min(q, G::CD - 1u));
+                const float v = QF == 1 ? dj : dj * (float)dn.s[j];
+                acc += q < G::CD ? v : 0.0f;
+            }
+        }
+        const float d = wave_sum(acc);
         out = d + (float)S.hres[c];
     }
     TLD(l, 12u);
@@ -1614,11 +1679,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
     __shared__ u32 selid[8];
     __shared__ unsigned long long keyw[NT / 64u];
     __shared__ float xsum[HID / 16u];
-    /* the exact-logit slices; sized so the block's LDS exceeds half a CU's
-     * 160 KB and no CU can hold two run workgroups whatever the register
-     * allocation (the run needs one workgroup on each of the 256 CUs) */
-    __shared__ __attribute__((aligned(16))) uint8_t lgw[10240];
-    Lds S{xs, hres, outv, red, zout, selw, zw, selid, keyw, scr, xsum, lgw};
+    __shared__ __attribute__((aligned(16))) uint8_t lgw[2u * LG_COLS * 2u];
+    /* the DN rows; with it the block's LDS exceeds half a CU's 160 KB, so no
+     * CU can hold two run workgroups whatever the register allocation (the
+     * run needs one workgroup on each of the 256 CUs) */
+    __shared__ __attribute__((aligned(16))) uint4 dnw[DN_ROWS * DnCfg<QF>::J * 64u];
+    Lds S{xs, hres, outv, red, zout, selw, zw, selid, keyw, scr, xsum, lgw, dnw};
     Run R;
     R.M = (const AS4 RunModelD *)A.M;
     R.pk = A.pk;
