@@ -1165,8 +1165,59 @@ __device__ __forceinline__ void gu_rows(GuFrags<QF> &F, const uint8_t *GW, const
     }
 }
 
+/* MoE-layer gate/up rows of block b, GU_ROWS each: blocks < 192 are routed
+ * (rank b / 32, rows 28 (b % 32) of that expert), the rest shared.  With
+ * UOCR_RUN_O_SHARED=1 the O blocks, which finish their own stage last, take
+ * shared slices 0 .. 39 instead (fixed rows, loaded once their O rows are
+ * out) and the other blocks, in order, the routed slices and then shared
+ * slices 40 ..: measured slower (Q4 3,716 against 3,804 tok/s, Q8 3,308
+ * against 3,333).  Returns the routed rank, or -1 with the shared slice. */
+#ifndef UOCR_RUN_O_SHARED
+#define UOCR_RUN_O_SHARED 0
+#endif
+__device__ __forceinline__ bool is_o_block(u32 b) {
+    return b >= O0 && b < O0 + O_BLOCKS;
+}
+__device__ __forceinline__ int gu_role(u32 b, u32 &slice) {
+    if (!UOCR_RUN_O_SHARED) {
+        slice = b < GU_ROUTED ? b % 32u : b - GU_ROUTED;
+        return b < GU_ROUTED ? (int)(b / 32u) : -1;
+    }
+    if (is_o_block(b)) {
+        slice = b - O0;
+        return -1;
+    }
+    const u32 n = b < O0 ? b : b - O_BLOCKS;
+    if (n < GU_ROUTED) {
+        slice = n % 32u;
+        return (int)(n / 32u);
+    }
+    slice = O_BLOCKS + (n - GU_ROUTED);
+    return -1;
+}
+static_assert(NB - O_BLOCKS >= GU_ROUTED && O_BLOCKS * GU_ROWS <= SI, "routed rows on non-O blocks, shared on the rest");
+
+/* Index of block b's first mid in the DN stage's mid vector: layer 0 the
+ * dense rows 27 b ..; MoE layers [routed rank 0 | .. | rank 5 | shared]. */
+__device__ __forceinline__ u32 mid_base(u32 b, bool moe) {
+    if (!moe) return b * DGU_ROWS;
+    u32 slice;
+    const int rank = gu_role(b, slice);
+    return (rank >= 0 ? (u32)rank * EI : TOPK * EI) + slice * GU_ROWS;
+}
+
+template <int QF>
+__device__ __forceinline__ void gu_load_shared(const Run &R, u32 l, GuFrags<QF> &F) {
+    const AS4 RunLayerD &L = R.M->L[l];
+    u32 slice;
+    if (gu_role(blockIdx.x, slice) < 0) {
+        gu_rows<QF, false>(F, gp<uint8_t>(L.sg), H(L.sgs), gp<uint8_t>(L.su), H(L.sus), slice * GU_ROWS, GU_ROWS, SI);
+    }
+}
+
 /* Loads that do not depend on the router: dense rows (layer 0) or the
- * shared experts' rows (blocks >= GU_ROUTED). */
+ * shared experts' rows of the shared-slice blocks outside the O stage (the O
+ * blocks issue theirs in the GU stage). */
 template <int QF>
 __device__ __forceinline__ void gu_load_static(const Run &R, u32 l, GuFrags<QF> &F) {
     const AS4 RunLayerD &L = R.M->L[l];
@@ -1174,9 +1225,8 @@ __device__ __forceinline__ void gu_load_static(const Run &R, u32 l, GuFrags<QF> 
     if (l == 0u) {
         gu_rows<QF, false>(F, gp<uint8_t>(L.gate), H(L.gs), gp<uint8_t>(L.up), H(L.us), b * DGU_ROWS,
                            min(DGU_ROWS, DI - min(b * DGU_ROWS, DI - 1u)), DI);
-    } else if (b >= GU_ROUTED) {
-        gu_rows<QF, false>(F, gp<uint8_t>(L.sg), H(L.sgs), gp<uint8_t>(L.su), H(L.sus), (b - GU_ROUTED) * GU_ROWS,
-                           GU_ROWS, SI);
+    } else if (!UOCR_RUN_O_SHARED || !is_o_block(b)) {
+        gu_load_shared<QF>(R, l, F);
     }
 }
 
@@ -1342,6 +1392,10 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     };
     float inv;
     if (moe) {
+        u32 slice;
+        const int rank = gu_role(b, slice);
+        /* the O blocks' shared rows, issued now that their O rows are out */
+        if (UOCR_RUN_O_SHARED && is_o_block(b)) gu_load_shared<QF>(R, l, F);
         /* the exact router logit's quarter this block owns (expert b / 4,
          * columns [320 (b % 4), + 320)): its router row and norm weight
          * pieces, by wavefront 0 ahead of its polls (used after the dots) */
@@ -1401,10 +1455,9 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                     if (e == k) S.selid[k] = sid[k] < NEXP ? sid[k] : 0u;
                 }
             }
-            const u32 rank = min(b / 32u, TOPK - 1u);
 #pragma unroll
             for (u32 k = 0; k < TOPK; ++k) {
-                if (rank == k) mye = sid[k] < NEXP ? sid[k] : 0u;
+                if (rank == (int)k) mye = sid[k] < NEXP ? sid[k] : 0u;
             }
         }
         /* the last wavefront's polls for a are in flight */
@@ -1413,10 +1466,10 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
             R.trace[((size_t)t * 11u + (l - 1u)) * TOPK + tid_()] = S.selid[tid_()];
         }
         TLD(l, 9u);
-        if (b < GU_ROUTED) {
-            const u32 rank = b / 32u, e = UOCR_RUN_WAVE_TOPK ? mye : S.selid[rank];
+        if (rank >= 0) {
+            const u32 e = UOCR_RUN_WAVE_TOPK ? mye : S.selid[rank];
             gu_rows<QF, true>(F, gp<uint8_t>(sd.eg) + e * sd.gws, H(sd.egs) + e * sd.gss, gp<uint8_t>(sd.eu) + e * sd.gws,
-                              H(sd.eus) + e * sd.gss, (b % 32u) * GU_ROWS, GU_ROWS, EI);
+                              H(sd.eus) + e * sd.gss, slice * GU_ROWS, GU_ROWS, EI);
         }
         TLD(l, 10u);
 #ifdef UOCR_RUN_TIMELINE
@@ -1554,7 +1607,7 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     static_assert((TOPK * EI + SI) * 2u + NB * 4u <= 24576u, "DN LDS");
     if (!gather<(PMID + NT - 1u) / NT>(R, R.pk + off_mid(l), PMID, PMID, tag, W_DN, (u32)t, [](u32 i) { return i; },
                         [&](u32 i, uint4 v) {
-                            const u32 blk = i / PMID_B, k = i % PMID_B, base = blk * rows_b + 6u * k;
+                            const u32 blk = i / PMID_B, k = i % PMID_B, base = mid_base(blk, moe) + 6u * k;
                             if (6u * k < rows_b) put6(mids + base, v, 6u * k, rows_b);
                             if (moe && k == PMID_B - 1u) lgp[blk] = __uint_as_float(v.w);
                             (void)nmid;
