@@ -83,7 +83,7 @@ UOCR_API int uocr_engine_trace_read_weights(uocr_engine *engine, float *weights)
  * engine's own input. */
 UOCR_API int uocr_engine_trace_read_router_inputs(uocr_engine *engine, uint16_t *inputs);
 /* Which decode loop served the engine's last generation (no counterpart in
- * the reference; for tests and diagnostics): 1 the persistent cooperative
+ * the reference; for tests and diagnostics): 1 the persistent
  * run, 0 the per-step kernels, 2 the per-step kernels after the run gave up
  * waiting on a workgroup and the request was served again, -1 none yet or
  * not a HIP engine. */

@@ -479,7 +479,7 @@ def test_config5_full_decode_matches_oracle(gpu, monkeypatch, profile, run):
     Free-running (the production path, no trace or forcing): ids equal the
     oracle's up to the first step with a margin of at most 1e-2 or after a
     router near-tie.
-    run "1" takes the persistent cooperative decode (UOCR_HIP_RUN=1) where
+    run "1" takes the persistent decode (UOCR_HIP_RUN=1) where
     the profile has one; "0" the per-step kernel path."""
     import sys
     from pathlib import Path
