@@ -30,6 +30,7 @@
 #ifndef UOCR_K_ATTN_SPLITS
 #define UOCR_K_ATTN_SPLITS 16      /* split-K blocks per head in decode attention */
 #endif
+#define UOCR_K_ATTN_SPLITS_WIDE 32 /* partials layout of the operator API's wide split (long contexts) */
 #define UOCR_K_LM_BLOCKS 1024      /* upper bound on LM-head blocks */
 #define UOCR_K_ROUTER_FIX_SHIFT 32 /* router fold accumulator: round(z * 2^32) in int64 */
 #define UOCR_K_ROUTER_ACC_COPIES 4 /* accumulator copies (block b adds into copy b % 4) */
@@ -67,6 +68,7 @@ typedef struct uocr_expert_slab {
 
 /* Scratch sizes (bytes) the launchers expect. */
 #define UOCR_ATTN_PARTIAL_FLOATS (UOCR_K_HEADS * UOCR_K_ATTN_SPLITS * (UOCR_K_HEAD_DIM + 2))
+#define UOCR_ATTN_PARTIAL_FLOATS_WIDE (UOCR_K_HEADS * UOCR_K_ATTN_SPLITS_WIDE * (UOCR_K_HEAD_DIM + 2))
 #define UOCR_LM_KEYS 16 /* LM-head argmax key copies (block b -> copy b % 16) */
 #define UOCR_LM_PARTIAL_WORDS (2 * UOCR_LM_KEYS) /* the 64-bit argmax keys, in 32-bit words */
 
@@ -108,6 +110,16 @@ hipError_t uocr_launch_attn_out(hipStream_t st, uocr_qmat O, const float *partia
                                 uint16_t *out, uint16_t *ctx_out, const float *router_fold, int64_t *router_acc);
 /* The merge alone: ctx = f16(merge(partials)). */
 hipError_t uocr_launch_attn_merge(hipStream_t st, const float *partials, uint16_t *ctx);
+/* The same three over the wide partials layout (UOCR_K_ATTN_SPLITS_WIDE
+ * splits, UOCR_ATTN_PARTIAL_FLOATS_WIDE floats): `splits` <= 32 blocks per
+ * head run, the layout's other splits are marked empty, so the merge is the
+ * same function of the live slots at any split count. */
+hipError_t uocr_launch_attention_wide(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
+                                      uint32_t cache_capacity, const uocr_step_state *state, float *partials,
+                                      uint32_t splits);
+hipError_t uocr_launch_attn_out_wide(hipStream_t st, uocr_qmat O, const float *partials, const uint16_t *res,
+                                     uint16_t *out, uint16_t *ctx_out);
+hipError_t uocr_launch_attn_merge_wide(hipStream_t st, const float *partials, uint16_t *ctx);
 /* Router logits: logits[e] = R_e . rmsnorm(x) (fp16 R [64][1280], fp32 dot),
  * one wavefront per expert row. */
 hipError_t uocr_launch_router_logits(hipStream_t st, const uint16_t *R, const uint16_t *x, const uint16_t *nw,

@@ -456,14 +456,18 @@ constexpr int ATT_GROUPS = ATT_THREADS / 16;
  * partial (max, sum, acc[128] / sum) per head:
  *   fp16 acc/sum at ((h16 *)part)[(h*S + s)*128 + d],
  *   fp32 (max, sum) at part[H*S*128 + (h*S + s)*2]. */
-template <int ATT_UNROLL>
+template <int ATT_UNROLL, int SL = UOCR_K_ATTN_SPLITS>
 __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict__ q, const h16 *__restrict__ kc,
                                                      const h16 *__restrict__ vc, u32 cap,
                                                      const uocr_step_state *__restrict__ st, float *__restrict__ part,
                                                      long long *__restrict__ racc,
                                                      unsigned long long *__restrict__ clear_keys) {
     TL(2);
-    constexpr int S = UOCR_K_ATTN_SPLITS;
+    /* SL: splits of the partials' layout; the grid runs gridDim.x <= SL of
+     * them, and block (s, h) with s < SL - gridDim.x also marks the unused
+     * split gridDim.x + s of head h empty (max -inf, sum 0) */
+    constexpr int S = SL;
+    const int SE = (int)gridDim.x;
     if (racc != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
         for (int i = threadIdx.x; i < UOCR_ROUTER_ACC_WORDS; i += ATT_THREADS) racc[i] = 0;
     }
@@ -476,7 +480,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
     __shared__ float sm[NW], sl[NW];
     __shared__ float sacc[NW][UOCR_K_HEAD_DIM];
     const int h = blockIdx.y, s = blockIdx.x;
-    const int chunk = ((int)cap + S - 1) / S;
+    const int chunk = ((int)cap + SE - 1) / SE;
     const int i0 = s * chunk, iend = min((int)cap, i0 + chunk);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int gq = lane >> 4, p = lane & 15;
@@ -596,6 +600,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
             ml[0] = M;
             ml[1] = Ls;
         }
+        if (S > 1 && s < S - SE) {
+            const int se = SE + s;
+            ((h16 *)part)[(size_t)(h * S + se) * UOCR_K_HEAD_DIM + d] = (h16)0.0f;
+            if (d == 0) {
+                float *ml = part + (size_t)UOCR_K_HEADS * S * UOCR_K_HEAD_DIM + (size_t)(h * S + se) * 2u;
+                ml[0] = -INFINITY;
+                ml[1] = 0.0f;
+            }
+        }
     }
 }
 
@@ -607,35 +620,47 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const h16 *__restrict
  * Threads t < H*S compute the weights into LDS; thread t < 160 owns dims
  * 8t..8t+7 and sums their S split values (loads issued by merge_load,
  * before the caller's weight loads). */
+template <int S>
 struct MergeLoads {
-    uint4 a[UOCR_K_ATTN_SPLITS];
-    float2 ml;
+    static constexpr int NML = (UOCR_K_HEADS * S + BLOCK - 1) / BLOCK; /* (max, sum) pairs per thread */
+    uint4 a[S];
+    float2 ml[NML];
 };
 
-__device__ __forceinline__ void merge_load(MergeLoads &m, const float *__restrict__ part) {
-    constexpr int S = UOCR_K_ATTN_SPLITS, HD = UOCR_K_HEAD_DIM, NO = UOCR_K_HIDDEN / 8;
+template <int S>
+__device__ __forceinline__ void merge_load(MergeLoads<S> &m, const float *__restrict__ part) {
+    constexpr int HD = UOCR_K_HEAD_DIM, NO = UOCR_K_HIDDEN / 8;
     const int t = threadIdx.x;
     const int o = min(t, NO - 1), hh = o / (HD / 8), d8 = o % (HD / 8);
     const h16 *accn = (const h16 *)part;
 #pragma unroll
     for (int k = 0; k < S; ++k) m.a[k] = *(const uint4 *)(accn + (size_t)(hh * S + k) * HD + 8 * d8);
-    m.ml = *(const float2 *)(part + (size_t)UOCR_K_HEADS * S * HD + 2u * min(t, UOCR_K_HEADS * S - 1));
+#pragma unroll
+    for (int i = 0; i < MergeLoads<S>::NML; ++i) {
+        m.ml[i] = *(const float2 *)(part + (size_t)UOCR_K_HEADS * S * HD + 2u * min(t + i * BLOCK, UOCR_K_HEADS * S - 1));
+    }
 }
 
-__device__ __forceinline__ void merge_finish(MergeLoads &m, h16 *ctx, float *wk) {
-    constexpr int S = UOCR_K_ATTN_SPLITS, HD = UOCR_K_HEAD_DIM, NO = UOCR_K_HIDDEN / 8;
-    static_assert(S == 4 || S == 8 || S == 16, "split weights use aligned S-lane groups");
-    hold(m.ml);
+template <int S>
+__device__ __forceinline__ void merge_finish(MergeLoads<S> &m, h16 *ctx, float *wk) {
+    constexpr int HD = UOCR_K_HEAD_DIM, NO = UOCR_K_HIDDEN / 8;
+    static_assert(S == 4 || S == 8 || S == 16 || S == 32, "split weights use aligned S-lane groups");
+    static_assert(BLOCK % S == 0, "a thread's (max, sum) pairs belong to whole S-lane groups");
+#pragma unroll
+    for (int i = 0; i < MergeLoads<S>::NML; ++i) hold(m.ml[i]);
 #pragma unroll
     for (int k = 0; k < S; ++k) hold(m.a[k]);
     const int t = threadIdx.x;
-    if (t < UOCR_K_HEADS * S) {
-        /* lanes S*h..S*h+S-1 hold the splits of head h */
-        float M = m.ml.x;
+#pragma unroll
+    for (int i = 0; i < MergeLoads<S>::NML; ++i) {
+        /* lanes S*h..S*h+S-1 of this pass hold the splits of head h */
+        const int j = t + i * BLOCK;
+        float M = m.ml[i].x;
 #pragma unroll
         for (int o = 1; o < S; o <<= 1) M = fmaxf(M, __shfl_xor(M, o));
-        const float lf = m.ml.x == -INFINITY ? 0.0f : m.ml.y * expf(m.ml.x - M);
-        wk[t] = lf / group_sum<S>(lf);
+        const float lf = m.ml[i].x == -INFINITY ? 0.0f : m.ml[i].y * expf(m.ml[i].x - M);
+        const float w = lf / group_sum<S>(lf);
+        if (j < UOCR_K_HEADS * S) wk[j] = w;
     }
     __syncthreads();
     if (t < NO) {
@@ -671,7 +696,7 @@ __device__ __forceinline__ void merge_finish(MergeLoads &m, h16 *ctx, float *wk)
  * depend on the order in which blocks arrive).  With fold = R * post_norm,
  * z * inv_rms(out) are the router logits R . rmsnorm(out) of the MoE
  * (moe.metal:53-189), less the fp16 rounding of the normalised vector. */
-template <int QT, bool FOLD>
+template <int QT, bool FOLD, int S = UOCR_K_ATTN_SPLITS>
 __global__ __launch_bounds__(BLOCK) void k_attn_out(uocr_qmat O, const float *__restrict__ part,
                                                     const h16 *__restrict__ res, h16 *__restrict__ out,
                                                     h16 *__restrict__ ctx_out, const float *__restrict__ fold,
@@ -680,11 +705,11 @@ __global__ __launch_bounds__(BLOCK) void k_attn_out(uocr_qmat O, const float *__
     constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_for(C), J = j_for(C), R = 64u / LPR;
     constexpr u32 rb = 16u * C, G = K / 64u;
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
-    __shared__ float wk[UOCR_K_HEADS * UOCR_K_ATTN_SPLITS];
+    __shared__ float wk[UOCR_K_HEADS * S];
     const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const u32 sub = lane % LPR, grp = lane / LPR;
     const u32 r = (blockIdx.x * NWAVE + wave) * R + grp, rr = min(r, K - 1u);
-    MergeLoads ml;
+    MergeLoads<S> ml;
     merge_load(ml, part);
     RowFrag<J> f;
     frag_load<QT, LPR, J, UOCR_ATT_W_NT>(f, (const uint8_t *)O.w + (size_t)rr * rb, (const h16 *)O.s + (size_t)rr * G, C, sub);
@@ -726,10 +751,11 @@ __global__ __launch_bounds__(BLOCK) void k_attn_out(uocr_qmat O, const float *__
 }
 
 /* Merge alone (operator API): ctx = merge of the partials. */
+template <int S>
 __global__ __launch_bounds__(BLOCK) void k_attn_merge(const float *__restrict__ part, h16 *__restrict__ ctx) {
     __shared__ __attribute__((aligned(16))) h16 xs[UOCR_K_HIDDEN];
-    __shared__ float wk[UOCR_K_HEADS * UOCR_K_ATTN_SPLITS];
-    MergeLoads ml;
+    __shared__ float wk[UOCR_K_HEADS * S];
+    MergeLoads<S> ml;
     merge_load(ml, part);
     merge_finish(ml, xs, wk);
     for (u32 i = threadIdx.x; i < UOCR_K_HIDDEN / 8u; i += blockDim.x) ((uint4 *)ctx)[i] = ((const uint4 *)xs)[i];
@@ -1316,6 +1342,23 @@ extern "C" hipError_t uocr_launch_qkv_rope_select(hipStream_t st, uocr_qmat Q, u
     return hipGetLastError();
 }
 
+/* splits blocks per head over a partials layout of SL splits; one round of
+ * loads per block where the range allows it */
+template <int SL>
+static void launch_attention_sl(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
+                                uint32_t cache_capacity, const uocr_step_state *state, float *partials,
+                                int64_t *router_acc, uint64_t *clear_keys, uint32_t splits) {
+    const u32 chunk = (cache_capacity + splits - 1u) / splits;
+    auto *kern = chunk <= 2u * ATT_GROUPS   ? k_attention<2, SL>
+                 : chunk <= 3u * ATT_GROUPS ? k_attention<3, SL>
+                 : chunk <= 5u * ATT_GROUPS ? k_attention<5, SL>
+                 : chunk <= 6u * ATT_GROUPS ? k_attention<6, SL>
+                                            : k_attention<9, SL>;
+    hipLaunchKernelGGL(kern, dim3(splits, UOCR_K_HEADS), dim3(ATT_THREADS), 0, st, (const h16 *)q,
+                       (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials,
+                       (long long *)router_acc, (unsigned long long *)clear_keys);
+}
+
 extern "C" hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, const uint16_t *kcache,
                                             const uint16_t *vcache, uint32_t cache_capacity,
                                             const uocr_step_state *state, float *partials, int64_t *router_acc,
@@ -1324,12 +1367,20 @@ extern "C" hipError_t uocr_launch_attention(hipStream_t st, const uint16_t *q, c
         partials == nullptr) {
         return hipErrorInvalidValue;
     }
-    /* one round of loads per block where the range allows it */
-    const u32 chunk = (cache_capacity + UOCR_K_ATTN_SPLITS - 1u) / UOCR_K_ATTN_SPLITS;
-    auto *kern = chunk <= 3u * ATT_GROUPS ? k_attention<3> : (chunk <= 5u * ATT_GROUPS ? k_attention<5> : k_attention<9>);
-    hipLaunchKernelGGL(kern, dim3(UOCR_K_ATTN_SPLITS, UOCR_K_HEADS), dim3(ATT_THREADS), 0, st, (const h16 *)q,
-                       (const h16 *)kcache, (const h16 *)vcache, cache_capacity, state, partials,
-                       (long long *)router_acc, (unsigned long long *)clear_keys);
+    launch_attention_sl<UOCR_K_ATTN_SPLITS>(st, q, kcache, vcache, cache_capacity, state, partials, router_acc,
+                                            clear_keys, UOCR_K_ATTN_SPLITS);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_attention_wide(hipStream_t st, const uint16_t *q, const uint16_t *kcache,
+                                                 const uint16_t *vcache, uint32_t cache_capacity,
+                                                 const uocr_step_state *state, float *partials, uint32_t splits) {
+    if (q == nullptr || kcache == nullptr || vcache == nullptr || cache_capacity == 0u || state == nullptr ||
+        partials == nullptr || splits == 0u || splits > UOCR_K_ATTN_SPLITS_WIDE) {
+        return hipErrorInvalidValue;
+    }
+    launch_attention_sl<UOCR_K_ATTN_SPLITS_WIDE>(st, q, kcache, vcache, cache_capacity, state, partials, nullptr,
+                                                 nullptr, splits);
     return hipGetLastError();
 }
 
@@ -1360,7 +1411,28 @@ extern "C" hipError_t uocr_launch_attn_out(hipStream_t st, uocr_qmat O, const fl
 
 extern "C" hipError_t uocr_launch_attn_merge(hipStream_t st, const float *partials, uint16_t *ctx) {
     if (partials == nullptr || ctx == nullptr) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attn_merge, dim3(1), dim3(BLOCK), 0, st, partials, (h16 *)ctx);
+    hipLaunchKernelGGL(k_attn_merge<UOCR_K_ATTN_SPLITS>, dim3(1), dim3(BLOCK), 0, st, partials, (h16 *)ctx);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_attn_merge_wide(hipStream_t st, const float *partials, uint16_t *ctx) {
+    if (partials == nullptr || ctx == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attn_merge<UOCR_K_ATTN_SPLITS_WIDE>, dim3(1), dim3(BLOCK), 0, st, partials, (h16 *)ctx);
+    return hipGetLastError();
+}
+
+template <int QT>
+static void launch_attn_out_wide_qt(hipStream_t st, uocr_qmat O, const float *partials, const uint16_t *res,
+                                    uint16_t *out, uint16_t *ctx_out) {
+    constexpr u32 rpb = NWAVE * (64u / lpr_for(chunks_per_row<QT>(UOCR_K_HIDDEN)));
+    hipLaunchKernelGGL((k_attn_out<QT, false, UOCR_K_ATTN_SPLITS_WIDE>), dim3((UOCR_K_HIDDEN + rpb - 1u) / rpb),
+                       dim3(BLOCK), 0, st, O, partials, (const h16 *)res, (h16 *)out, (h16 *)ctx_out, nullptr, nullptr);
+}
+
+extern "C" hipError_t uocr_launch_attn_out_wide(hipStream_t st, uocr_qmat O, const float *partials,
+                                                const uint16_t *res, uint16_t *out, uint16_t *ctx_out) {
+    if (!mat_ok(O) || partials == nullptr || res == nullptr || out == nullptr) return hipErrorInvalidValue;
+    DISPATCH_QT(O.qtype, launch_attn_out_wide_qt, st, O, partials, res, out, ctx_out);
     return hipGetLastError();
 }
 

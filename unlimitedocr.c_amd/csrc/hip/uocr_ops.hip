@@ -77,7 +77,8 @@ constexpr size_t A256(size_t v) {
 }
 constexpr size_t WS_STATE = 0;
 constexpr size_t WS_APART = WS_STATE + A256(sizeof(uocr_step_state));
-constexpr size_t WS_LOGITS = WS_APART + A256(UOCR_ATTN_PARTIAL_FLOATS * 4u);
+constexpr size_t WS_LOGITS = WS_APART + A256(UOCR_ATTN_PARTIAL_FLOATS_WIDE * 4u);
+static_assert(UOCR_ATTN_PARTIAL_FLOATS_WIDE >= UOCR_ATTN_PARTIAL_FLOATS, "wide partials layout");
 constexpr size_t WS_LPART = WS_LOGITS + 256u;
 constexpr size_t WS_IDS = WS_LPART + A256(UOCR_LM_PARTIAL_WORDS * 4u);
 constexpr size_t WS_WTS = WS_IDS + 256u;
@@ -232,6 +233,20 @@ static int set_plan(hipStream_t st, void *workspace, uint32_t cap, uint32_t P, u
     return hip_status(uocr_launch_decode_state(st, state, (int32_t)P, (int32_t)g - 1, invf), "attention plan");
 }
 
+/* Blocks per head of the operators' decode attention (wide partials
+ * layout): enough splits that each block's K/V range is small, at most one
+ * block per CU (10 heads x 25 splits = 250 blocks for 256 CUs); short
+ * caches keep 16.  UOCR_OP_ATT_SPLITS (1-32) overrides it, for measurement. */
+static uint32_t op_att_splits(uint32_t cap) {
+    static const int forced = [] {
+        const char *e = getenv("UOCR_OP_ATT_SPLITS");
+        const int v = e != nullptr ? atoi(e) : 0;
+        return v >= 1 && v <= UOCR_K_ATTN_SPLITS_WIDE ? v : 0;
+    }();
+    if (forced != 0) return (uint32_t)forced;
+    return cap >= 2048u ? 25u : 16u;
+}
+
 extern "C" int uocr_op_attention_decode(const void *q, const void *k_cache, const void *v_cache,
                                         uint32_t cache_capacity, uint32_t prompt_length, uint32_t generated_count,
                                         void *workspace, void *out) {
@@ -241,13 +256,14 @@ extern "C" int uocr_op_attention_decode(const void *q, const void *k_cache, cons
     STREAM_OR_RETURN(st);
     const int r = set_plan(st, workspace, cache_capacity, prompt_length, generated_count);
     if (r != UOCR_OK) return r;
-    int r2 = hip_status(uocr_launch_attention(st, (const uint16_t *)q, (const uint16_t *)k_cache,
-                                              (const uint16_t *)v_cache, cache_capacity,
-                                              ws<uocr_step_state>(workspace, WS_STATE), ws<float>(workspace, WS_APART), nullptr,
-                                              nullptr),
+    int r2 = hip_status(uocr_launch_attention_wide(st, (const uint16_t *)q, (const uint16_t *)k_cache,
+                                                   (const uint16_t *)v_cache, cache_capacity,
+                                                   ws<uocr_step_state>(workspace, WS_STATE),
+                                                   ws<float>(workspace, WS_APART), op_att_splits(cache_capacity)),
                         "attention_decode");
     if (r2 != UOCR_OK) return r2;
-    return hip_status(uocr_launch_attn_merge(st, ws<float>(workspace, WS_APART), (uint16_t *)out), "attention merge");
+    return hip_status(uocr_launch_attn_merge_wide(st, ws<float>(workspace, WS_APART), (uint16_t *)out),
+                      "attention merge");
 }
 
 extern "C" int uocr_op_attention_block(uint32_t qtype, const void *wq, const void *sq, const void *wk, const void *sk,
@@ -270,13 +286,14 @@ extern "C" int uocr_op_attention_block(uint32_t qtype, const void *wq, const voi
                        "qkv_rope");
     }
     if (r == UOCR_OK) {
-        r = hip_status(uocr_launch_attention(st, qb, (const uint16_t *)k_cache, (const uint16_t *)v_cache,
-                                             cache_capacity, state, ws<float>(workspace, WS_APART), nullptr, nullptr),
+        r = hip_status(uocr_launch_attention_wide(st, qb, (const uint16_t *)k_cache, (const uint16_t *)v_cache,
+                                                  cache_capacity, state, ws<float>(workspace, WS_APART),
+                                                  op_att_splits(cache_capacity)),
                        "attention");
     }
     if (r == UOCR_OK) {
-        r = hip_status(uocr_launch_attn_out(st, qm(qtype, wo, so), ws<float>(workspace, WS_APART),
-                                            (const uint16_t *)hidden, (uint16_t *)out, cb, nullptr, nullptr),
+        r = hip_status(uocr_launch_attn_out_wide(st, qm(qtype, wo, so), ws<float>(workspace, WS_APART),
+                                                 (const uint16_t *)hidden, (uint16_t *)out, cb),
                        "o_proj");
     }
     return r;
