@@ -391,6 +391,24 @@ __device__ __forceinline__ void publish(const Run &R, uint4 *region, u32 per_cop
     }
 }
 
+/* UOCR_RUN_DRAIN (bit mask: 1 QKV, 2 ATT, 4 O rows, 16 DN): after that
+ * stage's publish, the storing wavefronts wait for their packet stores to
+ * complete before issuing the next stage's loads; loads issued behind
+ * device-coherent stores still in flight delay the packets' visibility.
+ * Measured on config 5 (same box): 17 gives Q4 3,809-3,817 and Q8
+ * 3,351-3,355 tok/s against 3,803 and 3,331 with none; adding ATT (19) the
+ * same; adding the O rows (23) Q4 3,818-3,822 but Q8 3,335; the O rows
+ * alone cost Q4 0.6%.  (The GU stage's publish is followed by the compiler's
+ * own waits before the Q4 DN row loads; removing them cost Q4 0.6%.) */
+#ifndef UOCR_RUN_DRAIN
+#define UOCR_RUN_DRAIN 17
+#endif
+__device__ __forceinline__ void drain_stores(u32 bit, u32 npk) {
+    if ((UOCR_RUN_DRAIN & bit) && __builtin_amdgcn_readfirstlane(tid_() / 64u) * 64u < npk * NREP) {
+        __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */
+    }
+}
+
 __device__ __forceinline__ u32 pack2(h16 a, h16 b) {
     return (u32)__builtin_bit_cast(unsigned short, a) | ((u32)__builtin_bit_cast(unsigned short, b) << 16);
 }
@@ -736,6 +754,7 @@ __device__ bool qkv_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag,
     __syncthreads();
     TLD(l, 2u);
     publish(R, R.pk + off_qkv(l), PQKV, b * PQKV_B, PQKV_B, tag, [&](u32 p) { return pay6(S.outv, p, 16u); });
+    drain_stores(1u, PQKV_B);
     TLR(2u * (1u + 5u * l) + 1u);
     return true;
 }
@@ -918,6 +937,7 @@ __device__ bool att_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag,
     publish(R, R.pk + off_att(l), PATT, a * PATT_B, PATT_B, tag, [&](u32 q) {
         return q < PATT_B - 1u ? pay6(outa, q, HDIM) : make_uint3(__float_as_uint(mlo[0]), __float_as_uint(mlo[1]), 0u);
     });
+    drain_stores(2u, PATT_B);
     TLR(2u * (2u + 5u * l) + 1u);
     return true;
 }
@@ -1111,6 +1131,7 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
     __syncthreads();
     TLD(l, 8u);
     publish(R, R.pk + off_o(l), PO, j * PO_A, PO_A, tag, [&](u32 p) { return pay6(S.outv, p, O_ROWS); });
+    drain_stores(4u, PO_A);
     TLR(2u * (3u + 5u * l) + 1u);
     return true;
 }
@@ -1699,6 +1720,7 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     }
     __syncthreads();
     publish(R, R.pk + off_h(l), PH, b * PH_B, PH_B, tag, [&](u32 p) { return pay6(S.outv, p, DN_ROWS); });
+    drain_stores(16u, PH_B);
     TLR(2u * (5u + 5u * l) + 1u);
     return true;
 }
