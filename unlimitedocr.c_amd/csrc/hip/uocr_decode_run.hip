@@ -391,17 +391,20 @@ __device__ __forceinline__ void publish(const Run &R, uint4 *region, u32 per_cop
     }
 }
 
-/* UOCR_RUN_DRAIN (bit mask: 1 QKV, 2 ATT, 4 O rows, 16 DN): after that
+/* UOCR_RUN_DRAIN (bit mask: 1 QKV, 2 ATT, 4 O rows, 8 GU (Q8 instance),
+ * 16 DN, 32 z partials, 64 LM): after that
  * stage's publish, the storing wavefronts wait for their packet stores to
  * complete before issuing the next stage's loads; loads issued behind
  * device-coherent stores still in flight delay the packets' visibility.
  * Measured on config 5 (same box): 17 gives Q4 3,809-3,817 and Q8
  * 3,351-3,355 tok/s against 3,803 and 3,331 with none; adding ATT (19) the
  * same; adding the O rows (23) Q4 3,818-3,822 but Q8 3,335; the O rows
- * alone cost Q4 0.6%.  (The GU stage's publish is followed by the compiler's
+ * alone cost Q4 0.6%; GU (8) Q8 3,362 against 3,348 but Q4 -0.7%, so the
+ * Q8 instance only; z partials (32) Q4 -2.6%, Q8 -2.2%; LM (64) nothing.
+ * (The GU stage's publish is followed by the compiler's
  * own waits before the Q4 DN row loads; removing them cost Q4 0.6%.) */
 #ifndef UOCR_RUN_DRAIN
-#define UOCR_RUN_DRAIN 17
+#define UOCR_RUN_DRAIN 25
 #endif
 __device__ __forceinline__ void drain_stores(u32 bit, u32 npk) {
     if ((UOCR_RUN_DRAIN & bit) && __builtin_amdgcn_readfirstlane(tid_() / 64u) * 64u < npk * NREP) {
@@ -634,6 +637,7 @@ __device__ bool lm_stage(const Run &R, const Lds &S, u32 tag, u32 htag, int32_t 
     for (u32 w = 1; w < NT / 64u; ++w) k = S.keyw[w] > k ? S.keyw[w] : k;
     publish(R, R.pk + off_lm(), PLM, blockIdx.x, 1u, tag,
             [&](u32) { return make_uint3((u32)k, (u32)(k >> 32), 0u); });
+    drain_stores(64u, 1u);
     TLR(1u);
     return true;
 }
@@ -1110,6 +1114,7 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
             return make_uint3(__float_as_uint(S.zout[z0]), __float_as_uint(z0 + 1u < NEXP ? S.zout[z0 + 1u] : 0.0f),
                               __float_as_uint(z0 + 2u < NEXP ? S.zout[z0 + 2u] : 0.0f));
         });
+        drain_stores(32u, PO_Z);
     }
     float part[G::RPG];
 #pragma unroll
@@ -1595,6 +1600,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         }
         return v;
     });
+    drain_stores(dn_in_lds<QF>() ? 8u : 0u, PMID_B); /* Q8 only: Q4 -0.7% */
     TLD(l, 19u);
     if (!UOCR_RUN_DN_EARLY) {
         /* the DN rows after this stage's own loads are consumed */
