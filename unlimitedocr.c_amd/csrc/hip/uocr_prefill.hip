@@ -705,16 +705,26 @@ __device__ __forceinline__ u32 fa_tile_base(u32 qt, u32 ch) {
     return b;
 }
 
+/* Wavefront w owns queries q0 + 16w .. + 15 of the block's 64 and keeps
+ * everything of them in registers (16x16x32 MFMAs):
+ *   S^T = K Q^T per key tile: four 16-key tiles; lane l holds query l % 16
+ *   and keys 16t + 4(l / 16) + i (i < 4) of tile t;
+ *   the fp32 online softmax per query, its max reduced over the four lanes
+ *   that share the query (l, l ^ 16, l ^ 32, l ^ 48), its sum kept per lane
+ *   and reduced once at the end;
+ *   O^T = V^T P^T: the probabilities stay where S^T left them, because the
+ *   B operand's 8 K slots of lane l are chosen as keys {32u + 4(l / 16) + i,
+ *   32u + 16 + 4(l / 16) + i} (i < 4) and the A operand (V^T from LDS) is
+ *   read at the same keys; lane l holds dims 16d + 4(l / 16) + i of query
+ *   l % 16 in O^T tile d.
+ * Only the K and V^T tiles go through LDS (two barriers per key tile). */
 __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, const h16 *__restrict__ kc,
                                                    const h16 *__restrict__ vc, u32 cap, u32 P,
                                                    h16 *__restrict__ ctx, u32 ch, float *__restrict__ part) {
-    __shared__ __attribute__((aligned(16))) h16 qs[AQ * LDQ];
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
     __shared__ __attribute__((aligned(16))) h16 ks[AK * LDQ];
     __shared__ __attribute__((aligned(16))) h16 vt[UOCR_K_HEAD_DIM * LDV];
-    __shared__ float sS[AQ][AK + 1];
-    __shared__ __attribute__((aligned(16))) h16 ps[AQ * LDV];
-    __shared__ float rowm[AQ], rowl[AQ], rowc[AQ];
-    const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const u32 t = threadIdx.x, lane = t & 63u, wave = t >> 6, qc = lane & 15u, g = lane >> 4;
     /* which (query tile, head, key chunk) this block computes */
     u32 qt = blockIdx.x, h = blockIdx.y, sp = 0, ns = 1;
     if (ch != 0u) {
@@ -731,24 +741,18 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
     const u32 q0 = qt * AQ;
     const h16 *kh = kc + (size_t)h * cap * 128u, *vh = vc + (size_t)h * cap * 128u;
     const float scale = 0.08838834764831845f;
-
-    /* Q tile */
+    /* this lane's query row: B operand pieces of Q^T for the four 32-deep
+     * steps over the head dimension */
+    const u32 qr = q0 + 16u * wave + qc; /* query index */
+    U4H8 qreg[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const u32 idx = t + q * PB, r = idx >> 4, c8 = idx & 15u;
-        const u32 qr = min(q0 + r, P - 1u);
-        *(uint4 *)(qs + r * LDQ + 8u * c8) = *(const uint4 *)(Q + (size_t)qr * UOCR_K_HIDDEN + h * 128u + 8u * c8);
+    for (int st = 0; st < 4; ++st) {
+        qreg[st].u = *(const uint4 *)(Q + (size_t)min(qr, P - 1u) * UOCR_K_HIDDEN + h * 128u + 32u * st + 8u * g);
     }
-    if (t < AQ) {
-        rowm[t] = -INFINITY;
-        rowl[t] = 0.0f;
-    }
-    f32x16 o[2];
+    f32x4 o[UOCR_K_HEAD_DIM / 16];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[j][i] = 0.0f;
-    const u32 wm = wave & 1u, wn = wave >> 1;
+    for (int d = 0; d < UOCR_K_HEAD_DIM / 16; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
     const u32 qlast = min(q0 + AQ, P) - 1u;
     /* this block's keys: tiles [sp * ch, (sp + 1) * ch) of the causal range */
     const u32 kbeg = ch != 0u ? sp * ch * AK : 0u;
@@ -806,101 +810,86 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
         }
         __syncthreads();
         if (k0 + AK <= klast) load_kv(k0 + AK);
-        /* S = Q K^T: wave (wm, wn) computes rows 32wm.., keys 32wn.. */
-        {
-            f32x16 s;
+        /* S^T: four 16-key tiles x this wavefront's 16 queries */
+        float sc[4][4];
+        float tm = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+        for (int kt = 0; kt < 4; ++kt) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (u32 kk = 0; kk < UOCR_K_HEAD_DIM; kk += 16) {
-                U4H8 a, b;
-                a.u = *(const uint4 *)(qs + (32u * wm + (lane & 31u)) * LDQ + kk + 8u * (lane >> 5));
-                b.u = *(const uint4 *)(ks + (32u * wn + (lane & 31u)) * LDQ + kk + 8u * (lane >> 5));
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.v, b.v, s, 0, 0, 0);
+            for (int st = 0; st < 4; ++st) {
+                U4H8 a;
+                a.u = *(const uint4 *)(ks + (16u * kt + qc) * LDQ + 32u * st + 8u * g);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, qreg[st].v, acc, 0, 0, 0);
             }
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const u32 r = 32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4), c = 32u * wn + (lane & 31u);
-                const u32 qi = q0 + r, ki = k0 + c;
-                sS[r][c] = (ki <= qi && ki < P) ? s[i] * scale : -INFINITY;
-            }
-        }
-        __syncthreads();
-        /* online softmax: 4 threads per row, 16 keys each */
-        {
-            const u32 r = t >> 2, part = t & 3u;
-            float mx = -INFINITY;
-#pragma unroll
-            for (int c = 0; c < 16; ++c) mx = fmaxf(mx, sS[r][16u * part + c]);
-            mx = fmaxf(mx, __shfl_xor(mx, 1));
-            mx = fmaxf(mx, __shfl_xor(mx, 2));
-            const float mold = rowm[r], mnew = fmaxf(mold, mx);
-            float sum = 0.0f;
-            U4H8 pv[2];
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const float v = sS[r][16u * part + c];
-                const float e = v == -INFINITY ? 0.0f : expf(v - mnew);
-                sum += e;
-                pv[c >> 3].h[c & 7] = (h16)e;
-            }
-            /* the row's 16 probabilities as two 16-byte stores */
-            *(uint4 *)(ps + r * LDV + 16u * part) = pv[0].u;
-            *(uint4 *)(ps + r * LDV + 16u * part + 8u) = pv[1].u;
-            sum += __shfl_xor(sum, 1);
-            sum += __shfl_xor(sum, 2);
-            __syncthreads();
-            if (part == 0u) {
-                const float corr = mold == -INFINITY ? 0.0f : expf(mold - mnew);
-                rowc[r] = corr;
-                rowl[r] = rowl[r] * corr + sum;
-                rowm[r] = mnew;
+            for (int i = 0; i < 4; ++i) {
+                const u32 ki = k0 + 16u * kt + 4u * g + i;
+                const float v = (ki <= qr && ki < P) ? acc[i] * scale : -INFINITY;
+                sc[kt][i] = v;
+                tm = fmaxf(tm, v);
             }
         }
-        __syncthreads();
-        /* O = O * corr + P V: wave (wm, wn) owns rows 32wm.., dims 64wn.. */
+        tm = fmaxf(tm, __shfl_xor(tm, 16));
+        tm = fmaxf(tm, __shfl_xor(tm, 32));
+        const float mnew = fmaxf(m, tm);
+        /* every query sees key k0 (k0 <= q0 <= q), so mnew is finite */
+        const float corr = m == -INFINITY ? 0.0f : expf(m - mnew);
+        l *= corr;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int d = 0; d < UOCR_K_HEAD_DIM / 16; ++d) o[d] *= corr;
+        m = mnew;
+        /* probabilities in fp16, two B operands of 8 keys */
+        U4H8 pb[2];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[j][i] *= rowc[32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4)];
+        for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = sc[kt][i] == -INFINITY ? 0.0f : expf(sc[kt][i] - mnew);
+                l += e;
+                pb[kt >> 1].h[4 * (kt & 1) + i] = (h16)e;
+            }
         }
+        /* O^T += V^T P^T */
 #pragma unroll
-        for (u32 kk = 0; kk < AK; kk += 16) {
-            U4H8 a;
-            a.u = *(const uint4 *)(ps + (32u * wm + (lane & 31u)) * LDV + kk + 8u * (lane >> 5));
+        for (int u = 0; u < 2; ++u) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                U4H8 b;
-                b.u = *(const uint4 *)(vt + (64u * wn + 32u * j + (lane & 31u)) * LDV + kk + 8u * (lane >> 5));
-                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a.v, b.v, o[j], 0, 0, 0);
+            for (int d = 0; d < UOCR_K_HEAD_DIM / 16; ++d) {
+                const h16 *vr = vt + (16u * d + qc) * LDV + 32u * u + 4u * g;
+                U4H8 a;
+                const uint2 lo = *(const uint2 *)vr, hi = *(const uint2 *)(vr + 16);
+                a.u = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, pb[u].v, o[d], 0, 0, 0);
             }
         }
     }
-    __syncthreads();
+    /* the query's sum over its four lanes */
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const u32 r = 16u * wave + qc; /* row within the tile */
     if (ns > 1u) {
         /* partial of a split tile: unnormalised O, row max and row sum */
         float *po = part + (size_t)blockIdx.x * FA_PART_FLOATS;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const u32 r = 32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4);
-                po[r * UOCR_K_HEAD_DIM + 64u * wn + 32u * j + (lane & 31u)] = o[j][i];
-            }
+        for (int d = 0; d < UOCR_K_HEAD_DIM / 16; ++d) {
+            *(float4 *)(po + r * UOCR_K_HEAD_DIM + 16u * d + 4u * g) = make_float4(o[d][0], o[d][1], o[d][2], o[d][3]);
         }
-        if (t < AQ) {
-            po[AQ * UOCR_K_HEAD_DIM + t] = rowm[t];
-            po[AQ * UOCR_K_HEAD_DIM + AQ + t] = rowl[t];
+        if (g == 0u) {
+            po[AQ * UOCR_K_HEAD_DIM + r] = m;
+            po[AQ * UOCR_K_HEAD_DIM + AQ + r] = l;
         }
         return;
     }
+    if (qr < P) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+        for (int d = 0; d < UOCR_K_HEAD_DIM / 16; ++d) {
+            union {
+                h16 hh[4];
+                uint2 u;
+            } pk;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const u32 r = 32u * wm + 8u * (i / 4) + 4u * (lane >> 5) + (i % 4);
-            const u32 d = 64u * wn + 32u * j + (lane & 31u);
-            if (q0 + r < P) ctx[(size_t)(q0 + r) * UOCR_K_HIDDEN + h * 128u + d] = (h16)(o[j][i] / rowl[r]);
+            for (int i = 0; i < 4; ++i) pk.hh[i] = (h16)(o[d][i] / l);
+            *(uint2 *)(ctx + (size_t)qr * UOCR_K_HIDDEN + h * 128u + 16u * d + 4u * g) = pk.u;
         }
     }
 }
@@ -1406,7 +1395,9 @@ extern "C" hipError_t uocr_launch_rope_scatter(hipStream_t st, const uint16_t *q
  * per CU).  The key chunk is the smallest whose (tile, head, chunk) blocks
  * all fit at once; the longest block then walks ch key tiles instead of all
  * of the last query tile's.  0: one block per (tile, head), no split. */
+#ifndef FA_SLOTS
 #define FA_SLOTS 512u
+#endif
 
 static u32 fa_chunk(u32 P) {
     const u32 nq = (P + AQ - 1u) / AQ;
