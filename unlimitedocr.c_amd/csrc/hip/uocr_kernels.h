@@ -90,6 +90,14 @@ hipError_t uocr_launch_rmsnorm(hipStream_t st, const uint16_t *x, const uint16_t
 hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
                                 const uint16_t *nw, const uocr_step_state *state, uint16_t *qout, uint16_t *kcache,
                                 uint16_t *vcache, uint32_t cache_capacity);
+/* uocr_launch_qkv_rope for decode step t after a prompt_len-token prompt
+ * without a step state prepared beforehand: the launch computes the KV slot
+ * and RoPE of that step itself (uocr_launch_decode_state's arithmetic, with
+ * inv_freq [64]) and writes the step state for the attention launch after it. */
+hipError_t uocr_launch_qkv_rope_plan(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
+                                     const uint16_t *nw, uocr_step_state *state, uint16_t *qout, uint16_t *kcache,
+                                     uint16_t *vcache, uint32_t cache_capacity, int32_t prompt_len, int32_t t,
+                                     const float *inv_freq);
 /* Split-K decode attention over the live slots [0, state->attn_len) of one
  * layer's caches (UOCR_K_ATTN_SPLITS blocks per head, slots partitioned by
  * cache_capacity): writes UOCR_ATTN_PARTIAL_FLOATS of per-split partials.

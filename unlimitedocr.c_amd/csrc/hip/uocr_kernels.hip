@@ -351,11 +351,68 @@ __device__ __forceinline__ uint4 embed_piece(const SelArgs &sa, int32_t tok, u32
  * group computes rows h*128+d and h*128+d+64 of matrix m, rounds them to
  * fp16, rotates q/k by the split-half RoPE at st->pos and stores q, or k/v
  * into the cache slot st->cache_token.  One item per lane group. */
-template <int QT, int QE>
+/* The step plan a standalone attention-block call computes in its QKV
+ * launch instead of a separate plan launch: decode step t after a P-token
+ * prompt (k_decode_state's arithmetic). */
+struct QkvPlan {
+    int32_t P, t;
+    uocr_step_state *st;
+    RopeTab tab;
+};
+
+/* The plan as a kernel argument only where it is used. */
+template <bool PLAN>
+struct PlanArg {
+    char none;
+};
+template <>
+struct PlanArg<true> {
+    QkvPlan p;
+};
+
+/* Slot, cos and sin of pair d for the QKV stores: from the step state, or
+ * (PLAN) computed from the plan, whose step state block 0 also writes. */
+template <bool PLAN>
+__device__ __forceinline__ void qkv_slot(const uocr_step_state *__restrict__ st, const QkvPlan &pl, u32 d, u32 &ct,
+                                         float &cs, float &sn) {
+    if (PLAN) {
+        const int32_t pos = pl.P + pl.t;
+        ct = (u32)(pl.P + (pl.t % UOCR_K_RING));
+        const float ang = (float)pos * pl.tab.f[d];
+        cs = cosf(ang);
+        sn = sinf(ang);
+        if (blockIdx.x == 0u) {
+            uocr_step_state *sw = pl.st;
+            if (threadIdx.x < UOCR_K_HEAD_DIM / 2) {
+                const float a2 = (float)pos * pl.tab.f[threadIdx.x];
+                sw->rope_cos[threadIdx.x] = cosf(a2);
+                sw->rope_sin[threadIdx.x] = sinf(a2);
+            }
+            if (threadIdx.x == 0) {
+                const int32_t gcount = pl.t + 1;
+                const int32_t live = gcount < UOCR_K_RING ? gcount : UOCR_K_RING;
+                sw->t = pl.t;
+                sw->prompt_len = pl.P;
+                sw->pos = pos;
+                sw->cache_token = (int32_t)ct;
+                sw->attn_prompt = pl.P;
+                sw->attn_len = pl.P + live;
+                sw->first_gen = gcount - live;
+            }
+        }
+    } else {
+        ct = (u32)st->cache_token;
+        cs = st->rope_cos[d];
+        sn = st->rope_sin[d];
+    }
+}
+
+template <int QT, int QE, bool PLAN = false>
 __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat Km, uocr_qmat V, const h16 *__restrict__ hin,
                                                     const h16 *__restrict__ nw,
                                                     const uocr_step_state *__restrict__ st, h16 *__restrict__ qout,
-                                                    h16 *__restrict__ kc, h16 *__restrict__ vc, u32 cap, SelArgs sa) {
+                                                    h16 *__restrict__ kc, h16 *__restrict__ vc, u32 cap, SelArgs sa,
+                                                    PlanArg<PLAN> pa) {
     TL(1);
     constexpr u32 K = UOCR_K_HIDDEN, C = chunks_per_row<QT>(K), LPR = lpr_lat(C), J = j_lat(C), R = 64u / LPR;
     constexpr u32 rb = 16u * C, G = K / 64u;
@@ -381,8 +438,16 @@ __global__ __launch_bounds__(SMALL_BLOCK) void k_qkv_rope(uocr_qmat Q, uocr_qmat
     RowFrag<J> fa, fb;
     frag_load<QT, LPR, J, UOCR_ATT_W_NT>(fa, (const uint8_t *)M.w + (size_t)ra * rb, (const h16 *)M.s + (size_t)ra * G, C, sub);
     frag_load<QT, LPR, J, UOCR_ATT_W_NT>(fb, (const uint8_t *)M.w + (size_t)rbw * rb, (const h16 *)M.s + (size_t)rbw * G, C, sub);
-    const u32 ct = (u32)st->cache_token;
-    const float cs = st->rope_cos[d], sn = st->rope_sin[d];
+    u32 ct;
+    float cs, sn;
+    {
+        if constexpr (PLAN) {
+            qkv_slot<true>(st, pa.p, d, ct, cs, sn);
+        } else {
+            QkvPlan none{};
+            qkv_slot<false>(st, none, d, ct, cs, sn);
+        }
+    }
     if (QE != 0) {
         asm volatile("" : "+v"(key)::"memory");
         float b;
@@ -1289,7 +1354,23 @@ static void launch_qkv_qe(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V,
     constexpr u32 R = 64u / lpr_lat(chunks_per_row<QT>(UOCR_K_HIDDEN));
     constexpr u32 ipb = (SMALL_BLOCK / 64) * R;
     hipLaunchKernelGGL((k_qkv_rope<QT, QE>), dim3((1920u + ipb - 1u) / ipb), dim3(SMALL_BLOCK), 0, st, Q, K, V,
-                       (const h16 *)h, (const h16 *)nw, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap, sa);
+                       (const h16 *)h, (const h16 *)nw, state, (h16 *)qout, (h16 *)kc, (h16 *)vc, cap, sa,
+                       PlanArg<false>{});
+}
+
+template <int QT>
+static void launch_qkv_plan_qt(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V, const uint16_t *h,
+                               const uint16_t *nw, uocr_step_state *state, uint16_t *qout, uint16_t *kc,
+                               uint16_t *vc, u32 cap, const QkvPlan &pl) {
+    constexpr u32 R = 64u / lpr_lat(chunks_per_row<QT>(UOCR_K_HIDDEN));
+    constexpr u32 ipb = (SMALL_BLOCK / 64) * R;
+    SelArgs sa;
+    memset(&sa, 0, sizeof(sa));
+    PlanArg<true> pa;
+    pa.p = pl;
+    hipLaunchKernelGGL((k_qkv_rope<QT, 0, true>), dim3((1920u + ipb - 1u) / ipb), dim3(SMALL_BLOCK), 0, st, Q, K, V,
+                       (const h16 *)h, (const h16 *)nw, (const uocr_step_state *)state, (h16 *)qout, (h16 *)kc,
+                       (h16 *)vc, cap, sa, pa);
 }
 
 template <int QT>
@@ -1315,6 +1396,27 @@ extern "C" hipError_t uocr_launch_qkv_rope(hipStream_t st, uocr_qmat Q, uocr_qma
     SelArgs sa;
     memset(&sa, 0, sizeof(sa));
     DISPATCH_QT(Q.qtype, launch_qkv_qt, st, Q, K, V, h, nw, state, qout, kcache, vcache, cache_capacity, sa, 0u);
+    return hipGetLastError();
+}
+
+static RopeTab rope_tab(const float *inv_freq);
+
+extern "C" hipError_t uocr_launch_qkv_rope_plan(hipStream_t st, uocr_qmat Q, uocr_qmat K, uocr_qmat V,
+                                                const uint16_t *h, const uint16_t *nw, uocr_step_state *state,
+                                                uint16_t *qout, uint16_t *kcache, uint16_t *vcache,
+                                                uint32_t cache_capacity, int32_t prompt_len, int32_t t,
+                                                const float *inv_freq) {
+    if (!mat_ok(Q) || !mat_ok(K) || !mat_ok(V) || Q.qtype != K.qtype || Q.qtype != V.qtype || h == nullptr ||
+        nw == nullptr || state == nullptr || qout == nullptr || kcache == nullptr || vcache == nullptr ||
+        cache_capacity == 0u || inv_freq == nullptr || prompt_len <= 0 || t < 0) {
+        return hipErrorInvalidValue;
+    }
+    QkvPlan pl;
+    pl.P = prompt_len;
+    pl.t = t;
+    pl.st = state;
+    pl.tab = rope_tab(inv_freq);
+    DISPATCH_QT(Q.qtype, launch_qkv_plan_qt, st, Q, K, V, h, nw, state, qout, kcache, vcache, cache_capacity, pl);
     return hipGetLastError();
 }
 

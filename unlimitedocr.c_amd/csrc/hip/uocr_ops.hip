@@ -221,11 +221,17 @@ static void rope_inv_freq(float *invf) {
     for (int d = 0; d < UOCR_K_HEAD_DIM / 2; ++d) invf[d] = exp2f((float)d * freq_scale);
 }
 
-static int set_plan(hipStream_t st, void *workspace, uint32_t cap, uint32_t P, uint32_t g) {
+static int plan_ok(uint32_t cap, uint32_t P, uint32_t g) {
     if (P == 0u || (uint64_t)P + (g < UOCR_K_RING ? g : UOCR_K_RING) > cap) {
         return op_fail(UOCR_ERROR_INVALID_ARGUMENT, "attention plan (prompt %u, generated %u) exceeds cache capacity %u", P,
                        g, cap);
     }
+    return UOCR_OK;
+}
+
+static int set_plan(hipStream_t st, void *workspace, uint32_t cap, uint32_t P, uint32_t g) {
+    const int r = plan_ok(cap, P, g);
+    if (r != UOCR_OK) return r;
     float invf[UOCR_K_HEAD_DIM / 2];
     rope_inv_freq(invf);
     uocr_step_state *state = ws<uocr_step_state>(workspace, WS_STATE);
@@ -278,11 +284,16 @@ extern "C" int uocr_op_attention_block(uint32_t qtype, const void *wq, const voi
     STREAM_OR_RETURN(st);
     uocr_step_state *state = ws<uocr_step_state>(workspace, WS_STATE);
     uint16_t *qb = ws<uint16_t>(workspace, WS_Q), *cb = ws<uint16_t>(workspace, WS_CTX);
-    int r = set_plan(st, workspace, cache_capacity, prompt_length, generated_count);
+    /* the step plan (slot, RoPE, attention length) is computed by the QKV
+     * launch itself: one launch fewer than a separate plan kernel */
+    int r = plan_ok(cache_capacity, prompt_length, generated_count);
     if (r == UOCR_OK) {
-        r = hip_status(uocr_launch_qkv_rope(st, qm(qtype, wq, sq), qm(qtype, wk, sk), qm(qtype, wv, sv),
-                                            (const uint16_t *)hidden, (const uint16_t *)norm_w, state, qb,
-                                            (uint16_t *)k_cache, (uint16_t *)v_cache, cache_capacity),
+        float invf[UOCR_K_HEAD_DIM / 2];
+        rope_inv_freq(invf);
+        r = hip_status(uocr_launch_qkv_rope_plan(st, qm(qtype, wq, sq), qm(qtype, wk, sk), qm(qtype, wv, sv),
+                                                 (const uint16_t *)hidden, (const uint16_t *)norm_w, state, qb,
+                                                 (uint16_t *)k_cache, (uint16_t *)v_cache, cache_capacity,
+                                                 (int32_t)prompt_length, (int32_t)generated_count - 1, invf),
                        "qkv_rope");
     }
     if (r == UOCR_OK) {
