@@ -103,7 +103,14 @@ constexpr u32 HID = UOCR_K_HIDDEN, HDIM = UOCR_K_HEAD_DIM, NHEAD = UOCR_K_HEADS,
 constexpr u32 TOPK = UOCR_K_TOPK, EI = 896u, SI = 1792u, DI = 6848u, VOCAB = 129280u, RING = UOCR_K_RING;
 
 constexpr u32 QKV_BLOCKS = 240u;  /* 1920 items / 8 */
-constexpr u32 ATT_SPLITS = 8u, ATT_BLOCKS = NHEAD * ATT_SPLITS, ATT0 = NB - ATT_BLOCKS;
+#ifndef UOCR_RUN_ATT_SPLITS
+#define UOCR_RUN_ATT_SPLITS 8u
+#endif
+constexpr u32 ATT_SPLITS = UOCR_RUN_ATT_SPLITS, ATT_BLOCKS = NHEAD * ATT_SPLITS, ATT0 = NB - ATT_BLOCKS;
+/* the stages' LDS scratch: the O stage's attention partials at most */
+constexpr u32 SCR_BYTES = ATT_BLOCKS * 128u * 2u + ATT_BLOCKS * 12u + 512u * 4u > 24576u
+                              ? ((ATT_BLOCKS * 128u * 2u + ATT_BLOCKS * 12u + 512u * 4u + 255u) & ~255u)
+                              : 24576u;
 constexpr u32 O_BLOCKS = 40u, O_ROWS = 32u, O0 = ATT0 - O_BLOCKS;
 #ifndef UOCR_RUN_Z_BLOCKS
 #define UOCR_RUN_Z_BLOCKS 16u
@@ -1019,6 +1026,7 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
     float *ml = (float *)(S.scr + ATT_BLOCKS * HDIM * 2u); /* [80][2] */
     float *wk = ml + 2u * ATT_BLOCKS;                     /* [80] */
     float *zq = wk + ATT_BLOCKS;                          /* [NT / 64][64] */
+    static_assert(ATT_BLOCKS * HDIM * 2u + ATT_BLOCKS * 12u + NT * 4u <= SCR_BYTES, "O stage LDS");
     if (!gather<(PATT + NT - 1) / NT>(R, R.pk + off_att(l), PATT, PATT, tag, W_O, (u32)t, [](u32 i) { return i; },
                                       [&](u32 i, uint4 v) {
                                           const u32 a = i / PATT_B, k = i % PATT_B;
@@ -1631,7 +1639,7 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     u32 sel[TOPK];
 #pragma unroll
     for (u32 r = 0; r < TOPK; ++r) sel[r] = moe ? __builtin_amdgcn_readfirstlane(S.selid[r]) : 0u;
-    static_assert((TOPK * EI + SI) * 2u + NB * 4u <= 24576u, "DN LDS");
+    static_assert((TOPK * EI + SI) * 2u + NB * 4u <= SCR_BYTES, "DN LDS");
     if (!gather<(PMID + NT - 1u) / NT>(R, R.pk + off_mid(l), PMID, PMID, tag, W_DN, (u32)t, [](u32 i) { return i; },
                         [&](u32 i, uint4 v) {
                             const u32 blk = i / PMID_B, k = i % PMID_B, base = mid_base(blk, moe) + 6u * k;
@@ -1754,7 +1762,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
     __shared__ __attribute__((aligned(16))) h16 xs[HID];
     __shared__ __attribute__((aligned(16))) h16 hres[HID];
     __shared__ __attribute__((aligned(16))) h16 outv[64];
-    __shared__ __attribute__((aligned(16))) uint8_t scr[24576];
+    __shared__ __attribute__((aligned(16))) uint8_t scr[SCR_BYTES];
     __shared__ float red[16], zout[64], selw[8];
     __shared__ __attribute__((aligned(16))) float zw[2u * Z_COLS * NEXP];
     __shared__ u32 selid[8];
