@@ -112,8 +112,12 @@ constexpr u32 SCR_BYTES = ATT_BLOCKS * 128u * 2u + ATT_BLOCKS * 12u + 512u * 4u 
                               ? ((ATT_BLOCKS * 128u * 2u + ATT_BLOCKS * 12u + 512u * 4u + 255u) & ~255u)
                               : 24576u;
 constexpr u32 O_BLOCKS = 40u, O_ROWS = 32u, O0 = ATT0 - O_BLOCKS;
+/* O blocks that also publish z partials.  Measured on config 5 (same box,
+ * with the store drains): 20 Q4 3,860-3,862 and Q8 3,355-3,361 tok/s
+ * against 16 3,812-3,814 and 3,366-3,368, 10 3,794 and 3,354-3,356 (8 and
+ * 32, before the drains: both slower than 16). */
 #ifndef UOCR_RUN_Z_BLOCKS
-#define UOCR_RUN_Z_BLOCKS 16u
+#define UOCR_RUN_Z_BLOCKS 20u
 #endif
 constexpr u32 Z_BLOCKS = UOCR_RUN_Z_BLOCKS, Z_COLS = HID / Z_BLOCKS; /* O blocks j < Z_BLOCKS also publish z partials */
 constexpr u32 GU_ROUTED = 192u, GU_ROWS = 28u, DGU_ROWS = 27u;
@@ -134,6 +138,7 @@ static_assert(O0 >= 0u && O0 + O_BLOCKS <= QKV_BLOCKS, "O blocks also gather h i
 constexpr u32 PQKV_B = 3u, PQKV = QKV_BLOCKS * PQKV_B;
 constexpr u32 PATT_B = 23u, PATT = ATT_BLOCKS * PATT_B;
 constexpr u32 PO_A = (O_ROWS + 5u) / 6u, PO_Z = 22u, PO_AR = O_BLOCKS * PO_A, PO = PO_AR + Z_BLOCKS * PO_Z;
+static_assert(Z_BLOCKS * PO_Z <= NT && HID % Z_BLOCKS == 0u, "the GU stage gathers the z packets one per thread");
 constexpr u32 PMID_B = 5u, PMID = NB * PMID_B;
 constexpr u32 PH_B = 2u, PH = DN_BLOCKS * PH_B;
 constexpr u32 PLM = NB;
@@ -1414,7 +1419,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     const u32 b = blockIdx.x, grp = tid_() / G::LPR, sub = tid_() % G::LPR;
     const bool moe = l > 0u;
     const SlabD sd = moe ? slab_of(L) : SlabD{};
-    float *zpart = (float *)S.scr; /* [16][64] */
+    float *zpart = (float *)S.scr; /* [Z_BLOCKS][64] */
     h16 *hres = S.hres;
     const uint4 nwp = norm_piece(L.post_norm);
     auto gather_a = [&]() {
@@ -1461,10 +1466,10 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
          * chosen and ahead of the expert loads */
         uint4 *stg = (uint4 *)(S.scr + 8192u);
         gather_wave_issue<(PO_AR + 63u) / 64u>(R, R.pk + off_o(l), PO, PO_AR, NT / 64u - 1u, stg, [](u32 i) { return i; });
-        /* wavefront 0: z of expert e (lane e) over the 16 partials in a fixed
+        /* wavefront 0: z of expert e (lane e) over the Z_BLOCKS partials in a fixed
          * order, then the top-6 */
         TLD(l, 18u);
-        /* every wavefront sums z (lane e: expert e, the 16 partials in a fixed
+        /* every wavefront sums z (lane e: expert e, the Z_BLOCKS partials in a fixed
          * order) and takes the top-6 itself, so each issues its expert rows
          * without a barrier; wavefront 0 also leaves the ids in LDS for the
          * later readers (behind the barrier after the gather of a) */
