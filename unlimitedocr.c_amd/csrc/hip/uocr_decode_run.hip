@@ -111,7 +111,11 @@ constexpr u32 ATT_SPLITS = UOCR_RUN_ATT_SPLITS, ATT_BLOCKS = NHEAD * ATT_SPLITS,
 constexpr u32 SCR_BYTES = ATT_BLOCKS * 128u * 2u + ATT_BLOCKS * 12u + 512u * 4u > 24576u
                               ? ((ATT_BLOCKS * 128u * 2u + ATT_BLOCKS * 12u + 512u * 4u + 255u) & ~255u)
                               : 24576u;
-constexpr u32 O_BLOCKS = 40u, O_ROWS = 32u, O0 = ATT0 - O_BLOCKS;
+#ifndef UOCR_RUN_O_BLOCKS
+#define UOCR_RUN_O_BLOCKS 40u
+#endif
+constexpr u32 O_BLOCKS = UOCR_RUN_O_BLOCKS, O_ROWS = HID / O_BLOCKS, O0 = ATT0 - O_BLOCKS;
+static_assert(O_ROWS * O_BLOCKS == HID, "O rows split evenly");
 /* O blocks that also publish z partials.  Measured on config 5 (same box,
  * with the store drains): 20 Q4 3,860-3,862 and Q8 3,355-3,361 tok/s
  * against 16 3,812-3,814 and 3,366-3,368, 10 3,794 and 3,354-3,356 (8 and
@@ -1410,7 +1414,7 @@ __device__ __forceinline__ void dd_load(const Run &R, const Lds &S, DnFrags<QF> 
  * MoE layers also issue the DN stage's loads (dn) once the experts are known. */
 #define UOCR_RUN_DN_EARLY dn_in_lds<QF>()
 #ifndef UOCR_RUN_WAVE_TOPK
-#define UOCR_RUN_WAVE_TOPK (QF == 4) /* Q8: 3,180 against 3,196 tok/s with it */
+#define UOCR_RUN_WAVE_TOPK 1 /* Q8 with 20 z blocks and the store drains: 3,363-3,366 against 3,351-3,353 without it (before them: 3,196 against 3,180) */
 #endif
 template <int QF>
 __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, GuFrags<QF> &F, DnFrags<QF> &dn) {
