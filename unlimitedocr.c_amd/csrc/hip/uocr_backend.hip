@@ -1060,17 +1060,19 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         dd.w_stride = L.slab.dn_w_stride;
         dd.s_stride = L.slab.dn_s_stride;
         dd.a_idx = c->p_list_pair;
-        dd.out = c->p_y;
+        /* per-pair expert outputs in fp16, as the reference keeps them */
+        uint16_t *y16 = (uint16_t *)c->p_y;
+        dd.out = y16;
         dd.ldo = H_SIZE;
         if (sd_down) {
-            ENQ(uocr_launch_gemm_pair(s, UOCR_GEMM_F16, &dsd, UOCR_GEMM_F32, &dd));
+            ENQ(uocr_launch_gemm_pair(s, UOCR_GEMM_F16, &dsd, UOCR_GEMM_F16, &dd));
         } else {
-            ENQ(uocr_launch_gemm(s, UOCR_GEMM_F32, &dd));
+            ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &dd));
         }
         if (next_norm != nullptr) {
-            ENQ(uocr_launch_moe_combine_norm(s, c->p_y, c->p_wts, c->p_sout, c->p_a, P, H, next_norm, c->p_xn));
+            ENQ(uocr_launch_moe_combine_norm_h(s, y16, c->p_wts, c->p_sout, c->p_a, P, H, next_norm, c->p_xn));
         } else {
-            ENQ(uocr_launch_moe_combine(s, c->p_y, c->p_wts, c->p_sout, c->p_a, P, H));
+            ENQ(uocr_launch_moe_combine_h(s, y16, c->p_wts, c->p_sout, c->p_a, P, H));
         }
     }
     return hipMemcpyAsync(c->h, H + (size_t)(P - 1u) * H_SIZE, H_SIZE * 2u, hipMemcpyDeviceToDevice, s);

@@ -305,6 +305,12 @@ hipError_t uocr_launch_moe_combine_norm(hipStream_t st, const float *Y, const fl
                                         uint16_t *norm_out);
 hipError_t uocr_launch_moe_combine(hipStream_t st, const float *Y, const float *wts, const uint16_t *shared,
                                    const uint16_t *res, uint32_t P, uint16_t *out);
+/* The same two with fp16 per-pair outputs Y. */
+hipError_t uocr_launch_moe_combine_norm_h(hipStream_t st, const uint16_t *Y, const float *wts, const uint16_t *shared,
+                                          const uint16_t *res, uint32_t P, uint16_t *out, const uint16_t *norm_w,
+                                          uint16_t *norm_out);
+hipError_t uocr_launch_moe_combine_h(hipStream_t st, const uint16_t *Y, const float *wts, const uint16_t *shared,
+                                     const uint16_t *res, uint32_t P, uint16_t *out);
 
 #ifdef __cplusplus
 }

@@ -1070,7 +1070,21 @@ __global__ __launch_bounds__(BUCKET_THREADS) void k_bucket_build(const int32_t *
 
 /* h[t] = f16(sum_r w[t][r] * Y[t*6+r] + shared[t] + res[t]) (decode_gemv_q4.
  * metal:185-224 order: routed sum in fp32, shared already fp16). */
-__global__ __launch_bounds__(PB) void k_moe_combine(const float *__restrict__ Y, const float *__restrict__ wts,
+/* the per-pair expert outputs as fp32 (operator API) or fp16 (the prefill,
+ * rounded as the reference keeps them) */
+__device__ __forceinline__ void y_load8(const float *yr, float (&e)[8]) {
+    const float4 a = *(const float4 *)yr, b = *(const float4 *)(yr + 4);
+    e[0] = a.x; e[1] = a.y; e[2] = a.z; e[3] = a.w; e[4] = b.x; e[5] = b.y; e[6] = b.z; e[7] = b.w;
+}
+__device__ __forceinline__ void y_load8(const h16 *yr, float (&e)[8]) {
+    U4H8 v;
+    v.u = *(const uint4 *)yr;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = (float)v.h[j];
+}
+
+template <typename YT>
+__global__ __launch_bounds__(PB) void k_moe_combine(const YT *__restrict__ Y, const float *__restrict__ wts,
                                                     const h16 *__restrict__ shared, const h16 *__restrict__ res, u32 P,
                                                     h16 *__restrict__ out) {
     const u32 idx = blockIdx.x * PB + threadIdx.x;
@@ -1079,7 +1093,7 @@ __global__ __launch_bounds__(PB) void k_moe_combine(const float *__restrict__ Y,
     float acc = 0.0f;
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) {
-        acc = fmaf(wts[t * UOCR_K_TOPK + r], Y[((size_t)t * UOCR_K_TOPK + r) * UOCR_K_HIDDEN + c], acc);
+        acc = fmaf(wts[t * UOCR_K_TOPK + r], (float)Y[((size_t)t * UOCR_K_TOPK + r) * UOCR_K_HIDDEN + c], acc);
     }
     out[idx] = (h16)(acc + (float)shared[idx] + (float)res[idx]);
 }
@@ -1087,7 +1101,8 @@ __global__ __launch_bounds__(PB) void k_moe_combine(const float *__restrict__ Y,
 /* k_moe_combine fused with the next layer's input RMSNorm: one wavefront
  * per token row, the same per-element arithmetic, then y = rmsnorm(out) * w
  * as k_rows_rmsnorm rounds it. */
-__global__ __launch_bounds__(PB) void k_moe_combine_norm(const float *__restrict__ Y, const float *__restrict__ wts,
+template <typename YT>
+__global__ __launch_bounds__(PB) void k_moe_combine_norm(const YT *__restrict__ Y, const float *__restrict__ wts,
                                                          const h16 *__restrict__ shared, const h16 *__restrict__ res,
                                                          u32 P, h16 *__restrict__ out, const h16 *__restrict__ w,
                                                          h16 *__restrict__ y) {
@@ -1105,9 +1120,8 @@ __global__ __launch_bounds__(PB) void k_moe_combine_norm(const float *__restrict
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int r = 0; r < UOCR_K_TOPK; ++r) {
-            const float *yr = Y + ((size_t)t * UOCR_K_TOPK + r) * UOCR_K_HIDDEN + 8u * i;
-            const float4 a = *(const float4 *)yr, b = *(const float4 *)(yr + 4);
-            const float e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float e[8];
+            y_load8(Y + ((size_t)t * UOCR_K_TOPK + r) * UOCR_K_HIDDEN + 8u * i, e);
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[j] = fmaf(wr[r], e[j], acc[j]);
         }
@@ -1310,7 +1324,8 @@ extern "C" hipError_t uocr_launch_gemm_pair(hipStream_t st, int epi_a, const uoc
                         qb == UOCR_QT_F16;
     const bool experts = ok && epi_a == UOCR_GEMM_F16 && epi_b == UOCR_GEMM_SWIGLU && db->tile_e != nullptr && qa == qb;
     const bool downs = ok && epi_a == UOCR_GEMM_F16 && epi_b == UOCR_GEMM_F32 && db->tile_e != nullptr && qa == qb;
-    if (!router && !experts && !downs) {
+    const bool downs16 = ok && epi_a == UOCR_GEMM_F16 && epi_b == UOCR_GEMM_F16 && db->tile_e != nullptr && qa == qb;
+    if (!router && !experts && !downs && !downs16) {
         const hipError_t e = uocr_launch_gemm(st, epi_a, da);
         return e != hipSuccess ? e : uocr_launch_gemm(st, epi_b, db);
     }
@@ -1334,6 +1349,21 @@ extern "C" hipError_t uocr_launch_gemm_pair(hipStream_t st, int epi_a, const uoc
             default:
                 hipLaunchKernelGGL((k_gemm_pair<4, GE_SWIGLU, false, 1, GE_F32, false>), grid, dim3(PB), shm, st, a, ax,
                                    na, b, bx);
+                break;
+        }
+    } else if (downs16) {
+        switch (qa) {
+            case UOCR_QT_F16:
+                hipLaunchKernelGGL((k_gemm_pair<1, GE_F16, false, 1, GE_F16, true>), grid, dim3(PB), shm, st, a, ax, na,
+                                   b, bx);
+                break;
+            case UOCR_QT_Q8:
+                hipLaunchKernelGGL((k_gemm_pair<3, GE_F16, false, 3, GE_F16, true>), grid, dim3(PB), shm, st, a, ax, na,
+                                   b, bx);
+                break;
+            default:
+                hipLaunchKernelGGL((k_gemm_pair<4, GE_F16, false, 4, GE_F16, true>), grid, dim3(PB), shm, st, a, ax, na,
+                                   b, bx);
                 break;
         }
     } else if (downs) {
@@ -1455,8 +1485,20 @@ extern "C" hipError_t uocr_launch_moe_combine_norm(hipStream_t st, const float *
         norm_out == nullptr || P == 0u) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(k_moe_combine_norm, dim3((P + 3u) / 4u), dim3(PB), 0, st, Y, wts, (const h16 *)shared,
+    hipLaunchKernelGGL(k_moe_combine_norm<float>, dim3((P + 3u) / 4u), dim3(PB), 0, st, Y, wts, (const h16 *)shared,
                        (const h16 *)res, P, (h16 *)out, (const h16 *)norm_w, (h16 *)norm_out);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_moe_combine_norm_h(hipStream_t st, const uint16_t *Y, const float *wts,
+                                                     const uint16_t *shared, const uint16_t *res, uint32_t P,
+                                                     uint16_t *out, const uint16_t *norm_w, uint16_t *norm_out) {
+    if (Y == nullptr || wts == nullptr || shared == nullptr || res == nullptr || out == nullptr || norm_w == nullptr ||
+        norm_out == nullptr || P == 0u) {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(k_moe_combine_norm<h16>, dim3((P + 3u) / 4u), dim3(PB), 0, st, (const h16 *)Y, wts,
+                       (const h16 *)shared, (const h16 *)res, P, (h16 *)out, (const h16 *)norm_w, (h16 *)norm_out);
     return hipGetLastError();
 }
 
@@ -1466,8 +1508,20 @@ extern "C" hipError_t uocr_launch_moe_combine(hipStream_t st, const float *Y, co
         return hipErrorInvalidValue;
     }
     const u32 n = P * UOCR_K_HIDDEN;
-    hipLaunchKernelGGL(k_moe_combine, dim3((n + PB - 1u) / PB), dim3(PB), 0, st, Y, wts, (const h16 *)shared,
+    hipLaunchKernelGGL(k_moe_combine<float>, dim3((n + PB - 1u) / PB), dim3(PB), 0, st, Y, wts, (const h16 *)shared,
                        (const h16 *)res, P, (h16 *)out);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_moe_combine_h(hipStream_t st, const uint16_t *Y, const float *wts,
+                                                const uint16_t *shared, const uint16_t *res, uint32_t P,
+                                                uint16_t *out) {
+    if (Y == nullptr || wts == nullptr || shared == nullptr || res == nullptr || out == nullptr || P == 0u) {
+        return hipErrorInvalidValue;
+    }
+    const u32 n = P * UOCR_K_HIDDEN;
+    hipLaunchKernelGGL(k_moe_combine<h16>, dim3((n + PB - 1u) / PB), dim3(PB), 0, st, (const h16 *)Y, wts,
+                       (const h16 *)shared, (const h16 *)res, P, (h16 *)out);
     return hipGetLastError();
 }
 
