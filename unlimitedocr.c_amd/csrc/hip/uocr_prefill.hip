@@ -689,8 +689,9 @@ __global__ __launch_bounds__(PB) void k_rope_scatter(const h16 *__restrict__ qkv
  * qt + 1 key tiles; with chunks of CH key tiles it is nsplit(qt) = ceil((qt +
  * 1) / CH) blocks.  Blocks enumerate (qt, head, split) with the split
  * fastest, so the splits of one (qt, head) are consecutive block indices.
- * Each split of a tile with more than one writes its unnormalised O and its
- * row max / sum to its own partial slot; k_flash_merge combines them. */
+ * Each split of a tile with more than one writes its normalised O / l in
+ * fp16 (the first half of the O area of its slot) and its row max / sum in
+ * fp32 to its own partial slot; k_flash_merge combines them. */
 #define FA_PART_FLOATS (AQ * UOCR_K_HEAD_DIM + 2u * AQ)
 #define FA_MAX_SPLITS 16u /* splits of one query tile (the merge's weight table) */
 
@@ -868,11 +869,19 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
     l += __shfl_xor(l, 32);
     const u32 r = 16u * wave + qc; /* row within the tile */
     if (ns > 1u) {
-        /* partial of a split tile: unnormalised O, row max and row sum */
+        /* partial of a split tile: O / l in fp16 (a weighted mean of V rows,
+         * so within V's range), row max and row sum in fp32 */
         float *po = part + (size_t)blockIdx.x * FA_PART_FLOATS;
+        const float li = 1.0f / l;
 #pragma unroll
         for (int d = 0; d < UOCR_K_HEAD_DIM / 16; ++d) {
-            *(float4 *)(po + r * UOCR_K_HEAD_DIM + 16u * d + 4u * g) = make_float4(o[d][0], o[d][1], o[d][2], o[d][3]);
+            union {
+                h16 hh[4];
+                uint2 u;
+            } pk;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pk.hh[i] = (h16)(o[d][i] * li);
+            *(uint2 *)((h16 *)po + r * UOCR_K_HEAD_DIM + 16u * d + 4u * g) = pk.u;
         }
         if (g == 0u) {
             po[AQ * UOCR_K_HEAD_DIM + r] = m;
@@ -896,9 +905,9 @@ __global__ __launch_bounds__(PB) void k_flash_attn(const h16 *__restrict__ Q, co
 
 /* Merge of the split tiles: block (x, h, z) takes rows 16z..16z+15 of query
  * tile ch + x (every tile from ch on has at least two splits): ctx = sum_s
- * O_s e^(m_s - M) / sum_s l_s e^(m_s - M), M = max_s m_s (split 0 holds key
- * 0, so every row has L > 0).  Each thread owns two float4 of the 16 x 128
- * block and issues the splits' loads four at a time. */
+ * (O_s / l_s) l_s e^(m_s - M) / sum_s l_s e^(m_s - M), M = max_s m_s (split 0
+ * holds key 0, so every row has L > 0).  Each thread owns two 4-value pieces
+ * of the 16 x 128 block and issues the splits' loads four at a time. */
 __global__ __launch_bounds__(PB) void k_flash_merge(const float *__restrict__ part, u32 P, u32 ch,
                                                     h16 *__restrict__ ctx) {
     const u32 qt = ch + blockIdx.x, h = blockIdx.y, r0 = 16u * blockIdx.z, ns = fa_nsplit(qt, ch);
@@ -912,8 +921,9 @@ __global__ __launch_bounds__(PB) void k_flash_merge(const float *__restrict__ pa
         for (u32 s = 0; s < ns; ++s) {
             const float m = pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + r];
             const float w = m == -INFINITY ? 0.0f : expf(m - M);
-            wgt[s][threadIdx.x] = w;
-            L += w * pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + AQ + r];
+            const float wl = w * pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + AQ + r];
+            wgt[s][threadIdx.x] = wl; /* the split's O / l times its share */
+            L += wl;
         }
         linv[threadIdx.x] = 1.0f / L;
     }
@@ -928,7 +938,14 @@ __global__ __launch_bounds__(PB) void k_flash_merge(const float *__restrict__ pa
             float4 v[4];
 #pragma unroll
             for (u32 u = 0; u < 4u; ++u) {
-                if (s0 + u < ns) v[u] = *(const float4 *)(pb + (s0 + u) * FA_PART_FLOATS + off);
+                if (s0 + u < ns) {
+                    union {
+                        h16 hh[4];
+                        uint2 u2;
+                    } pk;
+                    pk.u2 = *(const uint2 *)((const h16 *)(pb + (s0 + u) * FA_PART_FLOATS) + off);
+                    v[u] = make_float4((float)pk.hh[0], (float)pk.hh[1], (float)pk.hh[2], (float)pk.hh[3]);
+                }
             }
 #pragma unroll
             for (u32 u = 0; u < 4u; ++u) {
