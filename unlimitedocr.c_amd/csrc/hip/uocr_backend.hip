@@ -95,7 +95,8 @@ struct uocr_hip_ctx {
     uint16_t *p_xn, *p_qkv, *p_q, *p_ctx, *p_a, *p_mid, *p_smid, *p_sout, *p_rmid;
     float *p_fa_ws; /* prefill attention key-split partials */
     float *p_kpart; /* prefill GEMM split-K partials */
-    float *p_logits, *p_wts, *p_y;
+    float *p_logits, *p_wts;
+    uint16_t *p_y; /* per-pair routed expert outputs, fp16 */
     int32_t *p_ids, *p_offsets, *p_tile_e, *p_tile_s0, *p_tile_s1, *p_ntiles, *p_list_tok,
         *p_list_pair;
     uint32_t p_max_tiles;
@@ -677,7 +678,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_psmid = p.take(Pc * UOCR_MOE_SHARED_INTERMEDIATE * 2u), o_psout = p.take(Pc * H_SIZE * 2u);
     const uint64_t o_prmid = p.take(PK * UOCR_MOE_EXPERT_INTERMEDIATE * 2u);
     const uint64_t o_plog = p.take(Pc * UOCR_ROUTED_EXPERTS * 4u), o_pwts = p.take(PK * 4u);
-    const uint64_t o_py = p.take(PK * H_SIZE * 4u), o_pids = p.take(PK * 4u);
+    const uint64_t o_py = p.take(PK * H_SIZE * 2u), o_pids = p.take(PK * 4u);
     const uint64_t o_poff = p.take(64u * 4u);
     const uint64_t o_pte = p.take(max_tiles * 4u), o_pts0 = p.take(max_tiles * 4u), o_pts1 = p.take(max_tiles * 4u);
     const uint64_t o_pnt = p.take(4u), o_plt = p.take(PK * 4u), o_plp = p.take(PK * 4u);
@@ -725,7 +726,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->p_rmid = (uint16_t *)(b + o_prmid);
     ctx->p_logits = (float *)(b + o_plog);
     ctx->p_wts = (float *)(b + o_pwts);
-    ctx->p_y = (float *)(b + o_py);
+    ctx->p_y = (uint16_t *)(b + o_py);
     ctx->p_ids = (int32_t *)(b + o_pids);
     ctx->p_offsets = (int32_t *)(b + o_poff);
     ctx->p_tile_e = (int32_t *)(b + o_pte);
@@ -1061,7 +1062,7 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         dd.s_stride = L.slab.dn_s_stride;
         dd.a_idx = c->p_list_pair;
         /* per-pair expert outputs in fp16, as the reference keeps them */
-        uint16_t *y16 = (uint16_t *)c->p_y;
+        uint16_t *y16 = c->p_y;
         dd.out = y16;
         dd.ldo = H_SIZE;
         if (sd_down) {
