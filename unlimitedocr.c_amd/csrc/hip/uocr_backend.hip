@@ -92,8 +92,9 @@ struct uocr_hip_ctx {
     int prefill_ksplit; /* small-grid prefill GEMMs split K */
     uint32_t *route_ids;
     /* MFMA prefill scratch, sized for prompt_cap rows */
-    uint16_t *p_xn, *p_qkv, *p_q, *p_ctx, *p_a, *p_mid, *p_smid, *p_sout, *p_rmid;
+    uint16_t *p_xn, *p_q, *p_ctx, *p_a, *p_mid, *p_smid, *p_sout, *p_rmid;
     float *p_fa_ws; /* prefill attention key-split partials */
+    float *p_rope;  /* prefill RoPE (cos, sin) per token and pair */
     float *p_kpart; /* prefill GEMM split-K partials */
     float *p_logits, *p_wts;
     uint16_t *p_y; /* per-pair routed expert outputs, fp16 */
@@ -672,7 +673,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t prompt_end = p.off;
     const uint64_t Pc = prompt_capacity, PK = Pc * UOCR_MOE_TOP_K;
     const uint32_t max_tiles = (uint32_t)((PK + 63u) / 64u + UOCR_ROUTED_EXPERTS);
-    const uint64_t o_pxn = p.take(Pc * H_SIZE * 2u), o_pqkv = p.take(Pc * 3u * H_SIZE * 2u);
+    const uint64_t o_pxn = p.take(Pc * H_SIZE * 2u), o_prope = p.take(Pc * 64u * 8u);
     const uint64_t o_pq = p.take(Pc * H_SIZE * 2u), o_pctx = p.take(Pc * H_SIZE * 2u), o_pa = p.take(Pc * H_SIZE * 2u);
     const uint64_t o_pmid = p.take(Pc * UOCR_DENSE_LAYER0_INTERMEDIATE * 2u);
     const uint64_t o_psmid = p.take(Pc * UOCR_MOE_SHARED_INTERMEDIATE * 2u), o_psout = p.take(Pc * H_SIZE * 2u);
@@ -716,7 +717,6 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->d_ids = (int32_t *)(b + o_dids);
     ctx->d_mask = (uint8_t *)(b + o_dmask);
     ctx->p_xn = (uint16_t *)(b + o_pxn);
-    ctx->p_qkv = (uint16_t *)(b + o_pqkv);
     ctx->p_q = (uint16_t *)(b + o_pq);
     ctx->p_ctx = (uint16_t *)(b + o_pctx);
     ctx->p_a = (uint16_t *)(b + o_pa);
@@ -736,6 +736,7 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     ctx->p_list_tok = (int32_t *)(b + o_plt);
     ctx->p_list_pair = (int32_t *)(b + o_plp);
     ctx->p_fa_ws = (float *)(b + o_pfa);
+    ctx->p_rope = (float *)(b + o_prope);
     ctx->p_kpart = (float *)(b + o_pkp);
     ctx->run_arena = b + o_run;
     ctx->run_tag = 1u; /* the arena is zero: tag 0 never matches */
@@ -967,8 +968,11 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
         const dev_layer &L = c->L[l];
         const uint16_t *next_norm = l + 1u < UOCR_DECODER_LAYERS ? c->L[l + 1u].in_norm : nullptr;
         uint16_t *kc = c->kc + l * kv_layer, *vc = c->vc + l * kv_layer;
-        if (l == 0u) ENQ(uocr_launch_rows_rmsnorm(s, H, L.in_norm, P, c->p_xn));
-        uocr_gemm_desc d = gdesc(c->p_xn, H_SIZE, P, 3u * H_SIZE, H_SIZE, c->p_qkv, 3u * H_SIZE);
+        if (l == 0u) {
+            ENQ(uocr_launch_rows_rmsnorm(s, H, L.in_norm, P, c->p_xn));
+            ENQ(uocr_launch_rope_table(s, c->invf, P, c->p_rope));
+        }
+        uocr_gemm_desc d = gdesc(c->p_xn, H_SIZE, P, 3u * H_SIZE, H_SIZE, c->p_q, 3u * H_SIZE);
         d.W[0] = packed_of(L.q, L.pq);
         d.W[1] = packed_of(L.k, L.pk);
         d.W[2] = packed_of(L.v, L.pv);
@@ -979,8 +983,7 @@ static hipError_t enqueue_prefill_mfma(uocr_hip_ctx *c, uint32_t P) {
             d.W[2] = L.v;
         }
         d.nseg = H_SIZE;
-        ENQ(uocr_launch_gemm(s, UOCR_GEMM_F16, &d));
-        ENQ(uocr_launch_rope_scatter(s, c->p_qkv, c->invf, P, c->p_q, kc, vc, c->cache_cap));
+        ENQ(uocr_launch_gemm_qkv_rope(s, &d, c->p_rope, c->p_q, kc, vc, c->cache_cap));
         ENQ(uocr_launch_flash_attn(s, c->p_q, kc, vc, c->cache_cap, P, c->p_ctx, c->p_fa_ws));
         d = gdesc(c->p_ctx, H_SIZE, P, H_SIZE, H_SIZE, c->p_a, H_SIZE);
         d.W[0] = packed_of(L.o, L.po);

@@ -279,9 +279,15 @@ hipError_t uocr_launch_pack_gemm_rows(hipStream_t st, uint32_t qtype, const void
 uint32_t uocr_gemm_ksplit(uint32_t M, uint32_t N, uint32_t K);
 /* y[t] = rmsnorm(x[t], w) for P rows of 1280. */
 hipError_t uocr_launch_rows_rmsnorm(hipStream_t st, const uint16_t *x, const uint16_t *w, uint32_t P, uint16_t *y);
-/* qkv [P][3840] -> RoPE'd q [P][1280]; RoPE'd k and v into cache slots 0..P-1. */
-hipError_t uocr_launch_rope_scatter(hipStream_t st, const uint16_t *qkv, const float *inv_freq, uint32_t P,
-                                    uint16_t *qout, uint16_t *kcache, uint16_t *vcache, uint32_t cap);
+/* cs [P][64][2] = (cos, sin) of t * inv_freq[d] for tokens t < P (inv_freq:
+ * 64 host floats). */
+hipError_t uocr_launch_rope_table(hipStream_t st, const float *inv_freq, uint32_t P, float *cs);
+/* The Q | K | V projection (d: UOCR_GEMM_F16 shape, N = 3840, nseg = 1280,
+ * not grouped, M <= cap; d->out unused) with RoPE and the cache scatter as
+ * its epilogue: RoPE'd q -> qout [M][1280], RoPE'd k and v -> cache slots
+ * 0..M-1 ([head][cap][128]); cs is uocr_launch_rope_table's table for M. */
+hipError_t uocr_launch_gemm_qkv_rope(hipStream_t st, const uocr_gemm_desc *d, const float *cs, uint16_t *qout,
+                                     uint16_t *kcache, uint16_t *vcache, uint32_t cap);
 /* Causal attention of P prompt queries over cache slots 0..P-1 -> ctx [P][1280]. */
 hipError_t uocr_launch_flash_attn(hipStream_t st, const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache,
                                   uint32_t cap, uint32_t P, uint16_t *ctx, float *ws);

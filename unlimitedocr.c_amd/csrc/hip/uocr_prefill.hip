@@ -73,7 +73,7 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
-enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2, GE_VISION = 3, GE_PART = 4 };
+enum { GE_F16 = 0, GE_F32 = 1, GE_SWIGLU = 2, GE_VISION = 3, GE_PART = 4, GE_ROPE = 5 };
 
 /* QuickGELU of the CLIP MLP: x * sigmoid(1.702 x) (dense.metal:63-66). */
 __device__ __forceinline__ float quick_gelu(float x) {
@@ -180,6 +180,19 @@ __device__ __forceinline__ void b_dequant(const u32 (&w)[BPiece<QT>::NW], u32 sc
     }
 }
 
+struct RopeTabP {
+    float f[UOCR_K_HEAD_DIM / 2];
+};
+
+/* GE_ROPE destinations: q rows [P][1280], the layer's K / V caches
+ * [head][cap][128]; cs holds (cos, sin) of token t's angle t * f[d] at
+ * cs[64 t + d]. */
+struct RopeDst {
+    const float2 *cs;
+    h16 *q, *k, *v;
+    u32 cap;
+};
+
 struct GemmArgs {
     const h16 *A;        /* activations, row stride lda (halves) */
     u32 lda;
@@ -219,7 +232,7 @@ struct GemmArgs {
 #endif
 
 template <int QT, int EPI, bool GROUPED, int TMR>
-__device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz) {
+__device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz, RopeDst rd = RopeDst{}) {
     constexpr int AQ4 = TMR * (TK / 8) / PB; /* activation pieces (8 halves) per thread per K step */
     static_assert(TMR % 32 == 0 && TMR <= PB && AQ4 * PB == TMR * (TK / 8), "tile rows");
     constexpr int NMAT = EPI == GE_SWIGLU ? 2 : 1;
@@ -429,6 +442,61 @@ __device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz) {
         if (st + (u32)decltype(D)::value < NS) step(D, st + (u32)decltype(D)::value);
     });
 
+    if constexpr (EPI == GE_ROPE) {
+        /* The Q | K | V projection with RoPE and the cache scatter as its
+         * epilogue: the block's 128 columns are one head of one of the three
+         * segments.  The tile is rounded to fp16 (the projection's output
+         * type) into LDS, then wavefront w takes rows w, w + 4, ..: lane d
+         * rotates the pair (x_d, x_{d+64}) in fp32 by the angle tok * f[d],
+         * cos and sin from the prompt's table (q and k; v is copied). */
+        static_assert(GROUPED == false && TMR == 64 && TN == UOCR_K_HEAD_DIM, "rope tile");
+        constexpr u32 RLD = TN + 8u; /* padded LDS row (halves) */
+        static_assert(TMR * RLD <= 2u * TMR * LDA, "rope tile in the activation buffers");
+        h16 *tile = &as[0][0];
+        const u32 seg = n0 / p.nseg, h = (n0 - seg * p.nseg) / TN, d = lane;
+        __syncthreads(); /* every wavefront's last MFMA reads of as[] are done */
+#pragma unroll
+        for (int j = 0; j < TMR / 32; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const u32 r = 32u * j + 8u * (i / 4) + 4u * hf + (i % 4);
+                tile[r * RLD + 32u * wave + (lane & 31u)] = (h16)acc[0][j][i];
+            }
+        /* the wavefront's cos / sin loads, all in flight across the barrier
+         * (issued after the accumulators are staged, so they add no
+         * registers to the main loop's) */
+        constexpr int RW = TMR / (PB / 64); /* rows per wavefront */
+        float2 csr[RW];
+        if (seg != 2u) {
+#pragma unroll
+            for (int k = 0; k < RW; ++k) {
+                const u32 r = min(wave + (PB / 64u) * k, rows - 1u);
+                csr[k] = rd.cs[(size_t)(s0 + r) * 64u + d];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < RW; ++k) {
+            const u32 r = wave + (PB / 64u) * k;
+            if (r >= rows) break;
+            const u32 tok = s0 + r;
+            const h16 xa = tile[r * RLD + d], xb = tile[r * RLD + d + 64u];
+            if (seg == 2u) {
+                const size_t ci = ((size_t)h * rd.cap + tok) * UOCR_K_HEAD_DIM + d;
+                rd.v[ci] = xa;
+                rd.v[ci + 64u] = xb;
+                continue;
+            }
+            const float cs = csr[k].x, sn = csr[k].y;
+            const float a = (float)xa, b = (float)xb;
+            h16 *dst = seg == 0u ? rd.q + (size_t)tok * UOCR_K_HIDDEN + h * UOCR_K_HEAD_DIM + d
+                                 : rd.k + ((size_t)h * rd.cap + tok) * UOCR_K_HEAD_DIM + d;
+            dst[0] = (h16)(a * cs - b * sn);
+            dst[64] = (h16)(a * sn + b * cs);
+        }
+        return;
+    }
+
     /* C layout of a 32x32 MFMA tile: lane l, element i -> row 8*(i/4) +
      * 4*(l/32) + i%4, column l%32.  Everything that depends only on the
      * column (output pointer, split routing, bias) is resolved once per lane;
@@ -479,6 +547,19 @@ __device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz) {
 template <int QT, int EPI, bool GROUPED, int TMR>
 __global__ __launch_bounds__(PB) void k_gemm(GemmArgs p) {
     gemm_body<QT, EPI, GROUPED, TMR>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+template <int QT>
+__global__ __launch_bounds__(PB) void k_gemm_rope(GemmArgs p, const float2 *cs, h16 *q, h16 *kc, h16 *vc, u32 cap) {
+    gemm_body<QT, GE_ROPE, false, TM>(p, blockIdx.x, blockIdx.y, 0u, RopeDst{cs, q, kc, vc, cap});
+}
+
+/* cs[64 t + d] = (cos, sin)(t * f[d]) for the P prompt tokens. */
+__global__ __launch_bounds__(PB) void k_rope_table(RopeTabP rope, u32 P, float2 *__restrict__ cs) {
+    const u32 idx = blockIdx.x * PB + threadIdx.x;
+    if (idx >= P * 64u) return;
+    const float ang = (float)(idx / 64u) * rope.f[idx % 64u];
+    cs[idx] = make_float2(cosf(ang), sinf(ang));
 }
 
 /* Two independent GEMMs in one launch: blocks [0, na) run A's tile grid
@@ -643,34 +724,6 @@ __global__ __launch_bounds__(PB) void k_reduce_norm(const float *__restrict__ pa
         *(uint4 *)(out + (size_t)row * ldo + 8u * i) = v[q].u;
     }
     row_norm_tail(v, lane, w, y + (size_t)row * UOCR_K_HIDDEN);
-}
-
-struct RopeTabP {
-    float f[UOCR_K_HEAD_DIM / 2];
-};
-
-/* qkv [P][3840] (q | k | v, fp16) -> q rotated into qout [P][1280]; k
- * rotated and v copied into cache slots 0..P-1 ([head][cap][128]).  One
- * thread per (token, head, pair d < 64). */
-__global__ __launch_bounds__(PB) void k_rope_scatter(const h16 *__restrict__ qkv, RopeTabP rope, u32 P,
-                                                     h16 *__restrict__ qout, h16 *__restrict__ kc,
-                                                     h16 *__restrict__ vc, u32 cap) {
-    const u32 idx = blockIdx.x * PB + threadIdx.x;
-    if (idx >= P * UOCR_K_HEADS * 64u) return;
-    const u32 t = idx / (UOCR_K_HEADS * 64u), rem = idx % (UOCR_K_HEADS * 64u), h = rem / 64u, d = rem % 64u;
-    const h16 *row = qkv + (size_t)t * 3u * UOCR_K_HIDDEN;
-    const float ang = (float)t * rope.f[d];
-    const float cs = cosf(ang), sn = sinf(ang);
-    const u32 c = h * 128u + d;
-    const float qa = (float)row[c], qb = (float)row[c + 64u];
-    const float ka = (float)row[UOCR_K_HIDDEN + c], kb = (float)row[UOCR_K_HIDDEN + c + 64u];
-    qout[(size_t)t * UOCR_K_HIDDEN + c] = (h16)(qa * cs - qb * sn);
-    qout[(size_t)t * UOCR_K_HIDDEN + c + 64u] = (h16)(qa * sn + qb * cs);
-    const size_t ci = ((size_t)h * cap + t) * 128u + d;
-    kc[ci] = (h16)(ka * cs - kb * sn);
-    kc[ci + 64u] = (h16)(ka * sn + kb * cs);
-    vc[ci] = row[2u * UOCR_K_HIDDEN + c];
-    vc[ci + 64u] = row[2u * UOCR_K_HIDDEN + c + 64u];
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1424,17 +1477,39 @@ extern "C" hipError_t uocr_launch_rows_rmsnorm(hipStream_t st, const uint16_t *x
     return hipGetLastError();
 }
 
-extern "C" hipError_t uocr_launch_rope_scatter(hipStream_t st, const uint16_t *qkv, const float *inv_freq, uint32_t P,
-                                               uint16_t *qout, uint16_t *kcache, uint16_t *vcache, uint32_t cap) {
-    if (qkv == nullptr || inv_freq == nullptr || qout == nullptr || kcache == nullptr || vcache == nullptr || P == 0u ||
-        P > cap) {
-        return hipErrorInvalidValue;
-    }
+extern "C" hipError_t uocr_launch_rope_table(hipStream_t st, const float *inv_freq, uint32_t P, float *cs) {
+    if (inv_freq == nullptr || cs == nullptr || P == 0u) return hipErrorInvalidValue;
     RopeTabP tab;
     for (int i = 0; i < UOCR_K_HEAD_DIM / 2; ++i) tab.f[i] = inv_freq[i];
-    const u32 n = P * UOCR_K_HEADS * 64u;
-    hipLaunchKernelGGL(k_rope_scatter, dim3((n + PB - 1u) / PB), dim3(PB), 0, st, (const h16 *)qkv, tab, P, (h16 *)qout,
-                       (h16 *)kcache, (h16 *)vcache, cap);
+    hipLaunchKernelGGL(k_rope_table, dim3((P * 64u + PB - 1u) / PB), dim3(PB), 0, st, tab, P, (float2 *)cs);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t uocr_launch_gemm_qkv_rope(hipStream_t st, const uocr_gemm_desc *d, const float *cs,
+                                                uint16_t *qout, uint16_t *kcache, uint16_t *vcache, uint32_t cap) {
+    if (!gemm_desc_ok(UOCR_GEMM_F16, d) || d->tile_e != nullptr || d->nseg != UOCR_K_HIDDEN ||
+        d->N != 3u * UOCR_K_HIDDEN || d->M > cap || cs == nullptr || qout == nullptr || kcache == nullptr ||
+        vcache == nullptr) {
+        return hipErrorInvalidValue;
+    }
+    GemmArgs a = gemm_args(d);
+    const size_t shm = gemm_scales(d->W[0].qtype, 1u, a);
+    const float2 *tab = (const float2 *)cs;
+    const dim3 grid((d->M + TM - 1u) / TM, d->N / TN);
+    switch (d->W[0].qtype) {
+        case UOCR_QT_F16:
+            hipLaunchKernelGGL(k_gemm_rope<1>, grid, dim3(PB), 0, st, a, tab, (h16 *)qout, (h16 *)kcache,
+                               (h16 *)vcache, cap);
+            break;
+        case UOCR_QT_Q8:
+            hipLaunchKernelGGL(k_gemm_rope<3>, grid, dim3(PB), shm, st, a, tab, (h16 *)qout, (h16 *)kcache,
+                               (h16 *)vcache, cap);
+            break;
+        default:
+            hipLaunchKernelGGL(k_gemm_rope<4>, grid, dim3(PB), shm, st, a, tab, (h16 *)qout, (h16 *)kcache,
+                               (h16 *)vcache, cap);
+            break;
+    }
     return hipGetLastError();
 }
 
