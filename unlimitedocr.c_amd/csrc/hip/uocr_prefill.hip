@@ -698,14 +698,43 @@ __global__ __launch_bounds__(PB) void k_reduce_norm(const float *__restrict__ pa
     const u32 row = blockIdx.x * (PB / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
     if (row >= M) return;
     const size_t MN = (size_t)M * UOCR_K_HIDDEN;
+    /* the first two planes of the row's pieces (and the residual), all in
+     * flight before any sum; planes beyond the second are added in order
+     * after them */
+    float4 pa[3][2], pb2[3][2];
+    U4H8 rr[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const u32 i = min(lane + 64u * q, UOCR_K_HIDDEN / 8u - 1u);
+        const float *p0 = part + (size_t)row * UOCR_K_HIDDEN + 8u * i;
+#pragma unroll
+        for (u32 z = 0; z < 2u; ++z) {
+            if (z < S) {
+                pa[q][z] = *(const float4 *)(p0 + z * MN);
+                pb2[q][z] = *(const float4 *)(p0 + z * MN + 4);
+            }
+        }
+        if (res != nullptr) rr[q].u = *(const uint4 *)(res + (size_t)row * ldr + 8u * i);
+    }
     U4H8 v[3];
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
         const u32 i = lane + 64u * q;
         if (i >= UOCR_K_HIDDEN / 8u) continue;
         const float *p0 = part + (size_t)row * UOCR_K_HIDDEN + 8u * i;
-        float4 a = *(const float4 *)p0, b = *(const float4 *)(p0 + 4);
-        for (u32 z = 1; z < S; ++z) {
+        float4 a = pa[q][0], b = pb2[q][0];
+        if (S > 1u) {
+            const float4 c = pa[q][1], d = pb2[q][1];
+            a.x += c.x;
+            a.y += c.y;
+            a.z += c.z;
+            a.w += c.w;
+            b.x += d.x;
+            b.y += d.y;
+            b.z += d.z;
+            b.w += d.w;
+        }
+        for (u32 z = 2; z < S; ++z) {
             const float4 c = *(const float4 *)(p0 + z * MN), d = *(const float4 *)(p0 + z * MN + 4);
             a.x += c.x;
             a.y += c.y;
@@ -717,10 +746,8 @@ __global__ __launch_bounds__(PB) void k_reduce_norm(const float *__restrict__ pa
             b.w += d.w;
         }
         const float r[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        U4H8 rr;
-        if (res != nullptr) rr.u = *(const uint4 *)(res + (size_t)row * ldr + 8u * i);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[q].h[j] = (h16)(res != nullptr ? r[j] + (float)rr.h[j] : r[j]);
+        for (int j = 0; j < 8; ++j) v[q].h[j] = (h16)(res != nullptr ? r[j] + (float)rr[q].h[j] : r[j]);
         *(uint4 *)(out + (size_t)row * ldo + 8u * i) = v[q].u;
     }
     row_norm_tail(v, lane, w, y + (size_t)row * UOCR_K_HIDDEN);
@@ -968,15 +995,29 @@ __global__ __launch_bounds__(PB) void k_flash_merge(const float *__restrict__ pa
     __shared__ float wgt[FA_MAX_SPLITS][16], linv[16];
     if (threadIdx.x < 16u) {
         const u32 r = r0 + threadIdx.x;
+        /* all of the row's (m, l) loads in flight at once */
+        float mv[FA_MAX_SPLITS], lv[FA_MAX_SPLITS];
+#pragma unroll
+        for (u32 s = 0; s < FA_MAX_SPLITS; ++s) {
+            if (s < ns) {
+                mv[s] = pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + r];
+                lv[s] = pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + AQ + r];
+            }
+        }
         float M = -INFINITY;
-        for (u32 s = 0; s < ns; ++s) M = fmaxf(M, pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + r]);
+#pragma unroll
+        for (u32 s = 0; s < FA_MAX_SPLITS; ++s) {
+            if (s < ns) M = fmaxf(M, mv[s]);
+        }
         float L = 0.0f;
-        for (u32 s = 0; s < ns; ++s) {
-            const float m = pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + r];
-            const float w = m == -INFINITY ? 0.0f : expf(m - M);
-            const float wl = w * pb[s * FA_PART_FLOATS + AQ * UOCR_K_HEAD_DIM + AQ + r];
-            wgt[s][threadIdx.x] = wl; /* the split's O / l times its share */
-            L += wl;
+#pragma unroll
+        for (u32 s = 0; s < FA_MAX_SPLITS; ++s) {
+            if (s < ns) {
+                const float w = mv[s] == -INFINITY ? 0.0f : expf(mv[s] - M);
+                const float wl = w * lv[s];
+                wgt[s][threadIdx.x] = wl; /* the split's O / l times its share */
+                L += wl;
+            }
         }
         linv[threadIdx.x] = 1.0f / L;
     }
@@ -1095,8 +1136,24 @@ __global__ __launch_bounds__(BUCKET_THREADS) void k_bucket_build(const int32_t *
         cnt[t] = 0;
         cur[t] = 0;
     }
+    /* the thread's pairs' ids, all loads in flight at once (up to BUCKET_R
+     * per thread; longer prompts loop) */
+    constexpr u32 BUCKET_R = 8u;
+    const bool inreg = n <= BUCKET_R * BUCKET_THREADS;
+    int32_t idr[BUCKET_R];
+    if (inreg) {
+#pragma unroll
+        for (u32 k = 0; k < BUCKET_R; ++k) idr[k] = t + k * BUCKET_THREADS < n ? ids[t + k * BUCKET_THREADS] : -1;
+    }
     __syncthreads();
-    for (u32 pr = t; pr < n; pr += BUCKET_THREADS) atomicAdd(&cnt[ids[pr]], 1);
+    if (inreg) {
+#pragma unroll
+        for (u32 k = 0; k < BUCKET_R; ++k) {
+            if (idr[k] >= 0) atomicAdd(&cnt[idr[k]], 1);
+        }
+    } else {
+        for (u32 pr = t; pr < n; pr += BUCKET_THREADS) atomicAdd(&cnt[ids[pr]], 1);
+    }
     __syncthreads();
     if (t < 64u) {
         /* exclusive scans of the bucket sizes and tile counts: one wavefront,
@@ -1130,11 +1187,23 @@ __global__ __launch_bounds__(BUCKET_THREADS) void k_bucket_build(const int32_t *
             tile_s1[ti] = off[t] + min(c, (k + 1) * GTM);
         }
     }
-    for (u32 pr = t; pr < n; pr += BUCKET_THREADS) {
-        const int32_t e = ids[pr];
-        const int32_t slot = off[e] + atomicAdd(&cur[e], 1);
-        list_tok[slot] = (int32_t)(pr / UOCR_K_TOPK);
-        list_pair[slot] = (int32_t)pr;
+    if (inreg) {
+#pragma unroll
+        for (u32 k = 0; k < BUCKET_R; ++k) {
+            const u32 pr = t + k * BUCKET_THREADS;
+            if (idr[k] >= 0) {
+                const int32_t slot = off[idr[k]] + atomicAdd(&cur[idr[k]], 1);
+                list_tok[slot] = (int32_t)(pr / UOCR_K_TOPK);
+                list_pair[slot] = (int32_t)pr;
+            }
+        }
+    } else {
+        for (u32 pr = t; pr < n; pr += BUCKET_THREADS) {
+            const int32_t e = ids[pr];
+            const int32_t slot = off[e] + atomicAdd(&cur[e], 1);
+            list_tok[slot] = (int32_t)(pr / UOCR_K_TOPK);
+            list_pair[slot] = (int32_t)pr;
+        }
     }
 }
 
