@@ -123,7 +123,16 @@ static_assert(O_ROWS * O_BLOCKS == HID, "O rows split evenly");
 #ifndef UOCR_RUN_Z_BLOCKS
 #define UOCR_RUN_Z_BLOCKS 20u
 #endif
-constexpr u32 Z_BLOCKS = UOCR_RUN_Z_BLOCKS, Z_COLS = HID / Z_BLOCKS; /* O blocks j < Z_BLOCKS also publish z partials */
+constexpr u32 Z_BLOCKS = UOCR_RUN_Z_BLOCKS, Z_COLS = HID / Z_BLOCKS;
+/* UOCR_RUN_Z_SEP 1: the z partials come from Z_BLOCKS blocks below the O
+ * blocks (QKV / GU / DN blocks otherwise idle in the O stage), so the O
+ * blocks only compute O rows; 0: O blocks j < Z_BLOCKS publish them before
+ * their O rows. */
+#ifndef UOCR_RUN_Z_SEP
+#define UOCR_RUN_Z_SEP 1
+#endif
+constexpr u32 Z0 = UOCR_RUN_Z_SEP ? O0 - Z_BLOCKS : O0; /* z block j is block Z0 + j */
+static_assert(Z0 + Z_BLOCKS <= QKV_BLOCKS, "z blocks hold h from the QKV stage");
 constexpr u32 GU_ROUTED = 192u, GU_ROWS = 28u, DGU_ROWS = 27u;
 #ifndef UOCR_RUN_EXACT_WEIGHTS
 #define UOCR_RUN_EXACT_WEIGHTS 1
@@ -976,7 +985,8 @@ struct OCfg {
     static constexpr u32 J = (RPG * C + LPR - 1u) / LPR;
     static_assert(J * LPR == RPG * C, "O chunks split evenly over the lane group");
     static constexpr u32 ZC = Z_COLS / (NT / 64u); /* columns per thread in a z partial */
-    static_assert(RPG * NG == O_ROWS && ZC * (NT / 64u) == Z_COLS && Z_BLOCKS <= O_BLOCKS, "O rows per group");
+    static_assert(RPG * NG == O_ROWS && ZC * (NT / 64u) == Z_COLS && (UOCR_RUN_Z_SEP || Z_BLOCKS <= O_BLOCKS),
+                  "O rows per group");
 };
 
 template <int QA>
@@ -984,7 +994,7 @@ struct OFrags {
     RowFrag<OCfg<QA>::J> f;
 };
 
-/* z-partial weights of O block j < Z_BLOCKS (MoE layers): rows
+/* z-partial weights of z block j (block Z0 + j; MoE layers): rows
  * [80j, 80j + 80) of fold and of fold_o, two contiguous 20 KB ranges,
  * copied into LDS (zw[0], zw[1]) by LDS-direct loads, so they take no
  * registers while the O stage waits; complete once the issuing thread's
@@ -994,9 +1004,9 @@ static_assert(ZW_BYTES % (64u * 16u) == 0u, "z weights in whole wavefront copies
 
 __device__ __forceinline__ void o_load_z(const Run &R, u32 l, float *zw) {
     const u32 b = blockIdx.x;
-    if (l == 0u || b < O0 || b >= O0 + Z_BLOCKS) return;
+    if (l == 0u || b < Z0 || b >= Z0 + Z_BLOCKS) return;
     const AS4 RunLayerD &L = R.M->L[l];
-    const u32 j = b - O0, wave = __builtin_amdgcn_readfirstlane(tid_() / 64u), lane = tid_() % 64u;
+    const u32 j = b - Z0, wave = __builtin_amdgcn_readfirstlane(tid_() / 64u), lane = tid_() % 64u;
     const AS1 uint8_t *src[2] = {(const AS1 uint8_t *)L.fold + (size_t)j * ZW_BYTES,
                                  (const AS1 uint8_t *)L.fold_o + (size_t)j * ZW_BYTES};
 #pragma unroll
@@ -1032,29 +1042,40 @@ template <int QA>
 __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, OFrags<QA> &F) {
     typedef OCfg<QA> G;
     const u32 b = blockIdx.x;
-    if (b < O0 || b >= O0 + O_BLOCKS) return true;
-    const u32 j = b - O0, g = tid_() / 32u, sub = tid_() % 32u;
+    const bool ob = b >= O0 && b < O0 + O_BLOCKS, zb = l > 0u && b >= Z0 && b < Z0 + Z_BLOCKS;
+    if (!ob && !zb) return true;
+    const u32 j = b - O0, jz = b - Z0, g = tid_() / 32u, sub = tid_() % 32u;
     h16 *accp = (h16 *)S.scr;                           /* [80][128] */
     float *ml = (float *)(S.scr + ATT_BLOCKS * HDIM * 2u); /* [80][2] */
     float *wk = ml + 2u * ATT_BLOCKS;                     /* [80] */
     float *zq = wk + ATT_BLOCKS;                          /* [NT / 64][64] */
     static_assert(ATT_BLOCKS * HDIM * 2u + ATT_BLOCKS * 12u + NT * 4u <= SCR_BYTES, "O stage LDS");
-    if (!gather<(PATT + NT - 1) / NT>(R, R.pk + off_att(l), PATT, PATT, tag, W_O, (u32)t, [](u32 i) { return i; },
-                                      [&](u32 i, uint4 v) {
-                                          const u32 a = i / PATT_B, k = i % PATT_B;
-                                          if (k < PATT_B - 1u) {
-                                              put6(accp + a * HDIM + 6u * k, v, 6u * k, HDIM);
-                                          } else {
-                                              ml[2u * a] = __uint_as_float(v.y);
-                                              ml[2u * a + 1u] = __uint_as_float(v.z);
-                                          }
-                                      })) {
-        return false;
-    }
+    static_assert(HDIM % Z_COLS == 0u, "a z block's columns lie in one head");
+    /* a z-only block needs the context of its own head only: that head's
+     * ATT_SPLITS attention blocks (packets of the other heads are not
+     * polled, and their merge is skipped) */
+    const bool zonly = !ob;
+    const u32 zh = jz * Z_COLS / HDIM, abase = zonly ? zh * ATT_SPLITS : 0u;
+    auto att_phys = [=](u32 i) { return abase * PATT_B + i; };
+    auto att_sink = [&](u32 i, uint4 v) {
+        const u32 a = abase + i / PATT_B, k = i % PATT_B;
+        if (k < PATT_B - 1u) {
+            put6(accp + a * HDIM + 6u * k, v, 6u * k, HDIM);
+        } else {
+            ml[2u * a] = __uint_as_float(v.y);
+            ml[2u * a + 1u] = __uint_as_float(v.z);
+        }
+    };
+    const bool got = zonly ? gather<(ATT_SPLITS * PATT_B + NT - 1) / NT>(R, R.pk + off_att(l), PATT,
+                                                                       ATT_SPLITS * PATT_B, tag, W_O, (u32)t,
+                                                                       att_phys, att_sink)
+                           : gather<(PATT + NT - 1) / NT>(R, R.pk + off_att(l), PATT, PATT, tag, W_O, (u32)t,
+                                                          att_phys, att_sink);
+    if (!got) return false;
     TLR(2u * (3u + 5u * l));
     /* merge weights: lanes 8h..8h+7 hold the splits of head h (the same
      * arithmetic as k_attn_out's merge) */
-    if (tid_() < ATT_BLOCKS) {
+    if (tid_() < ATT_BLOCKS && (!zonly || tid_() / ATT_SPLITS == zh)) {
         const float mk = ml[2u * tid_()], lk = ml[2u * tid_() + 1u];
         float M = mk;
 #pragma unroll
@@ -1067,7 +1088,7 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     TLD(l, 6u);
-    if (tid_() < HID / 8u) {
+    if (tid_() < HID / 8u && (!zonly || tid_() / (HDIM / 8u) == zh)) {
         const u32 hh = tid_() / (HDIM / 8u), d8 = tid_() % (HDIM / 8u);
         float acc[8];
 #pragma unroll
@@ -1090,11 +1111,11 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
     }
     __syncthreads();
     TLD(l, 7u);
-    if (l > 0u && j < Z_BLOCKS) {
+    if (zb) {
         /* the router's pre-norm logits are linear in h and ctx:
          * z = fold^T a = fold^T h + (O^T fold)^T ctx.  This block's partial
-         * over columns [80j, 80j + 80) goes out before the O rows, so the
-         * GU stage can choose the experts while the rows are computed. */
+         * over columns [Z_COLS jz, + Z_COLS) goes out before the O rows, so
+         * the GU stage can choose the experts while the rows are computed. */
         const u32 e = tid_() % 64u, q = tid_() / 64u;
         const float *zf = S.zw, *zo = S.zw + Z_COLS * NEXP;
         /* every operand read before the (ordered) sums, so the LDS round
@@ -1102,7 +1123,7 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
         float wf[G::ZC], wo[G::ZC], xh[G::ZC], xc[G::ZC];
 #pragma unroll
         for (u32 k = 0; k < G::ZC; ++k) {
-            const u32 cl = G::ZC * q + k, c = j * Z_COLS + cl;
+            const u32 cl = G::ZC * q + k, c = jz * Z_COLS + cl;
             wf[k] = zf[cl * NEXP + e];
             wo[k] = zo[cl * NEXP + e];
             xh[k] = (float)S.hres[c];
@@ -1129,13 +1150,14 @@ __device__ bool o_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, O
             S.zout[e2] = zs;
         }
         __syncthreads();
-        publish(R, R.pk + off_o(l), PO, PO_AR + j * PO_Z, PO_Z, tag, [&](u32 p) {
+        publish(R, R.pk + off_o(l), PO, PO_AR + jz * PO_Z, PO_Z, tag, [&](u32 p) {
             const u32 z0 = 3u * p;
             return make_uint3(__float_as_uint(S.zout[z0]), __float_as_uint(z0 + 1u < NEXP ? S.zout[z0 + 1u] : 0.0f),
                               __float_as_uint(z0 + 2u < NEXP ? S.zout[z0 + 2u] : 0.0f));
         });
         drain_stores(32u, PO_Z);
     }
+    if (!ob) return true; /* a z block only */
     float part[G::RPG];
 #pragma unroll
     for (u32 k = 0; k < G::RPG; ++k) part[k] = 0.0f;
@@ -1518,7 +1540,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                               H(sd.eus) + e * sd.gss, slice * GU_ROWS, GU_ROWS, EI);
         }
         TLD(l, 10u);
-#ifdef UOCR_RUN_TIMELINE
+#if defined(UOCR_RUN_TIMELINE) && !defined(UOCR_RUN_TL_NOWAIT)
         if (l == 5u && tid_() == 0u) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             TLR(128u + 17u);
@@ -1535,6 +1557,11 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                 put6(hres + j * O_ROWS + 6u * k, v, 6u * k, O_ROWS);
             });
         if (tid_() == NT - 64u) S.red[15] = ok_a ? 1.0f : 0.0f;
+#ifdef UOCR_RUN_TIMELINE
+        /* the eighth wavefront's gather of a complete (its own stamp) */
+        if (l == 5u && R.tl != nullptr && tid_() == NT - 64u)
+            R.tl[blockIdx.x * RUN_TL_EVENTS + 128u + 24u] = __builtin_amdgcn_s_memrealtime();
+#endif
         /* the other wavefronts' expert rows may still be arriving */
         lds_barrier();
         if (S.red[15] == 0.0f) return false;
