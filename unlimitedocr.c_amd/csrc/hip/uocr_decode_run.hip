@@ -1664,8 +1664,14 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
 
 /* DN stage: gathers the mids; MoE: out = f16(sum_r w_r D_r.mid_r + f16(SD.smid)
  * + a); layer 0: out = f16(D.mid + a). */
-template <int QF>
-__device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, DnFrags<QF> &dn) {
+/* UOCR_RUN_QKV_EARLY: a DN block issues the next layer's QKV rows once its
+ * mids are in, so they arrive during its dots; issued after the DN publish
+ * (at the top of the next layer), they sat in front of its polls for h. */
+#ifndef UOCR_RUN_QKV_EARLY
+#define UOCR_RUN_QKV_EARLY 1
+#endif
+template <int QF, int QA>
+__device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, DnFrags<QF> &dn, QkvFrags<QA> &qf) {
     typedef DnCfg<QF> G;
     const u32 b = blockIdx.x;
     if (b >= DN_BLOCKS) return true;
@@ -1698,6 +1704,7 @@ __device__ bool dn_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
     const u32 c = dn_row(), lane = tid_() & 63u, rl = c - b * DN_ROWS;
     /* the rows: registers, or this wavefront's LDS-direct loads */
     if (dn_in_lds<QF>()) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (UOCR_RUN_QKV_EARLY && l + 1u < UOCR_RUN_LAYERS) qkv_load<QA>(R, l + 1u, qf);
     const uint4 *dnw = S.dnw + (size_t)(tid_() >> 6) * G::J * 64u;
     auto dnrow = [&](u32 j) { return dn_in_lds<QF>() ? dnw[j * 64u + tid_() % 64u] : dn.w[dn_in_lds<QF>() ? 0u : j]; };
     float out;
@@ -1855,10 +1862,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
             }
             return;
         }
+        QkvFrags<QA> qf;
 #pragma unroll 1
         for (u32 l = 0; l < UOCR_RUN_LAYERS; ++l) {
-            QkvFrags<QA> qf;
-            qkv_load<QA>(R, l, qf);
+            /* the DN blocks issued this layer's QKV rows in their DN stage */
+            if (!(UOCR_RUN_QKV_EARLY && l > 0u && blockIdx.x < DN_BLOCKS)) qkv_load<QA>(R, l, qf);
             AttFrags af;
             if (blockIdx.x >= ATT0) att_load(R, l, att_plan(R, t), 0u, af);
             if (!qkv_stage<QA, QE>(R, S, l, t, tag, qf)) return;
@@ -1871,7 +1879,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
             o_load_z(R, l, S.zw);
             if (!o_stage<QA>(R, S, l, t, tag, of)) return;
             if (!gu_stage<QF>(R, S, l, t, tag, gf, dn)) return;
-            if (!dn_stage<QF>(R, S, l, t, tag, dn)) return;
+            if (!dn_stage<QF, QA>(R, S, l, t, tag, dn, qf)) return;
         }
     }
 }
