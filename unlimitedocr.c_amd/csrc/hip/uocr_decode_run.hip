@@ -1438,6 +1438,9 @@ __device__ __forceinline__ void dd_load(const Run &R, const Lds &S, DnFrags<QF> 
  * normalises a, selects the experts (MoE), and computes the block's mids.
  * MoE layers also issue the DN stage's loads (dn) once the experts are known. */
 #define UOCR_RUN_DN_EARLY dn_in_lds<QF>()
+#ifndef UOCR_RUN_Z_ALL_SKIP
+#define UOCR_RUN_Z_ALL_SKIP 1 /* Q4: blocks that do not need z skip its gather */
+#endif
 #ifndef UOCR_RUN_WAVE_TOPK
 #define UOCR_RUN_WAVE_TOPK 1 /* Q8 with 20 z blocks and the store drains: 3,363-3,366 against 3,351-3,353 without it (before them: 3,196 against 3,180) */
 #endif
@@ -1480,7 +1483,13 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         /* the z partials first (published before the O rows), the top-6 on z
          * (softmax is monotone and inv_rms > 0, so z orders the experts as
          * the probabilities do) and the expert loads; then a and its norm */
-        if (!gather<(Z_BLOCKS * PO_Z + NT - 1) / NT>(R, R.pk + off_o(l), PO, Z_BLOCKS * PO_Z, tag, W_GU, (u32)t,
+        /* z feeds the expert choice only: routed blocks, the DN blocks (their
+         * DN stage reads the ids) and the traced block; in the Q4 instance the
+         * other shared-row blocks skip its 440 packets (Q4 3,913 against 3,897
+         * tok/s; the Q8 instance measured 3,306 against 3,394 with the skip) */
+        const bool need_z = !(UOCR_RUN_Z_ALL_SKIP && QF == 4) ||
+                            (rank >= 0 || b < DN_BLOCKS || (R.trace != nullptr && b == 0u) || !UOCR_RUN_EXACT_WEIGHTS);
+        if (need_z && !gather<(Z_BLOCKS * PO_Z + NT - 1) / NT>(R, R.pk + off_o(l), PO, Z_BLOCKS * PO_Z, tag, W_GU, (u32)t,
                                                      [](u32 i) { return PO_AR + i; }, [&](u32 i, uint4 v) {
                                                          const u32 j = i / PO_Z, z0 = 3u * (i % PO_Z);
                                                          float *zp = zpart + j * NEXP + z0;
@@ -1504,7 +1513,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
          * later readers (behind the barrier after the gather of a) */
         float z = 0.0f;
         u32 mye = 0u;
-        if (UOCR_RUN_WAVE_TOPK || tid_() < 64u) {
+        if (need_z && (UOCR_RUN_WAVE_TOPK || tid_() < 64u)) {
             const u32 e = tid_() % 64u;
             /* all partials read before the (ordered) sum: one LDS round trip */
             float zp[Z_BLOCKS];
