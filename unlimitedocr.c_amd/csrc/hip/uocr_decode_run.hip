@@ -362,7 +362,7 @@ __device__ __forceinline__ void gather_wave_issue(const Run &R, const uint4 *reg
 /* PRE: gather_wave_issue() has issued the first round of polls into stg. */
 template <int MAXP, bool PRE = false, typename Phys, typename Sink>
 __device__ __forceinline__ bool gather_wave(const Run &R, const uint4 *region, u32 per_copy, u32 n, u32 tag, u32 where,
-                                            u32 step, u32 wave, uint4 *stg, Phys phys, Sink sink) {
+                                            u32 step, u32 wave, uint4 *stg, Phys phys, Sink sink, u32 tl_ev = 0u) {
     if (__builtin_amdgcn_readfirstlane(tid_() / 64u) != wave) return true;
     const uint4 *rep = region + (size_t)R.xcc * per_copy;
     const u32 t = tid_() % 64u;
@@ -381,6 +381,13 @@ __device__ __forceinline__ bool gather_wave(const Run &R, const uint4 *region, u
             }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#ifdef UOCR_RUN_TIMELINE
+        /* the completion of the first rounds, and their count (tl_ev + 7) */
+        if (tl_ev != 0u && R.tl != nullptr && t == 0u) {
+            R.tl[blockIdx.x * RUN_TL_EVENTS + tl_ev + min(it - 1u, 6u)] = __builtin_amdgcn_s_memrealtime();
+            R.tl[blockIdx.x * RUN_TL_EVENTS + tl_ev + 7u] = it;
+        }
+#endif
 #pragma unroll
         for (int k = 0; k < MAXP; ++k) {
             if ((pend & (1u << k)) && stg[k * 64 + t].x == tag) pend &= ~(1u << k);
@@ -1438,6 +1445,11 @@ __device__ __forceinline__ void dd_load(const Run &R, const Lds &S, DnFrags<QF> 
  * normalises a, selects the experts (MoE), and computes the block's mids.
  * MoE layers also issue the DN stage's loads (dn) once the experts are known. */
 #define UOCR_RUN_DN_EARLY dn_in_lds<QF>()
+#ifndef UOCR_RUN_APRE_LATE
+/* Q8: GU's first round of polls for a after the expert choice (Q8 3,426-3,430
+ * against 3,394 tok/s; the Q4 instance measured 3,836-3,846 against 3,906) */
+#define UOCR_RUN_APRE_LATE 1
+#endif
 #ifndef UOCR_RUN_Z_ALL_SKIP
 #define UOCR_RUN_Z_ALL_SKIP 1 /* Q4: blocks that do not need z skip its gather */
 #endif
@@ -1500,10 +1512,20 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
             return false;
         }
         TLR(2u * (4u + 5u * l));
-        /* the first round of a's polls, in flight while the experts are
-         * chosen and ahead of the expert loads */
+        /* the first round of a's polls: issued here (in flight while the
+         * experts are chosen), or with UOCR_RUN_APRE_LATE once they are
+         * chosen, still ahead of the expert loads */
         uint4 *stg = (uint4 *)(S.scr + 8192u);
-        gather_wave_issue<(PO_AR + 63u) / 64u>(R, R.pk + off_o(l), PO, PO_AR, NT / 64u - 1u, stg, [](u32 i) { return i; });
+        auto a_pre = [&]() {
+            gather_wave_issue<(PO_AR + 63u) / 64u>(R, R.pk + off_o(l), PO, PO_AR, NT / 64u - 1u, stg,
+                                                    [](u32 i) { return i; });
+#ifdef UOCR_RUN_TIMELINE
+            if (l == 5u && R.tl != nullptr && tid_() == NT - 64u)
+                R.tl[blockIdx.x * RUN_TL_EVENTS + 128u + 33u] = __builtin_amdgcn_s_memrealtime();
+#endif
+        };
+        constexpr bool apre_late = UOCR_RUN_APRE_LATE && QF == 3;
+        if (!apre_late) a_pre();
         /* wavefront 0: z of expert e (lane e) over the Z_BLOCKS partials in a fixed
          * order, then the top-6 */
         TLD(l, 18u);
@@ -1542,6 +1564,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         if (R.trace != nullptr && b == 0u && (u32)t < R.trace_steps && tid_() < TOPK) {
             R.trace[((size_t)t * 11u + (l - 1u)) * TOPK + tid_()] = S.selid[tid_()];
         }
+        if (apre_late) a_pre();
         TLD(l, 9u);
         if (rank >= 0) {
             const u32 e = UOCR_RUN_WAVE_TOPK ? mye : S.selid[rank];
@@ -1564,7 +1587,8 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
             [&](u32 i, uint4 v) {
                 const u32 j = i / PO_A, k = i % PO_A;
                 put6(hres + j * O_ROWS + 6u * k, v, 6u * k, O_ROWS);
-            });
+            },
+            l == 5u ? 128u + 25u : 0u);
         if (tid_() == NT - 64u) S.red[15] = ok_a ? 1.0f : 0.0f;
 #ifdef UOCR_RUN_TIMELINE
         /* the eighth wavefront's gather of a complete (its own stamp) */
