@@ -1524,7 +1524,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                 R.tl[blockIdx.x * RUN_TL_EVENTS + 128u + 33u] = __builtin_amdgcn_s_memrealtime();
 #endif
         };
-        constexpr bool apre_late = UOCR_RUN_APRE_LATE && QF == 3;
+        constexpr bool apre_late = UOCR_RUN_APRE_LATE == 2 || (UOCR_RUN_APRE_LATE == 1 && QF == 3); /* 2: both instances */
         if (!apre_late) a_pre();
         /* wavefront 0: z of expert e (lane e) over the Z_BLOCKS partials in a fixed
          * order, then the top-6 */
