@@ -136,6 +136,26 @@ def test_batched_and_token_prefill_agree(gpu):
     assert abs(float(a_sc[0]) - float(b_sc[0])) <= 2e-2 + 1e-2 * abs(float(b_sc[0]))
 
 
+def test_long_prompt_batched_and_token_prefill_agree(gpu):
+    """A 1,450-row prompt: 8,700 routed (token, expert) pairs, more than the
+    8,192 the bucket build keeps in registers, so its looped path runs; 23
+    query tiles of the split flash attention (key chunks of 7 tiles).  The
+    MFMA prefill and the per-position prefill agree on the first step's
+    winning score within the fp16 tolerance."""
+    uocr = gpu
+    m = model(uocr, 3)
+    rng = np.random.default_rng(31)
+    ids, mask, rows = prompt(rng, 50, 1400)
+    assert ids.size * 6 > 8192
+    eng = uocr.Engine.from_memory(m, backend="hip", max_prompt_tokens=1536, max_gen_tokens=8)
+    a_ids, a_sc, _, _ = eng.generate_embeddings(ids, mask, rows, 4, flags=uocr.GEN_IGNORE_EOS)
+    b_ids, b_sc, _, _ = eng.generate_embeddings(ids, mask, rows, 4,
+                                                flags=uocr.GEN_IGNORE_EOS | uocr.GEN_TOKEN_PREFILL)
+    eng.close()
+    assert a_ids.shape == (4,) and b_ids.shape == (4,)
+    assert abs(float(a_sc[0]) - float(b_sc[0])) <= 2e-2 + 1e-2 * abs(float(b_sc[0]))
+
+
 # vision linear: (qtype, m, k, n, act, split) at the SAM ViT-B global view
 # (4096 tokens, 768 wide: qkv 2304 split 768, lin1 3072 + GELU, lin2), the
 # CLIP-L view (257 tokens, 1024 wide: qkv split 1024, fc1 4096 + QuickGELU,
