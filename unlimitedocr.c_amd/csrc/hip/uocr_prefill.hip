@@ -43,6 +43,13 @@ typedef uint32_t u32;
 #ifndef GDEPTH
 #define GDEPTH 2 /* K steps in flight per GEMM block (2, 3 and 5 measured: 2 best on the SAM shapes, equal on the prefill) */
 #endif
+/* The SwiGLU GEMMs (two weight matrices) keep one K step in flight: 16
+ * fewer registers take them from 2 to 3 wavefronts per SIMD (routed gate/up
+ * 66.8 -> 62.4 us, dense gate/up 62.9 -> 60.8 us); the one-matrix GEMMs run
+ * 4 per SIMD either way and lose with one step (dense down 44.4 -> 48.7 us). */
+#ifndef GDEPTH_SWIGLU
+#define GDEPTH_SWIGLU 1
+#endif
 
 __device__ __forceinline__ float silu_p(float g) {
     return g / (1.0f + expf(-g));
@@ -236,6 +243,7 @@ __device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz, Ro
     constexpr int AQ4 = TMR * (TK / 8) / PB; /* activation pieces (8 halves) per thread per K step */
     static_assert(TMR % 32 == 0 && TMR <= PB && AQ4 * PB == TMR * (TK / 8), "tile rows");
     constexpr int NMAT = EPI == GE_SWIGLU ? 2 : 1;
+    constexpr int GD = EPI == GE_SWIGLU ? GDEPTH_SWIGLU : GDEPTH; /* K steps in flight */
     /* f16 with one weight matrix: the block loads each K step's raw weight
      * tile with eight lanes per row (whole 128-byte row pieces) into LDS, and
      * each wavefront reads its 32 rows back in the MFMA operand layout; loads
@@ -295,7 +303,7 @@ __device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz, Ro
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[m][j][i] = 0.0f;
 
-    /* K steps run GDEPTH deep: step s's loads were issued GDEPTH steps
+    /* K steps run GD deep: step s's loads were issued GD steps
      * earlier into a register ring (constant indices only, so the ring stays
      * in registers) */
     /* the lambdas below see plain locals: a reference to the kernel
@@ -305,8 +313,8 @@ __device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz, Ro
     const bool pk = p.packed != 0u;
     const u32 NT = Kd / TK, kb0 = p.kst != 0u ? bz * p.kst : 0u;
     const u32 NS = p.kst != 0u ? min(p.kst, NT - kb0) : NT;
-    u32 ka[GDEPTH][AQ4][4]; /* words, not uint4: no struct copies, so they stay in registers */
-    u32 kb[GDEPTH][NMAT][BPiece<QT>::NW], ks[GDEPTH][NMAT];
+    u32 ka[GD][AQ4][4]; /* words, not uint4: no struct copies, so they stay in registers */
+    u32 kb[GD][NMAT][BPiece<QT>::NW], ks[GD][NMAT];
     extern __shared__ __attribute__((aligned(16))) unsigned short ssc[];
     const bool scl = QT != 1 && p.sc_lds != 0u;
     const u32 lrow0 = n0 - nbase, nvalid = min((u32)TN, nmax - lrow0);
@@ -403,7 +411,7 @@ __device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz, Ro
          * no later step consumes): loads issued on every path keep the
          * compiler's load counting exact, so the wait before a step covers
          * only that step's loads and the later steps' stay in flight */
-        issue(D, min(st + GDEPTH, NS - 1u));
+        issue(D, min(st + GD, NS - 1u));
 #pragma unroll
         for (u32 i = 0; i < 4; ++i) {
 #pragma unroll
@@ -417,7 +425,7 @@ __device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz, Ro
             }
         }
     };
-    static_for<GDEPTH>([&](auto D) { issue(D, min((u32)decltype(D)::value, NS - 1u)); });
+    static_for<GD>([&](auto D) { issue(D, min((u32)decltype(D)::value, NS - 1u)); });
     if (scl) {
         /* after the first steps' loads are in flight; rows past nmax are not
          * loaded (their lanes read the last valid row, nrow is clamped) */
@@ -435,10 +443,10 @@ __device__ __forceinline__ void gemm_body(GemmArgs p, u32 bx, u32 by, u32 bz, Ro
         __syncthreads();
     }
     u32 st = 0;
-    for (; st + GDEPTH <= NS; st += GDEPTH) {
-        static_for<GDEPTH>([&](auto D) { step(D, st + (u32)decltype(D)::value); });
+    for (; st + GD <= NS; st += GD) {
+        static_for<GD>([&](auto D) { step(D, st + (u32)decltype(D)::value); });
     }
-    static_for<GDEPTH>([&](auto D) {
+    static_for<GD>([&](auto D) {
         if (st + (u32)decltype(D)::value < NS) step(D, st + (u32)decltype(D)::value);
     });
 
