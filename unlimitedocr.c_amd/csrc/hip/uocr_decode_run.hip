@@ -1848,9 +1848,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode_run(RunArgs A) {
     __shared__ unsigned long long keyw[NT / 64u];
     __shared__ float xsum[HID / 16u];
     __shared__ __attribute__((aligned(16))) uint8_t lgw[2u * LG_COLS * 2u];
-    /* the DN rows; with it the block's LDS exceeds half a CU's 160 KB, so no
-     * CU can hold two run workgroups whatever the register allocation (the
-     * run needs one workgroup on each of the 256 CUs) */
+    /* the DN rows (the Q8 instance; Q4 holds them in registers): with them
+     * the block's LDS exceeds half a CU's 160 KB, so no CU can hold two run
+     * workgroups whatever the register allocation (the run needs one
+     * workgroup on each of the 256 CUs; Q4's 241 VGPRs at 512 threads fill a
+     * CU's register file) */
     __shared__ __attribute__((aligned(16))) uint4 dnw[DN_ROWS * DnCfg<QF>::J * 64u];
     Lds S{xs, hres, outv, red, zout, selw, zw, selid, keyw, scr, xsum, lgw, dnw};
     Run R;
