@@ -1451,7 +1451,7 @@ __device__ __forceinline__ void dd_load(const Run &R, const Lds &S, DnFrags<QF> 
 #define UOCR_RUN_APRE_LATE 1
 #endif
 #ifndef UOCR_RUN_Z_ALL_SKIP
-#define UOCR_RUN_Z_ALL_SKIP 1 /* Q4: blocks that do not need z skip its gather */
+#define UOCR_RUN_Z_ALL_SKIP 1 /* Q4: blocks that do not need z skip its gather (2: both instances) */
 #endif
 #ifndef UOCR_RUN_WAVE_TOPK
 #define UOCR_RUN_WAVE_TOPK 1 /* Q8 with 20 z blocks and the store drains: 3,363-3,366 against 3,351-3,353 without it (before them: 3,196 against 3,180) */
@@ -1499,7 +1499,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
          * DN stage reads the ids) and the traced block; in the Q4 instance the
          * other shared-row blocks skip its 440 packets (Q4 3,913 against 3,897
          * tok/s; the Q8 instance measured 3,306 against 3,394 with the skip) */
-        const bool need_z = !(UOCR_RUN_Z_ALL_SKIP && QF == 4) ||
+        const bool need_z = !(UOCR_RUN_Z_ALL_SKIP == 2 || (UOCR_RUN_Z_ALL_SKIP == 1 && QF == 4)) ||
                             (rank >= 0 || b < DN_BLOCKS || (R.trace != nullptr && b == 0u) || !UOCR_RUN_EXACT_WEIGHTS);
         if (need_z && !gather<(Z_BLOCKS * PO_Z + NT - 1) / NT>(R, R.pk + off_o(l), PO, Z_BLOCKS * PO_Z, tag, W_GU, (u32)t,
                                                      [](u32 i) { return PO_AR + i; }, [&](u32 i, uint4 v) {
