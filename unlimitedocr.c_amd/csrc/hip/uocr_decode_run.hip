@@ -1445,10 +1445,15 @@ __device__ __forceinline__ void dd_load(const Run &R, const Lds &S, DnFrags<QF> 
  * normalises a, selects the experts (MoE), and computes the block's mids.
  * MoE layers also issue the DN stage's loads (dn) once the experts are known. */
 #define UOCR_RUN_DN_EARLY dn_in_lds<QF>()
-#ifndef UOCR_RUN_APRE_LATE
-/* Q8: GU's first round of polls for a after the expert choice (Q8 3,426-3,430
- * against 3,394 tok/s; the Q4 instance measured 3,836-3,846 against 3,906) */
-#define UOCR_RUN_APRE_LATE 1
+/* GU's first round of polls for a, per instance: 0 right after the z
+ * gather, 1 after the expert choice, 2 after it except in the O blocks.
+ * Q8: 1 (3,426-3,430 against 3,394 tok/s with 0); Q4: 0 (3,836-3,846 with 1
+ * against 3,906, 2 within the noise) */
+#ifndef UOCR_RUN_APRE_Q4
+#define UOCR_RUN_APRE_Q4 0
+#endif
+#ifndef UOCR_RUN_APRE_Q8
+#define UOCR_RUN_APRE_Q8 1
 #endif
 #ifndef UOCR_RUN_Z_ALL_SKIP
 #define UOCR_RUN_Z_ALL_SKIP 1 /* Q4: blocks that do not need z skip its gather (2: both instances) */
@@ -1513,7 +1518,7 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
         }
         TLR(2u * (4u + 5u * l));
         /* the first round of a's polls: issued here (in flight while the
-         * experts are chosen), or with UOCR_RUN_APRE_LATE once they are
+         * experts are chosen), or (UOCR_RUN_APRE_Q4 / _Q8) once they are
          * chosen, still ahead of the expert loads */
         uint4 *stg = (uint4 *)(S.scr + 8192u);
         auto a_pre = [&]() {
@@ -1524,7 +1529,8 @@ __device__ bool gu_stage(const Run &R, const Lds &S, u32 l, int32_t t, u32 tag, 
                 R.tl[blockIdx.x * RUN_TL_EVENTS + 128u + 33u] = __builtin_amdgcn_s_memrealtime();
 #endif
         };
-        constexpr bool apre_late = UOCR_RUN_APRE_LATE == 2 || (UOCR_RUN_APRE_LATE == 1 && QF == 3); /* 2: both instances */
+        constexpr int apre = QF == 4 ? UOCR_RUN_APRE_Q4 : UOCR_RUN_APRE_Q8;
+        const bool apre_late = apre == 1 || (apre == 2 && !is_o_block(b));
         if (!apre_late) a_pre();
         /* wavefront 0: z of expert e (lane e) over the Z_BLOCKS partials in a fixed
          * order, then the top-6 */
