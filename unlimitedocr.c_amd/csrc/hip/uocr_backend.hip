@@ -39,6 +39,10 @@
 
 namespace {
 
+#ifndef UOCR_PREFILL_KSPLIT_MAX
+#define UOCR_PREFILL_KSPLIT_MAX 4u /* K splits (P x 1280 fp32 planes) the prefill's partial buffer holds */
+#endif
+
 struct dev_layer {
     uocr_qmat q, k, v, o, gate, up, down, sgate, sup, sdown;
     const uint16_t *in_norm, *post_norm, *router;
@@ -684,9 +688,9 @@ extern "C" int uocr_hip_context_allocate_runtime(uocr_hip_ctx *ctx, uint32_t pro
     const uint64_t o_pte = p.take(max_tiles * 4u), o_pts0 = p.take(max_tiles * 4u), o_pts1 = p.take(max_tiles * 4u);
     const uint64_t o_pnt = p.take(4u), o_plt = p.take(PK * 4u), o_plp = p.take(PK * 4u);
     const uint64_t o_pfa = p.take(uocr_flash_attn_ws_bytes());
-    /* split-K partials of the O projection and the dense down (2 splits x
+    /* split-K partials of the O projection and the dense down (UOCR_PREFILL_KSPLIT_MAX splits x
      * P x 1280, fp32) */
-    const uint64_t o_pkp = p.take(Pc * H_SIZE * 2u * 4u);
+    const uint64_t o_pkp = p.take(Pc * H_SIZE * UOCR_PREFILL_KSPLIT_MAX * 4u);
     const uint64_t o_run = p.take(uocr_run_arena_bytes());
     const uint64_t total = p.off;
     HIPCHK(counted_malloc(ctx, (void **)&ctx->rarena, total), "runtime arena allocation");
@@ -915,14 +919,14 @@ static hipError_t enqueue_prefill_step(uocr_hip_ctx *c) {
 }
 
 /* Plain prefill GEMM with split K where its grid is small (the partials
- * buffer holds 2 x P x 1280 floats: at most 2 splits at N = 1280).  Used for
- * the O projection and layer 0's dense down (K = 6848): measured at P = 932,
- * O 26.3 -> 16 + 5 us (reduce), while the router logits (11.4 -> 6.6 + 4.9)
- * and the shared down (23.6 -> 19 + 5.2) gain nothing, an extra eager launch
- * costing about 5 us. */
+ * buffer holds UOCR_PREFILL_KSPLIT_MAX x P x 1280 floats; the split count is
+ * clamped to what it holds at this N).  Used for the O projection and layer
+ * 0's dense down (K = 6848): measured at P = 932, O 26.3 -> 16 + 5 us
+ * (reduce), while the router logits (11.4 -> 6.6 + 4.9) and the shared down
+ * (23.6 -> 19 + 5.2) gain nothing, an extra eager launch costing about 5 us. */
 static void with_ksplit(uocr_gemm_desc &d, float *part) {
-    const uint32_t s = uocr_gemm_ksplit(d.M, d.N, d.K);
-    if (s > 1u && (uint64_t)s * d.N <= 2u * H_SIZE) {
+    const uint32_t s = std::min<uint32_t>(uocr_gemm_ksplit(d.M, d.N, d.K), UOCR_PREFILL_KSPLIT_MAX * H_SIZE / d.N);
+    if (s > 1u) {
         d.ksplit = s;
         d.part = part;
     }

@@ -1328,7 +1328,11 @@ extern "C" uint32_t uocr_gemm_ksplit(uint32_t M, uint32_t N, uint32_t K) {
     const u32 blocks = ((M + tm - 1u) / tm) * ((N + TN - 1u) / TN), steps = K / TK;
     if (blocks >= 256u) return 1u;
     u32 s = 1u;
-    while (s < 8u && blocks * 2u * s <= 512u && steps / (2u * s) >= 5u) s *= 2u;
+    /* doubling while the split grid stays within 512 blocks and a split keeps
+     * 5 K steps, or a split keeps 16: the O projection at P = 932 (150 tiles,
+     * 20 steps) takes 2 (4 measured the same GEMM time and a longer reduce),
+     * layer 0's dense down (150 tiles, 107 steps) 4 (44.8 -> 36.0 us) */
+    while (s < 8u && ((blocks * 2u * s <= 512u && steps / (2u * s) >= 5u) || steps / (2u * s) >= 16u)) s *= 2u;
     return s;
 }
 
