@@ -657,7 +657,14 @@ __global__ __launch_bounds__(PB) void k_split_reduce(const float *__restrict__ p
  * pieces l, l + 64, l + 128 (< 160) in v.  Writes yr = f16(x * inv_rms * w)
  * (norm.metal:12-40), the sum of squares in fp32 in a fixed order (lane
  * pieces in order, then the butterfly), so every caller rounds alike. */
-__device__ __forceinline__ void row_norm_tail(U4H8 (&v)[3], u32 lane, const h16 *__restrict__ w, h16 *__restrict__ yr) {
+/* The norm weights' pieces of a lane (i = lane + 64q, clamped to the row),
+ * loaded at a kernel's start so the tail waits on no further load round. */
+__device__ __forceinline__ void norm_w_load(const h16 *__restrict__ w, u32 lane, U4H8 (&wv)[3]) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) wv[q].u = ((const uint4 *)w)[min(lane + 64u * q, UOCR_K_HIDDEN / 8u - 1u)];
+}
+
+__device__ __forceinline__ void row_norm_tail(U4H8 (&v)[3], u32 lane, const U4H8 (&wv)[3], h16 *__restrict__ yr) {
     float ss = 0.0f;
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
@@ -672,10 +679,9 @@ __device__ __forceinline__ void row_norm_tail(U4H8 (&v)[3], u32 lane, const h16 
     for (int q = 0; q < 3; ++q) {
         const u32 i = lane + 64u * q;
         if (i < UOCR_K_HIDDEN / 8u) {
-            U4H8 wv, y;
-            wv.u = ((const uint4 *)w)[i];
+            U4H8 y;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) y.h[j] = (h16)(((float)v[q].h[j] * inv) * (float)wv.h[j]);
+            for (int j = 0; j < 8; ++j) y.h[j] = (h16)(((float)v[q].h[j] * inv) * (float)wv[q].h[j]);
             ((uint4 *)yr)[i] = y.u;
         }
     }
@@ -687,13 +693,15 @@ __global__ __launch_bounds__(PB) void k_rows_rmsnorm(const h16 *__restrict__ x, 
     const u32 row = blockIdx.x * (PB / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
     if (row >= P) return;
     const h16 *xr = x + (size_t)row * UOCR_K_HIDDEN;
+    U4H8 wv[3];
+    norm_w_load(w, lane, wv);
     U4H8 v[3];
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
         const u32 i = lane + 64u * q;
         if (i < UOCR_K_HIDDEN / 8u) v[q].u = ((const uint4 *)xr)[i];
     }
-    row_norm_tail(v, lane, w, y + (size_t)row * UOCR_K_HIDDEN);
+    row_norm_tail(v, lane, wv, y + (size_t)row * UOCR_K_HIDDEN);
 }
 
 /* Split-K reduce of a 1280-column fp16 GEMM output with its residual, fused
@@ -710,7 +718,8 @@ __global__ __launch_bounds__(PB) void k_reduce_norm(const float *__restrict__ pa
      * flight before any sum; planes beyond the second are added in order
      * after them */
     float4 pa[3][2], pb2[3][2];
-    U4H8 rr[3];
+    U4H8 rr[3], wv[3];
+    norm_w_load(w, lane, wv);
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
         const u32 i = min(lane + 64u * q, UOCR_K_HIDDEN / 8u - 1u);
@@ -758,7 +767,7 @@ __global__ __launch_bounds__(PB) void k_reduce_norm(const float *__restrict__ pa
         for (int j = 0; j < 8; ++j) v[q].h[j] = (h16)(res != nullptr ? r[j] + (float)rr[q].h[j] : r[j]);
         *(uint4 *)(out + (size_t)row * ldo + 8u * i) = v[q].u;
     }
-    row_norm_tail(v, lane, w, y + (size_t)row * UOCR_K_HIDDEN);
+    row_norm_tail(v, lane, wv, y + (size_t)row * UOCR_K_HIDDEN);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1258,28 +1267,58 @@ __global__ __launch_bounds__(PB) void k_moe_combine_norm(const YT *__restrict__ 
     float wr[UOCR_K_TOPK];
 #pragma unroll
     for (int r = 0; r < UOCR_K_TOPK; ++r) wr[r] = wts[t * UOCR_K_TOPK + r];
-    U4H8 v[3];
+    U4H8 wv[3], v[3];
+    norm_w_load(w, lane, wv);
+    if constexpr (sizeof(YT) == 2) {
+        /* fp16 pair rows: every load of the row issued before any sum */
+        U4H8 ey[3][UOCR_K_TOPK], sh[3], rs[3];
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
-        const u32 i = lane + 64u * q;
-        if (i >= UOCR_K_HIDDEN / 8u) continue;
-        const size_t base = (size_t)t * UOCR_K_HIDDEN + 8u * i;
-        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        for (int q = 0; q < 3; ++q) {
+            const u32 i = min(lane + 64u * q, UOCR_K_HIDDEN / 8u - 1u);
+            const size_t base = (size_t)t * UOCR_K_HIDDEN + 8u * i;
 #pragma unroll
-        for (int r = 0; r < UOCR_K_TOPK; ++r) {
-            float e[8];
-            y_load8(Y + ((size_t)t * UOCR_K_TOPK + r) * UOCR_K_HIDDEN + 8u * i, e);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = fmaf(wr[r], e[j], acc[j]);
+            for (int r = 0; r < UOCR_K_TOPK; ++r)
+                ey[q][r].u = *(const uint4 *)(Y + ((size_t)t * UOCR_K_TOPK + r) * UOCR_K_HIDDEN + 8u * i);
+            sh[q].u = *(const uint4 *)(shared + base);
+            rs[q].u = *(const uint4 *)(res + base);
         }
-        U4H8 sh, rs;
-        sh.u = *(const uint4 *)(shared + base);
-        rs.u = *(const uint4 *)(res + base);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[q].h[j] = (h16)(acc[j] + (float)sh.h[j] + (float)rs.h[j]);
-        *(uint4 *)(out + base) = v[q].u;
+        for (int q = 0; q < 3; ++q) {
+            const u32 i = lane + 64u * q;
+            if (i >= UOCR_K_HIDDEN / 8u) continue;
+            float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int r = 0; r < UOCR_K_TOPK; ++r) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = fmaf(wr[r], (float)ey[q][r].h[j], acc[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[q].h[j] = (h16)(acc[j] + (float)sh[q].h[j] + (float)rs[q].h[j]);
+            *(uint4 *)(out + (size_t)t * UOCR_K_HIDDEN + 8u * i) = v[q].u;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+            const u32 i = lane + 64u * q;
+            if (i >= UOCR_K_HIDDEN / 8u) continue;
+            const size_t base = (size_t)t * UOCR_K_HIDDEN + 8u * i;
+            float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int r = 0; r < UOCR_K_TOPK; ++r) {
+                float e[8];
+                y_load8(Y + ((size_t)t * UOCR_K_TOPK + r) * UOCR_K_HIDDEN + 8u * i, e);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = fmaf(wr[r], e[j], acc[j]);
+            }
+            U4H8 sh, rs;
+            sh.u = *(const uint4 *)(shared + base);
+            rs.u = *(const uint4 *)(res + base);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[q].h[j] = (h16)(acc[j] + (float)sh.h[j] + (float)rs.h[j]);
+            *(uint4 *)(out + base) = v[q].u;
+        }
     }
-    row_norm_tail(v, lane, w, y + (size_t)t * UOCR_K_HIDDEN);
+    row_norm_tail(v, lane, wv, y + (size_t)t * UOCR_K_HIDDEN);
 }
 
 /* ------------------------------------------------------------------------ */
